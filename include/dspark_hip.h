@@ -1,0 +1,212 @@
+/*
+ * dspark_hip.h -- C ABI of the MI355X speculative-decoding verify engine
+ * (libdspark_hip.so, gfx950).
+ *
+ * The reference (regeter/mlx-dspark v0.3.1) has no native code: every kernel on its hot
+ * path is an MLX primitive called from Python. Each entry point below replaces one of those
+ * primitive call sites; the comment names the reference call site (file:line, paths
+ * relative to the reference root) whose behaviour it reproduces.
+ *
+ * Conventions (all entry points):
+ *   - return 0 (DSK_OK) on success, a negative DSK_E* code on failure; the message is kept
+ *     per thread and returned by dsk_last_error(). Nothing throws across this boundary.
+ *   - every device buffer is allocated by the caller; kernels never allocate and never
+ *     synchronise. Work is enqueued on `stream` (a hipStream_t; NULL = the null stream).
+ *   - lengths that change from one decode round to the next (sequence lengths, accepted
+ *     counts) live in device memory, so a captured HIP graph replays correctly.
+ *   - bf16 tensors are passed as uint16_t (raw bits); "W8" means MLX's affine 8-bit format,
+ *     group 64: w = scale * q + bias with bf16 scale/bias per 64 consecutive input columns.
+ */
+#ifndef DSPARK_HIP_H
+#define DSPARK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* dsk_stream_t; /* hipStream_t */
+
+enum {
+  DSK_OK = 0,
+  DSK_EINVAL = -1,  /* bad shape / argument */
+  DSK_ELAUNCH = -2, /* HIP launch or runtime error */
+  DSK_ERANGE = -3,  /* size beyond a documented maximum */
+  DSK_ENOWS = -4    /* workspace too small */
+};
+
+enum { DSK_F32 = 0, DSK_BF16 = 1 };
+
+enum { DSK_KV_BF16 = 0, DSK_KV_U8 = 1 };
+
+const char* dsk_last_error(void);
+int dsk_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------
+ * W8 weights.
+ * Replaces nn.quantize(..., bits=8, group_size=64) (src/mlx_dspark/load.py:204-206,
+ * :285-286) for the weights this engine creates, and the MLX-format packed weight that
+ * nn.QuantizedLinear holds (external mlx; used by the target layers reached from
+ * src/mlx_dspark/target.py:107-124).
+ *
+ * dsk_w8_quantize: w [N, K] (f32 or bf16, row-major) -> q [N, K] u8 (byte order identical
+ *   to MLX's uint32 packing, low byte first), scales/biases [N, K/64] bf16.
+ *   Rule per group of 64: lo = min, hi = max, scale = bf16((hi - lo) / 255) (scale = 1
+ *   when hi == lo), bias = bf16(lo), q = clamp(rint((w - bias) / scale), 0, 255).
+ * dsk_w8_repack: MLX layout -> the engine's tiled HBM layout consumed by dsk_w8_gemm:
+ *   wt [N/16][K/64][64 lanes][16 B], sb [N/16][16][K/64] u32 (bf16 scale | bf16 bias << 16).
+ *   N % 16 == 0, K % 64 == 0.
+ * ------------------------------------------------------------------------------------- */
+int dsk_w8_quantize(const void* w, int w_dtype, int64_t N, int64_t K, uint8_t* q,
+                    uint16_t* scales, uint16_t* biases, dsk_stream_t stream);
+int dsk_w8_repack(const uint8_t* q, const uint16_t* scales, const uint16_t* biases, int64_t N,
+                  int64_t K, uint8_t* wt, uint32_t* sb, dsk_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Activation pack (GEMM prologue).
+ * Replaces mx.fast.rms_norm (src/mlx_dspark/model.py:28, nn.RMSNorm at :103-106,
+ * :165-170, :233-235, and the Qwen3 input/post-attention norms inside mlx_lm), the MLP
+ * activation silu(gate) * up (src/mlx_dspark/model.py:44-45) / gelu_approx for the gemma
+ * family, and the bf16 -> MFMA operand staging in front of every quantized matmul.
+ *
+ * x [M, *] bf16 with row stride ldx (elements). mode:
+ *   DSK_PACK_PLAIN   a = x[:, :K]
+ *   DSK_PACK_RMSNORM a = bf16(x * rsqrt(mean(x^2) + eps) * norm_w)   (norm_w [K] bf16)
+ *   DSK_PACK_SILU    a = bf16(silu(x[:, :K]) * x[:, K:2K])
+ *   DSK_PACK_GELU    a = bf16(gelu_tanh(x[:, :K]) * x[:, K:2K])
+ * out: packed operand of dsk_act_pack_bytes(M, K) bytes. M <= 64, K % 64 == 0, K <= 24576.
+ * ------------------------------------------------------------------------------------- */
+enum { DSK_PACK_PLAIN = 0, DSK_PACK_RMSNORM = 1, DSK_PACK_SILU = 2, DSK_PACK_GELU = 3 };
+size_t dsk_act_pack_bytes(int M, int64_t K);
+int dsk_act_pack(const uint16_t* x, int64_t ldx, int M, int64_t K, int mode,
+                 const uint16_t* norm_w, float eps, void* out, dsk_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * W8 skinny GEMM: y[M, N] = residual + a[M, K] . deq(W)[N, K]^T
+ * Replaces mx.quantized_matmul behind nn.QuantizedLinear (external mlx), reached from
+ * src/mlx_dspark/target.py:115-123 (every target projection and the lm_head / tied
+ * embed_tokens.as_linear), src/mlx_dspark/batch_engine.py:199-204 (batched verify) and
+ * the drafter linears (src/mlx_dspark/model.py:97-101, :230-236; dflash_model.py:93-96).
+ *
+ * a: packed by dsk_act_pack. W: dsk_w8_repack layout. y: f32 or bf16, row stride ldy.
+ * residual: NULL or bf16 [M, N] with row stride ldr (may alias y when y is bf16).
+ * softcap > 0 applies y = tanh(y / softcap) * softcap (src/mlx_dspark/model.py:264-268).
+ * workspace: >= dsk_w8_gemm_ws_bytes(M, N, K) bytes; its counter region must be zeroed
+ * once after allocation (dsk_w8_gemm_ws_init); it is left zeroed after every call.
+ * ------------------------------------------------------------------------------------- */
+size_t dsk_w8_gemm_ws_bytes(int M, int64_t N, int64_t K);
+int dsk_w8_gemm_ws_init(void* workspace, size_t ws_bytes, dsk_stream_t stream);
+int dsk_w8_gemm(const void* a, const uint8_t* wt, const uint32_t* sb, int M, int64_t N,
+                int64_t K, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
+                int64_t ldr, float softcap, void* workspace, size_t ws_bytes,
+                dsk_stream_t stream);
+
+/* W8 row gather (embedding lookup): out[i, :] = bf16(deq(table)[ids[i], :]) * scale.
+ * Replaces nn.QuantizedEmbedding (mm.embed_tokens, src/mlx_dspark/target.py:112;
+ * drafter.embed, src/mlx_dspark/model.py:244-245; dflash_model.py:198).
+ * table in MLX layout: q [V, H] u8, scales/biases [V, H/64] bf16. */
+int dsk_w8_embed(const int32_t* ids, int n, const uint8_t* q, const uint16_t* scales,
+                 const uint16_t* biases, int64_t V, int64_t H, float scale, uint16_t* out,
+                 int64_t ldo, dsk_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Paged KV cache.
+ * Replaces mlx_lm KVCache / QuantizedKVCache (src/mlx_dspark/target.py:85-97) and the
+ * per-row BatchCache (src/mlx_dspark/batch_engine.py:61-163).
+ * A pool holds fixed pages of `page` tokens; page p, kv-head h, slot t:
+ *   bf16: kv[p][h][t][hd] bf16
+ *   u8:   kv[p][h][t][hd] u8 + sb[p][h][t][hd/64] u32 (bf16 scale | bf16 bias << 16),
+ *         affine group-64 along head_dim, same rule as dsk_w8_quantize.
+ * block_table [B, max_pages] int32 maps a row's logical page j to a physical page.
+ * seq_lens [B] int32 = tokens cached per row before the call (device memory).
+ * ------------------------------------------------------------------------------------- */
+
+/* qkv [B*W, (nq + 2*nkv) * hd] bf16 (rows b*W + i) -> per-head RMSNorm of q and k
+ * (q_norm/k_norm weights [hd] bf16), rotate-half RoPE at position seq_lens[b] + i
+ * (inv_freq [hd/2] f32), K/V appended to the pool at that position, and
+ * q_out [B*W, nq*hd] bf16. Replaces the Qwen3 attention prologue inside mlx_lm and
+ * DSparkAttention._kv/update_ctx (src/mlx_dspark/model.py:113-128). k_norm may be NULL
+ * (no norm). pos_offset is added to every position. */
+int dsk_qkv_rope_append(const uint16_t* qkv, int B, int W, int nq, int nkv, int hd,
+                        const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                        const float* inv_freq, const int32_t* seq_lens, int pos_offset,
+                        const int32_t* block_table, int max_pages, int page, int kv_dtype,
+                        void* k_pool, void* v_pool, uint32_t* k_sb, uint32_t* v_sb,
+                        uint16_t* q_out, dsk_stream_t stream);
+
+/* Attention of W new queries per row over the row's paged KV (already holding the W new
+ * tokens at positions seq_lens[b] .. seq_lens[b]+W-1).
+ * causal != 0: query i sees keys j <= seq_lens[b] + i  (mlx_lm create_attention_mask with
+ *   offset, src/mlx_dspark/target.py:113; build_batch_mask, batch_engine.py:170-178).
+ *   window > 0 additionally hides keys j <= seq_lens[b] + i - window (sliding layers).
+ * causal == 0: every query sees all seq_lens[b] + W keys (DSpark/DFlash block attention,
+ *   src/mlx_dspark/model.py:130-155, dflash_model.py:123-133).
+ * q [B*W, nq*hd] bf16 -> out [B*W, nq*hd] bf16. GQA: q head h reads kv head h/(nq/nkv).
+ * max_ctx bounds seq_lens[b] + W (sizes the split grid so the launch is graph-stable).
+ * softcap > 0: scores = tanh(scores / softcap) * softcap before the mask. */
+size_t dsk_attn_ws_bytes(int B, int W, int nq, int hd, int max_ctx);
+int dsk_attn_ws_init(void* workspace, size_t ws_bytes, dsk_stream_t stream);
+int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, int hd, float scale,
+                  int causal, int window, float softcap, const int32_t* seq_lens,
+                  int max_ctx, const int32_t* block_table, int max_pages, int page,
+                  int kv_dtype, const void* k_pool, const void* v_pool,
+                  const uint32_t* k_sb, const uint32_t* v_sb, uint16_t* out,
+                  void* workspace, size_t ws_bytes, dsk_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Acceptance.
+ * ------------------------------------------------------------------------------------- */
+
+/* Greedy: tt[b, i] = argmax_v logits[b, i, :] (lowest index on ties), i < W;
+ * n[b] = number of leading i < W-1 with draft[b, i] == tt[b, i];  token[b] = tt[b, n[b]];
+ * seq_lens[b] += n[b] + 1 when seq_lens != NULL (the KV rollback to the accepted length:
+ * W tokens were appended by the verify, W - 1 - n are trimmed).
+ * Replaces src/mlx_dspark/generate.py:910-933 (DSpark), :557-579 (DFlash),
+ * src/mlx_dspark/batch_engine.py:573-595 (batched). logits f32 or bf16 [B, W, V]
+ * (row stride ldl elements), draft [B, W-1] int32. */
+int dsk_accept_greedy(const void* logits, int dtype, int64_t ldl, int B, int W, int64_t V,
+                      const int32_t* draft, int32_t* tt, int32_t* n_out, int32_t* token_out,
+                      int32_t* seq_lens, void* workspace, size_t ws_bytes,
+                      dsk_stream_t stream);
+size_t dsk_accept_ws_bytes(int B, int W, int64_t V);
+int dsk_accept_ws_init(void* workspace, size_t ws_bytes, dsk_stream_t stream);
+
+/* Speculative sampling: replaces _spec_sample_accept (src/mlx_dspark/generate.py:659-688)
+ * with truncate_probs / sample_probs (src/mlx_dspark/sampling.py:18-49).
+ * p_logits [B, L+1, V] f32 (target), q_logits [B, L, V] f32 (draft; NULL = one-hot q at
+ * the drafted token, the lookup-draft case of generate.py:819-821), draft [B, L] int32.
+ * p = truncate(softmax(p_logits / T)); q = truncate(softmax(q_logits / T)) or, when
+ * q_mul_inv_t != 0, softmax(q_logits * (1/T)) (src/mlx_dspark/model.py:297, :304).
+ * Uniforms come from Philox4x32-10 keyed by (seed) at counter offset `offset`.
+ * Outputs: n_out[b] accepted drafts, token_out[b] residual/bonus token, seq_lens[b] +=
+ * n + 1 when non-NULL; accept_out [B, L] u8 and sample_out [B, L+1] int32 when non-NULL
+ * (per-position accept flags and the token each position would emit). */
+int dsk_accept_sample(const float* p_logits, const float* q_logits, int64_t V, int B, int L,
+                      const int32_t* draft, float temperature, float top_p, int top_k,
+                      int q_mul_inv_t, uint64_t seed, uint32_t offset, int32_t* n_out,
+                      int32_t* token_out, int32_t* seq_lens, uint8_t* accept_out,
+                      int32_t* sample_out, void* workspace, size_t ws_bytes,
+                      dsk_stream_t stream);
+
+/* Row-wise sampling of truncate(softmax(logits / T)) (temperature > 0) or argmax
+ * (temperature == 0): replaces _sample_arr / _pick (src/mlx_dspark/generate.py:135-146)
+ * and the DFlash draft sampling (generate.py:541-557). logits f32 [R, V]; uniforms use
+ * Philox counter row `row0 + r`. probs_out [R, V] f32 (the truncated distribution,
+ * needed as q by dsk_accept_sample) may be NULL. */
+int dsk_sample_rows(const float* logits, int64_t V, int R, float temperature, float top_p,
+                    int top_k, int mul_inv_t, uint64_t seed, uint32_t offset, int row0,
+                    int32_t* token_out, float* probs_out, dsk_stream_t stream);
+
+/* Device-side length update: lens[b] += (n ? n[b] : 0) + add. Advances a drafter context
+ * or KV length by the accepted count without a host round trip (the reference does this
+ * on the host: n_cached += n + 1, src/mlx_dspark/generate.py:938; ctx append of the
+ * accepted rows, :935-937). */
+int dsk_lens_add(int32_t* lens, const int32_t* n, int B, int add, dsk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSPARK_HIP_H */

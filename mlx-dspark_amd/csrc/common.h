@@ -1,0 +1,82 @@
+// Shared helpers for the gfx950 kernels behind include/dspark_hip.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "../../include/dspark_hip.h"
+
+namespace dsk {
+
+// ---- error reporting: a thread-local message per failing call ---------------------------
+void set_error(const char* fmt, ...);
+
+#define DSK_REQUIRE(cond, ...)              \
+  do {                                      \
+    if (!(cond)) {                          \
+      ::dsk::set_error(__VA_ARGS__);        \
+      return DSK_EINVAL;                    \
+    }                                       \
+  } while (0)
+
+#define DSK_LAUNCH_CHECK(what)                                                    \
+  do {                                                                            \
+    hipError_t e_ = hipGetLastError();                                            \
+    if (e_ != hipSuccess) {                                                       \
+      ::dsk::set_error("%s: launch failed: %s", what, hipGetErrorString(e_));     \
+      return DSK_ELAUNCH;                                                         \
+    }                                                                             \
+  } while (0)
+
+static inline hipStream_t as_stream(dsk_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---- vector types ---------------------------------------------------------------------
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---- bf16 <-> f32 (round to nearest even, as MLX/torch do) -----------------------------
+__host__ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+__host__ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);  // NaN stays NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+__host__ __device__ __forceinline__ uint32_t f32_bits(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  return u;
+}
+__host__ __device__ __forceinline__ float bits_f32(uint32_t u) {
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+// ---- wave-level reductions (wave64) ----------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace dsk

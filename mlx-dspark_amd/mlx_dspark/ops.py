@@ -1,0 +1,284 @@
+"""Tensor-level wrappers over libdspark_hip.so.
+
+Every function here launches hand-written gfx950 kernels through the C ABI on the current
+torch stream; torch only provides device memory and the stream. There is no CPU path: the
+tensors must live on a HIP device.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _hip
+from ._hip import (DSK_BF16, DSK_F32, DSK_KV_BF16, DSK_KV_U8, DSK_PACK_GELU, DSK_PACK_PLAIN,
+                   DSK_PACK_RMSNORM, DSK_PACK_SILU, call, ptr, stream_ptr)
+
+__all__ = [
+    "W8Weight", "W8Table", "Workspace", "act_pack", "w8_gemm", "w8_linear", "w8_embed",
+    "qkv_rope_append", "attention", "accept_greedy", "accept_sample", "sample_rows", "lens_add",
+    "rope_inv_freq", "DSK_PACK_PLAIN", "DSK_PACK_RMSNORM", "DSK_PACK_SILU", "DSK_PACK_GELU",
+    "DSK_KV_BF16", "DSK_KV_U8",
+]
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("dspark kernels need device tensors (got a CPU tensor)")
+
+
+# ----------------------------------------------------------------------------- workspace
+class Workspace:
+    """Per-device scratch for split-K partials and arrival counters.
+
+    The kernels leave every counter at zero when they return, so one zero-fill at allocation
+    is enough and a captured graph can replay without memsets. ``reserve`` grows a region;
+    growth is only legal outside graph capture (a warm-up call sizes everything first)."""
+
+    _per_device: dict[int, "Workspace"] = {}
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.buf: dict[str, torch.Tensor] = {}
+
+    @classmethod
+    def get(cls, device) -> "Workspace":
+        device = torch.device(device)
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        ws = cls._per_device.get(idx)
+        if ws is None:
+            ws = cls._per_device[idx] = Workspace(torch.device("cuda", idx))
+        return ws
+
+    def reserve(self, kind: str, nbytes: int) -> torch.Tensor:
+        t = self.buf.get(kind)
+        if t is not None and t.numel() >= nbytes:
+            return t
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"workspace '{kind}' must be sized before graph capture "
+                               f"(need {nbytes} bytes)")
+        nbytes = max(nbytes, 1 << 20)
+        t = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
+        self.buf[kind] = t
+        return t
+
+
+# ----------------------------------------------------------------------------- W8 weights
+@dataclass
+class W8Weight:
+    """A W8 affine group-64 matrix [N, K] in the engine's tiled layout (see w8.hip)."""
+
+    wt: torch.Tensor     # uint8 [N*K]
+    sb: torch.Tensor     # int32 [N, K/64] (bf16 scale | bf16 bias << 16)
+    N: int
+    K: int
+
+    @property
+    def nbytes(self) -> int:
+        return self.wt.numel() + self.sb.numel() * 4
+
+    @staticmethod
+    def quantize_mlx(w: torch.Tensor):
+        """w [N, K] f32/bf16 on device -> MLX-layout (q u8 [N, K], scales, biases bf16 [N, K/64])."""
+        _require_cuda(w)
+        w = w.contiguous()
+        N, K = w.shape
+        q = torch.empty((N, K), dtype=torch.uint8, device=w.device)
+        s = torch.empty((N, K // 64), dtype=torch.bfloat16, device=w.device)
+        b = torch.empty((N, K // 64), dtype=torch.bfloat16, device=w.device)
+        dt = DSK_BF16 if w.dtype == torch.bfloat16 else DSK_F32
+        if dt == DSK_F32 and w.dtype != torch.float32:
+            w = w.float()
+        call("dsk_w8_quantize", ptr(w), dt, N, K, ptr(q), ptr(s), ptr(b), stream_ptr())
+        return q, s, b
+
+    @classmethod
+    def from_mlx(cls, q: torch.Tensor, s: torch.Tensor, b: torch.Tensor) -> "W8Weight":
+        _require_cuda(q, s, b)
+        N, K = q.shape
+        wt = torch.empty(N * K, dtype=torch.uint8, device=q.device)
+        sb = torch.empty((N, K // 64), dtype=torch.int32, device=q.device)
+        call("dsk_w8_repack", ptr(q.contiguous()), ptr(s.contiguous()), ptr(b.contiguous()), N, K,
+             ptr(wt), ptr(sb), stream_ptr())
+        return cls(wt, sb, N, K)
+
+    @classmethod
+    def quantize(cls, w: torch.Tensor) -> "W8Weight":
+        q, s, b = cls.quantize_mlx(w)
+        return cls.from_mlx(q, s, b)
+
+
+@dataclass
+class W8Table:
+    """A W8 matrix kept in MLX row layout, for row gathers (embedding lookup)."""
+
+    q: torch.Tensor
+    s: torch.Tensor
+    b: torch.Tensor
+
+    @property
+    def shape(self):
+        return tuple(self.q.shape)
+
+    def dequantize(self) -> torch.Tensor:
+        V, H = self.q.shape
+        w = self.q.float().view(V, H // 64, 64) * self.s.float()[..., None] + self.b.float()[..., None]
+        return w.view(V, H)
+
+
+# ----------------------------------------------------------------------------- GEMM path
+def act_pack(x: torch.Tensor, mode: int = DSK_PACK_PLAIN, norm_w: torch.Tensor | None = None,
+             eps: float = 1e-6, K: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Pack bf16 activations [M, *] into the GEMM operand (optionally RMSNorm / SiLU / GeLU)."""
+    _require_cuda(x, norm_w)
+    if x.dtype != torch.bfloat16 or x.stride(-1) != 1:
+        raise ValueError("act_pack expects a bf16 tensor with unit column stride")
+    M = x.shape[0]
+    if K is None:
+        K = x.shape[1] // 2 if mode in (DSK_PACK_SILU, DSK_PACK_GELU) else x.shape[1]
+    nbytes = _hip.lib.dsk_act_pack_bytes(M, K)
+    if out is None:
+        out = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    elif out.numel() < nbytes:
+        raise ValueError("act_pack: output buffer too small")
+    call("dsk_act_pack", ptr(x), x.stride(0), M, K, mode, ptr(norm_w), float(eps), ptr(out), stream_ptr())
+    return out
+
+
+def w8_gemm(a: torch.Tensor, w: W8Weight, M: int, *, out: torch.Tensor | None = None,
+            out_dtype: torch.dtype = torch.bfloat16, residual: torch.Tensor | None = None,
+            softcap: float = 0.0) -> torch.Tensor:
+    """y[M, N] = residual + a . deq(W)^T (a from act_pack)."""
+    if out is None:
+        out = torch.empty((M, w.N), dtype=out_dtype, device=a.device)
+    yd = DSK_F32 if out.dtype == torch.float32 else DSK_BF16
+    ws = Workspace.get(a.device)
+    need = _hip.lib.dsk_w8_gemm_ws_bytes(M, w.N, w.K)
+    buf = ws.reserve("gemm", need)
+    call("dsk_w8_gemm", ptr(a), ptr(w.wt), ptr(w.sb), M, w.N, w.K, ptr(out), yd, out.stride(0),
+         ptr(residual), residual.stride(0) if residual is not None else 0, float(softcap),
+         ptr(buf), buf.numel(), stream_ptr())
+    return out
+
+
+def w8_linear(x: torch.Tensor, w: W8Weight, *, mode: int = DSK_PACK_PLAIN, norm_w=None, eps=1e-6,
+              out=None, out_dtype=torch.bfloat16, residual=None, softcap=0.0) -> torch.Tensor:
+    """act_pack + w8_gemm over rows in chunks of 64."""
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty((M, w.N), dtype=out_dtype, device=x.device)
+    for m0 in range(0, M, 64):
+        m1 = min(M, m0 + 64)
+        a = act_pack(x[m0:m1], mode, norm_w, eps, K=w.K)
+        w8_gemm(a, w, m1 - m0, out=out[m0:m1],
+                residual=None if residual is None else residual[m0:m1], softcap=softcap)
+    return out
+
+
+def w8_embed(ids: torch.Tensor, table: W8Table, scale: float = 1.0, out: torch.Tensor | None = None):
+    ids = ids.reshape(-1)
+    if ids.dtype != torch.int32:
+        ids = ids.to(torch.int32)
+    V, H = table.q.shape
+    n = ids.numel()
+    if out is None:
+        out = torch.empty((n, H), dtype=torch.bfloat16, device=ids.device)
+    call("dsk_w8_embed", ptr(ids), n, ptr(table.q), ptr(table.s), ptr(table.b), V, H, float(scale),
+         ptr(out), out.stride(0), stream_ptr())
+    return out
+
+
+# ----------------------------------------------------------------------------- attention
+def rope_inv_freq(head_dim: int, theta: float, device) -> torch.Tensor:
+    """theta ** (-2 d / head_dim) for d < head_dim / 2, computed in float64, stored f32."""
+    d = torch.arange(0, head_dim // 2, dtype=torch.float64)
+    return (theta ** (-2.0 * d / head_dim)).to(torch.float32).to(device)
+
+
+def qkv_rope_append(qkv, B, W, nq, nkv, hd, q_norm, k_norm, eps, inv_freq, seq_lens, block_table,
+                    page, kv_dtype, k_pool, v_pool, k_sb=None, v_sb=None, q_out=None, pos_offset=0):
+    if q_out is None:
+        q_out = torch.empty((B * W, nq * hd), dtype=torch.bfloat16, device=qkv.device)
+    call("dsk_qkv_rope_append", ptr(qkv), B, W, nq, nkv, hd, ptr(q_norm), ptr(k_norm), float(eps),
+         ptr(inv_freq), ptr(seq_lens), int(pos_offset), ptr(block_table), block_table.shape[1], page,
+         kv_dtype, ptr(k_pool), ptr(v_pool), ptr(k_sb), ptr(v_sb), ptr(q_out), stream_ptr())
+    return q_out
+
+
+def attention(q, B, W, nq, nkv, hd, scale, seq_lens, max_ctx, block_table, page, kv_dtype, k_pool,
+              v_pool, k_sb=None, v_sb=None, *, causal=True, window=0, softcap=0.0, out=None):
+    if out is None:
+        out = torch.empty((B * W, nq * hd), dtype=torch.bfloat16, device=q.device)
+    ws = Workspace.get(q.device)
+    need = _hip.lib.dsk_attn_ws_bytes(B, W, nq, hd, max_ctx)
+    buf = ws.reserve("attn", need)
+    call("dsk_attention", ptr(q), B, W, nq, nkv, hd, float(scale), int(bool(causal)), int(window),
+         float(softcap), ptr(seq_lens), int(max_ctx), ptr(block_table), block_table.shape[1], page,
+         kv_dtype, ptr(k_pool), ptr(v_pool), ptr(k_sb), ptr(v_sb), ptr(out), ptr(buf), buf.numel(),
+         stream_ptr())
+    return out
+
+
+# ----------------------------------------------------------------------------- acceptance
+def accept_greedy(logits: torch.Tensor, draft: torch.Tensor | None, *, seq_lens=None, tt=None,
+                  n_out=None, token_out=None):
+    """logits [B, W, V] (f32/bf16), draft [B, W-1] int32 -> (tt [B, W], n [B], token [B])."""
+    B, W, V = logits.shape
+    dev = logits.device
+    if logits.stride(2) != 1 or logits.stride(1) != V or logits.stride(0) != W * V:
+        logits = logits.contiguous()
+    tt = torch.empty((B, W), dtype=torch.int32, device=dev) if tt is None else tt
+    n_out = torch.empty(B, dtype=torch.int32, device=dev) if n_out is None else n_out
+    token_out = torch.empty(B, dtype=torch.int32, device=dev) if token_out is None else token_out
+    dt = DSK_BF16 if logits.dtype == torch.bfloat16 else DSK_F32
+    ws = Workspace.get(dev)
+    need = _hip.lib.dsk_accept_ws_bytes(B, W, V)
+    buf = ws.reserve("accept", need)
+    call("dsk_accept_greedy", ptr(logits), dt, V, B, W, V, ptr(draft), ptr(tt), ptr(n_out), ptr(token_out),
+         ptr(seq_lens), ptr(buf), buf.numel(), stream_ptr())
+    return tt, n_out, token_out
+
+
+def accept_sample(p_logits: torch.Tensor, q_logits: torch.Tensor | None, draft: torch.Tensor,
+                  temperature: float, top_p: float = 1.0, top_k: int = 0, *, q_mul_inv_t: bool = False,
+                  seed: int = 0, offset: int = 0, seq_lens=None, n_out=None, token_out=None,
+                  accept_out=None, sample_out=None):
+    """p_logits [B, L+1, V] f32, q_logits [B, L, V] f32 or None (one-hot q), draft [B, L] int32."""
+    B, R, V = p_logits.shape
+    L = R - 1
+    dev = p_logits.device
+    p_logits = p_logits.contiguous().float()
+    if q_logits is not None:
+        q_logits = q_logits.contiguous().float()
+    n_out = torch.empty(B, dtype=torch.int32, device=dev) if n_out is None else n_out
+    token_out = torch.empty(B, dtype=torch.int32, device=dev) if token_out is None else token_out
+    ws = Workspace.get(dev)
+    need = _hip.lib.dsk_accept_ws_bytes(B, R, V)
+    buf = ws.reserve("accept", need)
+    call("dsk_accept_sample", ptr(p_logits), ptr(q_logits), V, B, L, ptr(draft), float(temperature),
+         float(top_p), int(top_k or 0), int(bool(q_mul_inv_t)), int(seed) & ((1 << 64) - 1),
+         int(offset) & 0xFFFFFFFF, ptr(n_out), ptr(token_out), ptr(seq_lens), ptr(accept_out),
+         ptr(sample_out), ptr(buf), buf.numel(), stream_ptr())
+    return n_out, token_out
+
+
+def sample_rows(logits: torch.Tensor, temperature: float, top_p: float = 1.0, top_k: int = 0, *,
+                mul_inv_t: bool = False, seed: int = 0, offset: int = 0, row0: int = 0,
+                token_out=None, probs_out=None):
+    """logits [R, V] f32 -> tokens [R] (argmax at temperature 0) and the truncated probs."""
+    R, V = logits.shape
+    logits = logits.contiguous().float()
+    token_out = torch.empty(R, dtype=torch.int32, device=logits.device) if token_out is None else token_out
+    if temperature > 0 and probs_out is None:
+        probs_out = torch.empty((R, V), dtype=torch.float32, device=logits.device)
+    call("dsk_sample_rows", ptr(logits), V, R, float(temperature), float(top_p), int(top_k or 0),
+         int(bool(mul_inv_t)), int(seed) & ((1 << 64) - 1), int(offset) & 0xFFFFFFFF, int(row0),
+         ptr(token_out), ptr(probs_out), stream_ptr())
+    return token_out, probs_out
+
+
+def lens_add(lens: torch.Tensor, n: torch.Tensor | None, add: int) -> None:
+    call("dsk_lens_add", ptr(lens), ptr(n), lens.numel(), int(add), stream_ptr())

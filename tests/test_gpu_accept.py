@@ -1,0 +1,117 @@
+"""GPU parity: greedy and sampled acceptance are bit-identical to the oracle (decisions,
+sampled indices, rollback lengths), including the full [4, 17, 151936] acceptance config."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import accept as A
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(x, dev, dt=None):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dev) if dt is None else torch.from_numpy(np.ascontiguousarray(x)).to(dev, dt)
+
+
+@pytest.mark.parametrize("B,W,V,dtype", [(1, 16, 151936, "f32"), (2, 5, 1000, "f32"), (4, 9, 4099, "bf16"),
+                                         (3, 1, 77, "f32")])
+def test_accept_greedy_matches_oracle(dev, B, W, V, dtype):
+    from mlx_dspark.ops import accept_greedy
+    rng = np.random.default_rng(B * 100 + W)
+    logits = rng.integers(-3, 4, size=(B, W, V)).astype(np.float32)   # plenty of exact ties
+    tt_ref = logits.argmax(axis=2)
+    draft = tt_ref[:, : W - 1].copy().astype(np.int32)
+    for b in range(B):                                                  # break the match somewhere
+        k = rng.integers(0, W)
+        if k < W - 1:
+            draft[b, k] = (draft[b, k] + 1) % V
+    sl = rng.integers(0, 1000, size=B).astype(np.int32)
+    if dtype == "bf16":
+        lt = torch.from_numpy(logits).to(torch.bfloat16)
+        ref = A.accept_greedy(lt.view(torch.int16).numpy().view(np.uint16), draft, sl, bf16_bits_in=True)
+        lt = lt.to(dev)
+    else:
+        ref = A.accept_greedy(logits, draft, sl)
+        lt = _t(logits, dev)
+    sl_d = _t(sl, dev)
+    tt, n, tok = accept_greedy(lt, _t(draft, dev) if W > 1 else None, seq_lens=sl_d)
+    torch.cuda.synchronize()
+    assert np.array_equal(tt.cpu().numpy(), ref["tt"])
+    assert np.array_equal(n.cpu().numpy(), ref["n"])
+    assert np.array_equal(tok.cpu().numpy(), ref["token"])
+    assert np.array_equal(sl_d.cpu().numpy(), ref["seq_lens"])
+
+
+CASES = [
+    (2, 4, 1000, 1.0, 1.0, 0, False, False),
+    (2, 4, 1000, 0.7, 0.9, 0, False, False),
+    (2, 4, 1000, 1.0, 1.0, 50, True, False),
+    (3, 3, 2048, 1.3, 0.8, 20, False, False),
+    (2, 5, 999, 1.0, 0.95, 0, False, True),      # one-hot q (lookup drafts)
+    (1, 2, 64, 0.5, 0.0, 0, False, False),       # empty nucleus
+]
+
+
+@pytest.mark.parametrize("B,L,V,T,tp,tk,mulinv,onehot", CASES)
+def test_accept_sample_matches_oracle(dev, B, L, V, T, tp, tk, mulinv, onehot):
+    from mlx_dspark.ops import accept_sample
+    rng = np.random.default_rng(L * 31 + V)
+    q = (rng.standard_normal((B, L, V)) * 3).astype(np.float32)
+    p = np.concatenate([q + rng.standard_normal((B, L, V)).astype(np.float32),
+                        rng.standard_normal((B, 1, V)).astype(np.float32) * 3], axis=1)
+    # drafts: mostly the draft argmax (often accepted), some random
+    draft = q.argmax(axis=2).astype(np.int32)
+    draft[:, -1] = rng.integers(0, V, size=B)
+    sl = rng.integers(0, 500, size=B).astype(np.int32)
+    for seed, off in [(1, 0), (2**40 + 7, 123456)]:
+        ref = A.accept_sample(p, None if onehot else q, draft, T, tp, tk, mulinv, seed, off, sl)
+        sl_d = _t(sl, dev)
+        acc = torch.zeros((B, L), dtype=torch.uint8, device=dev)
+        smp = torch.zeros((B, L + 1), dtype=torch.int32, device=dev)
+        n, tok = accept_sample(_t(p, dev), None if onehot else _t(q, dev), _t(draft, dev), T, tp, tk,
+                               q_mul_inv_t=mulinv, seed=seed, offset=off, seq_lens=sl_d, accept_out=acc,
+                               sample_out=smp)
+        torch.cuda.synchronize()
+        assert np.array_equal(acc.cpu().numpy(), ref["accept"])
+        assert np.array_equal(smp.cpu().numpy(), ref["sample"])
+        assert np.array_equal(n.cpu().numpy(), ref["n"])
+        assert np.array_equal(tok.cpu().numpy(), ref["token"])
+        assert np.array_equal(sl_d.cpu().numpy(), ref["seq_lens"])
+
+
+def test_accept_sample_full_acceptance_config(dev):
+    """[4, 17, 151936] fp32: draft ~ N(0, 3^2), target = draft + N(0, 1), T=1, top_p=0.95."""
+    from mlx_dspark.ops import accept_sample
+    B, L, V = 4, 16, 151936
+    g = torch.Generator().manual_seed(2024)
+    q = torch.randn(B, L + 1, V, generator=g) * 3.0
+    p = q + torch.randn(B, L + 1, V, generator=g)
+    qn, pn = q[:, :L].contiguous().numpy(), p.numpy()
+    draft = qn.argmax(axis=2).astype(np.int32)
+    ref = A.accept_sample(pn, qn, draft, 1.0, 0.95, 0, False, 7, 11, np.zeros(B, np.int32))
+    acc = torch.zeros((B, L), dtype=torch.uint8, device=dev)
+    smp = torch.zeros((B, L + 1), dtype=torch.int32, device=dev)
+    sl = torch.zeros(B, dtype=torch.int32, device=dev)
+    n, tok = accept_sample(p.to(dev), q[:, :L].to(dev), _t(draft, dev), 1.0, 0.95, 0, seed=7, offset=11,
+                           seq_lens=sl, accept_out=acc, sample_out=smp)
+    torch.cuda.synchronize()
+    assert np.array_equal(acc.cpu().numpy(), ref["accept"])
+    assert np.array_equal(smp.cpu().numpy(), ref["sample"])
+    assert np.array_equal(n.cpu().numpy(), ref["n"])
+    assert np.array_equal(tok.cpu().numpy(), ref["token"])
+    assert np.array_equal(sl.cpu().numpy(), ref["seq_lens"])
+
+
+@pytest.mark.parametrize("T,tp,tk,mulinv", [(0.0, 1.0, 0, False), (1.0, 1.0, 0, False), (0.7, 0.9, 40, True)])
+def test_sample_rows_matches_oracle(dev, T, tp, tk, mulinv):
+    from mlx_dspark.ops import sample_rows
+    rng = np.random.default_rng(5)
+    R, V = 6, 5000
+    logits = (rng.standard_normal((R, V)) * 2).astype(np.float32)
+    ref_tok, ref_p = A.sample_rows(logits, T, tp, tk, mulinv, seed=99, offset=3, row0=4)
+    tok, pr = sample_rows(_t(logits, dev), T, tp, tk, mul_inv_t=mulinv, seed=99, offset=3, row0=4)
+    torch.cuda.synchronize()
+    assert np.array_equal(tok.cpu().numpy(), ref_tok)
+    if T > 0:
+        assert np.array_equal(pr.cpu().numpy(), ref_p)

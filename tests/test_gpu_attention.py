@@ -1,0 +1,132 @@
+"""GPU parity: q/k RMSNorm + RoPE + paged KV append, and split-K paged attention
+(causal-with-offset and bidirectional, bf16 and 8-bit KV) against float32 references."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import w8 as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _rope_ref(x, pos, inv_freq):
+    # x [..., hd] float32; rotate-half
+    hd = x.shape[-1]
+    ang = pos[:, None].float() * inv_freq[None, :]                  # [n, hd/2]
+    c, s = torch.cos(ang), torch.sin(ang)
+    x1, x2 = x[..., : hd // 2], x[..., hd // 2:]
+    while c.dim() < x1.dim():
+        c, s = c.unsqueeze(1), s.unsqueeze(1)
+    return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1)
+
+
+def _rms(x, w, eps):
+    return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) * w
+
+
+class Pool:
+    def __init__(self, B, nkv, hd, max_ctx, page, kv_dtype, dev, seed=0):
+        self.page = page
+        self.max_pages = (max_ctx + page - 1) // page
+        n_pages = B * self.max_pages + 3
+        g = torch.Generator().manual_seed(seed)
+        perm = torch.randperm(n_pages, generator=g)[: B * self.max_pages]
+        self.block_table = perm.view(B, self.max_pages).to(torch.int32).to(dev)   # shuffled pages
+        shape = (n_pages, nkv, page, hd)
+        if kv_dtype == 0:
+            self.k = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+            self.v = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+            self.ksb = self.vsb = None
+        else:
+            self.k = torch.zeros(shape, dtype=torch.uint8, device=dev)
+            self.v = torch.zeros(shape, dtype=torch.uint8, device=dev)
+            self.ksb = torch.zeros((n_pages, nkv, page, hd // 64), dtype=torch.int32, device=dev)
+            self.vsb = torch.zeros_like(self.ksb)
+        self.kv_dtype = kv_dtype
+
+    def read(self, b, n, which):
+        """token-major [n, nkv, hd] float32 values as stored (dequantized for u8)."""
+        bt = self.block_table[b].cpu()
+        pool = self.k if which == "k" else self.v
+        sb = self.ksb if which == "k" else self.vsb
+        rows = []
+        for j in range(n):
+            p = int(bt[j // self.page])
+            if self.kv_dtype == 0:
+                rows.append(pool[p, :, j % self.page].float().cpu())
+            else:
+                q = pool[p, :, j % self.page].cpu().numpy()
+                s = sb[p, :, j % self.page].cpu().numpy().view(np.uint32)
+                sc = O.bits_to_f32((s & 0xFFFF).astype(np.uint16))
+                bi = O.bits_to_f32((s >> 16).astype(np.uint16))
+                hd = q.shape[-1]
+                val = q.reshape(q.shape[0], hd // 64, 64).astype(np.float32) * sc[..., None] + bi[..., None]
+                rows.append(torch.from_numpy(O.bf16_round(val.reshape(q.shape[0], hd))))
+        return torch.stack(rows)
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+@pytest.mark.parametrize("B,W,L0,causal", [(1, 16, 0, True), (1, 16, 700, True), (2, 9, 37, True),
+                                           (1, 1, 300, True), (2, 8, 130, False), (1, 64, 64, True)])
+def test_append_and_attention(dev, kv_dtype, B, W, L0, causal):
+    from mlx_dspark.ops import attention, qkv_rope_append, rope_inv_freq
+    print(f"attn kv={kv_dtype} B={B} W={W} L0={L0} causal={causal}", flush=True)
+    nq, nkv, hd, page = 8, 2, 128, 64
+    eps, theta = 1e-6, 1e6
+    g = torch.Generator().manual_seed(B * 1000 + W * 10 + L0)
+    max_ctx = L0 + W + 5
+    pool = Pool(B, nkv, hd, max_ctx, page, kv_dtype, dev, seed=L0 + W)
+    inv = rope_inv_freq(hd, theta, dev)
+    qn = (1 + 0.1 * torch.randn(hd, generator=g)).to(torch.bfloat16)
+    kn = (1 + 0.1 * torch.randn(hd, generator=g)).to(torch.bfloat16)
+    nh = nq + 2 * nkv
+    zeros = torch.zeros(B, dtype=torch.int32, device=dev)
+    # prefix tokens (previous rounds), then the W new tokens
+    if L0:
+        pre = (torch.randn(B * L0, nh * hd, generator=g)).to(torch.bfloat16).to(dev)
+        qkv_rope_append(pre, B, L0, nq, nkv, hd, qn.to(dev), kn.to(dev), eps, inv, zeros, pool.block_table, page,
+                        kv_dtype, pool.k, pool.v, pool.ksb, pool.vsb)
+    qkv = (torch.randn(B * W, nh * hd, generator=g)).to(torch.bfloat16)
+    sl = torch.full((B,), L0, dtype=torch.int32, device=dev)
+    q = qkv_rope_append(qkv.to(dev), B, W, nq, nkv, hd, qn.to(dev), kn.to(dev), eps, inv, sl, pool.block_table,
+                        page, kv_dtype, pool.k, pool.v, pool.ksb, pool.vsb)
+    scale = hd ** -0.5
+    out = attention(q, B, W, nq, nkv, hd, scale, sl, max_ctx, pool.block_table, page, kv_dtype, pool.k, pool.v,
+                    pool.ksb, pool.vsb, causal=causal)
+    torch.cuda.synchronize()
+
+    # append check: q and the newly stored K/V against the float32 prologue
+    invc = inv.cpu()
+    x = qkv.float().view(B, W, nh, hd)
+    pos = (torch.arange(W) + L0)
+    for b in range(B):
+        qr = _rope_ref(_rms(x[b, :, :nq], qn.float(), eps), pos, invc)
+        assert (q.view(B, W, nq, hd)[b].float().cpu() - qr).abs().max() < 0.05
+        kr = _rope_ref(_rms(x[b, :, nq:nq + nkv], kn.float(), eps), pos, invc)
+        vr = x[b, :, nq + nkv:]
+        ks = pool.read(b, L0 + W, "k")[L0:]
+        vs = pool.read(b, L0 + W, "v")[L0:]
+        tol = 0.05 if kv_dtype == 0 else 0.1
+        assert (ks - kr).abs().max() < tol
+        assert (vs - vr).abs().max() < tol
+
+    # attention check against the stored K/V
+    G = nq // nkv
+    for b in range(B):
+        K = pool.read(b, L0 + W, "k")          # [Lk, nkv, hd]
+        V = pool.read(b, L0 + W, "v")
+        qb = q.view(B, W, nq, hd)[b].float().cpu()
+        ref = torch.empty(W, nq, hd)
+        for h in range(nq):
+            s = (qb[:, h] @ K[:, h // G].T) * scale          # [W, Lk]
+            if causal:
+                j = torch.arange(L0 + W)[None, :]
+                i = torch.arange(W)[:, None]
+                s = s.masked_fill(j > L0 + i, float("-inf"))
+            ref[:, h] = torch.softmax(s, -1) @ V[:, h // G]
+        got = out.view(B, W, nq, hd)[b].float().cpu()
+        err = (got - ref).abs().max().item()
+        assert err < 2e-2, err

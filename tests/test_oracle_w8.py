@@ -1,0 +1,37 @@
+"""CPU checks for the W8 oracle: round-trip bound, brute-force GEMM, degenerate groups."""
+
+import numpy as np
+
+from oracle import w8
+
+
+def test_quantize_roundtrip_within_half_step():
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((32, 256)) * 0.02).astype(np.float32)
+    q, s, b = w8.quantize(w)
+    deq = w8.dequantize(q, s, b)
+    step = w8.bits_to_f32(s).astype(np.float64)
+    err = np.abs(deq - w).reshape(32, 4, 64).max(axis=2)
+    # half a step, plus the bf16 rounding of scale and bias (relative 2^-8 of the range)
+    assert np.all(err <= step * 0.5 + step * 255 * 2**-8 + np.abs(w8.bits_to_f32(b)) * 2**-8 + 1e-9)
+
+
+def test_constant_group_uses_unit_scale():
+    w = np.full((1, 64), 0.5, np.float32)
+    q, s, b = w8.quantize(w)
+    assert s[0, 0] == 0x3F80 and np.all(q == 0)
+    assert np.allclose(w8.dequantize(q, s, b), 0.5)
+
+
+def test_gemm_matches_bruteforce_dot():
+    rng = np.random.default_rng(1)
+    w = rng.standard_normal((8, 128)).astype(np.float32)
+    x = rng.standard_normal((3, 128)).astype(np.float32)
+    q, s, b = w8.quantize(w)
+    y = w8.gemm(x, q, s, b)
+    sf = w8.bits_to_f32(s).astype(np.float64)
+    bf = w8.bits_to_f32(b).astype(np.float64)
+    for m in range(3):
+        for n in range(8):
+            ref = sum(float(x[m, k]) * (sf[n, k // 64] * int(q[n, k]) + bf[n, k // 64]) for k in range(128))
+            assert abs(y[m, n] - ref) < 1e-9 * max(1.0, abs(ref))
