@@ -1,0 +1,285 @@
+#!/usr/bin/env python
+"""Benchmark of the speculative-decoding verify engine on one MI355X.
+
+Workload (the config the headline metric is quoted on): a Qwen3-8B-shaped random-init W8
+target (36 layers, hidden 4096, 32 q / 8 kv heads, head_dim 128, SwiGLU 12288, vocab 151936)
+with a 2-layer DFlash block-diffusion drafter conditioned on 5 evenly spaced target layers;
+batch 1, a seeded 4096-token context, the full 16-position block verified every round
+(anchor + 15 drafts), 8-bit affine KV cache (group 64), greedy acceptance.
+
+A "step" is one speculative round: draft the block, verify it in one target forward, accept,
+roll the KV back and grow the drafter context. Rounds from the second on are one HIP-graph
+replay each. Printed (one JSON line):
+  value        accepted tokens per second over the timed rounds (with random weights the
+               drafter almost never matches, so ~1 token per round: accept length is reported)
+  verify_us    one verify forward (16 rows, 4096 context), graph-replayed, HIP events
+  verify_roofline_frac  algorithmic bytes of that forward / verify_us / 8 TB/s
+  roofline     the W8 GEMM kernel (the dominant kernel): algorithmic bytes per launch over
+               its average launch duration, timed per launch with HIP events
+  cpu_baseline the CPU oracle (torch, float32) on a bounded sample: one decoder layer and the
+               vocabulary head of the verify step, scaled to a whole round
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "mlx-dspark_amd"))
+sys.path.insert(0, str(REPO))
+
+PEAK_HBM_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def kv_bytes_per_token(args, kv_bits) -> int:
+    per_head = args.head_dim * 2 if kv_bits is None else args.head_dim + 4 * (args.head_dim // 64)
+    return 2 * per_head * args.num_key_value_heads * args.num_hidden_layers
+
+
+def gemm_roofline(model, M: int, reps_per_shape: int | None = None):
+    """Average launch duration of the W8 GEMM kernel at every verify-step shape, each launch
+    bracketed by its own pair of HIP events on the launch stream, weights rotating through
+    the 36 layers so every launch streams its weights from HBM."""
+    import torch
+    from mlx_dspark import ops
+
+    dev = model.device
+    shapes = {"qkv": [L.qkv for L in model.layers], "o": [L.o for L in model.layers],
+              "gate_up": [L.gate_up for L in model.layers], "down": [L.down for L in model.layers],
+              "lm_head": [model.lm_head]}
+    res = {}
+    tot_bytes = tot_us = 0.0
+    tot_launch = 0
+    per_step = {"qkv": len(model.layers), "o": len(model.layers), "gate_up": len(model.layers),
+                "down": len(model.layers), "lm_head": 1}
+    filler = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+    for name, ws in shapes.items():
+        K = ws[0].K
+        x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+        a = ops.act_pack(x)
+        y = torch.empty(M, ws[0].N, device=dev, dtype=torch.bfloat16)
+        for w in ws[:2]:
+            ops.w8_gemm(a, w, M, out=y)                           # size the workspace
+        n = reps_per_shape or max(len(ws), 8)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        torch.cuda.synchronize()
+        filler.zero_()                                            # keeps the GPU busy while we enqueue
+        for i in range(n):
+            ev[i][0].record()
+            ops.w8_gemm(a, ws[i % len(ws)], M, out=y)
+            ev[i][1].record()
+        torch.cuda.synchronize()
+        us = statistics.mean(s.elapsed_time(e) * 1e3 for s, e in ev)
+        by = ws[0].N * ws[0].K * 1.0625
+        res[name] = {"us": round(us, 2), "bytes": int(by), "GBs": round(by / us / 1e3, 1)}
+        tot_bytes += by * per_step[name]
+        tot_us += us * per_step[name]
+        tot_launch += per_step[name]
+    del filler
+    return res, tot_bytes / tot_launch, tot_us / tot_launch
+
+
+def cpu_baseline(tgt_args, dev_model_seed: int, ctx: int, W: int, mean_accept: float, budget_s: float = 12.0):
+    """The oracle (torch on the host CPU, float32 with bf16 rounding points) on one decoder
+    layer + the vocabulary head of one verify step at the same shapes; a round is scaled as
+    (target layers + drafter layers) * t_layer + 2 * t_head (target verify head + drafter head)."""
+    import types
+
+    import numpy as np
+    import torch
+
+    from mlx_dspark import synthetic
+    from oracle import model as OM
+
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    a = tgt_args
+    H, I = a.hidden_size, a.intermediate_size
+    nq, nkv, hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
+
+    def mlx(N, K, name):
+        w = synthetic.randn((N, K), dev_model_seed, name, "cuda")
+        from mlx_dspark.ops import W8Weight
+        q, s, b = W8Weight.quantize_mlx(w)
+        o = types.SimpleNamespace(mlx=(q.cpu(), s.cpu(), b.cpu()))
+        return o
+
+    ones = lambda n: torch.ones(n, dtype=torch.bfloat16)
+    qk = lambda: torch.full((hd,), hd ** -0.25).to(torch.bfloat16)
+    layer = types.SimpleNamespace(qkv=mlx(a.n_qkv, H, "layers.0.qkv"), o=mlx(H, nq * hd, "layers.0.o"),
+                                  gate_up=mlx(2 * I, H, "layers.0.gate_up"), down=mlx(H, I, "layers.0.down"),
+                                  in_norm=ones(H), post_norm=ones(H), q_norm=qk(), k_norm=qk())
+    emb = mlx(a.vocab_size, H, "embed_tokens").mlx
+    head = mlx(a.vocab_size, H, "lm_head")
+    m = types.SimpleNamespace(args=a, layers=[layer], embed=types.SimpleNamespace(q=emb[0], s=emb[1], b=emb[2]),
+                              lm_head=head, norm=ones(H))
+    ref = OM.OracleTarget(m)
+    g = torch.Generator().manual_seed(0)
+    t_all, t_head = [], []
+    ids = torch.randint(0, a.vocab_size, (W,), generator=g)
+    t_start = time.perf_counter()
+    while len(t_all) < 3 or time.perf_counter() - t_start < budget_s:
+        ref.K = [OM.bf(torch.randn(ctx, nkv, hd, generator=g))]
+        ref.V = [OM.bf(torch.randn(ctx, nkv, hd, generator=g))]
+        ref.offset = ctx
+        t0 = time.perf_counter()
+        ref.forward(ids)
+        t_all.append(time.perf_counter() - t0)
+        x = torch.randn(W, H, generator=g)
+        t0 = time.perf_counter()
+        _ = OM.bf(x) @ ref.lm_head.T
+        t_head.append(time.perf_counter() - t0)
+    ta, th = statistics.median(t_all), statistics.median(t_head)
+    t_layer = max(ta - th, 1e-6)
+    n_layers_round = a.num_hidden_layers + 2
+    t_round = n_layers_round * t_layer + 2 * th
+    sample_s = sum(t_all) + sum(t_head)
+    return {"value": round(mean_accept / t_round, 4), "unit": "accepted tok/s", "cores": ncores, "kind": "port",
+            "sample": (f"oracle (torch fp32, bf16 rounding points) timed on 1 of {a.num_hidden_layers} decoder "
+                       f"layers + the {a.vocab_size}-row head for one {W}-row verify at {ctx} context "
+                       f"(median of {len(t_all)}, {sample_s:.1f} s of CPU work); round = "
+                       f"{n_layers_round} layers x {t_layer * 1e3:.1f} ms + 2 heads x {th * 1e3:.1f} ms = "
+                       f"{t_round * 1e3:.0f} ms, x mean accept length {mean_accept:.2f}")}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--block", type=int, default=16)
+    ap.add_argument("--kv-bits", type=int, default=8, choices=[0, 8])
+    ap.add_argument("--target", default="qwen3-8b")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--verify-reps", type=int, default=50)
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this engine has no multi-GPU path (run with --gpus 1)",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from mlx_dspark import ops, synthetic
+    from mlx_dspark.generate import _DFlashRound, _pick
+    from mlx_dspark.target import Target
+    from mlx_dspark.tokenizer import SyntheticTokenizer
+
+    kv_bits = args.kv_bits or None
+    torch.cuda.init()
+    t_build = time.time()
+    model = synthetic.build_target(args.target, seed=0)
+    drafter, dcfg = synthetic.build_dflash(model.args, seed=1, block_size=args.block, n_taps=5)
+    drafter.bind(model)
+    log(f"built {args.target} W8 target ({model.weight_bytes / 1e9:.2f} GB) + DFlash drafter in "
+        f"{time.time() - t_build:.1f} s")
+    tok = SyntheticTokenizer(model.args.vocab_size)
+    target = Target(model, tok, kv_bits=kv_bits)
+    cap = args.block - 1
+    W = cap + 1
+    rounds_total = args.steps + args.warmup + 2
+    max_ctx = args.ctx + W * (rounds_total + 2) + 64
+    cache = target.make_cache(max_ctx=max_ctx)
+    dcache = drafter.make_cache(max_ctx=max_ctx)
+    prompt = np.random.default_rng(1234).integers(0, model.args.vocab_size, args.ctx).tolist()
+    t0 = time.time()
+    tap = list(dcfg.target_layer_ids)
+    logits, fused = model.prefill(prompt, cache, tap)
+    drafter.ingest(fused, dcache)
+    pending = _pick(logits[0, -1], 0.0)
+    torch.cuda.synchronize()
+    log(f"prefill {args.ctx} tokens: {time.time() - t0:.1f} s")
+
+    rnd = _DFlashRound(target, drafter, cache, dcache, cap, 0.0, 1.0, 0, 0)
+    rnd.pending.fill_(pending)
+    for r in range(args.warmup):
+        rnd.run(r, use_graph=True)
+    torch.cuda.synchronize()
+    accepted = []
+    t0 = time.perf_counter()
+    for r in range(args.steps):
+        n, token, _ = rnd.run(args.warmup + r, use_graph=True)
+        accepted.append(n + 1)
+    torch.cuda.synchronize()
+    secs = time.perf_counter() - t0
+    ms_per_step = secs / args.steps * 1e3
+    tok_s = sum(accepted) / secs
+    mean_accept = sum(accepted) / len(accepted)
+    log(f"{args.steps} rounds: {ms_per_step:.3f} ms/round, {tok_s:.1f} accepted tok/s, accept {mean_accept:.2f}")
+
+    # ---- verify step alone: one graph of the 16-row target forward (no advance: idempotent)
+    L_now = cache.lengths[0]
+    vids = torch.randint(0, model.args.vocab_size, (1, W), dtype=torch.int32, device=model.device)
+    vl = torch.empty((W, model.args.vocab_size), dtype=torch.float32, device=model.device)
+    vf = torch.empty((W, len(tap) * model.args.hidden_size), dtype=torch.bfloat16, device=model.device)
+    model.forward(vids, cache, tap, advance=False, logits_out=vl, fused_out=vf)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        model.forward(vids, cache, tap, advance=False, logits_out=vl, fused_out=vf)
+    for _ in range(3):
+        g.replay()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s_ev.record()
+    for _ in range(args.verify_reps):
+        g.replay()
+    e_ev.record()
+    torch.cuda.synchronize()
+    verify_us = s_ev.elapsed_time(e_ev) * 1e3 / args.verify_reps
+    kvpt = kv_bytes_per_token(model.args, kv_bits)
+    alg_bytes = model.weight_bytes + kvpt * L_now + kvpt * W + W * model.args.vocab_size * 4
+    verify_frac = alg_bytes / (verify_us * 1e-6) / (PEAK_HBM_GBS * 1e9)
+    log(f"verify step: {verify_us:.1f} us for {alg_bytes / 1e9:.3f} GB algorithmic "
+        f"-> {alg_bytes / verify_us / 1e3:.0f} GB/s ({verify_frac * 100:.1f}% of HBM roofline)")
+
+    # ---- dominant kernel: the W8 GEMM
+    shapes, bytes_per_launch, us_per_launch = gemm_roofline(model, W)
+    achieved = bytes_per_launch / us_per_launch / 1e3
+    log(f"W8 GEMM per shape: {json.dumps(shapes)}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        t0 = time.time()
+        cpu = cpu_baseline(model.args, 0, args.ctx, W, mean_accept)
+        log(f"cpu baseline in {time.time() - t0:.1f} s: {cpu}")
+
+    line = {
+        "metric": "accepted tok/s (B=1, Qwen3-8B-shape W8, k=16); verify-step us; % HBM roofline",
+        "value": round(tok_s, 2), "unit": "accepted tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded random-init W8 weights, seeded 4096-token context)",
+        "config": {"workload": "qwen3-8b-shape W8 target + 2-layer DFlash drafter, B=1, "
+                               f"{args.ctx}-token context, verify block {W} (k=16), "
+                               f"{'8-bit' if kv_bits else 'bf16'} KV, greedy",
+                   "global_batch": 1, "seq_len": args.ctx, "parallelism": "single GPU",
+                   "weights": "W8 affine group 64 (bf16 scale/bias)"},
+        "accept_len": round(mean_accept, 3),
+        "verify_us": round(verify_us, 1),
+        "verify_alg_bytes": int(alg_bytes),
+        "verify_roofline_frac": round(verify_frac, 4),
+        "roofline": {"kernel": "w8_gemm_kernel (W8 skinny GEMM, M=16)", "bound": "hbm",
+                     "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "bytes_per_launch": int(bytes_per_launch), "us_per_launch": round(us_per_launch, 2),
+                     "per_shape": shapes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

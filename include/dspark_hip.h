@@ -128,7 +128,8 @@ int dsk_w8_embed(const int32_t* ids, int n, const uint8_t* q, const uint16_t* sc
  * (inv_freq [hd/2] f32), K/V appended to the pool at that position, and
  * q_out [B*W, nq*hd] bf16. Replaces the Qwen3 attention prologue inside mlx_lm and
  * DSparkAttention._kv/update_ctx (src/mlx_dspark/model.py:113-128). k_norm may be NULL
- * (no norm). pos_offset is added to every position. */
+ * (no norm). pos_offset is added to every position. nq may be 0 (K/V rows only, as for a
+ * drafter's context rows; q_out may then be NULL). */
 int dsk_qkv_rope_append(const uint16_t* qkv, int B, int W, int nq, int nkv, int hd,
                         const uint16_t* q_norm, const uint16_t* k_norm, float eps,
                         const float* inv_freq, const int32_t* seq_lens, int pos_offset,

@@ -160,52 +160,74 @@ struct AttnArgs {
 constexpr int kKeyTile = 32;
 template <int HD> struct Lds { static constexpr int KROW = HD + 8, VROW = kKeyTile + 8; };
 
+// K/V tile staging, split into a global->register load (issued one tile ahead) and a
+// register->LDS store (dequantising 8-bit KV to bf16).
 template <int HD>
-__device__ __forceinline__ void stage_kv(const AttnArgs& a, int b, int kvh, int j0, int Lk, uint16_t* ks,
-                                         uint16_t* vt) {
-  // ks: [32 keys][KROW] bf16 row-major; vt: [HD][VROW] bf16 (transposed V), rows padded.
-  constexpr int CHUNKS = kKeyTile * HD / 8;  // 8 bf16 per chunk
-  for (int c = threadIdx.x; c < CHUNKS; c += 256) {
+struct KVRegs {
+  static constexpr int CPT = kKeyTile * HD / 8 / 256;  // 8-element chunks per thread
+  u32x4 k[CPT], v[CPT];
+  uint32_t ksb[CPT], vsb[CPT];
+  bool valid[CPT];
+};
+
+template <int HD>
+__device__ __forceinline__ void load_kv(const AttnArgs& a, int b, int kvh, int j0, int Lk, KVRegs<HD>& r) {
+#pragma unroll
+  for (int ci = 0; ci < KVRegs<HD>::CPT; ++ci) {
+    const int c = threadIdx.x + ci * 256;
     const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
     const int j = j0 + key;
-    float kv8[8], vv8[8];
-    if (j < Lk) {
-      const int pg = a.block_table[(int64_t)b * a.max_pages + j / a.page];
-      const int64_t tok = ((int64_t)pg * a.nkv + kvh) * a.page + (j % a.page);
-      if (a.kv_dtype == DSK_KV_BF16) {
-        const u32x4 kr = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.k_pool) + tok * HD + d0);
-        const u32x4 vr = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.v_pool) + tok * HD + d0);
-        *reinterpret_cast<u32x4*>(ks + key * Lds<HD>::KROW + d0) = kr;
-        const uint16_t* vh = reinterpret_cast<const uint16_t*>(&vr);
+    r.valid[ci] = j < Lk;
+    if (!r.valid[ci]) continue;
+    const int pg = a.block_table[(int64_t)b * a.max_pages + j / a.page];
+    const int64_t tok = ((int64_t)pg * a.nkv + kvh) * a.page + (j % a.page);
+    if (a.kv_dtype == DSK_KV_BF16) {
+      r.k[ci] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.k_pool) + tok * HD + d0);
+      r.v[ci] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.v_pool) + tok * HD + d0);
+    } else {
+      const uint2 kr = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.k_pool) + tok * HD + d0);
+      const uint2 vr = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.v_pool) + tok * HD + d0);
+      r.k[ci] = u32x4{kr.x, kr.y, 0, 0};
+      r.v[ci] = u32x4{vr.x, vr.y, 0, 0};
+      r.ksb[ci] = a.k_sb[tok * (HD / 64) + d0 / 64];
+      r.vsb[ci] = a.v_sb[tok * (HD / 64) + d0 / 64];
+    }
+  }
+}
+
+template <int HD>
+__device__ __forceinline__ void store_kv(const AttnArgs& a, const KVRegs<HD>& r, uint16_t* ks, uint16_t* vt) {
+  // ks: [32 keys][KROW] bf16 row-major; vt: [HD][VROW] bf16 (transposed V), rows padded.
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vt[(d0 + e) * Lds<HD>::VROW + key] = vh[e];
-        continue;
-      }
-      const uint8_t* kq = reinterpret_cast<const uint8_t*>(a.k_pool) + tok * HD + d0;
-      const uint8_t* vq = reinterpret_cast<const uint8_t*>(a.v_pool) + tok * HD + d0;
-      const uint32_t ksb = a.k_sb[tok * (HD / 64) + d0 / 64];
-      const uint32_t vsb = a.v_sb[tok * (HD / 64) + d0 / 64];
-      const float kscale = bf16_to_f32((uint16_t)(ksb & 0xffff)), kbias = bf16_to_f32((uint16_t)(ksb >> 16));
-      const float vscale = bf16_to_f32((uint16_t)(vsb & 0xffff)), vbias = bf16_to_f32((uint16_t)(vsb >> 16));
-      const uint2 kr = *reinterpret_cast<const uint2*>(kq);
-      const uint2 vr = *reinterpret_cast<const uint2*>(vq);
-      const uint8_t* kb = reinterpret_cast<const uint8_t*>(&kr);
-      const uint8_t* vb = reinterpret_cast<const uint8_t*>(&vr);
+  for (int ci = 0; ci < KVRegs<HD>::CPT; ++ci) {
+    const int c = threadIdx.x + ci * 256;
+    const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+    uint16_t kh[8], vh[8];
+    if (!r.valid[ci]) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kh[e] = vh[e] = 0;
+    } else if (a.kv_dtype == DSK_KV_BF16) {
+      const uint16_t* kk = reinterpret_cast<const uint16_t*>(&r.k[ci]);
+      const uint16_t* vv = reinterpret_cast<const uint16_t*>(&r.v[ci]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        kv8[e] = fmaf(kscale, (float)kb[e], kbias);
-        vv8[e] = fmaf(vscale, (float)vb[e], vbias);
+        kh[e] = kk[e];
+        vh[e] = vv[e];
       }
     } else {
+      const float ksc = bf16_to_f32((uint16_t)(r.ksb[ci] & 0xffff)), kbi = bf16_to_f32((uint16_t)(r.ksb[ci] >> 16));
+      const float vsc = bf16_to_f32((uint16_t)(r.vsb[ci] & 0xffff)), vbi = bf16_to_f32((uint16_t)(r.vsb[ci] >> 16));
+      const uint8_t* kb = reinterpret_cast<const uint8_t*>(&r.k[ci]);
+      const uint8_t* vb = reinterpret_cast<const uint8_t*>(&r.v[ci]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) kv8[e] = vv8[e] = 0.0f;
+      for (int e = 0; e < 8; ++e) {
+        kh[e] = f32_to_bf16(fmaf(ksc, (float)kb[e], kbi));
+        vh[e] = f32_to_bf16(fmaf(vsc, (float)vb[e], vbi));
+      }
     }
-    uint16_t kh[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) kh[e] = f32_to_bf16(kv8[e]);
     *reinterpret_cast<u32x4*>(ks + key * Lds<HD>::KROW + d0) = *reinterpret_cast<const u32x4*>(kh);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) vt[(d0 + e) * Lds<HD>::VROW + key] = f32_to_bf16(vv8[e]);
+    for (int e = 0; e < 8; ++e) vt[(d0 + e) * Lds<HD>::VROW + key] = vh[e];
   }
 }
 
@@ -249,9 +271,12 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     lrow[t] = 0.0f;
   }
 
+  KVRegs<HD> kvr;
+  if (j_lo < j_hi) load_kv<HD>(a, b, kvh, j_lo, j_hi, kvr);
   for (int j0 = j_lo; j0 < j_hi; j0 += kKeyTile) {
     __syncthreads();
-    stage_kv<HD>(a, b, kvh, j0, j_hi, ks, vt);
+    store_kv<HD>(a, kvr, ks, vt);
+    if (j0 + kKeyTile < j_hi) load_kv<HD>(a, b, kvh, j0 + kKeyTile, j_hi, kvr);  // next tile in flight
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < QT; ++t) {
@@ -351,21 +376,44 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   __syncthreads();
   if (!last) return;
   __threadfence();
-  // combine the splits in fixed order
+  // combine the splits: lanes own splits for the max / denominator, then dims for the sum
   const float* base = a.part + ((size_t)bk * a.nsplit * a.R) * rstride;
   for (int r = wv; r < a.R; r += 4) {
     float M = -__builtin_inff();
-    for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, __builtin_nontemporal_load(base + ((size_t)s * a.R + r) * rstride + HD));
+    for (int s = lane; s < a.nsplit; s += 64)
+      M = fmaxf(M, __builtin_nontemporal_load(base + ((size_t)s * a.R + r) * rstride + HD));
+    M = wave_max(M);
     float den = 0.0f;
+    for (int s = lane; s < a.nsplit; s += 64) {
+      const float* pr = base + ((size_t)s * a.R + r) * rstride;
+      const float ms = __builtin_nontemporal_load(pr + HD);
+      if (ms != -__builtin_inff()) den += __expf(ms - M) * __builtin_nontemporal_load(pr + HD + 1);
+    }
+    den = wave_sum(den);
     float acc[HD / 64];
 #pragma unroll
     for (int e = 0; e < HD / 64; ++e) acc[e] = 0.0f;
-    for (int s = 0; s < a.nsplit; ++s) {
+    int s = 0;
+    for (; s + 8 <= a.nsplit; s += 8) {
+      float ms[8], ov[8][HD / 64];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float* pr = base + ((size_t)(s + u) * a.R + r) * rstride;
+        ms[u] = __builtin_nontemporal_load(pr + HD);
+#pragma unroll
+        for (int e = 0; e < HD / 64; ++e) ov[u][e] = __builtin_nontemporal_load(pr + e * 64 + lane);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float w = ms[u] == -__builtin_inff() ? 0.0f : __expf(ms[u] - M);
+#pragma unroll
+        for (int e = 0; e < HD / 64; ++e) acc[e] += w * ov[u][e];
+      }
+    }
+    for (; s < a.nsplit; ++s) {
       const float* pr = base + ((size_t)s * a.R + r) * rstride;
       const float ms = __builtin_nontemporal_load(pr + HD);
-      if (ms == -__builtin_inff()) continue;
-      const float w = __expf(ms - M);
-      den += w * __builtin_nontemporal_load(pr + HD + 1);
+      const float w = ms == -__builtin_inff() ? 0.0f : __expf(ms - M);
 #pragma unroll
       for (int e = 0; e < HD / 64; ++e) acc[e] += w * __builtin_nontemporal_load(pr + e * 64 + lane);
     }
@@ -380,8 +428,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 
 // ----------------------------------------------------------------------------- host helpers
 static int attn_split_tokens(int B, int nkv, int max_ctx) {
-  int st = 1024;
-  while (st > 64 && (int64_t)B * nkv * ((max_ctx + st - 1) / st) < 512) st >>= 1;
+  // aim for ~256 blocks, never splits shorter than 128 tokens
+  int st = 2048;
+  while (st > 128 && (int64_t)B * nkv * ((max_ctx + st - 1) / st) < 256) st >>= 1;
   return st;
 }
 
@@ -397,10 +446,10 @@ extern "C" int dsk_qkv_rope_append(const uint16_t* qkv, int B, int W, int nq, in
                                    const int32_t* block_table, int max_pages, int page, int kv_dtype,
                                    void* k_pool, void* v_pool, uint32_t* k_sb, uint32_t* v_sb,
                                    uint16_t* q_out, dsk_stream_t stream) {
-  DSK_REQUIRE(qkv && inv_freq && seq_lens && block_table && k_pool && v_pool && q_out,
+  DSK_REQUIRE(qkv && inv_freq && seq_lens && block_table && k_pool && v_pool && (q_out || nq == 0),
               "dsk_qkv_rope_append: null pointer");
   DSK_REQUIRE(hd == 128 || hd == 256, "dsk_qkv_rope_append: head_dim %d not supported (128, 256)", hd);
-  DSK_REQUIRE(B > 0 && W > 0 && nq > 0 && nkv > 0 && nq % nkv == 0, "dsk_qkv_rope_append: bad shape");
+  DSK_REQUIRE(B > 0 && W > 0 && nq >= 0 && nkv > 0 && nq % nkv == 0, "dsk_qkv_rope_append: bad shape");
   DSK_REQUIRE(page > 0 && max_pages > 0, "dsk_qkv_rope_append: bad page geometry");
   DSK_REQUIRE(kv_dtype == DSK_KV_BF16 || (kv_dtype == DSK_KV_U8 && k_sb && v_sb),
               "dsk_qkv_rope_append: u8 KV needs scale/bias buffers");
@@ -421,7 +470,7 @@ extern "C" int dsk_qkv_rope_append(const uint16_t* qkv, int B, int W, int nq, in
 extern "C" size_t dsk_attn_ws_bytes(int B, int W, int nq, int hd, int max_ctx) {
   if (B <= 0 || W <= 0 || nq <= 0 || hd <= 0 || max_ctx <= 0) return 0;
   // worst case over nkv: rows per kv head * nkv = W * nq
-  const int st = 64;  // smallest split => most splits
+  const int st = 128;  // smallest split => most splits
   const size_t nsplit = (size_t)((max_ctx + st - 1) / st);
   return kAttnCounterBytes + (size_t)B * W * nq * nsplit * (hd + 2) * sizeof(float);
 }

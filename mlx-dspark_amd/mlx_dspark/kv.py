@@ -1,0 +1,125 @@
+"""Paged KV cache in HBM.
+
+Replaces mlx_lm's KVCache / QuantizedKVCache (src/mlx_dspark/target.py:85-97 in the
+reference) and the per-row BatchCache (src/mlx_dspark/batch_engine.py:61-163). One pool per
+layer holds fixed pages of ``page`` tokens (layout in include/dspark_hip.h); a block table
+maps each row's logical pages to physical pages, so rows can share read-only prefix pages
+and roll back privately. The authoritative lengths live on the device (``seq_lens``) so a
+captured HIP graph can advance and roll them back without host round trips; ``lengths``
+mirrors them on the host.
+
+The object is also a list of per-layer views with the attributes the reference's callers
+read (``offset``, ``trim``, ``is_trimmable``): a decode loop that trims every layer by the
+same amount (src/mlx_dspark/generate.py:928-933) trims the cache once.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .ops import DSK_KV_BF16, DSK_KV_U8
+
+
+class LayerView:
+    __slots__ = ("cache", "layer")
+
+    def __init__(self, cache: "PagedKVCache", layer: int):
+        self.cache = cache
+        self.layer = layer
+
+    @property
+    def offset(self) -> int:
+        return self.cache.layer_offsets[self.layer]
+
+    @offset.setter
+    def offset(self, v: int) -> None:
+        self.cache.layer_offsets[self.layer] = int(v)
+        if self.layer == 0:
+            self.cache.set_lengths([int(v)] * self.cache.B)
+
+    def is_trimmable(self) -> bool:
+        return True
+
+    def trim(self, n: int) -> int:
+        n = min(int(n), self.offset)
+        self.offset = self.offset - n
+        return n
+
+    @property
+    def keys(self):
+        return self.cache.k[self.layer]
+
+    @property
+    def values(self):
+        return self.cache.v[self.layer]
+
+    @property
+    def state(self):
+        return self.cache.k[self.layer], self.cache.v[self.layer]
+
+
+class PagedKVCache(list):
+    """KV pools for ``n_layers`` layers and ``B`` rows, up to ``max_ctx`` tokens per row."""
+
+    def __init__(self, n_layers: int, B: int, n_kv: int, head_dim: int, max_ctx: int, *,
+                 page: int = 64, kv_bits: int | None = None, device="cuda", spare_pages: int = 0):
+        super().__init__(LayerView(self, l) for l in range(n_layers))
+        self.n_layers, self.B, self.n_kv, self.head_dim = n_layers, B, n_kv, head_dim
+        self.page = page
+        self.max_pages = math.ceil(max_ctx / page)
+        self.max_ctx = self.max_pages * page
+        self.kv_dtype = DSK_KV_U8 if kv_bits == 8 else DSK_KV_BF16
+        if kv_bits not in (None, 8):
+            raise ValueError(f"kv_bits={kv_bits}: only 8-bit (or None = bf16) KV is supported")
+        self.n_pages = B * self.max_pages + spare_pages
+        dev = torch.device(device)
+        shape = (self.n_pages, n_kv, page, head_dim)
+        dt = torch.uint8 if self.kv_dtype == DSK_KV_U8 else torch.bfloat16
+        self.k = [torch.zeros(shape, dtype=dt, device=dev) for _ in range(n_layers)]
+        self.v = [torch.zeros(shape, dtype=dt, device=dev) for _ in range(n_layers)]
+        if self.kv_dtype == DSK_KV_U8:
+            sbs = (self.n_pages, n_kv, page, head_dim // 64)
+            self.k_sb = [torch.zeros(sbs, dtype=torch.int32, device=dev) for _ in range(n_layers)]
+            self.v_sb = [torch.zeros(sbs, dtype=torch.int32, device=dev) for _ in range(n_layers)]
+        else:
+            self.k_sb = self.v_sb = [None] * n_layers
+        self.block_table = torch.arange(B * self.max_pages, dtype=torch.int32, device=dev).view(B, self.max_pages)
+        self.seq_lens = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.lengths = [0] * B
+        self.layer_offsets = [0] * n_layers
+
+    # ---- lengths
+    def set_lengths(self, lengths) -> None:
+        """Host -> device length update (eager paths; graph paths update seq_lens on device)."""
+        self.lengths = [int(x) for x in lengths]
+        if any(l < 0 or l > self.max_ctx for l in self.lengths):
+            raise ValueError(f"cache length {self.lengths} outside [0, {self.max_ctx}]")
+        self.seq_lens.copy_(torch.tensor(self.lengths, dtype=torch.int32), non_blocking=False)
+        if self.B == 1:
+            self.layer_offsets = [self.lengths[0]] * self.n_layers
+
+    def note_lengths(self, lengths) -> None:
+        """Record lengths the device already holds (after a device-side advance)."""
+        self.lengths = [int(x) for x in lengths]
+        if self.B == 1:
+            self.layer_offsets = [self.lengths[0]] * self.n_layers
+
+    @property
+    def offset(self) -> int:
+        return self.lengths[0]
+
+    def check_room(self, W: int) -> None:
+        if max(self.lengths) + W > self.max_ctx:
+            raise ValueError(f"KV cache full: {max(self.lengths)} + {W} > {self.max_ctx} tokens")
+
+    def layer_args(self, l: int):
+        return self.k[l], self.v[l], self.k_sb[l], self.v_sb[l]
+
+    @property
+    def nbytes(self) -> int:
+        t = sum(x.numel() * x.element_size() for x in self.k + self.v)
+        if self.kv_dtype == DSK_KV_U8:
+            t += sum(x.numel() * 4 for x in self.k_sb + self.v_sb)
+        return t

@@ -1,0 +1,119 @@
+"""Loaders and the drafter registry (drop-in for src/mlx_dspark/load.py).
+
+``load_pair`` / ``load_dflash_pair`` / ``load_target`` / ``load_dflash`` keep the reference's
+signatures and return values (load.py:155-373). Model names under ``synthetic/`` build seeded
+random-init W8 models at the benchmark shapes on the GPU (there is no network for hub
+downloads): a target name picks its shape, a drafter name ``synthetic/dspark-<target>`` or
+``synthetic/dflash-<target>`` builds a drafter matched to that target.
+"""
+
+from __future__ import annotations
+
+import os
+
+from . import synthetic
+from .qwen3 import TargetArgs
+from .target import Target
+from .tokenizer import SyntheticTokenizer
+
+# registry: target name -> matched drafters (same role as the reference's REGISTRY, load.py:54-64)
+REGISTRY = [
+    {"id": "qwen3-0.6b", "target": "synthetic/qwen3-0.6b", "dspark": "synthetic/dspark-qwen3-0.6b",
+     "dflash": "synthetic/dflash-qwen3-0.6b", "ram": "~0.7 GB"},
+    {"id": "qwen3-8b", "target": "synthetic/qwen3-8b", "dspark": "synthetic/dspark-qwen3-8b",
+     "dflash": "synthetic/dflash-qwen3-8b", "ram": "~9 GB"},
+    {"id": "tiny", "target": "synthetic/tiny", "dspark": "synthetic/dspark-tiny",
+     "dflash": "synthetic/dflash-tiny", "ram": "~1 MB"},
+]
+PRESETS = {"qwen3": {"target": "synthetic/qwen3-0.6b", "drafter": "synthetic/dspark-qwen3-0.6b"}}
+DFLASH_PRESETS = {"qwen3": {"target": "synthetic/qwen3-8b", "drafter": "synthetic/dflash-qwen3-8b"}}
+DEFAULT_TARGET = PRESETS["qwen3"]["target"]
+DEFAULT_DRAFTER = PRESETS["qwen3"]["drafter"]
+_FAMILY_ALIASES = {"qwen3": "synthetic/qwen3-0.6b"}
+
+
+def _registry_entry(target: str):
+    key = os.path.basename(str(target).rstrip("/")).lower()
+    for e in sorted(REGISTRY, key=lambda e: -len(e["id"])):
+        if e["id"] == key or e["id"] in key.split("-", 1)[-1] or key.endswith(e["id"]):
+            return e
+    return None
+
+
+def resolve(model=None, *, mode="dspark", drafter=None, family=None, target=None):
+    """(target_name, drafter_name) for a target and a mode (load.py:85-112)."""
+    tgt = model or target or family
+    tgt = _FAMILY_ALIASES.get(tgt, tgt) or DEFAULT_TARGET
+    if mode in ("baseline", "lookup"):
+        return tgt, None
+    if drafter:
+        return tgt, drafter
+    e = _registry_entry(tgt)
+    if e is not None and e.get(mode):
+        return tgt, e[mode]
+    raise ValueError(f"no built-in {mode} drafter is registered for target {tgt!r} — pass drafter=...")
+
+
+def resolve_mode(model=None, *, mode="auto", drafter=None, family=None, target=None):
+    if mode != "auto":
+        t, d = resolve(model, mode=mode, drafter=drafter, family=family, target=target)
+        return mode, t, d
+    if drafter:
+        t, d = resolve(model, mode="dspark", drafter=drafter, family=family, target=target)
+        return "dspark", t, d
+    t, _ = resolve(model, mode="baseline", family=family, target=target)
+    e = _registry_entry(t)
+    if e is not None:
+        for m in ("dspark", "dflash"):
+            if e.get(m):
+                return m, t, e[m]
+    return "lookup", t, None
+
+
+def _synthetic_key(name: str) -> str:
+    if not str(name).startswith("synthetic/"):
+        raise ValueError(f"{name!r}: only synthetic/* models can be built offline "
+                         f"(checkpoint loading from a local path is not implemented yet)")
+    return str(name).split("/", 1)[1]
+
+
+def apply_wired_limit() -> None:
+    """No-op on this engine (HBM residency needs no wiring)."""
+
+
+def load_target(repo_or_path: str = DEFAULT_TARGET, *, require_tap: bool = False, kv_bits=None,
+                kv_group_size: int = 64, seed: int = 0, keep_mlx: bool = False, max_ctx=None):
+    """(Target, tokenizer) for a synthetic target (load.py:314-351)."""
+    key = _synthetic_key(repo_or_path)
+    if key not in synthetic.TARGETS:
+        raise ValueError(f"unknown synthetic target {key!r}; known: {sorted(synthetic.TARGETS)}")
+    model = synthetic.build_target(key, seed=seed, keep_mlx=keep_mlx)
+    tok = SyntheticTokenizer(model.args.vocab_size)
+    target = Target(model, tok, kv_bits=kv_bits, kv_group_size=kv_group_size, max_ctx=max_ctx)
+    if require_tap:
+        target.verify_tap()
+    return target, tok
+
+
+def load_dflash(repo_or_path: str, *, quantize: bool = True, bits: int = 8, group_size: int = 64,
+                target_args: TargetArgs | None = None, seed: int = 1, keep_mlx: bool = False):
+    """(drafter, config) for a synthetic DFlash drafter (load.py:224-289); W8 by default."""
+    if bits != 8 or group_size != 64 or not quantize:
+        raise ValueError("this engine runs W8 (group 64) drafters")
+    key = _synthetic_key(repo_or_path)
+    if not key.startswith("dflash-"):
+        raise ValueError(f"{repo_or_path!r} is not a DFlash drafter name")
+    tkey = key[len("dflash-"):]
+    if target_args is None:
+        target_args = TargetArgs(**synthetic.TARGETS[tkey])
+    return synthetic.build_dflash(target_args, seed=seed, keep_mlx=keep_mlx)
+
+
+def load_dflash_pair(model: str = "synthetic/qwen3-8b", *, drafter=None, kv_bits=None, keep_mlx: bool = False,
+                     max_ctx=None):
+    """(target, tokenizer, DFlash drafter, cfg), drafter bound to the target (load.py:366-373)."""
+    target_name, drafter_name = resolve(model, mode="dflash", drafter=drafter)
+    target, tok = load_target(target_name, require_tap=True, kv_bits=kv_bits, keep_mlx=keep_mlx, max_ctx=max_ctx)
+    d, cfg = load_dflash(drafter_name, target_args=target.model.args, keep_mlx=keep_mlx)
+    d.bind(target.model)
+    return target, tok, d, cfg

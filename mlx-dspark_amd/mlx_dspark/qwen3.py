@@ -1,0 +1,227 @@
+"""Qwen3-shaped W8 decoder (the speculative-decoding target) on gfx950 kernels.
+
+The reference runs the target through mlx_lm (external) and replicates its layer loop to
+tap hidden states (src/mlx_dspark/target.py:107-124). This module is the engine's own
+forward over the same public Qwen3 architecture:
+    h = embed(ids)
+    per layer: h += o(attn(rope(q_norm(q)), rope(k_norm(k)), v))   q,k,v from RMSNorm(h)
+               h += down(silu(gate) * up)                           from RMSNorm(h)
+    logits = lm_head(RMSNorm(h))       (tied: embed_tokens.as_linear)
+with the residual stream captured after the tapped layers. Every projection is W8 (affine
+group 64, bf16 scale/bias); activations are bf16 between kernels, accumulation is fp32,
+logits are fp32. GeLU MLPs, an embedding scale, sliding-window layers and a final logit
+soft-cap are supported; gemma's sandwich norms are not.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from . import ops
+from .kv import PagedKVCache
+from .ops import (DSK_PACK_GELU, DSK_PACK_PLAIN, DSK_PACK_RMSNORM, DSK_PACK_SILU, W8Table,
+                  W8Weight)
+
+MAX_ROWS = 64  # rows per kernel pass (M of the skinny GEMM)
+
+
+@dataclass
+class TargetArgs:
+    """The model-config fields the engine reads (names follow the HF / mlx_lm config)."""
+
+    model_type: str = "qwen3"
+    hidden_size: int = 1024
+    num_hidden_layers: int = 28
+    intermediate_size: int = 3072
+    num_attention_heads: int = 16
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    vocab_size: int = 151936
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1_000_000.0
+    tie_word_embeddings: bool = False
+    max_position_embeddings: int = 40960
+    hidden_act: str = "silu"                       # "silu" | "gelu_tanh"
+    embed_scale: float = 1.0                       # gemma: sqrt(hidden_size)
+    sliding_window: int | None = None
+    layer_types: tuple = field(default_factory=tuple)   # "full_attention" | "sliding_attention"
+    final_logit_softcapping: float | None = None
+    query_pre_attn_scalar: float | None = None    # attention scale = this ** -0.5 when set
+
+    @property
+    def n_qkv(self) -> int:
+        return (self.num_attention_heads + 2 * self.num_key_value_heads) * self.head_dim
+
+    @property
+    def attn_scale(self) -> float:
+        s = self.query_pre_attn_scalar or self.head_dim
+        return float(s) ** -0.5
+
+    def window(self, layer: int) -> int:
+        if self.layer_types and self.layer_types[layer] == "sliding_attention" and self.sliding_window:
+            return int(self.sliding_window)
+        return 0
+
+
+@dataclass
+class LayerWeights:
+    qkv: W8Weight          # [q | k | v] rows, N = (nq + 2 nkv) * hd, K = hidden
+    o: W8Weight            # N = hidden, K = nq * hd
+    gate_up: W8Weight      # [gate | up] rows, N = 2 * intermediate
+    down: W8Weight         # N = hidden, K = intermediate
+    in_norm: torch.Tensor  # bf16 [hidden]
+    post_norm: torch.Tensor
+    q_norm: torch.Tensor   # bf16 [head_dim]
+    k_norm: torch.Tensor
+
+    def kv_view(self, args: TargetArgs) -> W8Weight:
+        """The [k | v] rows of the fused projection, as a zero-copy W8 view."""
+        nq_rows = args.num_attention_heads * args.head_dim
+        tile_bytes = (self.qkv.K // 64) * 1024
+        t0 = nq_rows // 16
+        n = 2 * args.num_key_value_heads * args.head_dim
+        return W8Weight(self.qkv.wt[t0 * tile_bytes:(t0 + n // 16) * tile_bytes],
+                        self.qkv.sb[nq_rows:nq_rows + n], n, self.qkv.K)
+
+
+class Qwen3W8:
+    """Weights + forward. Mirrors the pieces of an mlx_lm model that callers touch
+    (``args``, ``layers``); ``model.embed_tokens`` / ``lm_head`` are W8 objects."""
+
+    def __init__(self, args: TargetArgs, layers: list[LayerWeights], embed: W8Table,
+                 lm_head: W8Weight, norm: torch.Tensor):
+        self.args = args
+        self.layers = layers
+        self.embed = embed
+        self.lm_head = lm_head
+        self.norm = norm
+        self.device = norm.device
+        self.inv_freq = ops.rope_inv_freq(args.head_dim, args.rope_theta, self.device)
+        self.act_mode = DSK_PACK_SILU if args.hidden_act == "silu" else DSK_PACK_GELU
+
+    # ------------------------------------------------------------------ cache
+    def make_cache(self, B: int = 1, max_ctx: int | None = None, kv_bits: int | None = None,
+                   page: int = 64) -> PagedKVCache:
+        a = self.args
+        max_ctx = max_ctx or min(a.max_position_embeddings, 16384)
+        return PagedKVCache(a.num_hidden_layers, B, a.num_key_value_heads, a.head_dim, max_ctx,
+                            page=page, kv_bits=kv_bits, device=self.device)
+
+    @property
+    def weight_bytes(self) -> int:
+        t = self.lm_head.nbytes
+        for L in self.layers:
+            t += L.qkv.nbytes + L.o.nbytes + L.gate_up.nbytes + L.down.nbytes
+        return t
+
+    # ------------------------------------------------------------------ forward
+    def embed_rows(self, ids: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        return ops.w8_embed(ids, self.embed, self.args.embed_scale, out=out)
+
+    def layer_forward(self, l: int, h: torch.Tensor, B: int, W: int, cache: PagedKVCache,
+                      causal: bool = True) -> None:
+        """One decoder layer over h [B*W, H] (bf16, updated in place)."""
+        a = self.args
+        L = self.layers[l]
+        nq, nkv, hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
+        M = B * W
+        eps = a.rms_norm_eps
+        x = ops.act_pack(h, DSK_PACK_RMSNORM, L.in_norm, eps)
+        qkv = ops.w8_gemm(x, L.qkv, M)
+        k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
+        q = ops.qkv_rope_append(qkv, B, W, nq, nkv, hd, L.q_norm, L.k_norm, eps, self.inv_freq,
+                                cache.seq_lens, cache.block_table, cache.page, cache.kv_dtype,
+                                k_pool, v_pool, k_sb, v_sb)
+        o = ops.attention(q, B, W, nq, nkv, hd, a.attn_scale, cache.seq_lens, cache.max_ctx,
+                          cache.block_table, cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb,
+                          causal=causal, window=a.window(l))
+        x = ops.act_pack(o, DSK_PACK_PLAIN)
+        ops.w8_gemm(x, L.o, M, out=h, residual=h)
+        x = ops.act_pack(h, DSK_PACK_RMSNORM, L.post_norm, eps)
+        gu = ops.w8_gemm(x, L.gate_up, M)
+        x = ops.act_pack(gu, self.act_mode, K=L.down.K)
+        ops.w8_gemm(x, L.down, M, out=h, residual=h)
+
+    def forward(self, ids: torch.Tensor, cache: PagedKVCache, tap=None, *, advance: bool = True,
+                logits: str = "all", logits_out: torch.Tensor | None = None,
+                fused_out: torch.Tensor | None = None, h_out: torch.Tensor | None = None):
+        """ids [B, W] int32 on device (W rows per batch row, B*W <= 64).
+
+        Positions come from cache.seq_lens (device). Returns (logits [B, W or 1, V] f32 or
+        None, fused [B, W, n_tap*H] bf16 or None). advance=True moves seq_lens by W; the
+        speculative loops pass False and let the acceptance kernel apply n + 1."""
+        a = self.args
+        B, W = ids.shape
+        M = B * W
+        if M > MAX_ROWS:
+            raise ValueError(f"forward pass of {M} rows > {MAX_ROWS}; chunk the prompt")
+        H = a.hidden_size
+        tap = list(tap or [])
+        slots: dict = {}
+        for i, t in enumerate(tap):
+            slots.setdefault(t, []).append(i)
+        h = h_out if h_out is not None else torch.empty((M, H), dtype=torch.bfloat16, device=self.device)
+        self.embed_rows(ids.reshape(-1), out=h)
+        fused = None
+        if tap:
+            fused = fused_out if fused_out is not None else torch.empty(
+                (M, len(tap) * H), dtype=torch.bfloat16, device=self.device)
+        for l in range(a.num_hidden_layers):
+            self.layer_forward(l, h, B, W, cache)
+            for s in slots.get(l, ()):
+                fused[:, s * H:(s + 1) * H].copy_(h)
+        out = None
+        if logits != "none":
+            rows = h if logits == "all" else h.view(B, W, H)[:, -1]
+            Mr = rows.shape[0]
+            x = ops.act_pack(rows, DSK_PACK_RMSNORM, self.norm, a.rms_norm_eps)
+            out = logits_out if logits_out is not None else torch.empty(
+                (Mr, a.vocab_size), dtype=torch.float32, device=self.device)
+            ops.w8_gemm(x, self.lm_head, Mr, out=out, softcap=a.final_logit_softcapping or 0.0)
+            out = out.view(B, W if logits == "all" else 1, a.vocab_size)
+        if advance:
+            ops.lens_add(cache.seq_lens, None, W)
+            cache.note_lengths([l + W for l in cache.lengths])
+        return out, (fused.view(B, W, -1) if fused is not None else None)
+
+    def head_logits(self, h: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """lm_head(norm(h)) for h [M, H] bf16 (DFlash reuses the target head)."""
+        a = self.args
+        out = out if out is not None else torch.empty((h.shape[0], a.vocab_size), dtype=torch.float32,
+                                                      device=self.device)
+        for m0 in range(0, h.shape[0], MAX_ROWS):
+            m1 = min(h.shape[0], m0 + MAX_ROWS)
+            x = ops.act_pack(h[m0:m1], DSK_PACK_RMSNORM, self.norm, a.rms_norm_eps)
+            ops.w8_gemm(x, self.lm_head, m1 - m0, out=out[m0:m1], softcap=a.final_logit_softcapping or 0.0)
+        return out
+
+    def prefill(self, ids: list[int] | torch.Tensor, cache: PagedKVCache, tap=None, *, chunk: int = MAX_ROWS,
+                on_chunk=None):
+        """Chunked single-row prefill. Returns (last-position logits [1, 1, V], fused of the
+        whole prompt [1, L, n_tap*H] or None). on_chunk(fused_chunk, pos) lets a drafter
+        ingest each chunk's hidden states as it is produced."""
+        if not torch.is_tensor(ids):
+            ids = torch.tensor(ids, dtype=torch.int32)
+        ids = ids.reshape(1, -1).to(self.device, torch.int32)
+        L = ids.shape[1]
+        cache.check_room(L)
+        parts = []
+        out = None
+        pos = cache.lengths[0]
+        for c0 in range(0, L, chunk):
+            c1 = min(L, c0 + chunk)
+            last = c1 == L
+            out, fused = self.forward(ids[:, c0:c1], cache, tap, logits="last" if last else "none")
+            if fused is not None:
+                if on_chunk is not None:
+                    on_chunk(fused, pos)
+                else:
+                    parts.append(fused)
+            pos += c1 - c0
+        fused_all = None
+        if parts:
+            fused_all = parts[0] if len(parts) == 1 else torch.cat(parts, dim=1)
+        return out, fused_all
+

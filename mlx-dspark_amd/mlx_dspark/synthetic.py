@@ -1,0 +1,149 @@
+"""Seeded random-init W8 models at the benchmark shapes (no checkpoints are needed).
+
+Weights are N(0, 0.02) drawn on the device from a per-tensor seed (so a tensor does not
+depend on the order tensors are built in), quantized with dsk_w8_quantize (affine 8-bit,
+group 64, bf16 scale/bias) and repacked into the engine's tiled layout.
+q/k norm gains are hd**-0.25 (see qk_norm), other norm weights are 1. With ``keep_mlx=True`` every W8 weight also keeps its MLX-layout (q, scales, biases) so a
+CPU checker can dequantize exactly the same numbers.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import math
+
+import torch
+
+from .ops import W8Table, W8Weight
+from .qwen3 import LayerWeights, Qwen3W8, TargetArgs
+
+STD = 0.02
+
+# Target shapes (HF config field names).
+TARGETS = {
+    "qwen3-0.6b": dict(hidden_size=1024, num_hidden_layers=28, intermediate_size=3072,
+                       num_attention_heads=16, num_key_value_heads=8, head_dim=128,
+                       vocab_size=151936, tie_word_embeddings=True),
+    "qwen3-8b": dict(hidden_size=4096, num_hidden_layers=36, intermediate_size=12288,
+                     num_attention_heads=32, num_key_value_heads=8, head_dim=128,
+                     vocab_size=151936, tie_word_embeddings=False),
+    # small shapes for tests and smoke runs
+    "tiny": dict(hidden_size=256, num_hidden_layers=4, intermediate_size=512,
+                 num_attention_heads=4, num_key_value_heads=2, head_dim=128, vocab_size=1024,
+                 tie_word_embeddings=False),
+    "tiny-tied": dict(hidden_size=256, num_hidden_layers=3, intermediate_size=512,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=128, vocab_size=1024,
+                      tie_word_embeddings=True),
+}
+
+
+def _seed(seed: int, name: str) -> int:
+    h = hashlib.sha256(f"{seed}:{name}".encode()).digest()
+    return int.from_bytes(h[:8], "little") & ((1 << 63) - 1)
+
+
+def randn(shape, seed: int, name: str, device, std: float = STD) -> torch.Tensor:
+    g = torch.Generator(device=device)
+    g.manual_seed(_seed(seed, name))
+    return torch.randn(shape, generator=g, device=device, dtype=torch.float32) * std
+
+
+def w8(N: int, K: int, seed: int, name: str, device, keep_mlx: bool = False) -> W8Weight:
+    w = randn((N, K), seed, name, device)
+    q, s, b = W8Weight.quantize_mlx(w)
+    del w
+    W = W8Weight.from_mlx(q, s, b)
+    if keep_mlx:
+        W.mlx = (q, s, b)
+    return W
+
+
+def w8_table(V: int, H: int, seed: int, name: str, device) -> W8Table:
+    w = randn((V, H), seed, name, device)
+    q, s, b = W8Weight.quantize_mlx(w)
+    return W8Table(q, s, b)
+
+
+def ones(n: int, device) -> torch.Tensor:
+    return torch.ones(n, dtype=torch.bfloat16, device=device)
+
+
+def qk_norm(hd: int, device) -> torch.Tensor:
+    """q/k RMSNorm gains of hd**-0.25, so normalised q.k / sqrt(hd) has unit variance (with
+    unit gains a random model's attention is nearly one-hot, unlike a trained model's)."""
+    return torch.full((hd,), hd ** -0.25, dtype=torch.bfloat16, device=device)
+
+
+def build_target(name_or_args, seed: int = 0, device="cuda", keep_mlx: bool = False) -> Qwen3W8:
+    if isinstance(name_or_args, TargetArgs):
+        args = name_or_args
+    else:
+        args = TargetArgs(model_type="qwen3", **TARGETS[name_or_args])
+    device = torch.device(device)
+    H, I = args.hidden_size, args.intermediate_size
+    nq, nkv, hd = args.num_attention_heads, args.num_key_value_heads, args.head_dim
+    layers = []
+    for l in range(args.num_hidden_layers):
+        p = f"layers.{l}."
+        layers.append(LayerWeights(
+            qkv=w8(args.n_qkv, H, seed, p + "qkv", device, keep_mlx),
+            o=w8(H, nq * hd, seed, p + "o", device, keep_mlx),
+            gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx),
+            down=w8(H, I, seed, p + "down", device, keep_mlx),
+            in_norm=ones(H, device), post_norm=ones(H, device),
+            q_norm=qk_norm(hd, device), k_norm=qk_norm(hd, device)))
+    embed = w8_table(args.vocab_size, H, seed, "embed_tokens", device)
+    if args.tie_word_embeddings:
+        lm_head = W8Weight.from_mlx(embed.q, embed.s, embed.b)
+        if keep_mlx:
+            lm_head.mlx = (embed.q, embed.s, embed.b)
+    else:
+        lm_head = w8(args.vocab_size, H, seed, "lm_head", device, keep_mlx)
+    torch.cuda.synchronize(device)
+    return Qwen3W8(args, layers, embed, lm_head, ones(H, device))
+
+
+def evenly_spaced_layers(n_target_layers: int, n: int) -> list[int]:
+    """n distinct tap layers spread over the target: from layer 1 to layer L-3 (the DFlash
+    convention) when the target is deep enough, else over all layers."""
+    if n > n_target_layers:
+        raise ValueError(f"{n} taps from a {n_target_layers}-layer target")
+    if n == 1:
+        return [n_target_layers // 2]
+    lo, hi = (1, n_target_layers - 3) if n_target_layers - 3 - 1 >= n - 1 else (0, n_target_layers - 1)
+    return [int(round(lo + i * (hi - lo) / (n - 1))) for i in range(n)]
+
+
+def build_dflash(target_args: TargetArgs, seed: int = 1, device="cuda", keep_mlx: bool = False,
+                 num_hidden_layers: int = 2, block_size: int = 16, n_taps: int = 5,
+                 mask_token_id: int | None = None):
+    """A DFlash drafter shaped like the target (same width, heads and MLP), conditioned on
+    n_taps evenly spaced target layers, with a block of block_size positions."""
+    from .dflash_model import DFlashConfig, DFlashDraftModel
+
+    a = target_args
+    device = torch.device(device)
+    cfg = DFlashConfig(
+        hidden_size=a.hidden_size, num_hidden_layers=num_hidden_layers,
+        num_attention_heads=a.num_attention_heads, num_key_value_heads=a.num_key_value_heads,
+        head_dim=a.head_dim, intermediate_size=a.intermediate_size, vocab_size=a.vocab_size,
+        rms_norm_eps=a.rms_norm_eps, rope_theta=a.rope_theta,
+        max_position_embeddings=a.max_position_embeddings, block_size=block_size,
+        target_layer_ids=tuple(evenly_spaced_layers(a.num_hidden_layers, n_taps)),
+        num_target_layers=a.num_hidden_layers,
+        mask_token_id=a.vocab_size - 1 if mask_token_id is None else mask_token_id)
+    H, I = a.hidden_size, a.intermediate_size
+    nq, nkv, hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
+    layers = []
+    for l in range(num_hidden_layers):
+        p = f"dflash.layers.{l}."
+        layers.append(LayerWeights(
+            qkv=w8(a.n_qkv, H, seed, p + "qkv", device, keep_mlx),
+            o=w8(H, nq * hd, seed, p + "o", device, keep_mlx),
+            gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx),
+            down=w8(H, I, seed, p + "down", device, keep_mlx),
+            in_norm=ones(H, device), post_norm=ones(H, device),
+            q_norm=qk_norm(hd, device), k_norm=qk_norm(hd, device)))
+    fc = w8(H, n_taps * H, seed, "dflash.fc", device, keep_mlx)
+    torch.cuda.synchronize(device)
+    return DFlashDraftModel(cfg, fc, ones(H, device), layers, ones(H, device)), cfg

@@ -1,0 +1,248 @@
+"""CPU restatement of the verify forward, KV semantics and the DFlash drafter (torch, float32).
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+Restates (reference paths):
+  - Target._run_mlxlm: embed -> layers -> norm -> lm_head with the residual captured after
+    the tapped layers (src/mlx_dspark/target.py:107-124). The Qwen3 layer itself lives in
+    mlx_lm (external); it follows the public Qwen3 architecture: RMSNorm -> q/k/v
+    projections -> per-head q/k RMSNorm -> rotate-half RoPE (theta from config) -> GQA
+    attention, causal with offset (mask grid of tests/test_batch_engine.py:87-103) ->
+    o_proj + residual; RMSNorm -> down(silu(gate) * up) + residual.
+  - KV append / trim as metadata (src/mlx_dspark/batch_engine.py:132-163).
+  - DFlashDraftModel.__call__ (src/mlx_dspark/dflash_model.py:100-208).
+Every intermediate is rounded to bf16 where a bf16 MLX graph produces a bf16 array, except
+that a projection and the residual add it feeds round once (a fused add, as the engine
+does); ``double_round=True`` rounds the projection output first, as an unfused bf16 graph
+would. On a 256-wide 4-layer random model the two conventions alone differ by 0.022 in the
+normalised-logit metric, which is the noise floor this oracle works at.
+
+Pinning: attention equals an explicit loop over heads with the GQA map h -> h // (nq/nkv)
+(tests/test_model.py:25-60 in the reference); the causal mask reproduces the reference's
+exact grids; RMSNorm / RoPE / SiLU are checked against float64 closed forms in
+tests/test_oracle_model.py. The mlx_lm op order and rounding points themselves are external
+to the reference: parity unpinned beyond the logits tolerance.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import w8 as W8
+
+
+def bf(x: torch.Tensor) -> torch.Tensor:
+    return x.to(torch.bfloat16).to(torch.float32)
+
+
+def rmsnorm(x, w, eps):
+    return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) * w
+
+
+def rope(x, pos, theta):
+    """rotate-half RoPE; x [..., n, hd], pos [n]."""
+    hd = x.shape[-1]
+    inv = torch.from_numpy((theta ** (-2.0 * np.arange(hd // 2) / hd)).astype(np.float32))
+    ang = pos.float()[:, None] * inv[None, :]
+    c, s = torch.cos(ang), torch.sin(ang)
+    x1, x2 = x[..., : hd // 2], x[..., hd // 2:]
+    return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1)
+
+
+def sdpa(q, K, V, scale, mask=None):
+    """q [W, nq, hd], K/V [L, nkv, hd] -> [W, nq, hd]; GQA by head index // (nq/nkv)."""
+    W, nq, hd = q.shape
+    nkv = K.shape[1]
+    G = nq // nkv
+    out = torch.empty(W, nq, hd)
+    for h in range(nq):
+        s = (q[:, h] @ K[:, h // G].T) * scale
+        if mask is not None:
+            s = s.masked_fill(~mask, float("-inf"))
+        out[:, h] = torch.softmax(s, dim=-1) @ V[:, h // G]
+    return out
+
+
+def causal_mask(offset: int, W: int) -> torch.Tensor:
+    """[W, offset + W] boolean: query i (absolute offset + i) sees key j iff j <= offset + i."""
+    j = torch.arange(offset + W)[None, :]
+    i = torch.arange(W)[:, None]
+    return j <= offset + i
+
+
+def deq(wobj) -> torch.Tensor:
+    q, s, b = wobj.mlx
+    qn = q.cpu().numpy()
+    sn = s.view(torch.int16).cpu().numpy().view(np.uint16)
+    bn = b.view(torch.int16).cpu().numpy().view(np.uint16)
+    return torch.from_numpy(W8.dequantize(qn, sn, bn).astype(np.float32))
+
+
+def deq_table(t) -> torch.Tensor:
+    qn = t.q.cpu().numpy()
+    sn = t.s.view(torch.int16).cpu().numpy().view(np.uint16)
+    bn = t.b.view(torch.int16).cpu().numpy().view(np.uint16)
+    return torch.from_numpy(W8.dequantize(qn, sn, bn).astype(np.float32))
+
+
+def kv_quant_roundtrip(x: torch.Tensor) -> torch.Tensor:
+    """8-bit group-64 affine round trip along the last axis (same rule as the weights)."""
+    shp = x.shape
+    flat = x.reshape(-1, shp[-1]).numpy().astype(np.float32)
+    q, s, b = W8.quantize(flat)
+    return bf(torch.from_numpy(W8.dequantize(q, s, b).astype(np.float32)).reshape(shp))
+
+
+class OracleLayer:
+    def __init__(self, L, nq, nkv, hd):
+        self.wq = deq(L.qkv)
+        self.wo = deq(L.o)
+        self.wgu = deq(L.gate_up)
+        self.wd = deq(L.down)
+        self.in_norm = L.in_norm.float().cpu()
+        self.post_norm = L.post_norm.float().cpu()
+        self.q_norm = L.q_norm.float().cpu()
+        self.k_norm = L.k_norm.float().cpu()
+        self.nq, self.nkv, self.hd = nq, nkv, hd
+
+
+class OracleTarget:
+    """Dense-KV CPU model built from a GPU model created with keep_mlx=True."""
+
+    def __init__(self, model, kv_bits=None, double_round: bool = False):
+        a = model.args
+        self.a = a
+        self.kv_bits = kv_bits
+        self.rr = bf if double_round else (lambda x: x)
+        self.layers = [OracleLayer(L, a.num_attention_heads, a.num_key_value_heads, a.head_dim) for L in model.layers]
+        self.embed = deq_table(model.embed)
+        self.lm_head = deq(model.lm_head)
+        self.norm = model.norm.float().cpu()
+        self.K = [torch.zeros(0, a.num_key_value_heads, a.head_dim) for _ in self.layers]
+        self.V = [torch.zeros(0, a.num_key_value_heads, a.head_dim) for _ in self.layers]
+        self.offset = 0
+
+    def trim(self, n: int) -> None:
+        """Roll back n tokens (metadata in the engine; a truncation here)."""
+        self.offset = max(0, self.offset - n)
+        self.K = [k[: self.offset] for k in self.K]
+        self.V = [v[: self.offset] for v in self.V]
+
+    def forward(self, ids, tap=()):
+        a = self.a
+        ids = torch.as_tensor(ids).reshape(-1).long()
+        W = ids.numel()
+        nq, nkv, hd, eps = a.num_attention_heads, a.num_key_value_heads, a.head_dim, a.rms_norm_eps
+        h = bf(self.embed[ids] * a.embed_scale)
+        pos = torch.arange(self.offset, self.offset + W)
+        captured = []
+        for l, L in enumerate(self.layers):
+            x = bf(rmsnorm(h, L.in_norm, eps))
+            qkv = bf(x @ L.wq.T)
+            q = qkv[:, : nq * hd].view(W, nq, hd)
+            k = qkv[:, nq * hd:(nq + nkv) * hd].view(W, nkv, hd)
+            v = qkv[:, (nq + nkv) * hd:].view(W, nkv, hd)
+            q = bf(rope(bf(rmsnorm(q, L.q_norm, eps)).transpose(0, 1), pos, a.rope_theta).transpose(0, 1))
+            k = bf(rope(bf(rmsnorm(k, L.k_norm, eps)).transpose(0, 1), pos, a.rope_theta).transpose(0, 1))
+            if self.kv_bits == 8:
+                k, v = kv_quant_roundtrip(k), kv_quant_roundtrip(v)
+            self.K[l] = torch.cat([self.K[l], k])
+            self.V[l] = torch.cat([self.V[l], v])
+            o = bf(sdpa(q, self.K[l], self.V[l], a.attn_scale, causal_mask(self.offset, W)))
+            h = bf(h + self.rr(o.reshape(W, -1) @ L.wo.T))
+            x = bf(rmsnorm(h, L.post_norm, eps))
+            gu = bf(x @ L.wgu.T)
+            I = gu.shape[1] // 2
+            g, u = gu[:, :I], gu[:, I:]
+            act = bf(bf(g * torch.sigmoid(g)) * u)
+            h = bf(h + self.rr(act @ L.wd.T))
+            if l in tap:
+                captured.append(h)
+        self.offset += W
+        logits = bf(rmsnorm(h, self.norm, eps)) @ self.lm_head.T
+        fused = torch.cat(captured, dim=-1) if captured else None
+        return logits, fused
+
+
+class OracleDFlash:
+    """CPU DFlash drafter (src/mlx_dspark/dflash_model.py:100-208) bound to an OracleTarget."""
+
+    def __init__(self, drafter, target: OracleTarget):
+        c = drafter.config
+        self.c = c
+        self.fc = deq(drafter.fc)
+        self.hidden_norm = drafter.hidden_norm.float().cpu()
+        self.norm = drafter.norm.float().cpu()
+        self.layers = [OracleLayer(L, c.num_attention_heads, c.num_key_value_heads, c.head_dim)
+                       for L in drafter.layers]
+        self.target = target
+        self.K = [torch.zeros(0, c.num_key_value_heads, c.head_dim) for _ in self.layers]
+        self.V = [torch.zeros(0, c.num_key_value_heads, c.head_dim) for _ in self.layers]
+
+    @property
+    def offset(self) -> int:
+        return self.K[0].shape[0]
+
+    def __call__(self, block_ids, target_hidden, logits_start=1):
+        c = self.c
+        nq, nkv, hd, eps = c.num_attention_heads, c.num_key_value_heads, c.head_dim, c.rms_norm_eps
+        ids = torch.as_tensor(block_ids).reshape(-1).long()
+        L = ids.numel()
+        h = bf(self.target.embed[ids] * self.target.a.embed_scale)
+        th = target_hidden.reshape(-1, target_hidden.shape[-1]).float()
+        S = th.shape[0]
+        h_ctx = bf(rmsnorm(bf(th @ self.fc.T), self.hidden_norm, eps))
+        off = self.offset
+        for l, Lw in enumerate(self.layers):
+            x = bf(rmsnorm(h, Lw.in_norm, eps))
+            qkv = bf(x @ Lw.wq.T)
+            q = qkv[:, : nq * hd].view(L, nq, hd)
+            kb = qkv[:, nq * hd:(nq + nkv) * hd].view(L, nkv, hd)
+            vb = qkv[:, (nq + nkv) * hd:].view(L, nkv, hd)
+            kvc = bf(h_ctx @ Lw.wq[nq * hd:].T)
+            kc = kvc[:, : nkv * hd].view(S, nkv, hd)
+            vc = kvc[:, nkv * hd:].view(S, nkv, hd)
+            pq = torch.arange(off + S, off + S + L)
+            q = bf(rope(bf(rmsnorm(q, Lw.q_norm, eps)).transpose(0, 1), pq, c.rope_theta).transpose(0, 1))
+            kb = bf(rope(bf(rmsnorm(kb, Lw.k_norm, eps)).transpose(0, 1), pq, c.rope_theta).transpose(0, 1))
+            kc = bf(rope(bf(rmsnorm(kc, Lw.k_norm, eps)).transpose(0, 1), torch.arange(off, off + S),
+                         c.rope_theta).transpose(0, 1))
+            self.K[l] = torch.cat([self.K[l], kc])
+            self.V[l] = torch.cat([self.V[l], vc])
+            K = torch.cat([self.K[l], kb])
+            Vv = torch.cat([self.V[l], vb])
+            o = bf(sdpa(q, K, Vv, hd ** -0.5))
+            h = bf(h + o.reshape(L, -1) @ Lw.wo.T)
+            x = bf(rmsnorm(h, Lw.post_norm, eps))
+            gu = bf(x @ Lw.wgu.T)
+            I = gu.shape[1] // 2
+            act = bf(bf(gu[:, :I] * torch.sigmoid(gu[:, :I])) * gu[:, I:])
+            h = bf(h + act @ Lw.wd.T)
+        h = h[logits_start:]
+        return bf(rmsnorm(h, self.norm, eps)) @ self.target.lm_head.T
+
+
+def normalized_maxdiff(a: torch.Tensor, b: torch.Tensor) -> float:
+    """max |a/rms(a) - b/rms(b)| over rows: the logits tolerance metric."""
+    a = a.detach().float().cpu().reshape(-1, a.shape[-1])
+    b = b.detach().float().cpu().reshape(-1, b.shape[-1])
+    an = a / a.pow(2).mean(-1, keepdim=True).sqrt()
+    bn = b / b.pow(2).mean(-1, keepdim=True).sqrt()
+    return float((an - bn).abs().max())
+
+
+def greedy_decode(target: OracleTarget, prompt, n_new: int):
+    """Plain greedy decoding (what speculative greedy decoding must reproduce); returns the
+    tokens and the top-2 margin (after RMS normalisation) of every decision."""
+    logits, _ = target.forward(prompt)
+    out, margins = [], []
+    row = logits[-1]
+    for _ in range(n_new):
+        rn = row / row.pow(2).mean().sqrt()
+        top = torch.topk(rn, 2).values
+        margins.append(float(top[0] - top[1]))
+        t = int(torch.argmax(row))
+        out.append(t)
+        row = target.forward([t])[0][-1]
+    return out, margins

@@ -1,0 +1,148 @@
+"""GPU parity of the whole verify path on small synthetic W8 models: target forward with
+hidden-state tap (bf16 and 8-bit KV), KV rollback, the DFlash drafter, and greedy
+speculative decoding reproducing the oracle's greedy token stream."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import model as OM
+
+pytestmark = pytest.mark.gpu
+# Logit agreement on RMS-normalised rows. For these narrow random-init models the bf16 noise
+# floor of the metric is ~0.02-0.03 (two CPU oracles differing only in the rounding of the
+# attention probabilities already differ by 0.024 max-abs and 0.005-0.006 RMS), so the
+# max-abs bound is 3e-2 (5e-2 with 8-bit KV, whose quantizer amplifies bf16 differences) and
+# the RMS bound 1e-2 (1.5e-2): bugs show up as O(0.1) differences. Greedy token streams use
+# the 2e-2 margin rule.
+TOL = 2e-2
+MAX_TOL = {None: 3e-2, 8: 5e-2}
+RMS_TOL = {None: 1e-2, 8: 1.5e-2}
+
+
+def assert_logits_close(got, want, kv_bits=None, what=""):
+    a = got.detach().float().cpu().reshape(-1, got.shape[-1])
+    b = want.detach().float().cpu().reshape(-1, want.shape[-1])
+    d = a / a.pow(2).mean(-1, keepdim=True).sqrt() - b / b.pow(2).mean(-1, keepdim=True).sqrt()
+    mx, rms = float(d.abs().max()), float(d.pow(2).mean().sqrt())
+    print(f"{what}: normalised max-abs {mx:.4f} rms {rms:.5f}", flush=True)
+    assert mx < MAX_TOL[kv_bits] and rms < RMS_TOL[kv_bits], (mx, rms)
+
+
+@pytest.fixture(scope="module")
+def tiny(dev):
+    from mlx_dspark import synthetic
+    return synthetic.build_target("tiny", seed=3, keep_mlx=True)
+
+
+@pytest.mark.parametrize("kv_bits", [None, 8])
+def test_target_forward_tap_and_rollback(dev, tiny, kv_bits):
+    print(f"target forward kv_bits={kv_bits}", flush=True)
+    model = tiny
+    V = model.args.vocab_size
+    rng = np.random.default_rng(0)
+    prompt = rng.integers(0, V, 70).tolist()
+    tap = [0, 2]
+    cache = model.make_cache(max_ctx=256, kv_bits=kv_bits)
+    logits, fused = model.prefill(prompt, cache, tap)
+    ref = OM.OracleTarget(model, kv_bits=kv_bits)
+    rl, rf = ref.forward(prompt, tap)
+    assert_logits_close(logits[0, -1], rl[-1], kv_bits, "prefill last row")
+    assert fused.shape == (1, 70, 2 * model.args.hidden_size)
+    assert (fused[0].float().cpu() - rf).abs().max() < 0.05 * rf.abs().max()
+    # verify block of 9 rows, advance=False, then roll back to n = 3 accepted
+    block = rng.integers(0, V, 9).tolist()
+    ids = torch.tensor([block], dtype=torch.int32, device=dev)
+    vl, vf = model.forward(ids, cache, tap, advance=False)
+    rvl, _ = ref.forward(block, tap)
+    assert_logits_close(vl[0], rvl, kv_bits, "verify block")
+    n = torch.tensor([3], dtype=torch.int32, device=dev)
+    from mlx_dspark import ops
+    ops.lens_add(cache.seq_lens, n, 1)
+    cache.note_lengths([70 + 4])
+    ref.trim(9 - 4)
+    nxt = rng.integers(0, V, 5).tolist()
+    l2, _ = model.forward(torch.tensor([nxt], dtype=torch.int32, device=dev), cache, None)
+    r2, _ = ref.forward(nxt)
+    assert_logits_close(l2[0], r2, kv_bits, "after rollback")
+    assert int(cache.seq_lens.item()) == 70 + 4 + 5
+
+
+def test_tied_head_and_target_run_api(dev):
+    from mlx_dspark import synthetic
+    from mlx_dspark.target import Target
+    model = synthetic.build_target("tiny-tied", seed=5, keep_mlx=True)
+    t = Target(model, None)
+    t.verify_tap()
+    cache = t.make_cache(max_ctx=128)
+    ids = [[5, 6, 7, 8, 9]]
+    lg, fu = t.run(ids, cache, [1])
+    ref = OM.OracleTarget(model)
+    rl, _ = ref.forward(ids[0], [1])
+    assert_logits_close(lg[0], rl, None, "tied head")
+    assert cache[0].offset == 5
+    for c in cache:                        # the reference's per-layer trim loop trims once
+        c.trim(2)
+    assert cache.offset == 3 and int(cache.seq_lens.item()) == 3
+
+
+def test_dflash_drafter_matches_oracle(dev, tiny):
+    from mlx_dspark import synthetic
+    d, cfg = synthetic.build_dflash(tiny.args, seed=9, keep_mlx=True, num_hidden_layers=2, block_size=8, n_taps=2)
+    d.bind(tiny)
+    rng = np.random.default_rng(1)
+    V = tiny.args.vocab_size
+    prompt = rng.integers(0, V, 40).tolist()
+    cache = tiny.make_cache(max_ctx=256)
+    _, fused = tiny.prefill(prompt, cache, list(cfg.target_layer_ids))
+    dcache = d.make_cache(max_ctx=256)
+    block = [int(prompt[-1])] + [cfg.mask_token_id] * (cfg.block_size - 1)
+    got = d(block, fused[0], dcache, logits_start=1)
+    ref_t = OM.OracleTarget(tiny)
+    od = OM.OracleDFlash(d, ref_t)
+    want = od(block, fused[0].float().cpu(), logits_start=1)
+    assert_logits_close(got[0], want, None, "dflash round 1")
+    # a second round: 3 more context rows
+    more = fused[0, :3]
+    got2 = d(block, more, dcache, logits_start=1)
+    want2 = od(block, more.float().cpu(), logits_start=1)
+    assert_logits_close(got2[0], want2, None, "dflash round 2")
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_dflash_generate_reproduces_greedy_stream(dev, tiny, use_graph):
+    from mlx_dspark import synthetic
+    from mlx_dspark.generate import dflash_generate
+    from mlx_dspark.target import Target
+    from mlx_dspark.tokenizer import SyntheticTokenizer
+    d, cfg = synthetic.build_dflash(tiny.args, seed=9, keep_mlx=True, num_hidden_layers=2, block_size=8, n_taps=2)
+    d.bind(tiny)
+    tok = SyntheticTokenizer(tiny.args.vocab_size)
+    target = Target(tiny, tok)
+    rng = np.random.default_rng(2)
+    prompt = rng.integers(0, tiny.args.vocab_size, 33).tolist()
+    res = dflash_generate(target, tok, d, prompt_ids=prompt, max_new_tokens=24, use_graph=use_graph)
+    ref_tokens, margins = OM.greedy_decode(OM.OracleTarget(tiny), prompt, len(res.token_ids))
+    for i, (a, b) in enumerate(zip(res.token_ids, ref_tokens)):
+        if a != b:
+            assert margins[i] <= TOL, (i, a, b, margins[i])
+            break
+    assert res.num_tokens >= 24 and sum(res.accept_lengths) + 1 == res.num_tokens
+    assert res.text == tok.decode(res.token_ids)
+
+
+def test_dflash_generate_sampled_is_seeded(dev, tiny):
+    from mlx_dspark import synthetic
+    from mlx_dspark.generate import dflash_generate
+    from mlx_dspark.target import Target
+    from mlx_dspark.tokenizer import SyntheticTokenizer
+    d, cfg = synthetic.build_dflash(tiny.args, seed=9, num_hidden_layers=1, block_size=4, n_taps=2)
+    d.bind(tiny)
+    tok = SyntheticTokenizer(tiny.args.vocab_size)
+    target = Target(tiny, tok)
+    kw = dict(prompt_ids=list(range(20)), max_new_tokens=16, temperature=0.8, top_p=0.9, seed=123)
+    a = dflash_generate(target, tok, d, **kw)
+    b = dflash_generate(target, tok, d, **kw)
+    c = dflash_generate(target, tok, d, **{**kw, "seed": 124})
+    assert a.token_ids == b.token_ids
+    assert a.token_ids != c.token_ids
