@@ -47,37 +47,40 @@ def kv_bytes_per_token(args, kv_bits) -> int:
 
 
 def gemm_roofline(model, M: int, reps_per_shape: int | None = None):
-    """Average launch duration of the W8 GEMM kernel at every verify-step shape, each launch
-    bracketed by its own pair of HIP events on the launch stream, weights rotating through
-    the 36 layers so every launch streams its weights from HBM."""
+    """Average launch duration of the W8 GEMM kernel at every verify-step shape, with the
+    epilogue the forward uses (split-K partials for qkv / o / down, fused SwiGLU for gate_up,
+    f32 logits for the head), each launch bracketed by its own pair of HIP events on the launch
+    stream, weights rotating through the 36 layers so every launch streams its weights from HBM."""
     import torch
     from mlx_dspark import ops
 
     dev = model.device
-    shapes = {"qkv": [L.qkv for L in model.layers], "o": [L.o for L in model.layers],
-              "gate_up": [L.gate_up for L in model.layers], "down": [L.down for L in model.layers],
-              "lm_head": [model.lm_head]}
+    P, SW = ops.DSK_EPI_PARTIAL, ops.DSK_EPI_SWIGLU
+    shapes = {"qkv": ([L.qkv for L in model.layers], P), "o": ([L.o for L in model.layers], P),
+              "gate_up": ([L.gate_up for L in model.layers], SW), "down": ([L.down for L in model.layers], P),
+              "lm_head": ([model.lm_head], ops.DSK_EPI_STORE)}
     res = {}
     tot_bytes = tot_us = 0.0
     tot_launch = 0
     per_step = {"qkv": len(model.layers), "o": len(model.layers), "gate_up": len(model.layers),
                 "down": len(model.layers), "lm_head": 1}
     filler = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
-    for name, ws in shapes.items():
+    stream = torch.cuda.current_stream()
+    for name, (ws, epi) in shapes.items():
         K = ws[0].K
-        x = torch.randn(M, K, device=dev).to(torch.bfloat16)
-        a = ops.act_pack(x)
-        y = torch.empty(M, ws[0].N, device=dev, dtype=torch.bfloat16)
-        for w in ws[:2]:
-            ops.w8_gemm(a, w, M, out=y)                           # size the workspace
+        x = ops.pack(torch.randn(M, K, device=dev).to(torch.bfloat16))
+        out = None
+        if epi == ops.DSK_EPI_STORE:
+            out = torch.empty(M, ws[0].N, device=dev, dtype=torch.float32)
+        y = ops.w8_gemm(x, ws[0], epi=epi, out=out)
         n = reps_per_shape or max(len(ws), 8)
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
         torch.cuda.synchronize()
         filler.zero_()                                            # keeps the GPU busy while we enqueue
         for i in range(n):
-            ev[i][0].record()
-            ops.w8_gemm(a, ws[i % len(ws)], M, out=y)
-            ev[i][1].record()
+            ev[i][0].record(stream)
+            ops.w8_gemm(x, ws[i % len(ws)], epi=epi, out=y)
+            ev[i][1].record(stream)
         torch.cuda.synchronize()
         us = statistics.mean(s.elapsed_time(e) * 1e3 for s, e in ev)
         by = ws[0].N * ws[0].K * 1.0625

@@ -56,52 +56,65 @@ int dsk_abi_version(void);
  *   Rule per group of 64: lo = min, hi = max, scale = bf16((hi - lo) / 255) (scale = 1
  *   when hi == lo), bias = bf16(lo), q = clamp(rint((w - bias) / scale), 0, 255).
  * dsk_w8_repack: MLX layout -> the engine's tiled HBM layout consumed by dsk_w8_gemm:
- *   wt [N/16][K/64][64 lanes][16 B], sb [N/16][16][K/64] u32 (bf16 scale | bf16 bias << 16).
- *   N % 16 == 0, K % 64 == 0.
+ *   wt [N/16][K/64][64 lanes][16 B], sb [N/16][K/64][16] u32 (bf16 scale | bf16 bias << 16).
+ *   N % 16 == 0, K % 64 == 0. paired != 0 (gated MLPs, N % 32 == 0): rows [0, N/2) are the
+ *   gate projection and [N/2, N) the up projection; tile 2p takes gate rows 16p..16p+15 and
+ *   tile 2p+1 up rows 16p..16p+15, as dsk_w8_gemm's gated epilogues expect.
  * ------------------------------------------------------------------------------------- */
 int dsk_w8_quantize(const void* w, int w_dtype, int64_t N, int64_t K, uint8_t* q,
                     uint16_t* scales, uint16_t* biases, dsk_stream_t stream);
 int dsk_w8_repack(const uint8_t* q, const uint16_t* scales, const uint16_t* biases, int64_t N,
-                  int64_t K, uint8_t* wt, uint32_t* sb, dsk_stream_t stream);
+                  int64_t K, int paired, uint8_t* wt, uint32_t* sb, dsk_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------
- * Activation pack (GEMM prologue).
- * Replaces mx.fast.rms_norm (src/mlx_dspark/model.py:28, nn.RMSNorm at :103-106,
- * :165-170, :233-235, and the Qwen3 input/post-attention norms inside mlx_lm), the MLP
- * activation silu(gate) * up (src/mlx_dspark/model.py:44-45) / gelu_approx for the gemma
- * family, and the bf16 -> MFMA operand staging in front of every quantized matmul.
+ * Packed activations.
+ * The W8 GEMM reads its activation operand in a packed layout: element (m, k) of an [M, K]
+ * bf16 matrix lives at P[m/16][k/64][m%16 + 16*((k%64)/16)][k%16] (dsk_act_pack_bytes(M, K)
+ * bytes; rows past M are padding with arbitrary values).
  *
- * x [M, *] bf16 with row stride ldx (elements). mode:
- *   DSK_PACK_PLAIN   a = x[:, :K]
- *   DSK_PACK_RMSNORM a = bf16(x * rsqrt(mean(x^2) + eps) * norm_w)   (norm_w [K] bf16)
- *   DSK_PACK_SILU    a = bf16(silu(x[:, :K]) * x[:, K:2K])
- *   DSK_PACK_GELU    a = bf16(gelu_tanh(x[:, :K]) * x[:, K:2K])
- * out: packed operand of dsk_act_pack_bytes(M, K) bytes. M <= 64, K % 64 == 0, K <= 24576.
+ * dsk_act_pack builds it, fusing what precedes every projection of a decoder layer:
+ *   v = part ? sum_{s < nsplit} part[s][m][k] : 0      (fp32 partial sums of a split-K
+ *                                                       GEMM, slice stride M*K, in order)
+ *   v = h ? (part ? bf16(h[m][k] + v) : h[m][k]) : bf16(v)    (residual add; h updated in
+ *                                                               place when part != NULL)
+ *   copy[m][k] = v                                     (copy != NULL: hidden-state tap)
+ *   out = packed(norm_w ? bf16((v * rsqrt(mean_k(v^2) + eps)) * norm_w[k]) : v)
+ * It replaces the residual adds of the Qwen3 layers (mlx_lm), the hidden-state capture of
+ * src/mlx_dspark/target.py:120-121 and mx.fast.rms_norm (src/mlx_dspark/model.py:28,
+ * nn.RMSNorm at :103-106, :165-170, :233-235, dflash_model.py:96-99, and the Qwen3 input /
+ * post-attention / final norms inside mlx_lm). M <= 64, K % 64 == 0, K <= 24576, row strides
+ * multiples of 8, 16-byte aligned pointers; out may be NULL (h update / copy only).
  * ------------------------------------------------------------------------------------- */
-enum { DSK_PACK_PLAIN = 0, DSK_PACK_RMSNORM = 1, DSK_PACK_SILU = 2, DSK_PACK_GELU = 3 };
 size_t dsk_act_pack_bytes(int M, int64_t K);
-int dsk_act_pack(const uint16_t* x, int64_t ldx, int M, int64_t K, int mode,
-                 const uint16_t* norm_w, float eps, void* out, dsk_stream_t stream);
+int dsk_act_pack(const float* part, int nsplit, uint16_t* h, int64_t ldh, uint16_t* copy,
+                 int64_t ldc, int M, int64_t K, const uint16_t* norm_w, float eps, uint16_t* out,
+                 dsk_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------
- * W8 skinny GEMM: y[M, N] = residual + a[M, K] . deq(W)[N, K]^T
+ * W8 skinny GEMM: y[M, N] = x[M, K] . deq(W)[N, K]^T
  * Replaces mx.quantized_matmul behind nn.QuantizedLinear (external mlx), reached from
  * src/mlx_dspark/target.py:115-123 (every target projection and the lm_head / tied
  * embed_tokens.as_linear), src/mlx_dspark/batch_engine.py:199-204 (batched verify) and
  * the drafter linears (src/mlx_dspark/model.py:97-101, :230-236; dflash_model.py:93-96).
  *
- * a: packed by dsk_act_pack. W: dsk_w8_repack layout. y: f32 or bf16, row stride ldy.
- * residual: NULL or bf16 [M, N] with row stride ldr (may alias y when y is bf16).
- * softcap > 0 applies y = tanh(y / softcap) * softcap (src/mlx_dspark/model.py:264-268).
- * workspace: >= dsk_w8_gemm_ws_bytes(M, N, K) bytes; its counter region must be zeroed
- * once after allocation (dsk_w8_gemm_ws_init); it is left zeroed after every call.
+ * x: packed (dsk_act_pack). W: dsk_w8_repack layout. M <= 64, N % 16 == 0, K % 256 == 0.
+ * epi = DSK_EPI_STORE: y f32 or bf16 [M, N] (row stride ldy) = residual + x.W^T, residual
+ *   NULL or bf16 [M, N] with row stride ldr (may alias y when y is bf16); softcap > 0
+ *   applies y = tanh(y / softcap) * softcap (src/mlx_dspark/model.py:264-268).
+ * epi = DSK_EPI_PARTIAL: y f32 [S][M][N], S = dsk_w8_gemm_splits(M, N, K) partial sums over
+ *   disjoint K ranges (their sum, in slice order, is the product; dsk_act_pack and
+ *   dsk_qkv_rope_append take them as input).
+ * epi = DSK_EPI_SWIGLU / DSK_EPI_GEGLU: W is a paired gate|up repack (N = 2 I, I % 128 == 0);
+ *   y = packed bf16 [M, I] of bf16(bf16(act(bf16(gate))) * bf16(up)), act = silu or
+ *   tanh-approximated gelu (the MLP of src/mlx_dspark/model.py:35-45 and of the Qwen3 /
+ *   Gemma layers), ready as the next GEMM's x.
+ * No workspace; no state is kept between calls.
  * ------------------------------------------------------------------------------------- */
-size_t dsk_w8_gemm_ws_bytes(int M, int64_t N, int64_t K);
-int dsk_w8_gemm_ws_init(void* workspace, size_t ws_bytes, dsk_stream_t stream);
-int dsk_w8_gemm(const void* a, const uint8_t* wt, const uint32_t* sb, int M, int64_t N,
-                int64_t K, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
-                int64_t ldr, float softcap, void* workspace, size_t ws_bytes,
-                dsk_stream_t stream);
+enum { DSK_EPI_STORE = 0, DSK_EPI_SWIGLU = 1, DSK_EPI_GEGLU = 2, DSK_EPI_PARTIAL = 3 };
+int dsk_w8_gemm_splits(int M, int64_t N, int64_t K);
+int dsk_w8_gemm(const uint16_t* x, const uint8_t* wt, const uint32_t* sb, int M, int64_t N,
+                int64_t K, int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
+                int64_t ldr, float softcap, dsk_stream_t stream);
 
 /* W8 row gather (embedding lookup): out[i, :] = bf16(deq(table)[ids[i], :]) * scale.
  * Replaces nn.QuantizedEmbedding (mm.embed_tokens, src/mlx_dspark/target.py:112;
@@ -123,14 +136,16 @@ int dsk_w8_embed(const int32_t* ids, int n, const uint8_t* q, const uint16_t* sc
  * seq_lens [B] int32 = tokens cached per row before the call (device memory).
  * ------------------------------------------------------------------------------------- */
 
-/* qkv [B*W, (nq + 2*nkv) * hd] bf16 (rows b*W + i) -> per-head RMSNorm of q and k
+/* qkv: the fused projection of B*W rows (row b*W + i), either bf16 [B*W, (nq + 2*nkv) * hd]
+ * (qkv_splits == 0) or the fp32 partial sums of dsk_w8_gemm DSK_EPI_PARTIAL
+ * [qkv_splits][B*W][(nq + 2*nkv) * hd] (summed in order and rounded to bf16) -> per-head RMSNorm of q and k
  * (q_norm/k_norm weights [hd] bf16), rotate-half RoPE at position seq_lens[b] + i
  * (inv_freq [hd/2] f32), K/V appended to the pool at that position, and
  * q_out [B*W, nq*hd] bf16. Replaces the Qwen3 attention prologue inside mlx_lm and
  * DSparkAttention._kv/update_ctx (src/mlx_dspark/model.py:113-128). k_norm may be NULL
  * (no norm). pos_offset is added to every position. nq may be 0 (K/V rows only, as for a
  * drafter's context rows; q_out may then be NULL). */
-int dsk_qkv_rope_append(const uint16_t* qkv, int B, int W, int nq, int nkv, int hd,
+int dsk_qkv_rope_append(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
                         const uint16_t* q_norm, const uint16_t* k_norm, float eps,
                         const float* inv_freq, const int32_t* seq_lens, int pos_offset,
                         const int32_t* block_table, int max_pages, int page, int kv_dtype,
@@ -146,14 +161,16 @@ int dsk_qkv_rope_append(const uint16_t* qkv, int B, int W, int nq, int nkv, int 
  *   src/mlx_dspark/model.py:130-155, dflash_model.py:123-133).
  * q [B*W, nq*hd] bf16 -> out [B*W, nq*hd] bf16. GQA: q head h reads kv head h/(nq/nkv).
  * max_ctx bounds seq_lens[b] + W (sizes the split grid so the launch is graph-stable).
- * softcap > 0: scores = tanh(scores / softcap) * softcap before the mask. */
+ * softcap > 0: scores = tanh(scores / softcap) * softcap before the mask.
+ * out_packed != 0 writes the output in the packed activation layout (the o-projection's x).
+ * workspace: dsk_attn_ws_bytes(...) bytes for the split partials (the splits are combined by
+ * a second kernel on the same stream; no state is kept between calls). */
 size_t dsk_attn_ws_bytes(int B, int W, int nq, int hd, int max_ctx);
-int dsk_attn_ws_init(void* workspace, size_t ws_bytes, dsk_stream_t stream);
 int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, int hd, float scale,
                   int causal, int window, float softcap, const int32_t* seq_lens,
                   int max_ctx, const int32_t* block_table, int max_pages, int page,
                   int kv_dtype, const void* k_pool, const void* v_pool,
-                  const uint32_t* k_sb, const uint32_t* v_sb, uint16_t* out,
+                  const uint32_t* k_sb, const uint32_t* v_sb, uint16_t* out, int out_packed,
                   void* workspace, size_t ws_bytes, dsk_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------

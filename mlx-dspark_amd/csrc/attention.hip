@@ -46,7 +46,7 @@ __device__ __forceinline__ void kv_quant_store(float v0, float v1, int lane, int
 // One wave per (token row, head): lane holds dims [PER*lane, PER*lane + PER) (PER = HD/64).
 template <int HD>
 __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
-    const uint16_t* __restrict__ qkv, int B, int W, int nq, int nkv, const uint16_t* __restrict__ q_norm,
+    const void* __restrict__ qkv, int qkv_splits, int B, int W, int nq, int nkv, const uint16_t* __restrict__ q_norm,
     const uint16_t* __restrict__ k_norm, float eps, const float* __restrict__ inv_freq,
     const int32_t* __restrict__ seq_lens, int pos_offset, const int32_t* __restrict__ block_table, int max_pages,
     int page, int kv_dtype, void* __restrict__ k_pool, void* __restrict__ v_pool, uint32_t* __restrict__ k_sb,
@@ -59,10 +59,34 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
   if (row >= B * W) return;
   const int b = row / W, i = row % W;
   const int pos = seq_lens[b] + i + pos_offset;
-  const uint16_t* src = qkv + (int64_t)row * nheads * HD + (int64_t)head * HD;
   float v[PER];
+  if (qkv_splits == 0) {
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(qkv) + (int64_t)row * nheads * HD + (int64_t)head * HD;
 #pragma unroll
-  for (int e = 0; e < PER; ++e) v[e] = bf16_to_f32(src[lane * PER + e]);
+    for (int e = 0; e < PER; ++e) v[e] = bf16_to_f32(src[lane * PER + e]);
+  } else {
+    // fp32 partial sums [splits][B*W][nheads*HD], summed in split order, rounded to bf16
+    // (the projection's output dtype)
+    const int64_t slice = (int64_t)B * W * nheads * HD;
+    const float* src = reinterpret_cast<const float*>(qkv) + (int64_t)row * nheads * HD + (int64_t)head * HD;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) v[e] = 0.0f;
+    // four slices' loads in flight at a time, summed in slice order
+    for (int sp = 0; sp < qkv_splits; sp += 4) {
+      float t[4][PER];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < PER; ++e) t[u][e] = sp + u < qkv_splits ? src[(sp + u) * slice + lane * PER + e] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < PER; ++e)
+          if (sp + u < qkv_splits) v[e] += t[u][e];
+    }
+#pragma unroll
+    for (int e = 0; e < PER; ++e) v[e] = round_bf16(v[e]);
+  }
 
   const bool is_q = head < nq, is_k = !is_q && head < nq + nkv;
   const uint16_t* nw = is_q ? q_norm : (is_k ? k_norm : nullptr);
@@ -83,9 +107,12 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
       const float partner = __shfl_xor(v[e], 32, 64);
       const int d = lane * PER + e;
       const int dd = first_half ? d : d - HD / 2;
+      // angle in fp32 as the reference computes it, reduced to [-1/2, 1/2) revolutions for
+      // v_sin_f32 / v_cos_f32 (the reduction error is below the angle's own rounding)
       const float ang = (float)pos * inv_freq[dd];
-      float sn, cs;
-      sincosf(ang, &sn, &cs);
+      float rev = ang * 0.15915494309189535f;
+      rev -= rintf(rev);
+      const float sn = __builtin_amdgcn_sinf(rev), cs = __builtin_amdgcn_cosf(rev);
       const float x1 = first_half ? v[e] : partner, x2 = first_half ? partner : v[e];
       v[e] = round_bf16(first_half ? x1 * cs - x2 * sn : x2 * cs + x1 * sn);
     }
@@ -152,295 +179,309 @@ struct AttnArgs {
   const uint32_t* k_sb;
   const uint32_t* v_sb;
   uint16_t* out;
-  int nsplit, split_tokens;
-  float* part;  // [B][nkv][nsplit][R][HD + 2]
-  int* cnt;     // [B * nkv]
+  int out_packed;
+  int nsplit;
+  float* part;  // [B][nkv][nsplit][R][HD + 4]: o (unnormalised) | m | l | 0 | 0
 };
 
-constexpr int kKeyTile = 32;
-template <int HD> struct Lds { static constexpr int KROW = HD + 8, VROW = kKeyTile + 8; };
-
-// K/V tile staging, split into a global->register load (issued one tile ahead) and a
-// register->LDS store (dequantising 8-bit KV to bf16).
-template <int HD>
-struct KVRegs {
-  static constexpr int CPT = kKeyTile * HD / 8 / 256;  // 8-element chunks per thread
-  u32x4 k[CPT], v[CPT];
-  uint32_t ksb[CPT], vsb[CPT];
-  bool valid[CPT];
+// keys per split: one workgroup loads its whole split at once
+template <int HD> struct Split {
+  static constexpr int KEYS = HD == 128 ? 128 : 64;
+  static constexpr int KROW = HD + 8;    // K rows in LDS (bf16, padded)
+  static constexpr int VROW = KEYS + 8;  // V^T rows in LDS (bf16, padded)
+  static constexpr int CK = KEYS * HD / 8 / 256;        // 8-element K chunks per thread
+  static constexpr int CV = (KEYS / 2) * (HD / 8) / 256;  // (2 keys x 8 dims) V chunks per thread
+  static constexpr int PSTRIDE = HD + 4;
 };
 
-template <int HD>
-__device__ __forceinline__ void load_kv(const AttnArgs& a, int b, int kvh, int j0, int Lk, KVRegs<HD>& r) {
+// output row (b, i), head h, dim d: row-major [B*W, nq*HD] or packed
+__device__ __forceinline__ int64_t attn_out_index(const AttnArgs& a, int HD, int b, int i, int h, int d) {
+  const int64_t m = (int64_t)b * a.W + i, k = (int64_t)h * HD + d;
+  return a.out_packed ? apack_index(m, k, (int64_t)a.nq * HD / 64) : m * a.nq * HD + k;
+}
+
+__device__ __forceinline__ int64_t kv_token(const AttnArgs& a, int b, int kvh, int j) {
+  const int pg = a.block_table[(int64_t)b * a.max_pages + j / a.page];
+  return ((int64_t)pg * a.nkv + kvh) * a.page + (j % a.page);
+}
+
+// 8 consecutive dims of one token as bf16 (dequantised for 8-bit KV)
+struct Chunk8 {
+  u32x4 raw;
+  uint32_t sb;
+};
+template <int KVT>
+__device__ __forceinline__ void load_chunk(const void* pool, const uint32_t* sbp, int HD, int64_t tok, int d0,
+                                           Chunk8& c) {
+  if (KVT == DSK_KV_BF16) {
+    c.raw = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(pool) + tok * HD + d0);
+  } else {
+    const uint2 r = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(pool) + tok * HD + d0);
+    c.raw = u32x4{r.x, r.y, 0, 0};
+    c.sb = sbp[tok * (HD / 64) + d0 / 64];
+  }
+}
+template <int KVT>
+__device__ __forceinline__ void chunk_bf16(const Chunk8& c, uint16_t (&h)[8]) {
+  if (KVT == DSK_KV_BF16) {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(&c.raw);
 #pragma unroll
-  for (int ci = 0; ci < KVRegs<HD>::CPT; ++ci) {
-    const int c = threadIdx.x + ci * 256;
-    const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
-    const int j = j0 + key;
-    r.valid[ci] = j < Lk;
-    if (!r.valid[ci]) continue;
-    const int pg = a.block_table[(int64_t)b * a.max_pages + j / a.page];
-    const int64_t tok = ((int64_t)pg * a.nkv + kvh) * a.page + (j % a.page);
-    if (a.kv_dtype == DSK_KV_BF16) {
-      r.k[ci] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.k_pool) + tok * HD + d0);
-      r.v[ci] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.v_pool) + tok * HD + d0);
-    } else {
-      const uint2 kr = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.k_pool) + tok * HD + d0);
-      const uint2 vr = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(a.v_pool) + tok * HD + d0);
-      r.k[ci] = u32x4{kr.x, kr.y, 0, 0};
-      r.v[ci] = u32x4{vr.x, vr.y, 0, 0};
-      r.ksb[ci] = a.k_sb[tok * (HD / 64) + d0 / 64];
-      r.vsb[ci] = a.v_sb[tok * (HD / 64) + d0 / 64];
-    }
+    for (int e = 0; e < 8; ++e) h[e] = p[e];
+  } else {
+    const float sc = bf16_to_f32((uint16_t)(c.sb & 0xffff)), bi = bf16_to_f32((uint16_t)(c.sb >> 16));
+    const uint8_t* qb = reinterpret_cast<const uint8_t*>(&c.raw);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = f32_to_bf16(fmaf(sc, (float)qb[e], bi));
   }
 }
 
-template <int HD>
-__device__ __forceinline__ void store_kv(const AttnArgs& a, const KVRegs<HD>& r, uint16_t* ks, uint16_t* vt) {
-  // ks: [32 keys][KROW] bf16 row-major; vt: [HD][VROW] bf16 (transposed V), rows padded.
-#pragma unroll
-  for (int ci = 0; ci < KVRegs<HD>::CPT; ++ci) {
-    const int c = threadIdx.x + ci * 256;
-    const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
-    uint16_t kh[8], vh[8];
-    if (!r.valid[ci]) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) kh[e] = vh[e] = 0;
-    } else if (a.kv_dtype == DSK_KV_BF16) {
-      const uint16_t* kk = reinterpret_cast<const uint16_t*>(&r.k[ci]);
-      const uint16_t* vv = reinterpret_cast<const uint16_t*>(&r.v[ci]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        kh[e] = kk[e];
-        vh[e] = vv[e];
-      }
-    } else {
-      const float ksc = bf16_to_f32((uint16_t)(r.ksb[ci] & 0xffff)), kbi = bf16_to_f32((uint16_t)(r.ksb[ci] >> 16));
-      const float vsc = bf16_to_f32((uint16_t)(r.vsb[ci] & 0xffff)), vbi = bf16_to_f32((uint16_t)(r.vsb[ci] >> 16));
-      const uint8_t* kb = reinterpret_cast<const uint8_t*>(&r.k[ci]);
-      const uint8_t* vb = reinterpret_cast<const uint8_t*>(&r.v[ci]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        kh[e] = f32_to_bf16(fmaf(ksc, (float)kb[e], kbi));
-        vh[e] = f32_to_bf16(fmaf(vsc, (float)vb[e], vbi));
-      }
-    }
-    *reinterpret_cast<u32x4*>(ks + key * Lds<HD>::KROW + d0) = *reinterpret_cast<const u32x4*>(kh);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) vt[(d0 + e) * Lds<HD>::VROW + key] = vh[e];
-  }
-}
-
-template <int HD, int QT>
+// One workgroup per (row b, kv head, split of KEYS keys): every K/V load of the split is
+// issued at once, dequantised into LDS (K row-major, V transposed), then each wave takes
+// 16-query tiles through scores, a one-pass softmax and P.V. Splits at or past the row's
+// key count exit at once (the combine reads only the live ones).
+template <int HD, int QT, int KVT, bool SOFTCAP>
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t ks[kKeyTile * Lds<HD>::KROW];
-  __shared__ __attribute__((aligned(16))) uint16_t vt[HD * Lds<HD>::VROW];
-  __shared__ int last;
+  using S = Split<HD>;
+  constexpr int KEYS = S::KEYS, KROW = S::KROW, VROW = S::VROW;
+  __shared__ __attribute__((aligned(16))) uint16_t ks[KEYS * KROW];
+  __shared__ __attribute__((aligned(16))) uint32_t vt[HD * VROW / 2];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int split = blockIdx.x % a.nsplit;
   const int bk = blockIdx.x / a.nsplit;  // b * nkv + kvh
   const int b = bk / a.nkv, kvh = bk % a.nkv;
   const int off = a.seq_lens[b];
-  const int Lk = off + a.W;
-  const int j_lo = split * a.split_tokens;
-  const int j_hi = min(min(Lk, j_lo + a.split_tokens), a.max_pages * a.page);
-  constexpr int DT = HD / 16;  // d tiles of the output
+  const int Lk = min(off + a.W, a.max_pages * a.page);
+  const int j_lo = split * KEYS;
+  if (j_lo >= Lk) return;
+  const int j_hi = min(Lk, j_lo + KEYS);
+  constexpr int DT = HD / 16;  // output d tiles
   constexpr int KS = HD / 32;  // k steps of the score MFMA
+  constexpr int NKT = KEYS / 16;  // key tiles
 
-  // query rows handled by this wave: tiles wv, wv + 4, ... ; row r = i * G + hl
-  f32x4 o[QT][DT];
-  float mrow[QT], lrow[QT];
-  bf16x8 qf[QT][KS];
-  int qi[QT];
-  bool qvalid[QT];
+  // ---- issue every load of the split
+  Chunk8 kc[S::CK], vc[S::CV][2];
 #pragma unroll
-  for (int t = 0; t < QT; ++t) {
-    const int r = (wv + 4 * t) * 16 + (lane & 15);
-    qvalid[t] = r < a.R;
-    const int i = qvalid[t] ? r / a.G : 0, hl = qvalid[t] ? r % a.G : 0;
-    qi[t] = i;
-    const uint16_t* qp = a.q + ((int64_t)(b * a.W + i) * a.nq + kvh * a.G + hl) * HD;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      u32x4 raw = qvalid[t] ? *reinterpret_cast<const u32x4*>(qp + s * 32 + (lane >> 4) * 8) : u32x4{0, 0, 0, 0};
-      qf[t][s] = __builtin_bit_cast(bf16x8, raw);
-    }
-#pragma unroll
-    for (int d = 0; d < DT; ++d) o[t][d] = f32x4{0, 0, 0, 0};
-    mrow[t] = -__builtin_inff();
-    lrow[t] = 0.0f;
+  for (int ci = 0; ci < S::CK; ++ci) {
+    const int c = threadIdx.x + ci * 256;
+    const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+    const int j = min(j_lo + key, j_hi - 1);  // keys past j_hi are masked below
+    load_chunk<KVT>(a.k_pool, a.k_sb, HD, kv_token(a, b, kvh, j), d0, kc[ci]);
   }
+#pragma unroll
+  for (int ci = 0; ci < S::CV; ++ci) {
+    const int c = threadIdx.x + ci * 256;
+    const int kp = c % (KEYS / 2), d0 = (c / (KEYS / 2)) * 8;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int j = min(j_lo + 2 * kp + u, j_hi - 1);
+      load_chunk<KVT>(a.v_pool, a.v_sb, HD, kv_token(a, b, kvh, j), d0, vc[ci][u]);
+    }
+  }
+  // query fragments of tile t (row r = tile * 16 + lane % 16 = i * G + hl); the first tile's
+  // are loaded with the K/V, each later tile's one tile ahead
+  auto load_q = [&](int t, u32x4 (&qr)[KS]) {
+    const int r = (wv + 4 * t) * 16 + (lane & 15);
+    const int rr = r < a.R ? r : 0;
+    const uint16_t* qp = a.q + ((int64_t)(b * a.W + rr / a.G) * a.nq + kvh * a.G + rr % a.G) * HD;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qp + s * 32 + (lane >> 4) * 8);
+  };
+  u32x4 qnext[KS];
+  load_q(0, qnext);
 
-  KVRegs<HD> kvr;
-  if (j_lo < j_hi) load_kv<HD>(a, b, kvh, j_lo, j_hi, kvr);
-  for (int j0 = j_lo; j0 < j_hi; j0 += kKeyTile) {
-    __syncthreads();
-    store_kv<HD>(a, kvr, ks, vt);
-    if (j0 + kKeyTile < j_hi) load_kv<HD>(a, b, kvh, j0 + kKeyTile, j_hi, kvr);  // next tile in flight
-    __syncthreads();
+  // ---- dequantise into LDS
 #pragma unroll
-    for (int t = 0; t < QT; ++t) {
-      if (wv + 4 * t >= (a.R + 15) / 16) continue;
-      // scores for keys j0 + {0..15} (h = 0) and j0 + {16..31} (h = 1)
-      f32x4 st[2];
+  for (int ci = 0; ci < S::CK; ++ci) {
+    const int c = threadIdx.x + ci * 256;
+    const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+    uint16_t h[8];
+    chunk_bf16<KVT>(kc[ci], h);
+    *reinterpret_cast<u32x4*>(ks + key * KROW + d0) = *reinterpret_cast<const u32x4*>(h);
+  }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        f32x4 acc = {0, 0, 0, 0};
+  for (int ci = 0; ci < S::CV; ++ci) {
+    const int c = threadIdx.x + ci * 256;
+    const int kp = c % (KEYS / 2), d0 = (c / (KEYS / 2)) * 8;
+    uint16_t h0[8], h1[8];
+    chunk_bf16<KVT>(vc[ci][0], h0);
+    chunk_bf16<KVT>(vc[ci][1], h1);
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + (h * 16 + (lane & 15)) * Lds<HD>::KROW + s * 32 + (lane >> 4) * 8);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[t][s], acc, 0, 0, 0);
-        }
-        st[h] = acc;
+    for (int e = 0; e < 8; ++e) vt[((d0 + e) * VROW) / 2 + kp] = (uint32_t)h0[e] | ((uint32_t)h1[e] << 16);
+  }
+  __syncthreads();
+
+  const uint16_t* vt16 = reinterpret_cast<const uint16_t*>(vt);
+#pragma unroll 1
+  for (int t = 0; t < QT; ++t) {
+    if (wv + 4 * t >= (a.R + 15) / 16) break;
+    bf16x8 qf[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = __builtin_bit_cast(bf16x8, qnext[s]);
+    if (t + 1 < QT && wv + 4 * (t + 1) < (a.R + 15) / 16) load_q(t + 1, qnext);
+    const int rq = (wv + 4 * t) * 16 + (lane & 15);
+    const bool qvalid = rq < a.R;
+    // ---- scores: lane holds S^T[key = 16h + 4*(lane/16) + r][q = lane % 16]
+    f32x4 st[NKT];
+#pragma unroll
+    for (int h = 0; h < NKT; ++h) {
+      f32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + (h * 16 + (lane & 15)) * KROW + s * 32 + (lane >> 4) * 8);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s], acc, 0, 0, 0);
       }
-      // lane holds S^T[key = h*16 + 4*(lane/16) + r][q = lane % 16]
-      const int qpos = off + qi[t];
-      float smax = -__builtin_inff();
-      float sv[2][4];
+      st[h] = acc;
+    }
+    const int qpos = off + (qvalid ? rq / a.G : 0);
+    float mx = -__builtin_inff();
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < NKT; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = j_lo + h * 16 + (lane >> 4) * 4 + r;
+        float sc = st[h][r] * a.scale;
+        if (SOFTCAP) sc = tanhf(sc / a.softcap) * a.softcap;
+        bool ok = j < j_hi && qvalid;
+        if (a.causal) {
+          ok = ok && j <= qpos;
+          if (a.window > 0) ok = ok && j > qpos - a.window;
+        }
+        sc = ok ? sc : -__builtin_inff();
+        st[h][r] = sc;
+        mx = fmaxf(mx, sc);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float lsum = 0.0f;
+    bf16x8 pb[KEYS / 32];
+#pragma unroll
+    for (int c = 0; c < KEYS / 32; ++c)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int j = j0 + h * 16 + (lane >> 4) * 4 + r;
-          float s = st[h][r] * a.scale;
-          if (a.softcap > 0.0f) s = tanhf(s / a.softcap) * a.softcap;
-          bool ok = j < j_hi && qvalid[t];
-          if (a.causal) {
-            ok = ok && j <= qpos;
-            if (a.window > 0) ok = ok && j > qpos - a.window;
-          }
-          s = ok ? s : -__builtin_inff();
-          sv[h][r] = s;
-          smax = fmaxf(smax, s);
+          const float sc = st[2 * c + hh][r];
+          const float p = sc == -__builtin_inff() ? 0.0f : round_bf16(__expf(sc - mx));
+          lsum += p;
+          pb[c][hh * 4 + r] = (__bf16)p;
         }
-      smax = fmaxf(smax, __shfl_xor(smax, 16, 64));
-      smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
-      const float mnew = fmaxf(mrow[t], smax);
-      const float alpha = (mnew == -__builtin_inff()) ? 1.0f : __expf(mrow[t] - mnew);
-      float psum = 0.0f;
-      float pv[8];
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    // ---- O^T[d][q] = V^T . P^T: A = V^T rows d*16 + lane%16, keys in pb's order
+    f32x4 o[DT];
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+    for (int d = 0; d < DT; ++d) {
+      f32x4 acc = {0, 0, 0, 0};
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = (sv[h][r] == -__builtin_inff()) ? 0.0f : __expf(sv[h][r] - mnew);
-          const float pr = round_bf16(p);
-          pv[h * 4 + r] = pr;
-          psum += pr;
-        }
-      psum += __shfl_xor(psum, 16, 64);
-      psum += __shfl_xor(psum, 32, 64);
-      lrow[t] = lrow[t] * alpha + psum;
-      mrow[t] = mnew;
-      bf16x8 pb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pb[e] = (__bf16)pv[e];
-#pragma unroll
-      for (int d = 0; d < DT; ++d) {
-        // A = V^T rows d*16 + lane%16, keys in the same order as pb: {4c..4c+3, 16+4c..16+4c+3}
-        const uint16_t* vr = vt + (d * 16 + (lane & 15)) * Lds<HD>::VROW + (lane >> 4) * 4;
+      for (int c = 0; c < KEYS / 32; ++c) {
+        const uint16_t* vr = vt16 + (d * 16 + (lane & 15)) * VROW + 32 * c + (lane >> 4) * 4;
         const uint2 lo = *reinterpret_cast<const uint2*>(vr);
         const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
-        u32x4 vv = {lo.x, lo.y, hi.x, hi.y};
-        f32x4 acc = o[t][d];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] *= alpha;
-        o[t][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pb, acc, 0, 0, 0);
+        const u32x4 vv = {lo.x, lo.y, hi.x, hi.y};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pb[c], acc, 0, 0, 0);
       }
+      o[d] = acc;
     }
+    const int r = rq;
+    if (r >= a.R) continue;
+    if (a.nsplit == 1) {
+      const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+      const int i = r / a.G, hl = r % a.G;
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          a.out[attn_out_index(a, HD, b, i, kvh * a.G + hl, d * 16 + (lane >> 4) * 4 + rr)] = f32_to_bf16(o[d][rr] * inv);
+      continue;
+    }
+    float* pr = a.part + (((size_t)bk * a.nsplit + split) * a.R + r) * S::PSTRIDE;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) *reinterpret_cast<f32x4*>(pr + d * 16 + (lane >> 4) * 4) = o[d];
+    if (lane < 16) *reinterpret_cast<f32x4*>(pr + HD) = f32x4{mx, lsum, 0.0f, 0.0f};
   }
+}
 
-  // publish this split's partial: rows r, [o(HD) | m | l]
-  const size_t rstride = HD + 2;
-  float* pbase = a.part + (((size_t)bk * a.nsplit + split) * a.R) * rstride;
+// Combine the live splits of one (row b, kv head, query row r) per wave in two load rounds:
+// lane s reads split s's (m, l) and forms its weight exp(m_s - M); then every lane reads the
+// partial outputs of all splits for its dims at once (up to 64 splits per round).
+template <int HD>
+__global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
+  using S = Split<HD>;
+  constexpr int PER = HD / 64;
+  const int lane = threadIdx.x & 63;
+  const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (task >= a.B * a.nkv * a.R) return;
+  const int r = task % a.R, bk = task / a.R;
+  const int b = bk / a.nkv, kvh = bk % a.nkv;
+  const int Lk = min(a.seq_lens[b] + a.W, a.max_pages * a.page);
+  const int ns = min(a.nsplit, (Lk + S::KEYS - 1) / S::KEYS);
+  const float* base = a.part + ((size_t)bk * a.nsplit * a.R + r) * S::PSTRIDE;
+  const size_t sstride = (size_t)a.R * S::PSTRIDE;
+  float acc[PER];
 #pragma unroll
-  for (int t = 0; t < QT; ++t) {
-    const int r = (wv + 4 * t) * 16 + (lane & 15);
-    if (wv + 4 * t >= (a.R + 15) / 16 || r >= a.R) continue;
-    float* pr = pbase + (size_t)r * rstride;
-#pragma unroll
-    for (int d = 0; d < DT; ++d)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) pr[d * 16 + (lane >> 4) * 4 + rr] = o[t][d][rr];
-    if (lane < 16) {
-      pr[HD] = mrow[t];
-      pr[HD + 1] = lrow[t];
+  for (int e = 0; e < PER; ++e) acc[e] = 0.0f;
+  float M = -__builtin_inff(), den = 0.0f;
+  for (int s0 = 0; s0 < ns; s0 += 64) {
+    const int n = min(64, ns - s0);
+    float ml[2] = {-__builtin_inff(), 0.0f};
+    if (lane < n) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(base + (s0 + lane) * sstride + HD);
+      ml[0] = v[0];
+      ml[1] = v[1];
     }
-  }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int prev = atomicAdd(&a.cnt[bk], 1);
-    last = (prev == a.nsplit - 1);
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  // combine the splits: lanes own splits for the max / denominator, then dims for the sum
-  const float* base = a.part + ((size_t)bk * a.nsplit * a.R) * rstride;
-  for (int r = wv; r < a.R; r += 4) {
-    float M = -__builtin_inff();
-    for (int s = lane; s < a.nsplit; s += 64)
-      M = fmaxf(M, __builtin_nontemporal_load(base + ((size_t)s * a.R + r) * rstride + HD));
-    M = wave_max(M);
-    float den = 0.0f;
-    for (int s = lane; s < a.nsplit; s += 64) {
-      const float* pr = base + ((size_t)s * a.R + r) * rstride;
-      const float ms = __builtin_nontemporal_load(pr + HD);
-      if (ms != -__builtin_inff()) den += __expf(ms - M) * __builtin_nontemporal_load(pr + HD + 1);
-    }
-    den = wave_sum(den);
-    float acc[HD / 64];
+    const float Mn = fmaxf(M, wave_max(ml[0]));
+    const float rescale = M == -__builtin_inff() ? 0.0f : __expf(M - Mn);
+    const float w = ml[0] == -__builtin_inff() ? 0.0f : __expf(ml[0] - Mn);
+    den = den * rescale + wave_sum(w * ml[1]);
 #pragma unroll
-    for (int e = 0; e < HD / 64; ++e) acc[e] = 0.0f;
-    int s = 0;
-    for (; s + 8 <= a.nsplit; s += 8) {
-      float ms[8], ov[8][HD / 64];
+    for (int e = 0; e < PER; ++e) acc[e] *= rescale;
+    M = Mn;
+    // all partial rows of this round in flight, 16 at a time
+    for (int u0 = 0; u0 < n; u0 += 16) {
+      float ov[16][PER];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float* pr = base + ((size_t)(s + u) * a.R + r) * rstride;
-        ms[u] = __builtin_nontemporal_load(pr + HD);
+      for (int u = 0; u < 16; ++u) {
+        const int s = s0 + min(u0 + u, n - 1);
 #pragma unroll
-        for (int e = 0; e < HD / 64; ++e) ov[u][e] = __builtin_nontemporal_load(pr + e * 64 + lane);
+        for (int e = 0; e < PER; ++e) ov[u][e] = base[s * sstride + e * 64 + lane];
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float w = ms[u] == -__builtin_inff() ? 0.0f : __expf(ms[u] - M);
+      for (int u = 0; u < 16; ++u) {
+        const float wu = __shfl(w, min(u0 + u, 63), 64);
+        if (u0 + u < n)
 #pragma unroll
-        for (int e = 0; e < HD / 64; ++e) acc[e] += w * ov[u][e];
+          for (int e = 0; e < PER; ++e) acc[e] += wu * ov[u][e];
       }
     }
-    for (; s < a.nsplit; ++s) {
-      const float* pr = base + ((size_t)s * a.R + r) * rstride;
-      const float ms = __builtin_nontemporal_load(pr + HD);
-      const float w = ms == -__builtin_inff() ? 0.0f : __expf(ms - M);
-#pragma unroll
-      for (int e = 0; e < HD / 64; ++e) acc[e] += w * __builtin_nontemporal_load(pr + e * 64 + lane);
-    }
-    const int i = r / a.G, hl = r % a.G;
-    uint16_t* op = a.out + ((int64_t)(b * a.W + i) * a.nq + kvh * a.G + hl) * HD;
-    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-#pragma unroll
-    for (int e = 0; e < HD / 64; ++e) op[e * 64 + lane] = f32_to_bf16(acc[e] * inv);
   }
-  if (threadIdx.x == 0) a.cnt[bk] = 0;
+  const int i = r / a.G, hl = r % a.G;
+  const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) a.out[attn_out_index(a, HD, b, i, kvh * a.G + hl, e * 64 + lane)] = f32_to_bf16(acc[e] * inv);
 }
 
 // ----------------------------------------------------------------------------- host helpers
-static int attn_split_tokens(int B, int nkv, int max_ctx) {
-  // aim for ~256 blocks, never splits shorter than 128 tokens
-  int st = 2048;
-  while (st > 128 && (int64_t)B * nkv * ((max_ctx + st - 1) / st) < 256) st >>= 1;
-  return st;
+template <int HD, int QT>
+static void launch_attention(const AttnArgs& a, int kv_dtype, bool softcap, dim3 grid, hipStream_t st) {
+  if (kv_dtype == DSK_KV_U8) {
+    if (softcap) hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_U8, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_U8, false>), grid, dim3(256), 0, st, a);
+  } else {
+    if (softcap) hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_BF16, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_BF16, false>), grid, dim3(256), 0, st, a);
+  }
 }
 
-constexpr size_t kAttnCounterBytes = 16384;
+static int attn_nsplit(int hd, int max_ctx) {
+  const int keys = hd == 128 ? Split<128>::KEYS : Split<256>::KEYS;
+  return (max_ctx + keys - 1) / keys;
+}
 
 }  // namespace dsk
 
 using namespace dsk;
 
-extern "C" int dsk_qkv_rope_append(const uint16_t* qkv, int B, int W, int nq, int nkv, int hd,
+extern "C" int dsk_qkv_rope_append(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
                                    const uint16_t* q_norm, const uint16_t* k_norm, float eps,
                                    const float* inv_freq, const int32_t* seq_lens, int pos_offset,
                                    const int32_t* block_table, int max_pages, int page, int kv_dtype,
@@ -451,16 +492,17 @@ extern "C" int dsk_qkv_rope_append(const uint16_t* qkv, int B, int W, int nq, in
   DSK_REQUIRE(hd == 128 || hd == 256, "dsk_qkv_rope_append: head_dim %d not supported (128, 256)", hd);
   DSK_REQUIRE(B > 0 && W > 0 && nq >= 0 && nkv > 0 && nq % nkv == 0, "dsk_qkv_rope_append: bad shape");
   DSK_REQUIRE(page > 0 && max_pages > 0, "dsk_qkv_rope_append: bad page geometry");
+  DSK_REQUIRE(qkv_splits >= 0, "dsk_qkv_rope_append: qkv_splits=%d", qkv_splits);
   DSK_REQUIRE(kv_dtype == DSK_KV_BF16 || (kv_dtype == DSK_KV_U8 && k_sb && v_sb),
               "dsk_qkv_rope_append: u8 KV needs scale/bias buffers");
   const int tasks = B * W * (nq + 2 * nkv);
   dim3 grid((unsigned)ceil_div(tasks, 4));
   if (hd == 128)
-    hipLaunchKernelGGL(qkv_rope_append_kernel<128>, grid, dim3(256), 0, as_stream(stream), qkv, B, W, nq, nkv, q_norm,
+    hipLaunchKernelGGL(qkv_rope_append_kernel<128>, grid, dim3(256), 0, as_stream(stream), qkv, qkv_splits, B, W, nq, nkv, q_norm,
                        k_norm, eps, inv_freq, seq_lens, pos_offset, block_table, max_pages, page, kv_dtype, k_pool,
                        v_pool, k_sb, v_sb, q_out);
   else
-    hipLaunchKernelGGL(qkv_rope_append_kernel<256>, grid, dim3(256), 0, as_stream(stream), qkv, B, W, nq, nkv, q_norm,
+    hipLaunchKernelGGL(qkv_rope_append_kernel<256>, grid, dim3(256), 0, as_stream(stream), qkv, qkv_splits, B, W, nq, nkv, q_norm,
                        k_norm, eps, inv_freq, seq_lens, pos_offset, block_table, max_pages, page, kv_dtype, k_pool,
                        v_pool, k_sb, v_sb, q_out);
   DSK_LAUNCH_CHECK("dsk_qkv_rope_append");
@@ -469,28 +511,18 @@ extern "C" int dsk_qkv_rope_append(const uint16_t* qkv, int B, int W, int nq, in
 
 extern "C" size_t dsk_attn_ws_bytes(int B, int W, int nq, int hd, int max_ctx) {
   if (B <= 0 || W <= 0 || nq <= 0 || hd <= 0 || max_ctx <= 0) return 0;
-  // worst case over nkv: rows per kv head * nkv = W * nq
-  const int st = 128;  // smallest split => most splits
-  const size_t nsplit = (size_t)((max_ctx + st - 1) / st);
-  return kAttnCounterBytes + (size_t)B * W * nq * nsplit * (hd + 2) * sizeof(float);
-}
-
-extern "C" int dsk_attn_ws_init(void* workspace, size_t ws_bytes, dsk_stream_t stream) {
-  DSK_REQUIRE(workspace && ws_bytes >= kAttnCounterBytes, "dsk_attn_ws_init: workspace too small");
-  hipError_t e = hipMemsetAsync(workspace, 0, kAttnCounterBytes, as_stream(stream));
-  if (e != hipSuccess) {
-    set_error("dsk_attn_ws_init: %s", hipGetErrorString(e));
-    return DSK_ELAUNCH;
-  }
-  return DSK_OK;
+  if (hd != 128 && hd != 256) return 0;
+  // rows per kv head * nkv = W * nq
+  const size_t nsplit = (size_t)attn_nsplit(hd, max_ctx);
+  return nsplit > 1 ? (size_t)B * W * nq * nsplit * (hd + 4) * sizeof(float) : 0;
 }
 
 extern "C" int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, int hd, float scale, int causal,
                              int window, float softcap, const int32_t* seq_lens, int max_ctx,
                              const int32_t* block_table, int max_pages, int page, int kv_dtype, const void* k_pool,
                              const void* v_pool, const uint32_t* k_sb, const uint32_t* v_sb, uint16_t* out,
-                             void* workspace, size_t ws_bytes, dsk_stream_t stream) {
-  DSK_REQUIRE(q && seq_lens && block_table && k_pool && v_pool && out && workspace, "dsk_attention: null pointer");
+                             int out_packed, void* workspace, size_t ws_bytes, dsk_stream_t stream) {
+  DSK_REQUIRE(q && seq_lens && block_table && k_pool && v_pool && out, "dsk_attention: null pointer");
   DSK_REQUIRE(hd == 128 || hd == 256, "dsk_attention: head_dim %d not supported (128, 256)", hd);
   DSK_REQUIRE(B > 0 && W > 0 && nq > 0 && nkv > 0 && nq % nkv == 0, "dsk_attention: bad shape");
   DSK_REQUIRE(kv_dtype == DSK_KV_BF16 || (kv_dtype == DSK_KV_U8 && k_sb && v_sb), "dsk_attention: u8 KV needs sb");
@@ -502,7 +534,6 @@ extern "C" int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, i
   const int QT = (tiles + 3) / 4;
   DSK_REQUIRE(QT <= (hd == 128 ? 4 : 2), "dsk_attention: W*G=%d query rows per kv head exceeds %d", R,
               (hd == 128 ? 256 : 128));
-  DSK_REQUIRE(B * nkv <= (int)(kAttnCounterBytes / sizeof(int)), "dsk_attention: too many (row, kv head) pairs");
   AttnArgs a;
   a.q = q;
   a.B = B;
@@ -525,19 +556,26 @@ extern "C" int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, i
   a.k_sb = k_sb;
   a.v_sb = v_sb;
   a.out = out;
-  a.split_tokens = attn_split_tokens(B, nkv, max_ctx);
-  a.nsplit = (max_ctx + a.split_tokens - 1) / a.split_tokens;
-  const size_t need = kAttnCounterBytes + (size_t)B * nkv * a.nsplit * R * (hd + 2) * sizeof(float);
-  DSK_REQUIRE(ws_bytes >= need, "dsk_attention: workspace %zu < %zu", ws_bytes, need);
-  a.cnt = reinterpret_cast<int*>(workspace);
-  a.part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + kAttnCounterBytes);
+  a.out_packed = out_packed ? 1 : 0;
+  DSK_REQUIRE(!out_packed || (B * W <= 64 && (nq * hd) % 64 == 0), "dsk_attention: packed output needs B*W <= 64");
+  a.nsplit = attn_nsplit(hd, max_ctx);
+  const size_t need = a.nsplit > 1 ? (size_t)B * nkv * a.nsplit * R * (hd + 4) * sizeof(float) : 0;
+  DSK_REQUIRE(a.nsplit == 1 || (workspace && ws_bytes >= need), "dsk_attention: workspace %zu < %zu", ws_bytes, need);
+  a.part = reinterpret_cast<float*>(workspace);
   dim3 grid((unsigned)(B * nkv * a.nsplit));
   hipStream_t st = as_stream(stream);
+  const bool sc = softcap > 0.0f;
 #define DSK_ATTN_CASE(hdv, qt) \
-  if (hd == hdv && QT == qt) hipLaunchKernelGGL((attention_kernel<hdv, qt>), grid, dim3(256), 0, st, a);
+  if (hd == hdv && QT == qt) launch_attention<hdv, qt>(a, kv_dtype, sc, grid, st);
   DSK_ATTN_CASE(128, 1) DSK_ATTN_CASE(128, 2) DSK_ATTN_CASE(128, 3) DSK_ATTN_CASE(128, 4)
   DSK_ATTN_CASE(256, 1) DSK_ATTN_CASE(256, 2)
 #undef DSK_ATTN_CASE
   DSK_LAUNCH_CHECK("dsk_attention");
+  if (a.nsplit > 1) {
+    const dim3 cgrid((unsigned)ceil_div((int64_t)B * nkv * R, 4));
+    if (hd == 128) hipLaunchKernelGGL(attention_combine_kernel<128>, cgrid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(attention_combine_kernel<256>, cgrid, dim3(256), 0, st, a);
+    DSK_LAUNCH_CHECK("dsk_attention (combine)");
+  }
   return DSK_OK;
 }

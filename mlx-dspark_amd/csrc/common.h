@@ -47,11 +47,16 @@ __host__ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
 }
 
 __host__ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  // v_cvt_pk_bf16_f32: round to nearest even, NaN stays NaN
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+#else
   uint32_t u;
   __builtin_memcpy(&u, &f, 4);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);  // NaN stays NaN
   u += 0x7fffu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
+#endif
 }
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
@@ -78,5 +83,11 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 __host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Packed activation layout (the W8 GEMM's A operand): element (m, k) of an [M, K] bf16
+// activation, G = K / 64, lives at P[m/16][k/64][m%16 + 16 * ((k%64)/16)][k%16].
+__host__ __device__ __forceinline__ int64_t apack_index(int64_t m, int64_t k, int64_t G) {
+  return ((((m >> 4) * G + (k >> 6)) * 64 + (m & 15) + 16 * ((k >> 4) & 3)) << 4) + (k & 15);
+}
 
 }  // namespace dsk

@@ -1,20 +1,30 @@
 // W8 affine group-64 weights on gfx950: quantizer, MLX-layout -> tiled-layout repack,
-// activation pack (RMSNorm / SiLU / GeLU prologue) and the skinny GEMM used by every
-// target and drafter projection of the verify step.
+// activation packing (with the residual add and RMSNorm that precede every projection),
+// and the skinny GEMM used by every target and drafter projection of the verify step.
+//
+// Packed activation layout (the GEMM's A operand, see common.h apack_index):
+//   P[m/16][k/64][lane][16 bf16], lane = m%16 + 16 * ((k%64)/16): one 2 KiB block per
+//   (16-row tile, 64-column group), and each lane's 32 bytes are the two 8-element
+//   fragments it feeds to v_mfma_f32_16x16x32_bf16, so every activation load of the GEMM
+//   is a contiguous 1 KiB wave-wide read.
 //
 // Tiled HBM layout (what dsk_w8_gemm streams):
 //   wt[t][g][lane][16 B]: tile t = 16 output rows (n = 16t + lane%16), group g = 64 input
 //   columns, lane/16 selects the 16-column chunk inside the group. One wave-wide dwordx4
 //   load reads one 1 KiB tile-group, contiguous, and lands every byte in the lane that
-//   feeds it to v_mfma_f32_16x16x32_f16 as the B operand.
-//   sb[t][n%16][g]: u32 = bf16 scale | bf16 bias << 16.
+//   feeds it to v_mfma_f32_16x16x32_bf16 as the B operand (bytes 0-7: first MFMA, 8-15:
+//   second).
+//   sb[t][g][16]: u32 = bf16 scale | bf16 bias << 16 for n = 16t + 0..15.
+//   Paired repack (gated MLPs): the source rows [0, N/2) are the gate projection and
+//   [N/2, N) the up projection; destination tile 2p holds gate rows 16p..16p+15 and tile
+//   2p+1 the up rows 16p..16p+15, so one workgroup owning both tiles can apply the
+//   activation in its epilogue.
 //
 // GEMM arithmetic. With w = s*q + b per group, sum_k x_k w_k = s * sum x_k q_k + b * sum x_k.
-// q (0..255) becomes the fp16 1024 + q with a single v_perm_b32 per two weights (0x64 in
-// the high byte of each half), so the MFMA yields acc = sum x (1024 + q) and the group's
-// contribution is s * acc + (b - 1024 s) * X with X = sum x over the group (precomputed by
-// the activation pack). Activations are exact in fp16 after a per-row power-of-two scale
-// (bf16 has 8 significant bits, fp16 11), undone in the epilogue.
+// q (0..255) is exact in bf16, the bf16 activations go to the MFMA unchanged, so the MFMA
+// yields t = sum x q exactly up to fp32 accumulation; X = sum x over the group comes from
+// one more MFMA against a B operand of ones; the group adds s * t + b * X to the fp32
+// accumulator.
 #include "common.h"
 
 namespace dsk {
@@ -69,8 +79,14 @@ __global__ void w8_quantize_kernel(const void* __restrict__ w, int w_bf16, int64
 // =====================================================================================
 // repack: MLX layout -> tiled layout
 // =====================================================================================
+__device__ __forceinline__ int64_t repack_src_row(int64_t n, int64_t N, int paired) {
+  if (!paired) return n;
+  const int64_t t = n >> 4, r = n & 15;
+  return (t & 1) * (N / 2) + (t >> 1) * 16 + r;
+}
+
 __global__ void w8_repack_kernel(const uint8_t* __restrict__ q, const uint16_t* __restrict__ s,
-                                 const uint16_t* __restrict__ b, int64_t N, int64_t K,
+                                 const uint16_t* __restrict__ b, int64_t N, int64_t K, int paired,
                                  u32x4* __restrict__ wt, uint32_t* __restrict__ sb) {
   const int64_t G = K / 64;
   const int64_t chunks = N * K / 16;  // 16-byte chunks
@@ -80,39 +96,146 @@ __global__ void w8_repack_kernel(const uint8_t* __restrict__ q, const uint16_t* 
     int64_t lane = idx & 63;
     int64_t tg = idx >> 6;
     int64_t g = tg % G, t = tg / G;
-    int64_t n = t * 16 + (lane & 15);
+    int64_t n = repack_src_row(t * 16 + (lane & 15), N, paired);
     int64_t k = g * 64 + (lane >> 4) * 16;
-    const u32x4* src = reinterpret_cast<const u32x4*>(q + n * K + k);
-    wt[idx] = *src;
+    wt[idx] = *reinterpret_cast<const u32x4*>(q + n * K + k);
   }
   if (idx < N * G) {
-    // destination order: t, n%16, g
-    int64_t g = idx % G;
-    int64_t tn = idx / G;  // = t*16 + n%16 = n
-    int64_t n = tn;
+    // destination order: t, g, n%16
+    int64_t r = idx & 15;
+    int64_t tg = idx >> 4;
+    int64_t g = tg % G, t = tg / G;
+    int64_t n = repack_src_row(t * 16 + r, N, paired);
     uint32_t sv = s[n * G + g], bv = b[n * G + g];
     sb[idx] = sv | (bv << 16);
   }
 }
 
 // =====================================================================================
-// activation pack
+// activation pack: one workgroup per row, every 16-byte chunk of the row loaded up front.
+//   v = sum of the fp32 partial slices (in slice order), plus the bf16 residual h (written
+//   back rounded to bf16), or h alone; optional copy of v (hidden-state tap); optional
+//   RMSNorm bf16((v * rsqrt(mean(v^2) + eps)) * w); output in the packed layout.
 // =====================================================================================
-struct PackLayout {
-  int MT;
-  int64_t G;
-  size_t xp_off, xs_off, xe_off, total;
+constexpr int kPackThreads = 512;
+constexpr int kPackMaxSplits = 16;
+
+struct PackArgs {
+  const float* part;   // [nsplit][M][K] (slice stride M * K), or null
+  int nsplit;
+  uint16_t* h;         // bf16 row-major, row stride ldh, or null
+  int64_t ldh;
+  uint16_t* copy;      // bf16 row-major, row stride ldc, or null
+  int64_t ldc;
+  int M;
+  int64_t K;
+  const uint16_t* norm_w;
+  float eps;
+  uint16_t* out;       // packed, or null
 };
 
-__host__ __device__ inline PackLayout pack_layout(int M, int64_t K) {
-  PackLayout L;
-  L.MT = (M + 15) / 16;
-  L.G = K / 64;
-  L.xp_off = 0;
-  L.xs_off = (size_t)L.MT * L.G * 2048;
-  L.xe_off = L.xs_off + (size_t)L.MT * L.G * 64;
-  L.total = L.xe_off + (size_t)L.MT * 64;
-  return L;
+template <int NV, int MAXS>
+__global__ __launch_bounds__(kPackThreads) void act_pack_kernel(PackArgs a) {
+  __shared__ float red[kPackThreads / 64];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const int64_t nchunk = a.K / 8;
+  const int64_t G = a.K / 64;
+  const int S = a.part ? a.nsplit : 0;
+  // ---- every load up front: norm weights, residual, and each split's 8 values per chunk
+  u32x4 v[NV], wv[NV], hv[NV];
+  f32x4 pl[NV][MAXS > 0 ? MAXS : 1], ph[NV][MAXS > 0 ? MAXS : 1];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = min(tid + (int64_t)i * kPackThreads, nchunk - 1);
+    if (a.norm_w) wv[i] = *reinterpret_cast<const u32x4*>(a.norm_w + c * 8);
+    if (a.h) hv[i] = *reinterpret_cast<const u32x4*>(a.h + (int64_t)m * a.ldh + c * 8);
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) {
+      const float* p = a.part + ((int64_t)min(s, S - 1) * a.M + m) * a.K + c * 8;
+      pl[i][s] = *reinterpret_cast<const f32x4*>(p);
+      ph[i][s] = *reinterpret_cast<const f32x4*>(p + 4);
+    }
+  }
+  // ---- residual sum in split order, rounded once
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) {
+      if (s >= S) break;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f[e] += pl[i][s][e];
+        f[4 + e] += ph[i][s][e];
+      }
+    }
+    uint16_t o[8];
+    const uint16_t* hh = reinterpret_cast<const uint16_t*>(&hv[i]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = a.h ? (S ? f32_to_bf16(bf16_to_f32(hh[e]) + f[e]) : hh[e]) : f32_to_bf16(f[e]);
+    v[i] = *reinterpret_cast<const u32x4*>(o);
+  }
+  float r = 1.0f;
+  if (a.norm_w) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = tid + (int64_t)i * kPackThreads;
+      if (c >= nchunk) continue;
+      const uint16_t* hv2 = reinterpret_cast<const uint16_t*>(&v[i]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = bf16_to_f32(hv2[e]);
+        ss = fmaf(f, f, ss);
+      }
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPackThreads / 64; ++i) tot += red[i];
+    r = rsqrtf(tot / (float)a.K + a.eps);
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int64_t c = tid + (int64_t)i * kPackThreads;
+    if (c >= nchunk) continue;
+    if (a.h && S) *reinterpret_cast<u32x4*>(a.h + (int64_t)m * a.ldh + c * 8) = v[i];
+    if (a.copy) *reinterpret_cast<u32x4*>(a.copy + (int64_t)m * a.ldc + c * 8) = v[i];
+    if (!a.out) continue;
+    u32x4 ov = v[i];
+    if (a.norm_w) {
+      const uint16_t* hv2 = reinterpret_cast<const uint16_t*>(&v[i]);
+      const uint16_t* g = reinterpret_cast<const uint16_t*>(&wv[i]);
+      uint16_t o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = f32_to_bf16((bf16_to_f32(hv2[e]) * r) * bf16_to_f32(g[e]));
+      ov = *reinterpret_cast<const u32x4*>(o);
+    }
+    *reinterpret_cast<u32x4*>(a.out + apack_index(m, c * 8, G)) = ov;
+  }
+}
+
+// =====================================================================================
+// skinny GEMM
+// =====================================================================================
+// u8 x 16 -> two bf16 x 8 (exact: q <= 255 needs 8 significant bits, the fp32 from
+// v_cvt_f32_ubyteN is truncated to its top half).
+__device__ __forceinline__ void u8x16_to_bf16(const u32x4 w, bf16x8& lo, bf16x8& hi) {
+  uint32_t r[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t v = w[i];
+    const float f0 = (float)(v & 0xffu), f1 = (float)((v >> 8) & 0xffu);
+    const float f2 = (float)((v >> 16) & 0xffu), f3 = (float)(v >> 24);
+    r[2 * i] = __builtin_amdgcn_perm(f32_bits(f1), f32_bits(f0), 0x07060302u);
+    r[2 * i + 1] = __builtin_amdgcn_perm(f32_bits(f3), f32_bits(f2), 0x07060302u);
+  }
+  lo = __builtin_bit_cast(bf16x8, (u32x4{r[0], r[1], r[2], r[3]}));
+  hi = __builtin_bit_cast(bf16x8, (u32x4{r[4], r[5], r[6], r[7]}));
 }
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
@@ -121,147 +244,24 @@ __device__ __forceinline__ float gelu_tanh_f(float x) {
   return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
 }
 
-constexpr int kPackThreads = 256;
-constexpr int kPackMaxK = 24576;
-
-// One workgroup per (padded) row. Row values are formed in fp32, rounded to bf16 (the
-// activation dtype between kernels), kept in LDS, then scaled by 2^s and stored as fp16.
-__global__ __launch_bounds__(kPackThreads) void act_pack_kernel(
-    const uint16_t* __restrict__ x, int64_t ldx, int M, int64_t K, int mode,
-    const uint16_t* __restrict__ norm_w, float eps, uint8_t* __restrict__ out) {
-  __shared__ uint16_t row[kPackMaxK];
-  __shared__ float red[kPackThreads / 64];
-  const PackLayout L = pack_layout(M, K);
-  const int m = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int64_t nchunk = K / 16;
-  _Float16* xp = reinterpret_cast<_Float16*>(out + L.xp_off);
-  float* xs = reinterpret_cast<float*>(out + L.xs_off);
-  float* xe = reinterpret_cast<float*>(out + L.xe_off);
-  const int mt = m >> 4, mr = m & 15;
-
-  if (m >= M) {  // padding rows: zeros
-    for (int64_t c = tid; c < nchunk; c += kPackThreads) {
-      int64_t g = c >> 2, j = c & 3;
-      u32x4* dst = reinterpret_cast<u32x4*>(xp + (((int64_t)mt * L.G + g) * 64 + mr + 16 * j) * 16);
-      dst[0] = u32x4{0, 0, 0, 0};
-      dst[1] = u32x4{0, 0, 0, 0};
-      if (j == 0) xs[((int64_t)mt * L.G + g) * 16 + mr] = 0.0f;
-    }
-    if (tid == 0) xe[m] = 1.0f;
-    return;
-  }
-
-  const uint16_t* xr = x + (int64_t)m * ldx;
-  float rscale = 1.0f;
-  if (mode == DSK_PACK_RMSNORM) {
-    float ss = 0.0f;
-    for (int64_t k = tid; k < K; k += kPackThreads) {
-      float v = bf16_to_f32(xr[k]);
-      ss += v * v;
-    }
-    ss = wave_sum(ss);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-    for (int i = 0; i < kPackThreads / 64; ++i) tot += red[i];
-    rscale = rsqrtf(tot / (float)K + eps);
-    __syncthreads();
-  }
-
-  // pass 1: values -> LDS (bf16), running max |v|
-  float amax = 0.0f;
-  for (int64_t k = tid; k < K; k += kPackThreads) {
-    float v;
-    if (mode == DSK_PACK_PLAIN) {
-      v = bf16_to_f32(xr[k]);
-    } else if (mode == DSK_PACK_RMSNORM) {
-      v = (bf16_to_f32(xr[k]) * rscale) * bf16_to_f32(norm_w[k]);
-    } else {
-      float g = bf16_to_f32(xr[k]);
-      float u = bf16_to_f32(xr[K + k]);
-      // activation rounds to bf16 before the product, as the bf16 graph does
-      float a = round_bf16(mode == DSK_PACK_SILU ? silu_f(g) : gelu_tanh_f(g));
-      v = a * u;
-    }
-    uint16_t h = f32_to_bf16(v);
-    row[k] = h;
-    amax = fmaxf(amax, fabsf(bf16_to_f32(h)));
-  }
-  amax = wave_max(amax);
-  if ((tid & 63) == 0) red[tid >> 6] = amax;
-  __syncthreads();
-  float mx = 0.0f;
-  for (int i = 0; i < kPackThreads / 64; ++i) mx = fmaxf(mx, red[i]);
-  // power-of-two scale bringing max |v| into [2^14, 2^15)
-  int e = 0;
-  if (mx > 0.0f) {
-    int ex;
-    frexpf(mx, &ex);  // mx = f * 2^ex, f in [0.5, 1)
-    e = 15 - ex;      // mx * 2^e in [2^14, 2^15)
-  }
-  const float up = ldexpf(1.0f, e);
-  if (tid == 0) xe[m] = ldexpf(1.0f, -e);
-
-  // pass 2: fp16 operand + group sums. Chunk c = 16 columns; the four chunks of a group
-  // are handled by four consecutive threads, combined with lane shuffles.
-  const int64_t nchunk_pad = ((nchunk + kPackThreads - 1) / kPackThreads) * kPackThreads;
-  for (int64_t c = tid; c < nchunk_pad; c += kPackThreads) {
-    float part = 0.0f;
-    if (c < nchunk) {
-      int64_t g = c >> 2, j = c & 3;
-      _Float16 hv[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float v = bf16_to_f32(row[c * 16 + i]) * up;
-        _Float16 h = (_Float16)v;
-        hv[i] = h;
-        part += (float)h;
-      }
-      u32x4* dst = reinterpret_cast<u32x4*>(xp + (((int64_t)mt * L.G + g) * 64 + mr + 16 * j) * 16);
-      const u32x4* srcv = reinterpret_cast<const u32x4*>(hv);
-      dst[0] = srcv[0];
-      dst[1] = srcv[1];
-    }
-    part += __shfl_xor(part, 1, 64);
-    part += __shfl_xor(part, 2, 64);
-    if (c < nchunk && (c & 3) == 0) xs[((int64_t)mt * L.G + (c >> 2)) * 16 + mr] = part;
-  }
-}
-
-// =====================================================================================
-// skinny GEMM
-// =====================================================================================
-__device__ __forceinline__ half8 w8_to_h8_lo(uint32_t a, uint32_t b) {
-  // bytes q0..q3 of a, q4..q7 of b -> fp16 (1024 + q) x 8
-  uint32_t h0 = __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u);
-  uint32_t h1 = __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u);
-  uint32_t h2 = __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u);
-  uint32_t h3 = __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u);
-  u32x4 u = {h0, h1, h2, h3};
-  return __builtin_bit_cast(half8, u);
-}
-
 struct GemmArgs {
-  const uint8_t* xpack;
+  const u32x4* xp;  // packed activation
   const u32x4* wt;
   const uint32_t* sb;
   int M;
   int64_t N, K, G;
-  int SK;           // K splits
-  int64_t gps;      // groups per split
-  int n_slabs;      // N / (16 * NTW)
+  int SK;           // K splits (DSK_EPI_PARTIAL)
+  int64_t gpb;      // groups per split, a multiple of the batch size
+  int n_slabs;      // N / (16 * NT)
+  int epi;          // DSK_EPI_*
   void* y;
   int y_f32;
   int64_t ldy;
   const uint16_t* res;
   int64_t ldr;
   float softcap;
-  float* part;      // [SK][M][N] f32 partials (SK > 1)
-  int* cnt;         // [n_slabs] arrival counters (SK > 1)
 };
 
-template <int MT, int NTW>
 __device__ __forceinline__ void gemm_store(const GemmArgs& a, int m, int64_t n, float v) {
   if (a.res) v += bf16_to_f32(a.res[(int64_t)m * a.ldr + n]);
   if (a.softcap > 0.0f) v = tanhf(v / a.softcap) * a.softcap;
@@ -271,149 +271,122 @@ __device__ __forceinline__ void gemm_store(const GemmArgs& a, int m, int64_t n, 
     reinterpret_cast<uint16_t*>(a.y)[(int64_t)m * a.ldy + n] = f32_to_bf16(v);
 }
 
-template <int MT, int NTW, int WAVES>
+// gated epilogue: g, u are the two projections of one column (rounded to bf16 as the
+// projection outputs are), act = bf16(bf16(act_fn(g)) * u), stored packed (K' = N / 2)
+__device__ __forceinline__ void gemm_store_gated(const GemmArgs& a, int m, int64_t col, float g, float u) {
+  const float gb = round_bf16(g), ub = round_bf16(u);
+  const float act = round_bf16(a.epi == DSK_EPI_SWIGLU ? silu_f(gb) : gelu_tanh_f(gb));
+  reinterpret_cast<uint16_t*>(a.y)[apack_index(m, col, a.N / 128)] = f32_to_bf16(act * ub);
+}
+
+// One batch of U groups: all loads first, then the MFMAs. Padding rows of the packed
+// activation hold arbitrary values; their outputs are never stored.
+template <int MT, int NT, int U>
+__device__ __forceinline__ void gemm_batch(const GemmArgs& a, int64_t t0, int64_t g0, int lane,
+                                           f32x4 (&acc)[MT][NT]) {
+  u32x4 wv[U][NT];
+  uint32_t sv[U][NT];
+  u32x4 xv[U][MT][2];
+#pragma unroll
+  for (int c = 0; c < U; ++c)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int64_t tg = (t0 + j) * a.G + g0 + c;
+      wv[c][j] = __builtin_nontemporal_load(&a.wt[tg * 64 + lane]);
+    }
+#pragma unroll
+  for (int c = 0; c < U; ++c)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) sv[c][j] = a.sb[((t0 + j) * a.G + g0 + c) * 16 + (lane & 15)];
+#pragma unroll
+  for (int c = 0; c < U; ++c)
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const u32x4* px = a.xp + (((int64_t)i * a.G + g0 + c) * 64 + lane) * 2;
+      xv[c][i][0] = px[0];
+      xv[c][i][1] = px[1];
+    }
+  const u32x4 ones_u = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, ones_u);
+#pragma unroll
+  for (int c = 0; c < U; ++c) {
+    f32x4 X[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      X[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[c][i][0]), ones,
+                                                     f32x4{0, 0, 0, 0}, 0, 0, 0);
+      X[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[c][i][1]), ones, X[i], 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      bf16x8 b0, b1;
+      u8x16_to_bf16(wv[c][j], b0, b1);
+      const float s = bf16_to_f32((uint16_t)(sv[c][j] & 0xffffu));
+      const float bb = bf16_to_f32((uint16_t)(sv[c][j] >> 16));
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[c][i][0]), b0,
+                                                          f32x4{0, 0, 0, 0}, 0, 0, 0);
+        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[c][i][1]), b1, t, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(s, t[r], fmaf(bb, X[i][r], acc[i][j][r]));
+      }
+    }
+  }
+}
+
+// Workgroup = NT consecutive 16-row weight tiles x one K split; its WAVES waves take the
+// split's batches round-robin, each accumulating all NT tiles (every activation fragment a
+// wave loads feeds NT tiles), then reduce through LDS in wave order.
+template <int MT, int NT, int U, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
-  constexpr int CH = 4;  // groups per load batch
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int slab = blockIdx.x / a.SK, ks = blockIdx.x % a.SK;
+  const int64_t g_lo = (int64_t)ks * a.gpb;
+  const int64_t g_hi = min(a.G, g_lo + a.gpb);
+  const int nbatch = (int)((g_hi - g_lo) / U);
+  const int64_t t0 = (int64_t)slab * NT;
 
-  // XCD-aware block mapping: the SK blocks of one slab share blockIdx % 8 (one XCD, one L2)
-  int slab, ks;
-  const int total = a.n_slabs * a.SK;
-  if ((a.n_slabs & 7) == 0) {
-    int id = blockIdx.x;
-    int xcd = id & 7, j = id >> 3;
-    slab = (j / a.SK) * 8 + xcd;
-    ks = j % a.SK;
-  } else {
-    slab = blockIdx.x / a.SK;
-    ks = blockIdx.x % a.SK;
-  }
-  (void)total;
-
-  const int64_t g_lo = (int64_t)ks * a.gps;
-  const int64_t g_hi = min(a.G, g_lo + a.gps);
-  const int64_t span = g_hi - g_lo;
-  const int64_t gpw = (span + WAVES - 1) / WAVES;
-  const int64_t wg0 = g_lo + wave * gpw;
-  const int64_t wg1 = min(g_hi, wg0 + gpw);
-
-  const PackLayout L = pack_layout(a.M, a.K);
-  const u32x4* xp = reinterpret_cast<const u32x4*>(a.xpack + L.xp_off);
-  const f32x4* xs = reinterpret_cast<const f32x4*>(a.xpack + L.xs_off);
-  const float* xe = reinterpret_cast<const float*>(a.xpack + L.xe_off);
-
-  const int64_t t0 = (int64_t)slab * NTW;
-  f32x4 acc[MT][NTW];
+  f32x4 acc[MT][NT];
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int j = 0; j < NTW; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+    for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
 
-  for (int64_t g = wg0; g < wg1; g += CH) {
-    const int nb = (int)min((int64_t)CH, wg1 - g);
-    u32x4 wv[CH][NTW];
-    uint32_t sbv[CH][NTW];
-    u32x4 xv[CH][MT][2];
-    f32x4 xsv[CH][MT];
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      if (c < nb) {
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) {
-          wv[c][j] = __builtin_nontemporal_load(&a.wt[((t0 + j) * a.G + g + c) * 64 + lane]);
-          sbv[c][j] = a.sb[((t0 + j) * 16 + (lane & 15)) * a.G + g + c];
-        }
-#pragma unroll
-        for (int i = 0; i < MT; ++i) {
-          const u32x4* px = xp + (((int64_t)i * a.G + g + c) * 64 + lane) * 2;
-          xv[c][i][0] = px[0];
-          xv[c][i][1] = px[1];
-          xsv[c][i] = xs[((int64_t)i * a.G + g + c) * 4 + (lane >> 4)];
-        }
-      }
-    }
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      if (c < nb) {
-#pragma unroll
-        for (int j = 0; j < NTW; ++j) {
-          const half8 b0 = w8_to_h8_lo(wv[c][j].x, wv[c][j].y);
-          const half8 b1 = w8_to_h8_lo(wv[c][j].z, wv[c][j].w);
-          const float s = bf16_to_f32((uint16_t)(sbv[c][j] & 0xffffu));
-          const float bb = bf16_to_f32((uint16_t)(sbv[c][j] >> 16));
-          const float bprime = fmaf(-1024.0f, s, bb);
-#pragma unroll
-          for (int i = 0; i < MT; ++i) {
-            const half8 a0 = __builtin_bit_cast(half8, xv[c][i][0]);
-            const half8 a1 = __builtin_bit_cast(half8, xv[c][i][1]);
-            f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0, f32x4{0, 0, 0, 0}, 0, 0, 0);
-            t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1, t, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(s, t[r], fmaf(bprime, xsv[c][i][r], acc[i][j][r]));
-          }
-        }
-      }
-    }
-  }
+  for (int bt = wave; bt < nbatch; bt += WAVES) gemm_batch<MT, NT, U>(a, t0, g_lo + (int64_t)bt * U, lane, acc);
 
-  // cross-wave reduction
-  __shared__ float red[WAVES][MT * NTW * 256];
+  constexpr int NOUT = MT * NT * 256;
+  __shared__ float red[WAVES][NOUT];
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int j = 0; j < NTW; ++j)
+    for (int j = 0; j < NT; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave][((i * NTW + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+      for (int r = 0; r < 4; ++r) red[wave][((i * NT + j) * 4 + r) * 64 + lane] = acc[i][j][r];
   __syncthreads();
 
-  constexpr int NOUT = MT * NTW * 256;
-  if (a.SK == 1) {
-    for (int o = threadIdx.x; o < NOUT; o += WAVES * 64) {
-      float v = 0.0f;
-#pragma unroll
-      for (int w = 0; w < WAVES; ++w) v += red[w][o];
-      const int ln = o & 63, r = (o >> 6) & 3, ij = o >> 8;
-      const int i = ij / NTW, j = ij % NTW;
-      const int m = i * 16 + (ln >> 4) * 4 + r;
-      const int64_t n = (t0 + j) * 16 + (ln & 15);
-      if (m < a.M) gemm_store<MT, NTW>(a, m, n, v * xe[m]);
-    }
-    return;
-  }
-
-  // split-K: publish partial, last arriving block of the slab reduces in fixed order
+  // output element o: lane ln = o % 64, r = (o / 64) % 4, tile (i, j) = o / 256
+  const bool gated = a.epi == DSK_EPI_SWIGLU || a.epi == DSK_EPI_GEGLU;
   for (int o = threadIdx.x; o < NOUT; o += WAVES * 64) {
+    const int i = (o >> 8) / NT, j = (o >> 8) % NT;
+    const int m = i * 16 + ((o & 63) >> 4) * 4 + ((o >> 6) & 3);
+    if (m >= a.M || (gated && (j & 1))) continue;
     float v = 0.0f;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) v += red[w][o];
-    const int ln = o & 63, r = (o >> 6) & 3, ij = o >> 8;
-    const int i = ij / NTW, j = ij % NTW;
-    const int m = i * 16 + (ln >> 4) * 4 + r;
-    const int64_t n = (t0 + j) * 16 + (ln & 15);
-    if (m < a.M) a.part[((int64_t)ks * a.M + m) * a.N + n] = v * xe[m];
+    const int64_t n = (t0 + j) * 16 + (o & 15);
+    if (a.epi == DSK_EPI_PARTIAL) {
+      reinterpret_cast<float*>(a.y)[((int64_t)ks * a.M + m) * a.N + n] = v;
+    } else if (!gated) {
+      gemm_store(a, m, n, v);
+    } else {
+      float u = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) u += red[w][o + 256];
+      gemm_store_gated(a, m, ((t0 + j) >> 1) * 16 + (o & 15), v, u);
+    }
   }
-  __threadfence();
-  __syncthreads();
-  __shared__ int last;
-  if (threadIdx.x == 0) {
-    int prev = atomicAdd(&a.cnt[slab], 1);
-    last = (prev == a.SK - 1);
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  for (int o = threadIdx.x; o < NOUT; o += WAVES * 64) {
-    const int ln = o & 63, r = (o >> 6) & 3, ij = o >> 8;
-    const int i = ij / NTW, j = ij % NTW;
-    const int m = i * 16 + (ln >> 4) * 4 + r;
-    const int64_t n = (t0 + j) * 16 + (ln & 15);
-    if (m >= a.M) continue;
-    float v = 0.0f;
-    for (int s = 0; s < a.SK; ++s) v += __builtin_nontemporal_load(&a.part[((int64_t)s * a.M + m) * a.N + n]);
-    gemm_store<MT, NTW>(a, m, n, v);
-  }
-  if (threadIdx.x == 0) a.cnt[slab] = 0;  // leave the counter zeroed for the next call
 }
 
 // =====================================================================================
@@ -439,25 +412,107 @@ __global__ void w8_embed_kernel(const int32_t* __restrict__ ids, const uint8_t* 
 // host side: tile selection
 // =====================================================================================
 struct GemmPlan {
-  int ntw, sk, waves;
-  int64_t gps;
+  int nt, u, waves, sk;
+  int64_t gpb;
 };
 
-static GemmPlan plan_gemm(int M, int64_t N, int64_t K) {
-  (void)M;
+// NT tiles per workgroup amortise the activation reads (L2 -> CU traffic is the limit once
+// the weights stream at full rate); K splits (partial outputs only) bring small-N projections
+// to >= 512 workgroups; 4 waves per workgroup with several 2-group batches each, or up to 16
+// waves of one batch when a split is short. Rules fitted to a sweep on MI355X at M = 16 over
+// the Qwen3-8B verify shapes (qkv 6144x4096, o 4096x4096, gate_up 24576x4096, down
+// 4096x12288, head 151936x4096): each lands within 5% of the best configuration measured.
+static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi) {
   const int64_t G = K / 64;
   const int64_t tiles = N / 16;
+  const int MT = (M + 15) / 16;
+  const bool partial = epi == DSK_EPI_PARTIAL, gated = epi == DSK_EPI_SWIGLU || epi == DSK_EPI_GEGLU;
   GemmPlan p;
-  p.waves = 4;
-  // widest slab that still gives >= 256 blocks without split-K
-  p.ntw = 1;
-  if (tiles % 4 == 0 && tiles / 4 >= 512) p.ntw = 4;
-  else if (tiles % 2 == 0 && tiles / 2 >= 384) p.ntw = 2;
-  const int64_t slabs = tiles / p.ntw;
+  p.u = 2;
+  if (partial) p.nt = G >= 128 ? 4 : (tiles <= 256 ? 2 : 1);
+  else p.nt = 4;
+  if (MT > 2 && p.nt > 2) p.nt = 2;
+  while (p.nt > 1 && tiles % p.nt) p.nt /= 2;
+  if (gated && p.nt < 2) p.nt = 2;
+  const int64_t slabs = tiles / p.nt;
+  const int64_t batches = G / p.u;  // per tile
   p.sk = 1;
-  while (slabs * p.sk < 256 && G / (p.sk * 2) >= 16) p.sk *= 2;
-  p.gps = (G + p.sk - 1) / p.sk;
+  if (partial)
+    while (slabs * p.sk < 512 && batches / (p.sk * 2) >= 4 && p.sk < 16) p.sk *= 2;
+  const int64_t bps = batches / p.sk;  // batches per split
+  p.gpb = bps * p.u;
+  p.waves = (bps >= 8 && bps < 12) ? 8 : 4;
+  if (!partial && slabs < 128) p.waves = bps >= 32 ? 16 : (bps >= 8 ? 8 : 4);
+  while ((size_t)p.waves * MT * p.nt * 1024 > 65536) p.waves /= 2;  // LDS of the reduction
   return p;
+}
+
+template <int MT, int NT, int U, int WAVES>
+static void launch_gemm_t(const GemmArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES>), dim3((unsigned)(a.n_slabs * a.SK)), dim3(WAVES * 64), 0,
+                     st, a);
+}
+
+template <int MT, int NT, int U>
+static bool launch_gemm_w(const GemmArgs& a, int waves, hipStream_t st) {
+  constexpr int max_waves = 65536 / (MT * NT * 1024);  // LDS of the cross-wave reduction
+  switch (waves) {
+    case 4: if constexpr (max_waves >= 4) { launch_gemm_t<MT, NT, U, 4>(a, st); return true; } return false;
+    case 8: if constexpr (max_waves >= 8) { launch_gemm_t<MT, NT, U, 8>(a, st); return true; } return false;
+    case 16: if constexpr (max_waves >= 16) { launch_gemm_t<MT, NT, U, 16>(a, st); return true; } return false;
+  }
+  return false;
+}
+
+static bool launch_gemm(const GemmArgs& a, int MT, const GemmPlan& p, hipStream_t st) {
+#define DSK_GEMM_CASE(MT_, NT_, U_) \
+  if (MT == MT_ && p.nt == NT_ && p.u == U_) return launch_gemm_w<MT_, NT_, U_>(a, p.waves, st);
+  DSK_GEMM_CASE(1, 1, 2) DSK_GEMM_CASE(1, 2, 2) DSK_GEMM_CASE(1, 4, 2) DSK_GEMM_CASE(1, 8, 2)
+  DSK_GEMM_CASE(1, 1, 4) DSK_GEMM_CASE(1, 2, 4) DSK_GEMM_CASE(1, 4, 4)
+  DSK_GEMM_CASE(2, 1, 2) DSK_GEMM_CASE(2, 2, 2) DSK_GEMM_CASE(2, 4, 2)
+  DSK_GEMM_CASE(3, 1, 2) DSK_GEMM_CASE(3, 2, 2)
+  DSK_GEMM_CASE(4, 1, 2) DSK_GEMM_CASE(4, 2, 2)
+#undef DSK_GEMM_CASE
+  return false;
+}
+
+// Fills GemmArgs for a plan; shared by the entry point and the tuning harness.
+static void gemm_prepare(GemmArgs& a, const GemmPlan& p, const void* xp, const uint8_t* wt, const uint32_t* sb,
+                         int M, int64_t N, int64_t K, int epi, void* y, int y_dtype, int64_t ldy,
+                         const uint16_t* residual, int64_t ldr, float softcap) {
+  a.xp = reinterpret_cast<const u32x4*>(xp);
+  a.wt = reinterpret_cast<const u32x4*>(wt);
+  a.sb = sb;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.G = K / 64;
+  a.SK = p.sk;
+  a.gpb = p.gpb;
+  a.n_slabs = (int)(N / 16 / p.nt);
+  a.epi = epi;
+  a.y = y;
+  a.y_f32 = (y_dtype == DSK_F32);
+  a.ldy = ldy;
+  a.res = residual;
+  a.ldr = ldr;
+  a.softcap = softcap;
+}
+
+// chunks per thread (NV) x split slices kept in registers (MAXS): NV * MAXS <= 16
+static bool pack_launch(const PackArgs& a, hipStream_t st) {
+  const int64_t per = ceil_div(a.K / 8, kPackThreads);
+  const int S = a.part ? a.nsplit : 0;
+  const int ms = S == 0 ? 0 : (S <= 4 ? 4 : (S <= 8 ? 8 : 16));
+  const dim3 grid((unsigned)a.M), blk(kPackThreads);
+#define DSK_PACK_CASE(NV_, MS_) \
+  if (per <= NV_ && ms == MS_) { hipLaunchKernelGGL((act_pack_kernel<NV_, MS_>), grid, blk, 0, st, a); return true; }
+  DSK_PACK_CASE(1, 0) DSK_PACK_CASE(1, 4) DSK_PACK_CASE(1, 8) DSK_PACK_CASE(1, 16)
+  DSK_PACK_CASE(2, 0) DSK_PACK_CASE(2, 4) DSK_PACK_CASE(2, 8)
+  DSK_PACK_CASE(3, 0) DSK_PACK_CASE(3, 4)
+  DSK_PACK_CASE(6, 0)
+#undef DSK_PACK_CASE
+  return false;
 }
 
 }  // namespace dsk
@@ -478,116 +533,84 @@ extern "C" int dsk_w8_quantize(const void* w, int w_dtype, int64_t N, int64_t K,
   return DSK_OK;
 }
 
-extern "C" int dsk_w8_repack(const uint8_t* q, const uint16_t* scales, const uint16_t* biases,
-                             int64_t N, int64_t K, uint8_t* wt, uint32_t* sb, dsk_stream_t stream) {
+extern "C" int dsk_w8_repack(const uint8_t* q, const uint16_t* scales, const uint16_t* biases, int64_t N,
+                             int64_t K, int paired, uint8_t* wt, uint32_t* sb, dsk_stream_t stream) {
   DSK_REQUIRE(q && scales && biases && wt && sb, "dsk_w8_repack: null pointer");
   DSK_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 64 == 0,
               "dsk_w8_repack: need N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)", (long long)N,
               (long long)K);
+  DSK_REQUIRE(!paired || N % 32 == 0, "dsk_w8_repack: paired layout needs N %% 32 == 0 (N=%lld)", (long long)N);
   int64_t total = N * K / 16;
   int threads = 256;
   hipLaunchKernelGGL(w8_repack_kernel, dim3((unsigned)ceil_div(total, threads)), dim3(threads), 0,
-                     as_stream(stream), q, scales, biases, N, K, reinterpret_cast<u32x4*>(wt), sb);
+                     as_stream(stream), q, scales, biases, N, K, paired ? 1 : 0, reinterpret_cast<u32x4*>(wt), sb);
   DSK_LAUNCH_CHECK("dsk_w8_repack");
   return DSK_OK;
 }
 
 extern "C" size_t dsk_act_pack_bytes(int M, int64_t K) {
   if (M <= 0 || K <= 0 || K % 64) return 0;
-  return pack_layout(M, K).total;
+  return (size_t)((M + 15) / 16) * (size_t)K * 32;
 }
 
-extern "C" int dsk_act_pack(const uint16_t* x, int64_t ldx, int M, int64_t K, int mode,
-                            const uint16_t* norm_w, float eps, void* out, dsk_stream_t stream) {
-  DSK_REQUIRE(x && out, "dsk_act_pack: null pointer");
+extern "C" int dsk_act_pack(const float* part, int nsplit, uint16_t* h, int64_t ldh, uint16_t* copy, int64_t ldc,
+                            int M, int64_t K, const uint16_t* norm_w, float eps, uint16_t* out, dsk_stream_t stream) {
+  DSK_REQUIRE(part || h, "dsk_act_pack: needs partial sums or an input h");
+  DSK_REQUIRE(out || copy || (h && part), "dsk_act_pack: no output");
+  DSK_REQUIRE(!part || (nsplit > 0 && nsplit <= kPackMaxSplits), "dsk_act_pack: nsplit=%d outside [1, %d]", nsplit,
+              kPackMaxSplits);
+  DSK_REQUIRE(!part || (int64_t)(nsplit <= 4 ? 4 : (nsplit <= 8 ? 8 : 16)) * ceil_div(K / 8, kPackThreads) <= 16,
+              "dsk_act_pack: %d partial slices of K=%lld exceed the kernel's registers", nsplit, (long long)K);
   DSK_REQUIRE(M > 0 && M <= 64, "dsk_act_pack: M=%d outside [1, 64]", M);
-  DSK_REQUIRE(K > 0 && K % 64 == 0 && K <= kPackMaxK, "dsk_act_pack: K=%lld must be a multiple of 64 <= %d",
-              (long long)K, kPackMaxK);
-  DSK_REQUIRE(mode >= DSK_PACK_PLAIN && mode <= DSK_PACK_GELU, "dsk_act_pack: bad mode %d", mode);
-  DSK_REQUIRE(mode != DSK_PACK_RMSNORM || norm_w, "dsk_act_pack: RMSNORM needs norm_w");
-  int64_t need = (mode == DSK_PACK_SILU || mode == DSK_PACK_GELU) ? 2 * K : K;
-  DSK_REQUIRE(ldx >= need, "dsk_act_pack: ldx=%lld < %lld", (long long)ldx, (long long)need);
-  const int MT = (M + 15) / 16;
-  hipLaunchKernelGGL(act_pack_kernel, dim3(MT * 16), dim3(kPackThreads), 0, as_stream(stream), x, ldx, M, K,
-                     mode, norm_w, eps, reinterpret_cast<uint8_t*>(out));
+  DSK_REQUIRE(K > 0 && K % 64 == 0 && K <= 6 * 8 * kPackThreads,
+              "dsk_act_pack: K=%lld must be a multiple of 64 <= %d", (long long)K, 6 * 8 * kPackThreads);
+  DSK_REQUIRE(!h || (ldh >= K && ldh % 8 == 0), "dsk_act_pack: bad ldh");
+  DSK_REQUIRE(!copy || (ldc >= K && ldc % 8 == 0), "dsk_act_pack: bad ldc");
+  DSK_REQUIRE((((uintptr_t)part | (uintptr_t)h | (uintptr_t)copy | (uintptr_t)norm_w | (uintptr_t)out) & 15) == 0,
+              "dsk_act_pack: pointers must be 16-byte aligned");
+  PackArgs a{part, nsplit, h, ldh, copy, ldc, M, K, norm_w, eps, out};
+  DSK_REQUIRE(pack_launch(a, as_stream(stream)), "dsk_act_pack: no kernel for K=%lld with %d slices", (long long)K,
+              nsplit);
   DSK_LAUNCH_CHECK("dsk_act_pack");
   return DSK_OK;
 }
 
-static constexpr size_t kCounterBytes = 65536;  // 16384 slab counters at the workspace head
-
-extern "C" size_t dsk_w8_gemm_ws_bytes(int M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
-  GemmPlan p = plan_gemm(M, N, K);
-  size_t part = p.sk > 1 ? (size_t)p.sk * M * N * sizeof(float) : 0;
-  return kCounterBytes + part;
+extern "C" int dsk_w8_gemm_splits(int M, int64_t N, int64_t K) {
+  if (M <= 0 || M > 64 || N <= 0 || N % 16 || K <= 0 || K % 256) return 0;
+  return plan_gemm(M, N, K, DSK_EPI_PARTIAL).sk;
 }
 
-extern "C" int dsk_w8_gemm_ws_init(void* workspace, size_t ws_bytes, dsk_stream_t stream) {
-  DSK_REQUIRE(workspace && ws_bytes >= kCounterBytes, "dsk_w8_gemm_ws_init: workspace too small");
-  hipError_t e = hipMemsetAsync(workspace, 0, kCounterBytes, as_stream(stream));
-  if (e != hipSuccess) {
-    set_error("dsk_w8_gemm_ws_init: %s", hipGetErrorString(e));
-    return DSK_ELAUNCH;
-  }
-  return DSK_OK;
-}
-
-template <int MT, int NTW>
-static void launch_gemm(const GemmArgs& a, int waves, hipStream_t st) {
-  dim3 grid((unsigned)(a.n_slabs * a.SK));
-  (void)waves;
-  hipLaunchKernelGGL((w8_gemm_kernel<MT, NTW, 4>), grid, dim3(256), 0, st, a);
-}
-
-extern "C" int dsk_w8_gemm(const void* a_, const uint8_t* wt, const uint32_t* sb, int M, int64_t N,
-                           int64_t K, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
-                           int64_t ldr, float softcap, void* workspace, size_t ws_bytes,
-                           dsk_stream_t stream) {
-  DSK_REQUIRE(a_ && wt && sb && y, "dsk_w8_gemm: null pointer");
+extern "C" int dsk_w8_gemm(const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int M, int64_t N, int64_t K,
+                           int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual, int64_t ldr,
+                           float softcap, dsk_stream_t stream) {
+  DSK_REQUIRE(xp && wt && sb && y, "dsk_w8_gemm: null pointer");
   DSK_REQUIRE(M > 0 && M <= 64, "dsk_w8_gemm: M=%d outside [1, 64]", M);
-  DSK_REQUIRE(N > 0 && N % 16 == 0 && K > 0 && K % 64 == 0,
-              "dsk_w8_gemm: need N %% 16 == 0, K %% 64 == 0 (N=%lld K=%lld)", (long long)N, (long long)K);
-  DSK_REQUIRE(y_dtype == DSK_F32 || y_dtype == DSK_BF16, "dsk_w8_gemm: y dtype must be f32 or bf16");
-  DSK_REQUIRE(ldy >= N, "dsk_w8_gemm: ldy=%lld < N", (long long)ldy);
-  DSK_REQUIRE(!residual || ldr >= N, "dsk_w8_gemm: ldr=%lld < N", (long long)ldr);
-  DSK_REQUIRE(!(residual && y_dtype != DSK_BF16 && (const void*)residual == y),
-              "dsk_w8_gemm: in-place residual needs bf16 output");
-  GemmPlan p = plan_gemm(M, N, K);
-  const size_t need = dsk_w8_gemm_ws_bytes(M, N, K);
-  DSK_REQUIRE(workspace && ws_bytes >= need, "dsk_w8_gemm: workspace %zu < %zu bytes", ws_bytes, need);
+  DSK_REQUIRE(N > 0 && N % 16 == 0 && K > 0 && K % 256 == 0,
+              "dsk_w8_gemm: need N %% 16 == 0, K %% 256 == 0 (N=%lld K=%lld)", (long long)N, (long long)K);
+  DSK_REQUIRE(((uintptr_t)xp & 15) == 0 && ((uintptr_t)wt & 15) == 0, "dsk_w8_gemm: x and W must be 16-byte aligned");
+  DSK_REQUIRE(epi >= DSK_EPI_STORE && epi <= DSK_EPI_PARTIAL, "dsk_w8_gemm: bad epilogue %d", epi);
+  const bool gated = epi == DSK_EPI_SWIGLU || epi == DSK_EPI_GEGLU;
+  if (epi == DSK_EPI_STORE) {
+    DSK_REQUIRE(y_dtype == DSK_F32 || y_dtype == DSK_BF16, "dsk_w8_gemm: y dtype must be f32 or bf16");
+    DSK_REQUIRE(ldy >= N, "dsk_w8_gemm: ldy=%lld < N", (long long)ldy);
+    DSK_REQUIRE(!residual || ldr >= N, "dsk_w8_gemm: ldr=%lld < N", (long long)ldr);
+    DSK_REQUIRE(!(residual && y_dtype != DSK_BF16 && (const void*)residual == y),
+                "dsk_w8_gemm: in-place residual needs bf16 output");
+  } else {
+    DSK_REQUIRE(!residual && softcap == 0.0f, "dsk_w8_gemm: residual / soft-cap need DSK_EPI_STORE");
+    DSK_REQUIRE(!gated || (N % 256 == 0 && y_dtype == DSK_BF16),
+                "dsk_w8_gemm: gated epilogue needs N %% 256 == 0 and a bf16 (packed) output");
+    DSK_REQUIRE(gated || y_dtype == DSK_F32, "dsk_w8_gemm: partial sums are f32");
+  }
+  const GemmPlan p = plan_gemm(M, N, K, epi);
   GemmArgs a;
-  a.xpack = reinterpret_cast<const uint8_t*>(a_);
-  a.wt = reinterpret_cast<const u32x4*>(wt);
-  a.sb = sb;
-  a.M = M;
-  a.N = N;
-  a.K = K;
-  a.G = K / 64;
-  a.SK = p.sk;
-  a.gps = p.gps;
-  a.n_slabs = (int)(N / 16 / p.ntw);
-  DSK_REQUIRE((int64_t)a.n_slabs <= (int64_t)(kCounterBytes / sizeof(int)) || p.sk == 1,
-              "dsk_w8_gemm: too many slabs for split-K counters");
-  a.y = y;
-  a.y_f32 = (y_dtype == DSK_F32);
-  a.ldy = ldy;
-  a.res = residual;
-  a.ldr = ldr;
-  a.softcap = softcap;
-  a.cnt = reinterpret_cast<int*>(workspace);
-  a.part = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + kCounterBytes);
-  hipStream_t st = as_stream(stream);
-  const int MT = (M + 15) / 16;
-#define DSK_GEMM_CASE(MT_, NTW_) \
-  if (MT == MT_ && p.ntw == NTW_) { launch_gemm<MT_, NTW_>(a, p.waves, st); DSK_LAUNCH_CHECK("dsk_w8_gemm"); return DSK_OK; }
-  DSK_GEMM_CASE(1, 1) DSK_GEMM_CASE(1, 2) DSK_GEMM_CASE(1, 4)
-  DSK_GEMM_CASE(2, 1) DSK_GEMM_CASE(2, 2) DSK_GEMM_CASE(2, 4)
-  DSK_GEMM_CASE(3, 1) DSK_GEMM_CASE(3, 2) DSK_GEMM_CASE(3, 4)
-  DSK_GEMM_CASE(4, 1) DSK_GEMM_CASE(4, 2) DSK_GEMM_CASE(4, 4)
-#undef DSK_GEMM_CASE
-  set_error("dsk_w8_gemm: no kernel for MT=%d NTW=%d", MT, p.ntw);
-  return DSK_EINVAL;
+  gemm_prepare(a, p, xp, wt, sb, M, N, K, epi, y, y_dtype, ldy, residual, ldr, softcap);
+  if (!launch_gemm(a, (M + 15) / 16, p, as_stream(stream))) {
+    set_error("dsk_w8_gemm: no kernel for M=%d NT=%d U=%d waves=%d", M, p.nt, p.u, p.waves);
+    return DSK_EINVAL;
+  }
+  DSK_LAUNCH_CHECK("dsk_w8_gemm");
+  return DSK_OK;
 }
 
 extern "C" int dsk_w8_embed(const int32_t* ids, int n, const uint8_t* q, const uint16_t* scales,

@@ -21,23 +21,23 @@ SIGNATURES: dict[str, tuple] = {
     "dsk_last_error": (C.c_char_p, []),
     "dsk_abi_version": (c_int, []),
     "dsk_w8_quantize": (c_int, [c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]),
-    "dsk_w8_repack": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
+    "dsk_w8_repack": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p,
+                              c_void_p]),
     "dsk_act_pack_bytes": (c_size_t, [c_int, c_int64]),
-    "dsk_act_pack": (c_int, [c_void_p, c_int64, c_int, c_int64, c_int, c_void_p, c_float, c_void_p, c_void_p]),
-    "dsk_w8_gemm_ws_bytes": (c_size_t, [c_int, c_int64, c_int64]),
-    "dsk_w8_gemm_ws_init": (c_int, [c_void_p, c_size_t, c_void_p]),
-    "dsk_w8_gemm": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_void_p, c_int, c_int64,
-                            c_void_p, c_int64, c_float, c_void_p, c_size_t, c_void_p]),
+    "dsk_act_pack": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_void_p, c_int64, c_int, c_int64, c_void_p, c_float,
+                             c_void_p, c_void_p]),
+    "dsk_w8_gemm_splits": (c_int, [c_int, c_int64, c_int64]),
+    "dsk_w8_gemm": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int, c_void_p, c_int, c_int64,
+                            c_void_p, c_int64, c_float, c_void_p]),
     "dsk_w8_embed": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float,
                              c_void_p, c_int64, c_void_p]),
-    "dsk_qkv_rope_append": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float,
+    "dsk_qkv_rope_append": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float,
                                     c_void_p, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p,
                                     c_void_p, c_void_p, c_void_p, c_void_p]),
     "dsk_attn_ws_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
-    "dsk_attn_ws_init": (c_int, [c_void_p, c_size_t, c_void_p]),
     "dsk_attention": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_float,
                               c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
-                              c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+                              c_void_p, c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
     "dsk_accept_greedy": (c_int, [c_void_p, c_int, c_int64, c_int, c_int, c_int64, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "dsk_accept_ws_bytes": (c_size_t, [c_int, c_int, c_int64]),
@@ -52,7 +52,7 @@ SIGNATURES: dict[str, tuple] = {
 
 DSK_F32, DSK_BF16 = 0, 1
 DSK_KV_BF16, DSK_KV_U8 = 0, 1
-DSK_PACK_PLAIN, DSK_PACK_RMSNORM, DSK_PACK_SILU, DSK_PACK_GELU = 0, 1, 2, 3
+DSK_EPI_STORE, DSK_EPI_SWIGLU, DSK_EPI_GEGLU, DSK_EPI_PARTIAL = 0, 1, 2, 3
 
 
 def _load():

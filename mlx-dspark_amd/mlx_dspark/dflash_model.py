@@ -24,7 +24,7 @@ import torch
 
 from . import ops
 from .kv import PagedKVCache
-from .ops import DSK_PACK_PLAIN, DSK_PACK_RMSNORM, DSK_PACK_SILU, W8Weight
+from .ops import W8Weight
 from .qwen3 import MAX_ROWS, LayerWeights, TargetArgs
 
 
@@ -110,13 +110,13 @@ class DFlashDraftModel:
         if n_valid is not None and S > MAX_ROWS:
             raise ValueError("a device-counted context append must fit one pass")
         cache.check_room(S + c.block_size)
+        H = c.hidden_size
         for r0 in range(0, S, MAX_ROWS):
             r1 = min(S, r0 + MAX_ROWS)
-            x = ops.act_pack(th[r0:r1])
-            hc = ops.w8_gemm(x, self.fc, r1 - r0)                     # fc(target_hidden)
-            xc = ops.act_pack(hc, DSK_PACK_RMSNORM, self.hidden_norm, c.rms_norm_eps)
+            hcp = ops.w8_gemm(ops.pack(th[r0:r1]), self.fc, epi=ops.DSK_EPI_PARTIAL)     # fc(target_hidden)
+            xc = ops.act_pack(M=r1 - r0, K=H, part=hcp, norm_w=self.hidden_norm, eps=c.rms_norm_eps)
             for l, L in enumerate(self.layers):
-                kv = ops.w8_gemm(xc, L.kv_view(self.args), r1 - r0)
+                kv = ops.w8_gemm(xc, L.kv_view(self.args), epi=ops.DSK_EPI_PARTIAL)
                 k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
                 ops.qkv_rope_append(kv, 1, r1 - r0, 0, c.num_key_value_heads, c.head_dim, None, L.k_norm,
                                     c.rms_norm_eps, self.inv_freq, cache.seq_lens, cache.block_table,
@@ -132,25 +132,28 @@ class DFlashDraftModel:
         """block_ids [B, bs] int32 (device) -> final hidden [B*bs, H] before the drafter norm."""
         c, a = self.config, self.args
         B, bs = block_ids.shape
-        M = B * bs
+        M, H = B * bs, c.hidden_size
+        eps = c.rms_norm_eps
+        nq, nkv, hd = c.num_attention_heads, c.num_key_value_heads, c.head_dim
         h = ops.w8_embed(block_ids.reshape(-1), self.embed_tokens, self.embed_scale)
+        x = ops.pack(h, self.layers[0].in_norm, eps)
+        nl = len(self.layers)
         for l, L in enumerate(self.layers):
-            x = ops.act_pack(h, DSK_PACK_RMSNORM, L.in_norm, c.rms_norm_eps)
-            qkv = ops.w8_gemm(x, L.qkv, M)
+            qkv = ops.w8_gemm(x, L.qkv, epi=ops.DSK_EPI_PARTIAL)
             k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
-            q = ops.qkv_rope_append(qkv, B, bs, c.num_attention_heads, c.num_key_value_heads, c.head_dim,
-                                    L.q_norm, L.k_norm, c.rms_norm_eps, self.inv_freq, cache.seq_lens,
+            q = ops.qkv_rope_append(qkv, B, bs, nq, nkv, hd, L.q_norm, L.k_norm, eps, self.inv_freq, cache.seq_lens,
                                     cache.block_table, cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb)
             win = a.window(l)
-            o = ops.attention(q, B, bs, c.num_attention_heads, c.num_key_value_heads, c.head_dim,
-                              c.head_dim ** -0.5, cache.seq_lens, cache.max_ctx, cache.block_table, cache.page,
-                              cache.kv_dtype, k_pool, v_pool, k_sb, v_sb, causal=bool(win), window=win)
-            x = ops.act_pack(o, DSK_PACK_PLAIN)
-            ops.w8_gemm(x, L.o, M, out=h, residual=h)
-            x = ops.act_pack(h, DSK_PACK_RMSNORM, L.post_norm, c.rms_norm_eps)
-            gu = ops.w8_gemm(x, L.gate_up, M)
-            x = ops.act_pack(gu, DSK_PACK_SILU, K=L.down.K)
-            ops.w8_gemm(x, L.down, M, out=h, residual=h)
+            o = ops.attention(q, B, bs, nq, nkv, hd, hd ** -0.5, cache.seq_lens, cache.max_ctx, cache.block_table,
+                              cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb, causal=bool(win), window=win,
+                              packed=True)
+            op = ops.w8_gemm(o, L.o, epi=ops.DSK_EPI_PARTIAL)
+            x = ops.act_pack(M=M, K=H, part=op, h=h, norm_w=L.post_norm, eps=eps)
+            act = ops.w8_gemm(x, L.gate_up, epi=ops.DSK_EPI_SWIGLU)
+            dp = ops.w8_gemm(act, L.down, epi=ops.DSK_EPI_PARTIAL)
+            last = l == nl - 1
+            x = ops.act_pack(M=M, K=H, part=dp, h=h, norm_w=None if last else self.layers[l + 1].in_norm, eps=eps,
+                             out=not last)
         return h
 
     def block_logits(self, block_ids: torch.Tensor, cache: PagedKVCache, logits_start: int = 1,
@@ -160,11 +163,11 @@ class DFlashDraftModel:
         B, bs = block_ids.shape
         cap = bs - logits_start if cap is None else cap
         h = self.block_hidden(block_ids, cache).view(B, bs, -1)[:, logits_start:logits_start + cap]
-        h = h.reshape(B * cap, -1)
-        x = ops.act_pack(h, DSK_PACK_RMSNORM, self.norm, c.rms_norm_eps)
+        h = h.reshape(B * cap, -1) if B > 1 else h[0]
+        x = ops.pack(h, self.norm, c.rms_norm_eps)
         out = out if out is not None else torch.empty((B * cap, c.vocab_size), dtype=torch.float32,
                                                       device=self.device)
-        ops.w8_gemm(x, self.lm_head, B * cap, out=out, softcap=c.final_logit_softcapping or 0.0)
+        ops.w8_gemm(x, self.lm_head, out=out, softcap=c.final_logit_softcapping or 0.0)
         return out.view(B, cap, c.vocab_size)
 
     def __call__(self, inputs, target_hidden, cache, logits_start: int = 0):

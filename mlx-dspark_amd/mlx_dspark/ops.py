@@ -13,14 +13,14 @@ from dataclasses import dataclass
 import torch
 
 from . import _hip
-from ._hip import (DSK_BF16, DSK_F32, DSK_KV_BF16, DSK_KV_U8, DSK_PACK_GELU, DSK_PACK_PLAIN,
-                   DSK_PACK_RMSNORM, DSK_PACK_SILU, call, ptr, stream_ptr)
+from ._hip import (DSK_BF16, DSK_EPI_GEGLU, DSK_EPI_PARTIAL, DSK_EPI_STORE, DSK_EPI_SWIGLU, DSK_F32, DSK_KV_BF16,
+                   DSK_KV_U8, call, ptr, stream_ptr)
 
 __all__ = [
-    "W8Weight", "W8Table", "Workspace", "act_pack", "w8_gemm", "w8_linear", "w8_embed",
+    "W8Weight", "W8Table", "Workspace", "Packed", "act_pack", "pack", "w8_gemm", "w8_embed",
     "qkv_rope_append", "attention", "accept_greedy", "accept_sample", "sample_rows", "lens_add",
-    "rope_inv_freq", "DSK_PACK_PLAIN", "DSK_PACK_RMSNORM", "DSK_PACK_SILU", "DSK_PACK_GELU",
-    "DSK_KV_BF16", "DSK_KV_U8",
+    "rope_inv_freq", "DSK_EPI_STORE", "DSK_EPI_SWIGLU", "DSK_EPI_GEGLU", "DSK_EPI_PARTIAL", "DSK_KV_BF16",
+    "DSK_KV_U8",
 ]
 
 
@@ -69,12 +69,16 @@ class Workspace:
 # ----------------------------------------------------------------------------- W8 weights
 @dataclass
 class W8Weight:
-    """A W8 affine group-64 matrix [N, K] in the engine's tiled layout (see w8.hip)."""
+    """A W8 affine group-64 matrix [N, K] in the engine's tiled layout (see w8.hip).
+
+    ``paired``: the rows are a gate projection stacked on an up projection, repacked so the
+    GEMM's gated epilogue (SwiGLU / GeGLU) sees both halves of a column in one workgroup."""
 
     wt: torch.Tensor     # uint8 [N*K]
-    sb: torch.Tensor     # int32 [N, K/64] (bf16 scale | bf16 bias << 16)
+    sb: torch.Tensor     # int32 [N/16, K/64, 16] (bf16 scale | bf16 bias << 16)
     N: int
     K: int
+    paired: bool = False
 
     @property
     def nbytes(self) -> int:
@@ -96,19 +100,26 @@ class W8Weight:
         return q, s, b
 
     @classmethod
-    def from_mlx(cls, q: torch.Tensor, s: torch.Tensor, b: torch.Tensor) -> "W8Weight":
+    def from_mlx(cls, q: torch.Tensor, s: torch.Tensor, b: torch.Tensor, paired: bool = False) -> "W8Weight":
         _require_cuda(q, s, b)
         N, K = q.shape
         wt = torch.empty(N * K, dtype=torch.uint8, device=q.device)
-        sb = torch.empty((N, K // 64), dtype=torch.int32, device=q.device)
-        call("dsk_w8_repack", ptr(q.contiguous()), ptr(s.contiguous()), ptr(b.contiguous()), N, K,
+        sb = torch.empty((N // 16, K // 64, 16), dtype=torch.int32, device=q.device)
+        call("dsk_w8_repack", ptr(q.contiguous()), ptr(s.contiguous()), ptr(b.contiguous()), N, K, int(paired),
              ptr(wt), ptr(sb), stream_ptr())
-        return cls(wt, sb, N, K)
+        return cls(wt, sb, N, K, paired)
 
     @classmethod
-    def quantize(cls, w: torch.Tensor) -> "W8Weight":
+    def quantize(cls, w: torch.Tensor, paired: bool = False) -> "W8Weight":
         q, s, b = cls.quantize_mlx(w)
-        return cls.from_mlx(q, s, b)
+        return cls.from_mlx(q, s, b, paired)
+
+    def rows(self, n0: int, n1: int) -> "W8Weight":
+        """Zero-copy view of output rows [n0, n1) (multiples of 16, unpaired layouts)."""
+        if self.paired or n0 % 16 or n1 % 16 or not 0 <= n0 < n1 <= self.N:
+            raise ValueError(f"rows({n0}, {n1}) of a {self.N}-row W8 weight")
+        tb = (self.K // 64) * 1024
+        return W8Weight(self.wt[n0 // 16 * tb:n1 // 16 * tb], self.sb[n0 // 16:n1 // 16], n1 - n0, self.K)
 
 
 @dataclass
@@ -130,51 +141,97 @@ class W8Table:
 
 
 # ----------------------------------------------------------------------------- GEMM path
-def act_pack(x: torch.Tensor, mode: int = DSK_PACK_PLAIN, norm_w: torch.Tensor | None = None,
-             eps: float = 1e-6, K: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """Pack bf16 activations [M, *] into the GEMM operand (optionally RMSNorm / SiLU / GeLU)."""
+@dataclass
+class Packed:
+    """An [M, K] bf16 activation in the GEMM's packed operand layout (see w8.hip)."""
+
+    data: torch.Tensor   # bf16, dsk_act_pack_bytes(M, K) / 2 elements
+    M: int
+    K: int
+
+    @staticmethod
+    def empty(M: int, K: int, device) -> "Packed":
+        n = _hip.lib.dsk_act_pack_bytes(M, K)
+        if n == 0:
+            raise ValueError(f"cannot pack [{M}, {K}] (K must be a multiple of 64)")
+        return Packed(torch.empty(n // 2, dtype=torch.bfloat16, device=device), M, K)
+
+    def unpack(self) -> torch.Tensor:
+        """[M, K] bf16 copy (for checks; the engine never unpacks)."""
+        MT, G = (self.M + 15) // 16, self.K // 64
+        v = self.data.view(MT, G, 4, 16, 16)               # [mt][g][c][r][e]
+        return v.permute(0, 3, 1, 2, 4).reshape(MT * 16, self.K)[: self.M]
+
+
+def _rows_ok(t: torch.Tensor) -> bool:
+    return t.data_ptr() % 16 == 0 and t.stride(-1) == 1 and t.stride(0) % 8 == 0
+
+
+def act_pack(*, M: int, K: int, part: torch.Tensor | None = None, h: torch.Tensor | None = None,
+             copy: torch.Tensor | None = None, norm_w: torch.Tensor | None = None, eps: float = 1e-6,
+             out: Packed | bool | None = True) -> Packed | None:
+    """Sum split-K partials [S, M, K] (f32) into the residual stream h (bf16 [M, K], in place),
+    optionally copy the result (tap), RMSNorm it and pack it for the next GEMM (see
+    dsk_act_pack). out=True allocates the packed output, None/False skips it."""
+    if h is not None and not _rows_ok(h):
+        raise ValueError("act_pack: h needs unit column stride, 16-byte aligned rows")
+    if copy is not None and not _rows_ok(copy):
+        raise ValueError("act_pack: copy needs unit column stride, 16-byte aligned rows")
+    if part is not None and (part.dtype != torch.float32 or not part.is_contiguous() or part.shape[1:] != (M, K)):
+        raise ValueError(f"act_pack: partials must be contiguous f32 [S, {M}, {K}]")
+    if out is True:
+        dev = (h if h is not None else part).device
+        out = Packed.empty(M, K, dev)
+    elif out is False:
+        out = None
+    call("dsk_act_pack", ptr(part), 0 if part is None else part.shape[0], ptr(h), 0 if h is None else h.stride(0),
+         ptr(copy), 0 if copy is None else copy.stride(0), M, K, ptr(norm_w), float(eps),
+         ptr(None if out is None else out.data), stream_ptr())
+    return out
+
+
+def pack(x: torch.Tensor, norm_w: torch.Tensor | None = None, eps: float = 1e-6) -> Packed:
+    """Pack bf16 rows x [M, K] (optionally RMSNorm-ed) for the GEMM."""
     _require_cuda(x, norm_w)
-    if x.dtype != torch.bfloat16 or x.stride(-1) != 1:
-        raise ValueError("act_pack expects a bf16 tensor with unit column stride")
-    M = x.shape[0]
-    if K is None:
-        K = x.shape[1] // 2 if mode in (DSK_PACK_SILU, DSK_PACK_GELU) else x.shape[1]
-    nbytes = _hip.lib.dsk_act_pack_bytes(M, K)
-    if out is None:
-        out = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
-    elif out.numel() < nbytes:
-        raise ValueError("act_pack: output buffer too small")
-    call("dsk_act_pack", ptr(x), x.stride(0), M, K, mode, ptr(norm_w), float(eps), ptr(out), stream_ptr())
-    return out
+    if x.dtype != torch.bfloat16 or not _rows_ok(x):
+        x = x.contiguous().to(torch.bfloat16)
+    return act_pack(M=x.shape[0], K=x.shape[1], h=x, norm_w=norm_w, eps=eps)
 
 
-def w8_gemm(a: torch.Tensor, w: W8Weight, M: int, *, out: torch.Tensor | None = None,
-            out_dtype: torch.dtype = torch.bfloat16, residual: torch.Tensor | None = None,
-            softcap: float = 0.0) -> torch.Tensor:
-    """y[M, N] = residual + a . deq(W)^T (a from act_pack)."""
-    if out is None:
-        out = torch.empty((M, w.N), dtype=out_dtype, device=a.device)
-    yd = DSK_F32 if out.dtype == torch.float32 else DSK_BF16
-    ws = Workspace.get(a.device)
-    need = _hip.lib.dsk_w8_gemm_ws_bytes(M, w.N, w.K)
-    buf = ws.reserve("gemm", need)
-    call("dsk_w8_gemm", ptr(a), ptr(w.wt), ptr(w.sb), M, w.N, w.K, ptr(out), yd, out.stride(0),
-         ptr(residual), residual.stride(0) if residual is not None else 0, float(softcap),
-         ptr(buf), buf.numel(), stream_ptr())
-    return out
+def gemm_splits(M: int, N: int, K: int) -> int:
+    return _hip.lib.dsk_w8_gemm_splits(M, N, K)
 
 
-def w8_linear(x: torch.Tensor, w: W8Weight, *, mode: int = DSK_PACK_PLAIN, norm_w=None, eps=1e-6,
-              out=None, out_dtype=torch.bfloat16, residual=None, softcap=0.0) -> torch.Tensor:
-    """act_pack + w8_gemm over rows in chunks of 64."""
-    M = x.shape[0]
-    if out is None:
-        out = torch.empty((M, w.N), dtype=out_dtype, device=x.device)
-    for m0 in range(0, M, 64):
-        m1 = min(M, m0 + 64)
-        a = act_pack(x[m0:m1], mode, norm_w, eps, K=w.K)
-        w8_gemm(a, w, m1 - m0, out=out[m0:m1],
-                residual=None if residual is None else residual[m0:m1], softcap=softcap)
+def w8_gemm(x: Packed, w: W8Weight, *, epi: int = DSK_EPI_STORE, out=None, out_dtype: torch.dtype = torch.bfloat16,
+            residual: torch.Tensor | None = None, softcap: float = 0.0):
+    """x . deq(W)^T for a packed x (M <= 64). Returns, by epilogue:
+    STORE   -> [M, N] (out_dtype; + residual; soft-cap)
+    PARTIAL -> f32 [S, M, N] split-K partial sums (S = gemm_splits(M, N, K))
+    SWIGLU / GEGLU (paired W) -> Packed [M, N/2], the next GEMM's x."""
+    M = x.M
+    if x.K != w.K:
+        raise ValueError(f"w8_gemm: x has K={x.K}, W has K={w.K}")
+    dev = x.data.device
+    ldy, yd = 0, DSK_BF16
+    if epi == DSK_EPI_STORE:
+        if out is None:
+            out = torch.empty((M, w.N), dtype=out_dtype, device=dev)
+        ydata, ldy, yd = out, out.stride(0), (DSK_F32 if out.dtype == torch.float32 else DSK_BF16)
+    elif epi == DSK_EPI_PARTIAL:
+        S = gemm_splits(M, w.N, w.K)
+        if out is None:
+            out = torch.empty((S, M, w.N), dtype=torch.float32, device=dev)
+        elif tuple(out.shape) != (S, M, w.N) or out.dtype != torch.float32:
+            raise ValueError(f"w8_gemm: partial output must be f32 [{S}, {M}, {w.N}]")
+        ydata, yd = out, DSK_F32
+    else:
+        if not w.paired:
+            raise ValueError("gated epilogue needs a paired gate|up weight")
+        if out is None:
+            out = Packed.empty(M, w.N // 2, dev)
+        ydata = out.data
+    call("dsk_w8_gemm", ptr(x.data), ptr(w.wt), ptr(w.sb), M, w.N, w.K, int(epi), ptr(ydata), yd, ldy,
+         ptr(residual), residual.stride(0) if residual is not None else 0, float(softcap), stream_ptr())
     return out
 
 
@@ -200,25 +257,34 @@ def rope_inv_freq(head_dim: int, theta: float, device) -> torch.Tensor:
 
 def qkv_rope_append(qkv, B, W, nq, nkv, hd, q_norm, k_norm, eps, inv_freq, seq_lens, block_table,
                     page, kv_dtype, k_pool, v_pool, k_sb=None, v_sb=None, q_out=None, pos_offset=0):
-    if q_out is None:
+    """qkv: bf16 [B*W, (nq+2nkv)*hd] or f32 split-K partials [S, B*W, (nq+2nkv)*hd]."""
+    splits = qkv.shape[0] if qkv.dim() == 3 else 0
+    if splits and (qkv.dtype != torch.float32 or not qkv.is_contiguous()):
+        raise ValueError("qkv partials must be contiguous f32")
+    if not splits and (qkv.dtype != torch.bfloat16 or not qkv.is_contiguous()):
+        qkv = qkv.contiguous().to(torch.bfloat16)
+    if q_out is None and nq:
         q_out = torch.empty((B * W, nq * hd), dtype=torch.bfloat16, device=qkv.device)
-    call("dsk_qkv_rope_append", ptr(qkv), B, W, nq, nkv, hd, ptr(q_norm), ptr(k_norm), float(eps),
+    call("dsk_qkv_rope_append", ptr(qkv), splits, B, W, nq, nkv, hd, ptr(q_norm), ptr(k_norm), float(eps),
          ptr(inv_freq), ptr(seq_lens), int(pos_offset), ptr(block_table), block_table.shape[1], page,
          kv_dtype, ptr(k_pool), ptr(v_pool), ptr(k_sb), ptr(v_sb), ptr(q_out), stream_ptr())
     return q_out
 
 
 def attention(q, B, W, nq, nkv, hd, scale, seq_lens, max_ctx, block_table, page, kv_dtype, k_pool,
-              v_pool, k_sb=None, v_sb=None, *, causal=True, window=0, softcap=0.0, out=None):
+              v_pool, k_sb=None, v_sb=None, *, causal=True, window=0, softcap=0.0, out=None, packed=False):
+    """Returns bf16 [B*W, nq*hd], or a Packed [B*W, nq*hd] (the o-projection's x) when packed."""
     if out is None:
-        out = torch.empty((B * W, nq * hd), dtype=torch.bfloat16, device=q.device)
+        out = Packed.empty(B * W, nq * hd, q.device) if packed else torch.empty(
+            (B * W, nq * hd), dtype=torch.bfloat16, device=q.device)
+    odata = out.data if isinstance(out, Packed) else out
     ws = Workspace.get(q.device)
     need = _hip.lib.dsk_attn_ws_bytes(B, W, nq, hd, max_ctx)
     buf = ws.reserve("attn", need)
     call("dsk_attention", ptr(q), B, W, nq, nkv, hd, float(scale), int(bool(causal)), int(window),
          float(softcap), ptr(seq_lens), int(max_ctx), ptr(block_table), block_table.shape[1], page,
-         kv_dtype, ptr(k_pool), ptr(v_pool), ptr(k_sb), ptr(v_sb), ptr(out), ptr(buf), buf.numel(),
-         stream_ptr())
+         kv_dtype, ptr(k_pool), ptr(v_pool), ptr(k_sb), ptr(v_sb), ptr(odata), int(isinstance(out, Packed)),
+         ptr(buf), buf.numel(), stream_ptr())
     return out
 
 

@@ -21,8 +21,7 @@ import torch
 
 from . import ops
 from .kv import PagedKVCache
-from .ops import (DSK_PACK_GELU, DSK_PACK_PLAIN, DSK_PACK_RMSNORM, DSK_PACK_SILU, W8Table,
-                  W8Weight)
+from .ops import DSK_EPI_GEGLU, DSK_EPI_SWIGLU, W8Table, W8Weight
 
 MAX_ROWS = 64  # rows per kernel pass (M of the skinny GEMM)
 
@@ -69,7 +68,7 @@ class TargetArgs:
 class LayerWeights:
     qkv: W8Weight          # [q | k | v] rows, N = (nq + 2 nkv) * hd, K = hidden
     o: W8Weight            # N = hidden, K = nq * hd
-    gate_up: W8Weight      # [gate | up] rows, N = 2 * intermediate
+    gate_up: W8Weight      # [gate | up] rows, N = 2 * intermediate, paired layout
     down: W8Weight         # N = hidden, K = intermediate
     in_norm: torch.Tensor  # bf16 [hidden]
     post_norm: torch.Tensor
@@ -79,11 +78,7 @@ class LayerWeights:
     def kv_view(self, args: TargetArgs) -> W8Weight:
         """The [k | v] rows of the fused projection, as a zero-copy W8 view."""
         nq_rows = args.num_attention_heads * args.head_dim
-        tile_bytes = (self.qkv.K // 64) * 1024
-        t0 = nq_rows // 16
-        n = 2 * args.num_key_value_heads * args.head_dim
-        return W8Weight(self.qkv.wt[t0 * tile_bytes:(t0 + n // 16) * tile_bytes],
-                        self.qkv.sb[nq_rows:nq_rows + n], n, self.qkv.K)
+        return self.qkv.rows(nq_rows, nq_rows + 2 * args.num_key_value_heads * args.head_dim)
 
 
 class Qwen3W8:
@@ -99,7 +94,7 @@ class Qwen3W8:
         self.norm = norm
         self.device = norm.device
         self.inv_freq = ops.rope_inv_freq(args.head_dim, args.rope_theta, self.device)
-        self.act_mode = DSK_PACK_SILU if args.hidden_act == "silu" else DSK_PACK_GELU
+        self.act_epi = DSK_EPI_SWIGLU if args.hidden_act == "silu" else DSK_EPI_GEGLU
 
     # ------------------------------------------------------------------ cache
     def make_cache(self, B: int = 1, max_ctx: int | None = None, kv_bits: int | None = None,
@@ -120,29 +115,32 @@ class Qwen3W8:
     def embed_rows(self, ids: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         return ops.w8_embed(ids, self.embed, self.args.embed_scale, out=out)
 
-    def layer_forward(self, l: int, h: torch.Tensor, B: int, W: int, cache: PagedKVCache,
-                      causal: bool = True) -> None:
-        """One decoder layer over h [B*W, H] (bf16, updated in place)."""
+    def layer(self, l: int, x: ops.Packed, h: torch.Tensor, B: int, W: int, cache: PagedKVCache, *,
+              causal: bool = True, next_norm: torch.Tensor | None = None, copy: torch.Tensor | None = None,
+              want_next: bool = True) -> ops.Packed | None:
+        """One decoder layer. x: this layer's input, RMSNorm(h) packed; h [B*W, H] bf16 residual
+        stream (updated in place). Returns the next projection's packed input,
+        RMSNorm(h_out) with next_norm (the next layer's input norm or the final norm), or the
+        plain packed h_out when next_norm is None; None when want_next is False. copy, when
+        given, receives h_out (hidden-state tap)."""
         a = self.args
         L = self.layers[l]
         nq, nkv, hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
-        M = B * W
+        M, H = B * W, a.hidden_size
         eps = a.rms_norm_eps
-        x = ops.act_pack(h, DSK_PACK_RMSNORM, L.in_norm, eps)
-        qkv = ops.w8_gemm(x, L.qkv, M)
+        qkv = ops.w8_gemm(x, L.qkv, epi=ops.DSK_EPI_PARTIAL)
         k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
         q = ops.qkv_rope_append(qkv, B, W, nq, nkv, hd, L.q_norm, L.k_norm, eps, self.inv_freq,
                                 cache.seq_lens, cache.block_table, cache.page, cache.kv_dtype,
                                 k_pool, v_pool, k_sb, v_sb)
         o = ops.attention(q, B, W, nq, nkv, hd, a.attn_scale, cache.seq_lens, cache.max_ctx,
                           cache.block_table, cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb,
-                          causal=causal, window=a.window(l))
-        x = ops.act_pack(o, DSK_PACK_PLAIN)
-        ops.w8_gemm(x, L.o, M, out=h, residual=h)
-        x = ops.act_pack(h, DSK_PACK_RMSNORM, L.post_norm, eps)
-        gu = ops.w8_gemm(x, L.gate_up, M)
-        x = ops.act_pack(gu, self.act_mode, K=L.down.K)
-        ops.w8_gemm(x, L.down, M, out=h, residual=h)
+                          causal=causal, window=a.window(l), packed=True)
+        op = ops.w8_gemm(o, L.o, epi=ops.DSK_EPI_PARTIAL)
+        x = ops.act_pack(M=M, K=H, part=op, h=h, norm_w=L.post_norm, eps=eps)
+        act = ops.w8_gemm(x, L.gate_up, epi=self.act_epi)
+        dp = ops.w8_gemm(act, L.down, epi=ops.DSK_EPI_PARTIAL)
+        return ops.act_pack(M=M, K=H, part=dp, h=h, copy=copy, norm_w=next_norm, eps=eps, out=want_next)
 
     def forward(self, ids: torch.Tensor, cache: PagedKVCache, tap=None, *, advance: bool = True,
                 logits: str = "all", logits_out: torch.Tensor | None = None,
@@ -158,6 +156,7 @@ class Qwen3W8:
         if M > MAX_ROWS:
             raise ValueError(f"forward pass of {M} rows > {MAX_ROWS}; chunk the prompt")
         H = a.hidden_size
+        eps = a.rms_norm_eps
         tap = list(tap or [])
         slots: dict = {}
         for i, t in enumerate(tap):
@@ -168,18 +167,26 @@ class Qwen3W8:
         if tap:
             fused = fused_out if fused_out is not None else torch.empty(
                 (M, len(tap) * H), dtype=torch.bfloat16, device=self.device)
-        for l in range(a.num_hidden_layers):
-            self.layer_forward(l, h, B, W, cache)
-            for s in slots.get(l, ()):
-                fused[:, s * H:(s + 1) * H].copy_(h)
+        nl = a.num_hidden_layers
+        x = ops.pack(h, self.layers[0].in_norm, eps)
+        for l in range(nl):
+            last = l == nl - 1
+            s = slots.get(l, ())
+            copy = fused[:, s[0] * H:(s[0] + 1) * H] if s else None
+            if not last:
+                x = self.layer(l, x, h, B, W, cache, next_norm=self.layers[l + 1].in_norm, copy=copy)
+            else:   # the final norm is fused into the last residual add when every row needs logits
+                x = self.layer(l, x, h, B, W, cache, next_norm=self.norm, copy=copy, want_next=logits == "all")
+            for extra in s[1:]:
+                fused[:, extra * H:(extra + 1) * H].copy_(fused[:, s[0] * H:(s[0] + 1) * H])
         out = None
         if logits != "none":
-            rows = h if logits == "all" else h.view(B, W, H)[:, -1]
-            Mr = rows.shape[0]
-            x = ops.act_pack(rows, DSK_PACK_RMSNORM, self.norm, a.rms_norm_eps)
+            if logits != "all":
+                x = ops.pack(h.view(B, W, H)[:, -1], self.norm, eps)
+            Mr = x.M
             out = logits_out if logits_out is not None else torch.empty(
                 (Mr, a.vocab_size), dtype=torch.float32, device=self.device)
-            ops.w8_gemm(x, self.lm_head, Mr, out=out, softcap=a.final_logit_softcapping or 0.0)
+            ops.w8_gemm(x, self.lm_head, out=out, softcap=a.final_logit_softcapping or 0.0)
             out = out.view(B, W if logits == "all" else 1, a.vocab_size)
         if advance:
             ops.lens_add(cache.seq_lens, None, W)
@@ -193,8 +200,8 @@ class Qwen3W8:
                                                       device=self.device)
         for m0 in range(0, h.shape[0], MAX_ROWS):
             m1 = min(h.shape[0], m0 + MAX_ROWS)
-            x = ops.act_pack(h[m0:m1], DSK_PACK_RMSNORM, self.norm, a.rms_norm_eps)
-            ops.w8_gemm(x, self.lm_head, m1 - m0, out=out[m0:m1], softcap=a.final_logit_softcapping or 0.0)
+            x = ops.pack(h[m0:m1], self.norm, a.rms_norm_eps)
+            ops.w8_gemm(x, self.lm_head, out=out[m0:m1], softcap=a.final_logit_softcapping or 0.0)
         return out
 
     def prefill(self, ids: list[int] | torch.Tensor, cache: PagedKVCache, tap=None, *, chunk: int = MAX_ROWS,

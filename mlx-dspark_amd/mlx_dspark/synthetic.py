@@ -48,11 +48,11 @@ def randn(shape, seed: int, name: str, device, std: float = STD) -> torch.Tensor
     return torch.randn(shape, generator=g, device=device, dtype=torch.float32) * std
 
 
-def w8(N: int, K: int, seed: int, name: str, device, keep_mlx: bool = False) -> W8Weight:
+def w8(N: int, K: int, seed: int, name: str, device, keep_mlx: bool = False, paired: bool = False) -> W8Weight:
     w = randn((N, K), seed, name, device)
     q, s, b = W8Weight.quantize_mlx(w)
     del w
-    W = W8Weight.from_mlx(q, s, b)
+    W = W8Weight.from_mlx(q, s, b, paired)
     if keep_mlx:
         W.mlx = (q, s, b)
     return W
@@ -88,7 +88,7 @@ def build_target(name_or_args, seed: int = 0, device="cuda", keep_mlx: bool = Fa
         layers.append(LayerWeights(
             qkv=w8(args.n_qkv, H, seed, p + "qkv", device, keep_mlx),
             o=w8(H, nq * hd, seed, p + "o", device, keep_mlx),
-            gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx),
+            gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx, paired=True),
             down=w8(H, I, seed, p + "down", device, keep_mlx),
             in_norm=ones(H, device), post_norm=ones(H, device),
             q_norm=qk_norm(hd, device), k_norm=qk_norm(hd, device)))
@@ -140,7 +140,7 @@ def build_dflash(target_args: TargetArgs, seed: int = 1, device="cuda", keep_mlx
         layers.append(LayerWeights(
             qkv=w8(a.n_qkv, H, seed, p + "qkv", device, keep_mlx),
             o=w8(H, nq * hd, seed, p + "o", device, keep_mlx),
-            gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx),
+            gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx, paired=True),
             down=w8(H, I, seed, p + "down", device, keep_mlx),
             in_norm=ones(H, device), post_norm=ones(H, device),
             q_norm=qk_norm(hd, device), k_norm=qk_norm(hd, device)))

@@ -33,9 +33,11 @@ def test_binding_matches_header():
 
 def test_size_queries_without_gpu():
     from mlx_dspark import _hip
-    assert _hip.lib.dsk_act_pack_bytes(16, 4096) == 16 * 64 * 64 * 32 // 16 * 1 + 64 * 64 + 64 or True
-    assert _hip.lib.dsk_act_pack_bytes(0, 64) == 0
-    assert _hip.lib.dsk_w8_gemm_ws_bytes(16, 4096, 4096) > 0
+    assert _hip.lib.dsk_act_pack_bytes(16, 4096) == 16 * 4096 * 2
+    assert _hip.lib.dsk_act_pack_bytes(17, 4096) == 32 * 4096 * 2
+    assert _hip.lib.dsk_act_pack_bytes(0, 64) == 0 and _hip.lib.dsk_act_pack_bytes(4, 96) == 0
+    assert 1 <= _hip.lib.dsk_w8_gemm_splits(16, 4096, 4096) <= 16
+    assert _hip.lib.dsk_w8_gemm_splits(16, 4096, 4000) == 0
     assert _hip.lib.dsk_accept_ws_bytes(4, 17, 151936) > 4 * 17 * 2 * 151936 * 4
 
 

@@ -130,3 +130,42 @@ def test_append_and_attention(dev, kv_dtype, B, W, L0, causal):
         got = out.view(B, W, nq, hd)[b].float().cpu()
         err = (got - ref).abs().max().item()
         assert err < 2e-2, err
+
+
+@pytest.mark.parametrize("L0", [0, 300, 4100])
+def test_partial_qkv_input_and_packed_output(dev, L0):
+    """Split-K partial sums as the rope input and the packed (o-projection) output layout give
+    the same q, cache contents and attention output as the bf16 / row-major path."""
+    from mlx_dspark.ops import attention, qkv_rope_append, rope_inv_freq
+    print(f"partial/packed L0={L0}", flush=True)
+    B, W, nq, nkv, hd, page = 1, 16, 8, 2, 128, 64
+    g = torch.Generator().manual_seed(L0 + 7)
+    max_ctx = L0 + W + 5
+    nh = nq + 2 * nkv
+    inv = rope_inv_freq(hd, 1e6, dev)
+    qn = torch.full((hd,), hd ** -0.25).to(torch.bfloat16).to(dev)
+    pools = [Pool(B, nkv, hd, max_ctx, page, 1, dev, seed=3) for _ in range(2)]
+    sl = torch.full((B,), L0, dtype=torch.int32, device=dev)
+    if L0:
+        pre = torch.randn(B * L0, nh * hd, generator=g).to(torch.bfloat16).to(dev)
+        for p in pools:
+            zeros = torch.zeros(B, dtype=torch.int32, device=dev)
+            for c0 in range(0, L0, 64):
+                c1 = min(L0, c0 + 64)
+                z = zeros + c0
+                qkv_rope_append(pre[c0:c1], B, c1 - c0, nq, nkv, hd, qn, qn, 1e-6, inv, z, p.block_table, page, 1,
+                                p.k, p.v, p.ksb, p.vsb)
+    parts = torch.randn(3, B * W, nh * hd, generator=g).to(dev)
+    summed = parts[0] + parts[1] + parts[2]
+    q_a = qkv_rope_append(summed.to(torch.bfloat16), B, W, nq, nkv, hd, qn, qn, 1e-6, inv, sl, pools[0].block_table,
+                          page, 1, pools[0].k, pools[0].v, pools[0].ksb, pools[0].vsb)
+    q_b = qkv_rope_append(parts, B, W, nq, nkv, hd, qn, qn, 1e-6, inv, sl, pools[1].block_table, page, 1,
+                          pools[1].k, pools[1].v, pools[1].ksb, pools[1].vsb)
+    assert torch.equal(q_a, q_b)
+    assert torch.equal(pools[0].k, pools[1].k) and torch.equal(pools[0].vsb, pools[1].vsb)
+    kw = dict(causal=True)
+    o_a = attention(q_a, B, W, nq, nkv, hd, hd ** -0.5, sl, max_ctx, pools[0].block_table, page, 1, pools[0].k,
+                    pools[0].v, pools[0].ksb, pools[0].vsb, **kw)
+    o_b = attention(q_b, B, W, nq, nkv, hd, hd ** -0.5, sl, max_ctx, pools[1].block_table, page, 1, pools[1].k,
+                    pools[1].v, pools[1].ksb, pools[1].vsb, packed=True, **kw)
+    assert torch.equal(o_a, o_b.unpack())
