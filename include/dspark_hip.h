@@ -223,6 +223,38 @@ int dsk_sample_rows(const float* logits, int64_t V, int R, float temperature, fl
  * accepted rows, :935-937). */
 int dsk_lens_add(int32_t* lens, const int32_t* n, int B, int add, dsk_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------
+ * DSpark drafter heads.
+ * ------------------------------------------------------------------------------------- */
+
+/* Block sampling with the rank-R Markov head: replaces DSparkDrafter.sample_block /
+ * sample_block_probs (src/mlx_dspark/model.py:270-309) and the batched form
+ * _batched_sample_block (src/mlx_dspark/batch_engine.py:414-428).
+ *   prev = first_prev[b]; for i < cap:
+ *     l_i[v] = bf16(bf16(base[b][i][v]) + bf16(sum_r deq(w2)[v][r] * bf16(deq(w1)[prev][r])))
+ *     greedy (temperature == 0): tok[b][i] = argmax_v l_i (lowest index on ties)
+ *     sampled: tok[b][i] ~ truncate(softmax(l_i * (1/T))) (dsk_sample_rows, Philox row b*cap + i),
+ *              q_logits_out[b][i] = l_i (the draft distribution's logits, for dsk_accept_sample
+ *              with q_mul_inv_t = 1)
+ *     prev = tok[b][i]
+ * base f32 [B][cap][V] (row stride ldb), first_prev int32 [B] (device), w1: MLX-layout W8 table
+ * [V, R] (q u8, scales/biases bf16 [V, R/64]), w2: dsk_w8_repack layout of [V, R]. R == 256,
+ * B <= 16, V % 16 == 0. tok_out int32 [B][cap]. workspace: dsk_markov_ws_bytes(B, V, sampled). */
+size_t dsk_markov_ws_bytes(int B, int64_t V, int sampled);
+int dsk_markov_block(const float* base, int64_t ldb, int B, int cap, int64_t V, int R,
+                     const int32_t* first_prev, const uint8_t* w1q, const uint16_t* w1s,
+                     const uint16_t* w1b, const uint8_t* w2t, const uint32_t* w2sb,
+                     float temperature, float top_p, int top_k, uint64_t seed, uint32_t offset,
+                     int32_t* tok_out, float* q_logits_out, void* workspace, size_t ws_bytes,
+                     dsk_stream_t stream);
+
+/* Presence / frequency penalties on verify logits: logits[r][ids[j]] -= vals[j] for
+ * j in [row_ptr[r], row_ptr[r+1]) (ids distinct within a row). The host builds the rows as
+ * _Penalizer.block_penalty does (src/mlx_dspark/generate.py:202-228): base completion counts
+ * plus each row's draft prefix. */
+int dsk_logits_penalize(float* logits, int64_t ldl, int R, const int32_t* row_ptr,
+                        const int32_t* ids, const float* vals, dsk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,16 +6,20 @@ for the decode path: loaders, Target, the drafters, the decode loops and GenResu
 
 __version__ = "0.1.0"
 
+from .config import DSparkConfig
 from .dflash_model import DFlashConfig, DFlashDraftModel
 from .generate import (GenResult, StopStreaming, dflash_generate, encode_messages, encode_prompt,
-                       greedy_generate)
+                       greedy_generate, speculative_generate)
 from .load import (DEFAULT_DRAFTER, DEFAULT_TARGET, DFLASH_PRESETS, PRESETS, REGISTRY, apply_wired_limit,
-                   load_dflash, load_dflash_pair, load_target, resolve, resolve_mode)
+                   load_dflash, load_dflash_pair, load_drafter, load_pair, load_target, resolve, resolve_mode)
+from .lookup import NGramIndex
+from .model import DSparkDrafter, Gemma4DSparkDrafter
 from .target import Target
 
 __all__ = [
-    "DFlashConfig", "DFlashDraftModel", "Target", "load_dflash", "load_target", "load_dflash_pair",
-    "dflash_generate", "greedy_generate", "StopStreaming", "encode_messages", "encode_prompt", "GenResult",
-    "PRESETS", "DFLASH_PRESETS", "REGISTRY", "resolve", "resolve_mode", "apply_wired_limit",
-    "DEFAULT_TARGET", "DEFAULT_DRAFTER",
+    "DSparkConfig", "DSparkDrafter", "Gemma4DSparkDrafter", "DFlashConfig", "DFlashDraftModel", "Target",
+    "load_pair", "load_drafter", "load_dflash", "load_target", "load_dflash_pair",
+    "speculative_generate", "dflash_generate", "greedy_generate", "StopStreaming", "encode_messages",
+    "encode_prompt", "GenResult", "NGramIndex", "PRESETS", "DFLASH_PRESETS", "REGISTRY", "resolve", "resolve_mode",
+    "apply_wired_limit", "DEFAULT_TARGET", "DEFAULT_DRAFTER",
 ]

@@ -1,0 +1,90 @@
+"""Forward pieces shared by the block drafters (DSpark and DFlash) on gfx950 kernels.
+
+Both drafters condition on the target's hidden states through an EAGLE-style context: the
+tapped target states are fused (fc, then RMSNorm) and every drafter layer projects them to
+K/V, K normed and roped at its absolute position, and keeps them in a per-layer cache
+(src/mlx_dspark/model.py:113-128, :247-256; src/mlx_dspark/dflash_model.py:111-123, :199).
+A drafted block then runs the drafter layers over [anchor] + [mask] * (k-1) with attention
+over context ++ block, bidirectional (model.py:130-155, dflash_model.py:123-133).
+
+Here the context K/V lives in a PagedKVCache. The block's own K/V is appended after the
+cached context in the same pages but outside the cached length, so the next context append
+overwrites it (the reference concatenates it on the fly and never stores it).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import ops
+from .kv import PagedKVCache
+from .qwen3 import MAX_ROWS
+
+
+def ingest_context(d, target_hidden: torch.Tensor, cache: PagedKVCache, n_valid=None) -> None:
+    """Append context rows for drafter ``d``: target_hidden [S, n_tap*H] (or [1, S, .]) bf16.
+
+    ``d`` provides config (hidden_size, num_key_value_heads, head_dim, rms_norm_eps, block_size),
+    fc, hidden_norm, layers (with kv_view / k_norm), args and inv_freq. n_valid (device int32
+    [1]) advances the cached length by n_valid + 1 instead of S: the fixed-shape form used when
+    only a device-side prefix of the rows is committed (speculative rounds)."""
+    c = d.config
+    th = target_hidden.reshape(-1, target_hidden.shape[-1])
+    S = th.shape[0]
+    if n_valid is not None and S > MAX_ROWS:
+        raise ValueError("a device-counted context append must fit one pass")
+    cache.check_room(S + c.block_size)
+    H = c.hidden_size
+    for r0 in range(0, S, MAX_ROWS):
+        r1 = min(S, r0 + MAX_ROWS)
+        hcp = ops.w8_gemm(ops.pack(th[r0:r1]), d.fc, epi=ops.DSK_EPI_PARTIAL)          # fc(target_hidden)
+        xc = ops.act_pack(M=r1 - r0, K=H, part=hcp, norm_w=d.hidden_norm, eps=c.rms_norm_eps)
+        for l, L in enumerate(d.layers):
+            kv = ops.w8_gemm(xc, L.kv_view(d.args), epi=ops.DSK_EPI_PARTIAL)
+            k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
+            ops.qkv_rope_append(kv, 1, r1 - r0, 0, c.num_key_value_heads, c.head_dim, None, L.k_norm,
+                                c.rms_norm_eps, d.inv_freq, cache.seq_lens, cache.block_table,
+                                cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb, None)
+        if n_valid is None:
+            ops.lens_add(cache.seq_lens, None, r1 - r0)
+            cache.note_lengths([cache.lengths[0] + (r1 - r0)])
+    if n_valid is not None:
+        ops.lens_add(cache.seq_lens, n_valid, 1)
+
+
+def block_layers(d, h: torch.Tensor, B: int, bs: int, cache: PagedKVCache, scale: float) -> torch.Tensor:
+    """Run drafter ``d``'s decoder layers (2-norm Qwen3 layout) over the block rows h [B*bs, H]
+    (bf16, updated in place) attending to context ++ block; returns h before the final norm."""
+    c, a = d.config, d.args
+    M, H = B * bs, c.hidden_size
+    eps = c.rms_norm_eps
+    nq, nkv, hd = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+    x = ops.pack(h, d.layers[0].in_norm, eps)
+    nl = len(d.layers)
+    for l, L in enumerate(d.layers):
+        qkv = ops.w8_gemm(x, L.qkv, epi=ops.DSK_EPI_PARTIAL)
+        k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
+        q = ops.qkv_rope_append(qkv, B, bs, nq, nkv, hd, L.q_norm, L.k_norm, eps, d.inv_freq, cache.seq_lens,
+                                cache.block_table, cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb)
+        win = a.window(l)
+        o = ops.attention(q, B, bs, nq, nkv, hd, scale, cache.seq_lens, cache.max_ctx, cache.block_table,
+                          cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb, causal=bool(win), window=win,
+                          packed=True)
+        op = ops.w8_gemm(o, L.o, epi=ops.DSK_EPI_PARTIAL)
+        x = ops.act_pack(M=M, K=H, part=op, h=h, norm_w=L.post_norm, eps=eps)
+        act = ops.w8_gemm(x, L.gate_up, epi=d.act_epi)
+        dp = ops.w8_gemm(act, L.down, epi=ops.DSK_EPI_PARTIAL)
+        last = l == nl - 1
+        x = ops.act_pack(M=M, K=H, part=dp, h=h, norm_w=None if last else d.layers[l + 1].in_norm, eps=eps,
+                         out=not last)
+    return h
+
+
+def head_rows(d, h_rows: torch.Tensor, lm_head, out: torch.Tensor | None = None) -> torch.Tensor:
+    """logits = lm_head(norm(h_rows)) (+ soft-cap) for h_rows [R, H] bf16 -> f32 [R, V]."""
+    c = d.config
+    x = ops.pack(h_rows, d.norm, c.rms_norm_eps)
+    out = out if out is not None else torch.empty((h_rows.shape[0], lm_head.N), dtype=torch.float32,
+                                                  device=h_rows.device)
+    ops.w8_gemm(x, lm_head, out=out, softcap=c.final_logit_softcapping or 0.0)
+    return out

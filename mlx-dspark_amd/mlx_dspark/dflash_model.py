@@ -22,10 +22,10 @@ from typing import Any, Dict, Optional, Tuple
 
 import torch
 
-from . import ops
+from . import blockdraft, ops
 from .kv import PagedKVCache
 from .ops import W8Weight
-from .qwen3 import MAX_ROWS, LayerWeights, TargetArgs
+from .qwen3 import LayerWeights, TargetArgs
 
 
 @dataclass
@@ -76,6 +76,7 @@ class DFlashDraftModel:
         self.norm = norm
         self.device = norm.device
         self.inv_freq = ops.rope_inv_freq(config.head_dim, config.rope_theta, self.device)
+        self.act_epi = ops.DSK_EPI_SWIGLU
         self.target = None
         self.embed_tokens = None
         self.lm_head = None
@@ -100,61 +101,16 @@ class DFlashDraftModel:
 
     # ---------------------------------------------------------------- context
     def ingest(self, target_hidden: torch.Tensor, cache: PagedKVCache, n_valid=None) -> None:
-        """Append context rows: target_hidden [S, n_tap*H] (or [1, S, .]) bf16.
-
-        n_valid (device int32 [1]) advances the cached length by n_valid + 1 instead of S:
-        the fixed-shape form used when only a device-side prefix of the rows is committed."""
-        c = self.config
-        th = target_hidden.reshape(-1, target_hidden.shape[-1])
-        S = th.shape[0]
-        if n_valid is not None and S > MAX_ROWS:
-            raise ValueError("a device-counted context append must fit one pass")
-        cache.check_room(S + c.block_size)
-        H = c.hidden_size
-        for r0 in range(0, S, MAX_ROWS):
-            r1 = min(S, r0 + MAX_ROWS)
-            hcp = ops.w8_gemm(ops.pack(th[r0:r1]), self.fc, epi=ops.DSK_EPI_PARTIAL)     # fc(target_hidden)
-            xc = ops.act_pack(M=r1 - r0, K=H, part=hcp, norm_w=self.hidden_norm, eps=c.rms_norm_eps)
-            for l, L in enumerate(self.layers):
-                kv = ops.w8_gemm(xc, L.kv_view(self.args), epi=ops.DSK_EPI_PARTIAL)
-                k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
-                ops.qkv_rope_append(kv, 1, r1 - r0, 0, c.num_key_value_heads, c.head_dim, None, L.k_norm,
-                                    c.rms_norm_eps, self.inv_freq, cache.seq_lens, cache.block_table,
-                                    cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb, None)
-            if n_valid is None:
-                ops.lens_add(cache.seq_lens, None, r1 - r0)
-                cache.note_lengths([cache.lengths[0] + (r1 - r0)])
-        if n_valid is not None:
-            ops.lens_add(cache.seq_lens, n_valid, 1)
+        """Append context rows: target_hidden [S, n_tap*H] (or [1, S, .]) bf16 (see
+        blockdraft.ingest_context; n_valid: device-counted append of n_valid + 1 rows)."""
+        blockdraft.ingest_context(self, target_hidden, cache, n_valid)
 
     # ---------------------------------------------------------------- block
     def block_hidden(self, block_ids: torch.Tensor, cache: PagedKVCache) -> torch.Tensor:
         """block_ids [B, bs] int32 (device) -> final hidden [B*bs, H] before the drafter norm."""
-        c, a = self.config, self.args
         B, bs = block_ids.shape
-        M, H = B * bs, c.hidden_size
-        eps = c.rms_norm_eps
-        nq, nkv, hd = c.num_attention_heads, c.num_key_value_heads, c.head_dim
         h = ops.w8_embed(block_ids.reshape(-1), self.embed_tokens, self.embed_scale)
-        x = ops.pack(h, self.layers[0].in_norm, eps)
-        nl = len(self.layers)
-        for l, L in enumerate(self.layers):
-            qkv = ops.w8_gemm(x, L.qkv, epi=ops.DSK_EPI_PARTIAL)
-            k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
-            q = ops.qkv_rope_append(qkv, B, bs, nq, nkv, hd, L.q_norm, L.k_norm, eps, self.inv_freq, cache.seq_lens,
-                                    cache.block_table, cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb)
-            win = a.window(l)
-            o = ops.attention(q, B, bs, nq, nkv, hd, hd ** -0.5, cache.seq_lens, cache.max_ctx, cache.block_table,
-                              cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb, causal=bool(win), window=win,
-                              packed=True)
-            op = ops.w8_gemm(o, L.o, epi=ops.DSK_EPI_PARTIAL)
-            x = ops.act_pack(M=M, K=H, part=op, h=h, norm_w=L.post_norm, eps=eps)
-            act = ops.w8_gemm(x, L.gate_up, epi=ops.DSK_EPI_SWIGLU)
-            dp = ops.w8_gemm(act, L.down, epi=ops.DSK_EPI_PARTIAL)
-            last = l == nl - 1
-            x = ops.act_pack(M=M, K=H, part=dp, h=h, norm_w=None if last else self.layers[l + 1].in_norm, eps=eps,
-                             out=not last)
-        return h
+        return blockdraft.block_layers(self, h, B, bs, cache, self.config.head_dim ** -0.5)
 
     def block_logits(self, block_ids: torch.Tensor, cache: PagedKVCache, logits_start: int = 1,
                      cap: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -164,10 +120,7 @@ class DFlashDraftModel:
         cap = bs - logits_start if cap is None else cap
         h = self.block_hidden(block_ids, cache).view(B, bs, -1)[:, logits_start:logits_start + cap]
         h = h.reshape(B * cap, -1) if B > 1 else h[0]
-        x = ops.pack(h, self.norm, c.rms_norm_eps)
-        out = out if out is not None else torch.empty((B * cap, c.vocab_size), dtype=torch.float32,
-                                                      device=self.device)
-        ops.w8_gemm(x, self.lm_head, out=out, softcap=c.final_logit_softcapping or 0.0)
+        out = blockdraft.head_rows(self, h, self.lm_head, out)
         return out.view(B, cap, c.vocab_size)
 
     def __call__(self, inputs, target_hidden, cache, logits_start: int = 0):

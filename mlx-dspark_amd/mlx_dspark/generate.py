@@ -20,7 +20,7 @@ from dataclasses import dataclass
 
 import torch
 
-from . import ops
+from . import blockdraft, ops
 
 # ============================================================================ results
 @dataclass
@@ -342,3 +342,269 @@ def dflash_generate(target_model, tokenizer, drafter, prompt: str = "", *, promp
     return GenResult(text=_final_text(tokenizer, st, out_ids, eos_ids), token_ids=out_ids, num_tokens=len(out_ids),
                      num_rounds=len(accept_lengths), accept_lengths=accept_lengths, target_forwards=target_forwards,
                      seconds=secs, finish_reason=_finish_reason(out_ids, max_new_tokens, pending, eos_ids, st))
+
+
+# ============================================================================ penalties
+class _Penalizer:
+    """OpenAI presence / frequency penalties on the target's verify logits (the behaviour of
+    the reference's _Penalizer, src/mlx_dspark/generate.py:179-228): row i of a verify block
+    subtracts presence * (count > 0) + frequency * count over the completion tokens so far
+    plus the block's own draft prefix draft[:i]. Inactive (both 0) it is a no-op."""
+
+    def __init__(self, presence: float = 0.0, frequency: float = 0.0):
+        self.presence = float(presence or 0.0)
+        self.frequency = float(frequency or 0.0)
+        self.active = bool(self.presence or self.frequency)
+        self.counts: dict = {}
+
+    def add(self, tokens) -> None:
+        if self.active:
+            for t in tokens:
+                self.counts[int(t)] = self.counts.get(int(t), 0) + 1
+
+    def block_rows(self, draft_prefix) -> list:
+        """[{token: penalty}] for the len(draft_prefix) + 1 rows of a verify block."""
+        base = {t: self.presence + self.frequency * c for t, c in self.counts.items()}
+        rows = [base]
+        seen = dict(self.counts)
+        for d in draft_prefix:
+            d = int(d)
+            nxt = dict(rows[-1])
+            nxt[d] = nxt.get(d, 0.0) + self.frequency + (self.presence if seen.get(d, 0) == 0 else 0.0)
+            seen[d] = seen.get(d, 0) + 1
+            rows.append(nxt)
+        return rows
+
+    def apply(self, v_logits: torch.Tensor, draft_prefix) -> torch.Tensor:
+        """Penalise v_logits [len(draft)+1, V] (f32, device) in place; identity when inactive."""
+        if not self.active:
+            return v_logits
+        rows = self.block_rows(draft_prefix)
+        ptr, ids, vals = [0], [], []
+        for r in rows:
+            for t, v in r.items():
+                if v:
+                    ids.append(t)
+                    vals.append(v)
+            ptr.append(len(ids))
+        if not ids:
+            return v_logits
+        dev = v_logits.device
+        ops.logits_penalize(v_logits, torch.tensor(ptr, dtype=torch.int32, device=dev),
+                            torch.tensor(ids, dtype=torch.int32, device=dev),
+                            torch.tensor(vals, dtype=torch.float32, device=dev))
+        return v_logits
+
+
+# ============================================================================ DSpark
+class _DSparkRound:
+    """Static buffers and the device-side body of a greedy DSpark round at a fixed cap: draft
+    the block, Markov-sample cap tokens, verify [pending] + draft, accept, roll back, grow the
+    drafter context. Replayed as one HIP graph from its second use on."""
+
+    def __init__(self, target, drafter, cache, dcache, cap: int):
+        self.target, self.drafter, self.cache, self.dcache = target, drafter, cache, dcache
+        self.model = target.model
+        cfg = drafter.config
+        self.tap = list(cfg.target_layer_ids)
+        self.k = int(cfg.block_size)
+        self.cap = cap
+        dev = self.model.device
+        V, H = self.model.args.vocab_size, self.model.args.hidden_size
+        self.block = torch.full((1, self.k), int(cfg.mask_token_id), dtype=torch.int32, device=dev)
+        self.pending = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.head = torch.empty((cap, drafter.lm_head.N), dtype=torch.float32, device=dev)
+        self.draft = torch.zeros((1, cap), dtype=torch.int32, device=dev)
+        self.verify = torch.zeros((1, cap + 1), dtype=torch.int32, device=dev)
+        self.v_logits = torch.empty((cap + 1, V), dtype=torch.float32, device=dev)
+        self.v_fused = torch.empty((cap + 1, len(self.tap) * H), dtype=torch.bfloat16, device=dev)
+        self.n = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.token = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.tt = torch.zeros((1, cap + 1), dtype=torch.int32, device=dev)
+        self.out = torch.zeros(2 + cap, dtype=torch.int32, device=dev)   # [n, token, draft...]
+        self.graph = None
+        self.uses = 0
+
+    def body(self) -> None:
+        self.block[0, 0:1].copy_(self.pending)
+        self.drafter.block_logits(self.block, self.dcache, self.cap, out=self.head)
+        self.drafter.sample_block(self.head.view(1, self.cap, -1), self.pending, out=self.draft)
+        self.verify[0, 0:1].copy_(self.pending)
+        self.verify[0, 1:].copy_(self.draft[0])
+        self.model.forward(self.verify, self.cache, self.tap, advance=False, logits_out=self.v_logits,
+                           fused_out=self.v_fused)
+        ops.accept_greedy(self.v_logits.view(1, self.cap + 1, -1), self.draft, seq_lens=self.cache.seq_lens,
+                          tt=self.tt, n_out=self.n, token_out=self.token)
+        self.pending.copy_(self.token)
+        self.drafter.update_context(self.v_fused, 0, self.dcache, n_valid=self.n)
+        self.out[0:1].copy_(self.n)
+        self.out[1:2].copy_(self.token)
+        self.out[2:].copy_(self.draft[0])
+
+    def run(self, use_graph: bool):
+        if use_graph and self.graph is None and self.uses >= 1:
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                self.body()
+        if use_graph and self.graph is not None:
+            self.graph.replay()
+        else:
+            self.body()
+        self.uses += 1
+        o = self.out.tolist()                                          # the round's one host sync
+        n, token, draft = o[0], o[1], o[2:]
+        self.cache.note_lengths([self.cache.lengths[0] + n + 1])
+        self.dcache.note_lengths([self.dcache.lengths[0] + n + 1])
+        return n, token, draft
+
+
+def speculative_generate(target_model, tokenizer, drafter, prompt: str = "", *, prompt_ids=None, cache=None,
+                         ctx_caches=None, reuse_len: int = 0, max_new_tokens: int = 128,
+                         confidence_threshold: float = 0.0, max_draft_tokens=2, cap_controller=None,
+                         lookup_drafts: bool = True, lookup_max_draft: int = 6, temperature: float = 0.0,
+                         top_p: float = 1.0, top_k: int = 0, presence_penalty: float = 0.0,
+                         frequency_penalty: float = 0.0, logprobs=None, seed=None, apply_chat_template: bool = True,
+                         stop=None, on_text=None, verbose: bool = False, use_graph: bool = True,
+                         max_ctx: int | None = None) -> GenResult:
+    """Speculative decoding with a DSpark drafter, batch 1 (src/mlx_dspark/generate.py:691-978).
+
+    Greedy (temperature 0): Markov-argmax draft, exact argmax-match verify; the output is the
+    target's greedy stream. temperature > 0: speculative sampling (accept with min(1, p/q),
+    residual resample, bonus from the target), exact wrt truncate(softmax(target / T)).
+    max_draft_tokens caps the drafted-and-verified positions per round (None = the whole
+    block); confidence_threshold > 0 truncates the draft with the confidence head's
+    cumulative survival; lookup_drafts verifies an n-gram continuation of an earlier
+    occurrence instead of drafting when one exists. The default greedy round (no penalties,
+    no confidence truncation) runs on the device end to end, graph-replayed, with one host
+    sync per round."""
+    if logprobs is not None:
+        raise NotImplementedError("logprobs are not supported by this engine yet")
+    cfg = drafter.config
+    tap = list(cfg.target_layer_ids)
+    k = int(cfg.block_size)
+    cap_ceiling = k if max_draft_tokens is None else max(1, min(int(max_draft_tokens), k))
+    eos_ids = eos_token_ids(tokenizer)
+    ids = prompt_ids if prompt_ids is not None else encode_prompt(tokenizer, prompt, apply_chat_template)
+    model = target_model.model
+    V = model.args.vocab_size
+    need = len(ids) + max_new_tokens + 2 * (k + max(lookup_max_draft, k)) + 8
+    if cache is None:
+        cache = target_model.make_cache(max_ctx=max(max_ctx or 0, need))
+        ctx_caches = drafter.make_ctx_cache(max_ctx=max(max_ctx or 0, need))
+        reuse_len = 0
+    elif ctx_caches is None:
+        raise ValueError("a reused target cache needs its drafter ctx_caches")
+    st = _Streamer(tokenizer, eos_ids, on_text, stop)
+    s64 = _seed64(seed)
+    t0 = time.time()
+
+    suffix = ids[reuse_len:] if reuse_len else ids
+    if reuse_len and (cache.lengths[0] != reuse_len or ctx_caches.lengths[0] != reuse_len):
+        raise ValueError(f"reused caches hold {cache.lengths[0]} / {ctx_caches.lengths[0]} tokens, "
+                         f"reuse_len={reuse_len}")
+
+    def feed(fused, pos):
+        drafter.update_context(fused, pos, ctx_caches)
+
+    logits, _ = model.prefill(suffix, cache, tap, on_chunk=feed)
+    pending = _pick(logits[0, -1], temperature, top_p, top_k, s64, 0xFFFFFFFF)
+    pen = _Penalizer(presence_penalty, frequency_penalty)
+    pen.add([pending])
+    index = None
+    if lookup_drafts:
+        from .lookup import NGramIndex
+        index = NGramIndex(min_n=4, max_n=5, max_draft=max(1, lookup_max_draft))
+        index.extend(list(ids) + [pending])
+
+    out_ids = [pending]
+    accept_lengths: list = []
+    target_forwards = 1
+    lookup_rounds = 0
+    rounds: dict = {}
+    mask_id = int(cfg.mask_token_id)
+    dev = model.device
+    st.update(out_ids)
+    r = 0
+    while len(out_ids) < max_new_tokens and pending not in eos_ids and not st.stopped:
+        lk = index.propose() if index is not None else []
+        cap = cap_ceiling if cap_controller is None else max(1, min(int(cap_controller.cap), cap_ceiling))
+        width = 1 + (len(lk) if lk else cap)
+        if cache.lengths[0] + width > cache.max_ctx or ctx_caches.lengths[0] + width + k > ctx_caches.max_ctx:
+            break
+        use_conf = confidence_threshold > 0.0 and drafter.confidence_head is not None
+        fast = not lk and temperature <= 0.0 and not use_conf and not pen.active
+        if fast:
+            rnd = rounds.get(cap)
+            if rnd is None:
+                rnd = rounds[cap] = _DSparkRound(target_model, drafter, cache, ctx_caches, cap)
+            rnd.pending.fill_(pending)
+            n, tok, draft = rnd.run(use_graph)
+        else:
+            q_logits = None
+            if lk:
+                lookup_rounds += 1
+                draft = list(lk)
+            else:
+                block = torch.tensor([[pending] + [mask_id] * (k - 1)], dtype=torch.int32, device=dev)
+                hb = drafter.block_hidden(block, ctx_caches)[:cap]
+                base = blockdraft.head_rows(drafter, hb, drafter.lm_head).view(1, cap, -1)
+                if temperature > 0.0:
+                    d_t, q_logits = drafter.sample_block_probs(base[0], pending, temperature, top_p, top_k,
+                                                               seed=s64, offset=r)
+                else:
+                    d_t = drafter.sample_block(base[0], pending)
+                draft = [int(x) for x in d_t.tolist()]
+                if use_conf:
+                    normed = ops.pack(hb, drafter.norm, cfg.rms_norm_eps).unpack()
+                    conf = torch.sigmoid(drafter.confidence_logits(normed, [pending] + draft[:-1])).tolist()
+                    surv, keep = 1.0, 0
+                    for i, c in enumerate(conf):
+                        surv *= c
+                        if surv < confidence_threshold:
+                            break
+                        keep = i + 1
+                    draft = draft[:max(keep, 1)]
+            L = len(draft)
+            vids = torch.tensor([[pending] + draft], dtype=torch.int32, device=dev)
+            v_logits, v_fused = model.forward(vids, cache, tap, advance=False)
+            v_logits = pen.apply(v_logits[0], draft)
+            n_t = torch.zeros(1, dtype=torch.int32, device=dev)
+            tok_t = torch.zeros(1, dtype=torch.int32, device=dev)
+            if temperature > 0.0:
+                ql = None if lk else q_logits[:L].reshape(1, L, V)
+                ops.accept_sample(v_logits.view(1, L + 1, V), ql, torch.tensor([draft], dtype=torch.int32, device=dev),
+                                  temperature, top_p, top_k, q_mul_inv_t=True, seed=s64, offset=r,
+                                  seq_lens=cache.seq_lens, n_out=n_t, token_out=tok_t)
+            else:
+                ops.accept_greedy(v_logits.view(1, L + 1, V), torch.tensor([draft], dtype=torch.int32, device=dev),
+                                  seq_lens=cache.seq_lens, n_out=n_t, token_out=tok_t)
+            drafter.update_context(v_fused[0], 0, ctx_caches, n_valid=n_t)
+            n, tok = int(n_t.item()), int(tok_t.item())
+            cache.note_lengths([cache.lengths[0] + n + 1])
+            ctx_caches.note_lengths([ctx_caches.lengths[0] + n + 1])
+        r += 1
+        committed = draft[:n] + [tok]
+        target_forwards += 1
+        accept_lengths.append(len(committed))
+        if cap_controller is not None and not lk:
+            cap_controller.update(n, len(draft))
+        appended = []
+        for t in committed:
+            out_ids.append(t)
+            appended.append(t)
+            if t in eos_ids:
+                break
+        pen.add(appended)
+        if index is not None:
+            index.extend(appended)
+        pending = out_ids[-1]
+        st.update(out_ids)
+        if verbose:
+            print(f"  round {len(accept_lengths):3d}: {'lookup' if lk else 'drafter'} drafted {len(draft)}, "
+                  f"accepted {n}, committed {len(committed)}")
+    st.flush()
+    secs = time.time() - t0
+    return GenResult(text=_final_text(tokenizer, st, out_ids, eos_ids), token_ids=out_ids, num_tokens=len(out_ids),
+                     num_rounds=len(accept_lengths), accept_lengths=accept_lengths, target_forwards=target_forwards,
+                     seconds=secs, finish_reason=_finish_reason(out_ids, max_new_tokens, pending, eos_ids, st),
+                     lookup_rounds=lookup_rounds)

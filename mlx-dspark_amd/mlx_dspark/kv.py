@@ -47,6 +47,16 @@ class LayerView:
         self.offset = self.offset - n
         return n
 
+    # drafter context-cache surface (src/mlx_dspark/model.py:48-80): append-only, trimmed only to
+    # roll back to a shared prefix; every layer holds the same positions
+    @property
+    def length(self) -> int:
+        return self.cache.lengths[0]
+
+    def trim_to(self, length: int) -> None:
+        if length < self.cache.lengths[0]:
+            self.cache.set_lengths([int(length)] * self.cache.B)
+
     @property
     def keys(self):
         return self.cache.k[self.layer]
@@ -109,6 +119,15 @@ class PagedKVCache(list):
     @property
     def offset(self) -> int:
         return self.lengths[0]
+
+    @property
+    def length(self) -> int:
+        return self.lengths[0]
+
+    def trim_to(self, length: int) -> None:
+        """Keep the first ``length`` positions of every row (K stays valid: roped at its
+        absolute position)."""
+        self.set_lengths([min(int(length), l) for l in self.lengths])
 
     def check_room(self, W: int) -> None:
         if max(self.lengths) + W > self.max_ctx:

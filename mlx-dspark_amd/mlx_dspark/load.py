@@ -109,6 +109,34 @@ def load_dflash(repo_or_path: str, *, quantize: bool = True, bits: int = 8, grou
     return synthetic.build_dflash(target_args, seed=seed, keep_mlx=keep_mlx)
 
 
+def load_drafter(repo_or_path: str = DEFAULT_DRAFTER, *, quantize: bool = True, bits: int = 8,
+                 group_size: int = 64, strict: bool = True, target_args: TargetArgs | None = None, seed: int = 2,
+                 keep_mlx: bool = False, **shape):
+    """(drafter, config) for a synthetic DSpark drafter (load.py:155-215); W8 by default.
+    ``shape`` overrides the builder's drafter knobs (num_hidden_layers, block_size, taps,
+    markov_rank, confidence)."""
+    if bits != 8 or group_size != 64 or not quantize:
+        raise ValueError("this engine runs W8 (group 64) drafters")
+    key = _synthetic_key(repo_or_path)
+    if not key.startswith("dspark-"):
+        raise ValueError(f"{repo_or_path!r} is not a DSpark drafter name")
+    tkey = key[len("dspark-"):]
+    if target_args is None:
+        if tkey not in synthetic.TARGETS:
+            raise ValueError(f"unknown synthetic target {tkey!r} for drafter {repo_or_path!r}")
+        target_args = TargetArgs(**synthetic.TARGETS[tkey])
+    return synthetic.build_dspark(target_args, seed=seed, keep_mlx=keep_mlx, **shape)
+
+
+def load_pair(model: str = DEFAULT_TARGET, *, drafter=None, kv_bits=None, keep_mlx: bool = False, max_ctx=None,
+              **drafter_shape):
+    """(target, tokenizer, DSpark drafter, cfg) (load.py:354-363)."""
+    target_name, drafter_name = resolve(model, mode="dspark", drafter=drafter)
+    target, tok = load_target(target_name, require_tap=True, kv_bits=kv_bits, keep_mlx=keep_mlx, max_ctx=max_ctx)
+    d, cfg = load_drafter(drafter_name, target_args=target.model.args, keep_mlx=keep_mlx, **drafter_shape)
+    return target, tok, d, cfg
+
+
 def load_dflash_pair(model: str = "synthetic/qwen3-8b", *, drafter=None, kv_bits=None, keep_mlx: bool = False,
                      max_ctx=None):
     """(target, tokenizer, DFlash drafter, cfg), drafter bound to the target (load.py:366-373)."""

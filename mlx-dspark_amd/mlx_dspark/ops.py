@@ -348,3 +348,42 @@ def sample_rows(logits: torch.Tensor, temperature: float, top_p: float = 1.0, to
 
 def lens_add(lens: torch.Tensor, n: torch.Tensor | None, add: int) -> None:
     call("dsk_lens_add", ptr(lens), ptr(n), lens.numel(), int(add), stream_ptr())
+
+
+# ----------------------------------------------------------------------------- DSpark Markov head
+def markov_block(base_logits: torch.Tensor, first_prev: torch.Tensor, w1: W8Table, w2: W8Weight, *,
+                 temperature: float = 0.0, top_p: float = 1.0, top_k: int = 0, seed: int = 0, offset: int = 0,
+                 tok_out: torch.Tensor | None = None, q_logits_out: torch.Tensor | None = None):
+    """Sequential block sampling with the rank-R Markov head (see markov.hip).
+
+    base_logits f32 [B, cap, V] (or [cap, V]), first_prev int32 [B] on device. Greedy
+    (temperature 0) -> tokens int32 [B, cap]; sampled -> (tokens, q_logits [B, cap, V]), the
+    step logits whose truncated softmax at 1/T each token was drawn from."""
+    if base_logits.dim() == 2:
+        base_logits = base_logits.unsqueeze(0)
+    B, cap, V = base_logits.shape
+    if base_logits.dtype != torch.float32 or base_logits.stride(2) != 1 or base_logits.stride(1) != base_logits.stride(2) * V \
+            or base_logits.stride(0) != cap * V:
+        base_logits = base_logits.float().contiguous()
+    dev = base_logits.device
+    first_prev = first_prev.reshape(-1)
+    if first_prev.dtype != torch.int32:
+        first_prev = first_prev.to(torch.int32)
+    tok_out = torch.empty((B, cap), dtype=torch.int32, device=dev) if tok_out is None else tok_out
+    sampled = temperature > 0
+    if sampled and q_logits_out is None:
+        q_logits_out = torch.empty((B, cap, V), dtype=torch.float32, device=dev)
+    R = w1.q.shape[1]
+    ws = Workspace.get(dev)
+    buf = ws.reserve("markov", _hip.lib.dsk_markov_ws_bytes(B, V, int(sampled)))
+    call("dsk_markov_block", ptr(base_logits), V, B, cap, V, R, ptr(first_prev), ptr(w1.q), ptr(w1.s), ptr(w1.b),
+         ptr(w2.wt), ptr(w2.sb), float(temperature), float(top_p), int(top_k or 0), int(seed) & ((1 << 64) - 1),
+         int(offset) & 0xFFFFFFFF, ptr(tok_out), ptr(q_logits_out if sampled else None), ptr(buf), buf.numel(),
+         stream_ptr())
+    return (tok_out, q_logits_out) if sampled else tok_out
+
+
+def logits_penalize(logits: torch.Tensor, row_ptr: torch.Tensor, ids: torch.Tensor, vals: torch.Tensor) -> None:
+    """logits[r, ids[j]] -= vals[j] for j in [row_ptr[r], row_ptr[r+1]) (CSR rows, in place)."""
+    R = logits.shape[0]
+    call("dsk_logits_penalize", ptr(logits), logits.stride(0), R, ptr(row_ptr), ptr(ids), ptr(vals), stream_ptr())

@@ -114,6 +114,64 @@ def evenly_spaced_layers(n_target_layers: int, n: int) -> list[int]:
     return [int(round(lo + i * (hi - lo) / (n - 1))) for i in range(n)]
 
 
+def build_dspark(target_args: TargetArgs, seed: int = 2, device="cuda", keep_mlx: bool = False,
+                 num_hidden_layers: int = 1, block_size: int = 7, taps=None, markov_rank: int = 256,
+                 confidence: bool = True, mask_token_id: int | None = None):
+    """A qwen3-family DSpark drafter shaped like the target (same width, heads and MLP), with
+    its own embedding and head, a rank-``markov_rank`` Markov head and a confidence head,
+    conditioned on the target layers ``taps`` (default: 3 spread over the target)."""
+    from .config import DSparkConfig
+    from .model import ConfidenceHead, DSparkDrafter, MarkovHead
+
+    a = target_args
+    device = torch.device(device)
+    L = a.num_hidden_layers
+    taps = list(taps) if taps is not None else [1, L // 2, L - 1] if L >= 3 else list(range(L))
+    cfg = DSparkConfig(
+        family="qwen3", hidden_size=a.hidden_size, vocab_size=a.vocab_size, num_hidden_layers=num_hidden_layers,
+        intermediate_size=a.intermediate_size, rms_norm_eps=a.rms_norm_eps,
+        num_attention_heads=a.num_attention_heads, num_key_value_heads=a.num_key_value_heads,
+        head_dim=a.head_dim, attention_k_eq_v=False, rope_theta=a.rope_theta, rope_type="default",
+        block_size=block_size, mask_token_id=a.vocab_size - 2 if mask_token_id is None else mask_token_id,
+        target_layer_ids=taps, num_target_layers=L, markov_rank=markov_rank,
+        enable_confidence_head=confidence, confidence_head_with_markov=markov_rank > 0,
+        final_logit_softcapping=None, mlp_activation="silu", norm_style="qwen", use_v_norm=False)
+    H, I = a.hidden_size, a.intermediate_size
+    nq, nkv, hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
+    layers = []
+    for l in range(num_hidden_layers):
+        p = f"dspark.layers.{l}."
+        layers.append(LayerWeights(
+            qkv=w8(a.n_qkv, H, seed, p + "qkv", device, keep_mlx),
+            o=w8(H, nq * hd, seed, p + "o", device, keep_mlx),
+            gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx, paired=True),
+            down=w8(H, I, seed, p + "down", device, keep_mlx),
+            in_norm=ones(H, device), post_norm=ones(H, device),
+            q_norm=qk_norm(hd, device), k_norm=qk_norm(hd, device)))
+    markov = None
+    if markov_rank > 0:
+        w1 = w8_table(a.vocab_size, markov_rank, seed, "dspark.markov_w1", device)
+        w2 = w8(a.vocab_size, markov_rank, seed, "dspark.markov_w2", device, keep_mlx)
+        markov = MarkovHead(w1, w2)
+    conf = None
+    if confidence:
+        K = H + (markov_rank if markov_rank > 0 else 0)
+        w = randn((1, K), seed, "dspark.confidence", device)
+        w = torch.cat([w, torch.zeros((15, K), device=device)])
+        q, s_, b_ = W8Weight.quantize_mlx(w)
+        cw = W8Weight.from_mlx(q, s_, b_)
+        if keep_mlx:
+            cw.mlx = (q, s_, b_)
+        conf = ConfidenceHead(cw, 0.5)
+    d = DSparkDrafter(cfg, embed=w8_table(a.vocab_size, H, seed, "dspark.embed_tokens", device),
+                      fc=w8(H, len(taps) * H, seed, "dspark.fc", device, keep_mlx), hidden_norm=ones(H, device),
+                      layers=layers, norm=ones(H, device),
+                      lm_head=w8(a.vocab_size, H, seed, "dspark.lm_head", device, keep_mlx),
+                      markov=markov, confidence=conf)
+    torch.cuda.synchronize(device)
+    return d, cfg
+
+
 def build_dflash(target_args: TargetArgs, seed: int = 1, device="cuda", keep_mlx: bool = False,
                  num_hidden_layers: int = 2, block_size: int = 16, n_taps: int = 5,
                  mask_token_id: int | None = None):

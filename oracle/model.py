@@ -246,3 +246,125 @@ def greedy_decode(target: OracleTarget, prompt, n_new: int):
         out.append(t)
         row = target.forward([t])[0][-1]
     return out, margins
+
+
+class OracleDSpark:
+    """CPU DSpark drafter, qwen3 family (src/mlx_dspark/model.py:83-320), built from a GPU
+    drafter created with keep_mlx=True.
+
+    Context rows: fused = RMSNorm(fc(target_hidden)); per layer K = rope(k_norm(k_proj(fused)),
+    ctx position), V = v_proj(fused), appended (model.py:113-128, :247-256). Block: embed ->
+    layers with attention over context ++ block, no mask, roped at block_offset + i (:130-193)
+    -> final RMSNorm. Heads: lm_head (:264-268), Markov block sampling (:270-281) with bf16
+    rounding points (logits, bias and their sum are bf16, as in a bf16 graph), confidence
+    logits (:311-320)."""
+
+    def __init__(self, drafter):
+        c = drafter.config
+        self.c = c
+        self.embed = deq_table(drafter.embed_tokens)
+        self.fc = deq(drafter.fc)
+        self.hidden_norm = drafter.hidden_norm.float().cpu()
+        self.norm = drafter.norm.float().cpu()
+        self.lm_head = deq(drafter.lm_head)
+        self.layers = [OracleLayer(L, c.num_attention_heads, c.num_key_value_heads, c.head_dim)
+                       for L in drafter.layers]
+        self.w1 = deq_table(drafter.markov_head.w1) if drafter.markov_head is not None else None
+        self.w2 = deq(drafter.markov_head.w2) if drafter.markov_head is not None else None
+        self.conf_w = deq(drafter.confidence_head.proj)[0] if drafter.confidence_head is not None else None
+        self.conf_b = drafter.confidence_head.bias if drafter.confidence_head is not None else 0.0
+        self.K = [torch.zeros(0, c.num_key_value_heads, c.head_dim) for _ in self.layers]
+        self.V = [torch.zeros(0, c.num_key_value_heads, c.head_dim) for _ in self.layers]
+
+    @property
+    def length(self) -> int:
+        return self.K[0].shape[0]
+
+    def update_context(self, target_hidden):
+        c = self.c
+        nkv, hd, eps = c.num_key_value_heads, c.head_dim, c.rms_norm_eps
+        th = torch.as_tensor(target_hidden).reshape(-1, self.fc.shape[1]).float()
+        S = th.shape[0]
+        fused = bf(rmsnorm(bf(th @ self.fc.T), self.hidden_norm, eps))
+        pos = torch.arange(self.length, self.length + S)
+        nq = c.num_attention_heads
+        for l, L in enumerate(self.layers):
+            kv = bf(fused @ L.wq[nq * hd:].T)
+            k = kv[:, : nkv * hd].view(S, nkv, hd)
+            v = kv[:, nkv * hd:].view(S, nkv, hd)
+            k = bf(rope(bf(rmsnorm(k, L.k_norm, eps)).transpose(0, 1), pos, c.rope_theta).transpose(0, 1))
+            self.K[l] = torch.cat([self.K[l], k])
+            self.V[l] = torch.cat([self.V[l], v])
+
+    def block_hidden(self, block_ids):
+        """normed block hidden [k, H]"""
+        c = self.c
+        nq, nkv, hd, eps = c.num_attention_heads, c.num_key_value_heads, c.head_dim, c.rms_norm_eps
+        ids = torch.as_tensor(block_ids).reshape(-1).long()
+        k = ids.numel()
+        h = bf(self.embed[ids])
+        pos = torch.arange(self.length, self.length + k)
+        for l, L in enumerate(self.layers):
+            x = bf(rmsnorm(h, L.in_norm, eps))
+            qkv = bf(x @ L.wq.T)
+            q = qkv[:, : nq * hd].view(k, nq, hd)
+            kb = qkv[:, nq * hd:(nq + nkv) * hd].view(k, nkv, hd)
+            vb = qkv[:, (nq + nkv) * hd:].view(k, nkv, hd)
+            q = bf(rope(bf(rmsnorm(q, L.q_norm, eps)).transpose(0, 1), pos, c.rope_theta).transpose(0, 1))
+            kb = bf(rope(bf(rmsnorm(kb, L.k_norm, eps)).transpose(0, 1), pos, c.rope_theta).transpose(0, 1))
+            o = bf(sdpa(q, torch.cat([self.K[l], kb]), torch.cat([self.V[l], vb]), c.scaling))
+            h = bf(h + o.reshape(k, -1) @ L.wo.T)
+            x = bf(rmsnorm(h, L.post_norm, eps))
+            gu = bf(x @ L.wgu.T)
+            I = gu.shape[1] // 2
+            h = bf(h + bf(bf(gu[:, :I] * torch.sigmoid(gu[:, :I])) * gu[:, I:]) @ L.wd.T)
+        return bf(rmsnorm(h, self.norm, eps))
+
+    def base_logits(self, block_ids, cap):
+        return self.block_hidden(block_ids)[:cap] @ self.lm_head.T
+
+    def step_logits(self, base_row, prev):
+        """bf16(bf16(base) + bf16(w2 . bf16(w1[prev])))"""
+        bias = bf(self.w2.double() @ bf(self.w1[int(prev)]).double())
+        return bf(bf(torch.as_tensor(base_row).float()) + bias.float())
+
+    def sample_block(self, base, first_prev):
+        """greedy Markov block: argmax (lowest index on ties) of step_logits, sequentially."""
+        toks, prev = [], int(first_prev)
+        for i in range(base.shape[0]):
+            row = self.step_logits(base[i], prev) if self.w1 is not None else bf(torch.as_tensor(base[i]).float())
+            t = int(torch.argmax(row))
+            toks.append(t)
+            prev = t
+        return toks
+
+    def confidence_logits(self, hidden_rows, prev_ids):
+        feats = torch.as_tensor(hidden_rows).float()
+        if self.w1 is not None:
+            feats = torch.cat([feats, bf(self.w1[torch.as_tensor(prev_ids).long()])], dim=-1)
+        return feats @ self.conf_w + self.conf_b
+
+
+def markov_sample_block(base, first_prev, step_bias):
+    """Sequential greedy Markov sampling with an arbitrary step_bias(prev) -> [V] (the control
+    flow of src/mlx_dspark/model.py:270-281 and batch_engine.py:414-428)."""
+    toks, prev = [], first_prev
+    for i in range(base.shape[0]):
+        t = int(torch.argmax(torch.as_tensor(base[i]) + step_bias(prev)))
+        toks.append(t)
+        prev = t
+    return toks
+
+
+def penalty_rows(counts: dict, presence: float, frequency: float, draft_prefix) -> list:
+    """Per-row {token: penalty} of a verify block (src/mlx_dspark/generate.py:202-228): base
+    completion counts, then each draft-prefix token adds frequency, plus presence the first
+    time it appears."""
+    base = {t: presence + frequency * c for t, c in counts.items()}
+    rows, seen = [base], dict(counts)
+    for d in draft_prefix:
+        r = dict(rows[-1])
+        r[d] = r.get(d, 0.0) + frequency + (presence if seen.get(d, 0) == 0 else 0.0)
+        seen[d] = seen.get(d, 0) + 1
+        rows.append(r)
+    return rows
