@@ -14,8 +14,9 @@ replay each. Printed (one JSON line):
                drafter almost never matches, so ~1 token per round: accept length is reported)
   verify_us    one verify forward (16 rows, 4096 context), graph-replayed, HIP events
   verify_roofline_frac  algorithmic bytes of that forward / verify_us / 8 TB/s
-  roofline     the W8 GEMM kernel (the dominant kernel): algorithmic bytes per launch over
-               its average launch duration, timed per launch with HIP events
+  roofline     the dominant kernel, the W8 GEMM at the gate_up shape (24576 x 4096, SwiGLU
+               epilogue): algorithmic bytes per launch over its in-graph average launch time
+               (36 launches, one per layer's weights, HIP events on the launch stream)
   cpu_baseline the CPU oracle (torch, float32) on a bounded sample: one decoder layer and the
                vocabulary head of the verify step, scaled to a whole round
 """
@@ -35,6 +36,9 @@ sys.path.insert(0, str(REPO / "mlx-dspark_amd"))
 sys.path.insert(0, str(REPO))
 
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per gate_up launch from the FETCH_SIZE / WRITE_SIZE counter runs (kept in
+# profiles/), scaled by the same counters read on a copy of known size; None until measured
+TRAFFIC_GATE_UP = None
 
 
 def log(*a):
@@ -46,11 +50,13 @@ def kv_bytes_per_token(args, kv_bits) -> int:
     return 2 * per_head * args.num_key_value_heads * args.num_hidden_layers
 
 
-def gemm_roofline(model, M: int, reps_per_shape: int | None = None):
-    """Average launch duration of the W8 GEMM kernel at every verify-step shape, with the
+def gemm_roofline(model, M: int, reps: int = 10):
+    """In-graph average launch duration of the W8 GEMM at every verify-step shape, with the
     epilogue the forward uses (split-K partials for qkv / o / down, fused SwiGLU for gate_up,
-    f32 logits for the head), each launch bracketed by its own pair of HIP events on the launch
-    stream, weights rotating through the 36 layers so every launch streams its weights from HBM."""
+    f32 logits for the head). One CUDA graph per shape holds one launch per layer, each on
+    that layer's weights (so every launch streams its weights from HBM), replayed `reps` times
+    between two HIP events recorded on the launch stream; the average includes the ~1.5 us
+    dispatch gap between back-to-back graph kernels, which a kernel trace does not count."""
     import torch
     from mlx_dspark import ops
 
@@ -60,11 +66,6 @@ def gemm_roofline(model, M: int, reps_per_shape: int | None = None):
               "gate_up": ([L.gate_up for L in model.layers], SW), "down": ([L.down for L in model.layers], P),
               "lm_head": ([model.lm_head], ops.DSK_EPI_STORE)}
     res = {}
-    tot_bytes = tot_us = 0.0
-    tot_launch = 0
-    per_step = {"qkv": len(model.layers), "o": len(model.layers), "gate_up": len(model.layers),
-                "down": len(model.layers), "lm_head": 1}
-    filler = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
     for name, (ws, epi) in shapes.items():
         K = ws[0].K
@@ -73,23 +74,39 @@ def gemm_roofline(model, M: int, reps_per_shape: int | None = None):
         if epi == ops.DSK_EPI_STORE:
             out = torch.empty(M, ws[0].N, device=dev, dtype=torch.float32)
         y = ops.w8_gemm(x, ws[0], epi=epi, out=out)
-        n = reps_per_shape or max(len(ws), 8)
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
         torch.cuda.synchronize()
-        filler.zero_()                                            # keeps the GPU busy while we enqueue
-        for i in range(n):
-            ev[i][0].record(stream)
-            ops.w8_gemm(x, ws[i % len(ws)], epi=epi, out=y)
-            ev[i][1].record(stream)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for w in ws:
+                ops.w8_gemm(x, w, epi=epi, out=y)
+        for _ in range(2):
+            g.replay()
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        us = statistics.mean(s.elapsed_time(e) * 1e3 for s, e in ev)
-        by = ws[0].N * ws[0].K * 1.0625
-        res[name] = {"us": round(us, 2), "bytes": int(by), "GBs": round(by / us / 1e3, 1)}
-        tot_bytes += by * per_step[name]
-        tot_us += us * per_step[name]
-        tot_launch += per_step[name]
-    del filler
-    return res, tot_bytes / tot_launch, tot_us / tot_launch
+        s_ev.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e_ev.record(stream)
+        torch.cuda.synchronize()
+        us = s_ev.elapsed_time(e_ev) * 1e3 / (reps * len(ws))
+        # algorithmic bytes: weights (q + scale/bias) + activation in + output out
+        out_b = {P: 4 * ops.gemm_splits(M, ws[0].N, K), SW: 1, ops.DSK_EPI_STORE: 4}[epi] * M * ws[0].N
+        by = ws[0].N * K * 1.0625 + M * K * 2 + out_b
+        res[name] = {"us": round(us, 2), "bytes": int(by), "GBs": round(by / us / 1e3, 1), "launches": len(ws)}
+        del g
+    return res
+
+
+def copy_calibration(nbytes: int = 256 << 20) -> None:
+    """A plain device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
 
 
 def cpu_baseline(tgt_args, dev_model_seed: int, ctx: int, W: int, mean_accept: float, budget_s: float = 12.0):
@@ -166,6 +183,8 @@ def main(argv=None) -> int:
     ap.add_argument("--target", default="qwen3-8b")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--verify-reps", type=int, default=50)
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="build the target, time the W8 GEMM shapes and a 256 MiB copy only (counter runs)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this engine has no multi-GPU path (run with --gpus 1)",
@@ -188,6 +207,11 @@ def main(argv=None) -> int:
     drafter.bind(model)
     log(f"built {args.target} W8 target ({model.weight_bytes / 1e9:.2f} GB) + DFlash drafter in "
         f"{time.time() - t_build:.1f} s")
+    if args.roofline_only:
+        shapes = gemm_roofline(model, args.block)
+        copy_calibration()
+        print(json.dumps({"roofline_only": shapes}), flush=True)
+        return 0
     tok = SyntheticTokenizer(model.args.vocab_size)
     target = Target(model, tok, kv_bits=kv_bits)
     cap = args.block - 1
@@ -247,9 +271,10 @@ def main(argv=None) -> int:
     log(f"verify step: {verify_us:.1f} us for {alg_bytes / 1e9:.3f} GB algorithmic "
         f"-> {alg_bytes / verify_us / 1e3:.0f} GB/s ({verify_frac * 100:.1f}% of HBM roofline)")
 
-    # ---- dominant kernel: the W8 GEMM
-    shapes, bytes_per_launch, us_per_launch = gemm_roofline(model, W)
-    achieved = bytes_per_launch / us_per_launch / 1e3
+    # ---- dominant kernel: the W8 GEMM, gate_up shape (the largest share of the verify step)
+    shapes = gemm_roofline(model, W)
+    dom = shapes["gate_up"]
+    achieved = dom["bytes"] / dom["us"] / 1e3
     log(f"W8 GEMM per shape: {json.dumps(shapes)}")
 
     cpu = None
@@ -273,11 +298,10 @@ def main(argv=None) -> int:
         "verify_us": round(verify_us, 1),
         "verify_alg_bytes": int(alg_bytes),
         "verify_roofline_frac": round(verify_frac, 4),
-        "roofline": {"kernel": "w8_gemm_kernel (W8 skinny GEMM, M=16)", "bound": "hbm",
-                     "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                     "bytes_per_launch": int(bytes_per_launch), "us_per_launch": round(us_per_launch, 2),
-                     "per_shape": shapes},
+        "roofline": {"kernel": "w8_gemm_kernel<1, 4, 2, 4, 1> (W8 GEMM, gate_up 24576x4096, M=16, SwiGLU)",
+                     "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_GATE_UP,
+                     "bytes_per_launch": dom["bytes"], "us_per_launch": dom["us"], "per_shape": shapes},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -163,8 +163,10 @@ int dsk_qkv_rope_append(const void* qkv, int qkv_splits, int B, int W, int nq, i
  * max_ctx bounds seq_lens[b] + W (sizes the split grid so the launch is graph-stable).
  * softcap > 0: scores = tanh(scores / softcap) * softcap before the mask.
  * out_packed != 0 writes the output in the packed activation layout (the o-projection's x).
- * workspace: dsk_attn_ws_bytes(...) bytes for the split partials (the splits are combined by
- * a second kernel on the same stream; no state is kept between calls). */
+ * workspace: dsk_attn_ws_bytes(...) bytes for the split partials (bf16 o / l per split and
+ * fp32 (m, l); the splits are combined by a second kernel on the same stream; no state is
+ * kept between calls). Every block_table entry of a row must name a valid page: a split
+ * reads its whole key range through the table before it knows the row's length. */
 size_t dsk_attn_ws_bytes(int B, int W, int nq, int hd, int max_ctx);
 int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, int hd, float scale,
                   int causal, int window, float softcap, const int32_t* seq_lens,
@@ -172,6 +174,24 @@ int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, int hd, floa
                   int kv_dtype, const void* k_pool, const void* v_pool,
                   const uint32_t* k_sb, const uint32_t* v_sb, uint16_t* out, int out_packed,
                   void* workspace, size_t ws_bytes, dsk_stream_t stream);
+
+/* dsk_qkv_rope_append followed by dsk_attention in one kernel (plus the split combine):
+ * from the qkv projection (bf16 or fp32 split-K slices, as for dsk_qkv_rope_append, with
+ * pos_offset 0) each workgroup forms its queries (q RMSNorm, RoPE at seq_lens[b] + i); the
+ * workgroup whose key range holds the W new tokens normalises and rotates their K, appends
+ * K/V to the pool and attends to the appended values directly. Same masks, output and
+ * workspace (dsk_attn_ws_bytes) as dsk_attention; W <= 64; q_norm/k_norm may be NULL and,
+ * when given, are 16-byte aligned. Replaces the attention block of a decoder layer between
+ * the qkv and o projections (mlx_lm Qwen3 attention reached from
+ * src/mlx_dspark/target.py:107-124; DSparkAttention, src/mlx_dspark/model.py:130-155;
+ * DFlash attention, src/mlx_dspark/dflash_model.py:100-133). */
+int dsk_qkv_attention(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
+                      const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                      const float* inv_freq, float scale, int causal, int window, float softcap,
+                      const int32_t* seq_lens, int max_ctx, const int32_t* block_table,
+                      int max_pages, int page, int kv_dtype, void* k_pool, void* v_pool,
+                      uint32_t* k_sb, uint32_t* v_sb, uint16_t* out, int out_packed,
+                      void* workspace, size_t ws_bytes, dsk_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------
  * Acceptance.

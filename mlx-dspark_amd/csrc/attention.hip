@@ -4,7 +4,8 @@
 //   bf16: kv[((p * nkv + h) * page + t) * hd + d]
 //   u8  : kv[((p * nkv + h) * page + t) * hd + d] and sb[((p * nkv + h) * page + t) * (hd/64) + g]
 //         (u32 = bf16 scale | bf16 bias << 16; affine group 64 along head_dim).
-// A row's logical token j lives in physical page block_table[b * max_pages + j / page].
+// A row's logical token j lives in physical page block_table[b * max_pages + j / page]; every
+// entry of the table must name a valid page (the kernels read whole splits through it).
 //
 // Attention is computed transposed so no register transposes are needed:
 //   S^T[key][q] = K . Q^T  (A = K tile from LDS, B = Q from registers), then
@@ -12,37 +13,144 @@
 //   the lane that holds S^T[4c + r][q] for two 16-key halves feeds exactly those 8 keys as
 //   its B items, and V^T is read from LDS with the same key order).
 // Every lane therefore owns one query column, which makes the online softmax lane-local.
+//
+// The fused entry (dsk_qkv_attention) starts from the qkv projection itself: each workgroup
+// forms its own queries (sum of the split-K partial slices, RMSNorm, RoPE) while its K/V loads
+// are in flight, and the workgroup whose key range holds the new tokens also normalises,
+// rotates and quantises their K/V, appends them to the pool and uses them straight from LDS.
 #include "common.h"
 
 namespace dsk {
 
-// ----------------------------------------------------------------------------- append
-__device__ __forceinline__ void kv_quant_store(float v0, float v1, int lane, int hd, uint8_t* qdst,
-                                               uint32_t* sbdst) {
-  // hd values spread 2 per lane over 64 lanes (hd = 128) or 4 per lane (hd = 256, called twice);
-  // groups of 64 = 32 consecutive lanes.
-  float lo = fminf(v0, v1), hi = fmaxf(v0, v1);
-  for (int o = 1; o < 32; o <<= 1) {
+// ----------------------------------------------------------------------------- row helpers
+// RoPE angle in fp32 as the reference computes it, reduced to [-1/2, 1/2) revolutions for
+// v_sin_f32 / v_cos_f32 (the reduction error is below the angle's own rounding).
+__device__ __forceinline__ void rope_sincos(int pos, float inv_freq, float& sn, float& cs) {
+  const float ang = (float)pos * inv_freq;
+  float rev = ang * 0.15915494309189535f;
+  rev -= rintf(rev);
+  sn = __builtin_amdgcn_sinf(rev);
+  cs = __builtin_amdgcn_cosf(rev);
+}
+
+// One head row of HD dims spread over L consecutive lanes (L = 64: a wave; L = 16: a quarter
+// wave), PER = HD / L consecutive dims per lane starting at dim PER * (lane % L).
+// Sum of the projection's split-K slices in slice order, rounded to bf16.
+template <int PER>
+__device__ __forceinline__ void load_proj_row(const void* qkv, int splits, int64_t slice, int64_t off, int sub,
+                                              float (&v)[PER]) {
+  if (splits == 0) {
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(qkv) + off + (int64_t)sub * PER;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) v[e] = bf16_to_f32(src[e]);
+    return;
+  }
+  const float* src = reinterpret_cast<const float*>(qkv) + off + (int64_t)sub * PER;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) v[e] = 0.0f;
+  // two slices' loads in flight at a time, summed in slice order
+  for (int sp = 0; sp < splits; sp += 2) {
+    float t[2][PER];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) t[u][e] = sp + u < splits ? src[(sp + u) * slice + e] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int e = 0; e < PER; ++e)
+        if (sp + u < splits) v[e] += t[u][e];
+  }
+#pragma unroll
+  for (int e = 0; e < PER; ++e) v[e] = round_bf16(v[e]);
+}
+
+// sum over the L lanes of a row (L a power of two, rows aligned to L lanes)
+template <int L>
+__device__ __forceinline__ float row_sum(float x) {
+#pragma unroll
+  for (int o = 1; o < L; o <<= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+// per-head RMSNorm (nw != NULL) and rotate-half RoPE (rope) of one row held as above
+template <int HD, int L>
+__device__ __forceinline__ void norm_rope_row(float (&v)[HD / L], int sub, const uint16_t* nw, float eps, bool rope,
+                                              const float* inv_freq, int pos) {
+  constexpr int PER = HD / L;
+  if (nw) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) ss += v[e] * v[e];
+    ss = row_sum<L>(ss);
+    const float r = rsqrtf(ss / (float)HD + eps);
+#pragma unroll
+    for (int e = 0; e < PER; ++e) v[e] = round_bf16((v[e] * r) * bf16_to_f32(nw[sub * PER + e]));
+  }
+  if (rope) {
+    // dim d pairs with d + HD/2, which sits L/2 lanes away
+    const bool first_half = sub < L / 2;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const float partner = __shfl_xor(v[e], L / 2, 64);
+      const int d = sub * PER + e;
+      float sn, cs;
+      rope_sincos(pos, inv_freq[first_half ? d : d - HD / 2], sn, cs);
+      const float x1 = first_half ? v[e] : partner, x2 = first_half ? partner : v[e];
+      v[e] = round_bf16(first_half ? x1 * cs - x2 * sn : x2 * cs + x1 * sn);
+    }
+  }
+}
+
+// Store one K or V row at pool token `tok` (bf16, or 8-bit affine group 64 with its scale and
+// bias) and leave in v the values attention reads back for it.
+template <int HD, int L>
+__device__ __forceinline__ void kv_store_row(float (&v)[HD / L], int sub, int kv_dtype, void* pool, uint32_t* sbp,
+                                             int64_t tok) {
+  constexpr int PER = HD / L;
+  if (kv_dtype == DSK_KV_BF16) {
+    uint16_t* dst = reinterpret_cast<uint16_t*>(pool) + tok * HD + sub * PER;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) dst[e] = f32_to_bf16(v[e]);
+    return;
+  }
+  constexpr int GL = 64 / PER;  // lanes per group of 64 dims
+  float lo = v[0], hi = v[0];
+#pragma unroll
+  for (int e = 1; e < PER; ++e) {
+    lo = fminf(lo, v[e]);
+    hi = fmaxf(hi, v[e]);
+  }
+#pragma unroll
+  for (int o = 1; o < GL; o <<= 1) {
     lo = fminf(lo, __shfl_xor(lo, o, 64));
     hi = fmaxf(hi, __shfl_xor(hi, o, 64));
   }
-  float s = (hi - lo) / 255.0f;
-  uint16_t s16 = f32_to_bf16(s);
+  uint16_t s16 = f32_to_bf16((hi - lo) / 255.0f);
   float sf = bf16_to_f32(s16);
   if (!(sf > 0.0f)) {
     s16 = 0x3f80;
     sf = 1.0f;
   }
-  uint16_t b16 = f32_to_bf16(lo);
-  float bf = bf16_to_f32(b16);
-  float q0 = fminf(fmaxf(rintf((v0 - bf) / sf), 0.0f), 255.0f);
-  float q1 = fminf(fmaxf(rintf((v1 - bf) / sf), 0.0f), 255.0f);
-  qdst[2 * lane] = (uint8_t)(int)q0;
-  qdst[2 * lane + 1] = (uint8_t)(int)q1;
-  if ((lane & 31) == 0) sbdst[lane >> 5] = (uint32_t)s16 | ((uint32_t)b16 << 16);
-  (void)hd;
+  const uint16_t b16 = f32_to_bf16(lo);
+  const float bf = bf16_to_f32(b16);
+  uint8_t* qd = reinterpret_cast<uint8_t*>(pool) + tok * HD + sub * PER;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const float q = fminf(fmaxf(rintf((v[e] - bf) / sf), 0.0f), 255.0f);
+    qd[e] = (uint8_t)(int)q;
+    v[e] = round_bf16(fmaf(sf, q, bf));
+  }
+  if ((sub % GL) == 0) sbp[tok * (HD / 64) + (sub * PER) / 64] = (uint32_t)s16 | ((uint32_t)b16 << 16);
 }
 
+__device__ __forceinline__ int64_t pool_token(const int32_t* block_table, int max_pages, int page, int nkv, int b,
+                                              int kvh, int j) {
+  const int pg = block_table[(int64_t)b * max_pages + j / page];
+  return ((int64_t)pg * nkv + kvh) * page + (j % page);
+}
+
+// ----------------------------------------------------------------------------- append
 // One wave per (token row, head): lane holds dims [PER*lane, PER*lane + PER) (PER = HD/64).
 template <int HD>
 __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
@@ -51,7 +159,7 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
     const int32_t* __restrict__ seq_lens, int pos_offset, const int32_t* __restrict__ block_table, int max_pages,
     int page, int kv_dtype, void* __restrict__ k_pool, void* __restrict__ v_pool, uint32_t* __restrict__ k_sb,
     uint32_t* __restrict__ v_sb, uint16_t* __restrict__ q_out) {
-  constexpr int PER = HD / 64;  // values per lane
+  constexpr int PER = HD / 64;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int nheads = nq + 2 * nkv;
   const int task = blockIdx.x * 4 + wv;
@@ -60,63 +168,9 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
   const int b = row / W, i = row % W;
   const int pos = seq_lens[b] + i + pos_offset;
   float v[PER];
-  if (qkv_splits == 0) {
-    const uint16_t* src = reinterpret_cast<const uint16_t*>(qkv) + (int64_t)row * nheads * HD + (int64_t)head * HD;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) v[e] = bf16_to_f32(src[lane * PER + e]);
-  } else {
-    // fp32 partial sums [splits][B*W][nheads*HD], summed in split order, rounded to bf16
-    // (the projection's output dtype)
-    const int64_t slice = (int64_t)B * W * nheads * HD;
-    const float* src = reinterpret_cast<const float*>(qkv) + (int64_t)row * nheads * HD + (int64_t)head * HD;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) v[e] = 0.0f;
-    // four slices' loads in flight at a time, summed in slice order
-    for (int sp = 0; sp < qkv_splits; sp += 4) {
-      float t[4][PER];
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int e = 0; e < PER; ++e) t[u][e] = sp + u < qkv_splits ? src[(sp + u) * slice + lane * PER + e] : 0.0f;
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int e = 0; e < PER; ++e)
-          if (sp + u < qkv_splits) v[e] += t[u][e];
-    }
-#pragma unroll
-    for (int e = 0; e < PER; ++e) v[e] = round_bf16(v[e]);
-  }
-
+  load_proj_row<PER>(qkv, qkv_splits, (int64_t)B * W * nheads * HD, ((int64_t)row * nheads + head) * HD, lane, v);
   const bool is_q = head < nq, is_k = !is_q && head < nq + nkv;
-  const uint16_t* nw = is_q ? q_norm : (is_k ? k_norm : nullptr);
-  if (nw) {
-    float ss = 0.0f;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) ss += v[e] * v[e];
-    ss = wave_sum(ss);
-    const float r = rsqrtf(ss / (float)HD + eps);
-#pragma unroll
-    for (int e = 0; e < PER; ++e) v[e] = round_bf16((v[e] * r) * bf16_to_f32(nw[lane * PER + e]));
-  }
-  if (is_q || is_k) {
-    // rotate-half RoPE: dim d pairs with d + HD/2, which sits 32 lanes away
-    const bool first_half = lane < 32;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      const float partner = __shfl_xor(v[e], 32, 64);
-      const int d = lane * PER + e;
-      const int dd = first_half ? d : d - HD / 2;
-      // angle in fp32 as the reference computes it, reduced to [-1/2, 1/2) revolutions for
-      // v_sin_f32 / v_cos_f32 (the reduction error is below the angle's own rounding)
-      const float ang = (float)pos * inv_freq[dd];
-      float rev = ang * 0.15915494309189535f;
-      rev -= rintf(rev);
-      const float sn = __builtin_amdgcn_sinf(rev), cs = __builtin_amdgcn_cosf(rev);
-      const float x1 = first_half ? v[e] : partner, x2 = first_half ? partner : v[e];
-      v[e] = round_bf16(first_half ? x1 * cs - x2 * sn : x2 * cs + x1 * sn);
-    }
-  }
+  norm_rope_row<HD, 64>(v, lane, is_q ? q_norm : (is_k ? k_norm : nullptr), eps, is_q || is_k, inv_freq, pos);
   if (is_q) {
     uint16_t* dst = q_out + (int64_t)row * nq * HD + (int64_t)head * HD;
 #pragma unroll
@@ -125,84 +179,51 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
   }
   const int h = is_k ? head - nq : head - nq - nkv;
   if (pos < 0 || pos >= max_pages * page) return;  // beyond the row's block table: dropped
-  const int pg = block_table[(int64_t)b * max_pages + pos / page];
-  const int slot = pos % page;
-  const int64_t tok = ((int64_t)pg * nkv + h) * page + slot;
-  if (kv_dtype == DSK_KV_BF16) {
-    uint16_t* dst = reinterpret_cast<uint16_t*>(is_k ? k_pool : v_pool) + tok * HD;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) dst[lane * PER + e] = f32_to_bf16(v[e]);
-  } else {
-    uint8_t* qd = reinterpret_cast<uint8_t*>(is_k ? k_pool : v_pool) + tok * HD;
-    uint32_t* sd = (is_k ? k_sb : v_sb) + tok * (HD / 64);
-    if (PER == 2) {
-      kv_quant_store(v[0], v[1], lane, HD, qd, sd);
-    } else {
-      // HD = 256: lane holds 4 consecutive dims; group = 16 lanes. Reuse the 2-wide path on
-      // a regrouped view: dims (4l, 4l+1) and (4l+2, 4l+3) both belong to group l / 16.
-      float lo = fminf(fminf(v[0], v[1]), fminf(v[2 % PER], v[3 % PER]));
-      float hi = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2 % PER], v[3 % PER]));
-      for (int o = 1; o < 16; o <<= 1) {
-        lo = fminf(lo, __shfl_xor(lo, o, 64));
-        hi = fmaxf(hi, __shfl_xor(hi, o, 64));
-      }
-      float s = (hi - lo) / 255.0f;
-      uint16_t s16 = f32_to_bf16(s);
-      float sf = bf16_to_f32(s16);
-      if (!(sf > 0.0f)) {
-        s16 = 0x3f80;
-        sf = 1.0f;
-      }
-      uint16_t b16 = f32_to_bf16(lo);
-      float bf = bf16_to_f32(b16);
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        float q = fminf(fmaxf(rintf((v[e] - bf) / sf), 0.0f), 255.0f);
-        qd[lane * PER + e] = (uint8_t)(int)q;
-      }
-      if ((lane & 15) == 0) sd[lane >> 4] = (uint32_t)s16 | ((uint32_t)b16 << 16);
-    }
-  }
+  const int64_t tok = pool_token(block_table, max_pages, page, nkv, b, h, pos);
+  kv_store_row<HD, 64>(v, lane, kv_dtype, is_k ? k_pool : v_pool, is_k ? k_sb : v_sb, tok);
 }
 
 // ----------------------------------------------------------------------------- attention
 struct AttnArgs {
-  const uint16_t* q;
+  const uint16_t* q;  // roped queries [B*W][nq*HD] (dsk_attention)
+  const void* qkv;    // the qkv projection (dsk_qkv_attention), bf16 or fp32 split-K slices
+  int qkv_splits;
+  const uint16_t* q_norm;
+  const uint16_t* k_norm;
+  float eps;
+  const float* inv_freq;
   int B, W, nq, nkv, G, R;  // R = W * G query rows per (b, kv head)
   float scale, softcap;
   int causal, window;
   const int32_t* seq_lens;
   const int32_t* block_table;
   int max_pages, page, kv_dtype;
-  const void* k_pool;
-  const void* v_pool;
-  const uint32_t* k_sb;
-  const uint32_t* v_sb;
+  void* k_pool;
+  void* v_pool;
+  uint32_t* k_sb;
+  uint32_t* v_sb;
   uint16_t* out;
   int out_packed;
   int nsplit;
-  float* part;  // [B][nkv][nsplit][R][HD + 4]: o (unnormalised) | m | l | 0 | 0
+  int kps;           // keys per (context) split, a multiple of 16, <= Split<HD>::KEYS
+  int fused;         // splits 0 .. nsplit-2: cached keys; split nsplit-1: the new tokens
+  uint16_t* part_o;  // [B*nkv][nsplit][R][HD] bf16: the split's o / l
+  float* part_ml;    // [B*nkv][nsplit][R][2]: the split's running max m and sum l
 };
 
-// keys per split: one workgroup loads its whole split at once
+// LDS capacity in keys of one split (a workgroup loads its whole split at once; kps = KEYS)
 template <int HD> struct Split {
   static constexpr int KEYS = HD == 128 ? 128 : 64;
   static constexpr int KROW = HD + 8;    // K rows in LDS (bf16, padded)
   static constexpr int VROW = KEYS + 8;  // V^T rows in LDS (bf16, padded)
   static constexpr int CK = KEYS * HD / 8 / 256;        // 8-element K chunks per thread
   static constexpr int CV = (KEYS / 2) * (HD / 8) / 256;  // (2 keys x 8 dims) V chunks per thread
-  static constexpr int PSTRIDE = HD + 4;
 };
 
 // output row (b, i), head h, dim d: row-major [B*W, nq*HD] or packed
 __device__ __forceinline__ int64_t attn_out_index(const AttnArgs& a, int HD, int b, int i, int h, int d) {
   const int64_t m = (int64_t)b * a.W + i, k = (int64_t)h * HD + d;
   return a.out_packed ? apack_index(m, k, (int64_t)a.nq * HD / 64) : m * a.nq * HD + k;
-}
-
-__device__ __forceinline__ int64_t kv_token(const AttnArgs& a, int b, int kvh, int j) {
-  const int pg = a.block_table[(int64_t)b * a.max_pages + j / a.page];
-  return ((int64_t)pg * a.nkv + kvh) * a.page + (j % a.page);
 }
 
 // 8 consecutive dims of one token as bf16 (dequantised for 8-bit KV)
@@ -235,118 +256,327 @@ __device__ __forceinline__ void chunk_bf16(const Chunk8& c, uint16_t (&h)[8]) {
   }
 }
 
-// One workgroup per (row b, kv head, split of KEYS keys): every K/V load of the split is
-// issued at once, dequantised into LDS (K row-major, V transposed), then each wave takes
-// 16-query tiles through scores, a one-pass softmax and P.V. Splits at or past the row's
-// key count exit at once (the combine reads only the live ones).
-template <int HD, int QT, int KVT, bool SOFTCAP>
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+// The queries of one 16-row tile in the score MFMA's B layout: lane holds row
+// r = tile * 16 + lane % 16 (token r / G, q head kvh * G + r % G), dims 32 s + 8 (lane / 16) + e.
+template <int HD, bool FUSED>
+struct QTile {
+  static constexpr int KS = HD / 32;
+  float v[FUSED ? KS : 1][FUSED ? 8 : 1];
+  u32x4 raw[FUSED ? 1 : KS];
+};
+
+template <int HD, bool FUSED>
+__device__ __forceinline__ void qtile_load(const AttnArgs& a, int b, int kvh, int tile, int lane, QTile<HD, FUSED>& q) {
+  constexpr int KS = HD / 32;
+  const int r = tile * 16 + (lane & 15);
+  const int rr = r < a.R ? r : 0;
+  const int i = rr / a.G, head = kvh * a.G + rr % a.G;
+  const int g8 = (lane >> 4) * 8;
+  if constexpr (!FUSED) {
+    const uint16_t* qp = a.q + ((int64_t)(b * a.W + i) * a.nq + head) * HD;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) q.raw[s] = *reinterpret_cast<const u32x4*>(qp + s * 32 + g8);
+  } else {
+    const int nheads = a.nq + 2 * a.nkv;
+    const int64_t off = ((int64_t)(b * a.W + i) * nheads + head) * HD;
+    if (a.qkv_splits == 0) {
+      const uint16_t* src = reinterpret_cast<const uint16_t*>(a.qkv) + off;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(src + s * 32 + g8);
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(&w);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q.v[s][e] = bf16_to_f32(h[e]);
+      }
+    } else {
+      const int64_t slice = (int64_t)a.B * a.W * nheads * HD;
+      const float* src = reinterpret_cast<const float*>(a.qkv) + off;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q.v[s][e] = 0.0f;
+      for (int sp = 0; sp < a.qkv_splits; sp += 2) {
+        f32x4 t[2][KS][2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+              t[u][s][h] = sp + u < a.qkv_splits
+                               ? *reinterpret_cast<const f32x4*>(src + (sp + u) * slice + s * 32 + g8 + 4 * h)
+                               : f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          if (sp + u < a.qkv_splits)
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+#pragma unroll
+              for (int e = 0; e < 8; ++e) q.v[s][e] += t[u][s][e / 4][e % 4];
+      }
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q.v[s][e] = round_bf16(q.v[s][e]);
+    }
+  }
+}
+
+// q norm and RoPE of a loaded tile (fused), or the loaded bf16 queries as they are
+template <int HD, bool FUSED>
+__device__ __forceinline__ void qtile_finish(const AttnArgs& a, int off, int tile, int lane, QTile<HD, FUSED>& q,
+                                             bf16x8 (&qf)[HD / 32]) {
+  constexpr int KS = HD / 32;
+  if constexpr (!FUSED) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = __builtin_bit_cast(bf16x8, q.raw[s]);
+  } else {
+    const int r = tile * 16 + (lane & 15);
+    const int rr = r < a.R ? r : 0;
+    const int pos = off + rr / a.G;
+    const int g8 = (lane >> 4) * 8;
+    if (a.q_norm) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += q.v[s][e] * q.v[s][e];
+      ss += __shfl_xor(ss, 16, 64);
+      ss += __shfl_xor(ss, 32, 64);
+      const float rn = rsqrtf(ss / (float)HD + a.eps);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(a.q_norm + s * 32 + g8);
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(&w);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q.v[s][e] = round_bf16((q.v[s][e] * rn) * bf16_to_f32(h[e]));
+      }
+    }
+    // rotate-half: dim 32 s + ... pairs with 32 (s + KS/2) + ... in the same lane
+#pragma unroll
+    for (int s = 0; s < KS / 2; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float sn, cs;
+        rope_sincos(pos, a.inv_freq[s * 32 + g8 + e], sn, cs);
+        const float x1 = q.v[s][e], x2 = q.v[s + KS / 2][e];
+        q.v[s][e] = round_bf16(x1 * cs - x2 * sn);
+        q.v[s + KS / 2][e] = round_bf16(x2 * cs + x1 * sn);
+      }
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[s][e] = (__bf16)q.v[s][e];
+  }
+}
+
+// One workgroup per (row b, kv head, split of KEYS keys): the page-table entries of the whole
+// split are read together with the row length, every K/V load of the split is issued at once,
+// dequantised into LDS (K row-major, V transposed), then each wave takes 16-query tiles
+// through scores, a one-pass softmax and P.V. Splits at or past the row's key count exit
+// before loading K/V (the combine reads only the live ones).
+// FUSED: splits 0 .. nsplit-2 cover the cached keys [0, seq_lens[b]) and the last split the W
+// new tokens, which it forms from the projection (K RMSNorm + RoPE, append to the pool) while
+// the context splits stream the cache; every workgroup forms its own queries meanwhile.
+template <int HD, int QT, int KVT, bool SOFTCAP, bool FUSED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attention_kernel(AttnArgs a) {
   using S = Split<HD>;
   constexpr int KEYS = S::KEYS, KROW = S::KROW, VROW = S::VROW;
+  constexpr int DT = HD / 16;     // output d tiles
+  constexpr int KS = HD / 32;     // k steps of the score MFMA
+  constexpr int NKT = KEYS / 16;  // key tiles
+  constexpr int PER16 = HD / 16;  // dims per lane when a quarter wave holds a row
   __shared__ __attribute__((aligned(16))) uint16_t ks[KEYS * KROW];
   __shared__ __attribute__((aligned(16))) uint32_t vt[HD * VROW / 2];
+  uint16_t* vt16 = reinterpret_cast<uint16_t*>(vt);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int split = blockIdx.x % a.nsplit;
   const int bk = blockIdx.x / a.nsplit;  // b * nkv + kvh
   const int b = bk / a.nkv, kvh = bk % a.nkv;
-  const int off = a.seq_lens[b];
-  const int Lk = min(off + a.W, a.max_pages * a.page);
-  const int j_lo = split * KEYS;
-  if (j_lo >= Lk) return;
-  const int j_hi = min(Lk, j_lo + KEYS);
-  constexpr int DT = HD / 16;  // output d tiles
-  constexpr int KS = HD / 32;  // k steps of the score MFMA
-  constexpr int NKT = KEYS / 16;  // key tiles
+  const int jmax = a.max_pages * a.page;
+  const bool newsplit = FUSED && split == a.nsplit - 1;
+  const int ntiles = (a.R + 15) / 16;
+  // keep the arguments the tile loop needs in SGPRs from here on: after the LDS barrier the
+  // compiler would otherwise reload them from the kernel-argument segment (a memory round trip)
+  float scale = a.scale, softcap = a.softcap;
+  int causal = a.causal, window = a.window, nsplit = a.nsplit, kps = a.kps;
+  uint16_t* part_o = a.part_o;
+  float* part_ml = a.part_ml;
+  asm volatile("" : "+s"(scale), "+s"(softcap), "+s"(causal), "+s"(window), "+s"(nsplit), "+s"(kps));
+  asm volatile("" : "+s"(part_o), "+s"(part_ml));
 
-  // ---- issue every load of the split
-  Chunk8 kc[S::CK], vc[S::CV][2];
+  // ---- independent loads: row length, the split's page-table entries, the first query tile
+  const int off = a.seq_lens[b];
+  int64_t ktok[S::CK], vtok[S::CV][2];
+  if (!newsplit) {
+    const int j0 = split * kps;
 #pragma unroll
-  for (int ci = 0; ci < S::CK; ++ci) {
-    const int c = threadIdx.x + ci * 256;
-    const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
-    const int j = min(j_lo + key, j_hi - 1);  // keys past j_hi are masked below
-    load_chunk<KVT>(a.k_pool, a.k_sb, HD, kv_token(a, b, kvh, j), d0, kc[ci]);
-  }
+    for (int ci = 0; ci < S::CK; ++ci) {
+      const int c = threadIdx.x + ci * 256;
+      const int j = min(j0 + c / (HD / 8), jmax - 1);
+      ktok[ci] = pool_token(a.block_table, a.max_pages, a.page, a.nkv, b, kvh, j);
+    }
 #pragma unroll
-  for (int ci = 0; ci < S::CV; ++ci) {
-    const int c = threadIdx.x + ci * 256;
-    const int kp = c % (KEYS / 2), d0 = (c / (KEYS / 2)) * 8;
+    for (int ci = 0; ci < S::CV; ++ci) {
+      const int kp = (threadIdx.x + ci * 256) % (KEYS / 2);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int j = min(j_lo + 2 * kp + u, j_hi - 1);
-      load_chunk<KVT>(a.v_pool, a.v_sb, HD, kv_token(a, b, kvh, j), d0, vc[ci][u]);
+      for (int u = 0; u < 2; ++u)
+        vtok[ci][u] = pool_token(a.block_table, a.max_pages, a.page, a.nkv, b, kvh, min(j0 + 2 * kp + u, jmax - 1));
     }
   }
-  // query fragments of tile t (row r = tile * 16 + lane % 16 = i * G + hl); the first tile's
-  // are loaded with the K/V, each later tile's one tile ahead
-  auto load_q = [&](int t, u32x4 (&qr)[KS]) {
-    const int r = (wv + 4 * t) * 16 + (lane & 15);
-    const int rr = r < a.R ? r : 0;
-    const uint16_t* qp = a.q + ((int64_t)(b * a.W + rr / a.G) * a.nq + kvh * a.G + rr % a.G) * HD;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) qr[s] = *reinterpret_cast<const u32x4*>(qp + s * 32 + (lane >> 4) * 8);
-  };
-  u32x4 qnext[KS];
-  load_q(0, qnext);
-
-  // ---- dequantise into LDS
-#pragma unroll
-  for (int ci = 0; ci < S::CK; ++ci) {
-    const int c = threadIdx.x + ci * 256;
-    const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
-    uint16_t h[8];
-    chunk_bf16<KVT>(kc[ci], h);
-    *reinterpret_cast<u32x4*>(ks + key * KROW + d0) = *reinterpret_cast<const u32x4*>(h);
+  const int Lk = min(off + a.W, jmax);
+  int j_lo, j_hi;
+  if (newsplit) {
+    j_lo = off;
+    j_hi = Lk;
+  } else {
+    j_lo = split * kps;
+    const int kend = FUSED ? min(off, jmax) : Lk;  // the fused context splits stop at the cache
+    if (j_lo >= kend) return;
+    j_hi = min(kend, j_lo + kps);
   }
+
+  QTile<HD, FUSED> qt;
+  if (wv < ntiles) qtile_load<HD, FUSED>(a, b, kvh, wv, lane, qt);
+  Chunk8 kc[S::CK], vc[S::CV][2];
+  if (!newsplit) {
+    // ---- issue every K/V load of the split
 #pragma unroll
-  for (int ci = 0; ci < S::CV; ++ci) {
-    const int c = threadIdx.x + ci * 256;
-    const int kp = c % (KEYS / 2), d0 = (c / (KEYS / 2)) * 8;
-    uint16_t h0[8], h1[8];
-    chunk_bf16<KVT>(vc[ci][0], h0);
-    chunk_bf16<KVT>(vc[ci][1], h1);
+    for (int ci = 0; ci < S::CK; ++ci) {
+      const int d0 = ((threadIdx.x + ci * 256) % (HD / 8)) * 8;
+      load_chunk<KVT>(a.k_pool, a.k_sb, HD, ktok[ci], d0, kc[ci]);
+    }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) vt[((d0 + e) * VROW) / 2 + kp] = (uint32_t)h0[e] | ((uint32_t)h1[e] << 16);
+    for (int ci = 0; ci < S::CV; ++ci) {
+      const int d0 = ((threadIdx.x + ci * 256) / (KEYS / 2)) * 8;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) load_chunk<KVT>(a.v_pool, a.v_sb, HD, vtok[ci][u], d0, vc[ci][u]);
+    }
+  }
+  // the first tile's queries while the K/V loads are in flight
+  bf16x8 qf[KS];
+  if (wv < ntiles) qtile_finish<HD, FUSED>(a, off, wv, lane, qt, qf);
+
+  if (newsplit) {
+    // ---- the new tokens: zero the tile, then K normed + roped, K/V appended to the pool and
+    // the values attention reads written to LDS; a quarter wave per (token, K or V) row, two
+    // rows per quarter in flight
+    for (int c = threadIdx.x; c < KEYS * KROW / 8; c += 256) reinterpret_cast<u32x4*>(ks)[c] = u32x4{0, 0, 0, 0};
+    for (int c = threadIdx.x; c < HD * VROW / 8; c += 256) reinterpret_cast<u32x4*>(vt)[c] = u32x4{0, 0, 0, 0};
+    __syncthreads();
+    const int n_new = j_hi - j_lo;  // <= W
+    const int nheads = a.nq + 2 * a.nkv;
+    const int quarter = lane >> 4, sub = lane & 15;
+    for (int t0 = wv * 4; t0 < 2 * n_new; t0 += 32) {
+      float v[2][PER16];
+      int jj[2];
+      bool kk[2], live[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int task = t0 + 16 * u + quarter;
+        live[u] = task < 2 * n_new;
+        const int tt = live[u] ? task : 0;
+        kk[u] = tt < n_new;
+        jj[u] = j_lo + (kk[u] ? tt : tt - n_new);
+        const int head = a.nq + (kk[u] ? kvh : a.nkv + kvh);
+        load_proj_row<PER16>(a.qkv, a.qkv_splits, (int64_t)a.B * a.W * nheads * HD,
+                             ((int64_t)(b * a.W + (jj[u] - off)) * nheads + head) * HD, sub, v[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        if (!live[u]) continue;  // a whole quarter: its shuffles stay inside it
+        norm_rope_row<HD, 16>(v[u], sub, kk[u] ? a.k_norm : nullptr, a.eps, kk[u], a.inv_freq, jj[u]);
+        const int64_t tok = pool_token(a.block_table, a.max_pages, a.page, a.nkv, b, kvh, jj[u]);
+        kv_store_row<HD, 16>(v[u], sub, a.kv_dtype, kk[u] ? a.k_pool : a.v_pool, kk[u] ? a.k_sb : a.v_sb, tok);
+        const int key = jj[u] - j_lo;
+        if (kk[u]) {
+          uint16_t h[PER16];
+#pragma unroll
+          for (int e = 0; e < PER16; ++e) h[e] = f32_to_bf16(v[u][e]);
+#pragma unroll
+          for (int e = 0; e < PER16; e += 8)
+            *reinterpret_cast<u32x4*>(ks + key * KROW + sub * PER16 + e) = *reinterpret_cast<const u32x4*>(h + e);
+        } else {
+#pragma unroll
+          for (int e = 0; e < PER16; ++e) vt16[(sub * PER16 + e) * VROW + key] = f32_to_bf16(v[u][e]);
+        }
+      }
+    }
+  } else {
+    // ---- dequantise into LDS (keys past the split's end are zeroed: masked, but finite)
+#pragma unroll
+    for (int ci = 0; ci < S::CK; ++ci) {
+      const int c = threadIdx.x + ci * 256;
+      const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+      uint16_t h[8];
+      chunk_bf16<KVT>(kc[ci], h);
+      u32x4 w = *reinterpret_cast<const u32x4*>(h);
+      if (j_lo + key >= j_hi) w = u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(ks + key * KROW + d0) = w;
+    }
+#pragma unroll
+    for (int ci = 0; ci < S::CV; ++ci) {
+      const int c = threadIdx.x + ci * 256;
+      const int kp = c % (KEYS / 2), d0 = (c / (KEYS / 2)) * 8;
+      const int j0 = j_lo + 2 * kp;
+      uint16_t h0[8], h1[8];
+      chunk_bf16<KVT>(vc[ci][0], h0);
+      chunk_bf16<KVT>(vc[ci][1], h1);
+      const bool z0 = j0 >= j_hi, z1 = j0 + 1 >= j_hi;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        vt[((d0 + e) * VROW) / 2 + kp] = (uint32_t)(z0 ? 0 : h0[e]) | ((uint32_t)(z1 ? 0 : h1[e]) << 16);
+    }
   }
   __syncthreads();
 
-  const uint16_t* vt16 = reinterpret_cast<const uint16_t*>(vt);
 #pragma unroll 1
   for (int t = 0; t < QT; ++t) {
-    if (wv + 4 * t >= (a.R + 15) / 16) break;
-    bf16x8 qf[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) qf[s] = __builtin_bit_cast(bf16x8, qnext[s]);
-    if (t + 1 < QT && wv + 4 * (t + 1) < (a.R + 15) / 16) load_q(t + 1, qnext);
-    const int rq = (wv + 4 * t) * 16 + (lane & 15);
+    const int tile = wv + 4 * t;
+    if (tile >= ntiles) break;
+    if (t > 0) {
+      qtile_load<HD, FUSED>(a, b, kvh, tile, lane, qt);
+      qtile_finish<HD, FUSED>(a, off, tile, lane, qt, qf);
+    }
+    const int rq = tile * 16 + (lane & 15);
     const bool qvalid = rq < a.R;
     // ---- scores: lane holds S^T[key = 16h + 4*(lane/16) + r][q = lane % 16]
+    // (all fragments of two key tiles read before their MFMAs: eight LDS reads in flight)
     f32x4 st[NKT];
 #pragma unroll
-    for (int h = 0; h < NKT; ++h) {
-      f32x4 acc = {0, 0, 0, 0};
+    for (int h = 0; h < NKT; h += 2) {
+      bf16x8 kf[2][KS];
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(ks + (h * 16 + (lane & 15)) * KROW + s * 32 + (lane >> 4) * 8);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[s], acc, 0, 0, 0);
-      }
-      st[h] = acc;
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          kf[u][s] = *reinterpret_cast<const bf16x8*>(ks + ((h + u) * 16 + (lane & 15)) * KROW + s * 32 + (lane >> 4) * 8);
+      __builtin_amdgcn_sched_barrier(0);  // keep the reads grouped ahead of the MFMAs
+      f32x4 acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[u][s], qf[s], acc[u], 0, 0, 0);
+      st[h] = acc[0];
+      st[h + 1] = acc[1];
     }
+    // visible keys of this lane's query: [k_first, k_last] (branch-free mask below)
     const int qpos = off + (qvalid ? rq / a.G : 0);
+    int k_last = j_hi - 1, k_first = 0;
+    if (causal) {
+      k_last = min(k_last, qpos);
+      if (window > 0) k_first = qpos - window + 1;
+    }
+    if (!qvalid) k_last = -1;
     float mx = -__builtin_inff();
 #pragma unroll
     for (int h = 0; h < NKT; ++h)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = j_lo + h * 16 + (lane >> 4) * 4 + r;
-        float sc = st[h][r] * a.scale;
-        if (SOFTCAP) sc = tanhf(sc / a.softcap) * a.softcap;
-        bool ok = j < j_hi && qvalid;
-        if (a.causal) {
-          ok = ok && j <= qpos;
-          if (a.window > 0) ok = ok && j > qpos - a.window;
-        }
-        sc = ok ? sc : -__builtin_inff();
+        float sc = st[h][r] * scale;
+        if (SOFTCAP) sc = tanhf(sc / softcap) * softcap;
+        sc = (j >= k_first && j <= k_last) ? sc : -__builtin_inff();
         st[h][r] = sc;
         mx = fmaxf(mx, sc);
       }
@@ -368,25 +598,34 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
     // ---- O^T[d][q] = V^T . P^T: A = V^T rows d*16 + lane%16, keys in pb's order
+    // (all fragments of two d tiles read before their MFMAs)
     f32x4 o[DT];
 #pragma unroll
-    for (int d = 0; d < DT; ++d) {
-      f32x4 acc = {0, 0, 0, 0};
+    for (int d = 0; d < DT; d += 2) {
+      u32x4 vv[2][KEYS / 32];
 #pragma unroll
-      for (int c = 0; c < KEYS / 32; ++c) {
-        const uint16_t* vr = vt16 + (d * 16 + (lane & 15)) * VROW + 32 * c + (lane >> 4) * 4;
-        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
-        const u32x4 vv = {lo.x, lo.y, hi.x, hi.y};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv), pb[c], acc, 0, 0, 0);
-      }
-      o[d] = acc;
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int c = 0; c < KEYS / 32; ++c) {
+          const uint16_t* vr = vt16 + ((d + u) * 16 + (lane & 15)) * VROW + 32 * c + (lane >> 4) * 4;
+          const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
+          vv[u][c] = u32x4{lo.x, lo.y, hi.x, hi.y};
+        }
+      __builtin_amdgcn_sched_barrier(0);
+      f32x4 acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+#pragma unroll
+      for (int c = 0; c < KEYS / 32; ++c)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv[u][c]), pb[c], acc[u], 0, 0, 0);
+      o[d] = acc[0];
+      o[d + 1] = acc[1];
     }
-    const int r = rq;
-    if (r >= a.R) continue;
-    if (a.nsplit == 1) {
-      const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-      const int i = r / a.G, hl = r % a.G;
+    if (!qvalid) continue;
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    if (nsplit == 1) {
+      const int i = rq / a.G, hl = rq % a.G;
 #pragma unroll
       for (int d = 0; d < DT; ++d)
 #pragma unroll
@@ -394,87 +633,170 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
           a.out[attn_out_index(a, HD, b, i, kvh * a.G + hl, d * 16 + (lane >> 4) * 4 + rr)] = f32_to_bf16(o[d][rr] * inv);
       continue;
     }
-    float* pr = a.part + (((size_t)bk * a.nsplit + split) * a.R + r) * S::PSTRIDE;
+    // partial: o / l in bf16 (4 consecutive dims per d tile), (m, l) in fp32
+    const size_t prow = ((size_t)bk * nsplit + split) * a.R + rq;
+    uint16_t* po = part_o + prow * HD + (lane >> 4) * 4;
 #pragma unroll
-    for (int d = 0; d < DT; ++d) *reinterpret_cast<f32x4*>(pr + d * 16 + (lane >> 4) * 4) = o[d];
-    if (lane < 16) *reinterpret_cast<f32x4*>(pr + HD) = f32x4{mx, lsum, 0.0f, 0.0f};
+    for (int d = 0; d < DT; ++d) {
+      const uint32_t lo = (uint32_t)f32_to_bf16(o[d][0] * inv) | ((uint32_t)f32_to_bf16(o[d][1] * inv) << 16);
+      const uint32_t hi = (uint32_t)f32_to_bf16(o[d][2] * inv) | ((uint32_t)f32_to_bf16(o[d][3] * inv) << 16);
+      *reinterpret_cast<uint2*>(po + d * 16) = uint2{lo, hi};
+    }
+    if (lane < 16) *reinterpret_cast<float2*>(part_ml + prow * 2) = float2{mx, lsum};
   }
 }
 
-// Combine the live splits of one (row b, kv head, query row r) per wave in two load rounds:
-// lane s reads split s's (m, l) and forms its weight exp(m_s - M); then every lane reads the
-// partial outputs of all splits for its dims at once (up to 64 splits per round).
+// Combine the live splits of one (row b, kv head, query row r) per wave, 64 (hd 128) or 32
+// splits per load round: lane s reads split s's (m, l) and forms its weight exp(m_s - M) * l_s while every lane
+// reads the normalised partial outputs of the round's splits for its dims.
 template <int HD>
 __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   using S = Split<HD>;
-  constexpr int PER = HD / 64;
+  constexpr int PER = HD / 64;  // consecutive dims per lane
   const int lane = threadIdx.x & 63;
   const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (task >= a.B * a.nkv * a.R) return;
   const int r = task % a.R, bk = task / a.R;
   const int b = bk / a.nkv, kvh = bk % a.nkv;
-  const int Lk = min(a.seq_lens[b] + a.W, a.max_pages * a.page);
-  const int ns = min(a.nsplit, (Lk + S::KEYS - 1) / S::KEYS);
-  const float* base = a.part + ((size_t)bk * a.nsplit * a.R + r) * S::PSTRIDE;
-  const size_t sstride = (size_t)a.R * S::PSTRIDE;
+  // live splits: the first ns; with a.fused the context splits [0, ns - 1) and the new-token
+  // split (the last one)
+  const int jmax = a.max_pages * a.page;
+  const int ns = a.fused ? min((min(a.seq_lens[b], jmax) + a.kps - 1) / a.kps, a.nsplit - 1) + 1
+                         : min(a.nsplit, (min(a.seq_lens[b] + a.W, jmax) + a.kps - 1) / a.kps);
+  const int nlast = a.fused ? a.nsplit - 1 - (ns - 1) : 0;  // split index shift of the last live one
+  const uint16_t* base_o = a.part_o + ((size_t)bk * a.nsplit * a.R + r) * HD + lane * PER;
+  const float* base_ml = a.part_ml + ((size_t)bk * a.nsplit * a.R + r) * 2;
+  const size_t so = (size_t)a.R * HD, sml = (size_t)a.R * 2;
   float acc[PER];
 #pragma unroll
   for (int e = 0; e < PER; ++e) acc[e] = 0.0f;
   float M = -__builtin_inff(), den = 0.0f;
-  for (int s0 = 0; s0 < ns; s0 += 64) {
-    const int n = min(64, ns - s0);
-    float ml[2] = {-__builtin_inff(), 0.0f};
+  // rounds of RS splits: the (m, l) and partial-output loads of a round are issued together
+  constexpr int RS = PER == 2 ? 64 : 32;
+  for (int s0 = 0; s0 < ns; s0 += RS) {
+    const int n = min(RS, ns - s0);
+    float m = -__builtin_inff(), l = 0.0f;
     if (lane < n) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(base + (s0 + lane) * sstride + HD);
-      ml[0] = v[0];
-      ml[1] = v[1];
+      const int sp = s0 + lane + (s0 + lane == ns - 1 ? nlast : 0);
+      const float2 v = *reinterpret_cast<const float2*>(base_ml + sp * sml);
+      m = v.x;
+      l = v.y;
     }
-    const float Mn = fmaxf(M, wave_max(ml[0]));
+    // loads of the live splits only, in batches of 16 (all batches issued before any use)
+    uint16_t ov[RS][PER];
+#pragma unroll
+    for (int u0 = 0; u0 < RS; u0 += 16) {
+      if (u0 >= n) break;
+#pragma unroll
+      for (int u = u0; u < u0 + 16; ++u) {
+        int sp = s0 + min(u, n - 1);
+        if (sp == ns - 1) sp += nlast;
+        if constexpr (PER == 2) {
+          const uint32_t x = *reinterpret_cast<const uint32_t*>(base_o + sp * so);
+          ov[u][0] = (uint16_t)(x & 0xffff);
+          ov[u][1] = (uint16_t)(x >> 16);
+        } else {
+          const uint2 x = *reinterpret_cast<const uint2*>(base_o + sp * so);
+          const uint16_t* hx = reinterpret_cast<const uint16_t*>(&x);
+#pragma unroll
+          for (int e = 0; e < PER; ++e) ov[u][e] = hx[e];
+        }
+      }
+    }
+    const float Mn = fmaxf(M, wave_max(m));
     const float rescale = M == -__builtin_inff() ? 0.0f : __expf(M - Mn);
-    const float w = ml[0] == -__builtin_inff() ? 0.0f : __expf(ml[0] - Mn);
-    den = den * rescale + wave_sum(w * ml[1]);
+    const float w = m == -__builtin_inff() ? 0.0f : __expf(m - Mn) * l;
+    den = den * rescale + wave_sum(w);
 #pragma unroll
     for (int e = 0; e < PER; ++e) acc[e] *= rescale;
     M = Mn;
-    // all partial rows of this round in flight, 16 at a time
-    for (int u0 = 0; u0 < n; u0 += 16) {
-      float ov[16][PER];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int s = s0 + min(u0 + u, n - 1);
+    for (int u0 = 0; u0 < RS; u0 += 16) {
+      if (u0 >= n) break;
 #pragma unroll
-        for (int e = 0; e < PER; ++e) ov[u][e] = base[s * sstride + e * 64 + lane];
-      }
+      for (int u = u0; u < u0 + 16; ++u) {
+        const float wu = __shfl(w, u, 64);
+        if (u < n)
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const float wu = __shfl(w, min(u0 + u, 63), 64);
-        if (u0 + u < n)
-#pragma unroll
-          for (int e = 0; e < PER; ++e) acc[e] += wu * ov[u][e];
+          for (int e = 0; e < PER; ++e) acc[e] += wu * bf16_to_f32(ov[u][e]);
       }
     }
   }
   const int i = r / a.G, hl = r % a.G;
   const float inv = den > 0.0f ? 1.0f / den : 0.0f;
 #pragma unroll
-  for (int e = 0; e < PER; ++e) a.out[attn_out_index(a, HD, b, i, kvh * a.G + hl, e * 64 + lane)] = f32_to_bf16(acc[e] * inv);
+  for (int e = 0; e < PER; ++e)
+    a.out[attn_out_index(a, HD, b, i, kvh * a.G + hl, lane * PER + e)] = f32_to_bf16(acc[e] * inv);
 }
 
 // ----------------------------------------------------------------------------- host helpers
-template <int HD, int QT>
+template <int HD, int QT, bool FUSED>
 static void launch_attention(const AttnArgs& a, int kv_dtype, bool softcap, dim3 grid, hipStream_t st) {
   if (kv_dtype == DSK_KV_U8) {
-    if (softcap) hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_U8, true>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_U8, false>), grid, dim3(256), 0, st, a);
+    if (softcap) hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_U8, true, FUSED>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_U8, false, FUSED>), grid, dim3(256), 0, st, a);
   } else {
-    if (softcap) hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_BF16, true>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_BF16, false>), grid, dim3(256), 0, st, a);
+    if (softcap) hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_BF16, true, FUSED>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_BF16, false, FUSED>), grid, dim3(256), 0, st, a);
   }
 }
 
-static int attn_nsplit(int hd, int max_ctx) {
-  const int keys = hd == 128 ? Split<128>::KEYS : Split<256>::KEYS;
-  return (max_ctx + keys - 1) / keys;
+// Keys per split: the LDS capacity (graph-stable: the split grid depends on max_ctx only).
+static int attn_split_keys(int hd, int) { return hd == 128 ? Split<128>::KEYS : Split<256>::KEYS; }
+static int attn_nsplit(int hd, int max_ctx) { return (int)ceil_div(max_ctx, attn_split_keys(hd, max_ctx)); }
+
+// partial outputs first, then (m, l) at a 256-byte boundary
+static size_t attn_part_o_bytes(int B, int W, int nq, int hd, int nsplit) {
+  return ((size_t)B * W * nq * nsplit * hd * 2 + 255) & ~(size_t)255;
+}
+static size_t attn_ws_need(int B, int W, int nq, int hd, int nsplit) {
+  return nsplit > 1 ? attn_part_o_bytes(B, W, nq, hd, nsplit) + (size_t)B * W * nq * nsplit * 2 * sizeof(float) : 0;
+}
+
+// shared validation and launch of both attention entries
+static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* workspace, size_t ws_bytes,
+                         bool fused, hipStream_t st, const char* who) {
+  DSK_REQUIRE(hd == 128 || hd == 256, "%s: head_dim %d not supported (128, 256)", who, hd);
+  DSK_REQUIRE(a.B > 0 && a.W > 0 && a.nq > 0 && a.nkv > 0 && a.nq % a.nkv == 0, "%s: bad shape", who);
+  DSK_REQUIRE(a.kv_dtype == DSK_KV_BF16 || (a.kv_dtype == DSK_KV_U8 && a.k_sb && a.v_sb), "%s: u8 KV needs sb", who);
+  DSK_REQUIRE(a.page > 0 && a.max_pages > 0, "%s: bad page geometry", who);
+  DSK_REQUIRE(max_ctx >= a.W && (int64_t)a.max_pages * a.page >= max_ctx, "%s: max_ctx %d beyond block table", who,
+              max_ctx);
+  a.G = a.nq / a.nkv;
+  a.R = a.W * a.G;
+  const int tiles = (a.R + 15) / 16;
+  const int QT = (tiles + 3) / 4;
+  DSK_REQUIRE(QT <= (hd == 128 ? 4 : 2), "%s: W*G=%d query rows per kv head exceeds %d", who, a.R,
+              (hd == 128 ? 256 : 128));
+  DSK_REQUIRE(!fused || a.W <= 64, "%s: W=%d new tokens exceeds 64", who, a.W);
+  DSK_REQUIRE(!a.out_packed || (a.B * a.W <= 64 && (a.nq * hd) % 64 == 0), "%s: packed output needs B*W <= 64", who);
+  a.fused = fused ? 1 : 0;
+  a.kps = attn_split_keys(hd, max_ctx);
+  a.nsplit = attn_nsplit(hd, max_ctx) + (fused ? 1 : 0);
+  const size_t need = attn_ws_need(a.B, a.W, a.nq, hd, a.nsplit);
+  DSK_REQUIRE(a.nsplit == 1 || (workspace && ws_bytes >= need), "%s: workspace %zu < %zu", who, ws_bytes, need);
+  a.part_o = reinterpret_cast<uint16_t*>(workspace);
+  a.part_ml = a.nsplit > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
+                                                       attn_part_o_bytes(a.B, a.W, a.nq, hd, a.nsplit))
+                           : nullptr;
+  dim3 grid((unsigned)(a.B * a.nkv * a.nsplit));
+  const bool sc = softcap > 0.0f;
+#define DSK_ATTN_CASE(hdv, qt)                                      \
+  if (hd == hdv && QT == qt) {                                      \
+    if (fused) launch_attention<hdv, qt, true>(a, a.kv_dtype, sc, grid, st); \
+    else launch_attention<hdv, qt, false>(a, a.kv_dtype, sc, grid, st);      \
+  }
+  DSK_ATTN_CASE(128, 1) DSK_ATTN_CASE(128, 2) DSK_ATTN_CASE(128, 3) DSK_ATTN_CASE(128, 4)
+  DSK_ATTN_CASE(256, 1) DSK_ATTN_CASE(256, 2)
+#undef DSK_ATTN_CASE
+  DSK_LAUNCH_CHECK(who);
+  if (a.nsplit > 1) {
+    const dim3 cgrid((unsigned)ceil_div((int64_t)a.B * a.nkv * a.R, 4));
+    if (hd == 128) hipLaunchKernelGGL(attention_combine_kernel<128>, cgrid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(attention_combine_kernel<256>, cgrid, dim3(256), 0, st, a);
+    DSK_LAUNCH_CHECK(who);
+  }
+  return DSK_OK;
 }
 
 }  // namespace dsk
@@ -512,9 +834,7 @@ extern "C" int dsk_qkv_rope_append(const void* qkv, int qkv_splits, int B, int W
 extern "C" size_t dsk_attn_ws_bytes(int B, int W, int nq, int hd, int max_ctx) {
   if (B <= 0 || W <= 0 || nq <= 0 || hd <= 0 || max_ctx <= 0) return 0;
   if (hd != 128 && hd != 256) return 0;
-  // rows per kv head * nkv = W * nq
-  const size_t nsplit = (size_t)attn_nsplit(hd, max_ctx);
-  return nsplit > 1 ? (size_t)B * W * nq * nsplit * (hd + 4) * sizeof(float) : 0;
+  return attn_ws_need(B, W, nq, hd, attn_nsplit(hd, max_ctx) + 1);  // + the fused new-token split
 }
 
 extern "C" int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, int hd, float scale, int causal,
@@ -523,25 +843,51 @@ extern "C" int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, i
                              const void* v_pool, const uint32_t* k_sb, const uint32_t* v_sb, uint16_t* out,
                              int out_packed, void* workspace, size_t ws_bytes, dsk_stream_t stream) {
   DSK_REQUIRE(q && seq_lens && block_table && k_pool && v_pool && out, "dsk_attention: null pointer");
-  DSK_REQUIRE(hd == 128 || hd == 256, "dsk_attention: head_dim %d not supported (128, 256)", hd);
-  DSK_REQUIRE(B > 0 && W > 0 && nq > 0 && nkv > 0 && nq % nkv == 0, "dsk_attention: bad shape");
-  DSK_REQUIRE(kv_dtype == DSK_KV_BF16 || (kv_dtype == DSK_KV_U8 && k_sb && v_sb), "dsk_attention: u8 KV needs sb");
-  DSK_REQUIRE(max_ctx >= W && (int64_t)max_pages * page >= max_ctx, "dsk_attention: max_ctx %d beyond block table",
-              max_ctx);
-  const int G = nq / nkv;
-  const int R = W * G;
-  const int tiles = (R + 15) / 16;
-  const int QT = (tiles + 3) / 4;
-  DSK_REQUIRE(QT <= (hd == 128 ? 4 : 2), "dsk_attention: W*G=%d query rows per kv head exceeds %d", R,
-              (hd == 128 ? 256 : 128));
-  AttnArgs a;
+  AttnArgs a = {};
   a.q = q;
   a.B = B;
   a.W = W;
   a.nq = nq;
   a.nkv = nkv;
-  a.G = G;
-  a.R = R;
+  a.scale = scale;
+  a.softcap = softcap;
+  a.causal = causal;
+  a.window = window;
+  a.seq_lens = seq_lens;
+  a.block_table = block_table;
+  a.max_pages = max_pages;
+  a.page = page;
+  a.kv_dtype = kv_dtype;
+  a.k_pool = const_cast<void*>(k_pool);
+  a.v_pool = const_cast<void*>(v_pool);
+  a.k_sb = const_cast<uint32_t*>(k_sb);
+  a.v_sb = const_cast<uint32_t*>(v_sb);
+  a.out = out;
+  a.out_packed = out_packed ? 1 : 0;
+  return attention_run(a, hd, max_ctx, softcap, workspace, ws_bytes, false, as_stream(stream), "dsk_attention");
+}
+
+extern "C" int dsk_qkv_attention(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
+                                 const uint16_t* q_norm, const uint16_t* k_norm, float eps, const float* inv_freq,
+                                 float scale, int causal, int window, float softcap, const int32_t* seq_lens,
+                                 int max_ctx, const int32_t* block_table, int max_pages, int page, int kv_dtype,
+                                 void* k_pool, void* v_pool, uint32_t* k_sb, uint32_t* v_sb, uint16_t* out,
+                                 int out_packed, void* workspace, size_t ws_bytes, dsk_stream_t stream) {
+  DSK_REQUIRE(qkv && inv_freq && seq_lens && block_table && k_pool && v_pool && out,
+              "dsk_qkv_attention: null pointer");
+  DSK_REQUIRE(qkv_splits >= 0, "dsk_qkv_attention: qkv_splits=%d", qkv_splits);
+  DSK_REQUIRE(((uintptr_t)q_norm | (uintptr_t)qkv) % 16 == 0, "dsk_qkv_attention: q_norm and qkv must be 16-byte aligned");
+  AttnArgs a = {};
+  a.qkv = qkv;
+  a.qkv_splits = qkv_splits;
+  a.q_norm = q_norm;
+  a.k_norm = k_norm;
+  a.eps = eps;
+  a.inv_freq = inv_freq;
+  a.B = B;
+  a.W = W;
+  a.nq = nq;
+  a.nkv = nkv;
   a.scale = scale;
   a.softcap = softcap;
   a.causal = causal;
@@ -557,25 +903,5 @@ extern "C" int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, i
   a.v_sb = v_sb;
   a.out = out;
   a.out_packed = out_packed ? 1 : 0;
-  DSK_REQUIRE(!out_packed || (B * W <= 64 && (nq * hd) % 64 == 0), "dsk_attention: packed output needs B*W <= 64");
-  a.nsplit = attn_nsplit(hd, max_ctx);
-  const size_t need = a.nsplit > 1 ? (size_t)B * nkv * a.nsplit * R * (hd + 4) * sizeof(float) : 0;
-  DSK_REQUIRE(a.nsplit == 1 || (workspace && ws_bytes >= need), "dsk_attention: workspace %zu < %zu", ws_bytes, need);
-  a.part = reinterpret_cast<float*>(workspace);
-  dim3 grid((unsigned)(B * nkv * a.nsplit));
-  hipStream_t st = as_stream(stream);
-  const bool sc = softcap > 0.0f;
-#define DSK_ATTN_CASE(hdv, qt) \
-  if (hd == hdv && QT == qt) launch_attention<hdv, qt>(a, kv_dtype, sc, grid, st);
-  DSK_ATTN_CASE(128, 1) DSK_ATTN_CASE(128, 2) DSK_ATTN_CASE(128, 3) DSK_ATTN_CASE(128, 4)
-  DSK_ATTN_CASE(256, 1) DSK_ATTN_CASE(256, 2)
-#undef DSK_ATTN_CASE
-  DSK_LAUNCH_CHECK("dsk_attention");
-  if (a.nsplit > 1) {
-    const dim3 cgrid((unsigned)ceil_div((int64_t)B * nkv * R, 4));
-    if (hd == 128) hipLaunchKernelGGL(attention_combine_kernel<128>, cgrid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(attention_combine_kernel<256>, cgrid, dim3(256), 0, st, a);
-    DSK_LAUNCH_CHECK("dsk_attention (combine)");
-  }
-  return DSK_OK;
+  return attention_run(a, hd, max_ctx, softcap, workspace, ws_bytes, true, as_stream(stream), "dsk_qkv_attention");
 }

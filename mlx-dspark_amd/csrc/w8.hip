@@ -338,7 +338,9 @@ __device__ __forceinline__ void gemm_batch(const GemmArgs& a, int64_t t0, int64_
 // Workgroup = NT consecutive 16-row weight tiles x one K split; its WAVES waves take the
 // split's batches round-robin, each accumulating all NT tiles (every activation fragment a
 // wave loads feeds NT tiles), then reduce through LDS in wave order.
-template <int MT, int NT, int U, int WAVES>
+// EK: the epilogue family (0 store, 1 gated, 2 split-K partial) as a template parameter, so each
+// family is its own (smaller) kernel
+template <int MT, int NT, int U, int WAVES, int EK>
 __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -367,7 +369,7 @@ __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
   __syncthreads();
 
   // output element o: lane ln = o % 64, r = (o / 64) % 4, tile (i, j) = o / 256
-  const bool gated = a.epi == DSK_EPI_SWIGLU || a.epi == DSK_EPI_GEGLU;
+  constexpr bool gated = EK == 1;
   for (int o = threadIdx.x; o < NOUT; o += WAVES * 64) {
     const int i = (o >> 8) / NT, j = (o >> 8) % NT;
     const int m = i * 16 + ((o & 63) >> 4) * 4 + ((o >> 6) & 3);
@@ -376,9 +378,9 @@ __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) v += red[w][o];
     const int64_t n = (t0 + j) * 16 + (o & 15);
-    if (a.epi == DSK_EPI_PARTIAL) {
+    if constexpr (EK == 2) {
       reinterpret_cast<float*>(a.y)[((int64_t)ks * a.M + m) * a.N + n] = v;
-    } else if (!gated) {
+    } else if constexpr (!gated) {
       gemm_store(a, m, n, v);
     } else {
       float u = 0.0f;
@@ -448,18 +450,26 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi) {
 }
 
 template <int MT, int NT, int U, int WAVES>
-static void launch_gemm_t(const GemmArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES>), dim3((unsigned)(a.n_slabs * a.SK)), dim3(WAVES * 64), 0,
-                     st, a);
+static bool launch_gemm_t(const GemmArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)(a.n_slabs * a.SK)), blk(WAVES * 64);
+  if (a.epi == DSK_EPI_PARTIAL) {
+    hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 2>), grid, blk, 0, st, a);
+  } else if (a.epi == DSK_EPI_STORE) {
+    hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 0>), grid, blk, 0, st, a);
+  } else {
+    if constexpr (NT % 2 != 0) return false;  // gated tiles come in gate|up pairs
+    else hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 1>), grid, blk, 0, st, a);
+  }
+  return true;
 }
 
 template <int MT, int NT, int U>
 static bool launch_gemm_w(const GemmArgs& a, int waves, hipStream_t st) {
   constexpr int max_waves = 65536 / (MT * NT * 1024);  // LDS of the cross-wave reduction
   switch (waves) {
-    case 4: if constexpr (max_waves >= 4) { launch_gemm_t<MT, NT, U, 4>(a, st); return true; } return false;
-    case 8: if constexpr (max_waves >= 8) { launch_gemm_t<MT, NT, U, 8>(a, st); return true; } return false;
-    case 16: if constexpr (max_waves >= 16) { launch_gemm_t<MT, NT, U, 16>(a, st); return true; } return false;
+    case 4: if constexpr (max_waves >= 4) return launch_gemm_t<MT, NT, U, 4>(a, st); return false;
+    case 8: if constexpr (max_waves >= 8) return launch_gemm_t<MT, NT, U, 8>(a, st); return false;
+    case 16: if constexpr (max_waves >= 16) return launch_gemm_t<MT, NT, U, 16>(a, st); return false;
   }
   return false;
 }

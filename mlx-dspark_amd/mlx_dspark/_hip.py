@@ -38,6 +38,10 @@ SIGNATURES: dict[str, tuple] = {
     "dsk_attention": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_float,
                               c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,
                               c_void_p, c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
+    "dsk_qkv_attention": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float,
+                                  c_void_p, c_float, c_int, c_int, c_float, c_void_p, c_int, c_void_p, c_int, c_int,
+                                  c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_size_t,
+                                  c_void_p]),
     "dsk_accept_greedy": (c_int, [c_void_p, c_int, c_int64, c_int, c_int, c_int64, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "dsk_accept_ws_bytes": (c_size_t, [c_int, c_int, c_int64]),

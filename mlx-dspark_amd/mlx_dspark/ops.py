@@ -18,7 +18,7 @@ from ._hip import (DSK_BF16, DSK_EPI_GEGLU, DSK_EPI_PARTIAL, DSK_EPI_STORE, DSK_
 
 __all__ = [
     "W8Weight", "W8Table", "Workspace", "Packed", "act_pack", "pack", "w8_gemm", "w8_embed",
-    "qkv_rope_append", "attention", "accept_greedy", "accept_sample", "sample_rows", "lens_add",
+    "qkv_rope_append", "attention", "qkv_attention", "accept_greedy", "accept_sample", "sample_rows", "lens_add",
     "rope_inv_freq", "DSK_EPI_STORE", "DSK_EPI_SWIGLU", "DSK_EPI_GEGLU", "DSK_EPI_PARTIAL", "DSK_KV_BF16",
     "DSK_KV_U8",
 ]
@@ -287,6 +287,30 @@ def attention(q, B, W, nq, nkv, hd, scale, seq_lens, max_ctx, block_table, page,
          ptr(buf), buf.numel(), stream_ptr())
     return out
 
+
+
+def qkv_attention(qkv, B, W, nq, nkv, hd, q_norm, k_norm, eps, inv_freq, scale, seq_lens, max_ctx, block_table,
+                  page, kv_dtype, k_pool, v_pool, k_sb=None, v_sb=None, *, causal=True, window=0, softcap=0.0,
+                  out=None, packed=False):
+    """qkv_rope_append + attention in one kernel: qkv is the projection (bf16 [B*W, (nq+2nkv)*hd]
+    or f32 split-K partials [S, B*W, (nq+2nkv)*hd]); the W new tokens' K/V are appended to the
+    pool at seq_lens[b] + i. Returns bf16 [B*W, nq*hd] or a Packed when packed."""
+    splits = qkv.shape[0] if qkv.dim() == 3 else 0
+    if splits and (qkv.dtype != torch.float32 or not qkv.is_contiguous()):
+        raise ValueError("qkv partials must be contiguous f32")
+    if not splits and (qkv.dtype != torch.bfloat16 or not qkv.is_contiguous()):
+        qkv = qkv.contiguous().to(torch.bfloat16)
+    if out is None:
+        out = Packed.empty(B * W, nq * hd, qkv.device) if packed else torch.empty(
+            (B * W, nq * hd), dtype=torch.bfloat16, device=qkv.device)
+    odata = out.data if isinstance(out, Packed) else out
+    ws = Workspace.get(qkv.device)
+    buf = ws.reserve("attn", _hip.lib.dsk_attn_ws_bytes(B, W, nq, hd, max_ctx))
+    call("dsk_qkv_attention", ptr(qkv), splits, B, W, nq, nkv, hd, ptr(q_norm), ptr(k_norm), float(eps),
+         ptr(inv_freq), float(scale), int(bool(causal)), int(window), float(softcap), ptr(seq_lens), int(max_ctx),
+         ptr(block_table), block_table.shape[1], page, kv_dtype, ptr(k_pool), ptr(v_pool), ptr(k_sb), ptr(v_sb),
+         ptr(odata), int(isinstance(out, Packed)), ptr(buf), buf.numel(), stream_ptr())
+    return out
 
 # ----------------------------------------------------------------------------- acceptance
 def accept_greedy(logits: torch.Tensor, draft: torch.Tensor | None, *, seq_lens=None, tt=None,
