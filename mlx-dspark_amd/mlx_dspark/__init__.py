@@ -6,6 +6,7 @@ for the decode path: loaders, Target, the drafters, the decode loops and GenResu
 
 __version__ = "0.1.0"
 
+from .batch_engine import SpecSlots, batch_generate_baseline, batch_spec_generate, batchable
 from .config import DSparkConfig
 from .dflash_model import DFlashConfig, DFlashDraftModel
 from .generate import (GenResult, StopStreaming, dflash_generate, encode_messages, encode_prompt,
@@ -21,5 +22,6 @@ __all__ = [
     "load_pair", "load_drafter", "load_dflash", "load_target", "load_dflash_pair",
     "speculative_generate", "dflash_generate", "greedy_generate", "StopStreaming", "encode_messages",
     "encode_prompt", "GenResult", "NGramIndex", "PRESETS", "DFLASH_PRESETS", "REGISTRY", "resolve", "resolve_mode",
-    "apply_wired_limit", "DEFAULT_TARGET", "DEFAULT_DRAFTER",
+    "apply_wired_limit", "DEFAULT_TARGET", "DEFAULT_DRAFTER", "SpecSlots", "batch_spec_generate",
+    "batch_generate_baseline", "batchable",
 ]

@@ -52,6 +52,28 @@ def ingest_context(d, target_hidden: torch.Tensor, cache: PagedKVCache, n_valid=
         ops.lens_add(cache.seq_lens, n_valid, 1)
 
 
+def ingest_rows(d, fused: torch.Tensor, cache: PagedKVCache, n_valid: torch.Tensor) -> None:
+    """Batched context append for rows 0 .. B-1 of a multi-row drafter cache: fused [B, W,
+    n_tap*H] bf16 holds each row's W candidate positions (at its own cached length); row b
+    keeps n_valid[b] + 1 of them (n_valid device int32 [B]), the rest lies past its length
+    and is overwritten by the next append."""
+    c = d.config
+    B, W = fused.shape[0], fused.shape[1]
+    if B * W > MAX_ROWS:
+        raise ValueError(f"batched context append of {B}x{W} rows > {MAX_ROWS}")
+    H = c.hidden_size
+    th = fused.reshape(B * W, -1)
+    hcp = ops.w8_gemm(ops.pack(th), d.fc, epi=ops.DSK_EPI_PARTIAL)
+    xc = ops.act_pack(M=B * W, K=H, part=hcp, norm_w=d.hidden_norm, eps=c.rms_norm_eps)
+    for l, L in enumerate(d.layers):
+        kv = ops.w8_gemm(xc, L.kv_view(d.args), epi=ops.DSK_EPI_PARTIAL)
+        k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
+        ops.qkv_rope_append(kv, B, W, 0, c.num_key_value_heads, c.head_dim, None, L.k_norm, c.rms_norm_eps,
+                            d.inv_freq, cache.seq_lens, cache.block_table, cache.page, cache.kv_dtype, k_pool,
+                            v_pool, k_sb, v_sb, None)
+    ops.lens_add(cache.seq_lens[:B], n_valid, 1)
+
+
 def block_layers(d, h: torch.Tensor, B: int, bs: int, cache: PagedKVCache, scale: float) -> torch.Tensor:
     """Run drafter ``d``'s decoder layers (2-norm Qwen3 layout) over the block rows h [B*bs, H]
     (bf16, updated in place) attending to context ++ block; returns h before the final norm."""

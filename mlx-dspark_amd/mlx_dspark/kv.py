@@ -142,3 +142,64 @@ class PagedKVCache(list):
         if self.kv_dtype == DSK_KV_U8:
             t += sum(x.numel() * 4 for x in self.k_sb + self.v_sb)
         return t
+
+    # ---- rows of a multi-row cache (continuous batching)
+    def row(self, b: int) -> "RowCache":
+        """A one-row cache over row b: same pools, views of row b's block table and device
+        length. Every single-row op (prefill, forward, drafter ingest) runs on it unchanged."""
+        return RowCache(self, b)
+
+    def row_pages(self, b: int) -> list[int]:
+        return [int(x) for x in self.block_table[b].tolist()]
+
+    def set_row_pages(self, b: int, pages: list[int]) -> None:
+        """Point row b's logical pages at physical pages (shared read-only prefix pages first,
+        then the row's own pages). Every entry must be a valid page of the pool."""
+        if len(pages) != self.max_pages or min(pages) < 0 or max(pages) >= self.n_pages:
+            raise ValueError("a block-table row needs max_pages valid page indices")
+        self.block_table[b].copy_(torch.tensor(pages, dtype=torch.int32))
+
+    def swap_rows(self, a: int, b: int) -> None:
+        """Exchange two rows' block tables and lengths (slot compaction is metadata only)."""
+        if a == b:
+            return
+        idx = torch.tensor([b, a], device=self.block_table.device)
+        self.block_table[[a, b]] = self.block_table[idx]
+        self.seq_lens[[a, b]] = self.seq_lens[idx]
+        self.lengths[a], self.lengths[b] = self.lengths[b], self.lengths[a]
+
+    def set_row_length(self, b: int, n: int) -> None:
+        if n < 0 or n > self.max_ctx:
+            raise ValueError(f"row length {n} outside [0, {self.max_ctx}]")
+        self.lengths[b] = int(n)
+        self.seq_lens[b].fill_(int(n))
+
+
+class RowCache(PagedKVCache):
+    """Row b of a PagedKVCache seen as a B = 1 cache (shares the parent's pools)."""
+
+    def __init__(self, parent: PagedKVCache, b: int):  # noqa: no super().__init__: nothing is allocated
+        list.__init__(self, (LayerView(self, l) for l in range(parent.n_layers)))
+        self.parent, self.b = parent, int(b)
+        for name in ("n_layers", "n_kv", "head_dim", "page", "max_pages", "max_ctx", "kv_dtype", "n_pages",
+                     "k", "v", "k_sb", "v_sb"):
+            setattr(self, name, getattr(parent, name))
+        self.B = 1
+        self.block_table = parent.block_table[self.b:self.b + 1]
+        self.seq_lens = parent.seq_lens[self.b:self.b + 1]
+
+    @property
+    def lengths(self):
+        return [self.parent.lengths[self.b]]
+
+    @lengths.setter
+    def lengths(self, v):
+        self.parent.lengths[self.b] = int(list(v)[0])
+
+    @property
+    def layer_offsets(self):
+        return [self.parent.lengths[self.b]] * self.n_layers
+
+    @layer_offsets.setter
+    def layer_offsets(self, v):
+        pass
