@@ -75,6 +75,9 @@ int dsk_w8_repack(const uint8_t* q, const uint16_t* scales, const uint16_t* bias
  * dsk_act_pack builds it, fusing what precedes every projection of a decoder layer:
  *   v = part ? sum_{s < nsplit} part[s][m][k] : 0      (fp32 partial sums of a split-K
  *                                                       GEMM, slice stride M*K, in order)
+ *   part_norm_w != NULL (gemma sandwich norms: the post-attention / post-feedforward norm of
+ *   the projection output before the residual add):
+ *     v = bf16((bf16(v) * rsqrt(mean_k(bf16(v)^2) + eps)) * part_norm_w[k])
  *   v = h ? (part ? bf16(h[m][k] + v) : h[m][k]) : bf16(v)    (residual add; h updated in
  *                                                               place when part != NULL)
  *   copy[m][k] = v                                     (copy != NULL: hidden-state tap)
@@ -86,9 +89,9 @@ int dsk_w8_repack(const uint8_t* q, const uint16_t* scales, const uint16_t* bias
  * multiples of 8, 16-byte aligned pointers; out may be NULL (h update / copy only).
  * ------------------------------------------------------------------------------------- */
 size_t dsk_act_pack_bytes(int M, int64_t K);
-int dsk_act_pack(const float* part, int nsplit, uint16_t* h, int64_t ldh, uint16_t* copy,
-                 int64_t ldc, int M, int64_t K, const uint16_t* norm_w, float eps, uint16_t* out,
-                 dsk_stream_t stream);
+int dsk_act_pack(const float* part, int nsplit, const uint16_t* part_norm_w, uint16_t* h,
+                 int64_t ldh, uint16_t* copy, int64_t ldc, int M, int64_t K,
+                 const uint16_t* norm_w, float eps, uint16_t* out, dsk_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------
  * W8 skinny GEMM: y[M, N] = x[M, K] . deq(W)[N, K]^T
@@ -274,6 +277,15 @@ int dsk_markov_block(const float* base, int64_t ldb, int B, int cap, int64_t V, 
  * plus each row's draft prefix. */
 int dsk_logits_penalize(float* logits, int64_t ldl, int R, const int32_t* row_ptr,
                         const int32_t* ids, const float* vals, dsk_stream_t stream);
+
+/* Per-token log-probabilities of committed tokens (OpenAI logprobs): for each row r of
+ * logits [R][V] (row stride ldl, fp32), lse = max + log(sum exp(x - max)) (the raw target
+ * distribution, independent of temperature and penalties), chosen[r] = x[tokens[r]] - lse,
+ * and the top_k (0..64) largest entries as (top_ids, top_vals = x - lse) [R][top_k], ordered by
+ * value descending then index ascending. Replaces _logprobs_for_block
+ * (src/mlx_dspark/generate.py:149-176). */
+int dsk_row_logprobs(const float* logits, int64_t ldl, int R, int64_t V, const int32_t* tokens,
+                     int top_k, float* chosen, int32_t* top_ids, float* top_vals, dsk_stream_t stream);
 
 #ifdef __cplusplus
 }

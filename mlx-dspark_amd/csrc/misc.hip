@@ -16,9 +16,101 @@ __global__ void penalize_kernel(float* __restrict__ logits, int64_t ldl, const i
   for (int j = row_ptr[r] + threadIdx.x; j < row_ptr[r + 1]; j += blockDim.x) logits[(int64_t)r * ldl + ids[j]] -= vals[j];
 }
 
+// One workgroup per row: a max / sum-of-exp pass for the log-normaliser, then top_k
+// selection passes, each taking the largest entry that ranks below the previous pick in the
+// order (value descending, index ascending), so ties resolve to the lowest index.
+constexpr int kLpThreads = 1024;
+
+__device__ __forceinline__ bool lp_before(float va, int64_t ia, float vb, int64_t ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+__global__ __launch_bounds__(kLpThreads) void row_logprobs_kernel(const float* __restrict__ logits, int64_t ldl,
+                                                                  int64_t V, const int32_t* __restrict__ tokens,
+                                                                  int top_k, float* __restrict__ chosen,
+                                                                  int32_t* __restrict__ top_ids,
+                                                                  float* __restrict__ top_vals) {
+  __shared__ float sv[kLpThreads / 64];
+  __shared__ int64_t si[kLpThreads / 64];
+  const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const float* x = logits + (int64_t)r * ldl;
+  float m = -__builtin_inff();
+  for (int64_t j = tid; j < V; j += kLpThreads) m = fmaxf(m, x[j]);
+  m = wave_max(m);
+  if (lane == 0) sv[wv] = m;
+  __syncthreads();
+  m = -__builtin_inff();
+  for (int i = 0; i < kLpThreads / 64; ++i) m = fmaxf(m, sv[i]);
+  __syncthreads();
+  float se = 0.0f;
+  for (int64_t j = tid; j < V; j += kLpThreads) se += expf(x[j] - m);
+  se = wave_sum(se);
+  if (lane == 0) sv[wv] = se;
+  __syncthreads();
+  se = 0.0f;
+  for (int i = 0; i < kLpThreads / 64; ++i) se += sv[i];
+  const float lse = m + logf(se);
+  if (tid == 0) {
+    int64_t t = tokens[r];
+    t = t < 0 ? 0 : (t >= V ? V - 1 : t);
+    chosen[r] = x[t] - lse;
+  }
+  float pv = __builtin_inff();
+  int64_t pi = -1;
+  for (int k = 0; k < top_k; ++k) {
+    float bv = -__builtin_inff();
+    int64_t bi = V;
+    for (int64_t j = tid; j < V; j += kLpThreads) {
+      const float v = x[j];
+      if (lp_before(pv, pi, v, j) && lp_before(v, j, bv, bi)) {
+        bv = v;
+        bi = j;
+      }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int64_t oi = __shfl_xor(bi, o, 64);
+      if (lp_before(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    __syncthreads();
+    if (lane == 0) {
+      sv[wv] = bv;
+      si[wv] = bi;
+    }
+    __syncthreads();
+    bv = sv[0];
+    bi = si[0];
+    for (int i = 1; i < kLpThreads / 64; ++i)
+      if (lp_before(sv[i], si[i], bv, bi)) {
+        bv = sv[i];
+        bi = si[i];
+      }
+    if (tid == 0) {
+      top_ids[(int64_t)r * top_k + k] = (int32_t)(bi < V ? bi : 0);
+      top_vals[(int64_t)r * top_k + k] = bi < V ? bv - lse : -__builtin_inff();
+    }
+    pv = bv;
+    pi = bi;
+  }
+}
+
 }  // namespace dsk
 
 using namespace dsk;
+
+extern "C" int dsk_row_logprobs(const float* logits, int64_t ldl, int R, int64_t V, const int32_t* tokens,
+                                int top_k, float* chosen, int32_t* top_ids, float* top_vals, dsk_stream_t stream) {
+  DSK_REQUIRE(logits && tokens && chosen && R > 0 && V > 0 && ldl >= V, "dsk_row_logprobs: bad arguments");
+  DSK_REQUIRE(top_k >= 0 && top_k <= 64 && (top_k == 0 || (top_ids && top_vals)),
+              "dsk_row_logprobs: top_k=%d outside [0, 64] or no output", top_k);
+  hipLaunchKernelGGL(row_logprobs_kernel, dim3((unsigned)R), dim3(kLpThreads), 0, as_stream(stream), logits, ldl, V,
+                     tokens, top_k, chosen, top_ids, top_vals);
+  DSK_LAUNCH_CHECK("dsk_row_logprobs");
+  return DSK_OK;
+}
 
 extern "C" int dsk_logits_penalize(float* logits, int64_t ldl, int R, const int32_t* row_ptr, const int32_t* ids,
                                    const float* vals, dsk_stream_t stream) {

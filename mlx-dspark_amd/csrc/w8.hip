@@ -132,6 +132,7 @@ struct PackArgs {
   const uint16_t* norm_w;
   float eps;
   uint16_t* out;       // packed, or null
+  const uint16_t* res_norm_w;  // RMSNorm of the partial sum before the residual add, or null
 };
 
 template <int NV, int MAXS>
@@ -156,25 +157,64 @@ __global__ __launch_bounds__(kPackThreads) void act_pack_kernel(PackArgs a) {
       ph[i][s] = *reinterpret_cast<const f32x4*>(p + 4);
     }
   }
-  // ---- residual sum in split order, rounded once
+  // block-wide sum (red is reused: barriers on both sides)
+  auto block_sum = [&](float x) {
+    x = wave_sum(x);
+    __syncthreads();
+    if ((tid & 63) == 0) red[tid >> 6] = x;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPackThreads / 64; ++i) t += red[i];
+    return t;
+  };
+  // ---- partial sum in split order
+  float fv[NV][8];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    float f[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = 0.0f;
+    for (int e = 0; e < 8; ++e) fv[i][e] = 0.0f;
 #pragma unroll
     for (int s = 0; s < MAXS; ++s) {
       if (s >= S) break;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        f[e] += pl[i][s][e];
-        f[4 + e] += ph[i][s][e];
+        fv[i][e] += pl[i][s][e];
+        fv[i][4 + e] += ph[i][s][e];
       }
     }
+  }
+  // ---- sandwich norm: the projection output (rounded to bf16) normed before the residual add
+  if (a.res_norm_w && S) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = tid + (int64_t)i * kPackThreads;
+      if (c >= nchunk) continue;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        fv[i][e] = round_bf16(fv[i][e]);
+        ss = fmaf(fv[i][e], fv[i][e], ss);
+      }
+    }
+    const float r1 = rsqrtf(block_sum(ss) / (float)a.K + a.eps);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = min(tid + (int64_t)i * kPackThreads, nchunk - 1);
+      const u32x4 w1 = *reinterpret_cast<const u32x4*>(a.res_norm_w + c * 8);
+      const uint16_t* g = reinterpret_cast<const uint16_t*>(&w1);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) fv[i][e] = round_bf16((fv[i][e] * r1) * bf16_to_f32(g[e]));
+    }
+  }
+  // ---- residual add, rounded once
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
     uint16_t o[8];
     const uint16_t* hh = reinterpret_cast<const uint16_t*>(&hv[i]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = a.h ? (S ? f32_to_bf16(bf16_to_f32(hh[e]) + f[e]) : hh[e]) : f32_to_bf16(f[e]);
+    for (int e = 0; e < 8; ++e)
+      o[e] = a.h ? (S ? f32_to_bf16(bf16_to_f32(hh[e]) + fv[i][e]) : hh[e]) : f32_to_bf16(fv[i][e]);
     v[i] = *reinterpret_cast<const u32x4*>(o);
   }
   float r = 1.0f;
@@ -191,13 +231,7 @@ __global__ __launch_bounds__(kPackThreads) void act_pack_kernel(PackArgs a) {
         ss = fmaf(f, f, ss);
       }
     }
-    ss = wave_sum(ss);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kPackThreads / 64; ++i) tot += red[i];
-    r = rsqrtf(tot / (float)a.K + a.eps);
+    r = rsqrtf(block_sum(ss) / (float)a.K + a.eps);
   }
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -563,8 +597,9 @@ extern "C" size_t dsk_act_pack_bytes(int M, int64_t K) {
   return (size_t)((M + 15) / 16) * (size_t)K * 32;
 }
 
-extern "C" int dsk_act_pack(const float* part, int nsplit, uint16_t* h, int64_t ldh, uint16_t* copy, int64_t ldc,
-                            int M, int64_t K, const uint16_t* norm_w, float eps, uint16_t* out, dsk_stream_t stream) {
+extern "C" int dsk_act_pack(const float* part, int nsplit, const uint16_t* part_norm_w, uint16_t* h, int64_t ldh,
+                            uint16_t* copy, int64_t ldc, int M, int64_t K, const uint16_t* norm_w, float eps,
+                            uint16_t* out, dsk_stream_t stream) {
   DSK_REQUIRE(part || h, "dsk_act_pack: needs partial sums or an input h");
   DSK_REQUIRE(out || copy || (h && part), "dsk_act_pack: no output");
   DSK_REQUIRE(!part || (nsplit > 0 && nsplit <= kPackMaxSplits), "dsk_act_pack: nsplit=%d outside [1, %d]", nsplit,
@@ -576,9 +611,11 @@ extern "C" int dsk_act_pack(const float* part, int nsplit, uint16_t* h, int64_t 
               "dsk_act_pack: K=%lld must be a multiple of 64 <= %d", (long long)K, 6 * 8 * kPackThreads);
   DSK_REQUIRE(!h || (ldh >= K && ldh % 8 == 0), "dsk_act_pack: bad ldh");
   DSK_REQUIRE(!copy || (ldc >= K && ldc % 8 == 0), "dsk_act_pack: bad ldc");
-  DSK_REQUIRE((((uintptr_t)part | (uintptr_t)h | (uintptr_t)copy | (uintptr_t)norm_w | (uintptr_t)out) & 15) == 0,
+  DSK_REQUIRE((((uintptr_t)part | (uintptr_t)h | (uintptr_t)copy | (uintptr_t)norm_w | (uintptr_t)out |
+                (uintptr_t)part_norm_w) & 15) == 0,
               "dsk_act_pack: pointers must be 16-byte aligned");
-  PackArgs a{part, nsplit, h, ldh, copy, ldc, M, K, norm_w, eps, out};
+  DSK_REQUIRE(!part_norm_w || part, "dsk_act_pack: part_norm_w needs partial sums");
+  PackArgs a{part, nsplit, h, ldh, copy, ldc, M, K, norm_w, eps, out, part_norm_w};
   DSK_REQUIRE(pack_launch(a, as_stream(stream)), "dsk_act_pack: no kernel for K=%lld with %d slices", (long long)K,
               nsplit);
   DSK_LAUNCH_CHECK("dsk_act_pack");

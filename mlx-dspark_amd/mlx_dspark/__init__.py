@@ -13,7 +13,7 @@ from .generate import (GenResult, StopStreaming, dflash_generate, encode_message
                        greedy_generate, speculative_generate)
 from .load import (DEFAULT_DRAFTER, DEFAULT_TARGET, DFLASH_PRESETS, PRESETS, REGISTRY, apply_wired_limit,
                    load_dflash, load_dflash_pair, load_drafter, load_pair, load_target, resolve, resolve_mode)
-from .lookup import NGramIndex
+from .lookup import NGramIndex, lookup_generate
 from .model import DSparkDrafter, Gemma4DSparkDrafter
 from .target import Target
 
@@ -21,7 +21,7 @@ __all__ = [
     "DSparkConfig", "DSparkDrafter", "Gemma4DSparkDrafter", "DFlashConfig", "DFlashDraftModel", "Target",
     "load_pair", "load_drafter", "load_dflash", "load_target", "load_dflash_pair",
     "speculative_generate", "dflash_generate", "greedy_generate", "StopStreaming", "encode_messages",
-    "encode_prompt", "GenResult", "NGramIndex", "PRESETS", "DFLASH_PRESETS", "REGISTRY", "resolve", "resolve_mode",
+    "encode_prompt", "GenResult", "NGramIndex", "lookup_generate", "PRESETS", "DFLASH_PRESETS", "REGISTRY", "resolve", "resolve_mode",
     "apply_wired_limit", "DEFAULT_TARGET", "DEFAULT_DRAFTER", "SpecSlots", "batch_spec_generate",
     "batch_generate_baseline", "batchable",
 ]

@@ -24,8 +24,8 @@ SIGNATURES: dict[str, tuple] = {
     "dsk_w8_repack": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p,
                               c_void_p]),
     "dsk_act_pack_bytes": (c_size_t, [c_int, c_int64]),
-    "dsk_act_pack": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_void_p, c_int64, c_int, c_int64, c_void_p, c_float,
-                             c_void_p, c_void_p]),
+    "dsk_act_pack": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int, c_int64, c_void_p,
+                             c_float, c_void_p, c_void_p]),
     "dsk_w8_gemm_splits": (c_int, [c_int, c_int64, c_int64]),
     "dsk_w8_gemm": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int, c_void_p, c_int, c_int64,
                             c_void_p, c_int64, c_float, c_void_p]),
@@ -56,6 +56,8 @@ SIGNATURES: dict[str, tuple] = {
     "dsk_markov_block": (c_int, [c_void_p, c_int64, c_int, c_int, c_int64, c_int, c_void_p, c_void_p, c_void_p,
                                  c_void_p, c_void_p, c_void_p, c_float, c_float, c_int, c_uint64, c_uint32, c_void_p,
                                  c_void_p, c_void_p, c_size_t, c_void_p]),
+    "dsk_row_logprobs": (c_int, [c_void_p, c_int64, c_int, c_int64, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
+                                 c_void_p]),
     "dsk_logits_penalize": (c_int, [c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
 }
 

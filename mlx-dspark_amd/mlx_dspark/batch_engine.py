@@ -34,11 +34,12 @@ from .kv import PagedKVCache
 
 
 def batchable(target) -> bool:
-    """True when the target runs the batched path: the engine's dense Qwen3-layout targets
-    (per-row lengths and block tables are native to its kernels)."""
+    """True when the target runs the batched path: both target layouts of this engine (per-row
+    lengths, block tables and sliding windows are native to its kernels; the reference falls
+    back to its serial engine for gemma)."""
     if getattr(target, "is_vlm", False):
         return False
-    return getattr(target, "family", "qwen3") in ("qwen3",)
+    return getattr(target, "family", "qwen3") in ("qwen3", "gemma4")
 
 
 def _as_list(x, B):

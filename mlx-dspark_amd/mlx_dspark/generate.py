@@ -179,14 +179,38 @@ def _seed64(seed) -> int:
     return 0x5EED if seed is None else int(seed) & ((1 << 64) - 1)
 
 
+def _logprobs_for_block(logits_rows: torch.Tensor, token_ids, top_k: int) -> list:
+    """Per-token logprobs of the committed tokens from the raw target logits rows [P, V] at
+    their positions: [{token_id, logprob, top: [(id, logprob), ...]}] of log_softmax (the
+    target's own distribution, independent of temperature and penalties; top_k 0 = chosen
+    token only; ties ordered by token id). One device kernel, one host sync
+    (src/mlx_dspark/generate.py:149-176)."""
+    P = len(token_ids)
+    if P == 0:
+        return []
+    top_k = max(0, min(int(top_k or 0), logits_rows.shape[-1]))
+    if top_k > 64:
+        raise ValueError(f"logprobs={top_k}: at most 64 alternatives per token")
+    toks = torch.tensor([int(t) for t in token_ids], dtype=torch.int32, device=logits_rows.device)
+    chosen, ids, vals = ops.row_logprobs(logits_rows[:P], toks, top_k)
+    ch = chosen.tolist()
+    if top_k:
+        ids, vals = ids.tolist(), vals.tolist()
+    out = []
+    for i in range(P):
+        e = {"token_id": int(token_ids[i]), "logprob": float(ch[i])}
+        if top_k:
+            e["top"] = [(int(t), float(v)) for t, v in zip(ids[i], vals[i])]
+        out.append(e)
+    return out
+
+
 # ============================================================================ greedy baseline
 def greedy_generate(target_model, tokenizer, prompt: str = "", *, prompt_ids=None, cache=None, reuse_len: int = 0,
                     max_new_tokens: int = 128, temperature: float = 0.0, top_p: float = 1.0, top_k: int = 0,
                     presence_penalty: float = 0.0, frequency_penalty: float = 0.0, logprobs=None, seed=None,
                     apply_chat_template: bool = True, stop=None, on_text=None) -> GenResult:
     """Plain one-token-per-forward decoding of the target (src/mlx_dspark/generate.py:373-465)."""
-    if presence_penalty or frequency_penalty or logprobs is not None:
-        raise NotImplementedError("penalties and logprobs are not supported by this engine yet")
     eos_ids = eos_token_ids(tokenizer)
     ids = prompt_ids if prompt_ids is not None else encode_prompt(tokenizer, prompt, apply_chat_template)
     if cache is None:
@@ -194,26 +218,36 @@ def greedy_generate(target_model, tokenizer, prompt: str = "", *, prompt_ids=Non
         reuse_len = 0
     st = _Streamer(tokenizer, eos_ids, on_text, stop)
     s64 = _seed64(seed)
+    pen = _Penalizer(presence_penalty, frequency_penalty)
+    lp_list: list | None = [] if logprobs is not None else None
     t0 = time.time()
     model = target_model.model
     logits, _ = model.prefill(ids[reuse_len:] if reuse_len else ids, cache)
-    nxt = _pick(logits[0, -1], temperature, top_p, top_k, s64, 0)
-    out_ids = [nxt]
-    st.update(out_ids)
+    row = logits[0, -1:]
+    out_ids: list = []
     cur = torch.empty((1, 1), dtype=torch.int32, device=model.device)
-    step = 1
-    while len(out_ids) < max_new_tokens and nxt not in eos_ids and not st.stopped:
-        cur.fill_(nxt)
-        lg, _ = model.forward(cur, cache, None)
-        nxt = _pick(lg[0, -1], temperature, top_p, top_k, s64, step)
+    step = 0
+    while True:
+        # penalties see every token emitted so far; logprobs read the raw row
+        picked = pen.apply(row.clone(), []) if pen.active else row
+        nxt = _pick(picked[0], temperature, top_p, top_k, s64, step)
         step += 1
         out_ids.append(nxt)
+        pen.add([nxt])
+        if lp_list is not None:
+            lp_list.extend(_logprobs_for_block(row, [nxt], logprobs))
         st.update(out_ids)
+        if len(out_ids) >= max_new_tokens or nxt in eos_ids or st.stopped:
+            break
+        cur.fill_(nxt)
+        lg, _ = model.forward(cur, cache, None)
+        row = lg[0, -1:]
     st.flush()
     secs = time.time() - t0
     return GenResult(text=_final_text(tokenizer, st, out_ids, eos_ids), token_ids=out_ids, num_tokens=len(out_ids),
                      num_rounds=len(out_ids), accept_lengths=[1] * len(out_ids), target_forwards=len(out_ids),
-                     seconds=secs, finish_reason=_finish_reason(out_ids, max_new_tokens, nxt, eos_ids, st))
+                     seconds=secs, finish_reason=_finish_reason(out_ids, max_new_tokens, nxt, eos_ids, st),
+                     logprobs=lp_list)
 
 
 # ============================================================================ DFlash
@@ -477,8 +511,6 @@ def speculative_generate(target_model, tokenizer, drafter, prompt: str = "", *, 
     occurrence instead of drafting when one exists. The default greedy round (no penalties,
     no confidence truncation) runs on the device end to end, graph-replayed, with one host
     sync per round."""
-    if logprobs is not None:
-        raise NotImplementedError("logprobs are not supported by this engine yet")
     cfg = drafter.config
     tap = list(cfg.target_layer_ids)
     k = int(cfg.block_size)
@@ -510,6 +542,9 @@ def speculative_generate(target_model, tokenizer, drafter, prompt: str = "", *, 
     pending = _pick(logits[0, -1], temperature, top_p, top_k, s64, 0xFFFFFFFF)
     pen = _Penalizer(presence_penalty, frequency_penalty)
     pen.add([pending])
+    lp_list: list | None = [] if logprobs is not None else None
+    if lp_list is not None:                                  # the first token came from the prefill row
+        lp_list.extend(_logprobs_for_block(logits[0, -1:], [pending], logprobs))
     index = None
     if lookup_drafts:
         from .lookup import NGramIndex
@@ -539,6 +574,7 @@ def speculative_generate(target_model, tokenizer, drafter, prompt: str = "", *, 
                 rnd = rounds[cap] = _DSparkRound(target_model, drafter, cache, ctx_caches, cap)
             rnd.pending.fill_(pending)
             n, tok, draft = rnd.run(use_graph)
+            raw = rnd.v_logits                                # static buffer, unpenalised
         else:
             q_logits = None
             if lk:
@@ -567,7 +603,8 @@ def speculative_generate(target_model, tokenizer, drafter, prompt: str = "", *, 
             L = len(draft)
             vids = torch.tensor([[pending] + draft], dtype=torch.int32, device=dev)
             v_logits, v_fused = model.forward(vids, cache, tap, advance=False)
-            v_logits = pen.apply(v_logits[0], draft)
+            raw = v_logits[0]
+            v_logits = pen.apply(raw.clone() if pen.active and lp_list is not None else raw, draft)
             n_t = torch.zeros(1, dtype=torch.int32, device=dev)
             tok_t = torch.zeros(1, dtype=torch.int32, device=dev)
             if temperature > 0.0:
@@ -595,6 +632,8 @@ def speculative_generate(target_model, tokenizer, drafter, prompt: str = "", *, 
             if t in eos_ids:
                 break
         pen.add(appended)
+        if lp_list is not None and appended:                  # raw rows at the committed positions
+            lp_list.extend(_logprobs_for_block(raw[:len(appended)], appended, logprobs))
         if index is not None:
             index.extend(appended)
         pending = out_ids[-1]
@@ -607,4 +646,4 @@ def speculative_generate(target_model, tokenizer, drafter, prompt: str = "", *, 
     return GenResult(text=_final_text(tokenizer, st, out_ids, eos_ids), token_ids=out_ids, num_tokens=len(out_ids),
                      num_rounds=len(accept_lengths), accept_lengths=accept_lengths, target_forwards=target_forwards,
                      seconds=secs, finish_reason=_finish_reason(out_ids, max_new_tokens, pending, eos_ids, st),
-                     lookup_rounds=lookup_rounds)
+                     lookup_rounds=lookup_rounds, logprobs=lp_list)

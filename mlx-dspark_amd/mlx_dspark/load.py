@@ -24,12 +24,16 @@ REGISTRY = [
      "dflash": "synthetic/dflash-qwen3-8b", "ram": "~9 GB"},
     {"id": "tiny", "target": "synthetic/tiny", "dspark": "synthetic/dspark-tiny",
      "dflash": "synthetic/dflash-tiny", "ram": "~1 MB"},
+    {"id": "gemma-12b", "target": "synthetic/gemma-12b", "dspark": "synthetic/dspark-gemma-12b",
+     "ram": "~13 GB"},
+    {"id": "tiny-gemma", "target": "synthetic/tiny-gemma", "dspark": "synthetic/dspark-tiny-gemma", "ram": "~2 MB"},
 ]
-PRESETS = {"qwen3": {"target": "synthetic/qwen3-0.6b", "drafter": "synthetic/dspark-qwen3-0.6b"}}
+PRESETS = {"qwen3": {"target": "synthetic/qwen3-0.6b", "drafter": "synthetic/dspark-qwen3-0.6b"},
+           "gemma4": {"target": "synthetic/gemma-12b", "drafter": "synthetic/dspark-gemma-12b"}}
 DFLASH_PRESETS = {"qwen3": {"target": "synthetic/qwen3-8b", "drafter": "synthetic/dflash-qwen3-8b"}}
 DEFAULT_TARGET = PRESETS["qwen3"]["target"]
 DEFAULT_DRAFTER = PRESETS["qwen3"]["drafter"]
-_FAMILY_ALIASES = {"qwen3": "synthetic/qwen3-0.6b"}
+_FAMILY_ALIASES = {"qwen3": "synthetic/qwen3-0.6b", "gemma4": "synthetic/gemma-12b"}
 
 
 def _registry_entry(target: str):
@@ -105,7 +109,7 @@ def load_dflash(repo_or_path: str, *, quantize: bool = True, bits: int = 8, grou
         raise ValueError(f"{repo_or_path!r} is not a DFlash drafter name")
     tkey = key[len("dflash-"):]
     if target_args is None:
-        target_args = TargetArgs(**synthetic.TARGETS[tkey])
+        target_args = synthetic.target_args(tkey)
     return synthetic.build_dflash(target_args, seed=seed, keep_mlx=keep_mlx)
 
 
@@ -124,7 +128,7 @@ def load_drafter(repo_or_path: str = DEFAULT_DRAFTER, *, quantize: bool = True, 
     if target_args is None:
         if tkey not in synthetic.TARGETS:
             raise ValueError(f"unknown synthetic target {tkey!r} for drafter {repo_or_path!r}")
-        target_args = TargetArgs(**synthetic.TARGETS[tkey])
+        target_args = synthetic.target_args(tkey)
     return synthetic.build_dspark(target_args, seed=seed, keep_mlx=keep_mlx, **shape)
 
 

@@ -40,3 +40,90 @@ class NGramIndex:
             if draft:
                 return draft
         return []
+
+
+def lookup_generate(target_model, tokenizer, prompt: str = "", *, prompt_ids=None, cache=None, reuse_len: int = 0,
+                    max_new_tokens: int = 128, max_draft_tokens: int = 6, ngram_min: int = 3, ngram_max: int = 4,
+                    temperature: float = 0.0, top_p: float = 1.0, top_k: int = 0, seed=None,
+                    apply_chat_template: bool = True, stop=None, on_text=None):
+    """Prompt-lookup speculative decoding, batch 1, no drafter model (src/mlx_dspark/lookup.py:92-202).
+
+    Each round verifies the n-gram continuation the index proposes ([pending] + draft in one
+    target forward) and accepts on the device: greedy is the argmax-match prefix plus one
+    token (the target's greedy stream), temperature > 0 is speculative sampling with a
+    point-mass proposal at each drafted token (an exact sample of the truncated target
+    distribution). With no proposal the round is a plain one-token step. cache / reuse_len
+    reuse a prefix exactly as in greedy_generate."""
+    import time
+
+    import torch
+
+    from . import ops
+    from .generate import (GenResult, _final_text, _finish_reason, _pick, _seed64, _Streamer, encode_prompt,
+                           eos_token_ids)
+    eos_ids = eos_token_ids(tokenizer)
+    ids = prompt_ids if prompt_ids is not None else encode_prompt(tokenizer, prompt, apply_chat_template)
+    model = target_model.model
+    if cache is None:
+        cache = target_model.make_cache(max_ctx=len(ids) + max_new_tokens + max_draft_tokens + 8)
+        reuse_len = 0
+    elif reuse_len and cache.lengths[0] != reuse_len:
+        raise ValueError(f"reused cache holds {cache.lengths[0]} tokens, reuse_len={reuse_len}")
+    st = _Streamer(tokenizer, eos_ids, on_text, stop)
+    s64 = _seed64(seed)
+    index = NGramIndex(min_n=ngram_min, max_n=ngram_max, max_draft=max(1, max_draft_tokens))
+    index.extend(ids)
+    dev = model.device
+    V = model.args.vocab_size
+
+    t0 = time.time()
+    logits, _ = model.prefill(ids[reuse_len:] if reuse_len else ids, cache)
+    pending = _pick(logits[0, -1], temperature, top_p, top_k, s64, 0xFFFFFFFF)
+    out_ids = [pending]
+    index.extend([pending])
+    accept_lengths: list = []
+    target_forwards = 1
+    n_t = torch.zeros(1, dtype=torch.int32, device=dev)
+    tok_t = torch.zeros(1, dtype=torch.int32, device=dev)
+    r = lookup_rounds = 0
+    st.update(out_ids)
+    while len(out_ids) < max_new_tokens and pending not in eos_ids and not st.stopped:
+        draft = index.propose()
+        if cache.lengths[0] + 1 + len(draft) > cache.max_ctx:
+            break
+        if not draft:
+            lg, _ = model.forward(torch.tensor([[pending]], dtype=torch.int32, device=dev), cache, None)
+            committed = [_pick(lg[0, -1], temperature, top_p, top_k, s64, r)]
+        else:
+            lookup_rounds += 1
+            L = len(draft)
+            vids = torch.tensor([[pending] + draft], dtype=torch.int32, device=dev)
+            d_t = vids[:, 1:].contiguous()
+            v_logits, _ = model.forward(vids, cache, None, advance=False)
+            if temperature > 0.0:
+                ops.accept_sample(v_logits.view(1, L + 1, V), None, d_t, temperature, top_p, top_k, seed=s64,
+                                  offset=r, seq_lens=cache.seq_lens, n_out=n_t, token_out=tok_t)
+            else:
+                ops.accept_greedy(v_logits.view(1, L + 1, V), d_t, seq_lens=cache.seq_lens, n_out=n_t,
+                                  token_out=tok_t)
+            n, tok = int(n_t.item()), int(tok_t.item())
+            cache.note_lengths([cache.lengths[0] + n + 1])
+            committed = draft[:n] + [tok]
+        r += 1
+        target_forwards += 1
+        accept_lengths.append(len(committed))
+        appended = []
+        for t in committed:
+            out_ids.append(t)
+            appended.append(t)
+            if t in eos_ids:
+                break
+        index.extend(appended)
+        pending = out_ids[-1]
+        st.update(out_ids)
+    st.flush()
+    secs = time.time() - t0
+    return GenResult(text=_final_text(tokenizer, st, out_ids, eos_ids), token_ids=out_ids, num_tokens=len(out_ids),
+                     num_rounds=len(accept_lengths), accept_lengths=accept_lengths, target_forwards=target_forwards,
+                     seconds=secs, finish_reason=_finish_reason(out_ids, max_new_tokens, pending, eos_ids, st),
+                     lookup_rounds=lookup_rounds)

@@ -18,7 +18,7 @@ from ._hip import (DSK_BF16, DSK_EPI_GEGLU, DSK_EPI_PARTIAL, DSK_EPI_STORE, DSK_
 
 __all__ = [
     "W8Weight", "W8Table", "Workspace", "Packed", "act_pack", "pack", "w8_gemm", "w8_embed",
-    "qkv_rope_append", "attention", "qkv_attention", "accept_greedy", "accept_sample", "sample_rows", "lens_add",
+    "qkv_rope_append", "attention", "qkv_attention", "row_logprobs", "accept_greedy", "accept_sample", "sample_rows", "lens_add",
     "rope_inv_freq", "DSK_EPI_STORE", "DSK_EPI_SWIGLU", "DSK_EPI_GEGLU", "DSK_EPI_PARTIAL", "DSK_KV_BF16",
     "DSK_KV_U8",
 ]
@@ -169,10 +169,11 @@ def _rows_ok(t: torch.Tensor) -> bool:
 
 def act_pack(*, M: int, K: int, part: torch.Tensor | None = None, h: torch.Tensor | None = None,
              copy: torch.Tensor | None = None, norm_w: torch.Tensor | None = None, eps: float = 1e-6,
-             out: Packed | bool | None = True) -> Packed | None:
+             out: Packed | bool | None = True, part_norm_w: torch.Tensor | None = None) -> Packed | None:
     """Sum split-K partials [S, M, K] (f32) into the residual stream h (bf16 [M, K], in place),
     optionally copy the result (tap), RMSNorm it and pack it for the next GEMM (see
-    dsk_act_pack). out=True allocates the packed output, None/False skips it."""
+    dsk_act_pack). part_norm_w RMSNorms the partial sum before the residual add (gemma's
+    sandwich norms). out=True allocates the packed output, None/False skips it."""
     if h is not None and not _rows_ok(h):
         raise ValueError("act_pack: h needs unit column stride, 16-byte aligned rows")
     if copy is not None and not _rows_ok(copy):
@@ -184,7 +185,8 @@ def act_pack(*, M: int, K: int, part: torch.Tensor | None = None, h: torch.Tenso
         out = Packed.empty(M, K, dev)
     elif out is False:
         out = None
-    call("dsk_act_pack", ptr(part), 0 if part is None else part.shape[0], ptr(h), 0 if h is None else h.stride(0),
+    call("dsk_act_pack", ptr(part), 0 if part is None else part.shape[0], ptr(part_norm_w), ptr(h),
+         0 if h is None else h.stride(0),
          ptr(copy), 0 if copy is None else copy.stride(0), M, K, ptr(norm_w), float(eps),
          ptr(None if out is None else out.data), stream_ptr())
     return out
@@ -411,3 +413,20 @@ def logits_penalize(logits: torch.Tensor, row_ptr: torch.Tensor, ids: torch.Tens
     """logits[r, ids[j]] -= vals[j] for j in [row_ptr[r], row_ptr[r+1]) (CSR rows, in place)."""
     R = logits.shape[0]
     call("dsk_logits_penalize", ptr(logits), logits.stride(0), R, ptr(row_ptr), ptr(ids), ptr(vals), stream_ptr())
+
+
+# ----------------------------------------------------------------------------- logprobs
+def row_logprobs(logits: torch.Tensor, tokens: torch.Tensor, top_k: int = 0):
+    """logits [R, V] f32 (unit column stride), tokens int32 [R] -> (chosen f32 [R], top_ids
+    int32 [R, top_k], top_vals f32 [R, top_k]) of log_softmax(logits) (see dsk_row_logprobs)."""
+    R, V = logits.shape
+    if logits.dtype != torch.float32 or logits.stride(1) != 1:
+        logits = logits.float().contiguous()
+    dev = logits.device
+    tokens = tokens.to(dev, torch.int32).contiguous()
+    chosen = torch.empty(R, dtype=torch.float32, device=dev)
+    ids = torch.empty((R, max(top_k, 1)), dtype=torch.int32, device=dev)
+    vals = torch.empty((R, max(top_k, 1)), dtype=torch.float32, device=dev)
+    call("dsk_row_logprobs", ptr(logits), logits.stride(0), R, V, ptr(tokens), int(top_k), ptr(chosen), ptr(ids),
+         ptr(vals), stream_ptr())
+    return chosen, ids[:, :top_k], vals[:, :top_k]

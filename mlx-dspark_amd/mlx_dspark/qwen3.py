@@ -9,8 +9,14 @@ forward over the same public Qwen3 architecture:
     logits = lm_head(RMSNorm(h))       (tied: embed_tokens.as_linear)
 with the residual stream captured after the tapped layers. Every projection is W8 (affine
 group 64, bf16 scale/bias); activations are bf16 between kernels, accumulation is fp32,
-logits are fp32. GeLU MLPs, an embedding scale, sliding-window layers and a final logit
-soft-cap are supported; gemma's sandwich norms are not.
+logits are fp32.
+
+The same forward runs the Gemma-style layout (model_type gemma*): embedding scaled by
+sqrt(hidden) (rounded to bf16), sandwich norms (the attention and MLP outputs are RMSNorm-ed
+before their residual adds, fused into the act_pack that follows each projection), GeGLU
+(tanh-approximated GeLU), sliding-window layers with their own RoPE base, a query scale of
+query_pre_attn_scalar ** -0.5 and a final logit soft-cap. Norm gains are stored as the
+effective multipliers (gemma's 1 + w).
 """
 
 from __future__ import annotations
@@ -48,6 +54,11 @@ class TargetArgs:
     layer_types: tuple = field(default_factory=tuple)   # "full_attention" | "sliding_attention"
     final_logit_softcapping: float | None = None
     query_pre_attn_scalar: float | None = None    # attention scale = this ** -0.5 when set
+    rope_local_base_freq: float | None = None     # RoPE base of the sliding-window layers
+
+    @property
+    def sandwich_norms(self) -> bool:
+        return self.model_type.startswith("gemma")
 
     @property
     def n_qkv(self) -> int:
@@ -58,8 +69,11 @@ class TargetArgs:
         s = self.query_pre_attn_scalar or self.head_dim
         return float(s) ** -0.5
 
+    def is_sliding(self, layer: int) -> bool:
+        return bool(self.layer_types) and self.layer_types[layer] == "sliding_attention"
+
     def window(self, layer: int) -> int:
-        if self.layer_types and self.layer_types[layer] == "sliding_attention" and self.sliding_window:
+        if self.is_sliding(layer) and self.sliding_window:
             return int(self.sliding_window)
         return 0
 
@@ -74,6 +88,8 @@ class LayerWeights:
     post_norm: torch.Tensor
     q_norm: torch.Tensor   # bf16 [head_dim]
     k_norm: torch.Tensor
+    attn_out_norm: torch.Tensor | None = None  # sandwich norms: attention output before its add
+    ff_out_norm: torch.Tensor | None = None    # sandwich norms: MLP output before its add
 
     def kv_view(self, args: TargetArgs) -> W8Weight:
         """The [k | v] rows of the fused projection, as a zero-copy W8 view."""
@@ -94,6 +110,8 @@ class Qwen3W8:
         self.norm = norm
         self.device = norm.device
         self.inv_freq = ops.rope_inv_freq(args.head_dim, args.rope_theta, self.device)
+        self.inv_freq_local = (ops.rope_inv_freq(args.head_dim, args.rope_local_base_freq, self.device)
+                               if args.rope_local_base_freq else self.inv_freq)
         self.act_epi = DSK_EPI_SWIGLU if args.hidden_act == "silu" else DSK_EPI_GEGLU
 
     # ------------------------------------------------------------------ cache
@@ -130,17 +148,19 @@ class Qwen3W8:
         eps = a.rms_norm_eps
         qkv = ops.w8_gemm(x, L.qkv, epi=ops.DSK_EPI_PARTIAL)
         k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
-        q = ops.qkv_rope_append(qkv, B, W, nq, nkv, hd, L.q_norm, L.k_norm, eps, self.inv_freq,
+        inv_freq = self.inv_freq_local if a.is_sliding(l) else self.inv_freq
+        q = ops.qkv_rope_append(qkv, B, W, nq, nkv, hd, L.q_norm, L.k_norm, eps, inv_freq,
                                 cache.seq_lens, cache.block_table, cache.page, cache.kv_dtype,
                                 k_pool, v_pool, k_sb, v_sb)
         o = ops.attention(q, B, W, nq, nkv, hd, a.attn_scale, cache.seq_lens, cache.max_ctx,
                           cache.block_table, cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb,
                           causal=causal, window=a.window(l), packed=True)
         op = ops.w8_gemm(o, L.o, epi=ops.DSK_EPI_PARTIAL)
-        x = ops.act_pack(M=M, K=H, part=op, h=h, norm_w=L.post_norm, eps=eps)
+        x = ops.act_pack(M=M, K=H, part=op, h=h, norm_w=L.post_norm, eps=eps, part_norm_w=L.attn_out_norm)
         act = ops.w8_gemm(x, L.gate_up, epi=self.act_epi)
         dp = ops.w8_gemm(act, L.down, epi=ops.DSK_EPI_PARTIAL)
-        return ops.act_pack(M=M, K=H, part=dp, h=h, copy=copy, norm_w=next_norm, eps=eps, out=want_next)
+        return ops.act_pack(M=M, K=H, part=dp, h=h, copy=copy, norm_w=next_norm, eps=eps, out=want_next,
+                            part_norm_w=L.ff_out_norm)
 
     def forward(self, ids: torch.Tensor, cache: PagedKVCache, tap=None, *, advance: bool = True,
                 logits: str = "all", logits_out: torch.Tensor | None = None,

@@ -34,7 +34,28 @@ TARGETS = {
     "tiny-tied": dict(hidden_size=256, num_hidden_layers=3, intermediate_size=512,
                       num_attention_heads=4, num_key_value_heads=2, head_dim=128, vocab_size=1024,
                       tie_word_embeddings=True),
+    # Gemma-style 12B shape: sandwich norms, GeGLU, 5 sliding (1024) : 1 global layers, soft-cap 30
+    "gemma-12b": dict(model_type="gemma4_text", hidden_size=3840, num_hidden_layers=48, intermediate_size=15360,
+                      num_attention_heads=16, num_key_value_heads=8, head_dim=256, vocab_size=262144,
+                      tie_word_embeddings=True, hidden_act="gelu_tanh", sliding_window=1024,
+                      final_logit_softcapping=30.0, query_pre_attn_scalar=256.0, rope_local_base_freq=10_000.0),
+    "tiny-gemma": dict(model_type="gemma4_text", hidden_size=512, num_hidden_layers=6, intermediate_size=1024,
+                       num_attention_heads=4, num_key_value_heads=2, head_dim=256, vocab_size=1024,
+                       tie_word_embeddings=True, hidden_act="gelu_tanh", sliding_window=32,
+                       final_logit_softcapping=30.0, query_pre_attn_scalar=256.0, rope_local_base_freq=10_000.0),
 }
+
+
+def target_args(name: str) -> TargetArgs:
+    """TargetArgs of a named synthetic shape (Gemma-style shapes get their embedding scale,
+    bf16(sqrt(hidden)), and the 5:1 sliding/global layer pattern)."""
+    spec = {"model_type": "qwen3", **TARGETS[name]}
+    a = TargetArgs(**spec)
+    if a.sandwich_norms:
+        a.embed_scale = float(torch.tensor(a.hidden_size ** 0.5).to(torch.bfloat16))
+        a.layer_types = tuple("full_attention" if (l + 1) % 6 == 0 else "sliding_attention"
+                              for l in range(a.num_hidden_layers))
+    return a
 
 
 def _seed(seed: int, name: str) -> int:
@@ -78,7 +99,7 @@ def build_target(name_or_args, seed: int = 0, device="cuda", keep_mlx: bool = Fa
     if isinstance(name_or_args, TargetArgs):
         args = name_or_args
     else:
-        args = TargetArgs(model_type="qwen3", **TARGETS[name_or_args])
+        args = target_args(name_or_args)
     device = torch.device(device)
     H, I = args.hidden_size, args.intermediate_size
     nq, nkv, hd = args.num_attention_heads, args.num_key_value_heads, args.head_dim
@@ -91,7 +112,9 @@ def build_target(name_or_args, seed: int = 0, device="cuda", keep_mlx: bool = Fa
             gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx, paired=True),
             down=w8(H, I, seed, p + "down", device, keep_mlx),
             in_norm=ones(H, device), post_norm=ones(H, device),
-            q_norm=qk_norm(hd, device), k_norm=qk_norm(hd, device)))
+            q_norm=qk_norm(hd, device), k_norm=qk_norm(hd, device),
+            attn_out_norm=ones(H, device) if args.sandwich_norms else None,
+            ff_out_norm=ones(H, device) if args.sandwich_norms else None))
     embed = w8_table(args.vocab_size, H, seed, "embed_tokens", device)
     if args.tie_word_embeddings:
         lm_head = W8Weight.from_mlx(embed.q, embed.s, embed.b)

@@ -26,7 +26,8 @@ class Target:
         self.model = model
         self.tokenizer = tokenizer
         self.is_vlm = False
-        self.family = getattr(model.args, "model_type", "qwen3")
+        mt = getattr(model.args, "model_type", "qwen3")
+        self.family = "gemma4" if mt.startswith("gemma") else mt
         if kv_bits not in (None, 8):
             raise ValueError(f"kv_bits={kv_bits}: the engine supports 8-bit KV (or bf16)")
         if kv_group_size != 64:
@@ -67,7 +68,10 @@ class Target:
         checks structure (windowed layers cannot be tapped by one causal mask in the
         reference's generic loop) and that both give the same logits on 4 tokens."""
         a = self.model.args
-        if a.layer_types and any(t != "full_attention" for t in a.layer_types):
+        # The reference refuses windowed layers because its tap replays mlx_lm's loop with one
+        # causal mask; this engine's forward is the model itself (per-layer windows included),
+        # so only a family it does not implement is refused.
+        if a.layer_types and any(t != "full_attention" for t in a.layer_types) and not a.sandwich_norms:
             raise ValueError(f"hidden-state tap unsupported for model_type {self.family!r}: it uses "
                              f"windowed/alternating attention layers")
         ids = [[1, 2, 3, 4]]

@@ -8,7 +8,11 @@ Restates (reference paths):
     mlx_lm (external); it follows the public Qwen3 architecture: RMSNorm -> q/k/v
     projections -> per-head q/k RMSNorm -> rotate-half RoPE (theta from config) -> GQA
     attention, causal with offset (mask grid of tests/test_batch_engine.py:87-103) ->
-    o_proj + residual; RMSNorm -> down(silu(gate) * up) + residual.
+    o_proj + residual; RMSNorm -> down(silu(gate) * up) + residual. The Gemma-style layout
+    (public Gemma 3 architecture; the reference runs it through mlx_vlm, target.py:53-55)
+    adds the embedding scale, sandwich norms (the o_proj and down outputs RMSNorm-ed before
+    their residual adds), GeGLU with tanh GeLU, sliding-window layers with their own RoPE base
+    and a final tanh soft-cap on the logits.
   - KV append / trim as metadata (src/mlx_dspark/batch_engine.py:132-163).
   - DFlashDraftModel.__call__ (src/mlx_dspark/dflash_model.py:100-208).
 Every intermediate is rounded to bf16 where a bf16 MLX graph produces a bf16 array, except
@@ -64,11 +68,20 @@ def sdpa(q, K, V, scale, mask=None):
     return out
 
 
-def causal_mask(offset: int, W: int) -> torch.Tensor:
-    """[W, offset + W] boolean: query i (absolute offset + i) sees key j iff j <= offset + i."""
+def causal_mask(offset: int, W: int, window: int = 0) -> torch.Tensor:
+    """[W, offset + W] boolean: query i (absolute offset + i) sees key j iff j <= offset + i,
+    and, for a sliding-window layer, j > offset + i - window."""
     j = torch.arange(offset + W)[None, :]
     i = torch.arange(W)[:, None]
-    return j <= offset + i
+    m = j <= offset + i
+    if window:
+        m &= j > offset + i - window
+    return m
+
+
+def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
+    """tanh-approximated GeLU (gemma's gelu_pytorch_tanh)."""
+    return 0.5 * x * (1.0 + torch.tanh(0.7978845608028654 * (x + 0.044715 * x * x * x)))
 
 
 def deq(wobj) -> torch.Tensor:
@@ -104,6 +117,9 @@ class OracleLayer:
         self.post_norm = L.post_norm.float().cpu()
         self.q_norm = L.q_norm.float().cpu()
         self.k_norm = L.k_norm.float().cpu()
+        an, fn = getattr(L, "attn_out_norm", None), getattr(L, "ff_out_norm", None)
+        self.attn_out_norm = None if an is None else an.float().cpu()
+        self.ff_out_norm = None if fn is None else fn.float().cpu()
         self.nq, self.nkv, self.hd = nq, nkv, hd
 
 
@@ -134,33 +150,45 @@ class OracleTarget:
         ids = torch.as_tensor(ids).reshape(-1).long()
         W = ids.numel()
         nq, nkv, hd, eps = a.num_attention_heads, a.num_key_value_heads, a.head_dim, a.rms_norm_eps
-        h = bf(self.embed[ids] * a.embed_scale)
+        h = bf(bf(self.embed[ids]) * a.embed_scale)   # bf16 embedding rows, then the bf16 scale
         pos = torch.arange(self.offset, self.offset + W)
+        gelu = getattr(a, "hidden_act", "silu") != "silu"
         captured = []
         for l, L in enumerate(self.layers):
+            win = a.window(l)
+            theta = (a.rope_local_base_freq or a.rope_theta) if a.is_sliding(l) else a.rope_theta
             x = bf(rmsnorm(h, L.in_norm, eps))
             qkv = bf(x @ L.wq.T)
             q = qkv[:, : nq * hd].view(W, nq, hd)
             k = qkv[:, nq * hd:(nq + nkv) * hd].view(W, nkv, hd)
             v = qkv[:, (nq + nkv) * hd:].view(W, nkv, hd)
-            q = bf(rope(bf(rmsnorm(q, L.q_norm, eps)).transpose(0, 1), pos, a.rope_theta).transpose(0, 1))
-            k = bf(rope(bf(rmsnorm(k, L.k_norm, eps)).transpose(0, 1), pos, a.rope_theta).transpose(0, 1))
+            q = bf(rope(bf(rmsnorm(q, L.q_norm, eps)).transpose(0, 1), pos, theta).transpose(0, 1))
+            k = bf(rope(bf(rmsnorm(k, L.k_norm, eps)).transpose(0, 1), pos, theta).transpose(0, 1))
             if self.kv_bits == 8:
                 k, v = kv_quant_roundtrip(k), kv_quant_roundtrip(v)
             self.K[l] = torch.cat([self.K[l], k])
             self.V[l] = torch.cat([self.V[l], v])
-            o = bf(sdpa(q, self.K[l], self.V[l], a.attn_scale, causal_mask(self.offset, W)))
-            h = bf(h + self.rr(o.reshape(W, -1) @ L.wo.T))
+            o = bf(sdpa(q, self.K[l], self.V[l], a.attn_scale, causal_mask(self.offset, W, win)))
+            if L.attn_out_norm is not None:     # sandwich: norm the projection output, then add
+                h = bf(h + bf(rmsnorm(bf(o.reshape(W, -1) @ L.wo.T), L.attn_out_norm, eps)))
+            else:
+                h = bf(h + self.rr(o.reshape(W, -1) @ L.wo.T))
             x = bf(rmsnorm(h, L.post_norm, eps))
             gu = bf(x @ L.wgu.T)
             I = gu.shape[1] // 2
             g, u = gu[:, :I], gu[:, I:]
-            act = bf(bf(g * torch.sigmoid(g)) * u)
-            h = bf(h + self.rr(act @ L.wd.T))
+            act = bf(bf(gelu_tanh(g) if gelu else g * torch.sigmoid(g)) * u)
+            if L.ff_out_norm is not None:
+                h = bf(h + bf(rmsnorm(bf(act @ L.wd.T), L.ff_out_norm, eps)))
+            else:
+                h = bf(h + self.rr(act @ L.wd.T))
             if l in tap:
                 captured.append(h)
         self.offset += W
         logits = bf(rmsnorm(h, self.norm, eps)) @ self.lm_head.T
+        cap = getattr(a, "final_logit_softcapping", None)
+        if cap:
+            logits = torch.tanh(logits / cap) * cap
         fused = torch.cat(captured, dim=-1) if captured else None
         return logits, fused
 

@@ -94,6 +94,34 @@ def test_act_pack_residual_norm(dev, M, K, S):
     assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30)
 
 
+@pytest.mark.parametrize("M,K,S", [(16, 3840, 2), (9, 512, 8), (1, 4096, 1)])
+def test_act_pack_sandwich_norm(dev, M, K, S):
+    """part_norm_w: the partial sum (rounded to bf16) is RMSNorm-ed before the residual add."""
+    from mlx_dspark.ops import act_pack
+    g = torch.Generator().manual_seed(M * 3 + K + S)
+    h0 = (torch.randn(M, K, generator=g) * 3).to(torch.bfloat16)
+    w1 = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16)
+    w2 = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16)
+    part = torch.randn(S, M, K, generator=g)
+    h = h0.to(dev).clone()
+    x = act_pack(M=M, K=K, part=part.to(dev), h=h, norm_w=w2.to(dev), eps=1e-6, part_norm_w=w1.to(dev))
+    acc = np.zeros((M, K), np.float32)
+    for s_ in range(S):
+        acc = acc + part[s_].numpy()
+    ob = O.bf16_round(acc).astype(np.float64)
+    r1 = 1.0 / np.sqrt((ob ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    n1 = O.bf16_round(((ob * r1) * w1.float().numpy()).astype(np.float32))
+    v = O.bf16_round(h0.float().numpy() + n1)
+    got_h = h.float().cpu().numpy()
+    # one bf16 ulp of the normed term (fp32 vs float64 rsqrt) may move the sum by one ulp
+    assert np.all(np.abs(got_h - v) <= np.abs(v) * 2.0 ** -7 + np.abs(n1) * 2.0 ** -7 + 1e-30)
+    vf = got_h.astype(np.float64)
+    r2 = 1.0 / np.sqrt((vf ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    ref = O.bf16_round(((vf * r2) * w2.float().numpy()).astype(np.float32))
+    got = x.unpack().float().cpu().numpy()
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30)
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 64, 256), (9, 256, 1024), (16, 6144, 4096), (17, 512, 4096),
                                    (36, 4096, 1024), (64, 128, 3072), (16, 192, 4096), (16, 4096, 12288),
                                    (9, 151936 // 8, 1024), (16, 1024, 3072), (3, 2048, 256), (64, 4096, 4096),

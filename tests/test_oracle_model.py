@@ -61,3 +61,19 @@ def test_rmsnorm_closed_form():
 def test_normalized_metric_is_scale_invariant():
     a = torch.randn(2, 50)
     assert OM.normalized_maxdiff(a, 3.0 * a) < 1e-5
+
+
+def test_gelu_tanh_matches_library():
+    x = torch.linspace(-6, 6, 1001)
+    ref = torch.nn.functional.gelu(x, approximate="tanh")
+    assert torch.allclose(OM.gelu_tanh(x), ref, atol=1e-6)
+
+
+def test_sliding_window_mask_bruteforce():
+    off, W, win = 7, 4, 3
+    m = OM.causal_mask(off, W, win)
+    for i in range(W):
+        for j in range(off + W):
+            want = (j <= off + i) and (j > off + i - win)
+            assert bool(m[i, j]) == want
+    assert torch.equal(OM.causal_mask(off, W, 0), OM.causal_mask(off, W))
