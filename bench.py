@@ -299,7 +299,7 @@ def main(argv=None) -> int:
         "verify_us": round(verify_us, 1),
         "verify_alg_bytes": int(alg_bytes),
         "verify_roofline_frac": round(verify_frac, 4),
-        "roofline": {"kernel": "w8_gemm_kernel<1, 4, 2, 4, 1> (W8 GEMM, gate_up 24576x4096, M=16, SwiGLU)",
+        "roofline": {"kernel": "w8_gemm_kernel<1, 2, 2, 8, 1, true> (W8 GEMM, gate_up 24576x4096, M=16, SwiGLU)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_GATE_UP,
                      "bytes_per_launch": dom["bytes"], "us_per_launch": dom["us"], "per_shape": shapes},

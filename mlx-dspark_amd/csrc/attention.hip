@@ -424,6 +424,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         vtok[ci][u] = pool_token(a.block_table, a.max_pages, a.page, a.nkv, b, kvh, min(j0 + 2 * kp + u, jmax - 1));
     }
   }
+  // the first tile's queries do not depend on the row length: in flight with it
+  QTile<HD, FUSED> qt;
+  if (wv < ntiles) qtile_load<HD, FUSED>(a, b, kvh, wv, lane, qt);
   const int Lk = min(off + a.W, jmax);
   int j_lo, j_hi;
   if (newsplit) {
@@ -436,8 +439,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     j_hi = min(kend, j_lo + kps);
   }
 
-  QTile<HD, FUSED> qt;
-  if (wv < ntiles) qtile_load<HD, FUSED>(a, b, kvh, wv, lane, qt);
   Chunk8 kc[S::CK], vc[S::CV][2];
   if (!newsplit) {
     // ---- issue every K/V load of the split
@@ -541,24 +542,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const int rq = tile * 16 + (lane & 15);
     const bool qvalid = rq < a.R;
     // ---- scores: lane holds S^T[key = 16h + 4*(lane/16) + r][q = lane % 16]
-    // (all fragments of two key tiles read before their MFMAs: eight LDS reads in flight)
+    // k-step outer, key tile inner: NKT independent accumulators per k-step keep the MFMA
+    // pipe busy, and the next k-step's K fragments are read from LDS while these run
     f32x4 st[NKT];
 #pragma unroll
-    for (int h = 0; h < NKT; h += 2) {
-      bf16x8 kf[2][KS];
+    for (int h = 0; h < NKT; ++h) st[h] = f32x4{0, 0, 0, 0};
+    {
+      bf16x8 kf[2][NKT];
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int h = 0; h < NKT; ++h)
+        kf[0][h] = *reinterpret_cast<const bf16x8*>(ks + (h * 16 + (lane & 15)) * KROW + (lane >> 4) * 8);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
-          kf[u][s] = *reinterpret_cast<const bf16x8*>(ks + ((h + u) * 16 + (lane & 15)) * KROW + s * 32 + (lane >> 4) * 8);
-      __builtin_amdgcn_sched_barrier(0);  // keep the reads grouped ahead of the MFMAs
-      f32x4 acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+      for (int s = 0; s < KS; ++s) {
+        if (s + 1 < KS)
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
+          for (int h = 0; h < NKT; ++h)
+            kf[(s + 1) & 1][h] =
+                *reinterpret_cast<const bf16x8*>(ks + (h * 16 + (lane & 15)) * KROW + (s + 1) * 32 + (lane >> 4) * 8);
+        __builtin_amdgcn_sched_barrier(0);  // the reads stay grouped ahead of this step's MFMAs
 #pragma unroll
-        for (int u = 0; u < 2; ++u) acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[u][s], qf[s], acc[u], 0, 0, 0);
-      st[h] = acc[0];
-      st[h + 1] = acc[1];
+        for (int h = 0; h < NKT; ++h) st[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[s & 1][h], qf[s], st[h], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     // visible keys of this lane's query: [k_first, k_last] (branch-free mask below)
     const int qpos = off + (qvalid ? rq / a.G : 0);
@@ -598,29 +604,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
     // ---- O^T[d][q] = V^T . P^T: A = V^T rows d*16 + lane%16, keys in pb's order
-    // (all fragments of two d tiles read before their MFMAs)
+    // (key chunk outer, d tile inner: DT independent accumulators, next chunk's reads ahead)
     f32x4 o[DT];
 #pragma unroll
-    for (int d = 0; d < DT; d += 2) {
-      u32x4 vv[2][KEYS / 32];
+    for (int d = 0; d < DT; ++d) o[d] = f32x4{0, 0, 0, 0};
+    {
+      auto vfrag = [&](int d, int c) {
+        const uint16_t* vr = vt16 + (d * 16 + (lane & 15)) * VROW + 32 * c + (lane >> 4) * 4;
+        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
+        return __builtin_bit_cast(bf16x8, (u32x4{lo.x, lo.y, hi.x, hi.y}));
+      };
+      bf16x8 vv[2][DT];
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int c = 0; c < KEYS / 32; ++c) {
-          const uint16_t* vr = vt16 + ((d + u) * 16 + (lane & 15)) * VROW + 32 * c + (lane >> 4) * 4;
-          const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
-          vv[u][c] = u32x4{lo.x, lo.y, hi.x, hi.y};
-        }
+      for (int d = 0; d < DT; ++d) vv[0][d] = vfrag(d, 0);
       __builtin_amdgcn_sched_barrier(0);
-      f32x4 acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
-      for (int c = 0; c < KEYS / 32; ++c)
+      for (int c = 0; c < KEYS / 32; ++c) {
+        if (c + 1 < KEYS / 32)
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-          acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vv[u][c]), pb[c], acc[u], 0, 0, 0);
-      o[d] = acc[0];
-      o[d + 1] = acc[1];
+          for (int d = 0; d < DT; ++d) vv[(c + 1) & 1][d] = vfrag(d, c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int d = 0; d < DT; ++d) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv[c & 1][d], pb[c], o[d], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     if (!qvalid) continue;
     const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;

@@ -313,33 +313,42 @@ __device__ __forceinline__ void gemm_store_gated(const GemmArgs& a, int m, int64
   reinterpret_cast<uint16_t*>(a.y)[apack_index(m, col, a.N / 128)] = f32_to_bf16(act * ub);
 }
 
-// One batch of U groups: all loads first, then the MFMAs. Padding rows of the packed
-// activation hold arbitrary values; their outputs are never stored.
+// One batch of U groups: the weight, scale/bias and activation registers of U consecutive
+// groups for NT tiles. Padding rows of the packed activation hold arbitrary values; their
+// outputs are never stored.
 template <int MT, int NT, int U>
-__device__ __forceinline__ void gemm_batch(const GemmArgs& a, int64_t t0, int64_t g0, int lane,
-                                           f32x4 (&acc)[MT][NT]) {
+struct Batch {
   u32x4 wv[U][NT];
   uint32_t sv[U][NT];
   u32x4 xv[U][MT][2];
+};
+
+template <int MT, int NT, int U>
+__device__ __forceinline__ void batch_load(const GemmArgs& a, int64_t t0, int64_t g0, int lane,
+                                           Batch<MT, NT, U>& r) {
 #pragma unroll
   for (int c = 0; c < U; ++c)
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       const int64_t tg = (t0 + j) * a.G + g0 + c;
-      wv[c][j] = __builtin_nontemporal_load(&a.wt[tg * 64 + lane]);
+      r.wv[c][j] = __builtin_nontemporal_load(&a.wt[tg * 64 + lane]);
     }
 #pragma unroll
   for (int c = 0; c < U; ++c)
 #pragma unroll
-    for (int j = 0; j < NT; ++j) sv[c][j] = a.sb[((t0 + j) * a.G + g0 + c) * 16 + (lane & 15)];
+    for (int j = 0; j < NT; ++j) r.sv[c][j] = a.sb[((t0 + j) * a.G + g0 + c) * 16 + (lane & 15)];
 #pragma unroll
   for (int c = 0; c < U; ++c)
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
       const u32x4* px = a.xp + (((int64_t)i * a.G + g0 + c) * 64 + lane) * 2;
-      xv[c][i][0] = px[0];
-      xv[c][i][1] = px[1];
+      r.xv[c][i][0] = px[0];
+      r.xv[c][i][1] = px[1];
     }
+}
+
+template <int MT, int NT, int U>
+__device__ __forceinline__ void batch_compute(const Batch<MT, NT, U>& r, f32x4 (&acc)[MT][NT]) {
   const u32x4 ones_u = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
   const bf16x8 ones = __builtin_bit_cast(bf16x8, ones_u);
 #pragma unroll
@@ -347,23 +356,23 @@ __device__ __forceinline__ void gemm_batch(const GemmArgs& a, int64_t t0, int64_
     f32x4 X[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
-      X[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[c][i][0]), ones,
+      X[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.xv[c][i][0]), ones,
                                                      f32x4{0, 0, 0, 0}, 0, 0, 0);
-      X[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[c][i][1]), ones, X[i], 0, 0, 0);
+      X[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.xv[c][i][1]), ones, X[i], 0, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       bf16x8 b0, b1;
-      u8x16_to_bf16(wv[c][j], b0, b1);
-      const float s = bf16_to_f32((uint16_t)(sv[c][j] & 0xffffu));
-      const float bb = bf16_to_f32((uint16_t)(sv[c][j] >> 16));
+      u8x16_to_bf16(r.wv[c][j], b0, b1);
+      const float s = bf16_to_f32((uint16_t)(r.sv[c][j] & 0xffffu));
+      const float bb = bf16_to_f32((uint16_t)(r.sv[c][j] >> 16));
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
-        f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[c][i][0]), b0,
+        f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.xv[c][i][0]), b0,
                                                           f32x4{0, 0, 0, 0}, 0, 0, 0);
-        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, xv[c][i][1]), b1, t, 0, 0, 0);
+        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.xv[c][i][1]), b1, t, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(s, t[r], fmaf(bb, X[i][r], acc[i][j][r]));
+        for (int q = 0; q < 4; ++q) acc[i][j][q] = fmaf(s, t[q], fmaf(bb, X[i][q], acc[i][j][q]));
       }
     }
   }
@@ -373,8 +382,8 @@ __device__ __forceinline__ void gemm_batch(const GemmArgs& a, int64_t t0, int64_
 // split's batches round-robin, each accumulating all NT tiles (every activation fragment a
 // wave loads feeds NT tiles), then reduce through LDS in wave order.
 // EK: the epilogue family (0 store, 1 gated, 2 split-K partial) as a template parameter, so each
-// family is its own (smaller) kernel
-template <int MT, int NT, int U, int WAVES, int EK>
+// family is its own (smaller) kernel. PF: software-pipelined batch loads (two register sets).
+template <int MT, int NT, int U, int WAVES, int EK, bool PF>
 __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -390,7 +399,30 @@ __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
 
-  for (int bt = wave; bt < nbatch; bt += WAVES) gemm_batch<MT, NT, U>(a, t0, g_lo + (int64_t)bt * U, lane, acc);
+  if constexpr (PF) {
+    // software pipeline over the wave's batches (bt = wave, wave + WAVES, ...): the next
+    // batch's loads are issued before the current one is computed, alternating two register sets
+    if (wave < nbatch) {
+      Batch<MT, NT, U> ra, rb;
+      batch_load<MT, NT, U>(a, t0, g_lo + (int64_t)wave * U, lane, ra);
+      for (int bt = wave;;) {
+        if (bt + WAVES < nbatch) batch_load<MT, NT, U>(a, t0, g_lo + (int64_t)(bt + WAVES) * U, lane, rb);
+        batch_compute<MT, NT, U>(ra, acc);
+        bt += WAVES;
+        if (bt >= nbatch) break;
+        if (bt + WAVES < nbatch) batch_load<MT, NT, U>(a, t0, g_lo + (int64_t)(bt + WAVES) * U, lane, ra);
+        batch_compute<MT, NT, U>(rb, acc);
+        bt += WAVES;
+        if (bt >= nbatch) break;
+      }
+    }
+  } else {
+    for (int bt = wave; bt < nbatch; bt += WAVES) {
+      Batch<MT, NT, U> r;
+      batch_load<MT, NT, U>(a, t0, g_lo + (int64_t)bt * U, lane, r);
+      batch_compute<MT, NT, U>(r, acc);
+    }
+  }
 
   constexpr int NOUT = MT * NT * 256;
   __shared__ float red[WAVES][NOUT];
@@ -450,6 +482,7 @@ __global__ void w8_embed_kernel(const int32_t* __restrict__ ids, const uint8_t* 
 struct GemmPlan {
   int nt, u, waves, sk;
   int64_t gpb;
+  bool pf;
 };
 
 // NT tiles per workgroup amortise the activation reads (L2 -> CU traffic is the limit once
@@ -479,39 +512,53 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi) {
   p.gpb = bps * p.u;
   p.waves = (bps >= 8 && bps < 12) ? 8 : 4;
   if (!partial && slabs < 128) p.waves = bps >= 32 ? 16 : (bps >= 8 ? 8 : 4);
+  p.pf = false;
+  // wide gated projections (>= 1024 tiles): pairs of tiles, 8 waves, pipelined loads
+  if (gated && MT == 1 && tiles >= 1024 && tiles % 2 == 0) {
+    p.nt = 2;
+    p.sk = 1;
+    p.gpb = G;
+    p.waves = 8;
+    p.pf = true;
+  }
   while ((size_t)p.waves * MT * p.nt * 1024 > 65536) p.waves /= 2;  // LDS of the reduction
   return p;
 }
 
-template <int MT, int NT, int U, int WAVES>
+template <int MT, int NT, int U, int WAVES, bool PF>
 static bool launch_gemm_t(const GemmArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)(a.n_slabs * a.SK)), blk(WAVES * 64);
   if (a.epi == DSK_EPI_PARTIAL) {
-    hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 2>), grid, blk, 0, st, a);
+    hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 2, PF>), grid, blk, 0, st, a);
   } else if (a.epi == DSK_EPI_STORE) {
-    hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 0>), grid, blk, 0, st, a);
+    hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 0, PF>), grid, blk, 0, st, a);
   } else {
     if constexpr (NT % 2 != 0) return false;  // gated tiles come in gate|up pairs
-    else hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 1>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 1, PF>), grid, blk, 0, st, a);
   }
   return true;
 }
 
-template <int MT, int NT, int U>
+template <int MT, int NT, int U, bool PF>
 static bool launch_gemm_w(const GemmArgs& a, int waves, hipStream_t st) {
   constexpr int max_waves = 65536 / (MT * NT * 1024);  // LDS of the cross-wave reduction
   switch (waves) {
-    case 4: if constexpr (max_waves >= 4) return launch_gemm_t<MT, NT, U, 4>(a, st); return false;
-    case 8: if constexpr (max_waves >= 8) return launch_gemm_t<MT, NT, U, 8>(a, st); return false;
-    case 16: if constexpr (max_waves >= 16) return launch_gemm_t<MT, NT, U, 16>(a, st); return false;
+    case 4: if constexpr (max_waves >= 4) return launch_gemm_t<MT, NT, U, 4, PF>(a, st); return false;
+    case 8: if constexpr (max_waves >= 8) return launch_gemm_t<MT, NT, U, 8, PF>(a, st); return false;
+    case 16: if constexpr (max_waves >= 16) return launch_gemm_t<MT, NT, U, 16, PF>(a, st); return false;
   }
   return false;
 }
 
 static bool launch_gemm(const GemmArgs& a, int MT, const GemmPlan& p, hipStream_t st) {
+  if (p.pf) {  // the pipelined variant is built for the shapes the planner gives it
+    if (MT == 1 && p.nt == 2 && p.u == 2) return launch_gemm_w<1, 2, 2, true>(a, p.waves, st);
+    return false;
+  }
 #define DSK_GEMM_CASE(MT_, NT_, U_) \
-  if (MT == MT_ && p.nt == NT_ && p.u == U_) return launch_gemm_w<MT_, NT_, U_>(a, p.waves, st);
+  if (MT == MT_ && p.nt == NT_ && p.u == U_) return launch_gemm_w<MT_, NT_, U_, false>(a, p.waves, st);
   DSK_GEMM_CASE(1, 1, 2) DSK_GEMM_CASE(1, 2, 2) DSK_GEMM_CASE(1, 4, 2) DSK_GEMM_CASE(1, 8, 2)
+  DSK_GEMM_CASE(1, 3, 2) DSK_GEMM_CASE(1, 6, 2)
   DSK_GEMM_CASE(1, 1, 4) DSK_GEMM_CASE(1, 2, 4) DSK_GEMM_CASE(1, 4, 4)
   DSK_GEMM_CASE(2, 1, 2) DSK_GEMM_CASE(2, 2, 2) DSK_GEMM_CASE(2, 4, 2)
   DSK_GEMM_CASE(3, 1, 2) DSK_GEMM_CASE(3, 2, 2)

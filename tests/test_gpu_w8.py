@@ -166,7 +166,7 @@ def test_gemm_residual_softcap(dev):
 
 
 @pytest.mark.parametrize("M,I,K,act", [(16, 12288, 4096, "silu"), (9, 3072, 1024, "silu"), (40, 512, 1024, "silu"),
-                                       (8, 15360 // 4, 3840, "gelu"), (2, 128, 256, "silu")])
+                                       (8, 15360 // 4, 3840, "gelu"), (2, 128, 256, "silu"), (5, 15360, 3840, "gelu")])
 def test_gemm_gated_epilogue(dev, M, I, K, act):
     from mlx_dspark.ops import DSK_EPI_GEGLU, DSK_EPI_SWIGLU, W8Weight, pack, w8_gemm
     print(f"gated M={M} I={I} K={K} {act}", flush=True)
