@@ -18,6 +18,10 @@
 // forms its own queries (sum of the split-K partial slices, RMSNorm, RoPE) while its K/V loads
 // are in flight, and the workgroup whose key range holds the new tokens also normalises,
 // rotates and quantises their K/V, appends them to the pool and uses them straight from LDS.
+#include <stdlib.h>
+
+#include <algorithm>
+
 #include "common.h"
 
 namespace dsk {
@@ -205,19 +209,20 @@ struct AttnArgs {
   uint16_t* out;
   int out_packed;
   int nsplit;
-  int kps;           // keys per (context) split, a multiple of 16, <= Split<HD>::KEYS
+  int kps;           // keys per (context) split: a whole number of LDS blocks (Split<HD>::KEYS)
   int fused;         // splits 0 .. nsplit-2: cached keys; split nsplit-1: the new tokens
   uint16_t* part_o;  // [B*nkv][nsplit][R][HD] bf16: the split's o / l
   float* part_ml;    // [B*nkv][nsplit][R][2]: the split's running max m and sum l
 };
 
-// LDS capacity in keys of one split (a workgroup loads its whole split at once; kps = KEYS)
+// page ids one split may span (kps / page + 1), held in LDS
+constexpr int kAttnMaxSplitPages = 256;
+
+// LDS capacity in keys of one block (a split streams kps / KEYS blocks through it)
 template <int HD> struct Split {
   static constexpr int KEYS = HD == 128 ? 128 : 64;
   static constexpr int KROW = HD + 8;    // K rows in LDS (bf16, padded)
   static constexpr int VROW = KEYS + 8;  // V^T rows in LDS (bf16, padded)
-  static constexpr int CK = KEYS * HD / 8 / 256;        // 8-element K chunks per thread
-  static constexpr int CV = (KEYS / 2) * (HD / 8) / 256;  // (2 keys x 8 dims) V chunks per thread
 };
 
 // output row (b, i), head h, dim d: row-major [B*W, nq*HD] or packed
@@ -370,17 +375,24 @@ __device__ __forceinline__ void qtile_finish(const AttnArgs& a, int off, int til
   }
 }
 
-// One workgroup per (row b, kv head, split of KEYS keys): the page-table entries of the whole
-// split are read together with the row length, every K/V load of the split is issued at once,
-// dequantised into LDS (K row-major, V transposed), then each wave takes 16-query tiles
-// through scores, a one-pass softmax and P.V. Splits at or past the row's key count exit
-// before loading K/V (the combine reads only the live ones).
+// One workgroup per (row b, kv head, split of kps keys). A split is nblk blocks of KEYS keys
+// streamed through LDS: each block's K/V chunks are dequantised into LDS (K row-major, V
+// transposed) and, while the waves run scores, a one-pass online softmax and P.V on it, the
+// next block's loads are already in flight. Every wave owns one 16-query tile for the whole
+// split (nblk > 1 needs QT == 1), carrying its running max, sum and output across blocks.
+// Splits at or past the row's key count exit before loading (the combine reads only the live
+// ones).
 // FUSED: splits 0 .. nsplit-2 cover the cached keys [0, seq_lens[b]) and the last split the W
 // new tokens, which it forms from the projection (K RMSNorm + RoPE, append to the pool) while
 // the context splits stream the cache; every workgroup forms its own queries meanwhile.
-template <int HD, int QT, int KVT, bool SOFTCAP, bool FUSED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attention_kernel(AttnArgs a) {
+template <int HD, int QT, int KVT, bool SOFTCAP, bool FUSED, int WPT>
+__global__ __launch_bounds__(256 * WPT) __attribute__((amdgpu_waves_per_eu(1, 2))) void attention_kernel(AttnArgs a) {
   using S = Split<HD>;
+  static_assert(WPT == 1 || (WPT == 2 && QT == 1 && !FUSED), "two waves per tile: one tile per wave, no new-token split");
+  constexpr int NTHR = 256 * WPT;                      // WPT waves per 16-query tile
+  constexpr int CK = S::KEYS * HD / 8 / NTHR;          // 8-element K chunks per thread
+  constexpr int CV = (S::KEYS / 2) * (HD / 8) / NTHR;  // (2 keys x 8 dims) V chunks per thread
+  constexpr int KH = S::KEYS / WPT;                    // keys of a block one wave scores
   constexpr int KEYS = S::KEYS, KROW = S::KROW, VROW = S::VROW;
   constexpr int DT = HD / 16;     // output d tiles
   constexpr int KS = HD / 32;     // k steps of the score MFMA
@@ -405,67 +417,108 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
   asm volatile("" : "+s"(scale), "+s"(softcap), "+s"(causal), "+s"(window), "+s"(nsplit), "+s"(kps));
   asm volatile("" : "+s"(part_o), "+s"(part_ml));
 
-  // ---- independent loads: row length, the split's page-table entries, the first query tile
-  const int off = a.seq_lens[b];
-  int64_t ktok[S::CK], vtok[S::CV][2];
-  if (!newsplit) {
-    const int j0 = split * kps;
+  // page ids of the split's keys, read once into LDS (the blocks after the first then cost no
+  // page-table round trip); pool tokens of the block starting at key j0, clamped into the block
+  // table (keys past the split's end are loaded but zeroed in LDS)
+  __shared__ int pgs[kAttnMaxSplitPages];
+  const int pg0 = (split * kps) / a.page;
+  int64_t ktok[CK], vtok[CV][2];
+  auto tok_of = [&](int j) -> int64_t {
+    j = min(j, jmax - 1);
+    return ((int64_t)pgs[j / a.page - pg0] * a.nkv + kvh) * a.page + (j % a.page);
+  };
+  auto tokens = [&](int j0) {
 #pragma unroll
-    for (int ci = 0; ci < S::CK; ++ci) {
-      const int c = threadIdx.x + ci * 256;
-      const int j = min(j0 + c / (HD / 8), jmax - 1);
-      ktok[ci] = pool_token(a.block_table, a.max_pages, a.page, a.nkv, b, kvh, j);
+    for (int ci = 0; ci < CK; ++ci) {
+      const int c = threadIdx.x + ci * NTHR;
+      ktok[ci] = tok_of(j0 + c / (HD / 8));
     }
 #pragma unroll
-    for (int ci = 0; ci < S::CV; ++ci) {
-      const int kp = (threadIdx.x + ci * 256) % (KEYS / 2);
+    for (int ci = 0; ci < CV; ++ci) {
+      const int kp = (threadIdx.x + ci * NTHR) % (KEYS / 2);
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-        vtok[ci][u] = pool_token(a.block_table, a.max_pages, a.page, a.nkv, b, kvh, min(j0 + 2 * kp + u, jmax - 1));
+      for (int u = 0; u < 2; ++u) vtok[ci][u] = tok_of(j0 + 2 * kp + u);
     }
-  }
-  // the first tile's queries do not depend on the row length: in flight with it
-  QTile<HD, FUSED> qt;
-  if (wv < ntiles) qtile_load<HD, FUSED>(a, b, kvh, wv, lane, qt);
-  const int Lk = min(off + a.W, jmax);
-  int j_lo, j_hi;
-  if (newsplit) {
-    j_lo = off;
-    j_hi = Lk;
-  } else {
-    j_lo = split * kps;
-    const int kend = FUSED ? min(off, jmax) : Lk;  // the fused context splits stop at the cache
-    if (j_lo >= kend) return;
-    j_hi = min(kend, j_lo + kps);
-  }
-
-  Chunk8 kc[S::CK], vc[S::CV][2];
-  if (!newsplit) {
-    // ---- issue every K/V load of the split
+  };
+  Chunk8 kc[CK], vc[CV][2];
+  auto issue = [&]() {
 #pragma unroll
-    for (int ci = 0; ci < S::CK; ++ci) {
-      const int d0 = ((threadIdx.x + ci * 256) % (HD / 8)) * 8;
+    for (int ci = 0; ci < CK; ++ci) {
+      const int d0 = ((threadIdx.x + ci * NTHR) % (HD / 8)) * 8;
       load_chunk<KVT>(a.k_pool, a.k_sb, HD, ktok[ci], d0, kc[ci]);
     }
 #pragma unroll
-    for (int ci = 0; ci < S::CV; ++ci) {
-      const int d0 = ((threadIdx.x + ci * 256) / (KEYS / 2)) * 8;
+    for (int ci = 0; ci < CV; ++ci) {
+      const int d0 = ((threadIdx.x + ci * NTHR) / (KEYS / 2)) * 8;
 #pragma unroll
       for (int u = 0; u < 2; ++u) load_chunk<KVT>(a.v_pool, a.v_sb, HD, vtok[ci][u], d0, vc[ci][u]);
     }
+  };
+  // dequantise the loaded block [j_lo, j_hi) into LDS (keys past j_hi are zeroed: masked, but finite)
+  auto to_lds = [&](int j_lo, int j_hi) {
+#pragma unroll
+    for (int ci = 0; ci < CK; ++ci) {
+      const int c = threadIdx.x + ci * NTHR;
+      const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+      uint16_t h[8];
+      chunk_bf16<KVT>(kc[ci], h);
+      u32x4 w = *reinterpret_cast<const u32x4*>(h);
+      if (j_lo + key >= j_hi) w = u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(ks + key * KROW + d0) = w;
+    }
+#pragma unroll
+    for (int ci = 0; ci < CV; ++ci) {
+      const int c = threadIdx.x + ci * NTHR;
+      const int kp = c % (KEYS / 2), d0 = (c / (KEYS / 2)) * 8;
+      const int j0 = j_lo + 2 * kp;
+      uint16_t h0[8], h1[8];
+      chunk_bf16<KVT>(vc[ci][0], h0);
+      chunk_bf16<KVT>(vc[ci][1], h1);
+      const bool z0 = j0 >= j_hi, z1 = j0 + 1 >= j_hi;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        vt[((d0 + e) * VROW) / 2 + kp] = (uint32_t)(z0 ? 0 : h0[e]) | ((uint32_t)(z1 ? 0 : h1[e]) << 16);
+    }
+  };
+
+  // ---- independent loads: the split's page ids, the first query tile, the row length
+  if (!newsplit) {
+    const int npg = min((split * kps + kps - 1) / a.page, a.max_pages - 1) - pg0 + 1;
+    for (int t = threadIdx.x; t < npg; t += NTHR) pgs[t] = a.block_table[(int64_t)b * a.max_pages + pg0 + t];
+  }
+  const int mytile = wv & 3, half = wv >> 2;  // WPT == 2: waves w and w + 4 share tile w, key halves
+  QTile<HD, FUSED> qt;
+  if (mytile < ntiles) qtile_load<HD, FUSED>(a, b, kvh, mytile, lane, qt);
+  const int off = a.seq_lens[b];
+  __syncthreads();  // the page ids
+  const int Lk = min(off + a.W, jmax);
+  int j_beg, j_end;
+  if (newsplit) {
+    j_beg = off;
+    j_end = Lk;
+  } else {
+    j_beg = split * kps;
+    const int kend = FUSED ? min(off, jmax) : Lk;  // the fused context splits stop at the cache
+    if (j_beg >= kend) return;
+    j_end = min(kend, j_beg + kps);
+  }
+  const int nb = newsplit ? 1 : (j_end - j_beg + KEYS - 1) / KEYS;
+  if (!newsplit) {
+    tokens(j_beg);
+    issue();
   }
   // the first tile's queries while the K/V loads are in flight
   bf16x8 qf[KS];
-  if (wv < ntiles) qtile_finish<HD, FUSED>(a, off, wv, lane, qt, qf);
+  if (mytile < ntiles) qtile_finish<HD, FUSED>(a, off, mytile, lane, qt, qf);
 
   if (newsplit) {
     // ---- the new tokens: zero the tile, then K normed + roped, K/V appended to the pool and
     // the values attention reads written to LDS; a quarter wave per (token, K or V) row, two
     // rows per quarter in flight
-    for (int c = threadIdx.x; c < KEYS * KROW / 8; c += 256) reinterpret_cast<u32x4*>(ks)[c] = u32x4{0, 0, 0, 0};
-    for (int c = threadIdx.x; c < HD * VROW / 8; c += 256) reinterpret_cast<u32x4*>(vt)[c] = u32x4{0, 0, 0, 0};
+    for (int c = threadIdx.x; c < KEYS * KROW / 8; c += NTHR) reinterpret_cast<u32x4*>(ks)[c] = u32x4{0, 0, 0, 0};
+    for (int c = threadIdx.x; c < HD * VROW / 8; c += NTHR) reinterpret_cast<u32x4*>(vt)[c] = u32x4{0, 0, 0, 0};
     __syncthreads();
-    const int n_new = j_hi - j_lo;  // <= W
+    const int n_new = j_end - j_beg;  // <= W
     const int nheads = a.nq + 2 * a.nkv;
     const int quarter = lane >> 4, sub = lane & 15;
     for (int t0 = wv * 4; t0 < 2 * n_new; t0 += 32) {
@@ -478,7 +531,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         live[u] = task < 2 * n_new;
         const int tt = live[u] ? task : 0;
         kk[u] = tt < n_new;
-        jj[u] = j_lo + (kk[u] ? tt : tt - n_new);
+        jj[u] = j_beg + (kk[u] ? tt : tt - n_new);
         const int head = a.nq + (kk[u] ? kvh : a.nkv + kvh);
         load_proj_row<PER16>(a.qkv, a.qkv_splits, (int64_t)a.B * a.W * nheads * HD,
                              ((int64_t)(b * a.W + (jj[u] - off)) * nheads + head) * HD, sub, v[u]);
@@ -489,7 +542,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         norm_rope_row<HD, 16>(v[u], sub, kk[u] ? a.k_norm : nullptr, a.eps, kk[u], a.inv_freq, jj[u]);
         const int64_t tok = pool_token(a.block_table, a.max_pages, a.page, a.nkv, b, kvh, jj[u]);
         kv_store_row<HD, 16>(v[u], sub, a.kv_dtype, kk[u] ? a.k_pool : a.v_pool, kk[u] ? a.k_sb : a.v_sb, tok);
-        const int key = jj[u] - j_lo;
+        const int key = jj[u] - j_beg;
         if (kk[u]) {
           uint16_t h[PER16];
 #pragma unroll
@@ -503,66 +556,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         }
       }
     }
-  } else {
-    // ---- dequantise into LDS (keys past the split's end are zeroed: masked, but finite)
-#pragma unroll
-    for (int ci = 0; ci < S::CK; ++ci) {
-      const int c = threadIdx.x + ci * 256;
-      const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
-      uint16_t h[8];
-      chunk_bf16<KVT>(kc[ci], h);
-      u32x4 w = *reinterpret_cast<const u32x4*>(h);
-      if (j_lo + key >= j_hi) w = u32x4{0, 0, 0, 0};
-      *reinterpret_cast<u32x4*>(ks + key * KROW + d0) = w;
-    }
-#pragma unroll
-    for (int ci = 0; ci < S::CV; ++ci) {
-      const int c = threadIdx.x + ci * 256;
-      const int kp = c % (KEYS / 2), d0 = (c / (KEYS / 2)) * 8;
-      const int j0 = j_lo + 2 * kp;
-      uint16_t h0[8], h1[8];
-      chunk_bf16<KVT>(vc[ci][0], h0);
-      chunk_bf16<KVT>(vc[ci][1], h1);
-      const bool z0 = j0 >= j_hi, z1 = j0 + 1 >= j_hi;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        vt[((d0 + e) * VROW) / 2 + kp] = (uint32_t)(z0 ? 0 : h0[e]) | ((uint32_t)(z1 ? 0 : h1[e]) << 16);
-    }
   }
-  __syncthreads();
 
-#pragma unroll 1
-  for (int t = 0; t < QT; ++t) {
-    const int tile = wv + 4 * t;
-    if (tile >= ntiles) break;
-    if (t > 0) {
-      qtile_load<HD, FUSED>(a, b, kvh, tile, lane, qt);
-      qtile_finish<HD, FUSED>(a, off, tile, lane, qt, qf);
-    }
-    const int rq = tile * 16 + (lane & 15);
-    const bool qvalid = rq < a.R;
+  // running state of this wave's tile across the blocks (one tile per wave when nb > 1)
+  float m_run = -__builtin_inff(), l_run = 0.0f;
+  f32x4 o[DT];
+
+  // scores, one-pass online softmax and P.V of one 16-query tile over the wave's KH keys of the
+  // block in LDS (keys kb .. kb + KH - 1 of the block)
+  constexpr int NKH = KH / 16;  // key tiles of the wave
+  auto block_compute = [&](int j_lo, int j_hi, int rq, bool qvalid, int kb) {
     // ---- scores: lane holds S^T[key = 16h + 4*(lane/16) + r][q = lane % 16]
     // k-step outer, key tile inner: NKT independent accumulators per k-step keep the MFMA
     // pipe busy, and the next k-step's K fragments are read from LDS while these run
-    f32x4 st[NKT];
+    f32x4 st[NKH];
 #pragma unroll
-    for (int h = 0; h < NKT; ++h) st[h] = f32x4{0, 0, 0, 0};
+    for (int h = 0; h < NKH; ++h) st[h] = f32x4{0, 0, 0, 0};
     {
-      bf16x8 kf[2][NKT];
+      const uint16_t* kbase = ks + (kb + (lane & 15)) * KROW + (lane >> 4) * 8;
+      bf16x8 kf[2][NKH];
 #pragma unroll
-      for (int h = 0; h < NKT; ++h)
-        kf[0][h] = *reinterpret_cast<const bf16x8*>(ks + (h * 16 + (lane & 15)) * KROW + (lane >> 4) * 8);
+      for (int h = 0; h < NKH; ++h) kf[0][h] = *reinterpret_cast<const bf16x8*>(kbase + h * 16 * KROW);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         if (s + 1 < KS)
 #pragma unroll
-          for (int h = 0; h < NKT; ++h)
-            kf[(s + 1) & 1][h] =
-                *reinterpret_cast<const bf16x8*>(ks + (h * 16 + (lane & 15)) * KROW + (s + 1) * 32 + (lane >> 4) * 8);
+          for (int h = 0; h < NKH; ++h)
+            kf[(s + 1) & 1][h] = *reinterpret_cast<const bf16x8*>(kbase + h * 16 * KROW + (s + 1) * 32);
         __builtin_amdgcn_sched_barrier(0);  // the reads stay grouped ahead of this step's MFMAs
 #pragma unroll
-        for (int h = 0; h < NKT; ++h) st[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[s & 1][h], qf[s], st[h], 0, 0, 0);
+        for (int h = 0; h < NKH; ++h) st[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[s & 1][h], qf[s], st[h], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -574,12 +598,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       if (window > 0) k_first = qpos - window + 1;
     }
     if (!qvalid) k_last = -1;
-    float mx = -__builtin_inff();
+    float mx = m_run;
 #pragma unroll
-    for (int h = 0; h < NKT; ++h)
+    for (int h = 0; h < NKH; ++h)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int j = j_lo + h * 16 + (lane >> 4) * 4 + r;
+        const int j = j_lo + kb + h * 16 + (lane >> 4) * 4 + r;
         float sc = st[h][r] * scale;
         if (SOFTCAP) sc = tanhf(sc / softcap) * softcap;
         sc = (j >= k_first && j <= k_last) ? sc : -__builtin_inff();
@@ -588,10 +612,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       }
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    // rescale of the previous blocks' sum and output (none on the first block)
+    const float alpha = m_run == -__builtin_inff() ? 0.0f : __expf(m_run - mx);
     float lsum = 0.0f;
-    bf16x8 pb[KEYS / 32];
+    bf16x8 pb[KH / 32];
 #pragma unroll
-    for (int c = 0; c < KEYS / 32; ++c)
+    for (int c = 0; c < KH / 32; ++c)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
@@ -603,14 +629,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         }
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
+    l_run = l_run * alpha + lsum;
+    m_run = mx;
     // ---- O^T[d][q] = V^T . P^T: A = V^T rows d*16 + lane%16, keys in pb's order
     // (key chunk outer, d tile inner: DT independent accumulators, next chunk's reads ahead)
-    f32x4 o[DT];
 #pragma unroll
-    for (int d = 0; d < DT; ++d) o[d] = f32x4{0, 0, 0, 0};
+    for (int d = 0; d < DT; ++d) o[d] *= alpha;
     {
       auto vfrag = [&](int d, int c) {
-        const uint16_t* vr = vt16 + (d * 16 + (lane & 15)) * VROW + 32 * c + (lane >> 4) * 4;
+        const uint16_t* vr = vt16 + (d * 16 + (lane & 15)) * VROW + kb + 32 * c + (lane >> 4) * 4;
         const uint2 lo = *reinterpret_cast<const uint2*>(vr);
         const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
         return __builtin_bit_cast(bf16x8, (u32x4{lo.x, lo.y, hi.x, hi.y}));
@@ -620,8 +647,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       for (int d = 0; d < DT; ++d) vv[0][d] = vfrag(d, 0);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int c = 0; c < KEYS / 32; ++c) {
-        if (c + 1 < KEYS / 32)
+      for (int c = 0; c < KH / 32; ++c) {
+        if (c + 1 < KH / 32)
 #pragma unroll
           for (int d = 0; d < DT; ++d) vv[(c + 1) & 1][d] = vfrag(d, c + 1);
         __builtin_amdgcn_sched_barrier(0);
@@ -630,8 +657,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (!qvalid) continue;
-    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+  };
+
+  // the tile's result: the output itself (one split) or the split's partial o / l and (m, l)
+  auto store_tile = [&](int rq, bool qvalid) {
+    if (!qvalid) return;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
     if (nsplit == 1) {
       const int i = rq / a.G, hl = rq % a.G;
 #pragma unroll
@@ -639,7 +670,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
           a.out[attn_out_index(a, HD, b, i, kvh * a.G + hl, d * 16 + (lane >> 4) * 4 + rr)] = f32_to_bf16(o[d][rr] * inv);
-      continue;
+      return;
     }
     // partial: o / l in bf16 (4 consecutive dims per d tile), (m, l) in fp32
     const size_t prow = ((size_t)bk * nsplit + split) * a.R + rq;
@@ -650,7 +681,79 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       const uint32_t hi = (uint32_t)f32_to_bf16(o[d][2] * inv) | ((uint32_t)f32_to_bf16(o[d][3] * inv) << 16);
       *reinterpret_cast<uint2*>(po + d * 16) = uint2{lo, hi};
     }
-    if (lane < 16) *reinterpret_cast<float2*>(part_ml + prow * 2) = float2{mx, lsum};
+    if (lane < 16) *reinterpret_cast<float2*>(part_ml + prow * 2) = float2{m_run, l_run};
+  };
+
+  if (nb > 1 || QT == 1) {
+    // ---- one tile per wave (WPT waves per tile), blocks streamed: block blk+1's loads fly
+    // while blk is computed
+    const int rq = mytile * 16 + (lane & 15);
+    const bool qvalid = rq < a.R;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) o[d] = f32x4{0, 0, 0, 0};
+#pragma unroll 1
+    for (int blk = 0; blk < nb; ++blk) {
+      const int j_lo = j_beg + blk * KEYS, j_hi = min(j_end, j_lo + KEYS);
+      if (!newsplit) {
+        if (blk > 0) __syncthreads();  // every wave is done with the previous block's LDS
+        to_lds(j_lo, j_hi);
+        if (blk + 1 < nb) {
+          tokens(j_lo + KEYS);
+          issue();
+        }
+      }
+      __syncthreads();
+      if (mytile < ntiles) block_compute(j_lo, j_hi, rq, qvalid, half * KH);
+    }
+    if constexpr (WPT == 2) {
+      static_assert(4 * (DT * 4 + 2) * 64 * sizeof(float) <= KEYS * KROW * sizeof(uint16_t), "merge area");
+      // the second key half's (m, l, o) through LDS (the K tile area) into the first half's waves
+      float* mb = reinterpret_cast<float*>(ks) + mytile * (DT * 4 + 2) * 64 + lane;
+      __syncthreads();  // every wave is done with the last block
+      if (half == 1 && mytile < ntiles) {
+        mb[0] = m_run;
+        mb[64] = l_run;
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mb[(2 + d * 4 + r) * 64] = o[d][r];
+      }
+      __syncthreads();
+      if (half == 1 || mytile >= ntiles) return;
+      const float m1 = mb[0], l1 = mb[64];
+      const float M = fmaxf(m_run, m1);
+      const float a0 = m_run == -__builtin_inff() ? 0.0f : __expf(m_run - M);
+      const float a1 = m1 == -__builtin_inff() ? 0.0f : __expf(m1 - M);
+      l_run = l_run * a0 + l1 * a1;
+      m_run = M;
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[d][r] = o[d][r] * a0 + mb[(2 + d * 4 + r) * 64] * a1;
+    }
+    if (mytile < ntiles) store_tile(rq, qvalid);
+    return;
+  }
+
+  // ---- one block, QT tiles per wave (nb == 1)
+  if (!newsplit) to_lds(j_beg, j_end);
+  __syncthreads();
+#pragma unroll 1
+  for (int t = 0; t < QT; ++t) {
+    const int tile = wv + 4 * t;
+    if (tile >= ntiles) break;
+    if (t > 0) {
+      qtile_load<HD, FUSED>(a, b, kvh, tile, lane, qt);
+      qtile_finish<HD, FUSED>(a, off, tile, lane, qt, qf);
+    }
+    const int rq = tile * 16 + (lane & 15);
+    const bool qvalid = rq < a.R;
+    m_run = -__builtin_inff();
+    l_run = 0.0f;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) o[d] = f32x4{0, 0, 0, 0};
+    block_compute(j_beg, j_end, rq, qvalid, 0);
+    store_tile(rq, qvalid);
   }
 }
 
@@ -740,18 +843,34 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
 // ----------------------------------------------------------------------------- host helpers
 template <int HD, int QT, bool FUSED>
 static void launch_attention(const AttnArgs& a, int kv_dtype, bool softcap, dim3 grid, hipStream_t st) {
+  // one tile per wave and no new-token split: two waves per tile, each scoring half of a block
+  // (head_dim 128: the halves' merge fits the K tile's LDS)
+  constexpr int WPT = (QT == 1 && !FUSED && HD == 128) ? 2 : 1;
+  const dim3 blk(256 * WPT);
   if (kv_dtype == DSK_KV_U8) {
-    if (softcap) hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_U8, true, FUSED>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_U8, false, FUSED>), grid, dim3(256), 0, st, a);
+    if (softcap) hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_U8, true, FUSED, WPT>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_U8, false, FUSED, WPT>), grid, blk, 0, st, a);
   } else {
-    if (softcap) hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_BF16, true, FUSED>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_BF16, false, FUSED>), grid, dim3(256), 0, st, a);
+    if (softcap) hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_BF16, true, FUSED, WPT>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((attention_kernel<HD, QT, DSK_KV_BF16, false, FUSED, WPT>), grid, blk, 0, st, a);
   }
 }
 
-// Keys per split: the LDS capacity (graph-stable: the split grid depends on max_ctx only).
+// Keys of one LDS block; a split streams nblk blocks (graph-stable: the split grid depends on
+// max_ctx only). One block per split gives the most splits, which sizes the workspace.
 static int attn_split_keys(int hd, int) { return hd == 128 ? Split<128>::KEYS : Split<256>::KEYS; }
 static int attn_nsplit(int hd, int max_ctx) { return (int)ceil_div(max_ctx, attn_split_keys(hd, max_ctx)); }
+// blocks per split of the streamed path: about 24 splits per (row, kv head), at most 8 blocks
+// (DSK_ATTN_BLOCKS overrides, for tuning)
+static int attn_blocks(int hd, int max_ctx) {
+  static const int forced = [] {
+    const char* e = getenv("DSK_ATTN_BLOCKS");
+    return e ? atoi(e) : 0;
+  }();
+  if (forced > 0) return forced;
+  const int64_t blocks = ceil_div(max_ctx, attn_split_keys(hd, max_ctx));
+  return (int)std::min<int64_t>(8, std::max<int64_t>(1, ceil_div(blocks, 24)));
+}
 
 // partial outputs first, then (m, l) at a 256-byte boundary
 static size_t attn_part_o_bytes(int B, int W, int nq, int hd, int nsplit) {
@@ -779,8 +898,12 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
   DSK_REQUIRE(!fused || a.W <= 64, "%s: W=%d new tokens exceeds 64", who, a.W);
   DSK_REQUIRE(!a.out_packed || (a.B * a.W <= 64 && (a.nq * hd) % 64 == 0), "%s: packed output needs B*W <= 64", who);
   a.fused = fused ? 1 : 0;
-  a.kps = attn_split_keys(hd, max_ctx);
-  a.nsplit = attn_nsplit(hd, max_ctx) + (fused ? 1 : 0);
+  int nblk = (fused || QT != 1) ? 1 : attn_blocks(hd, max_ctx);
+  while (nblk > 1 && attn_split_keys(hd, max_ctx) * nblk / a.page + 1 > kAttnMaxSplitPages) --nblk;
+  DSK_REQUIRE(attn_split_keys(hd, max_ctx) / a.page + 1 <= kAttnMaxSplitPages, "%s: page size %d too small", who,
+              a.page);
+  a.kps = attn_split_keys(hd, max_ctx) * nblk;
+  a.nsplit = (int)ceil_div(max_ctx, a.kps) + (fused ? 1 : 0);
   const size_t need = attn_ws_need(a.B, a.W, a.nq, hd, a.nsplit);
   DSK_REQUIRE(a.nsplit == 1 || (workspace && ws_bytes >= need), "%s: workspace %zu < %zu", who, ws_bytes, need);
   a.part_o = reinterpret_cast<uint16_t*>(workspace);

@@ -25,6 +25,8 @@
 // yields t = sum x q exactly up to fp32 accumulation; X = sum x over the group comes from
 // one more MFMA against a B operand of ones; the group adds s * t + b * X to the fp32
 // accumulator.
+#include <stdlib.h>
+
 #include "common.h"
 
 namespace dsk {
@@ -488,7 +490,8 @@ struct GemmPlan {
 // NT tiles per workgroup amortise the activation reads (L2 -> CU traffic is the limit once
 // the weights stream at full rate); K splits (partial outputs only) bring small-N projections
 // to >= 512 workgroups; 4 waves per workgroup with several 2-group batches each, or up to 16
-// waves of one batch when a split is short. Rules fitted to a sweep on MI355X at M = 16 over
+// waves of one batch when a split is short (wide short-K partials, like the fused qkv: pairs of
+// tiles, 4 K splits, 8 waves). Rules fitted to a sweep on MI355X at M = 16 over
 // the Qwen3-8B verify shapes (qkv 6144x4096, o 4096x4096, gate_up 24576x4096, down
 // 4096x12288, head 151936x4096): each lands within 5% of the best configuration measured.
 static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi) {
@@ -498,7 +501,7 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi) {
   const bool partial = epi == DSK_EPI_PARTIAL, gated = epi == DSK_EPI_SWIGLU || epi == DSK_EPI_GEGLU;
   GemmPlan p;
   p.u = 2;
-  if (partial) p.nt = G >= 128 ? 4 : (tiles <= 256 ? 2 : 1);
+  if (partial) p.nt = G >= 128 ? 4 : 2;
   else p.nt = 4;
   if (MT > 2 && p.nt > 2) p.nt = 2;
   while (p.nt > 1 && tiles % p.nt) p.nt /= 2;
@@ -522,6 +525,20 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi) {
     p.pf = true;
   }
   while ((size_t)p.waves * MT * p.nt * 1024 > 65536) p.waves /= 2;  // LDS of the reduction
+  // tuning override (DSK_GEMM_TUNE="epi,N,nt,u,waves,sk,pf": applies to that epilogue and N)
+  static const char* tune = getenv("DSK_GEMM_TUNE");
+  if (tune) {
+    int te, tn, tnt, tu, tw, tsk, tpf;
+    if (sscanf(tune, "%d,%d,%d,%d,%d,%d,%d", &te, &tn, &tnt, &tu, &tw, &tsk, &tpf) == 7 && te == epi && tn == N &&
+        MT == 1) {
+      p.nt = tnt;
+      p.u = tu;
+      p.waves = tw;
+      p.sk = tsk;
+      p.gpb = (G / p.u / p.sk) * p.u;
+      p.pf = tpf != 0;
+    }
+  }
   return p;
 }
 
@@ -553,6 +570,10 @@ static bool launch_gemm_w(const GemmArgs& a, int waves, hipStream_t st) {
 static bool launch_gemm(const GemmArgs& a, int MT, const GemmPlan& p, hipStream_t st) {
   if (p.pf) {  // the pipelined variant is built for the shapes the planner gives it
     if (MT == 1 && p.nt == 2 && p.u == 2) return launch_gemm_w<1, 2, 2, true>(a, p.waves, st);
+    if (MT == 1 && p.nt == 2 && p.u == 4) return launch_gemm_w<1, 2, 4, true>(a, p.waves, st);
+    if (MT == 1 && p.nt == 4 && p.u == 2) return launch_gemm_w<1, 4, 2, true>(a, p.waves, st);
+    if (MT == 1 && p.nt == 1 && p.u == 4) return launch_gemm_w<1, 1, 4, true>(a, p.waves, st);
+    if (MT == 1 && p.nt == 1 && p.u == 2) return launch_gemm_w<1, 1, 2, true>(a, p.waves, st);
     return false;
   }
 #define DSK_GEMM_CASE(MT_, NT_, U_) \
