@@ -216,3 +216,67 @@ def test_fused_partial_input_and_packed_output(dev, L0):
     assert torch.equal(pools[0].k, pools[1].k) and torch.equal(pools[0].v, pools[1].v)
     assert torch.equal(pools[0].ksb, pools[1].ksb) and torch.equal(pools[0].vsb, pools[1].vsb)
     assert torch.equal(o_a, o_b.unpack())
+
+
+def _read_tokens(pool, b, n, which):
+    """token-major [n, nkv, hd] float32 of row b (dequantized for u8), all pages gathered at once."""
+    pages = pool.block_table[b, : (n + pool.page - 1) // pool.page].long()
+    data = (pool.k if which == "k" else pool.v)[pages]                    # [P, nkv, page, hd]
+    P, nkv, page, hd = data.shape
+    if pool.kv_dtype == 0:
+        vals = data.float()
+    else:
+        sb = (pool.ksb if which == "k" else pool.vsb)[pages].cpu().numpy().view(np.uint32)
+        sc = torch.from_numpy(O.bits_to_f32((sb & 0xFFFF).astype(np.uint16)))
+        bi = torch.from_numpy(O.bits_to_f32((sb >> 16).astype(np.uint16)))
+        q = data.cpu().float().view(P, nkv, page, hd // 64, 64)
+        vals = torch.from_numpy(O.bf16_round((q * sc[..., None] + bi[..., None]).view(P, nkv, page, hd).numpy()))
+    return vals.cpu().permute(0, 2, 1, 3).reshape(P * page, nkv, hd)[:n]
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+@pytest.mark.parametrize("lens,W,max_ctx", [([4096], 16, 5184), ([3000, 5000], 9, 5200), ([100], 16, 8000),
+                                            ([6000, 1000], 16, 12288), ([0, 64, 127], 4, 3500)])
+def test_attention_streamed_splits(dev, kv_dtype, lens, W, max_ctx):
+    """Long contexts: each split streams several key blocks (the split size grows with max_ctx),
+    with ragged rows, splits past a row's length, a causal edge inside a block and rows whose
+    keys end mid-block; against a float32 softmax over the stored K/V."""
+    from mlx_dspark.ops import attention
+    print(f"attn streamed kv={kv_dtype} lens={lens} W={W} max_ctx={max_ctx}", flush=True)
+    B, nq, nkv, hd, page = len(lens), 8, 2, 128, 64
+    g = torch.Generator().manual_seed(sum(lens) + W + kv_dtype)
+    pool = Pool(B, nkv, hd, max_ctx, page, kv_dtype, dev, seed=W)
+    if kv_dtype == 0:
+        pool.k.copy_(torch.randn(pool.k.shape, generator=g).to(torch.bfloat16))
+        pool.v.copy_(torch.randn(pool.v.shape, generator=g).to(torch.bfloat16))
+    else:
+        pool.k.copy_(torch.randint(0, 256, pool.k.shape, generator=g, dtype=torch.uint8))
+        pool.v.copy_(torch.randint(0, 256, pool.v.shape, generator=g, dtype=torch.uint8))
+        # scale ~ U(0.005, 0.02), bias ~ U(-1.5, -0.5): bf16 pairs packed scale | bias << 16
+        def sbv():
+            s = (0.005 + 0.015 * torch.rand(pool.ksb.shape, generator=g)).to(torch.bfloat16).view(torch.int16)
+            bb = (-1.5 + torch.rand(pool.ksb.shape, generator=g)).to(torch.bfloat16).view(torch.int16)
+            return (s.to(torch.int32) & 0xFFFF) | (bb.to(torch.int32) << 16)
+        pool.ksb.copy_(sbv())
+        pool.vsb.copy_(sbv())
+    q = torch.randn(B * W, nq * hd, generator=g).to(torch.bfloat16)
+    sl = torch.tensor(lens, dtype=torch.int32, device=dev)
+    scale = hd ** -0.5
+    out = attention(q.to(dev), B, W, nq, nkv, hd, scale, sl, max_ctx, pool.block_table, page, kv_dtype, pool.k,
+                    pool.v, pool.ksb, pool.vsb, causal=True)
+    torch.cuda.synchronize()
+    G = nq // nkv
+    for b, L0 in enumerate(lens):
+        K = _read_tokens(pool, b, L0 + W, "k")
+        V = _read_tokens(pool, b, L0 + W, "v")
+        qb = q.view(B, W, nq, hd)[b].float()
+        ref = torch.empty(W, nq, hd)
+        j = torch.arange(L0 + W)[None, :]
+        i = torch.arange(W)[:, None]
+        for h in range(nq):
+            s = (qb[:, h] @ K[:, h // G].T) * scale
+            s = s.masked_fill(j > L0 + i, float("-inf"))
+            ref[:, h] = torch.softmax(s, -1) @ V[:, h // G]
+        got = out.view(B, W, nq, hd)[b].float().cpu()
+        err = (got - ref).abs().max().item()
+        assert err < 2e-2, (b, err)
