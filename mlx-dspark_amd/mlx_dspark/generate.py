@@ -278,6 +278,7 @@ class _DFlashRound:
         self.tt = torch.zeros((1, cap + 1), dtype=torch.int32, device=dev)
         self.out = torch.zeros(2 + cap, dtype=torch.int32, device=dev)   # [n, token, draft...]
         self.graph = None
+        self.calls = 0
 
     def body(self, round_idx: int = 0) -> None:
         self.block[0, 0:1].copy_(self.pending)
@@ -306,8 +307,10 @@ class _DFlashRound:
         self.out[2:].copy_(self.draft)
 
     def run(self, round_idx: int, use_graph: bool):
+        # the first round of this width runs eagerly (it sizes the workspaces), later ones
+        # replay one captured graph
         if use_graph and self.T == 0:
-            if self.graph is None and round_idx >= 1:
+            if self.graph is None and self.calls >= 1:
                 self.graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(self.graph):
                     self.body()
@@ -317,6 +320,7 @@ class _DFlashRound:
                 self.body(round_idx)
         else:
             self.body(round_idx)
+        self.calls += 1
         o = self.out.tolist()                                         # the round's one host sync
         n, token, draft = o[0], o[1], o[2:]
         self.cache.note_lengths([self.cache.lengths[0] + n + 1])
@@ -331,8 +335,6 @@ def dflash_generate(target_model, tokenizer, drafter, prompt: str = "", *, promp
     """Speculative decoding with a DFlash block-diffusion drafter (src/mlx_dspark/generate.py:468-601)."""
     if getattr(drafter, "embed_tokens", None) is None:
         drafter.bind(target_model.model)
-    if cap_controller is not None:
-        raise NotImplementedError("cap_controller is not supported by this engine")
     cfg = drafter.config
     tap = list(cfg.target_layer_ids)
     kdraft = int(cfg.block_size) - 1
@@ -353,15 +355,23 @@ def dflash_generate(target_model, tokenizer, drafter, prompt: str = "", *, promp
     out_ids = [pending]
     accept_lengths: list = []
     target_forwards = 1
-    rnd = _DFlashRound(target_model, drafter, cache, dcache, cap, temperature, top_p, top_k, s64)
-    rnd.pending.fill_(pending)
+    # one round object (static buffers, captured graph) per verify width: a cap controller may
+    # pick a different cap every round (generate.py:537-538)
+    rounds: dict = {}
     st.update(out_ids)
     r = 0
     while len(out_ids) < max_new_tokens and pending not in eos_ids and not st.stopped:
-        if cache.lengths[0] + cap + 1 > cache.max_ctx:
+        c = cap if cap_controller is None else max(1, min(int(cap_controller.cap), cap))
+        if cache.lengths[0] + c + 1 > cache.max_ctx:
             break
+        rnd = rounds.get(c)
+        if rnd is None:
+            rnd = rounds[c] = _DFlashRound(target_model, drafter, cache, dcache, c, temperature, top_p, top_k, s64)
+        rnd.pending.fill_(pending)
         n, token, draft = rnd.run(r, use_graph)
         r += 1
+        if cap_controller is not None:
+            cap_controller.update(n, len(draft))
         committed = draft[:n] + [token]
         target_forwards += 1
         accept_lengths.append(len(committed))
@@ -457,6 +467,7 @@ class _DSparkRound:
         self.tt = torch.zeros((1, cap + 1), dtype=torch.int32, device=dev)
         self.out = torch.zeros(2 + cap, dtype=torch.int32, device=dev)   # [n, token, draft...]
         self.graph = None
+        self.calls = 0
         self.uses = 0
 
     def body(self) -> None:

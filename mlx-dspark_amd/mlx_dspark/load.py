@@ -76,8 +76,8 @@ def resolve_mode(model=None, *, mode="auto", drafter=None, family=None, target=N
 
 def _synthetic_key(name: str) -> str:
     if not str(name).startswith("synthetic/"):
-        raise ValueError(f"{name!r}: only synthetic/* models can be built offline "
-                         f"(checkpoint loading from a local path is not implemented yet)")
+        raise ValueError(f"{name!r}: not a synthetic/* model name, nor a local checkpoint directory "
+                         f"(config.json + *.safetensors); hub downloads are not available offline")
     return str(name).split("/", 1)[1]
 
 
@@ -87,12 +87,21 @@ def apply_wired_limit() -> None:
 
 def load_target(repo_or_path: str = DEFAULT_TARGET, *, require_tap: bool = False, kv_bits=None,
                 kv_group_size: int = 64, seed: int = 0, keep_mlx: bool = False, max_ctx=None):
-    """(Target, tokenizer) for a synthetic target (load.py:314-351)."""
-    key = _synthetic_key(repo_or_path)
-    if key not in synthetic.TARGETS:
-        raise ValueError(f"unknown synthetic target {key!r}; known: {sorted(synthetic.TARGETS)}")
-    model = synthetic.build_target(key, seed=seed, keep_mlx=keep_mlx)
-    tok = SyntheticTokenizer(model.args.vocab_size)
+    """(Target, tokenizer) for a synthetic target or a local MLX checkpoint directory
+    (config.json + safetensors, 8-bit group-64 or unquantized qwen3; load.py:314-351)."""
+    from . import checkpoint
+    if checkpoint.is_checkpoint_dir(repo_or_path):
+        model = checkpoint.load_qwen3_w8(repo_or_path)
+        if checkpoint.has_tokenizer(repo_or_path):
+            tok = checkpoint.load_tokenizer(repo_or_path)
+        else:                               # weights-only directory: token ids in and out
+            tok = SyntheticTokenizer(model.args.vocab_size)
+    else:
+        key = _synthetic_key(repo_or_path)
+        if key not in synthetic.TARGETS:
+            raise ValueError(f"unknown synthetic target {key!r}; known: {sorted(synthetic.TARGETS)}")
+        model = synthetic.build_target(key, seed=seed, keep_mlx=keep_mlx)
+        tok = SyntheticTokenizer(model.args.vocab_size)
     target = Target(model, tok, kv_bits=kv_bits, kv_group_size=kv_group_size, max_ctx=max_ctx)
     if require_tap:
         target.verify_tap()

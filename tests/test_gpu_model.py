@@ -131,6 +131,48 @@ def test_dflash_generate_reproduces_greedy_stream(dev, tiny, use_graph):
     assert res.text == tok.decode(res.token_ids)
 
 
+class _CyclingCap:
+    """A duck-typed cap controller (calibrate.py CapController's .cap / .update): cycles through
+    caps and records every update."""
+
+    def __init__(self, caps):
+        self.caps, self.i, self.updates = list(caps), 0, []
+
+    @property
+    def cap(self):
+        return self.caps[self.i % len(self.caps)]
+
+    def update(self, n_accepted, n_drafted):
+        self.updates.append((n_accepted, n_drafted))
+        self.i += 1
+
+
+def test_dflash_generate_with_cap_controller(dev, tiny):
+    """The cap is re-read every round (generate.py:537-538): verify widths vary, the greedy
+    stream still equals greedy decoding, and update() sees (accepted, drafted) per round."""
+    from mlx_dspark import synthetic
+    from mlx_dspark.generate import dflash_generate
+    from mlx_dspark.target import Target
+    from mlx_dspark.tokenizer import SyntheticTokenizer
+    d, cfg = synthetic.build_dflash(tiny.args, seed=9, keep_mlx=True, num_hidden_layers=2, block_size=8, n_taps=2)
+    d.bind(tiny)
+    tok = SyntheticTokenizer(tiny.args.vocab_size)
+    target = Target(tiny, tok)
+    prompt = np.random.default_rng(4).integers(0, tiny.args.vocab_size, 29).tolist()
+    ctl = _CyclingCap([3, 7, 1, 12, 5])      # 12 is clamped to the block's 7 drafts
+    res = dflash_generate(target, tok, d, prompt_ids=prompt, max_new_tokens=30, cap_controller=ctl)
+    ref_tokens, margins = OM.greedy_decode(OM.OracleTarget(tiny), prompt, len(res.token_ids))
+    for i, (a, b) in enumerate(zip(res.token_ids, ref_tokens)):
+        if a != b:
+            assert margins[i] <= TOL, (i, a, b, margins[i])
+            break
+    assert len(ctl.updates) == res.num_rounds
+    want = [min(c, 7) for c in (ctl.caps * res.num_rounds)[: res.num_rounds]]
+    assert [dr for _, dr in ctl.updates] == want
+    assert all(0 <= n <= dr for n, dr in ctl.updates)
+    assert [n + 1 for n, _ in ctl.updates][:-1] == res.accept_lengths[:-1]
+
+
 def test_dflash_generate_sampled_is_seeded(dev, tiny):
     from mlx_dspark import synthetic
     from mlx_dspark.generate import dflash_generate
