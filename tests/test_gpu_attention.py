@@ -234,42 +234,46 @@ def _read_tokens(pool, b, n, which):
     return vals.cpu().permute(0, 2, 1, 3).reshape(P * page, nkv, hd)[:n]
 
 
-@pytest.mark.parametrize("kv_dtype", [0, 1])
-@pytest.mark.parametrize("lens,W,max_ctx", [([4096], 16, 5184), ([3000, 5000], 9, 5200), ([100], 16, 8000),
-                                            ([6000, 1000], 16, 12288), ([0, 64, 127], 4, 3500)])
-def test_attention_streamed_splits(dev, kv_dtype, lens, W, max_ctx):
-    """Long contexts: each split streams several key blocks (the split size grows with max_ctx),
-    with ragged rows, splits past a row's length, a causal edge inside a block and rows whose
-    keys end mid-block; against a float32 softmax over the stored K/V."""
-    from mlx_dspark.ops import attention
-    print(f"attn streamed kv={kv_dtype} lens={lens} W={W} max_ctx={max_ctx}", flush=True)
-    B, nq, nkv, hd, page = len(lens), 8, 2, 128, 64
-    g = torch.Generator().manual_seed(sum(lens) + W + kv_dtype)
-    pool = Pool(B, nkv, hd, max_ctx, page, kv_dtype, dev, seed=W)
+def _random_case(dev, kv_dtype, lens, W, max_ctx, nq=8, nkv=2, hd=128, page=64):
+    """A pool of random stored K/V (8-bit: random codes with scale ~ U(0.005, 0.02), bias ~
+    U(-1.5, -0.5)) and random queries for rows of the given lengths."""
+    B = len(lens)
+    g = torch.Generator().manual_seed(sum(lens) + W + kv_dtype + 7 * nkv)
+    pool = Pool(B, nkv, hd, max_ctx, page, kv_dtype, dev, seed=W + nkv)
     if kv_dtype == 0:
         pool.k.copy_(torch.randn(pool.k.shape, generator=g).to(torch.bfloat16))
         pool.v.copy_(torch.randn(pool.v.shape, generator=g).to(torch.bfloat16))
     else:
         pool.k.copy_(torch.randint(0, 256, pool.k.shape, generator=g, dtype=torch.uint8))
         pool.v.copy_(torch.randint(0, 256, pool.v.shape, generator=g, dtype=torch.uint8))
-        # scale ~ U(0.005, 0.02), bias ~ U(-1.5, -0.5): bf16 pairs packed scale | bias << 16
-        def sbv():
-            s = (0.005 + 0.015 * torch.rand(pool.ksb.shape, generator=g)).to(torch.bfloat16).view(torch.int16)
+
+        def sbv():   # bf16 pairs packed scale | bias << 16
+            sc = (0.005 + 0.015 * torch.rand(pool.ksb.shape, generator=g)).to(torch.bfloat16).view(torch.int16)
             bb = (-1.5 + torch.rand(pool.ksb.shape, generator=g)).to(torch.bfloat16).view(torch.int16)
-            return (s.to(torch.int32) & 0xFFFF) | (bb.to(torch.int32) << 16)
+            return (sc.to(torch.int32) & 0xFFFF) | (bb.to(torch.int32) << 16)
         pool.ksb.copy_(sbv())
         pool.vsb.copy_(sbv())
     q = torch.randn(B * W, nq * hd, generator=g).to(torch.bfloat16)
     sl = torch.tensor(lens, dtype=torch.int32, device=dev)
-    scale = hd ** -0.5
-    out = attention(q.to(dev), B, W, nq, nkv, hd, scale, sl, max_ctx, pool.block_table, page, kv_dtype, pool.k,
-                    pool.v, pool.ksb, pool.vsb, causal=True)
-    torch.cuda.synchronize()
+    return dict(pool=pool, q=q, qd=q.to(dev), sl=sl, B=B, W=W, nq=nq, nkv=nkv, hd=hd, page=page,
+                max_ctx=max_ctx, kv_dtype=kv_dtype, lens=lens)
+
+
+def _run_case(c, out=None):
+    from mlx_dspark.ops import attention
+    p = c["pool"]
+    return attention(c["qd"], c["B"], c["W"], c["nq"], c["nkv"], c["hd"], c["hd"] ** -0.5, c["sl"], c["max_ctx"],
+                     p.block_table, c["page"], c["kv_dtype"], p.k, p.v, p.ksb, p.vsb, causal=True, out=out)
+
+
+def _check_case(c, out):
+    B, W, nq, nkv, hd = c["B"], c["W"], c["nq"], c["nkv"], c["hd"]
     G = nq // nkv
-    for b, L0 in enumerate(lens):
-        K = _read_tokens(pool, b, L0 + W, "k")
-        V = _read_tokens(pool, b, L0 + W, "v")
-        qb = q.view(B, W, nq, hd)[b].float()
+    scale = hd ** -0.5
+    for b, L0 in enumerate(c["lens"]):
+        K = _read_tokens(c["pool"], b, L0 + W, "k")
+        V = _read_tokens(c["pool"], b, L0 + W, "v")
+        qb = c["q"].view(B, W, nq, hd)[b].float()
         ref = torch.empty(W, nq, hd)
         j = torch.arange(L0 + W)[None, :]
         i = torch.arange(W)[:, None]
@@ -280,3 +284,39 @@ def test_attention_streamed_splits(dev, kv_dtype, lens, W, max_ctx):
         got = out.view(B, W, nq, hd)[b].float().cpu()
         err = (got - ref).abs().max().item()
         assert err < 2e-2, (b, err)
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+@pytest.mark.parametrize("lens,W,max_ctx", [([4096], 16, 5184), ([3000, 5000], 9, 5200), ([100], 16, 8000),
+                                            ([6000, 1000], 16, 12288), ([0, 64, 127], 4, 3500),
+                                            ([0, 130], 16, 300), ([8100], 4, 8192)])
+def test_attention_streamed_splits(dev, kv_dtype, lens, W, max_ctx):
+    """Long contexts: each split streams several key blocks (the split size grows with max_ctx),
+    with ragged rows, splits past a row's length, a causal edge inside a block and rows whose
+    keys end mid-block; against a float32 softmax over the stored K/V."""
+    print(f"attn streamed kv={kv_dtype} lens={lens} W={W} max_ctx={max_ctx}", flush=True)
+    c = _random_case(dev, kv_dtype, lens, W, max_ctx)
+    out = _run_case(c)
+    torch.cuda.synchronize()
+    _check_case(c, out)
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+def test_attention_interleaved_shapes_repeat(dev, kv_dtype):
+    """Calls of different shapes (rows, kv heads, split counts) interleaved on the shared split
+    workspace, each output cleared first, repeat bit for bit and match the float32 softmax."""
+    print(f"attn interleaved kv={kv_dtype}", flush=True)
+    cases = [_random_case(dev, kv_dtype, [4096], 16, 5184),
+             _random_case(dev, kv_dtype, [700, 2500, 30], 9, 3000, nq=16, nkv=4),
+             _random_case(dev, kv_dtype, [1500, 64], 16, 2048, nq=8, nkv=1)]
+    first = []
+    for rep in range(3):
+        for k, c in enumerate(cases):
+            out = torch.full((c["B"] * c["W"], c["nq"] * c["hd"]), float("nan"), dtype=torch.bfloat16, device=dev)
+            _run_case(c, out=out)
+            torch.cuda.synchronize()
+            if rep == 0:
+                _check_case(c, out)
+                first.append(out.clone())
+            else:
+                assert torch.equal(out, first[k]), (rep, k)
