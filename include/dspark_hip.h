@@ -92,6 +92,13 @@ size_t dsk_act_pack_bytes(int M, int64_t K);
 int dsk_act_pack(const float* part, int nsplit, const uint16_t* part_norm_w, uint16_t* h,
                  int64_t ldh, uint16_t* copy, int64_t ldc, int M, int64_t K,
                  const uint16_t* norm_w, float eps, uint16_t* out, dsk_stream_t stream);
+/* dsk_act_pack with the residual-stream result scaled before it is stored, copied and normed:
+ * v = bf16(v * out_scale) after the residual add (the gemma4 drafter layer's layer_scalar,
+ * src/mlx_dspark/model.py:181-184). out_scale 1 is dsk_act_pack. */
+int dsk_act_pack_scaled(const float* part, int nsplit, const uint16_t* part_norm_w, uint16_t* h,
+                        int64_t ldh, uint16_t* copy, int64_t ldc, int M, int64_t K,
+                        const uint16_t* norm_w, float eps, float out_scale, uint16_t* out,
+                        dsk_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------
  * W8 skinny GEMM: y[M, N] = x[M, K] . deq(W)[N, K]^T
@@ -154,6 +161,16 @@ int dsk_qkv_rope_append(const void* qkv, int qkv_splits, int B, int W, int nq, i
                         const int32_t* block_table, int max_pages, int page, int kv_dtype,
                         void* k_pool, void* v_pool, uint32_t* k_sb, uint32_t* v_sb,
                         uint16_t* q_out, dsk_stream_t stream);
+/* dsk_qkv_rope_append with an RMSNorm on V as well (v_norm weights [hd] bf16, NULL for
+ * none; V is not rotated): the gemma4 DSpark drafter's v_norm, which with k_eq_v normalises
+ * the shared k_proj output (src/mlx_dspark/model.py:113-124; RMSNormNoScale is a v_norm of
+ * ones). head_dim 128, 256 or 512. */
+int dsk_qkv_norm_rope_append(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv,
+                             int hd, const uint16_t* q_norm, const uint16_t* k_norm,
+                             const uint16_t* v_norm, float eps, const float* inv_freq,
+                             const int32_t* seq_lens, int pos_offset, const int32_t* block_table,
+                             int max_pages, int page, int kv_dtype, void* k_pool, void* v_pool,
+                             uint32_t* k_sb, uint32_t* v_sb, uint16_t* q_out, dsk_stream_t stream);
 
 /* Attention of W new queries per row over the row's paged KV (already holding the W new
  * tokens at positions seq_lens[b] .. seq_lens[b]+W-1).
@@ -169,7 +186,8 @@ int dsk_qkv_rope_append(const void* qkv, int qkv_splits, int B, int W, int nq, i
  * workspace: dsk_attn_ws_bytes(...) bytes for the split partials (bf16 o / l per split and
  * fp32 (m, l); the splits are combined by a second kernel on the same stream; no state is
  * kept between calls). Every block_table entry of a row must name a valid page: a split
- * reads its whole key range through the table before it knows the row's length. */
+ * reads its whole key range through the table before it knows the row's length.
+ * head_dim 128 or 256, or 512 (the gemma4 drafter's global head) without the fused entry. */
 size_t dsk_attn_ws_bytes(int B, int W, int nq, int hd, int max_ctx);
 int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, int hd, float scale,
                   int causal, int window, float softcap, const int32_t* seq_lens,

@@ -159,10 +159,11 @@ __device__ __forceinline__ int64_t pool_token(const int32_t* block_table, int ma
 template <int HD>
 __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
     const void* __restrict__ qkv, int qkv_splits, int B, int W, int nq, int nkv, const uint16_t* __restrict__ q_norm,
-    const uint16_t* __restrict__ k_norm, float eps, const float* __restrict__ inv_freq,
-    const int32_t* __restrict__ seq_lens, int pos_offset, const int32_t* __restrict__ block_table, int max_pages,
-    int page, int kv_dtype, void* __restrict__ k_pool, void* __restrict__ v_pool, uint32_t* __restrict__ k_sb,
-    uint32_t* __restrict__ v_sb, uint16_t* __restrict__ q_out) {
+    const uint16_t* __restrict__ k_norm, const uint16_t* __restrict__ v_norm, float eps,
+    const float* __restrict__ inv_freq, const int32_t* __restrict__ seq_lens, int pos_offset,
+    const int32_t* __restrict__ block_table, int max_pages, int page, int kv_dtype, void* __restrict__ k_pool,
+    void* __restrict__ v_pool, uint32_t* __restrict__ k_sb, uint32_t* __restrict__ v_sb,
+    uint16_t* __restrict__ q_out) {
   constexpr int PER = HD / 64;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int nheads = nq + 2 * nkv;
@@ -174,7 +175,7 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
   float v[PER];
   load_proj_row<PER>(qkv, qkv_splits, (int64_t)B * W * nheads * HD, ((int64_t)row * nheads + head) * HD, lane, v);
   const bool is_q = head < nq, is_k = !is_q && head < nq + nkv;
-  norm_rope_row<HD, 64>(v, lane, is_q ? q_norm : (is_k ? k_norm : nullptr), eps, is_q || is_k, inv_freq, pos);
+  norm_rope_row<HD, 64>(v, lane, is_q ? q_norm : (is_k ? k_norm : v_norm), eps, is_q || is_k, inv_freq, pos);
   if (is_q) {
     uint16_t* dst = q_out + (int64_t)row * nq * HD + (int64_t)head * HD;
 #pragma unroll
@@ -220,7 +221,7 @@ constexpr int kAttnMaxSplitPages = 256;
 
 // LDS capacity in keys of one block (a split streams kps / KEYS blocks through it)
 template <int HD> struct Split {
-  static constexpr int KEYS = HD == 128 ? 128 : 64;
+  static constexpr int KEYS = HD == 128 ? 128 : (HD == 256 ? 64 : 32);
   static constexpr int KROW = HD + 8;    // K rows in LDS (bf16, padded)
   static constexpr int VROW = KEYS + 8;  // V^T rows in LDS (bf16, padded)
 };
@@ -486,7 +487,9 @@ __global__ __launch_bounds__(256 * WPT) __attribute__((amdgpu_waves_per_eu(1, 2)
     const int npg = min((split * kps + kps - 1) / a.page, a.max_pages - 1) - pg0 + 1;
     for (int t = threadIdx.x; t < npg; t += NTHR) pgs[t] = a.block_table[(int64_t)b * a.max_pages + pg0 + t];
   }
-  const int mytile = wv & 3, half = wv >> 2;  // WPT == 2: waves w and w + 4 share tile w, key halves
+  // WPT == 2: waves w and w + 4 share tile w, key halves; blockIdx.y: groups of 4 query tiles
+  // (head_dim 512, whose one-tile-per-wave kernel covers any number of query rows this way)
+  const int mytile = (int)blockIdx.y * 4 + (wv & 3), half = wv >> 2;
   QTile<HD, FUSED> qt;
   if (mytile < ntiles) qtile_load<HD, FUSED>(a, b, kvh, mytile, lane, qt);
   const int off = a.seq_lens[b];
@@ -783,7 +786,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   for (int e = 0; e < PER; ++e) acc[e] = 0.0f;
   float M = -__builtin_inff(), den = 0.0f;
   // rounds of RS splits: the (m, l) and partial-output loads of a round are issued together
-  constexpr int RS = PER == 2 ? 64 : 32;
+  constexpr int RS = PER == 2 ? 64 : (PER == 4 ? 32 : 16);
   for (int s0 = 0; s0 < ns; s0 += RS) {
     const int n = min(RS, ns - s0);
     float m = -__builtin_inff(), l = 0.0f;
@@ -806,8 +809,13 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
           const uint32_t x = *reinterpret_cast<const uint32_t*>(base_o + sp * so);
           ov[u][0] = (uint16_t)(x & 0xffff);
           ov[u][1] = (uint16_t)(x >> 16);
-        } else {
+        } else if constexpr (PER == 4) {
           const uint2 x = *reinterpret_cast<const uint2*>(base_o + sp * so);
+          const uint16_t* hx = reinterpret_cast<const uint16_t*>(&x);
+#pragma unroll
+          for (int e = 0; e < PER; ++e) ov[u][e] = hx[e];
+        } else {
+          const u32x4 x = *reinterpret_cast<const u32x4*>(base_o + sp * so);
           const uint16_t* hx = reinterpret_cast<const uint16_t*>(&x);
 #pragma unroll
           for (int e = 0; e < PER; ++e) ov[u][e] = hx[e];
@@ -858,7 +866,9 @@ static void launch_attention(const AttnArgs& a, int kv_dtype, bool softcap, dim3
 
 // Keys of one LDS block; a split streams nblk blocks (graph-stable: the split grid depends on
 // max_ctx only). One block per split gives the most splits, which sizes the workspace.
-static int attn_split_keys(int hd, int) { return hd == 128 ? Split<128>::KEYS : Split<256>::KEYS; }
+static int attn_split_keys(int hd, int) {
+  return hd == 128 ? Split<128>::KEYS : (hd == 256 ? Split<256>::KEYS : Split<512>::KEYS);
+}
 static int attn_nsplit(int hd, int max_ctx) { return (int)ceil_div(max_ctx, attn_split_keys(hd, max_ctx)); }
 // blocks per split of the streamed path: about 24 splits per (row, kv head), at most 8 blocks
 // (DSK_ATTN_BLOCKS overrides, for tuning)
@@ -883,7 +893,8 @@ static size_t attn_ws_need(int B, int W, int nq, int hd, int nsplit) {
 // shared validation and launch of both attention entries
 static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* workspace, size_t ws_bytes,
                          bool fused, hipStream_t st, const char* who) {
-  DSK_REQUIRE(hd == 128 || hd == 256, "%s: head_dim %d not supported (128, 256)", who, hd);
+  DSK_REQUIRE(hd == 128 || hd == 256 || (hd == 512 && !fused), "%s: head_dim %d not supported (128, 256; 512 "
+              "without the fused append)", who, hd);
   DSK_REQUIRE(a.B > 0 && a.W > 0 && a.nq > 0 && a.nkv > 0 && a.nq % a.nkv == 0, "%s: bad shape", who);
   DSK_REQUIRE(a.kv_dtype == DSK_KV_BF16 || (a.kv_dtype == DSK_KV_U8 && a.k_sb && a.v_sb), "%s: u8 KV needs sb", who);
   DSK_REQUIRE(a.page > 0 && a.max_pages > 0, "%s: bad page geometry", who);
@@ -892,7 +903,9 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
   a.G = a.nq / a.nkv;
   a.R = a.W * a.G;
   const int tiles = (a.R + 15) / 16;
-  const int QT = (tiles + 3) / 4;
+  // head_dim 512: one tile per wave, query-tile groups on the grid's y axis
+  const int QT = hd == 512 ? 1 : (tiles + 3) / 4;
+  const int tile_groups = hd == 512 ? (tiles + 3) / 4 : 1;
   DSK_REQUIRE(QT <= (hd == 128 ? 4 : 2), "%s: W*G=%d query rows per kv head exceeds %d", who, a.R,
               (hd == 128 ? 256 : 128));
   DSK_REQUIRE(!fused || a.W <= 64, "%s: W=%d new tokens exceeds 64", who, a.W);
@@ -910,7 +923,7 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
   a.part_ml = a.nsplit > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
                                                        attn_part_o_bytes(a.B, a.W, a.nq, hd, a.nsplit))
                            : nullptr;
-  dim3 grid((unsigned)(a.B * a.nkv * a.nsplit));
+  dim3 grid((unsigned)(a.B * a.nkv * a.nsplit), (unsigned)tile_groups);
   const bool sc = softcap > 0.0f;
 #define DSK_ATTN_CASE(hdv, qt)                                      \
   if (hd == hdv && QT == qt) {                                      \
@@ -920,11 +933,13 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
   DSK_ATTN_CASE(128, 1) DSK_ATTN_CASE(128, 2) DSK_ATTN_CASE(128, 3) DSK_ATTN_CASE(128, 4)
   DSK_ATTN_CASE(256, 1) DSK_ATTN_CASE(256, 2)
 #undef DSK_ATTN_CASE
+  if (hd == 512) launch_attention<512, 1, false>(a, a.kv_dtype, sc, grid, st);
   DSK_LAUNCH_CHECK(who);
   if (a.nsplit > 1) {
     const dim3 cgrid((unsigned)ceil_div((int64_t)a.B * a.nkv * a.R, 4));
     if (hd == 128) hipLaunchKernelGGL(attention_combine_kernel<128>, cgrid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(attention_combine_kernel<256>, cgrid, dim3(256), 0, st, a);
+    else if (hd == 256) hipLaunchKernelGGL(attention_combine_kernel<256>, cgrid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(attention_combine_kernel<512>, cgrid, dim3(256), 0, st, a);
     DSK_LAUNCH_CHECK(who);
   }
   return DSK_OK;
@@ -934,15 +949,16 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
 
 using namespace dsk;
 
-extern "C" int dsk_qkv_rope_append(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
-                                   const uint16_t* q_norm, const uint16_t* k_norm, float eps,
-                                   const float* inv_freq, const int32_t* seq_lens, int pos_offset,
-                                   const int32_t* block_table, int max_pages, int page, int kv_dtype,
-                                   void* k_pool, void* v_pool, uint32_t* k_sb, uint32_t* v_sb,
-                                   uint16_t* q_out, dsk_stream_t stream) {
+extern "C" int dsk_qkv_norm_rope_append(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
+                                        const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* v_norm,
+                                        float eps, const float* inv_freq, const int32_t* seq_lens, int pos_offset,
+                                        const int32_t* block_table, int max_pages, int page, int kv_dtype,
+                                        void* k_pool, void* v_pool, uint32_t* k_sb, uint32_t* v_sb, uint16_t* q_out,
+                                        dsk_stream_t stream) {
   DSK_REQUIRE(qkv && inv_freq && seq_lens && block_table && k_pool && v_pool && (q_out || nq == 0),
               "dsk_qkv_rope_append: null pointer");
-  DSK_REQUIRE(hd == 128 || hd == 256, "dsk_qkv_rope_append: head_dim %d not supported (128, 256)", hd);
+  DSK_REQUIRE(hd == 128 || hd == 256 || hd == 512, "dsk_qkv_rope_append: head_dim %d not supported (128, 256, 512)",
+              hd);
   DSK_REQUIRE(B > 0 && W > 0 && nq >= 0 && nkv > 0 && nq % nkv == 0, "dsk_qkv_rope_append: bad shape");
   DSK_REQUIRE(page > 0 && max_pages > 0, "dsk_qkv_rope_append: bad page geometry");
   DSK_REQUIRE(qkv_splits >= 0, "dsk_qkv_rope_append: qkv_splits=%d", qkv_splits);
@@ -950,21 +966,32 @@ extern "C" int dsk_qkv_rope_append(const void* qkv, int qkv_splits, int B, int W
               "dsk_qkv_rope_append: u8 KV needs scale/bias buffers");
   const int tasks = B * W * (nq + 2 * nkv);
   dim3 grid((unsigned)ceil_div(tasks, 4));
-  if (hd == 128)
-    hipLaunchKernelGGL(qkv_rope_append_kernel<128>, grid, dim3(256), 0, as_stream(stream), qkv, qkv_splits, B, W, nq, nkv, q_norm,
-                       k_norm, eps, inv_freq, seq_lens, pos_offset, block_table, max_pages, page, kv_dtype, k_pool,
-                       v_pool, k_sb, v_sb, q_out);
-  else
-    hipLaunchKernelGGL(qkv_rope_append_kernel<256>, grid, dim3(256), 0, as_stream(stream), qkv, qkv_splits, B, W, nq, nkv, q_norm,
-                       k_norm, eps, inv_freq, seq_lens, pos_offset, block_table, max_pages, page, kv_dtype, k_pool,
-                       v_pool, k_sb, v_sb, q_out);
+#define DSK_APPEND(HDV)                                                                                             \
+  hipLaunchKernelGGL(qkv_rope_append_kernel<HDV>, grid, dim3(256), 0, as_stream(stream), qkv, qkv_splits, B, W, nq, \
+                     nkv, q_norm, k_norm, v_norm, eps, inv_freq, seq_lens, pos_offset, block_table, max_pages, page, \
+                     kv_dtype, k_pool, v_pool, k_sb, v_sb, q_out)
+  if (hd == 128) DSK_APPEND(128);
+  else if (hd == 256) DSK_APPEND(256);
+  else DSK_APPEND(512);
+#undef DSK_APPEND
   DSK_LAUNCH_CHECK("dsk_qkv_rope_append");
   return DSK_OK;
 }
 
+extern "C" int dsk_qkv_rope_append(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
+                                   const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                   const float* inv_freq, const int32_t* seq_lens, int pos_offset,
+                                   const int32_t* block_table, int max_pages, int page, int kv_dtype,
+                                   void* k_pool, void* v_pool, uint32_t* k_sb, uint32_t* v_sb,
+                                   uint16_t* q_out, dsk_stream_t stream) {
+  return dsk_qkv_norm_rope_append(qkv, qkv_splits, B, W, nq, nkv, hd, q_norm, k_norm, nullptr, eps, inv_freq,
+                                  seq_lens, pos_offset, block_table, max_pages, page, kv_dtype, k_pool, v_pool, k_sb,
+                                  v_sb, q_out, stream);
+}
+
 extern "C" size_t dsk_attn_ws_bytes(int B, int W, int nq, int hd, int max_ctx) {
   if (B <= 0 || W <= 0 || nq <= 0 || hd <= 0 || max_ctx <= 0) return 0;
-  if (hd != 128 && hd != 256) return 0;
+  if (hd != 128 && hd != 256 && hd != 512) return 0;
   return attn_ws_need(B, W, nq, hd, attn_nsplit(hd, max_ctx) + 1);  // + the fused new-token split
 }
 

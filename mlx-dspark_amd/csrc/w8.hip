@@ -135,6 +135,7 @@ struct PackArgs {
   float eps;
   uint16_t* out;       // packed, or null
   const uint16_t* res_norm_w;  // RMSNorm of the partial sum before the residual add, or null
+  float out_scale;             // the residual-stream result is multiplied by this (rounded again)
 };
 
 template <int NV, int MAXS>
@@ -215,8 +216,10 @@ __global__ __launch_bounds__(kPackThreads) void act_pack_kernel(PackArgs a) {
     uint16_t o[8];
     const uint16_t* hh = reinterpret_cast<const uint16_t*>(&hv[i]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
+    for (int e = 0; e < 8; ++e) {
       o[e] = a.h ? (S ? f32_to_bf16(bf16_to_f32(hh[e]) + fv[i][e]) : hh[e]) : f32_to_bf16(fv[i][e]);
+      if (a.out_scale != 1.0f) o[e] = f32_to_bf16(bf16_to_f32(o[e]) * a.out_scale);
+    }
     v[i] = *reinterpret_cast<const u32x4*>(o);
   }
   float r = 1.0f;
@@ -665,9 +668,9 @@ extern "C" size_t dsk_act_pack_bytes(int M, int64_t K) {
   return (size_t)((M + 15) / 16) * (size_t)K * 32;
 }
 
-extern "C" int dsk_act_pack(const float* part, int nsplit, const uint16_t* part_norm_w, uint16_t* h, int64_t ldh,
-                            uint16_t* copy, int64_t ldc, int M, int64_t K, const uint16_t* norm_w, float eps,
-                            uint16_t* out, dsk_stream_t stream) {
+extern "C" int dsk_act_pack_scaled(const float* part, int nsplit, const uint16_t* part_norm_w, uint16_t* h,
+                                   int64_t ldh, uint16_t* copy, int64_t ldc, int M, int64_t K, const uint16_t* norm_w,
+                                   float eps, float out_scale, uint16_t* out, dsk_stream_t stream) {
   DSK_REQUIRE(part || h, "dsk_act_pack: needs partial sums or an input h");
   DSK_REQUIRE(out || copy || (h && part), "dsk_act_pack: no output");
   DSK_REQUIRE(!part || (nsplit > 0 && nsplit <= kPackMaxSplits), "dsk_act_pack: nsplit=%d outside [1, %d]", nsplit,
@@ -683,11 +686,17 @@ extern "C" int dsk_act_pack(const float* part, int nsplit, const uint16_t* part_
                 (uintptr_t)part_norm_w) & 15) == 0,
               "dsk_act_pack: pointers must be 16-byte aligned");
   DSK_REQUIRE(!part_norm_w || part, "dsk_act_pack: part_norm_w needs partial sums");
-  PackArgs a{part, nsplit, h, ldh, copy, ldc, M, K, norm_w, eps, out, part_norm_w};
+  PackArgs a{part, nsplit, h, ldh, copy, ldc, M, K, norm_w, eps, out, part_norm_w, out_scale};
   DSK_REQUIRE(pack_launch(a, as_stream(stream)), "dsk_act_pack: no kernel for K=%lld with %d slices", (long long)K,
               nsplit);
   DSK_LAUNCH_CHECK("dsk_act_pack");
   return DSK_OK;
+}
+
+extern "C" int dsk_act_pack(const float* part, int nsplit, const uint16_t* part_norm_w, uint16_t* h, int64_t ldh,
+                            uint16_t* copy, int64_t ldc, int M, int64_t K, const uint16_t* norm_w, float eps,
+                            uint16_t* out, dsk_stream_t stream) {
+  return dsk_act_pack_scaled(part, nsplit, part_norm_w, h, ldh, copy, ldc, M, K, norm_w, eps, 1.0f, out, stream);
 }
 
 extern "C" int dsk_w8_gemm_splits(int M, int64_t N, int64_t K) {

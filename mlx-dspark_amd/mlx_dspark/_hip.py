@@ -26,6 +26,8 @@ SIGNATURES: dict[str, tuple] = {
     "dsk_act_pack_bytes": (c_size_t, [c_int, c_int64]),
     "dsk_act_pack": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int, c_int64, c_void_p,
                              c_float, c_void_p, c_void_p]),
+    "dsk_act_pack_scaled": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int, c_int64,
+                                    c_void_p, c_float, c_float, c_void_p, c_void_p]),
     "dsk_w8_gemm_splits": (c_int, [c_int, c_int64, c_int64]),
     "dsk_w8_gemm": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int, c_void_p, c_int, c_int64,
                             c_void_p, c_int64, c_float, c_void_p]),
@@ -34,6 +36,9 @@ SIGNATURES: dict[str, tuple] = {
     "dsk_qkv_rope_append": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float,
                                     c_void_p, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p,
                                     c_void_p, c_void_p, c_void_p, c_void_p]),
+    "dsk_qkv_norm_rope_append": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
+                                         c_void_p, c_float, c_void_p, c_void_p, c_int, c_void_p, c_int, c_int, c_int,
+                                         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "dsk_attn_ws_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "dsk_attention": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_float,
                               c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,

@@ -182,7 +182,8 @@ class SpecSlots:
         a, c = self.model.args, drafter.config
         self.cache = PagedKVCache(a.num_hidden_layers, self.capacity, a.num_key_value_heads, a.head_dim, max_ctx,
                                   kv_bits=target.kv_bits, device=self.dev, spare_pages=prefix_pages)
-        self.ctx = PagedKVCache(c.num_hidden_layers, self.capacity, c.num_key_value_heads, c.head_dim,
+        da = drafter.args    # the drafter's own attention shape (gemma4: the global kv heads)
+        self.ctx = PagedKVCache(c.num_hidden_layers, self.capacity, da.num_key_value_heads, da.head_dim,
                                 max_ctx + c.block_size, device=self.dev, spare_pages=prefix_pages)
         self._spare_next = 0
         self.prefixes: list = []          # (token tuple, target pages, drafter pages)

@@ -24,11 +24,13 @@ from .qwen3 import MAX_ROWS
 def ingest_context(d, target_hidden: torch.Tensor, cache: PagedKVCache, n_valid=None) -> None:
     """Append context rows for drafter ``d``: target_hidden [S, n_tap*H] (or [1, S, .]) bf16.
 
-    ``d`` provides config (hidden_size, num_key_value_heads, head_dim, rms_norm_eps, block_size),
-    fc, hidden_norm, layers (with kv_view / k_norm), args and inv_freq. n_valid (device int32
-    [1]) advances the cached length by n_valid + 1 instead of S: the fixed-shape form used when
-    only a device-side prefix of the rows is committed (speculative rounds)."""
-    c = d.config
+    ``d`` provides config (hidden_size, rms_norm_eps, block_size), args (the attention shape:
+    num_key_value_heads, head_dim), fc, hidden_norm, layers (with kv_view / k_norm), inv_freq
+    and optionally v_norm (an RMSNorm on V). n_valid (device int32 [1]) advances the cached
+    length by n_valid + 1 instead of S: the fixed-shape form used when only a device-side prefix
+    of the rows is committed (speculative rounds)."""
+    c, a = d.config, d.args
+    v_norm = getattr(d, "v_norm", None)
     th = target_hidden.reshape(-1, target_hidden.shape[-1])
     S = th.shape[0]
     if n_valid is not None and S > MAX_ROWS:
@@ -42,9 +44,9 @@ def ingest_context(d, target_hidden: torch.Tensor, cache: PagedKVCache, n_valid=
         for l, L in enumerate(d.layers):
             kv = ops.w8_gemm(xc, L.kv_view(d.args), epi=ops.DSK_EPI_PARTIAL)
             k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
-            ops.qkv_rope_append(kv, 1, r1 - r0, 0, c.num_key_value_heads, c.head_dim, None, L.k_norm,
+            ops.qkv_rope_append(kv, 1, r1 - r0, 0, a.num_key_value_heads, a.head_dim, None, L.k_norm,
                                 c.rms_norm_eps, d.inv_freq, cache.seq_lens, cache.block_table,
-                                cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb, None)
+                                cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb, None, v_norm=v_norm)
         if n_valid is None:
             ops.lens_add(cache.seq_lens, None, r1 - r0)
             cache.note_lengths([cache.lengths[0] + (r1 - r0)])
@@ -57,7 +59,8 @@ def ingest_rows(d, fused: torch.Tensor, cache: PagedKVCache, n_valid: torch.Tens
     n_tap*H] bf16 holds each row's W candidate positions (at its own cached length); row b
     keeps n_valid[b] + 1 of them (n_valid device int32 [B]), the rest lies past its length
     and is overwritten by the next append."""
-    c = d.config
+    c, a = d.config, d.args
+    v_norm = getattr(d, "v_norm", None)
     B, W = fused.shape[0], fused.shape[1]
     if B * W > MAX_ROWS:
         raise ValueError(f"batched context append of {B}x{W} rows > {MAX_ROWS}")
@@ -68,37 +71,42 @@ def ingest_rows(d, fused: torch.Tensor, cache: PagedKVCache, n_valid: torch.Tens
     for l, L in enumerate(d.layers):
         kv = ops.w8_gemm(xc, L.kv_view(d.args), epi=ops.DSK_EPI_PARTIAL)
         k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
-        ops.qkv_rope_append(kv, B, W, 0, c.num_key_value_heads, c.head_dim, None, L.k_norm, c.rms_norm_eps,
+        ops.qkv_rope_append(kv, B, W, 0, a.num_key_value_heads, a.head_dim, None, L.k_norm, c.rms_norm_eps,
                             d.inv_freq, cache.seq_lens, cache.block_table, cache.page, cache.kv_dtype, k_pool,
-                            v_pool, k_sb, v_sb, None)
+                            v_pool, k_sb, v_sb, None, v_norm=v_norm)
     ops.lens_add(cache.seq_lens[:B], n_valid, 1)
 
 
 def block_layers(d, h: torch.Tensor, B: int, bs: int, cache: PagedKVCache, scale: float) -> torch.Tensor:
-    """Run drafter ``d``'s decoder layers (2-norm Qwen3 layout) over the block rows h [B*bs, H]
-    (bf16, updated in place) attending to context ++ block; returns h before the final norm."""
+    """Run drafter ``d``'s decoder layers over the block rows h [B*bs, H] (bf16, updated in
+    place) attending to context ++ block; returns h before the final norm. Llama 2-norm layers,
+    or sandwich norms when the layers carry attn_out_norm / ff_out_norm (gemma4), with
+    d.layer_scalars multiplying each layer's output and d.v_norm normalising V."""
     c, a = d.config, d.args
     M, H = B * bs, c.hidden_size
     eps = c.rms_norm_eps
-    nq, nkv, hd = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+    nq, nkv, hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
+    v_norm = getattr(d, "v_norm", None)
+    scalars = getattr(d, "layer_scalars", None)
     x = ops.pack(h, d.layers[0].in_norm, eps)
     nl = len(d.layers)
     for l, L in enumerate(d.layers):
         qkv = ops.w8_gemm(x, L.qkv, epi=ops.DSK_EPI_PARTIAL)
         k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
         q = ops.qkv_rope_append(qkv, B, bs, nq, nkv, hd, L.q_norm, L.k_norm, eps, d.inv_freq, cache.seq_lens,
-                                cache.block_table, cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb)
+                                cache.block_table, cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb,
+                                v_norm=v_norm)
         win = a.window(l)
         o = ops.attention(q, B, bs, nq, nkv, hd, scale, cache.seq_lens, cache.max_ctx, cache.block_table,
                           cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb, causal=bool(win), window=win,
                           packed=True)
         op = ops.w8_gemm(o, L.o, epi=ops.DSK_EPI_PARTIAL)
-        x = ops.act_pack(M=M, K=H, part=op, h=h, norm_w=L.post_norm, eps=eps)
+        x = ops.act_pack(M=M, K=H, part=op, h=h, norm_w=L.post_norm, eps=eps, part_norm_w=L.attn_out_norm)
         act = ops.w8_gemm(x, L.gate_up, epi=d.act_epi)
         dp = ops.w8_gemm(act, L.down, epi=ops.DSK_EPI_PARTIAL)
         last = l == nl - 1
         x = ops.act_pack(M=M, K=H, part=dp, h=h, norm_w=None if last else d.layers[l + 1].in_norm, eps=eps,
-                         out=not last)
+                         out=not last, part_norm_w=L.ff_out_norm, scale=scalars[l] if scalars else 1.0)
     return h
 
 

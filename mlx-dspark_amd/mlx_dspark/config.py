@@ -4,8 +4,7 @@ Same fields, defaults and config.json schema as the reference's DSparkConfig (co
 so DeepSpec drafter configs parse identically: family detection from model_type, the
 rejection of vLLM "speculators" packagings and of targets with an embedded drafter, the
 required-field check, and the family-derived knobs (MLP activation, norm layout, v_norm,
-attention scaling). The engine runs the qwen3 family; gemma4 configs parse but the drafter
-refuses them (model.py).
+attention scaling). The engine's drafter runs both families (model.py).
 """
 
 from __future__ import annotations

@@ -127,7 +127,7 @@ def load_drafter(repo_or_path: str = DEFAULT_DRAFTER, *, quantize: bool = True, 
                  keep_mlx: bool = False, **shape):
     """(drafter, config) for a synthetic DSpark drafter (load.py:155-215); W8 by default.
     ``shape`` overrides the builder's drafter knobs (num_hidden_layers, block_size, taps,
-    markov_rank, confidence)."""
+    markov_rank, confidence, family: gemma4 by default for Gemma-style targets)."""
     if bits != 8 or group_size != 64 or not quantize:
         raise ValueError("this engine runs W8 (group 64) drafters")
     key = _synthetic_key(repo_or_path)
@@ -138,6 +138,8 @@ def load_drafter(repo_or_path: str = DEFAULT_DRAFTER, *, quantize: bool = True, 
         if tkey not in synthetic.TARGETS:
             raise ValueError(f"unknown synthetic target {tkey!r} for drafter {repo_or_path!r}")
         target_args = synthetic.target_args(tkey)
+    # Gemma-family targets get the gemma4 drafter layout, as their DeepSpec drafters have
+    shape.setdefault("family", "gemma4" if str(target_args.model_type).startswith("gemma") else "qwen3")
     return synthetic.build_dspark(target_args, seed=seed, keep_mlx=keep_mlx, **shape)
 
 

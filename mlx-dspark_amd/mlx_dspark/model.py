@@ -1,12 +1,18 @@
 """DSpark drafter on gfx950 kernels (drop-in for src/mlx_dspark/model.py).
 
-Behaviour follows the reference's DSparkDrafter (model.py:220-320), qwen3 family:
+Behaviour follows the reference's DSparkDrafter (model.py:220-320), both families:
   - context: fused = RMSNorm(fc(concat of tapped target states)); per layer K = rope(k_norm(
-    k_proj(fused)), ctx_offset + i), V = v_proj(fused), appended to the layer's context cache
-    (:113-128, :247-256);
-  - block: [pending] + [mask] * (k-1) embedded (x embed_scale), then Qwen3-layout layers whose
-    attention is bidirectional over context ++ block, roped at block_offset = committed length
-    (:130-193, :258-262), final RMSNorm;
+    k_proj(fused)), ctx_offset + i), V = v_proj(fused) (qwen3) or, with gemma4's k_eq_v,
+    V = v_norm(k_proj(fused)) (an RMSNorm without weight on the un-normed, un-roped k
+    projection), appended to the layer's context cache (:113-128, :247-256);
+  - block: [pending] + [mask] * (k-1) embedded (x embed_scale: sqrt(hidden) for gemma4), then
+    the layers, attention bidirectional over context ++ block, roped at block_offset =
+    committed length (:130-193, :258-262), final RMSNorm. qwen3: Llama 2-norm layers, SiLU MLP,
+    scale head_dim^-1/2. gemma4: sandwich norms (post-attention and post-feedforward norms of
+    the projection outputs before their residual adds) and the layer_scalar multiply (:172-184),
+    tanh-GeLU MLP, attention scale 1, head_dim = global_head_dim over the global kv heads,
+    proportional RoPE (the first partial_rotary_factor of the rotate-half frequencies, exponents
+    over the full head_dim; the rest pass through);
   - heads: logits = lm_head(h[:cap]) (+ tanh soft-cap) (:264-268); Markov block sampling
     tok_i = argmax(logits_i + w2(w1[tok_{i-1}])) (:270-281) or its sampled form (:283-309); the
     confidence head sigmoid(Linear(concat(h, w1[prev]))) (:311-320).
@@ -55,14 +61,19 @@ class ConfidenceHead:
 class DSparkDrafter:
     def __init__(self, config: DSparkConfig, *, embed: W8Table, fc: W8Weight, hidden_norm: torch.Tensor,
                  layers: list[LayerWeights], norm: torch.Tensor, lm_head: W8Weight,
-                 markov: MarkovHead | None = None, confidence: ConfidenceHead | None = None):
-        if config.family != "qwen3":
-            raise NotImplementedError(f"DSpark family {config.family!r}: this engine runs the qwen3 drafter "
-                                      f"layout (gemma4's k_eq_v / partial-rope drafter is not implemented)")
+                 markov: MarkovHead | None = None, confidence: ConfidenceHead | None = None,
+                 layer_scalars: list[float] | None = None):
+        """layers: the qkv projection is [q | k | v] rows; with k_eq_v the v rows repeat the k
+        rows (the shared k_proj). layer_scalars: gemma4's per-layer output multipliers."""
+        if config.family not in ("qwen3", "gemma4"):
+            raise ValueError(f"DSpark family {config.family!r}: qwen3 or gemma4")
+        gemma = config.family == "gemma4"
+        if gemma and config.attention_k_eq_v and not config.use_v_norm:
+            raise ValueError("gemma4 k_eq_v drafter without v_norm")
         self.config = config
         self.block_size = config.block_size
         self.mask_token_id = config.mask_token_id
-        self.embed_scale = 1.0
+        self.embed_scale = float(config.hidden_size) ** 0.5 if gemma else 1.0
         self.softcap = config.final_logit_softcapping
         self.embed_tokens = embed
         self.fc = fc
@@ -73,13 +84,18 @@ class DSparkDrafter:
         self.markov_head = markov
         self.confidence_head = confidence
         self.device = norm.device
+        hd, nkv = config.attn_head_dim, config.n_kv_heads
         self.args = TargetArgs(hidden_size=config.hidden_size, num_hidden_layers=config.num_hidden_layers,
                                intermediate_size=config.intermediate_size,
                                num_attention_heads=config.num_attention_heads,
-                               num_key_value_heads=config.num_key_value_heads, head_dim=config.head_dim,
+                               num_key_value_heads=nkv, head_dim=hd,
                                vocab_size=config.vocab_size, rms_norm_eps=config.rms_norm_eps,
                                rope_theta=config.rope_theta)
-        self.inv_freq = ops.rope_inv_freq(config.head_dim, config.rope_theta, self.device)
+        frac = config.partial_rotary_factor if config.rope_type == "proportional" else 1.0
+        self.inv_freq = ops.rope_inv_freq(hd, config.rope_theta, self.device, rotary_fraction=frac)
+        # RMSNorm without weight on V (gemma4 v_norm): a unit weight
+        self.v_norm = torch.ones(hd, dtype=torch.bfloat16, device=self.device) if config.use_v_norm else None
+        self.layer_scalars = [float(x) for x in layer_scalars] if layer_scalars is not None else None
         self.act_epi = ops.DSK_EPI_SWIGLU if config.mlp_activation == "silu" else ops.DSK_EPI_GEGLU
 
     # ---------------------------------------------------------------- context
@@ -92,7 +108,7 @@ class DSparkDrafter:
     def make_ctx_cache(self, max_ctx: int = 16384, B: int = 1) -> PagedKVCache:
         """Per-layer context K/V (the reference's [CtxCache] * n_layers, model.py:48-80, 250-251)."""
         c = self.config
-        return PagedKVCache(c.num_hidden_layers, B, c.num_key_value_heads, c.head_dim, max_ctx + c.block_size,
+        return PagedKVCache(c.num_hidden_layers, B, c.n_kv_heads, c.attn_head_dim, max_ctx + c.block_size,
                             device=self.device)
 
     def update_context(self, target_hidden_cat: torch.Tensor, ctx_offset: int, ctx_caches: PagedKVCache,

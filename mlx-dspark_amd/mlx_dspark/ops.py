@@ -169,7 +169,8 @@ def _rows_ok(t: torch.Tensor) -> bool:
 
 def act_pack(*, M: int, K: int, part: torch.Tensor | None = None, h: torch.Tensor | None = None,
              copy: torch.Tensor | None = None, norm_w: torch.Tensor | None = None, eps: float = 1e-6,
-             out: Packed | bool | None = True, part_norm_w: torch.Tensor | None = None) -> Packed | None:
+             out: Packed | bool | None = True, part_norm_w: torch.Tensor | None = None,
+             scale: float = 1.0) -> Packed | None:
     """Sum split-K partials [S, M, K] (f32) into the residual stream h (bf16 [M, K], in place),
     optionally copy the result (tap), RMSNorm it and pack it for the next GEMM (see
     dsk_act_pack). part_norm_w RMSNorms the partial sum before the residual add (gemma's
@@ -185,9 +186,9 @@ def act_pack(*, M: int, K: int, part: torch.Tensor | None = None, h: torch.Tenso
         out = Packed.empty(M, K, dev)
     elif out is False:
         out = None
-    call("dsk_act_pack", ptr(part), 0 if part is None else part.shape[0], ptr(part_norm_w), ptr(h),
+    call("dsk_act_pack_scaled", ptr(part), 0 if part is None else part.shape[0], ptr(part_norm_w), ptr(h),
          0 if h is None else h.stride(0),
-         ptr(copy), 0 if copy is None else copy.stride(0), M, K, ptr(norm_w), float(eps),
+         ptr(copy), 0 if copy is None else copy.stride(0), M, K, ptr(norm_w), float(eps), float(scale),
          ptr(None if out is None else out.data), stream_ptr())
     return out
 
@@ -251,15 +252,22 @@ def w8_embed(ids: torch.Tensor, table: W8Table, scale: float = 1.0, out: torch.T
 
 
 # ----------------------------------------------------------------------------- attention
-def rope_inv_freq(head_dim: int, theta: float, device) -> torch.Tensor:
-    """theta ** (-2 d / head_dim) for d < head_dim / 2, computed in float64, stored f32."""
+def rope_inv_freq(head_dim: int, theta: float, device, *, rotary_fraction: float = 1.0) -> torch.Tensor:
+    """theta ** (-2 d / head_dim) for d < head_dim / 2, computed in float64, stored f32.
+    rotary_fraction < 1 is proportional RoPE (gemma4): only the first
+    int(rotary_fraction * head_dim / 2) frequencies rotate, with exponents still over the full
+    head_dim; the rest are 0 (those dims pass through)."""
     d = torch.arange(0, head_dim // 2, dtype=torch.float64)
-    return (theta ** (-2.0 * d / head_dim)).to(torch.float32).to(device)
+    inv = theta ** (-2.0 * d / head_dim)
+    if rotary_fraction < 1.0:
+        inv[int(rotary_fraction * head_dim // 2):] = 0.0
+    return inv.to(torch.float32).to(device)
 
 
 def qkv_rope_append(qkv, B, W, nq, nkv, hd, q_norm, k_norm, eps, inv_freq, seq_lens, block_table,
-                    page, kv_dtype, k_pool, v_pool, k_sb=None, v_sb=None, q_out=None, pos_offset=0):
-    """qkv: bf16 [B*W, (nq+2nkv)*hd] or f32 split-K partials [S, B*W, (nq+2nkv)*hd]."""
+                    page, kv_dtype, k_pool, v_pool, k_sb=None, v_sb=None, q_out=None, pos_offset=0, v_norm=None):
+    """qkv: bf16 [B*W, (nq+2nkv)*hd] or f32 split-K partials [S, B*W, (nq+2nkv)*hd]. v_norm
+    (bf16 [hd]) RMSNorms V too."""
     splits = qkv.shape[0] if qkv.dim() == 3 else 0
     if splits and (qkv.dtype != torch.float32 or not qkv.is_contiguous()):
         raise ValueError("qkv partials must be contiguous f32")
@@ -267,8 +275,8 @@ def qkv_rope_append(qkv, B, W, nq, nkv, hd, q_norm, k_norm, eps, inv_freq, seq_l
         qkv = qkv.contiguous().to(torch.bfloat16)
     if q_out is None and nq:
         q_out = torch.empty((B * W, nq * hd), dtype=torch.bfloat16, device=qkv.device)
-    call("dsk_qkv_rope_append", ptr(qkv), splits, B, W, nq, nkv, hd, ptr(q_norm), ptr(k_norm), float(eps),
-         ptr(inv_freq), ptr(seq_lens), int(pos_offset), ptr(block_table), block_table.shape[1], page,
+    call("dsk_qkv_norm_rope_append", ptr(qkv), splits, B, W, nq, nkv, hd, ptr(q_norm), ptr(k_norm), ptr(v_norm),
+         float(eps), ptr(inv_freq), ptr(seq_lens), int(pos_offset), ptr(block_table), block_table.shape[1], page,
          kv_dtype, ptr(k_pool), ptr(v_pool), ptr(k_sb), ptr(v_sb), ptr(q_out), stream_ptr())
     return q_out
 

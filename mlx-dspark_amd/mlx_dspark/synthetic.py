@@ -137,12 +137,29 @@ def evenly_spaced_layers(n_target_layers: int, n: int) -> list[int]:
     return [int(round(lo + i * (hi - lo) / (n - 1))) for i in range(n)]
 
 
+def _w8_k_eq_v(nq_rows: int, k_rows: int, K: int, seed: int, name: str, device, keep_mlx: bool) -> W8Weight:
+    """The [q | k | k] projection of a k_eq_v attention: the shared k_proj rows twice (the
+    second copy is V's input), quantized row by row, so both copies are identical."""
+    q1, s1, b1 = W8Weight.quantize_mlx(randn((nq_rows, K), seed, name + ".q_proj", device))
+    q2, s2, b2 = W8Weight.quantize_mlx(randn((k_rows, K), seed, name + ".k_proj", device))
+    q, s, b = torch.cat([q1, q2, q2]), torch.cat([s1, s2, s2]), torch.cat([b1, b2, b2])
+    W = W8Weight.from_mlx(q, s, b)
+    if keep_mlx:
+        W.mlx = (q, s, b)
+    return W
+
+
 def build_dspark(target_args: TargetArgs, seed: int = 2, device="cuda", keep_mlx: bool = False,
                  num_hidden_layers: int = 1, block_size: int = 7, taps=None, markov_rank: int = 256,
-                 confidence: bool = True, mask_token_id: int | None = None):
-    """A qwen3-family DSpark drafter shaped like the target (same width, heads and MLP), with
-    its own embedding and head, a rank-``markov_rank`` Markov head and a confidence head,
-    conditioned on the target layers ``taps`` (default: 3 spread over the target)."""
+                 confidence: bool = True, mask_token_id: int | None = None, family: str = "qwen3",
+                 global_head_dim: int = 512):
+    """A DSpark drafter of the target's width, with its own embedding and head, a
+    rank-``markov_rank`` Markov head and a confidence head, conditioned on the target layers
+    ``taps`` (default: 3 spread over the target).
+    family "qwen3": heads and MLP shaped like the target, Llama 2-norm layers.
+    family "gemma4": the target's q heads over one global kv head of ``global_head_dim``
+    (k_eq_v, v_norm, proportional RoPE over a quarter of the dims), sandwich norms with
+    layer_scalar 1, tanh-GeLU MLP, soft-cap 30, embedding scale sqrt(hidden)."""
     from .config import DSparkConfig
     from .model import ConfidenceHead, DSparkDrafter, MarkovHead
 
@@ -150,27 +167,41 @@ def build_dspark(target_args: TargetArgs, seed: int = 2, device="cuda", keep_mlx
     device = torch.device(device)
     L = a.num_hidden_layers
     taps = list(taps) if taps is not None else [1, L // 2, L - 1] if L >= 3 else list(range(L))
-    cfg = DSparkConfig(
-        family="qwen3", hidden_size=a.hidden_size, vocab_size=a.vocab_size, num_hidden_layers=num_hidden_layers,
-        intermediate_size=a.intermediate_size, rms_norm_eps=a.rms_norm_eps,
-        num_attention_heads=a.num_attention_heads, num_key_value_heads=a.num_key_value_heads,
-        head_dim=a.head_dim, attention_k_eq_v=False, rope_theta=a.rope_theta, rope_type="default",
-        block_size=block_size, mask_token_id=a.vocab_size - 2 if mask_token_id is None else mask_token_id,
-        target_layer_ids=taps, num_target_layers=L, markov_rank=markov_rank,
-        enable_confidence_head=confidence, confidence_head_with_markov=markov_rank > 0,
-        final_logit_softcapping=None, mlp_activation="silu", norm_style="qwen", use_v_norm=False)
+    gemma = family == "gemma4"
+    if family not in ("qwen3", "gemma4"):
+        raise ValueError(f"unknown DSpark family {family!r}")
+    common = dict(hidden_size=a.hidden_size, vocab_size=a.vocab_size, num_hidden_layers=num_hidden_layers,
+                  intermediate_size=a.intermediate_size, rms_norm_eps=a.rms_norm_eps,
+                  num_attention_heads=a.num_attention_heads, block_size=block_size,
+                  mask_token_id=a.vocab_size - 2 if mask_token_id is None else mask_token_id,
+                  target_layer_ids=taps, num_target_layers=L, markov_rank=markov_rank,
+                  enable_confidence_head=confidence, confidence_head_with_markov=markov_rank > 0)
+    if gemma:
+        cfg = DSparkConfig(family="gemma4", num_key_value_heads=a.num_key_value_heads, num_global_key_value_heads=1,
+                           head_dim=a.head_dim, global_head_dim=global_head_dim, attention_k_eq_v=True,
+                           rope_theta=1_000_000.0, partial_rotary_factor=0.25, rope_type="proportional",
+                           final_logit_softcapping=30.0, mlp_activation="gelu_tanh", norm_style="gemma",
+                           use_v_norm=True, **common)
+    else:
+        cfg = DSparkConfig(family="qwen3", num_key_value_heads=a.num_key_value_heads, head_dim=a.head_dim,
+                           attention_k_eq_v=False, rope_theta=a.rope_theta, rope_type="default",
+                           final_logit_softcapping=None, mlp_activation="silu", norm_style="qwen", use_v_norm=False,
+                           **common)
     H, I = a.hidden_size, a.intermediate_size
-    nq, nkv, hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
+    nq, nkv, hd = cfg.num_attention_heads, cfg.n_kv_heads, cfg.attn_head_dim
     layers = []
     for l in range(num_hidden_layers):
         p = f"dspark.layers.{l}."
+        qkv = (_w8_k_eq_v(nq * hd, nkv * hd, H, seed, p + "attn", device, keep_mlx) if gemma
+               else w8(a.n_qkv, H, seed, p + "qkv", device, keep_mlx))
         layers.append(LayerWeights(
-            qkv=w8(a.n_qkv, H, seed, p + "qkv", device, keep_mlx),
+            qkv=qkv,
             o=w8(H, nq * hd, seed, p + "o", device, keep_mlx),
             gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx, paired=True),
             down=w8(H, I, seed, p + "down", device, keep_mlx),
             in_norm=ones(H, device), post_norm=ones(H, device),
-            q_norm=qk_norm(hd, device), k_norm=qk_norm(hd, device)))
+            q_norm=qk_norm(hd, device), k_norm=qk_norm(hd, device),
+            attn_out_norm=ones(H, device) if gemma else None, ff_out_norm=ones(H, device) if gemma else None))
     markov = None
     if markov_rank > 0:
         w1 = w8_table(a.vocab_size, markov_rank, seed, "dspark.markov_w1", device)
@@ -190,7 +221,7 @@ def build_dspark(target_args: TargetArgs, seed: int = 2, device="cuda", keep_mlx
                       fc=w8(H, len(taps) * H, seed, "dspark.fc", device, keep_mlx), hidden_norm=ones(H, device),
                       layers=layers, norm=ones(H, device),
                       lm_head=w8(a.vocab_size, H, seed, "dspark.lm_head", device, keep_mlx),
-                      markov=markov, confidence=conf)
+                      markov=markov, confidence=conf, layer_scalars=[1.0] * num_hidden_layers if gemma else None)
     torch.cuda.synchronize(device)
     return d, cfg
 

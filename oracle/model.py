@@ -44,10 +44,23 @@ def rmsnorm(x, w, eps):
     return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) * w
 
 
-def rope(x, pos, theta):
-    """rotate-half RoPE; x [..., n, hd], pos [n]."""
+def inv_freq(hd: int, theta: float, rotary_fraction: float = 1.0) -> torch.Tensor:
+    """Rotate-half RoPE frequencies theta^(-2i/hd), i < hd/2 (float64, stored f32). A
+    rotary_fraction below 1 is proportional RoPE (the gemma4 drafter's "proportional" rope
+    type, src/mlx_dspark/config.py:38-42, :161-163; the public definition, as in transformers'
+    _compute_proportional_rope_parameters): the first int(fraction * hd / 2) frequencies keep
+    their full-head_dim exponents, the rest are 0, so those dims are not rotated."""
+    inv = theta ** (-2.0 * np.arange(hd // 2) / hd)
+    if rotary_fraction < 1.0:
+        inv[int(rotary_fraction * hd // 2):] = 0.0
+    return torch.from_numpy(inv.astype(np.float32))
+
+
+def rope(x, pos, theta, inv=None):
+    """rotate-half RoPE; x [..., n, hd], pos [n]; inv overrides the theta frequencies."""
     hd = x.shape[-1]
-    inv = torch.from_numpy((theta ** (-2.0 * np.arange(hd // 2) / hd)).astype(np.float32))
+    if inv is None:
+        inv = torch.from_numpy((theta ** (-2.0 * np.arange(hd // 2) / hd)).astype(np.float32))
     ang = pos.float()[:, None] * inv[None, :]
     c, s = torch.cos(ang), torch.sin(ang)
     x1, x2 = x[..., : hd // 2], x[..., hd // 2:]
@@ -277,79 +290,109 @@ def greedy_decode(target: OracleTarget, prompt, n_new: int):
 
 
 class OracleDSpark:
-    """CPU DSpark drafter, qwen3 family (src/mlx_dspark/model.py:83-320), built from a GPU
-    drafter created with keep_mlx=True.
+    """CPU DSpark drafter, qwen3 and gemma4 families (src/mlx_dspark/model.py:83-320), built
+    from a GPU drafter created with keep_mlx=True.
 
     Context rows: fused = RMSNorm(fc(target_hidden)); per layer K = rope(k_norm(k_proj(fused)),
-    ctx position), V = v_proj(fused), appended (model.py:113-128, :247-256). Block: embed ->
-    layers with attention over context ++ block, no mask, roped at block_offset + i (:130-193)
-    -> final RMSNorm. Heads: lm_head (:264-268), Markov block sampling (:270-281) with bf16
-    rounding points (logits, bias and their sum are bf16, as in a bf16 graph), confidence
-    logits (:311-320)."""
+    ctx position), V = v_proj(fused) or, gemma4 with k_eq_v, V = v_norm(k_proj(fused)) (RMSNorm
+    without weight, not roped) (model.py:113-128, :247-256). Block: embed (x sqrt(hidden) for
+    gemma4, :244-245) -> layers with attention over context ++ block, no mask, roped at
+    block_offset + i (:130-155); the qwen3 layer is Llama 2-norm with SiLU, the gemma4 layer has
+    sandwich norms, tanh-GeLU and the layer_scalar multiply (:172-193) -> final RMSNorm. gemma4
+    attends over the global kv heads at global_head_dim with scale 1 and proportional RoPE
+    (config.py:64-84). Heads: lm_head (+ tanh soft-cap) (:264-268), Markov block sampling
+    (:270-281) with bf16 rounding points (logits, bias and their sum are bf16, as in a bf16
+    graph), confidence logits (:311-320)."""
 
     def __init__(self, drafter):
         c = drafter.config
         self.c = c
+        self.gemma = c.family == "gemma4"
+        self.nq, self.nkv, self.hd = c.num_attention_heads, c.n_kv_heads, c.attn_head_dim
+        frac = c.partial_rotary_factor if c.rope_type == "proportional" else 1.0
+        self.inv = inv_freq(self.hd, c.rope_theta, frac)
+        self.embed_scale = float(c.hidden_size) ** 0.5 if self.gemma else 1.0
+        self.scalars = list(drafter.layer_scalars) if getattr(drafter, "layer_scalars", None) else None
         self.embed = deq_table(drafter.embed_tokens)
         self.fc = deq(drafter.fc)
         self.hidden_norm = drafter.hidden_norm.float().cpu()
         self.norm = drafter.norm.float().cpu()
         self.lm_head = deq(drafter.lm_head)
-        self.layers = [OracleLayer(L, c.num_attention_heads, c.num_key_value_heads, c.head_dim)
-                       for L in drafter.layers]
+        self.layers = [OracleLayer(L, self.nq, self.nkv, self.hd) for L in drafter.layers]
         self.w1 = deq_table(drafter.markov_head.w1) if drafter.markov_head is not None else None
         self.w2 = deq(drafter.markov_head.w2) if drafter.markov_head is not None else None
         self.conf_w = deq(drafter.confidence_head.proj)[0] if drafter.confidence_head is not None else None
         self.conf_b = drafter.confidence_head.bias if drafter.confidence_head is not None else 0.0
-        self.K = [torch.zeros(0, c.num_key_value_heads, c.head_dim) for _ in self.layers]
-        self.V = [torch.zeros(0, c.num_key_value_heads, c.head_dim) for _ in self.layers]
+        self.K = [torch.zeros(0, self.nkv, self.hd) for _ in self.layers]
+        self.V = [torch.zeros(0, self.nkv, self.hd) for _ in self.layers]
 
     @property
     def length(self) -> int:
         return self.K[0].shape[0]
 
+    def _kv(self, L, x, n, pos):
+        """(roped normed K, V) [n, nkv, hd] of rows x (model.py:113-124)."""
+        c = self.c
+        nq, nkv, hd, eps = self.nq, self.nkv, self.hd, c.rms_norm_eps
+        kp = bf(x @ L.wq[nq * hd:(nq + nkv) * hd].T).view(n, nkv, hd)
+        if self.gemma and c.attention_k_eq_v:
+            v = bf(rmsnorm(kp, torch.ones(hd), eps))
+        else:
+            v = bf(x @ L.wq[(nq + nkv) * hd:].T).view(n, nkv, hd)
+            if c.use_v_norm:
+                v = bf(rmsnorm(v, torch.ones(hd), eps))
+        k = bf(rope(bf(rmsnorm(kp, L.k_norm, eps)).transpose(0, 1), pos, c.rope_theta, self.inv).transpose(0, 1))
+        return k, v
+
     def update_context(self, target_hidden):
         c = self.c
-        nkv, hd, eps = c.num_key_value_heads, c.head_dim, c.rms_norm_eps
+        eps = c.rms_norm_eps
         th = torch.as_tensor(target_hidden).reshape(-1, self.fc.shape[1]).float()
         S = th.shape[0]
         fused = bf(rmsnorm(bf(th @ self.fc.T), self.hidden_norm, eps))
         pos = torch.arange(self.length, self.length + S)
-        nq = c.num_attention_heads
         for l, L in enumerate(self.layers):
-            kv = bf(fused @ L.wq[nq * hd:].T)
-            k = kv[:, : nkv * hd].view(S, nkv, hd)
-            v = kv[:, nkv * hd:].view(S, nkv, hd)
-            k = bf(rope(bf(rmsnorm(k, L.k_norm, eps)).transpose(0, 1), pos, c.rope_theta).transpose(0, 1))
+            k, v = self._kv(L, fused, S, pos)
             self.K[l] = torch.cat([self.K[l], k])
             self.V[l] = torch.cat([self.V[l], v])
 
     def block_hidden(self, block_ids):
         """normed block hidden [k, H]"""
         c = self.c
-        nq, nkv, hd, eps = c.num_attention_heads, c.num_key_value_heads, c.head_dim, c.rms_norm_eps
+        nq, hd, eps = self.nq, self.hd, c.rms_norm_eps
         ids = torch.as_tensor(block_ids).reshape(-1).long()
         k = ids.numel()
         h = bf(self.embed[ids])
+        if self.embed_scale != 1.0:
+            h = bf(h * self.embed_scale)
         pos = torch.arange(self.length, self.length + k)
         for l, L in enumerate(self.layers):
             x = bf(rmsnorm(h, L.in_norm, eps))
-            qkv = bf(x @ L.wq.T)
-            q = qkv[:, : nq * hd].view(k, nq, hd)
-            kb = qkv[:, nq * hd:(nq + nkv) * hd].view(k, nkv, hd)
-            vb = qkv[:, (nq + nkv) * hd:].view(k, nkv, hd)
-            q = bf(rope(bf(rmsnorm(q, L.q_norm, eps)).transpose(0, 1), pos, c.rope_theta).transpose(0, 1))
-            kb = bf(rope(bf(rmsnorm(kb, L.k_norm, eps)).transpose(0, 1), pos, c.rope_theta).transpose(0, 1))
+            q = bf(x @ L.wq[: nq * hd].T).view(k, nq, hd)
+            q = bf(rope(bf(rmsnorm(q, L.q_norm, eps)).transpose(0, 1), pos, c.rope_theta, self.inv).transpose(0, 1))
+            kb, vb = self._kv(L, x, k, pos)
             o = bf(sdpa(q, torch.cat([self.K[l], kb]), torch.cat([self.V[l], vb]), c.scaling))
-            h = bf(h + o.reshape(k, -1) @ L.wo.T)
-            x = bf(rmsnorm(h, L.post_norm, eps))
-            gu = bf(x @ L.wgu.T)
-            I = gu.shape[1] // 2
-            h = bf(h + bf(bf(gu[:, :I] * torch.sigmoid(gu[:, :I])) * gu[:, I:]) @ L.wd.T)
+            if self.gemma:     # sandwich norms, tanh-GeLU, layer_scalar (model.py:172-184)
+                h = bf(h + bf(rmsnorm(bf(o.reshape(k, -1) @ L.wo.T), L.attn_out_norm, eps)))
+                x = bf(rmsnorm(h, L.post_norm, eps))
+                gu = bf(x @ L.wgu.T)
+                I = gu.shape[1] // 2
+                act = bf(bf(gelu_tanh(gu[:, :I])) * gu[:, I:])
+                h = bf(h + bf(rmsnorm(bf(act @ L.wd.T), L.ff_out_norm, eps)))
+                if self.scalars is not None and self.scalars[l] != 1.0:
+                    h = bf(h * self.scalars[l])
+            else:
+                h = bf(h + o.reshape(k, -1) @ L.wo.T)
+                x = bf(rmsnorm(h, L.post_norm, eps))
+                gu = bf(x @ L.wgu.T)
+                I = gu.shape[1] // 2
+                h = bf(h + bf(bf(gu[:, :I] * torch.sigmoid(gu[:, :I])) * gu[:, I:]) @ L.wd.T)
         return bf(rmsnorm(h, self.norm, eps))
 
     def base_logits(self, block_ids, cap):
-        return self.block_hidden(block_ids)[:cap] @ self.lm_head.T
+        logits = self.block_hidden(block_ids)[:cap] @ self.lm_head.T
+        cap_ = self.c.final_logit_softcapping
+        return torch.tanh(logits / cap_) * cap_ if cap_ else logits
 
     def step_logits(self, base_row, prev):
         """bf16(bf16(base) + bf16(w2 . bf16(w1[prev])))"""

@@ -173,3 +173,41 @@ def test_config_parsing(tmp_path):
         _cfg(tmp_path, {k: v for k, v in QWEN3_MIN.items() if k != "model_type"})
     with pytest.raises(ValueError, match="target_layer_ids"):
         _cfg(tmp_path, {k: v for k, v in QWEN3_MIN.items() if k != "target_layer_ids"})
+
+
+def test_proportional_rope_frequencies_match_transformers():
+    """The oracle's proportional RoPE table (gemma4 drafter) against transformers' published
+    definition (_compute_proportional_rope_parameters), and the engine's table against the
+    oracle's: the first int(0.25 * hd / 2) frequencies are theta^(-2i/hd), the rest 0."""
+    from transformers import PretrainedConfig
+    from transformers import modeling_rope_utils as m
+    for hd, frac, theta in ((512, 0.25, 1e6), (256, 0.5, 1e4), (128, 1.0, 1e6)):
+        cfg = PretrainedConfig(head_dim=hd, hidden_size=hd * 4, num_attention_heads=4,
+                               rope_parameters={"rope_type": "proportional", "rope_theta": theta,
+                                                "partial_rotary_factor": frac})
+        want, _ = m.ROPE_INIT_FUNCTIONS["proportional"](cfg, "cpu")
+        got = OM.inv_freq(hd, theta, frac)
+        assert got.shape == want.shape
+        assert torch.allclose(got, want.float(), rtol=2e-6, atol=0), (hd, frac)
+        n_rot = int(frac * hd // 2)
+        assert torch.all(got[n_rot:] == 0) and torch.all(got[:n_rot] > 0)
+        from mlx_dspark.ops import rope_inv_freq
+        assert torch.equal(rope_inv_freq(hd, theta, "cpu", rotary_fraction=frac), got)
+
+
+def test_proportional_rope_leaves_unrotated_dims():
+    """Dims whose frequency is 0 pass through RoPE unchanged (closed form); the rotated ones
+    keep their pair norms."""
+    hd = 512
+    inv = OM.inv_freq(hd, 1e6, 0.25)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 5, hd, generator=g)
+    pos = torch.tensor([0, 7, 100, 4095, 8191])
+    y = OM.rope(x, pos, 1e6, inv)
+    n_rot = 64
+    keep = torch.cat([torch.arange(n_rot, hd // 2), torch.arange(hd // 2 + n_rot, hd)])
+    assert torch.equal(y[..., keep], x[..., keep])
+    r_in = x[..., :n_rot] ** 2 + x[..., hd // 2:hd // 2 + n_rot] ** 2
+    r_out = y[..., :n_rot] ** 2 + y[..., hd // 2:hd // 2 + n_rot] ** 2
+    assert torch.allclose(r_in, r_out, rtol=1e-5)
+    assert torch.equal(y[:, 0], x[:, 0])       # position 0: identity
