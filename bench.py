@@ -3,7 +3,8 @@
 
 Workload (the config the headline metric is quoted on): a Qwen3-8B-shaped random-init W8
 target (36 layers, hidden 4096, 32 q / 8 kv heads, head_dim 128, SwiGLU 12288, vocab 151936)
-with a 2-layer DFlash block-diffusion drafter conditioned on 5 evenly spaced target layers;
+with a 2-layer DFlash block-diffusion drafter (4-bit linear layers, as the reference quantizes
+drafters) conditioned on 5 evenly spaced target layers;
 batch 1, a seeded 4096-token context, the full 16-position block verified every round
 (anchor + 15 drafts), 8-bit affine KV cache (group 64), greedy acceptance.
 
@@ -204,7 +205,7 @@ def main(argv=None) -> int:
     torch.cuda.init()
     t_build = time.time()
     model = synthetic.build_target(args.target, seed=0)
-    drafter, dcfg = synthetic.build_dflash(model.args, seed=1, block_size=args.block, n_taps=5)
+    drafter, dcfg = synthetic.build_dflash(model.args, seed=1, block_size=args.block, n_taps=5, bits=4)
     drafter.bind(model)
     log(f"built {args.target} W8 target ({model.weight_bytes / 1e9:.2f} GB) + DFlash drafter in "
         f"{time.time() - t_build:.1f} s")
@@ -294,7 +295,8 @@ def main(argv=None) -> int:
                                f"{args.ctx}-token context, verify block {W} (k=16), "
                                f"{'8-bit' if kv_bits else 'bf16'} KV, greedy",
                    "global_batch": 1, "seq_len": args.ctx, "parallelism": "single GPU",
-                   "weights": "W8 affine group 64 (bf16 scale/bias)"},
+                   "weights": "target W8 affine group 64 (bf16 scale/bias); DFlash drafter linears 4-bit "
+                              "group 64 (the reference's drafter default)"},
         "accept_len": round(mean_accept, 3),
         "verify_us": round(verify_us, 1),
         "verify_alg_bytes": int(alg_bytes),

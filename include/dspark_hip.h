@@ -126,6 +126,22 @@ int dsk_w8_gemm(const uint16_t* x, const uint8_t* wt, const uint32_t* sb, int M,
                 int64_t K, int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
                 int64_t ldr, float softcap, dsk_stream_t stream);
 
+/* 4-bit codes (MLX nn.quantize bits=4, group 64: the reference's drafter default,
+ * src/mlx_dspark/load.py:155-215, :224-289 with bits=4; 4-bit target checkpoints).
+ * dsk_w4_quantize: as dsk_w8_quantize with codes 0..15 (s = (max - min) / 15), one per byte.
+ * dsk_w4_repack: codes [N, K] one per byte -> wt [N * K / 2] in the W8 tile order with two
+ *   codes per byte (byte j of a lane's 8 = columns 2j | 2j+1 << 4); sb as dsk_w8_repack.
+ * dsk_w4_gemm: dsk_w8_gemm (same arguments, epilogues and limits) on that layout; its
+ *   DSK_EPI_PARTIAL slice count is dsk_w4_gemm_splits(M, N, K). */
+int dsk_w4_gemm_splits(int M, int64_t N, int64_t K);
+int dsk_w4_quantize(const void* w, int w_dtype, int64_t N, int64_t K, uint8_t* q,
+                    uint16_t* scales, uint16_t* biases, dsk_stream_t stream);
+int dsk_w4_repack(const uint8_t* q, const uint16_t* scales, const uint16_t* biases, int64_t N,
+                  int64_t K, int paired, uint8_t* wt, uint32_t* sb, dsk_stream_t stream);
+int dsk_w4_gemm(const uint16_t* x, const uint8_t* wt, const uint32_t* sb, int M, int64_t N,
+                int64_t K, int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
+                int64_t ldr, float softcap, dsk_stream_t stream);
+
 /* W8 row gather (embedding lookup): out[i, :] = bf16(deq(table)[ids[i], :]) * scale.
  * Replaces nn.QuantizedEmbedding (mm.embed_tokens, src/mlx_dspark/target.py:112;
  * drafter.embed, src/mlx_dspark/model.py:244-245; dflash_model.py:198).

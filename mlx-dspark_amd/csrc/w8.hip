@@ -20,6 +20,9 @@
 //   2p+1 the up rows 16p..16p+15, so one workgroup owning both tiles can apply the
 //   activation in its epilogue.
 //
+// W4 (dsk_w4_gemm): the same tiles with two codes per byte (8 bytes per lane per tile-group),
+// converted to 128 + q in bf16 by byte permutes, the 128 * sum x term folded into the bias.
+//
 // GEMM arithmetic. With w = s*q + b per group, sum_k x_k w_k = s * sum x_k q_k + b * sum x_k.
 // q (0..255) is exact in bf16, the bf16 activations go to the MFMA unchanged, so the MFMA
 // yields t = sum x q exactly up to fp32 accumulation; X = sum x over the group comes from
@@ -36,7 +39,7 @@ namespace dsk {
 // =====================================================================================
 __global__ void w8_quantize_kernel(const void* __restrict__ w, int w_bf16, int64_t N, int64_t K,
                                    uint8_t* __restrict__ q, uint16_t* __restrict__ scales,
-                                   uint16_t* __restrict__ biases) {
+                                   uint16_t* __restrict__ biases, float levels) {
   int64_t G = K / 64;
   int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= N * G) return;
@@ -58,7 +61,7 @@ __global__ void w8_quantize_kernel(const void* __restrict__ w, int w_bf16, int64
     lo = fminf(lo, v[i]);
     hi = fmaxf(hi, v[i]);
   }
-  float s = (hi - lo) / 255.0f;
+  float s = (hi - lo) / levels;
   uint16_t sb16 = f32_to_bf16(s);
   float sf = bf16_to_f32(sb16);
   if (!(sf > 0.0f)) {
@@ -73,7 +76,7 @@ __global__ void w8_quantize_kernel(const void* __restrict__ w, int w_bf16, int64
 #pragma unroll
   for (int i = 0; i < 64; ++i) {
     float t = rintf((v[i] - bf) / sf);
-    t = fminf(fmaxf(t, 0.0f), 255.0f);
+    t = fminf(fmaxf(t, 0.0f), levels);
     qo[i] = (uint8_t)(int)t;
   }
 }
@@ -104,6 +107,48 @@ __global__ void w8_repack_kernel(const uint8_t* __restrict__ q, const uint16_t* 
   }
   if (idx < N * G) {
     // destination order: t, g, n%16
+    int64_t r = idx & 15;
+    int64_t tg = idx >> 4;
+    int64_t g = tg % G, t = tg / G;
+    int64_t n = repack_src_row(t * 16 + r, N, paired);
+    uint32_t sv = s[n * G + g], bv = b[n * G + g];
+    sb[idx] = sv | (bv << 16);
+  }
+}
+
+// W4 tiled layout: wt4[t][g][lane][8 B], the same (row, 16-column chunk) per lane as the W8
+// layout with two codes per byte: byte j holds columns 2j (low nibble) and 2j + 1 (high nibble)
+// of the lane's 16. One thread per lane-chunk; sb as for W8 (written by the W8 repack's loop).
+__global__ void w4_repack_kernel(const uint8_t* __restrict__ q, const uint16_t* __restrict__ s,
+                                 const uint16_t* __restrict__ b, int64_t N, int64_t K, int paired,
+                                 uint2* __restrict__ wt, uint32_t* __restrict__ sb) {
+  const int64_t G = K / 64;
+  const int64_t chunks = N * K / 16;
+  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx < chunks) {
+    int64_t lane = idx & 63;
+    int64_t tg = idx >> 6;
+    int64_t g = tg % G, t = tg / G;
+    int64_t n = repack_src_row(t * 16 + (lane & 15), N, paired);
+    int64_t k = g * 64 + (lane >> 4) * 16;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(q + n * K + k);
+    uint32_t o[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t lo = v[2 * h], hi = v[2 * h + 1];  // codes 8h .. 8h + 7, one per byte
+      uint32_t w = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t src = j < 2 ? lo : hi;
+        const int sh = (j & 1) * 16;
+        const uint32_t c0 = (src >> sh) & 0xfu, c1 = (src >> (sh + 8)) & 0xfu;
+        w |= (c0 | (c1 << 4)) << (8 * j);
+      }
+      o[h] = w;
+    }
+    wt[idx] = uint2{o[0], o[1]};
+  }
+  if (idx < N * G) {
     int64_t r = idx & 15;
     int64_t tg = idx >> 4;
     int64_t g = tg % G, t = tg / G;
@@ -299,6 +344,7 @@ struct GemmArgs {
   const uint16_t* res;
   int64_t ldr;
   float softcap;
+  int bits;         // weight code width: 8 (dsk_w8_gemm) or 4 (dsk_w4_gemm)
 };
 
 __device__ __forceinline__ void gemm_store(const GemmArgs& a, int m, int64_t n, float v) {
@@ -321,22 +367,45 @@ __device__ __forceinline__ void gemm_store_gated(const GemmArgs& a, int m, int64
 // One batch of U groups: the weight, scale/bias and activation registers of U consecutive
 // groups for NT tiles. Padding rows of the packed activation hold arbitrary values; their
 // outputs are never stored.
-template <int MT, int NT, int U>
+// 16 4-bit codes (8 bytes, byte j = codes 2j | 2j+1 << 4) -> two bf16 x 8 holding 128 + code
+// (exact: 0x4300 | c is the bf16 of 128 + c); the group's bias is offset by -128 s to match.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void u4x16_to_bf16(const u32x2 w, bf16x8& lo, bf16x8& hi) {
+  uint32_t r[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t v = w[h];
+    const uint32_t t = v & 0x0f0f0f0fu, u = (v >> 4) & 0x0f0f0f0fu;  // even / odd codes, one per byte
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      r[4 * h + i] = __builtin_amdgcn_perm(u, t, 0x0c040c00u + 0x00010001u * i) | 0x43004300u;
+  }
+  lo = __builtin_bit_cast(bf16x8, (u32x4{r[0], r[1], r[2], r[3]}));
+  hi = __builtin_bit_cast(bf16x8, (u32x4{r[4], r[5], r[6], r[7]}));
+}
+
+template <int BITS> struct WeightChunk;
+template <> struct WeightChunk<8> { using type = u32x4; };
+template <> struct WeightChunk<4> { using type = u32x2; };
+
+template <int MT, int NT, int U, int BITS>
 struct Batch {
-  u32x4 wv[U][NT];
+  typename WeightChunk<BITS>::type wv[U][NT];
   uint32_t sv[U][NT];
   u32x4 xv[U][MT][2];
 };
 
-template <int MT, int NT, int U>
+template <int MT, int NT, int U, int BITS>
 __device__ __forceinline__ void batch_load(const GemmArgs& a, int64_t t0, int64_t g0, int lane,
-                                           Batch<MT, NT, U>& r) {
+                                           Batch<MT, NT, U, BITS>& r) {
+  using WT = typename WeightChunk<BITS>::type;
+  const WT* wt = reinterpret_cast<const WT*>(a.wt);
 #pragma unroll
   for (int c = 0; c < U; ++c)
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       const int64_t tg = (t0 + j) * a.G + g0 + c;
-      r.wv[c][j] = __builtin_nontemporal_load(&a.wt[tg * 64 + lane]);
+      r.wv[c][j] = __builtin_nontemporal_load(&wt[tg * 64 + lane]);
     }
 #pragma unroll
   for (int c = 0; c < U; ++c)
@@ -352,8 +421,8 @@ __device__ __forceinline__ void batch_load(const GemmArgs& a, int64_t t0, int64_
     }
 }
 
-template <int MT, int NT, int U>
-__device__ __forceinline__ void batch_compute(const Batch<MT, NT, U>& r, f32x4 (&acc)[MT][NT]) {
+template <int MT, int NT, int U, int BITS>
+__device__ __forceinline__ void batch_compute(const Batch<MT, NT, U, BITS>& r, f32x4 (&acc)[MT][NT]) {
   const u32x4 ones_u = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
   const bf16x8 ones = __builtin_bit_cast(bf16x8, ones_u);
 #pragma unroll
@@ -368,9 +437,14 @@ __device__ __forceinline__ void batch_compute(const Batch<MT, NT, U>& r, f32x4 (
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       bf16x8 b0, b1;
-      u8x16_to_bf16(r.wv[c][j], b0, b1);
       const float s = bf16_to_f32((uint16_t)(r.sv[c][j] & 0xffffu));
-      const float bb = bf16_to_f32((uint16_t)(r.sv[c][j] >> 16));
+      float bb = bf16_to_f32((uint16_t)(r.sv[c][j] >> 16));
+      if constexpr (BITS == 8) {
+        u8x16_to_bf16(r.wv[c][j], b0, b1);
+      } else {
+        u4x16_to_bf16(r.wv[c][j], b0, b1);
+        bb = fmaf(-128.0f, s, bb);  // x . (128 + q) = 128 X + x . q
+      }
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.xv[c][i][0]), b0,
@@ -388,12 +462,12 @@ __device__ __forceinline__ void batch_compute(const Batch<MT, NT, U>& r, f32x4 (
 // wave loads feeds NT tiles), then reduce through LDS in wave order.
 // EK: the epilogue family (0 store, 1 gated, 2 split-K partial) as a template parameter, so each
 // family is its own (smaller) kernel. PF: software-pipelined batch loads (two register sets).
-template <int MT, int NT, int U, int WAVES, int EK, bool PF>
+template <int MT, int NT, int U, int WAVES, int EK, bool PF, int BITS>
 __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int slab = blockIdx.x / a.SK, ks = blockIdx.x % a.SK;
-  const int64_t g_lo = (int64_t)ks * a.gpb;
+  const int64_t g_lo = min(a.G, (int64_t)ks * a.gpb);  // a trailing split may be empty: it stores zeros
   const int64_t g_hi = min(a.G, g_lo + a.gpb);
   const int nbatch = (int)((g_hi - g_lo) / U);
   const int64_t t0 = (int64_t)slab * NT;
@@ -408,24 +482,24 @@ __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
     // software pipeline over the wave's batches (bt = wave, wave + WAVES, ...): the next
     // batch's loads are issued before the current one is computed, alternating two register sets
     if (wave < nbatch) {
-      Batch<MT, NT, U> ra, rb;
-      batch_load<MT, NT, U>(a, t0, g_lo + (int64_t)wave * U, lane, ra);
+      Batch<MT, NT, U, BITS> ra, rb;
+      batch_load<MT, NT, U, BITS>(a, t0, g_lo + (int64_t)wave * U, lane, ra);
       for (int bt = wave;;) {
-        if (bt + WAVES < nbatch) batch_load<MT, NT, U>(a, t0, g_lo + (int64_t)(bt + WAVES) * U, lane, rb);
-        batch_compute<MT, NT, U>(ra, acc);
+        if (bt + WAVES < nbatch) batch_load<MT, NT, U, BITS>(a, t0, g_lo + (int64_t)(bt + WAVES) * U, lane, rb);
+        batch_compute<MT, NT, U, BITS>(ra, acc);
         bt += WAVES;
         if (bt >= nbatch) break;
-        if (bt + WAVES < nbatch) batch_load<MT, NT, U>(a, t0, g_lo + (int64_t)(bt + WAVES) * U, lane, ra);
-        batch_compute<MT, NT, U>(rb, acc);
+        if (bt + WAVES < nbatch) batch_load<MT, NT, U, BITS>(a, t0, g_lo + (int64_t)(bt + WAVES) * U, lane, ra);
+        batch_compute<MT, NT, U, BITS>(rb, acc);
         bt += WAVES;
         if (bt >= nbatch) break;
       }
     }
   } else {
     for (int bt = wave; bt < nbatch; bt += WAVES) {
-      Batch<MT, NT, U> r;
-      batch_load<MT, NT, U>(a, t0, g_lo + (int64_t)bt * U, lane, r);
-      batch_compute<MT, NT, U>(r, acc);
+      Batch<MT, NT, U, BITS> r;
+      batch_load<MT, NT, U, BITS>(a, t0, g_lo + (int64_t)bt * U, lane, r);
+      batch_compute<MT, NT, U, BITS>(r, acc);
     }
   }
 
@@ -497,7 +571,7 @@ struct GemmPlan {
 // tiles, 4 K splits, 8 waves). Rules fitted to a sweep on MI355X at M = 16 over
 // the Qwen3-8B verify shapes (qkv 6144x4096, o 4096x4096, gate_up 24576x4096, down
 // 4096x12288, head 151936x4096): each lands within 5% of the best configuration measured.
-static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi) {
+static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi, int bits = 8) {
   const int64_t G = K / 64;
   const int64_t tiles = N / 16;
   const int MT = (M + 15) / 16;
@@ -514,7 +588,9 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi) {
   p.sk = 1;
   if (partial)
     while (slabs * p.sk < 512 && batches / (p.sk * 2) >= 4 && p.sk < 16) p.sk *= 2;
-  const int64_t bps = batches / p.sk;  // batches per split
+  // batches per split, rounded up: the last split takes what is left (K = 9728 in 8 splits:
+  // 7 x 20 groups + 12)
+  const int64_t bps = (batches + p.sk - 1) / p.sk;
   p.gpb = bps * p.u;
   p.waves = (bps >= 8 && bps < 12) ? 8 : 4;
   if (!partial && slabs < 128) p.waves = bps >= 32 ? 16 : (bps >= 8 ? 8 : 4);
@@ -528,6 +604,15 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi) {
     p.pf = true;
   }
   while ((size_t)p.waves * MT * p.nt * 1024 > 65536) p.waves /= 2;  // LDS of the reduction
+  // 4-bit codes: a wave's load of one tile-group is 512 B, half the 8-bit one. Where the waves
+  // of the plan above each run several unpipelined batches (4 waves: down, the head), batches
+  // of 4 groups halve the iterations at the same bytes in flight (W4 down 4096x12288 at M = 16:
+  // 13.6 -> 10.6 us, head 151936x4096: 120 -> 71 us); with 8 waves of one batch each (qkv, o)
+  // or the pipelined gated plan, 2-group batches measured faster.
+  if (bits == 4 && MT == 1 && !p.pf && p.waves == 4 && (p.nt == 1 || p.nt == 2 || p.nt == 4)) {
+    p.u = 4;
+    p.gpb = ((G / 4 + p.sk - 1) / p.sk) * 4;
+  }
   // tuning override (DSK_GEMM_TUNE="epi,N,nt,u,waves,sk,pf": applies to that epilogue and N)
   static const char* tune = getenv("DSK_GEMM_TUNE");
   if (tune) {
@@ -538,49 +623,50 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi) {
       p.u = tu;
       p.waves = tw;
       p.sk = tsk;
-      p.gpb = (G / p.u / p.sk) * p.u;
+      p.gpb = ((G / p.u + p.sk - 1) / p.sk) * p.u;
       p.pf = tpf != 0;
     }
   }
   return p;
 }
 
-template <int MT, int NT, int U, int WAVES, bool PF>
+template <int MT, int NT, int U, int WAVES, bool PF, int BITS>
 static bool launch_gemm_t(const GemmArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)(a.n_slabs * a.SK)), blk(WAVES * 64);
   if (a.epi == DSK_EPI_PARTIAL) {
-    hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 2, PF>), grid, blk, 0, st, a);
+    hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 2, PF, BITS>), grid, blk, 0, st, a);
   } else if (a.epi == DSK_EPI_STORE) {
-    hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 0, PF>), grid, blk, 0, st, a);
+    hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 0, PF, BITS>), grid, blk, 0, st, a);
   } else {
     if constexpr (NT % 2 != 0) return false;  // gated tiles come in gate|up pairs
-    else hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 1, PF>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 1, PF, BITS>), grid, blk, 0, st, a);
   }
   return true;
 }
 
-template <int MT, int NT, int U, bool PF>
+template <int MT, int NT, int U, bool PF, int BITS>
 static bool launch_gemm_w(const GemmArgs& a, int waves, hipStream_t st) {
   constexpr int max_waves = 65536 / (MT * NT * 1024);  // LDS of the cross-wave reduction
   switch (waves) {
-    case 4: if constexpr (max_waves >= 4) return launch_gemm_t<MT, NT, U, 4, PF>(a, st); return false;
-    case 8: if constexpr (max_waves >= 8) return launch_gemm_t<MT, NT, U, 8, PF>(a, st); return false;
-    case 16: if constexpr (max_waves >= 16) return launch_gemm_t<MT, NT, U, 16, PF>(a, st); return false;
+    case 4: if constexpr (max_waves >= 4) return launch_gemm_t<MT, NT, U, 4, PF, BITS>(a, st); return false;
+    case 8: if constexpr (max_waves >= 8) return launch_gemm_t<MT, NT, U, 8, PF, BITS>(a, st); return false;
+    case 16: if constexpr (max_waves >= 16) return launch_gemm_t<MT, NT, U, 16, PF, BITS>(a, st); return false;
   }
   return false;
 }
 
-static bool launch_gemm(const GemmArgs& a, int MT, const GemmPlan& p, hipStream_t st) {
+template <int BITS>
+static bool launch_gemm_bits(const GemmArgs& a, int MT, const GemmPlan& p, hipStream_t st) {
   if (p.pf) {  // the pipelined variant is built for the shapes the planner gives it
-    if (MT == 1 && p.nt == 2 && p.u == 2) return launch_gemm_w<1, 2, 2, true>(a, p.waves, st);
-    if (MT == 1 && p.nt == 2 && p.u == 4) return launch_gemm_w<1, 2, 4, true>(a, p.waves, st);
-    if (MT == 1 && p.nt == 4 && p.u == 2) return launch_gemm_w<1, 4, 2, true>(a, p.waves, st);
-    if (MT == 1 && p.nt == 1 && p.u == 4) return launch_gemm_w<1, 1, 4, true>(a, p.waves, st);
-    if (MT == 1 && p.nt == 1 && p.u == 2) return launch_gemm_w<1, 1, 2, true>(a, p.waves, st);
+    if (MT == 1 && p.nt == 2 && p.u == 2) return launch_gemm_w<1, 2, 2, true, BITS>(a, p.waves, st);
+    if (MT == 1 && p.nt == 2 && p.u == 4) return launch_gemm_w<1, 2, 4, true, BITS>(a, p.waves, st);
+    if (MT == 1 && p.nt == 4 && p.u == 2) return launch_gemm_w<1, 4, 2, true, BITS>(a, p.waves, st);
+    if (MT == 1 && p.nt == 1 && p.u == 4) return launch_gemm_w<1, 1, 4, true, BITS>(a, p.waves, st);
+    if (MT == 1 && p.nt == 1 && p.u == 2) return launch_gemm_w<1, 1, 2, true, BITS>(a, p.waves, st);
     return false;
   }
 #define DSK_GEMM_CASE(MT_, NT_, U_) \
-  if (MT == MT_ && p.nt == NT_ && p.u == U_) return launch_gemm_w<MT_, NT_, U_, false>(a, p.waves, st);
+  if (MT == MT_ && p.nt == NT_ && p.u == U_) return launch_gemm_w<MT_, NT_, U_, false, BITS>(a, p.waves, st);
   DSK_GEMM_CASE(1, 1, 2) DSK_GEMM_CASE(1, 2, 2) DSK_GEMM_CASE(1, 4, 2) DSK_GEMM_CASE(1, 8, 2)
   DSK_GEMM_CASE(1, 3, 2) DSK_GEMM_CASE(1, 6, 2)
   DSK_GEMM_CASE(1, 1, 4) DSK_GEMM_CASE(1, 2, 4) DSK_GEMM_CASE(1, 4, 4)
@@ -589,6 +675,10 @@ static bool launch_gemm(const GemmArgs& a, int MT, const GemmPlan& p, hipStream_
   DSK_GEMM_CASE(4, 1, 2) DSK_GEMM_CASE(4, 2, 2)
 #undef DSK_GEMM_CASE
   return false;
+}
+
+static bool launch_gemm(const GemmArgs& a, int MT, const GemmPlan& p, hipStream_t st) {
+  return a.bits == 4 ? launch_gemm_bits<4>(a, MT, p, st) : launch_gemm_bits<8>(a, MT, p, st);
 }
 
 // Fills GemmArgs for a plan; shared by the entry point and the tuning harness.
@@ -612,6 +702,7 @@ static void gemm_prepare(GemmArgs& a, const GemmPlan& p, const void* xp, const u
   a.res = residual;
   a.ldr = ldr;
   a.softcap = softcap;
+  a.bits = 8;
 }
 
 // chunks per thread (NV) x split slices kept in registers (MAXS): NV * MAXS <= 16
@@ -643,8 +734,22 @@ extern "C" int dsk_w8_quantize(const void* w, int w_dtype, int64_t N, int64_t K,
   int64_t total = N * (K / 64);
   int threads = 256;
   hipLaunchKernelGGL(w8_quantize_kernel, dim3((unsigned)ceil_div(total, threads)), dim3(threads), 0,
-                     as_stream(stream), w, w_dtype == DSK_BF16 ? 1 : 0, N, K, q, scales, biases);
+                     as_stream(stream), w, w_dtype == DSK_BF16 ? 1 : 0, N, K, q, scales, biases, 255.0f);
   DSK_LAUNCH_CHECK("dsk_w8_quantize");
+  return DSK_OK;
+}
+
+extern "C" int dsk_w4_quantize(const void* w, int w_dtype, int64_t N, int64_t K, uint8_t* q,
+                               uint16_t* scales, uint16_t* biases, dsk_stream_t stream) {
+  DSK_REQUIRE(w && q && scales && biases, "dsk_w4_quantize: null pointer");
+  DSK_REQUIRE(N > 0 && K > 0 && K % 64 == 0, "dsk_w4_quantize: need K %% 64 == 0 (N=%lld K=%lld)",
+              (long long)N, (long long)K);
+  DSK_REQUIRE(w_dtype == DSK_F32 || w_dtype == DSK_BF16, "dsk_w4_quantize: dtype must be f32 or bf16");
+  int64_t total = N * (K / 64);
+  int threads = 256;
+  hipLaunchKernelGGL(w8_quantize_kernel, dim3((unsigned)ceil_div(total, threads)), dim3(threads), 0,
+                     as_stream(stream), w, w_dtype == DSK_BF16 ? 1 : 0, N, K, q, scales, biases, 15.0f);
+  DSK_LAUNCH_CHECK("dsk_w4_quantize");
   return DSK_OK;
 }
 
@@ -660,6 +765,22 @@ extern "C" int dsk_w8_repack(const uint8_t* q, const uint16_t* scales, const uin
   hipLaunchKernelGGL(w8_repack_kernel, dim3((unsigned)ceil_div(total, threads)), dim3(threads), 0,
                      as_stream(stream), q, scales, biases, N, K, paired ? 1 : 0, reinterpret_cast<u32x4*>(wt), sb);
   DSK_LAUNCH_CHECK("dsk_w8_repack");
+  return DSK_OK;
+}
+
+extern "C" int dsk_w4_repack(const uint8_t* q, const uint16_t* scales, const uint16_t* biases, int64_t N,
+                             int64_t K, int paired, uint8_t* wt, uint32_t* sb, dsk_stream_t stream) {
+  DSK_REQUIRE(q && scales && biases && wt && sb, "dsk_w4_repack: null pointer");
+  DSK_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 64 == 0,
+              "dsk_w4_repack: need N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)", (long long)N,
+              (long long)K);
+  DSK_REQUIRE(!paired || N % 32 == 0, "dsk_w4_repack: paired layout needs N %% 32 == 0 (N=%lld)", (long long)N);
+  DSK_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)wt & 7) == 0, "dsk_w4_repack: q 16-byte, wt 8-byte aligned");
+  int64_t total = N * K / 16;
+  int threads = 256;
+  hipLaunchKernelGGL(w4_repack_kernel, dim3((unsigned)ceil_div(total, threads)), dim3(threads), 0,
+                     as_stream(stream), q, scales, biases, N, K, paired ? 1 : 0, reinterpret_cast<uint2*>(wt), sb);
+  DSK_LAUNCH_CHECK("dsk_w4_repack");
   return DSK_OK;
 }
 
@@ -704,9 +825,32 @@ extern "C" int dsk_w8_gemm_splits(int M, int64_t N, int64_t K) {
   return plan_gemm(M, N, K, DSK_EPI_PARTIAL).sk;
 }
 
+extern "C" int dsk_w4_gemm_splits(int M, int64_t N, int64_t K) {
+  if (M <= 0 || M > 64 || N <= 0 || N % 16 || K <= 0 || K % 256) return 0;
+  return plan_gemm(M, N, K, DSK_EPI_PARTIAL, 4).sk;
+}
+
+static int gemm_entry(const char* who, int bits, const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int M,
+                      int64_t N, int64_t K, int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
+                      int64_t ldr, float softcap, hipStream_t st);
+
 extern "C" int dsk_w8_gemm(const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int M, int64_t N, int64_t K,
                            int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual, int64_t ldr,
                            float softcap, dsk_stream_t stream) {
+  return gemm_entry("dsk_w8_gemm", 8, xp, wt, sb, M, N, K, epi, y, y_dtype, ldy, residual, ldr, softcap,
+                    as_stream(stream));
+}
+
+extern "C" int dsk_w4_gemm(const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int M, int64_t N, int64_t K,
+                           int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual, int64_t ldr,
+                           float softcap, dsk_stream_t stream) {
+  return gemm_entry("dsk_w4_gemm", 4, xp, wt, sb, M, N, K, epi, y, y_dtype, ldy, residual, ldr, softcap,
+                    as_stream(stream));
+}
+
+static int gemm_entry(const char* who, int bits, const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int M,
+                      int64_t N, int64_t K, int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
+                      int64_t ldr, float softcap, hipStream_t st) {
   DSK_REQUIRE(xp && wt && sb && y, "dsk_w8_gemm: null pointer");
   DSK_REQUIRE(M > 0 && M <= 64, "dsk_w8_gemm: M=%d outside [1, 64]", M);
   DSK_REQUIRE(N > 0 && N % 16 == 0 && K > 0 && K % 256 == 0,
@@ -726,14 +870,15 @@ extern "C" int dsk_w8_gemm(const uint16_t* xp, const uint8_t* wt, const uint32_t
                 "dsk_w8_gemm: gated epilogue needs N %% 256 == 0 and a bf16 (packed) output");
     DSK_REQUIRE(gated || y_dtype == DSK_F32, "dsk_w8_gemm: partial sums are f32");
   }
-  const GemmPlan p = plan_gemm(M, N, K, epi);
+  const GemmPlan p = plan_gemm(M, N, K, epi, bits);
   GemmArgs a;
   gemm_prepare(a, p, xp, wt, sb, M, N, K, epi, y, y_dtype, ldy, residual, ldr, softcap);
-  if (!launch_gemm(a, (M + 15) / 16, p, as_stream(stream))) {
-    set_error("dsk_w8_gemm: no kernel for M=%d NT=%d U=%d waves=%d", M, p.nt, p.u, p.waves);
+  a.bits = bits;
+  if (!launch_gemm(a, (M + 15) / 16, p, st)) {
+    set_error("%s: no kernel for M=%d NT=%d U=%d waves=%d", who, M, p.nt, p.u, p.waves);
     return DSK_EINVAL;
   }
-  DSK_LAUNCH_CHECK("dsk_w8_gemm");
+  DSK_LAUNCH_CHECK(who);
   return DSK_OK;
 }
 

@@ -23,12 +23,18 @@ SIGNATURES: dict[str, tuple] = {
     "dsk_w8_quantize": (c_int, [c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]),
     "dsk_w8_repack": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p,
                               c_void_p]),
+    "dsk_w4_quantize": (c_int, [c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "dsk_w4_repack": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p,
+                              c_void_p]),
+    "dsk_w4_gemm": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int, c_void_p, c_int, c_int64,
+                            c_void_p, c_int64, c_float, c_void_p]),
     "dsk_act_pack_bytes": (c_size_t, [c_int, c_int64]),
     "dsk_act_pack": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int, c_int64, c_void_p,
                              c_float, c_void_p, c_void_p]),
     "dsk_act_pack_scaled": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int, c_int64,
                                     c_void_p, c_float, c_float, c_void_p, c_void_p]),
     "dsk_w8_gemm_splits": (c_int, [c_int, c_int64, c_int64]),
+    "dsk_w4_gemm_splits": (c_int, [c_int, c_int64, c_int64]),
     "dsk_w8_gemm": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int, c_void_p, c_int, c_int64,
                             c_void_p, c_int64, c_float, c_void_p]),
     "dsk_w8_embed": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float,

@@ -1,11 +1,12 @@
 """Local MLX-format checkpoints for the target (the on-disk format the reference loads through
 mlx_lm.load, src/mlx_dspark/load.py:314-351).
 
-A checkpoint directory holds ``config.json`` and ``model*.safetensors``. Each linear layer of an
-8-bit MLX checkpoint is three tensors: ``<name>.weight`` uint32 [N, K/4] (four 8-bit codes per
-word, lowest byte first), ``<name>.scales`` and ``<name>.biases`` [N, K/64] (w = s * q + b,
-group 64); ``config.json["quantization"]`` names the bits and group size. Unquantized
-checkpoints (bf16/f32 ``<name>.weight`` [N, K]) are quantized to W8 on load. The tensors are
+A checkpoint directory holds ``config.json`` and ``model*.safetensors``. Each linear layer of a
+quantized MLX checkpoint is three tensors: ``<name>.weight`` uint32 [N, K * bits / 32] (four
+8-bit or eight 4-bit codes per word, lowest bits first), ``<name>.scales`` and
+``<name>.biases`` [N, K/64] (w = s * q + b, group 64); ``config.json["quantization"]`` names
+the bits (8 or 4) and group size. Unquantized checkpoints (bf16/f32 ``<name>.weight`` [N, K])
+are quantized to W8 on load. The tensors are
 read once, the q/k/v rows stacked into the fused projection and gate/up paired, and every
 matrix repacked into the engine's tiled layout (dsk_w8_repack).
 
@@ -66,9 +67,9 @@ def _quantization(cfg: dict):
     if not q:
         return None
     bits, gs = int(q.get("bits", 0)), int(q.get("group_size", 0))
-    if bits != 8 or gs != 64:
-        raise ValueError(f"quantization bits={bits} group_size={gs}: this engine runs W8 group 64 "
-                         f"(8-bit MLX checkpoints or unquantized ones, which it quantizes)")
+    if bits not in (4, 8) or gs != 64:
+        raise ValueError(f"quantization bits={bits} group_size={gs}: this engine runs 8- or 4-bit codes "
+                         f"with group 64 (or unquantized checkpoints, which it quantizes)")
     return bits, gs
 
 
@@ -93,14 +94,20 @@ class _Tensors:
         return self.files[key].get_tensor(key).to(self.device)
 
 
-def _mlx_triplet(t: _Tensors, name: str, N: int, K: int, quantized: bool):
-    """(q u8 [N, K], scales, biases bf16 [N, K/64]) of one linear (quantizing a plain weight)."""
+def _mlx_triplet(t: _Tensors, name: str, N: int, K: int, bits: int | None):
+    """(codes u8 [N, K] one per byte, scales, biases bf16 [N, K/64]) of one linear (quantizing a
+    plain weight when bits is None)."""
     w = t.get(name + ".weight")
-    if quantized:
-        if w.dtype not in (torch.uint32, torch.int32) or tuple(w.shape) != (N, K // 4):
-            raise ValueError(f"{name}.weight: expected 8-bit packed uint32 [{N}, {K // 4}], got {w.dtype} "
+    if bits:
+        words = K * bits // 32
+        if w.dtype not in (torch.uint32, torch.int32) or tuple(w.shape) != (N, words):
+            raise ValueError(f"{name}.weight: expected {bits}-bit packed uint32 [{N}, {words}], got {w.dtype} "
                              f"{tuple(w.shape)}")
-        q = w.contiguous().view(torch.uint8).view(N, K)
+        by = w.contiguous().view(torch.uint8).view(N, K * bits // 8)
+        if bits == 8:
+            q = by
+        else:   # two codes per byte, low nibble first
+            q = torch.stack([by & 0xF, by >> 4], dim=-1).view(N, K)
         s = t.get(name + ".scales").to(torch.bfloat16)
         b = t.get(name + ".biases").to(torch.bfloat16)
         if tuple(s.shape) != (N, K // 64) or tuple(b.shape) != (N, K // 64):
@@ -111,12 +118,12 @@ def _mlx_triplet(t: _Tensors, name: str, N: int, K: int, quantized: bool):
     return W8Weight.quantize_mlx(w.to(torch.bfloat16) if w.dtype != torch.float32 else w)
 
 
-def _w8(t, names_rows, K, quantized, paired=False) -> W8Weight:
-    parts = [_mlx_triplet(t, n, rows, K, quantized) for n, rows in names_rows]
+def _w8(t, names_rows, K, bits, paired=False) -> W8Weight:
+    parts = [_mlx_triplet(t, n, rows, K, bits) for n, rows in names_rows]
     q = torch.cat([p[0] for p in parts]) if len(parts) > 1 else parts[0][0]
     s = torch.cat([p[1] for p in parts]) if len(parts) > 1 else parts[0][1]
     b = torch.cat([p[2] for p in parts]) if len(parts) > 1 else parts[0][2]
-    return W8Weight.from_mlx(q, s, b, paired)
+    return W8Weight.from_mlx(q, s, b, paired, bits or 8)
 
 
 def _vec(t: _Tensors, name: str, n: int) -> torch.Tensor:
@@ -130,7 +137,8 @@ def load_qwen3_w8(path, device="cuda") -> Qwen3W8:
     """The target of a local MLX checkpoint directory as the engine's W8 model."""
     cfg = read_config(path)
     args = target_args_from_config(cfg)
-    quantized = _quantization(cfg) is not None
+    qz = _quantization(cfg)
+    quantized = qz[0] if qz is not None else None   # code width, or None: quantize to 8-bit
     device = torch.device(device)
     t = _Tensors(path, device)
     H, I = args.hidden_size, args.intermediate_size
@@ -150,7 +158,7 @@ def load_qwen3_w8(path, device="cuda") -> Qwen3W8:
     eq, es, eb = _mlx_triplet(t, "model.embed_tokens", args.vocab_size, H, quantized)
     embed = W8Table(eq, es, eb)
     if args.tie_word_embeddings or not t.has("lm_head.weight"):
-        lm_head = W8Weight.from_mlx(eq, es, eb)
+        lm_head = W8Weight.from_mlx(eq, es, eb, bits=quantized or 8)
     else:
         lm_head = _w8(t, [("lm_head", args.vocab_size)], H, quantized)
     norm = _vec(t, "model.norm.weight", H)
@@ -170,18 +178,24 @@ def load_tokenizer(path):
 
 
 def save_qwen3_w8(model: Qwen3W8, path, config_extra: dict | None = None) -> None:
-    """Write a model built with keep_mlx=True as an 8-bit MLX checkpoint (config.json +
-    model.safetensors) - the inverse of load_qwen3_w8, for tests and round trips."""
+    """Write a model built with keep_mlx=True as a quantized MLX checkpoint (config.json +
+    model.safetensors; 8- or 4-bit codes as the model's layers hold them; the embedding table
+    is written at the same width) - the inverse of load_qwen3_w8, for tests and round trips."""
     from safetensors.torch import save_file
     a = model.args
     nq, nkv, hd, I = a.num_attention_heads, a.num_key_value_heads, a.head_dim, a.intermediate_size
     out = {}
 
+    bits = model.layers[0].qkv.bits
+
     def put(name, trip, r0=None, r1=None):
         q, s, b = trip
         if r0 is not None:
             q, s, b = q[r0:r1], s[r0:r1], b[r0:r1]
-        out[name + ".weight"] = q.contiguous().view(torch.uint32).cpu()
+        q = q.contiguous()
+        if bits == 4:    # two codes per byte, low nibble first
+            q = (q.view(q.shape[0], -1, 2)[..., 0] | (q.view(q.shape[0], -1, 2)[..., 1] << 4)).contiguous()
+        out[name + ".weight"] = q.view(torch.uint32).cpu()
         out[name + ".scales"] = s.contiguous().cpu()
         out[name + ".biases"] = b.contiguous().cpu()
 
@@ -208,7 +222,7 @@ def save_qwen3_w8(model: Qwen3W8, path, config_extra: dict | None = None) -> Non
            "intermediate_size": I, "num_attention_heads": nq, "num_key_value_heads": nkv, "head_dim": hd,
            "vocab_size": a.vocab_size, "rms_norm_eps": a.rms_norm_eps, "rope_theta": a.rope_theta,
            "tie_word_embeddings": a.tie_word_embeddings, "max_position_embeddings": a.max_position_embeddings,
-           "quantization": {"group_size": 64, "bits": 8}}
+           "quantization": {"group_size": 64, "bits": bits}}
     cfg.update(config_extra or {})
     with open(Path(str(path)) / "config.json", "w") as f:
         json.dump(cfg, f, indent=1)

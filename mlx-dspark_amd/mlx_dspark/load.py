@@ -108,28 +108,30 @@ def load_target(repo_or_path: str = DEFAULT_TARGET, *, require_tap: bool = False
     return target, tok
 
 
-def load_dflash(repo_or_path: str, *, quantize: bool = True, bits: int = 8, group_size: int = 64,
+def load_dflash(repo_or_path: str, *, quantize: bool = True, bits: int = 4, group_size: int = 64,
                 target_args: TargetArgs | None = None, seed: int = 1, keep_mlx: bool = False):
-    """(drafter, config) for a synthetic DFlash drafter (load.py:224-289); W8 by default."""
-    if bits != 8 or group_size != 64 or not quantize:
-        raise ValueError("this engine runs W8 (group 64) drafters")
+    """(drafter, config) for a synthetic DFlash drafter (load.py:224-289); its linear layers
+    4-bit by default, as the reference quantizes them (8 also runs)."""
+    if bits not in (4, 8) or group_size != 64 or not quantize:
+        raise ValueError("this engine runs 4- or 8-bit (group 64) drafters")
     key = _synthetic_key(repo_or_path)
     if not key.startswith("dflash-"):
         raise ValueError(f"{repo_or_path!r} is not a DFlash drafter name")
     tkey = key[len("dflash-"):]
     if target_args is None:
         target_args = synthetic.target_args(tkey)
-    return synthetic.build_dflash(target_args, seed=seed, keep_mlx=keep_mlx)
+    return synthetic.build_dflash(target_args, seed=seed, keep_mlx=keep_mlx, bits=bits)
 
 
-def load_drafter(repo_or_path: str = DEFAULT_DRAFTER, *, quantize: bool = True, bits: int = 8,
+def load_drafter(repo_or_path: str = DEFAULT_DRAFTER, *, quantize: bool = True, bits: int = 4,
                  group_size: int = 64, strict: bool = True, target_args: TargetArgs | None = None, seed: int = 2,
                  keep_mlx: bool = False, **shape):
-    """(drafter, config) for a synthetic DSpark drafter (load.py:155-215); W8 by default.
+    """(drafter, config) for a synthetic DSpark drafter (load.py:155-215); linear layers 4-bit by
+    default, as the reference quantizes them (8 also runs; the embedding and Markov head 8-bit).
     ``shape`` overrides the builder's drafter knobs (num_hidden_layers, block_size, taps,
     markov_rank, confidence, family: gemma4 by default for Gemma-style targets)."""
-    if bits != 8 or group_size != 64 or not quantize:
-        raise ValueError("this engine runs W8 (group 64) drafters")
+    if bits not in (4, 8) or group_size != 64 or not quantize:
+        raise ValueError("this engine runs 4- or 8-bit (group 64) drafters")
     key = _synthetic_key(repo_or_path)
     if not key.startswith("dspark-"):
         raise ValueError(f"{repo_or_path!r} is not a DSpark drafter name")
@@ -140,7 +142,7 @@ def load_drafter(repo_or_path: str = DEFAULT_DRAFTER, *, quantize: bool = True, 
         target_args = synthetic.target_args(tkey)
     # Gemma-family targets get the gemma4 drafter layout, as their DeepSpec drafters have
     shape.setdefault("family", "gemma4" if str(target_args.model_type).startswith("gemma") else "qwen3")
-    return synthetic.build_dspark(target_args, seed=seed, keep_mlx=keep_mlx, **shape)
+    return synthetic.build_dspark(target_args, seed=seed, keep_mlx=keep_mlx, bits=bits, **shape)
 
 
 def load_pair(model: str = DEFAULT_TARGET, *, drafter=None, kv_bits=None, keep_mlx: bool = False, max_ctx=None,

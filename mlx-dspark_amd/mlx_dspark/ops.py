@@ -69,25 +69,30 @@ class Workspace:
 # ----------------------------------------------------------------------------- W8 weights
 @dataclass
 class W8Weight:
-    """A W8 affine group-64 matrix [N, K] in the engine's tiled layout (see w8.hip).
+    """An affine group-64 matrix [N, K] (8-bit codes, or 4-bit with bits=4) in the engine's tiled
+    layout (see w8.hip).
 
     ``paired``: the rows are a gate projection stacked on an up projection, repacked so the
     GEMM's gated epilogue (SwiGLU / GeGLU) sees both halves of a column in one workgroup."""
 
-    wt: torch.Tensor     # uint8 [N*K]
+    wt: torch.Tensor     # uint8 [N*K*bits/8]
     sb: torch.Tensor     # int32 [N/16, K/64, 16] (bf16 scale | bf16 bias << 16)
     N: int
     K: int
     paired: bool = False
+    bits: int = 8
 
     @property
     def nbytes(self) -> int:
         return self.wt.numel() + self.sb.numel() * 4
 
     @staticmethod
-    def quantize_mlx(w: torch.Tensor):
-        """w [N, K] f32/bf16 on device -> MLX-layout (q u8 [N, K], scales, biases bf16 [N, K/64])."""
+    def quantize_mlx(w: torch.Tensor, bits: int = 8):
+        """w [N, K] f32/bf16 on device -> MLX-layout codes (q u8 [N, K], 0..2^bits-1, one per
+        byte), scales, biases bf16 [N, K/64]."""
         _require_cuda(w)
+        if bits not in (4, 8):
+            raise ValueError(f"bits={bits}: 4 or 8")
         w = w.contiguous()
         N, K = w.shape
         q = torch.empty((N, K), dtype=torch.uint8, device=w.device)
@@ -96,30 +101,34 @@ class W8Weight:
         dt = DSK_BF16 if w.dtype == torch.bfloat16 else DSK_F32
         if dt == DSK_F32 and w.dtype != torch.float32:
             w = w.float()
-        call("dsk_w8_quantize", ptr(w), dt, N, K, ptr(q), ptr(s), ptr(b), stream_ptr())
+        call("dsk_w8_quantize" if bits == 8 else "dsk_w4_quantize", ptr(w), dt, N, K, ptr(q), ptr(s), ptr(b),
+             stream_ptr())
         return q, s, b
 
     @classmethod
-    def from_mlx(cls, q: torch.Tensor, s: torch.Tensor, b: torch.Tensor, paired: bool = False) -> "W8Weight":
+    def from_mlx(cls, q: torch.Tensor, s: torch.Tensor, b: torch.Tensor, paired: bool = False,
+                 bits: int = 8) -> "W8Weight":
+        """q: codes one per byte [N, K] (4-bit codes in 0..15 with bits=4)."""
         _require_cuda(q, s, b)
         N, K = q.shape
-        wt = torch.empty(N * K, dtype=torch.uint8, device=q.device)
+        wt = torch.empty(N * K * bits // 8, dtype=torch.uint8, device=q.device)
         sb = torch.empty((N // 16, K // 64, 16), dtype=torch.int32, device=q.device)
-        call("dsk_w8_repack", ptr(q.contiguous()), ptr(s.contiguous()), ptr(b.contiguous()), N, K, int(paired),
-             ptr(wt), ptr(sb), stream_ptr())
-        return cls(wt, sb, N, K, paired)
+        call("dsk_w8_repack" if bits == 8 else "dsk_w4_repack", ptr(q.contiguous()), ptr(s.contiguous()),
+             ptr(b.contiguous()), N, K, int(paired), ptr(wt), ptr(sb), stream_ptr())
+        return cls(wt, sb, N, K, paired, bits)
 
     @classmethod
-    def quantize(cls, w: torch.Tensor, paired: bool = False) -> "W8Weight":
-        q, s, b = cls.quantize_mlx(w)
-        return cls.from_mlx(q, s, b, paired)
+    def quantize(cls, w: torch.Tensor, paired: bool = False, bits: int = 8) -> "W8Weight":
+        q, s, b = cls.quantize_mlx(w, bits)
+        return cls.from_mlx(q, s, b, paired, bits)
 
     def rows(self, n0: int, n1: int) -> "W8Weight":
         """Zero-copy view of output rows [n0, n1) (multiples of 16, unpaired layouts)."""
         if self.paired or n0 % 16 or n1 % 16 or not 0 <= n0 < n1 <= self.N:
             raise ValueError(f"rows({n0}, {n1}) of a {self.N}-row W8 weight")
-        tb = (self.K // 64) * 1024
-        return W8Weight(self.wt[n0 // 16 * tb:n1 // 16 * tb], self.sb[n0 // 16:n1 // 16], n1 - n0, self.K)
+        tb = (self.K // 64) * 128 * self.bits
+        return W8Weight(self.wt[n0 // 16 * tb:n1 // 16 * tb], self.sb[n0 // 16:n1 // 16], n1 - n0, self.K,
+                        bits=self.bits)
 
 
 @dataclass
@@ -201,8 +210,9 @@ def pack(x: torch.Tensor, norm_w: torch.Tensor | None = None, eps: float = 1e-6)
     return act_pack(M=x.shape[0], K=x.shape[1], h=x, norm_w=norm_w, eps=eps)
 
 
-def gemm_splits(M: int, N: int, K: int) -> int:
-    return _hip.lib.dsk_w8_gemm_splits(M, N, K)
+def gemm_splits(M: int, N: int, K: int, bits: int = 8) -> int:
+    """K-split slices of a DSK_EPI_PARTIAL product (the 4-bit kernel plans its own)."""
+    return (_hip.lib.dsk_w8_gemm_splits if bits == 8 else _hip.lib.dsk_w4_gemm_splits)(M, N, K)
 
 
 def w8_gemm(x: Packed, w: W8Weight, *, epi: int = DSK_EPI_STORE, out=None, out_dtype: torch.dtype = torch.bfloat16,
@@ -221,7 +231,7 @@ def w8_gemm(x: Packed, w: W8Weight, *, epi: int = DSK_EPI_STORE, out=None, out_d
             out = torch.empty((M, w.N), dtype=out_dtype, device=dev)
         ydata, ldy, yd = out, out.stride(0), (DSK_F32 if out.dtype == torch.float32 else DSK_BF16)
     elif epi == DSK_EPI_PARTIAL:
-        S = gemm_splits(M, w.N, w.K)
+        S = gemm_splits(M, w.N, w.K, w.bits)
         if out is None:
             out = torch.empty((S, M, w.N), dtype=torch.float32, device=dev)
         elif tuple(out.shape) != (S, M, w.N) or out.dtype != torch.float32:
@@ -233,8 +243,9 @@ def w8_gemm(x: Packed, w: W8Weight, *, epi: int = DSK_EPI_STORE, out=None, out_d
         if out is None:
             out = Packed.empty(M, w.N // 2, dev)
         ydata = out.data
-    call("dsk_w8_gemm", ptr(x.data), ptr(w.wt), ptr(w.sb), M, w.N, w.K, int(epi), ptr(ydata), yd, ldy,
-         ptr(residual), residual.stride(0) if residual is not None else 0, float(softcap), stream_ptr())
+    call("dsk_w8_gemm" if w.bits == 8 else "dsk_w4_gemm", ptr(x.data), ptr(w.wt), ptr(w.sb), M, w.N, w.K, int(epi),
+         ptr(ydata), yd, ldy, ptr(residual), residual.stride(0) if residual is not None else 0, float(softcap),
+         stream_ptr())
     return out
 
 

@@ -69,19 +69,21 @@ def randn(shape, seed: int, name: str, device, std: float = STD) -> torch.Tensor
     return torch.randn(shape, generator=g, device=device, dtype=torch.float32) * std
 
 
-def w8(N: int, K: int, seed: int, name: str, device, keep_mlx: bool = False, paired: bool = False) -> W8Weight:
+def w8(N: int, K: int, seed: int, name: str, device, keep_mlx: bool = False, paired: bool = False,
+       bits: int = 8) -> W8Weight:
+    """A seeded random [N, K] weight quantized affine group 64 (8-bit, or 4-bit codes)."""
     w = randn((N, K), seed, name, device)
-    q, s, b = W8Weight.quantize_mlx(w)
+    q, s, b = W8Weight.quantize_mlx(w, bits)
     del w
-    W = W8Weight.from_mlx(q, s, b, paired)
+    W = W8Weight.from_mlx(q, s, b, paired, bits)
     if keep_mlx:
         W.mlx = (q, s, b)
     return W
 
 
-def w8_table(V: int, H: int, seed: int, name: str, device) -> W8Table:
+def w8_table(V: int, H: int, seed: int, name: str, device, bits: int = 8) -> W8Table:
     w = randn((V, H), seed, name, device)
-    q, s, b = W8Weight.quantize_mlx(w)
+    q, s, b = W8Weight.quantize_mlx(w, bits)
     return W8Table(q, s, b)
 
 
@@ -95,7 +97,9 @@ def qk_norm(hd: int, device) -> torch.Tensor:
     return torch.full((hd,), hd ** -0.25, dtype=torch.bfloat16, device=device)
 
 
-def build_target(name_or_args, seed: int = 0, device="cuda", keep_mlx: bool = False) -> Qwen3W8:
+def build_target(name_or_args, seed: int = 0, device="cuda", keep_mlx: bool = False, bits: int = 8) -> Qwen3W8:
+    """A seeded random-init target; bits = 4 quantizes every linear and the embedding to 4-bit
+    codes (an MLX 4-bit checkpoint's layout)."""
     if isinstance(name_or_args, TargetArgs):
         args = name_or_args
     else:
@@ -107,21 +111,21 @@ def build_target(name_or_args, seed: int = 0, device="cuda", keep_mlx: bool = Fa
     for l in range(args.num_hidden_layers):
         p = f"layers.{l}."
         layers.append(LayerWeights(
-            qkv=w8(args.n_qkv, H, seed, p + "qkv", device, keep_mlx),
-            o=w8(H, nq * hd, seed, p + "o", device, keep_mlx),
-            gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx, paired=True),
-            down=w8(H, I, seed, p + "down", device, keep_mlx),
+            qkv=w8(args.n_qkv, H, seed, p + "qkv", device, keep_mlx, bits=bits),
+            o=w8(H, nq * hd, seed, p + "o", device, keep_mlx, bits=bits),
+            gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx, paired=True, bits=bits),
+            down=w8(H, I, seed, p + "down", device, keep_mlx, bits=bits),
             in_norm=ones(H, device), post_norm=ones(H, device),
             q_norm=qk_norm(hd, device), k_norm=qk_norm(hd, device),
             attn_out_norm=ones(H, device) if args.sandwich_norms else None,
             ff_out_norm=ones(H, device) if args.sandwich_norms else None))
-    embed = w8_table(args.vocab_size, H, seed, "embed_tokens", device)
+    embed = w8_table(args.vocab_size, H, seed, "embed_tokens", device, bits=bits)
     if args.tie_word_embeddings:
-        lm_head = W8Weight.from_mlx(embed.q, embed.s, embed.b)
+        lm_head = W8Weight.from_mlx(embed.q, embed.s, embed.b, bits=bits)
         if keep_mlx:
             lm_head.mlx = (embed.q, embed.s, embed.b)
     else:
-        lm_head = w8(args.vocab_size, H, seed, "lm_head", device, keep_mlx)
+        lm_head = w8(args.vocab_size, H, seed, "lm_head", device, keep_mlx, bits=bits)
     torch.cuda.synchronize(device)
     return Qwen3W8(args, layers, embed, lm_head, ones(H, device))
 
@@ -137,13 +141,14 @@ def evenly_spaced_layers(n_target_layers: int, n: int) -> list[int]:
     return [int(round(lo + i * (hi - lo) / (n - 1))) for i in range(n)]
 
 
-def _w8_k_eq_v(nq_rows: int, k_rows: int, K: int, seed: int, name: str, device, keep_mlx: bool) -> W8Weight:
+def _w8_k_eq_v(nq_rows: int, k_rows: int, K: int, seed: int, name: str, device, keep_mlx: bool,
+               bits: int = 8) -> W8Weight:
     """The [q | k | k] projection of a k_eq_v attention: the shared k_proj rows twice (the
     second copy is V's input), quantized row by row, so both copies are identical."""
-    q1, s1, b1 = W8Weight.quantize_mlx(randn((nq_rows, K), seed, name + ".q_proj", device))
-    q2, s2, b2 = W8Weight.quantize_mlx(randn((k_rows, K), seed, name + ".k_proj", device))
+    q1, s1, b1 = W8Weight.quantize_mlx(randn((nq_rows, K), seed, name + ".q_proj", device), bits)
+    q2, s2, b2 = W8Weight.quantize_mlx(randn((k_rows, K), seed, name + ".k_proj", device), bits)
     q, s, b = torch.cat([q1, q2, q2]), torch.cat([s1, s2, s2]), torch.cat([b1, b2, b2])
-    W = W8Weight.from_mlx(q, s, b)
+    W = W8Weight.from_mlx(q, s, b, bits=bits)
     if keep_mlx:
         W.mlx = (q, s, b)
     return W
@@ -152,14 +157,16 @@ def _w8_k_eq_v(nq_rows: int, k_rows: int, K: int, seed: int, name: str, device, 
 def build_dspark(target_args: TargetArgs, seed: int = 2, device="cuda", keep_mlx: bool = False,
                  num_hidden_layers: int = 1, block_size: int = 7, taps=None, markov_rank: int = 256,
                  confidence: bool = True, mask_token_id: int | None = None, family: str = "qwen3",
-                 global_head_dim: int = 512):
+                 global_head_dim: int = 512, bits: int = 4):
     """A DSpark drafter of the target's width, with its own embedding and head, a
     rank-``markov_rank`` Markov head and a confidence head, conditioned on the target layers
     ``taps`` (default: 3 spread over the target).
     family "qwen3": heads and MLP shaped like the target, Llama 2-norm layers.
     family "gemma4": the target's q heads over one global kv head of ``global_head_dim``
     (k_eq_v, v_norm, proportional RoPE over a quarter of the dims), sandwich norms with
-    layer_scalar 1, tanh-GeLU MLP, soft-cap 30, embedding scale sqrt(hidden)."""
+    layer_scalar 1, tanh-GeLU MLP, soft-cap 30, embedding scale sqrt(hidden).
+    bits: the linear layers' code width (4, the reference's drafter default, or 8); the
+    embedding and the Markov head stay 8-bit."""
     from .config import DSparkConfig
     from .model import ConfidenceHead, DSparkDrafter, MarkovHead
 
@@ -192,13 +199,13 @@ def build_dspark(target_args: TargetArgs, seed: int = 2, device="cuda", keep_mlx
     layers = []
     for l in range(num_hidden_layers):
         p = f"dspark.layers.{l}."
-        qkv = (_w8_k_eq_v(nq * hd, nkv * hd, H, seed, p + "attn", device, keep_mlx) if gemma
-               else w8(a.n_qkv, H, seed, p + "qkv", device, keep_mlx))
+        qkv = (_w8_k_eq_v(nq * hd, nkv * hd, H, seed, p + "attn", device, keep_mlx, bits) if gemma
+               else w8(a.n_qkv, H, seed, p + "qkv", device, keep_mlx, bits=bits))
         layers.append(LayerWeights(
             qkv=qkv,
-            o=w8(H, nq * hd, seed, p + "o", device, keep_mlx),
-            gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx, paired=True),
-            down=w8(H, I, seed, p + "down", device, keep_mlx),
+            o=w8(H, nq * hd, seed, p + "o", device, keep_mlx, bits=bits),
+            gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx, paired=True, bits=bits),
+            down=w8(H, I, seed, p + "down", device, keep_mlx, bits=bits),
             in_norm=ones(H, device), post_norm=ones(H, device),
             q_norm=qk_norm(hd, device), k_norm=qk_norm(hd, device),
             attn_out_norm=ones(H, device) if gemma else None, ff_out_norm=ones(H, device) if gemma else None))
@@ -212,15 +219,16 @@ def build_dspark(target_args: TargetArgs, seed: int = 2, device="cuda", keep_mlx
         K = H + (markov_rank if markov_rank > 0 else 0)
         w = randn((1, K), seed, "dspark.confidence", device)
         w = torch.cat([w, torch.zeros((15, K), device=device)])
-        q, s_, b_ = W8Weight.quantize_mlx(w)
-        cw = W8Weight.from_mlx(q, s_, b_)
+        q, s_, b_ = W8Weight.quantize_mlx(w, bits)
+        cw = W8Weight.from_mlx(q, s_, b_, bits=bits)
         if keep_mlx:
             cw.mlx = (q, s_, b_)
         conf = ConfidenceHead(cw, 0.5)
     d = DSparkDrafter(cfg, embed=w8_table(a.vocab_size, H, seed, "dspark.embed_tokens", device),
-                      fc=w8(H, len(taps) * H, seed, "dspark.fc", device, keep_mlx), hidden_norm=ones(H, device),
+                      fc=w8(H, len(taps) * H, seed, "dspark.fc", device, keep_mlx, bits=bits),
+                      hidden_norm=ones(H, device),
                       layers=layers, norm=ones(H, device),
-                      lm_head=w8(a.vocab_size, H, seed, "dspark.lm_head", device, keep_mlx),
+                      lm_head=w8(a.vocab_size, H, seed, "dspark.lm_head", device, keep_mlx, bits=bits),
                       markov=markov, confidence=conf, layer_scalars=[1.0] * num_hidden_layers if gemma else None)
     torch.cuda.synchronize(device)
     return d, cfg
@@ -228,9 +236,10 @@ def build_dspark(target_args: TargetArgs, seed: int = 2, device="cuda", keep_mlx
 
 def build_dflash(target_args: TargetArgs, seed: int = 1, device="cuda", keep_mlx: bool = False,
                  num_hidden_layers: int = 2, block_size: int = 16, n_taps: int = 5,
-                 mask_token_id: int | None = None):
+                 mask_token_id: int | None = None, bits: int = 4):
     """A DFlash drafter shaped like the target (same width, heads and MLP), conditioned on
-    n_taps evenly spaced target layers, with a block of block_size positions."""
+    n_taps evenly spaced target layers, with a block of block_size positions; its linear
+    layers quantized to ``bits`` (4, the reference's default, or 8)."""
     from .dflash_model import DFlashConfig, DFlashDraftModel
 
     a = target_args
@@ -250,12 +259,12 @@ def build_dflash(target_args: TargetArgs, seed: int = 1, device="cuda", keep_mlx
     for l in range(num_hidden_layers):
         p = f"dflash.layers.{l}."
         layers.append(LayerWeights(
-            qkv=w8(a.n_qkv, H, seed, p + "qkv", device, keep_mlx),
-            o=w8(H, nq * hd, seed, p + "o", device, keep_mlx),
-            gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx, paired=True),
-            down=w8(H, I, seed, p + "down", device, keep_mlx),
+            qkv=w8(a.n_qkv, H, seed, p + "qkv", device, keep_mlx, bits=bits),
+            o=w8(H, nq * hd, seed, p + "o", device, keep_mlx, bits=bits),
+            gate_up=w8(2 * I, H, seed, p + "gate_up", device, keep_mlx, paired=True, bits=bits),
+            down=w8(H, I, seed, p + "down", device, keep_mlx, bits=bits),
             in_norm=ones(H, device), post_norm=ones(H, device),
             q_norm=qk_norm(hd, device), k_norm=qk_norm(hd, device)))
-    fc = w8(H, n_taps * H, seed, "dflash.fc", device, keep_mlx)
+    fc = w8(H, n_taps * H, seed, "dflash.fc", device, keep_mlx, bits=bits)
     torch.cuda.synchronize(device)
     return DFlashDraftModel(cfg, fc, ones(H, device), layers, ones(H, device)), cfg

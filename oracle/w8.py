@@ -1,4 +1,4 @@
-"""W8 affine group-64 quantization, dequantization and GEMM (numpy, CPU).
+"""Affine group-64 quantization (8- and 4-bit codes), dequantization and GEMM (numpy, CPU).
 
 TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 
@@ -34,14 +34,16 @@ def bits_to_f32(h: np.ndarray) -> np.ndarray:
     return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
-def quantize(w: np.ndarray):
-    """w [N, K] float32 -> (q uint8 [N, K], scale bf16-bits [N, K/64], bias bf16-bits [N, K/64])."""
+def quantize(w: np.ndarray, bits: int = 8):
+    """w [N, K] float32 -> (q uint8 [N, K], scale bf16-bits [N, K/64], bias bf16-bits [N, K/64]);
+    codes 0 .. 2^bits - 1 (bits 8 or 4), s = (max - min) / (2^bits - 1)."""
+    levels = np.float32((1 << bits) - 1)
     w = np.ascontiguousarray(w, dtype=np.float32)
     N, K = w.shape
     g = w.reshape(N, K // 64, 64)
     lo = g.min(axis=2)
     hi = g.max(axis=2)
-    s = (hi - lo) / np.float32(255.0)
+    s = (hi - lo) / levels
     s16 = bf16_bits(s)
     sf = bits_to_f32(s16)
     bad = ~(sf > 0)
@@ -50,7 +52,7 @@ def quantize(w: np.ndarray):
     b16 = bf16_bits(lo)
     bf = bits_to_f32(b16)
     t = np.rint((g - bf[..., None]) / sf[..., None])
-    q = np.clip(t, 0, 255).astype(np.uint8).reshape(N, K)
+    q = np.clip(t, 0, levels).astype(np.uint8).reshape(N, K)
     return q, s16, b16
 
 

@@ -38,6 +38,8 @@ def test_size_queries_without_gpu():
     assert _hip.lib.dsk_act_pack_bytes(0, 64) == 0 and _hip.lib.dsk_act_pack_bytes(4, 96) == 0
     assert 1 <= _hip.lib.dsk_w8_gemm_splits(16, 4096, 4096) <= 16
     assert _hip.lib.dsk_w8_gemm_splits(16, 4096, 4000) == 0
+    assert 1 <= _hip.lib.dsk_w4_gemm_splits(16, 4096, 4096) <= 16
+    assert _hip.lib.dsk_w4_gemm_splits(65, 4096, 4096) == 0
     assert _hip.lib.dsk_accept_ws_bytes(4, 17, 151936) > 4 * 17 * 2 * 151936 * 4
 
 

@@ -41,11 +41,13 @@ def test_config_rejections(bad, what):
         checkpoint.target_args_from_config(cfg)
 
 
-@pytest.mark.parametrize("q", [{"bits": 4, "group_size": 64}, {"bits": 8, "group_size": 32}])
+@pytest.mark.parametrize("q", [{"bits": 3, "group_size": 64}, {"bits": 8, "group_size": 32},
+                               {"bits": 6, "group_size": 64}])
 def test_quantization_rejections(q):
     from mlx_dspark import checkpoint
-    with pytest.raises(ValueError, match="W8 group 64"):
+    with pytest.raises(ValueError, match="8- or 4-bit codes with group 64"):
         checkpoint._quantization(dict(QWEN3_8B_CONFIG, quantization=q))
+    assert checkpoint._quantization(dict(QWEN3_8B_CONFIG, quantization={"bits": 4, "group_size": 64})) == (4, 64)
 
 
 def test_checkpoint_dir_detection(tmp_path):
@@ -70,16 +72,17 @@ def _logits(model, prompt, block):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", ["tiny", "tiny-tied"])
-def test_mlx_checkpoint_round_trip_is_bit_exact(dev, tmp_path, name):
+@pytest.mark.parametrize("name,bits", [("tiny", 8), ("tiny-tied", 8), ("tiny", 4), ("tiny-tied", 4)])
+def test_mlx_checkpoint_round_trip_is_bit_exact(dev, tmp_path, name, bits):
     from mlx_dspark import checkpoint, synthetic
     from mlx_dspark.load import load_target
-    print(f"checkpoint round trip {name}", flush=True)
-    model = synthetic.build_target(name, seed=11, keep_mlx=True)
+    print(f"checkpoint round trip {name} {bits}-bit", flush=True)
+    model = synthetic.build_target(name, seed=11, keep_mlx=True, bits=bits)
     checkpoint.save_qwen3_w8(model, tmp_path)
     target, tok = load_target(str(tmp_path))
     loaded = target.model
     assert loaded.args.num_hidden_layers == model.args.num_hidden_layers
+    assert loaded.layers[0].qkv.bits == bits and loaded.lm_head.bits == bits
     assert loaded.args.tie_word_embeddings == model.args.tie_word_embeddings
     for La, Lb in zip(model.layers, loaded.layers):
         for f in ("qkv", "o", "gate_up", "down"):

@@ -125,7 +125,8 @@ def test_act_pack_sandwich_norm(dev, M, K, S):
 @pytest.mark.parametrize("M,N,K", [(1, 64, 256), (9, 256, 1024), (16, 6144, 4096), (17, 512, 4096),
                                    (36, 4096, 1024), (64, 128, 3072), (16, 192, 4096), (16, 4096, 12288),
                                    (9, 151936 // 8, 1024), (16, 1024, 3072), (3, 2048, 256), (64, 4096, 4096),
-                                   (16, 151936, 4096), (16, 4096, 20480)])
+                                   (16, 151936, 4096), (16, 4096, 20480), (16, 2560, 9728), (16, 512, 2304),
+                                   (4, 1024, 16640)])
 def test_gemm_matches_oracle(dev, M, N, K):
     from mlx_dspark.ops import DSK_EPI_PARTIAL, W8Weight, pack, w8_gemm
     print(f"gemm M={M} N={N} K={K}", flush=True)
@@ -211,3 +212,98 @@ def test_embed_gather(dev):
     deq = O.dequantize(*_mlx_np(q, s, b))
     ref = O.bf16_round(O.bf16_round(deq[ids.cpu().numpy()].astype(np.float32)) * 2.0)
     assert np.array_equal(out.float().cpu().numpy(), ref)
+
+
+# ---------------------------------------------------------------------------- 4-bit codes
+def test_w4_quantize_bitexact(dev):
+    from mlx_dspark.ops import W8Weight
+    g = torch.Generator().manual_seed(40)
+    w = torch.randn(96, 512, generator=g) * 0.02
+    w[5, 0:64] = -0.5                                     # constant group
+    q, s, b = W8Weight.quantize_mlx(w.to(dev), bits=4)
+    qo, so, bo = O.quantize(w.numpy(), bits=4)
+    assert int(q.max()) <= 15
+    assert np.array_equal(q.cpu().numpy(), qo)
+    assert np.array_equal(s.view(torch.int16).cpu().numpy().view(np.uint16), so)
+    assert np.array_equal(b.view(torch.int16).cpu().numpy().view(np.uint16), bo)
+    # round trip within half a step (closed form)
+    deq = O.dequantize(qo, so, bo)
+    step = O.bits_to_f32(so).astype(np.float64)
+    err = np.abs(deq - w.numpy()).reshape(96, 8, 64).max(axis=2)
+    assert np.all(err <= step * 0.5 + np.abs(O.bits_to_f32(bo)) * 2 ** -8 + 1e-7)
+
+
+def test_w4_repack_layout(dev):
+    """wt4[t][g][lane][8 B]: byte j of a lane = codes of columns 2j (low nibble) and 2j+1 of
+    its 16-column chunk, plain and paired; sb as for 8-bit."""
+    from mlx_dspark.ops import W8Weight
+    N, K = 64, 256
+    g = torch.Generator().manual_seed(41)
+    q, s, b = W8Weight.quantize_mlx((torch.randn(N, K, generator=g) * 0.02).to(dev), bits=4)
+    qn, sn, bn = _mlx_np(q, s, b)
+    for paired in (False, True):
+        W = W8Weight.from_mlx(q, s, b, paired, bits=4)
+        assert W.wt.numel() == N * K // 2 and W.nbytes == N * K // 2 + N * K // 64 * 4
+        wt = W.wt.cpu().numpy().reshape(N // 16, K // 64, 64, 8)
+        sb = W.sb.cpu().numpy().view(np.uint32).reshape(N // 16, K // 64, 16)
+        for t in range(N // 16):
+            for r in range(16):
+                n = (t % 2) * (N // 2) + (t // 2) * 16 + r if paired else 16 * t + r
+                for gg in range(K // 64):
+                    for c in range(4):
+                        codes = qn[n, 64 * gg + 16 * c: 64 * gg + 16 * c + 16]
+                        assert np.array_equal(wt[t, gg, 16 * c + r], codes[0::2] | (codes[1::2] << 4))
+                    assert sb[t, gg, r] == (int(sn[n, gg]) | (int(bn[n, gg]) << 16))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 256), (9, 256, 1024), (16, 6144, 4096), (17, 512, 4096),
+                                   (64, 128, 3072), (16, 4096, 12288), (16, 151936 // 8, 1024), (16, 24576, 4096),
+                                   (16, 2560, 9728), (16, 512, 2304), (16, 151936, 4096)])
+def test_w4_gemm_matches_oracle(dev, M, N, K):
+    from mlx_dspark.ops import DSK_EPI_PARTIAL, W8Weight, pack, w8_gemm
+    print(f"w4 gemm M={M} N={N} K={K}", flush=True)
+    g = torch.Generator().manual_seed(M * 11 + N + K)
+    w = torch.randn(N, K, generator=g) * 0.02
+    x = (torch.randn(M, K, generator=g) * 3.0).to(torch.bfloat16)
+    q, s, b = W8Weight.quantize_mlx(w.to(dev), bits=4)
+    W = W8Weight.from_mlx(q, s, b, bits=4)
+    xp = pack(x.to(dev))
+    y = w8_gemm(xp, W, out_dtype=torch.float32)
+    yp = w8_gemm(xp, W, epi=DSK_EPI_PARTIAL)
+    torch.cuda.synchronize()
+    ref = O.gemm(_bf16_vals(x), *_mlx_np(q, s, b))
+    scale = np.sqrt((ref ** 2).mean())
+    err = np.abs(y.cpu().numpy() - ref).max() / scale
+    assert err < 2e-4, err
+    errp = np.abs(yp.sum(0).cpu().numpy() - ref).max() / scale
+    assert errp < 2e-4, errp
+    # a row view of the 4-bit layout multiplies like the full weight's rows
+    if N >= 64 and N % 32 == 0:
+        sub = W.rows(16, 48)
+        ys = w8_gemm(xp, sub, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert torch.allclose(ys, y[:, 16:48], rtol=0, atol=float(scale) * 1e-5)
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+def test_w4_gated_epilogue(dev, act):
+    from mlx_dspark.ops import DSK_EPI_GEGLU, DSK_EPI_SWIGLU, W8Weight, pack, w8_gemm
+    M, I, K = 7, 1024, 2048
+    g = torch.Generator().manual_seed(len(act))
+    wg = torch.randn(I, K, generator=g) * 0.03
+    wu = torch.randn(I, K, generator=g) * 0.03
+    x = (torch.randn(M, K, generator=g) * 2.0).to(torch.bfloat16)
+    q, s, b = W8Weight.quantize_mlx(torch.cat([wg, wu]).to(dev), bits=4)
+    W = W8Weight.from_mlx(q, s, b, paired=True, bits=4)
+    out = w8_gemm(pack(x.to(dev)), W, epi=DSK_EPI_SWIGLU if act == "silu" else DSK_EPI_GEGLU)
+    torch.cuda.synchronize()
+    gu = O.gemm(_bf16_vals(x), *_mlx_np(q, s, b))
+    gt = torch.from_numpy(gu[:, :I]).float().to(torch.bfloat16).float()
+    ut = torch.from_numpy(gu[:, I:]).float().to(torch.bfloat16).float()
+    if act == "silu":
+        a = (gt * torch.sigmoid(gt)).to(torch.bfloat16).float()
+    else:
+        a = (0.5 * gt * (1 + torch.tanh(0.7978845608028654 * (gt + 0.044715 * gt ** 3)))).to(torch.bfloat16).float()
+    ref = (a * ut).to(torch.bfloat16).float()
+    got = out.unpack().float().cpu()
+    assert (got - ref).abs().max() <= 2 ** -6 * ref.abs().max()
