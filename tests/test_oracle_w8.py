@@ -1,19 +1,35 @@
 """CPU checks for the W8 oracle: round-trip bound, brute-force GEMM, degenerate groups."""
 
 import numpy as np
+import pytest
 
 from oracle import w8
 
 
-def test_quantize_roundtrip_within_half_step():
-    rng = np.random.default_rng(0)
+@pytest.mark.parametrize("bits", [8, 4])
+def test_quantize_roundtrip_within_half_step(bits):
+    rng = np.random.default_rng(bits)
     w = (rng.standard_normal((32, 256)) * 0.02).astype(np.float32)
-    q, s, b = w8.quantize(w)
+    q, s, b = w8.quantize(w, bits)
+    levels = (1 << bits) - 1
+    assert q.max() <= levels
     deq = w8.dequantize(q, s, b)
     step = w8.bits_to_f32(s).astype(np.float64)
     err = np.abs(deq - w).reshape(32, 4, 64).max(axis=2)
     # half a step, plus the bf16 rounding of scale and bias (relative 2^-8 of the range)
-    assert np.all(err <= step * 0.5 + step * 255 * 2**-8 + np.abs(w8.bits_to_f32(b)) * 2**-8 + 1e-9)
+    assert np.all(err <= step * 0.5 + step * levels * 2**-8 + np.abs(w8.bits_to_f32(b)) * 2**-8 + 1e-9)
+    # each group's minimum maps to code 0 and its maximum to the top code (up to bf16 rounding)
+    g = q.reshape(32, 4, 64)
+    assert np.all(g.min(axis=2) == 0) and np.all(g.max(axis=2) >= levels - 1)
+
+
+def test_four_bit_codes_on_an_exact_grid():
+    """Weights on a 16-level grid with a bf16-exact step come back exactly at 4 bits."""
+    codes = np.arange(64) % 16
+    w = (0.25 + 0.125 * codes).astype(np.float32)[None, :]
+    q, s, b = w8.quantize(w, 4)
+    assert np.array_equal(q[0], codes) and w8.bits_to_f32(s)[0, 0] == 0.125 and w8.bits_to_f32(b)[0, 0] == 0.25
+    assert np.array_equal(w8.dequantize(q, s, b), w)
 
 
 def test_constant_group_uses_unit_scale():
