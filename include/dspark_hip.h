@@ -274,6 +274,15 @@ int dsk_sample_rows(const float* logits, int64_t V, int R, float temperature, fl
                     int top_k, int mul_inv_t, uint64_t seed, uint32_t offset, int row0,
                     int32_t* token_out, float* probs_out, dsk_stream_t stream);
 
+/* Greedy pick per row, each row split over 64 workgroups: token_out[r] = argmax_v logits[r][v]
+ * (lowest index on ties, 0 for a row of -inf / NaN). Replaces mx.argmax(head, axis=-1), the
+ * DFlash greedy draft (src/mlx_dspark/generate.py:557), and _pick at temperature 0
+ * (generate.py:135-141). logits [R, ldl] f32 or bf16 (dtype), R <= 1024; workspace of
+ * dsk_argmax_ws_bytes(R) (slice maxima; two kernels, no counters). */
+size_t dsk_argmax_ws_bytes(int R);
+int dsk_argmax_rows(const void* logits, int dtype, int64_t ldl, int64_t V, int R, int32_t* token_out,
+                    void* workspace, size_t ws_bytes, dsk_stream_t stream);
+
 /* Device-side length update: lens[b] += (n ? n[b] : 0) + add. Advances a drafter context
  * or KV length by the accepted count without a host round trip (the reference does this
  * on the host: n_cached += n + 1, src/mlx_dspark/generate.py:938; ctx append of the

@@ -323,7 +323,7 @@ struct AcceptWs {
   float* scratch;   // [B*(L+1)][2][V]
 };
 
-constexpr int kGreedySlices = 16;
+constexpr int kGreedySlices = 64;  // slices per row: one per lane of the merging wave
 constexpr size_t kAcceptCounterBytes = 4096;
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -354,29 +354,51 @@ __host__ __device__ inline size_t accept_ws_total(int B, int W, int64_t V) {
 }
 
 // ----------------------------------------------------------------------------- greedy
-template <int BF16>
-__global__ __launch_bounds__(256) void accept_greedy_kernel(const void* __restrict__ logits, int64_t ldl, int B,
-                                                            int W, int64_t V, const int32_t* __restrict__ draft,
-                                                            int32_t* __restrict__ tt, int32_t* __restrict__ n_out,
-                                                            int32_t* __restrict__ token_out,
-                                                            int32_t* __restrict__ seq_lens, AcceptWs ws) {
-  const int S = kGreedySlices;
-  const int slice = blockIdx.x % S;
-  const int row = blockIdx.x / S;  // b*W + i
-  const int b = row / W;
-  const int64_t per = (V + S - 1) / S;
-  const int64_t lo = slice * per, hi = min(V, lo + per);
-  float best = -__builtin_inff();
-  int64_t bi = V;
+// Running argmax (lowest index on ties; NaN never wins) of this thread's share of row[lo, hi),
+// 256 threads. VEC: the row is 16-byte aligned and lo a multiple of 8, so whole 16-byte chunks
+// (4 f32 / 8 bf16) are read with four loads in flight per thread; the scalar loop takes the tail.
+template <int BF16, bool VEC>
+__device__ inline void span_argmax(const void* __restrict__ row, int64_t lo, int64_t hi, float& best, int64_t& bi) {
+  if constexpr (VEC) {
+    constexpr int E = BF16 ? 8 : 4;
+    constexpr int UN = 4;
+    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(row) + lo * (BF16 ? 2 : 4));
+    const int64_t nv = hi > lo ? (hi - lo) / E : 0;
+    for (int64_t c0 = threadIdx.x; c0 < nv; c0 += 256 * UN) {
+      u32x4 v[UN];
+#pragma unroll
+      for (int u = 0; u < UN; ++u)
+        if (c0 + u * 256 < nv) v[u] = __builtin_nontemporal_load(p + c0 + u * 256);
+#pragma unroll
+      for (int u = 0; u < UN; ++u) {
+        const int64_t c = c0 + u * 256;
+        if (c < nv) {
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            const uint32_t w = v[u][BF16 ? e / 2 : e];
+            const float x = __uint_as_float(BF16 ? ((e & 1) ? (w & 0xffff0000u) : (w << 16)) : w);
+            const int64_t j = lo + c * E + e;
+            if (x > best || (x == best && j < bi)) {
+              best = x;
+              bi = j;
+            }
+          }
+        }
+      }
+    }
+    lo += nv * E;
+  }
   for (int64_t j = lo + threadIdx.x; j < hi; j += 256) {
-    float v = BF16 ? bf16_to_f32(reinterpret_cast<const uint16_t*>(logits)[row * ldl + j])
-                   : reinterpret_cast<const float*>(logits)[row * ldl + j];
-    if (v > best || (v == best && j < bi)) {
-      best = v;
+    const float x = BF16 ? bf16_to_f32(reinterpret_cast<const uint16_t*>(row)[j]) : reinterpret_cast<const float*>(row)[j];
+    if (x > best || (x == best && j < bi)) {
+      best = x;
       bi = j;
     }
   }
-  // block argmax, lowest index on ties
+}
+
+// wave-wide argmax of (best, bi), lowest index on ties; every lane ends with the result
+__device__ inline void wave_argmax(float& best, int64_t& bi) {
   for (int o = 32; o > 0; o >>= 1) {
     float ov = __shfl_xor(best, o, 64);
     int64_t oi = (int64_t)__shfl_xor((int)bi, o, 64);
@@ -385,9 +407,29 @@ __global__ __launch_bounds__(256) void accept_greedy_kernel(const void* __restri
       bi = oi;
     }
   }
+}
+
+// slice length: ceil(V / S) rounded up to 8 elements, so every slice starts 16-byte aligned
+__host__ __device__ inline int64_t slice_len(int64_t V) { return ((V + kGreedySlices - 1) / kGreedySlices + 7) & ~(int64_t)7; }
+
+// Pass 1 of a greedy pick: block (row, slice) writes the argmax of logits[row][slice range]
+// (lowest index on ties; index V when the range is empty or all NaN) to partial slot
+// row * kGreedySlices + slice. The merge runs as the next kernel: no fences or atomics.
+template <int BF16, bool VEC>
+__global__ __launch_bounds__(256) void slice_argmax_kernel(const void* __restrict__ logits, int64_t ldl, int64_t V,
+                                                           float* __restrict__ gval, int* __restrict__ gidx) {
+  const int S = kGreedySlices;
+  const int slice = blockIdx.x % S;
+  const int row = blockIdx.x / S;
+  const int64_t per = slice_len(V);
+  const int64_t lo = min(V, slice * per), hi = min(V, lo + per);
+  float best = -__builtin_inff();
+  int64_t bi = V;
+  span_argmax<BF16, VEC>(reinterpret_cast<const uint8_t*>(logits) + (int64_t)row * ldl * (BF16 ? 2 : 4), lo, hi,
+                         best, bi);
+  wave_argmax(best, bi);
   __shared__ float sv[4];
   __shared__ int si[4];
-  __shared__ int last;
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
     sv[w] = best;
@@ -402,32 +444,36 @@ __global__ __launch_bounds__(256) void accept_greedy_kernel(const void* __restri
         bv = sv[i];
         bidx = si[i];
       }
-    ws.gval[blockIdx.x] = bv;
-    ws.gidx[blockIdx.x] = bidx;
-    __threadfence();
-    int prev = atomicAdd(&ws.cnt[b], 1);
-    last = (prev == W * S - 1);
+    gval[blockIdx.x] = bv;
+    gidx[blockIdx.x] = bidx;
   }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  // the last block of batch row b: per-position argmax over slices, then the accept length
+}
+
+// The calling wave's merge of row r's kGreedySlices (= 64) partials, a lane per slice; 0 for a
+// row of -inf / NaN.
+__device__ inline int merge_row_argmax(const float* gval, const int* gidx, int r, int64_t V) {
+  const int lane = threadIdx.x & 63;
+  float bv = gval[r * kGreedySlices + lane];
+  int64_t bidx = gidx[r * kGreedySlices + lane];
+  wave_argmax(bv, bidx);
+  return bidx >= V ? 0 : (int)bidx;
+}
+
+// Pass 2 of the greedy acceptance, one block per batch row b: per-position argmax tt (a wave
+// per position), then the accept length n = matching draft prefix, the next token tt[n], and
+// the rollback seq_lens[b] += n + 1.
+__global__ __launch_bounds__(256) void accept_greedy_finish_kernel(int W, int64_t V, const int32_t* __restrict__ draft,
+                                                                   int32_t* __restrict__ tt, int32_t* __restrict__ n_out,
+                                                                   int32_t* __restrict__ token_out,
+                                                                   int32_t* __restrict__ seq_lens, AcceptWs ws) {
+  const int b = blockIdx.x;
   __shared__ int tts[256];
-  for (int i = threadIdx.x; i < W; i += 256) {
-    float bv = -__builtin_inff();
-    int bidx = 0x7fffffff;
-    for (int s = 0; s < S; ++s) {
-      const int k = (b * W + i) * S + s;
-      float v = __builtin_nontemporal_load(&ws.gval[k]);
-      int id = __builtin_nontemporal_load(&ws.gidx[k]);
-      if (v > bv || (v == bv && id < bidx)) {
-        bv = v;
-        bidx = id;
-      }
+  for (int i = threadIdx.x >> 6; i < W; i += 4) {
+    const int id = merge_row_argmax(ws.gval, ws.gidx, b * W + i, V);
+    if ((threadIdx.x & 63) == 0) {
+      tts[i] = id;
+      if (tt) tt[b * W + i] = id;
     }
-    if (bidx >= V) bidx = 0;  // all -inf / NaN row
-    if (i < 256) tts[i] = bidx;
-    if (tt) tt[b * W + i] = bidx;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -436,8 +482,14 @@ __global__ __launch_bounds__(256) void accept_greedy_kernel(const void* __restri
     n_out[b] = n;
     token_out[b] = tts[n];
     if (seq_lens) seq_lens[b] += n + 1;
-    ws.cnt[b] = 0;
   }
+}
+
+// Pass 2 of a row-wise greedy pick: token_out[r] = merged argmax of row r (one wave per row).
+__global__ __launch_bounds__(64) void argmax_merge_kernel(int64_t V, const float* __restrict__ gval,
+                                                          const int* __restrict__ gidx, int32_t* __restrict__ token_out) {
+  const int id = merge_row_argmax(gval, gidx, blockIdx.x, V);
+  if (threadIdx.x == 0) token_out[blockIdx.x] = id;
 }
 
 // ----------------------------------------------------------------------------- sampled
@@ -593,6 +645,22 @@ __global__ __launch_bounds__(kNT) void sample_rows_kernel(const float* __restric
 
 using namespace dsk;
 
+// Pass 1 over `rows` rows of logits into ws.gval / ws.gidx; 16-byte chunk loads when every row
+// starts 16-byte aligned.
+static void launch_slice_argmax(const void* logits, int dtype, int64_t ldl, int64_t V, int rows, const AcceptWs& ws,
+                                hipStream_t st) {
+  const int64_t esz = dtype == DSK_BF16 ? 2 : 4;
+  const bool vec = ((uintptr_t)logits & 15) == 0 && (ldl * esz) % 16 == 0;
+  const dim3 grid((unsigned)(rows * kGreedySlices)), blk(256);
+  if (dtype == DSK_BF16) {
+    if (vec) hipLaunchKernelGGL((slice_argmax_kernel<1, true>), grid, blk, 0, st, logits, ldl, V, ws.gval, ws.gidx);
+    else hipLaunchKernelGGL((slice_argmax_kernel<1, false>), grid, blk, 0, st, logits, ldl, V, ws.gval, ws.gidx);
+  } else {
+    if (vec) hipLaunchKernelGGL((slice_argmax_kernel<0, true>), grid, blk, 0, st, logits, ldl, V, ws.gval, ws.gidx);
+    else hipLaunchKernelGGL((slice_argmax_kernel<0, false>), grid, blk, 0, st, logits, ldl, V, ws.gval, ws.gidx);
+  }
+}
+
 extern "C" size_t dsk_accept_ws_bytes(int B, int W, int64_t V) {
   if (B <= 0 || W <= 0 || V <= 0) return 0;
   return accept_ws_total(B, W, V);
@@ -620,14 +688,33 @@ extern "C" int dsk_accept_greedy(const void* logits, int dtype, int64_t ldl, int
   DSK_REQUIRE(ws_bytes >= accept_ws_total(B, W, V) - (size_t)B * W * 2 * V * 4,
               "dsk_accept_greedy: workspace too small");
   AcceptWs ws = accept_ws(workspace, B, W, V);
-  dim3 grid((unsigned)(B * W * kGreedySlices));
-  if (dtype == DSK_BF16)
-    hipLaunchKernelGGL(accept_greedy_kernel<1>, grid, dim3(256), 0, as_stream(stream), logits, ldl, B, W, V, draft,
-                       tt, n_out, token_out, seq_lens, ws);
-  else
-    hipLaunchKernelGGL(accept_greedy_kernel<0>, grid, dim3(256), 0, as_stream(stream), logits, ldl, B, W, V, draft,
-                       tt, n_out, token_out, seq_lens, ws);
+  const hipStream_t st = as_stream(stream);
+  launch_slice_argmax(logits, dtype, ldl, V, B * W, ws, st);
+  hipLaunchKernelGGL(accept_greedy_finish_kernel, dim3((unsigned)B), dim3(256), 0, st, W, V, draft, tt, n_out,
+                     token_out, seq_lens, ws);
   DSK_LAUNCH_CHECK("dsk_accept_greedy");
+  return DSK_OK;
+}
+
+extern "C" size_t dsk_argmax_ws_bytes(int R) {
+  if (R <= 0 || R > 1024) return 0;
+  return kAcceptCounterBytes + 2 * align256((size_t)R * kGreedySlices * 4);
+}
+
+extern "C" int dsk_argmax_rows(const void* logits, int dtype, int64_t ldl, int64_t V, int R, int32_t* token_out,
+                               void* workspace, size_t ws_bytes, dsk_stream_t stream) {
+  DSK_REQUIRE(logits && token_out && workspace, "dsk_argmax_rows: null pointer");
+  DSK_REQUIRE(R > 0 && R <= 1024 && V > 0 && V < (1ll << 31), "dsk_argmax_rows: bad shape R=%d V=%lld", R,
+              (long long)V);
+  DSK_REQUIRE(ldl >= V, "dsk_argmax_rows: ldl < V");
+  DSK_REQUIRE(dtype == DSK_F32 || dtype == DSK_BF16, "dsk_argmax_rows: dtype must be f32 or bf16");
+  DSK_REQUIRE(ws_bytes >= dsk_argmax_ws_bytes(R), "dsk_argmax_rows: workspace %zu < %zu", ws_bytes,
+              dsk_argmax_ws_bytes(R));
+  AcceptWs ws = accept_ws(workspace, R, 1, V);
+  const hipStream_t st = as_stream(stream);
+  launch_slice_argmax(logits, dtype, ldl, V, R, ws, st);
+  hipLaunchKernelGGL(argmax_merge_kernel, dim3((unsigned)R), dim3(64), 0, st, V, ws.gval, ws.gidx, token_out);
+  DSK_LAUNCH_CHECK("dsk_argmax_rows");
   return DSK_OK;
 }
 

@@ -267,16 +267,16 @@ class _DFlashRound:
         V = self.model.args.vocab_size
         H = self.model.args.hidden_size
         self.block = torch.full((1, self.bs), int(cfg.mask_token_id), dtype=torch.int32, device=dev)
-        self.pending = torch.zeros(1, dtype=torch.int32, device=dev)
-        self.draft = torch.zeros(cap, dtype=torch.int32, device=dev)
-        self.verify = torch.zeros((1, cap + 1), dtype=torch.int32, device=dev)
+        # one id buffer [n, token, draft...]: the verify ids [pending] + draft are its tail, and
+        # acceptance writes the next round's pending over this round's: no copies between steps
+        self.out = torch.zeros(2 + cap, dtype=torch.int32, device=dev)
+        self.n, self.pending, self.draft = self.out[0:1], self.out[1:2], self.out[2:]
+        self.token = self.pending
+        self.verify = self.out[1:].view(1, cap + 1)
         self.head = torch.empty((cap, V), dtype=torch.float32, device=dev)
         self.v_logits = torch.empty((cap + 1, V), dtype=torch.float32, device=dev)
         self.v_fused = torch.empty((cap + 1, len(self.tap) * H), dtype=torch.bfloat16, device=dev)
-        self.n = torch.zeros(1, dtype=torch.int32, device=dev)
-        self.token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.tt = torch.zeros((1, cap + 1), dtype=torch.int32, device=dev)
-        self.out = torch.zeros(2 + cap, dtype=torch.int32, device=dev)   # [n, token, draft...]
         self.graph = None
         self.calls = 0
 
@@ -289,8 +289,6 @@ class _DFlashRound:
                             token_out=self.draft, probs_out=q_probs)
         else:
             ops.sample_rows(self.head, 0.0, token_out=self.draft)
-        self.verify[0, 0:1].copy_(self.pending)
-        self.verify[0, 1:].copy_(self.draft)
         self.model.forward(self.verify, self.cache, self.tap, advance=False, logits_out=self.v_logits,
                            fused_out=self.v_fused)
         if self.T > 0:
@@ -300,11 +298,7 @@ class _DFlashRound:
         else:
             ops.accept_greedy(self.v_logits.view(1, self.cap + 1, -1), self.draft.view(1, -1),
                               seq_lens=self.cache.seq_lens, tt=self.tt, n_out=self.n, token_out=self.token)
-        self.pending.copy_(self.token)
         self.drafter.ingest(self.v_fused, self.dcache, n_valid=self.n)     # commit [anchor, accepted]
-        self.out[0:1].copy_(self.n)
-        self.out[1:2].copy_(self.token)
-        self.out[2:].copy_(self.draft)
 
     def run(self, round_idx: int, use_graph: bool):
         # the first round of this width runs eagerly (it sizes the workspaces), later ones
@@ -456,16 +450,16 @@ class _DSparkRound:
         dev = self.model.device
         V, H = self.model.args.vocab_size, self.model.args.hidden_size
         self.block = torch.full((1, self.k), int(cfg.mask_token_id), dtype=torch.int32, device=dev)
-        self.pending = torch.zeros(1, dtype=torch.int32, device=dev)
+        # one id buffer [n, token, draft...] (as in _DFlashRound): verify ids = its tail
+        self.out = torch.zeros(2 + cap, dtype=torch.int32, device=dev)
+        self.n, self.pending = self.out[0:1], self.out[1:2]
+        self.draft = self.out[2:].view(1, cap)
+        self.token = self.pending
+        self.verify = self.out[1:].view(1, cap + 1)
         self.head = torch.empty((cap, drafter.lm_head.N), dtype=torch.float32, device=dev)
-        self.draft = torch.zeros((1, cap), dtype=torch.int32, device=dev)
-        self.verify = torch.zeros((1, cap + 1), dtype=torch.int32, device=dev)
         self.v_logits = torch.empty((cap + 1, V), dtype=torch.float32, device=dev)
         self.v_fused = torch.empty((cap + 1, len(self.tap) * H), dtype=torch.bfloat16, device=dev)
-        self.n = torch.zeros(1, dtype=torch.int32, device=dev)
-        self.token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.tt = torch.zeros((1, cap + 1), dtype=torch.int32, device=dev)
-        self.out = torch.zeros(2 + cap, dtype=torch.int32, device=dev)   # [n, token, draft...]
         self.graph = None
         self.calls = 0
         self.uses = 0
@@ -474,17 +468,11 @@ class _DSparkRound:
         self.block[0, 0:1].copy_(self.pending)
         self.drafter.block_logits(self.block, self.dcache, self.cap, out=self.head)
         self.drafter.sample_block(self.head.view(1, self.cap, -1), self.pending, out=self.draft)
-        self.verify[0, 0:1].copy_(self.pending)
-        self.verify[0, 1:].copy_(self.draft[0])
         self.model.forward(self.verify, self.cache, self.tap, advance=False, logits_out=self.v_logits,
                            fused_out=self.v_fused)
         ops.accept_greedy(self.v_logits.view(1, self.cap + 1, -1), self.draft, seq_lens=self.cache.seq_lens,
                           tt=self.tt, n_out=self.n, token_out=self.token)
-        self.pending.copy_(self.token)
         self.drafter.update_context(self.v_fused, 0, self.dcache, n_valid=self.n)
-        self.out[0:1].copy_(self.n)
-        self.out[1:2].copy_(self.token)
-        self.out[2:].copy_(self.draft[0])
 
     def run(self, use_graph: bool):
         if use_graph and self.graph is None and self.uses >= 1:

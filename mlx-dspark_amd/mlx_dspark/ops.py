@@ -18,7 +18,8 @@ from ._hip import (DSK_BF16, DSK_EPI_GEGLU, DSK_EPI_PARTIAL, DSK_EPI_STORE, DSK_
 
 __all__ = [
     "W8Weight", "W8Table", "Workspace", "Packed", "act_pack", "pack", "w8_gemm", "w8_embed",
-    "qkv_rope_append", "attention", "qkv_attention", "row_logprobs", "accept_greedy", "accept_sample", "sample_rows", "lens_add",
+    "qkv_rope_append", "attention", "qkv_attention", "row_logprobs", "accept_greedy", "accept_sample", "sample_rows",
+    "argmax_rows", "lens_add",
     "rope_inv_freq", "DSK_EPI_STORE", "DSK_EPI_SWIGLU", "DSK_EPI_GEGLU", "DSK_EPI_PARTIAL", "DSK_KV_BF16",
     "DSK_KV_U8",
 ]
@@ -381,6 +382,8 @@ def sample_rows(logits: torch.Tensor, temperature: float, top_p: float = 1.0, to
                 token_out=None, probs_out=None):
     """logits [R, V] f32 -> tokens [R] (argmax at temperature 0) and the truncated probs."""
     R, V = logits.shape
+    if temperature <= 0 and R <= 1024 and logits.dtype in (torch.float32, torch.bfloat16):
+        return argmax_rows(logits, token_out=token_out), probs_out
     logits = logits.contiguous().float()
     token_out = torch.empty(R, dtype=torch.int32, device=logits.device) if token_out is None else token_out
     if temperature > 0 and probs_out is None:
@@ -389,6 +392,20 @@ def sample_rows(logits: torch.Tensor, temperature: float, top_p: float = 1.0, to
          int(bool(mul_inv_t)), int(seed) & ((1 << 64) - 1), int(offset) & 0xFFFFFFFF, int(row0),
          ptr(token_out), ptr(probs_out), stream_ptr())
     return token_out, probs_out
+
+
+def argmax_rows(logits: torch.Tensor, *, token_out=None) -> torch.Tensor:
+    """logits [R, V] f32/bf16 (rows may be strided) -> argmax per row, int32 [R] (lowest index on
+    ties), each row split over 64 workgroups."""
+    R, V = logits.shape
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    token_out = torch.empty(R, dtype=torch.int32, device=logits.device) if token_out is None else token_out
+    dt = DSK_BF16 if logits.dtype == torch.bfloat16 else DSK_F32
+    buf = Workspace.get(logits.device).reserve("argmax", _hip.lib.dsk_argmax_ws_bytes(R))
+    call("dsk_argmax_rows", ptr(logits), dt, logits.stride(0), V, R, ptr(token_out), ptr(buf), buf.numel(),
+         stream_ptr())
+    return token_out
 
 
 def lens_add(lens: torch.Tensor, n: torch.Tensor | None, add: int) -> None:

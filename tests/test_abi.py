@@ -40,6 +40,8 @@ def test_size_queries_without_gpu():
     assert _hip.lib.dsk_w8_gemm_splits(16, 4096, 4000) == 0
     assert 1 <= _hip.lib.dsk_w4_gemm_splits(16, 4096, 4096) <= 16
     assert _hip.lib.dsk_w4_gemm_splits(65, 4096, 4096) == 0
+    assert _hip.lib.dsk_argmax_ws_bytes(15) >= 4096 + 2 * 15 * 16 * 4
+    assert _hip.lib.dsk_argmax_ws_bytes(0) == 0 and _hip.lib.dsk_argmax_ws_bytes(1025) == 0
     assert _hip.lib.dsk_accept_ws_bytes(4, 17, 151936) > 4 * 17 * 2 * 151936 * 4
 
 

@@ -115,3 +115,28 @@ def test_sample_rows_matches_oracle(dev, T, tp, tk, mulinv):
     assert np.array_equal(tok.cpu().numpy(), ref_tok)
     if T > 0:
         assert np.array_equal(pr.cpu().numpy(), ref_p)
+
+
+@pytest.mark.parametrize("R,V,ld,dtype", [(15, 151936, 151936, "f32"), (3, 77, 77, "f32"), (4, 4099, 4099, "bf16"),
+                                         (5, 1000, 1003, "f32"), (2, 5000, 5008, "bf16"), (1, 8, 8, "f32")])
+def test_argmax_rows_first_index_on_ties(dev, R, V, ld, dtype):
+    """argmax_rows == numpy's argmax (first maximal index) on rows full of exact ties, aligned and
+    unaligned row strides, f32 and bf16, a row of -inf; twice in a row on one workspace (the
+    arrival counters must return to zero)."""
+    from mlx_dspark.ops import argmax_rows, sample_rows
+    print(f"argmax R={R} V={V} ld={ld} {dtype}", flush=True)
+    rng = np.random.default_rng(R * 7 + V)
+    for rep in range(2):
+        full = rng.integers(-3, 4, size=(R, ld)).astype(np.float32)
+        if R > 2:
+            full[1, :V] = -np.inf
+        ref = full[:, :V].argmax(axis=1).astype(np.int32)
+        t = torch.from_numpy(full)
+        if dtype == "bf16":
+            t = t.to(torch.bfloat16)
+        t = t.to(dev)[:, :V]
+        tok = argmax_rows(t)
+        tok2, _ = sample_rows(t.float() if dtype == "f32" else t, 0.0)
+        torch.cuda.synchronize()
+        assert np.array_equal(tok.cpu().numpy(), ref), rep
+        assert np.array_equal(tok2.cpu().numpy(), ref), rep
