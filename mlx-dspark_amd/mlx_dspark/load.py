@@ -120,7 +120,9 @@ def load_dflash(repo_or_path: str, *, quantize: bool = True, bits: int = 4, grou
     tkey = key[len("dflash-"):]
     if target_args is None:
         target_args = synthetic.target_args(tkey)
-    return synthetic.build_dflash(target_args, seed=seed, keep_mlx=keep_mlx, bits=bits)
+    # 5 tapped layers, or every layer of a shallower target
+    n_taps = min(5, target_args.num_hidden_layers)
+    return synthetic.build_dflash(target_args, seed=seed, keep_mlx=keep_mlx, bits=bits, n_taps=n_taps)
 
 
 def load_drafter(repo_or_path: str = DEFAULT_DRAFTER, *, quantize: bool = True, bits: int = 4,

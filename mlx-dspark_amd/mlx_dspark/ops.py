@@ -398,7 +398,7 @@ def argmax_rows(logits: torch.Tensor, *, token_out=None) -> torch.Tensor:
     """logits [R, V] f32/bf16 (rows may be strided) -> argmax per row, int32 [R] (lowest index on
     ties), each row split over 64 workgroups."""
     R, V = logits.shape
-    if logits.stride(1) != 1:
+    if logits.stride(1) != 1 or logits.stride(0) < V:
         logits = logits.contiguous()
     token_out = torch.empty(R, dtype=torch.int32, device=logits.device) if token_out is None else token_out
     dt = DSK_BF16 if logits.dtype == torch.bfloat16 else DSK_F32
