@@ -263,7 +263,11 @@ int dsk_accept_sample(const float* p_logits, const float* q_logits, int64_t V, i
                       int q_mul_inv_t, uint64_t seed, uint32_t offset, int32_t* n_out,
                       int32_t* token_out, int32_t* seq_lens, uint8_t* accept_out,
                       int32_t* sample_out, void* workspace, size_t ws_bytes,
-                      dsk_stream_t stream);
+                      const uint32_t* offset_dev, dsk_stream_t stream);
+
+/* offset_dev (dsk_accept_sample, dsk_sample_rows): when non-NULL, the Philox offset is read
+ * from this device word instead of `offset`, so a captured graph can replay a sampled round
+ * with a per-round offset the host writes before each replay. */
 
 /* Row-wise sampling of truncate(softmax(logits / T)) (temperature > 0) or argmax
  * (temperature == 0): replaces _sample_arr / _pick (src/mlx_dspark/generate.py:135-146)
@@ -272,7 +276,8 @@ int dsk_accept_sample(const float* p_logits, const float* q_logits, int64_t V, i
  * needed as q by dsk_accept_sample) may be NULL. */
 int dsk_sample_rows(const float* logits, int64_t V, int R, float temperature, float top_p,
                     int top_k, int mul_inv_t, uint64_t seed, uint32_t offset, int row0,
-                    int32_t* token_out, float* probs_out, dsk_stream_t stream);
+                    int32_t* token_out, float* probs_out, const uint32_t* offset_dev,
+                    dsk_stream_t stream);
 
 /* Greedy pick per row, each row split over 64 workgroups: token_out[r] = argmax_v logits[r][v]
  * (lowest index on ties, 0 for a row of -inf / NaN). Replaces mx.argmax(head, axis=-1), the

@@ -503,6 +503,7 @@ struct SampleArgs {
   int top_k, q_mul_inv_t;
   uint64_t seed;
   uint32_t offset;
+  const uint32_t* offset_dev;  // when non-null, the Philox offset is read here (graph replays)
   int32_t* n_out;
   int32_t* token_out;
   int32_t* seq_lens;
@@ -515,6 +516,7 @@ __global__ __launch_bounds__(kNT) void accept_sample_kernel(SampleArgs a) {
   __shared__ RowSmem sm;
   __shared__ int last;
   const int R = a.L + 1;
+  const uint32_t off = a.offset_dev ? a.offset_dev[0] : a.offset;
   const int b = blockIdx.x / R, i = blockIdx.x % R;
   const int64_t V = a.V;
   float* ps = a.ws.scratch + (size_t)blockIdx.x * 2 * V;
@@ -536,7 +538,7 @@ __global__ __launch_bounds__(kNT) void accept_sample_kernel(SampleArgs a) {
     const bool dvalid = d >= 0 && (int64_t)d < V;
     const float pd = dvalid ? final_prob(pr, ps[d]) : 0.0f;
     const float qd = !dvalid ? 1.0f : (onehot ? 1.0f : final_prob(qr, qs[d]));
-    const float u = u24_to_float(philox_word(a.seed, (uint32_t)i, (uint32_t)b, 0u, a.offset));
+    const float u = u24_to_float(philox_word(a.seed, (uint32_t)i, (uint32_t)b, 0u, off));
     float ratio = pd / (qd > 1e-9f ? qd : 1e-9f);
     if (ratio > 1.0f) ratio = 1.0f;
     acc = u < ratio;
@@ -551,10 +553,10 @@ __global__ __launch_bounds__(kNT) void accept_sample_kernel(SampleArgs a) {
     const uint64_t Rs = block_sum_u64(r, sm);
     const float Rf = fx_to_float(Rs);
     const float den = Rf > 1e-9f ? Rf : 1e-9f;
-    samp = block_categorical(V, philox_word(a.seed, (uint32_t)i, (uint32_t)b, 1u, a.offset),
+    samp = block_categorical(V, philox_word(a.seed, (uint32_t)i, (uint32_t)b, 1u, off),
                              [&](int64_t j) { return resid(j) / den; }, sm);
   } else {
-    samp = block_categorical(V, philox_word(a.seed, (uint32_t)i, (uint32_t)b, 1u, a.offset),
+    samp = block_categorical(V, philox_word(a.seed, (uint32_t)i, (uint32_t)b, 1u, off),
                              [&](int64_t j) { return final_prob(pr, ps[j]); }, sm);
   }
   if (threadIdx.x == 0) {
@@ -592,10 +594,12 @@ __global__ __launch_bounds__(kNT) void accept_sample_kernel(SampleArgs a) {
 // ----------------------------------------------------------------------------- row sampling
 __global__ __launch_bounds__(kNT) void sample_rows_kernel(const float* __restrict__ logits, int64_t V, float T,
                                                           float top_p, int top_k, int mul_inv, uint64_t seed,
-                                                          uint32_t offset, int row0, int32_t* __restrict__ token_out,
+                                                          uint32_t offset, const uint32_t* __restrict__ offset_dev,
+                                                          int row0, int32_t* __restrict__ token_out,
                                                           float* __restrict__ probs) {
   __shared__ RowSmem sm;
   const int r = blockIdx.x;
+  if (offset_dev) offset = offset_dev[0];
   const float* l = logits + (int64_t)r * V;
   if (T <= 0.0f) {
     float best = -__builtin_inff();
@@ -722,7 +726,7 @@ extern "C" int dsk_accept_sample(const float* p_logits, const float* q_logits, i
                                  const int32_t* draft, float temperature, float top_p, int top_k, int q_mul_inv_t,
                                  uint64_t seed, uint32_t offset, int32_t* n_out, int32_t* token_out,
                                  int32_t* seq_lens, uint8_t* accept_out, int32_t* sample_out, void* workspace,
-                                 size_t ws_bytes, dsk_stream_t stream) {
+                                 size_t ws_bytes, const uint32_t* offset_dev, dsk_stream_t stream) {
   DSK_REQUIRE(p_logits && n_out && token_out && workspace, "dsk_accept_sample: null pointer");
   DSK_REQUIRE(L == 0 || draft, "dsk_accept_sample: draft is null");
   DSK_REQUIRE(B > 0 && B <= 1024 && L >= 0 && L < 255 && V > 0 && V < (1ll << 31),
@@ -743,6 +747,7 @@ extern "C" int dsk_accept_sample(const float* p_logits, const float* q_logits, i
   a.q_mul_inv_t = q_mul_inv_t;
   a.seed = seed;
   a.offset = offset;
+  a.offset_dev = offset_dev;
   a.n_out = n_out;
   a.token_out = token_out;
   a.seq_lens = seq_lens;
@@ -756,12 +761,12 @@ extern "C" int dsk_accept_sample(const float* p_logits, const float* q_logits, i
 
 extern "C" int dsk_sample_rows(const float* logits, int64_t V, int R, float temperature, float top_p, int top_k,
                                int mul_inv_t, uint64_t seed, uint32_t offset, int row0, int32_t* token_out,
-                               float* probs_out, dsk_stream_t stream) {
+                               float* probs_out, const uint32_t* offset_dev, dsk_stream_t stream) {
   DSK_REQUIRE(logits && token_out, "dsk_sample_rows: null pointer");
   DSK_REQUIRE(R > 0 && V > 0 && V < (1ll << 31), "dsk_sample_rows: bad shape");
   DSK_REQUIRE(temperature <= 0.0f || probs_out, "dsk_sample_rows: probs_out is required when temperature > 0");
   hipLaunchKernelGGL(sample_rows_kernel, dim3((unsigned)R), dim3(kNT), 0, as_stream(stream), logits, V, temperature,
-                     top_p, top_k, mul_inv_t, seed, offset, row0, token_out, probs_out);
+                     top_p, top_k, mul_inv_t, seed, offset, offset_dev, row0, token_out, probs_out);
   DSK_LAUNCH_CHECK("dsk_sample_rows");
   return DSK_OK;
 }

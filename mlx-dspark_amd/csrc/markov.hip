@@ -302,7 +302,7 @@ extern "C" int dsk_markov_block(const float* base, int64_t ldb, int B, int cap, 
       for (int b = 0; b < B; ++b) {
         const int rc = dsk_sample_rows(q_logits_out + ((int64_t)b * cap + s) * V, V, 1, temperature, top_p, top_k, 1,
                                        seed, offset, b * cap + s, tok_out + b * cap + s, probs + (int64_t)b * V,
-                                       stream);
+                                       nullptr, stream);
         if (rc != DSK_OK) return rc;
       }
     }

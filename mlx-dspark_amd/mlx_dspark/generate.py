@@ -277,16 +277,19 @@ class _DFlashRound:
         self.v_logits = torch.empty((cap + 1, V), dtype=torch.float32, device=dev)
         self.v_fused = torch.empty((cap + 1, len(self.tap) * H), dtype=torch.bfloat16, device=dev)
         self.tt = torch.zeros((1, cap + 1), dtype=torch.int32, device=dev)
+        # sampled rounds: the draft distribution, and the round's Philox offset as a device
+        # word (written before each call, so one captured graph serves every round)
+        self.q_probs = torch.empty((cap, V), dtype=torch.float32, device=dev) if temperature > 0 else None
+        self.rng_off = torch.zeros(1, dtype=torch.int32, device=dev)
         self.graph = None
         self.calls = 0
 
-    def body(self, round_idx: int = 0) -> None:
+    def body(self) -> None:
         self.block[0, 0:1].copy_(self.pending)
         self.drafter.block_logits(self.block, self.dcache, 1, self.cap, out=self.head)
         if self.T > 0:
-            q_probs = torch.empty_like(self.head)
-            ops.sample_rows(self.head, self.T, self.top_p, self.top_k, seed=self.seed, offset=round_idx,
-                            token_out=self.draft, probs_out=q_probs)
+            ops.sample_rows(self.head, self.T, self.top_p, self.top_k, seed=self.seed, token_out=self.draft,
+                            probs_out=self.q_probs, offset_dev=self.rng_off)
         else:
             ops.sample_rows(self.head, 0.0, token_out=self.draft)
         self.model.forward(self.verify, self.cache, self.tap, advance=False, logits_out=self.v_logits,
@@ -294,7 +297,8 @@ class _DFlashRound:
         if self.T > 0:
             ops.accept_sample(self.v_logits.view(1, self.cap + 1, -1), self.head.view(1, self.cap, -1),
                               self.draft.view(1, -1), self.T, self.top_p, self.top_k, seed=self.seed,
-                              offset=round_idx, seq_lens=self.cache.seq_lens, n_out=self.n, token_out=self.token)
+                              seq_lens=self.cache.seq_lens, n_out=self.n, token_out=self.token,
+                              offset_dev=self.rng_off)
         else:
             ops.accept_greedy(self.v_logits.view(1, self.cap + 1, -1), self.draft.view(1, -1),
                               seq_lens=self.cache.seq_lens, tt=self.tt, n_out=self.n, token_out=self.token)
@@ -303,7 +307,8 @@ class _DFlashRound:
     def run(self, round_idx: int, use_graph: bool):
         # the first round of this width runs eagerly (it sizes the workspaces), later ones
         # replay one captured graph
-        if use_graph and self.T == 0:
+        self.rng_off.fill_(round_idx & 0x7FFFFFFF)
+        if use_graph:
             if self.graph is None and self.calls >= 1:
                 self.graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(self.graph):
@@ -311,9 +316,9 @@ class _DFlashRound:
             if self.graph is not None:
                 self.graph.replay()
             else:
-                self.body(round_idx)
+                self.body()
         else:
-            self.body(round_idx)
+            self.body()
         self.calls += 1
         o = self.out.tolist()                                         # the round's one host sync
         n, token, draft = o[0], o[1], o[2:]

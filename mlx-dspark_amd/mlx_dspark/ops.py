@@ -357,7 +357,7 @@ def accept_greedy(logits: torch.Tensor, draft: torch.Tensor | None, *, seq_lens=
 def accept_sample(p_logits: torch.Tensor, q_logits: torch.Tensor | None, draft: torch.Tensor,
                   temperature: float, top_p: float = 1.0, top_k: int = 0, *, q_mul_inv_t: bool = False,
                   seed: int = 0, offset: int = 0, seq_lens=None, n_out=None, token_out=None,
-                  accept_out=None, sample_out=None):
+                  accept_out=None, sample_out=None, offset_dev=None):
     """p_logits [B, L+1, V] f32, q_logits [B, L, V] f32 or None (one-hot q), draft [B, L] int32."""
     B, R, V = p_logits.shape
     L = R - 1
@@ -373,13 +373,13 @@ def accept_sample(p_logits: torch.Tensor, q_logits: torch.Tensor | None, draft: 
     call("dsk_accept_sample", ptr(p_logits), ptr(q_logits), V, B, L, ptr(draft), float(temperature),
          float(top_p), int(top_k or 0), int(bool(q_mul_inv_t)), int(seed) & ((1 << 64) - 1),
          int(offset) & 0xFFFFFFFF, ptr(n_out), ptr(token_out), ptr(seq_lens), ptr(accept_out),
-         ptr(sample_out), ptr(buf), buf.numel(), stream_ptr())
+         ptr(sample_out), ptr(buf), buf.numel(), ptr(offset_dev), stream_ptr())
     return n_out, token_out
 
 
 def sample_rows(logits: torch.Tensor, temperature: float, top_p: float = 1.0, top_k: int = 0, *,
                 mul_inv_t: bool = False, seed: int = 0, offset: int = 0, row0: int = 0,
-                token_out=None, probs_out=None):
+                token_out=None, probs_out=None, offset_dev=None):
     """logits [R, V] f32 -> tokens [R] (argmax at temperature 0) and the truncated probs."""
     R, V = logits.shape
     if temperature <= 0 and R <= 1024 and logits.dtype in (torch.float32, torch.bfloat16):
@@ -390,7 +390,7 @@ def sample_rows(logits: torch.Tensor, temperature: float, top_p: float = 1.0, to
         probs_out = torch.empty((R, V), dtype=torch.float32, device=logits.device)
     call("dsk_sample_rows", ptr(logits), V, R, float(temperature), float(top_p), int(top_k or 0),
          int(bool(mul_inv_t)), int(seed) & ((1 << 64) - 1), int(offset) & 0xFFFFFFFF, int(row0),
-         ptr(token_out), ptr(probs_out), stream_ptr())
+         ptr(token_out), ptr(probs_out), ptr(offset_dev), stream_ptr())
     return token_out, probs_out
 
 

@@ -188,3 +188,7 @@ def test_dflash_generate_sampled_is_seeded(dev, tiny):
     c = dflash_generate(target, tok, d, **{**kw, "seed": 124})
     assert a.token_ids == b.token_ids
     assert a.token_ids != c.token_ids
+    # sampled rounds replayed from one captured graph (Philox offset read from a device word)
+    # draw exactly what the eager rounds draw
+    e = dflash_generate(target, tok, d, use_graph=False, **kw)
+    assert a.token_ids == e.token_ids and a.num_rounds >= 3
