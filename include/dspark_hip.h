@@ -49,7 +49,7 @@ int dsk_abi_version(void);
  * Replaces nn.quantize(..., bits=8, group_size=64) (src/mlx_dspark/load.py:204-206,
  * :285-286) for the weights this engine creates, and the MLX-format packed weight that
  * nn.QuantizedLinear holds (external mlx; used by the target layers reached from
- * src/mlx_dspark/target.py:107-124).
+ * src/mlx_dspark/target.py:66-67, the layer loop of _run_mlxlm).
  *
  * dsk_w8_quantize: w [N, K] (f32 or bf16, row-major) -> q [N, K] u8 (byte order identical
  *   to MLX's uint32 packing, low byte first), scales/biases [N, K/64] bf16.
@@ -83,7 +83,7 @@ int dsk_w8_repack(const uint8_t* q, const uint16_t* scales, const uint16_t* bias
  *   copy[m][k] = v                                     (copy != NULL: hidden-state tap)
  *   out = packed(norm_w ? bf16((v * rsqrt(mean_k(v^2) + eps)) * norm_w[k]) : v)
  * It replaces the residual adds of the Qwen3 layers (mlx_lm), the hidden-state capture of
- * src/mlx_dspark/target.py:120-121 and mx.fast.rms_norm (src/mlx_dspark/model.py:28,
+ * src/mlx_dspark/target.py:68-69 and mx.fast.rms_norm (src/mlx_dspark/model.py:28,
  * nn.RMSNorm at :103-106, :165-170, :233-235, dflash_model.py:96-99, and the Qwen3 input /
  * post-attention / final norms inside mlx_lm). M <= 64, K % 64 == 0, K <= 24576, row strides
  * multiples of 8, 16-byte aligned pointers; out may be NULL (h update / copy only).
@@ -103,7 +103,7 @@ int dsk_act_pack_scaled(const float* part, int nsplit, const uint16_t* part_norm
 /* ---------------------------------------------------------------------------------------
  * W8 skinny GEMM: y[M, N] = x[M, K] . deq(W)[N, K]^T
  * Replaces mx.quantized_matmul behind nn.QuantizedLinear (external mlx), reached from
- * src/mlx_dspark/target.py:115-123 (every target projection and the lm_head / tied
+ * src/mlx_dspark/target.py:66-74 (every target projection and the lm_head / tied
  * embed_tokens.as_linear), src/mlx_dspark/batch_engine.py:199-204 (batched verify) and
  * the drafter linears (src/mlx_dspark/model.py:97-101, :230-236; dflash_model.py:93-96).
  *
@@ -143,7 +143,7 @@ int dsk_w4_gemm(const uint16_t* x, const uint8_t* wt, const uint32_t* sb, int M,
                 int64_t ldr, float softcap, dsk_stream_t stream);
 
 /* W8 row gather (embedding lookup): out[i, :] = bf16(deq(table)[ids[i], :]) * scale.
- * Replaces nn.QuantizedEmbedding (mm.embed_tokens, src/mlx_dspark/target.py:112;
+ * Replaces nn.QuantizedEmbedding (mm.embed_tokens, src/mlx_dspark/target.py:63;
  * drafter.embed, src/mlx_dspark/model.py:244-245; dflash_model.py:198).
  * table in MLX layout: q [V, H] u8, scales/biases [V, H/64] bf16. */
 int dsk_w8_embed(const int32_t* ids, int n, const uint8_t* q, const uint16_t* scales,
@@ -152,7 +152,7 @@ int dsk_w8_embed(const int32_t* ids, int n, const uint8_t* q, const uint16_t* sc
 
 /* ---------------------------------------------------------------------------------------
  * Paged KV cache.
- * Replaces mlx_lm KVCache / QuantizedKVCache (src/mlx_dspark/target.py:85-97) and the
+ * Replaces mlx_lm KVCache / QuantizedKVCache (src/mlx_dspark/target.py:36-48) and the
  * per-row BatchCache (src/mlx_dspark/batch_engine.py:61-163).
  * A pool holds fixed pages of `page` tokens; page p, kv-head h, slot t:
  *   bf16: kv[p][h][t][hd] bf16
@@ -191,7 +191,7 @@ int dsk_qkv_norm_rope_append(const void* qkv, int qkv_splits, int B, int W, int 
 /* Attention of W new queries per row over the row's paged KV (already holding the W new
  * tokens at positions seq_lens[b] .. seq_lens[b]+W-1).
  * causal != 0: query i sees keys j <= seq_lens[b] + i  (mlx_lm create_attention_mask with
- *   offset, src/mlx_dspark/target.py:113; build_batch_mask, batch_engine.py:170-178).
+ *   offset, src/mlx_dspark/target.py:64; build_batch_mask, batch_engine.py:170-178).
  *   window > 0 additionally hides keys j <= seq_lens[b] + i - window (sliding layers).
  * causal == 0: every query sees all seq_lens[b] + W keys (DSpark/DFlash block attention,
  *   src/mlx_dspark/model.py:130-155, dflash_model.py:123-133).
@@ -220,7 +220,7 @@ int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, int hd, floa
  * workspace (dsk_attn_ws_bytes) as dsk_attention; W <= 64; q_norm/k_norm may be NULL and,
  * when given, are 16-byte aligned. Replaces the attention block of a decoder layer between
  * the qkv and o projections (mlx_lm Qwen3 attention reached from
- * src/mlx_dspark/target.py:107-124; DSparkAttention, src/mlx_dspark/model.py:130-155;
+ * src/mlx_dspark/target.py:66-67; DSparkAttention, src/mlx_dspark/model.py:130-155;
  * DFlash attention, src/mlx_dspark/dflash_model.py:100-133). */
 int dsk_qkv_attention(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
                       const uint16_t* q_norm, const uint16_t* k_norm, float eps,
@@ -247,6 +247,7 @@ int dsk_accept_greedy(const void* logits, int dtype, int64_t ldl, int B, int W, 
                       dsk_stream_t stream);
 size_t dsk_accept_ws_bytes(int B, int W, int64_t V);
 int dsk_accept_ws_init(void* workspace, size_t ws_bytes, dsk_stream_t stream);
+
 
 /* Speculative sampling: replaces _spec_sample_accept (src/mlx_dspark/generate.py:659-688)
  * with truncate_probs / sample_probs (src/mlx_dspark/sampling.py:18-49).

@@ -871,13 +871,7 @@ static int attn_split_keys(int hd, int) {
 }
 static int attn_nsplit(int hd, int max_ctx) { return (int)ceil_div(max_ctx, attn_split_keys(hd, max_ctx)); }
 // blocks per split of the streamed path: about 24 splits per (row, kv head), at most 8 blocks
-// (DSK_ATTN_BLOCKS overrides, for tuning)
 static int attn_blocks(int hd, int max_ctx) {
-  static const int forced = [] {
-    const char* e = getenv("DSK_ATTN_BLOCKS");
-    return e ? atoi(e) : 0;
-  }();
-  if (forced > 0) return forced;
   const int64_t blocks = ceil_div(max_ctx, attn_split_keys(hd, max_ctx));
   return (int)std::min<int64_t>(8, std::max<int64_t>(1, ceil_div(blocks, 24)));
 }

@@ -613,20 +613,6 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi, int bits = 8) {
     p.u = 4;
     p.gpb = ((G / 4 + p.sk - 1) / p.sk) * 4;
   }
-  // tuning override (DSK_GEMM_TUNE="epi,N,nt,u,waves,sk,pf": applies to that epilogue and N)
-  static const char* tune = getenv("DSK_GEMM_TUNE");
-  if (tune) {
-    int te, tn, tnt, tu, tw, tsk, tpf;
-    if (sscanf(tune, "%d,%d,%d,%d,%d,%d,%d", &te, &tn, &tnt, &tu, &tw, &tsk, &tpf) == 7 && te == epi && tn == N &&
-        MT == 1) {
-      p.nt = tnt;
-      p.u = tu;
-      p.waves = tw;
-      p.sk = tsk;
-      p.gpb = ((G / p.u + p.sk - 1) / p.sk) * p.u;
-      p.pf = tpf != 0;
-    }
-  }
   return p;
 }
 

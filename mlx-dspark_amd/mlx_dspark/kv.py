@@ -1,6 +1,6 @@
 """Paged KV cache in HBM.
 
-Replaces mlx_lm's KVCache / QuantizedKVCache (src/mlx_dspark/target.py:85-97 in the
+Replaces mlx_lm's KVCache / QuantizedKVCache (src/mlx_dspark/target.py:36-48 in the
 reference) and the per-row BatchCache (src/mlx_dspark/batch_engine.py:61-163). One pool per
 layer holds fixed pages of ``page`` tokens (layout in include/dspark_hip.h); a block table
 maps each row's logical pages to physical pages, so rows can share read-only prefix pages

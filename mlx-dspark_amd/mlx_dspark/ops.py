@@ -33,17 +33,22 @@ def _require_cuda(*ts):
 
 # ----------------------------------------------------------------------------- workspace
 class Workspace:
-    """Per-device scratch for split-K partials and arrival counters.
+    """Per-device scratch for split partials and per-slice reductions.
 
-    The kernels leave every counter at zero when they return, so one zero-fill at allocation
-    is enough and a captured graph can replay without memsets. ``reserve`` grows a region;
-    growth is only legal outside graph capture (a warm-up call sizes everything first)."""
+    ``reserve`` grows a region (outside graph capture only). A captured graph keeps the raw
+    address of every region it used, and a generation may widen a region after a narrower
+    round was captured (a cap controller picking a wider block, a lookup round): so a region
+    that is outgrown is never freed, only superseded, and every graph keeps replaying on the
+    buffer it captured. Regions grow to the next power of two, which bounds the superseded
+    bytes by the live ones. The kernels behind these regions hold no state between calls
+    (no counters that must be zero on entry), so a fresh region needs no initialisation."""
 
     _per_device: dict[int, "Workspace"] = {}
 
     def __init__(self, device: torch.device):
         self.device = device
         self.buf: dict[str, torch.Tensor] = {}
+        self.retired: list[torch.Tensor] = []
 
     @classmethod
     def get(cls, device) -> "Workspace":
@@ -61,7 +66,9 @@ class Workspace:
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError(f"workspace '{kind}' must be sized before graph capture "
                                f"(need {nbytes} bytes)")
-        nbytes = max(nbytes, 1 << 20)
+        nbytes = 1 << max(20, (int(nbytes) - 1).bit_length())
+        if t is not None:
+            self.retired.append(t)      # a captured graph may still replay on it
         t = torch.zeros(nbytes, dtype=torch.uint8, device=self.device)
         self.buf[kind] = t
         return t

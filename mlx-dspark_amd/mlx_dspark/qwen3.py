@@ -1,7 +1,7 @@
 """Qwen3-shaped W8 decoder (the speculative-decoding target) on gfx950 kernels.
 
 The reference runs the target through mlx_lm (external) and replicates its layer loop to
-tap hidden states (src/mlx_dspark/target.py:107-124). This module is the engine's own
+tap hidden states (src/mlx_dspark/target.py:58-75). This module is the engine's own
 forward over the same public Qwen3 architecture:
     h = embed(ids)
     per layer: h += o(attn(rope(q_norm(q)), rope(k_norm(k)), v))   q,k,v from RMSNorm(h)

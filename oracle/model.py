@@ -4,7 +4,7 @@ TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 
 Restates (reference paths):
   - Target._run_mlxlm: embed -> layers -> norm -> lm_head with the residual captured after
-    the tapped layers (src/mlx_dspark/target.py:107-124). The Qwen3 layer itself lives in
+    the tapped layers (src/mlx_dspark/target.py:58-75). The Qwen3 layer itself lives in
     mlx_lm (external); it follows the public Qwen3 architecture: RMSNorm -> q/k/v
     projections -> per-head q/k RMSNorm -> rotate-half RoPE (theta from config) -> GQA
     attention, causal with offset (mask grid of tests/test_batch_engine.py:87-103) ->

@@ -4,7 +4,7 @@ TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 
 Restates the quantized-linear arithmetic the reference gets from nn.quantize /
 nn.QuantizedLinear (src/mlx_dspark/load.py:204-206, :285-286; target layers reached from
-src/mlx_dspark/target.py:107-124): w = scale * q + bias per group of 64 input columns, with
+src/mlx_dspark/target.py:66-74): w = scale * q + bias per group of 64 input columns, with
 bf16 scale and bias. MLX's own quantizer rounding is external and unpinned; the engine
 documents its own rule (include/dspark_hip.h, dsk_w8_quantize) and this module restates it.
 
