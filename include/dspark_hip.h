@@ -248,6 +248,16 @@ int dsk_accept_greedy(const void* logits, int dtype, int64_t ldl, int B, int W, 
 size_t dsk_accept_ws_bytes(int B, int W, int64_t V);
 int dsk_accept_ws_init(void* workspace, size_t ws_bytes, dsk_stream_t stream);
 
+/* dsk_accept_greedy without a workspace argument and without any allocation: the slice
+ * partials live in a file-scope device array of 512 KiB (2 x 1024 rows x 64 slices x 4 B) that
+ * each GPU the library runs on holds until the process ends. No counterpart in the reference
+ * (MLX allocates inside its graph); it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops that forbid hipMalloc). Same arguments, results
+ * and limits as dsk_accept_greedy, plus B * W <= 1024 (DSK_ERANGE beyond). Every call on one
+ * GPU shares that GPU's array: calls that overlap on one GPU (concurrent streams) race. */
+int dsk_accept_greedy_static(const void* logits, int dtype, int64_t ldl, int B, int W, int64_t V,
+                             const int32_t* draft, int32_t* tt, int32_t* n_out, int32_t* token_out,
+                             int32_t* seq_lens, dsk_stream_t stream);
 
 /* Speculative sampling: replaces _spec_sample_accept (src/mlx_dspark/generate.py:659-688)
  * with truncate_probs / sample_probs (src/mlx_dspark/sampling.py:18-49).

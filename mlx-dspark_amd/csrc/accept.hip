@@ -10,6 +10,8 @@
 // Floating-point contraction is off in this file: every fma is written out.
 #pragma clang fp contract(off)
 
+#include <mutex>
+
 #include "common.h"
 
 namespace dsk {
@@ -697,6 +699,71 @@ extern "C" int dsk_accept_greedy(const void* logits, int dtype, int64_t ldl, int
   hipLaunchKernelGGL(accept_greedy_finish_kernel, dim3((unsigned)B), dim3(256), 0, st, W, V, draft, tt, n_out,
                      token_out, seq_lens, ws);
   DSK_LAUNCH_CHECK("dsk_accept_greedy");
+  return DSK_OK;
+}
+
+// ----------------------------------------------------------------------------- no-allocation greedy
+// dsk_accept_greedy_static: the greedy acceptance with its slice partials in a file-scope device
+// array instead of a caller workspace, for callers that cannot allocate. Each device holds its
+// own copy of `scratch`; its address on the current device is looked up once (the array's host
+// name is only a stand-in: a kernel given it would fault) and cached per device. Every call on a
+// device shares that device's array, so calls that overlap on one GPU race. The slice pass
+// writes every partial the merge reads, so nothing needs clearing between calls.
+constexpr int kStaticRows = 1024;
+constexpr size_t kStaticSliceBytes = (size_t)kStaticRows * kGreedySlices * 4;
+static __device__ __align__(256) uint8_t scratch[2 * kStaticSliceBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_dev[kMaxDevices];
+
+static int static_scratch(void** out, const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("%s: hipGetDevice: %s", who, hipGetErrorString(e));
+    return DSK_ELAUNCH;
+  }
+  DSK_REQUIRE(dev >= 0 && dev < kMaxDevices, "%s: device %d beyond %d", who, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("%s: hipGetSymbolAddress(scratch): %s", who, hipGetErrorString(e));
+      return DSK_ELAUNCH;
+    }
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return DSK_OK;
+}
+
+extern "C" int dsk_accept_greedy_static(const void* logits, int dtype, int64_t ldl, int B, int W, int64_t V,
+                                        const int32_t* draft, int32_t* tt, int32_t* n_out, int32_t* token_out,
+                                        int32_t* seq_lens, dsk_stream_t stream) {
+  DSK_REQUIRE(logits && n_out && token_out, "dsk_accept_greedy_static: null pointer");
+  DSK_REQUIRE(W == 1 || draft, "dsk_accept_greedy_static: draft is null");
+  DSK_REQUIRE(B > 0 && W > 0 && W <= 256 && V > 0 && V < (1ll << 31),
+              "dsk_accept_greedy_static: bad shape B=%d W=%d V=%lld", B, W, (long long)V);
+  DSK_REQUIRE(ldl >= V, "dsk_accept_greedy_static: ldl < V");
+  DSK_REQUIRE(dtype == DSK_F32 || dtype == DSK_BF16, "dsk_accept_greedy_static: dtype must be f32 or bf16");
+  if ((int64_t)B * W > kStaticRows) {
+    set_error("dsk_accept_greedy_static: B*W = %lld rows beyond the static scratch maximum of %d",
+              (long long)B * W, kStaticRows);
+    return DSK_ERANGE;
+  }
+  void* base = nullptr;
+  const int rc = static_scratch(&base, "dsk_accept_greedy_static");
+  if (rc != DSK_OK) return rc;
+  AcceptWs ws{};
+  ws.gval = reinterpret_cast<float*>(base);
+  ws.gidx = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(base) + kStaticSliceBytes);
+  const hipStream_t st = as_stream(stream);
+  launch_slice_argmax(logits, dtype, ldl, V, B * W, ws, st);
+  hipLaunchKernelGGL(accept_greedy_finish_kernel, dim3((unsigned)B), dim3(256), 0, st, W, V, draft, tt, n_out,
+                     token_out, seq_lens, ws);
+  DSK_LAUNCH_CHECK("dsk_accept_greedy_static");
   return DSK_OK;
 }
 

@@ -55,6 +55,8 @@ SIGNATURES: dict[str, tuple] = {
                                   c_void_p]),
     "dsk_accept_greedy": (c_int, [c_void_p, c_int, c_int64, c_int, c_int, c_int64, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "dsk_accept_greedy_static": (c_int, [c_void_p, c_int, c_int64, c_int, c_int, c_int64, c_void_p, c_void_p,
+                                         c_void_p, c_void_p, c_void_p, c_void_p]),
     "dsk_accept_ws_bytes": (c_size_t, [c_int, c_int, c_int64]),
     "dsk_accept_ws_init": (c_int, [c_void_p, c_size_t, c_void_p]),
     "dsk_accept_sample": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_int, c_void_p, c_float, c_float, c_int,
