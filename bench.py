@@ -99,6 +99,59 @@ def gemm_roofline(model, M: int, reps: int = 10):
     return res
 
 
+ACC_SHAPE = (4, 16, 151936)   # batch, drafts per row, vocabulary
+
+
+def acc_inputs(seed: int = 2024):
+    """The standalone acceptance workload: draft logits N(0, 3^2) [4, 16, 151936], target logits
+    = draft + N(0, 1) [4, 17, 151936] (the 17th row draws the bonus), drafts = the draft argmax."""
+    import torch
+    B, L, V = ACC_SHAPE
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, L + 1, V, generator=g) * 3.0
+    p = q + torch.randn(B, L + 1, V, generator=g)
+    q = q[:, :L].contiguous()
+    draft = q.argmax(dim=2).to(torch.int32)
+    return p, q, draft
+
+
+def acc_timing(reps: int = 50):
+    """Speculative-sampling acceptance on [4, 17, 151936] fp32 (T = 1, top-p 0.95, top-k 0,
+    Philox uniforms), inputs resident in HBM: one captured graph of the whole acceptance
+    (its kernel chain, rollback included) replayed `reps` times between HIP events on the
+    launch stream. Algorithmic bytes: one pass over the target and draft logits."""
+    import torch
+    from mlx_dspark import ops
+    p, q, draft = (t.cuda() for t in acc_inputs())
+    B = p.shape[0]
+    sl = torch.zeros(B, dtype=torch.int32, device="cuda")
+    n = torch.empty(B, dtype=torch.int32, device="cuda")
+    tok = torch.empty(B, dtype=torch.int32, device="cuda")
+    word = torch.zeros(1, dtype=torch.int32, device="cuda")
+    run = lambda: ops.accept_sample(p, q, draft, 1.0, 0.95, 0, seed=7, offset_dev=word, seq_lens=sl, n_out=n,
+                                    token_out=tok)
+    run()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    for _ in range(3):
+        g.replay()
+    stream = torch.cuda.current_stream()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s_ev.record(stream)
+    for _ in range(reps):
+        g.replay()
+    e_ev.record(stream)
+    torch.cuda.synchronize()
+    us = s_ev.elapsed_time(e_ev) * 1e3 / reps
+    nbytes = (p.numel() + q.numel()) * 4
+    return {"us": round(us, 2), "bytes": int(nbytes), "GBs": round(nbytes / us / 1e3, 1),
+            "roofline_frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4),
+            "config": "B=4, 16 drafts + bonus, V=151936 fp32, T=1, top_p=0.95, top_k=0"}
+
+
 def copy_calibration(nbytes: int = 256 << 20) -> None:
     """A plain device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters."""
     import torch
@@ -187,6 +240,8 @@ def main(argv=None) -> int:
     ap.add_argument("--verify-reps", type=int, default=50)
     ap.add_argument("--roofline-only", action="store_true",
                     help="build the target, time the W8 GEMM shapes and a 256 MiB copy only (counter runs)")
+    ap.add_argument("--acc-only", action="store_true",
+                    help="time the standalone acceptance workload [4, 17, 151936] only")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this engine has no multi-GPU path (run with --gpus 1)",
@@ -203,6 +258,9 @@ def main(argv=None) -> int:
 
     kv_bits = args.kv_bits or None
     torch.cuda.init()
+    if args.acc_only:
+        print(json.dumps({"acc": acc_timing()}), flush=True)
+        return 0
     t_build = time.time()
     model = synthetic.build_target(args.target, seed=0)
     drafter, dcfg = synthetic.build_dflash(model.args, seed=1, block_size=args.block, n_taps=5, bits=4)

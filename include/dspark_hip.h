@@ -245,6 +245,8 @@ int dsk_accept_greedy(const void* logits, int dtype, int64_t ldl, int B, int W, 
                       const int32_t* draft, int32_t* tt, int32_t* n_out, int32_t* token_out,
                       int32_t* seq_lens, void* workspace, size_t ws_bytes,
                       dsk_stream_t stream);
+/* Workspace of dsk_accept_greedy (B, W, V) and of dsk_accept_sample (B, L + 1 = W, V). No state
+ * is kept in it between calls; dsk_accept_ws_init only validates it. */
 size_t dsk_accept_ws_bytes(int B, int W, int64_t V);
 int dsk_accept_ws_init(void* workspace, size_t ws_bytes, dsk_stream_t stream);
 
@@ -262,13 +264,26 @@ int dsk_accept_greedy_static(const void* logits, int dtype, int64_t ldl, int B, 
 /* Speculative sampling: replaces _spec_sample_accept (src/mlx_dspark/generate.py:659-688)
  * with truncate_probs / sample_probs (src/mlx_dspark/sampling.py:18-49).
  * p_logits [B, L+1, V] f32 (target), q_logits [B, L, V] f32 (draft; NULL = one-hot q at
- * the drafted token, the lookup-draft case of generate.py:819-821), draft [B, L] int32.
+ * the drafted token, the lookup-draft case of generate.py:819-821), draft [B, L] int32,
+ * V <= 2^19.
  * p = truncate(softmax(p_logits / T)); q = truncate(softmax(q_logits / T)) or, when
  * q_mul_inv_t != 0, softmax(q_logits * (1/T)) (src/mlx_dspark/model.py:297, :304).
- * Uniforms come from Philox4x32-10 keyed by (seed) at counter offset `offset`.
+ * Canonical arithmetic (shared bit for bit with the CPU oracle): e_j = exp(y_j - max y) by
+ * the library's own exp, masses floor(e_j * 2^44) summed as integers, top-k keeps e_j >= the
+ * k-th largest e, top-p keeps e_j >= the largest c whose mass at or above c reaches
+ * ceil(top_p * Z), both keep e_j >= the larger threshold (the reference's top-k followed by
+ * top-p on the zeroed values); a kept element's probability is e_j / (kept mass).
+ * Position i accepts when u < min(1, p(d)/max(q(d), 1e-9)); the first rejected position n draws
+ * from the residual max(p - q, 0), or, when every draft is accepted, position L draws from p;
+ * draws are inverse CDFs over the fixed-point masses in index order.
+ * Uniforms come from Philox4x32-10 keyed by (seed) at counter offset `offset`: the accept
+ * test of (b, i) uses counter {i, b, 0, offset}, the draw at (b, i) {i, b, 1, offset}.
  * Outputs: n_out[b] accepted drafts, token_out[b] residual/bonus token, seq_lens[b] +=
  * n + 1 when non-NULL; accept_out [B, L] u8 and sample_out [B, L+1] int32 when non-NULL
- * (per-position accept flags and the token each position would emit). */
+ * (per-position accept flags and the token each position would emit; sample_out makes every
+ * position draw, otherwise only position n does).
+ * Every row is split over many workgroups; six kernels on `stream` (five without top-k /
+ * top-p), no counters kept between calls: workspace of dsk_accept_ws_bytes(B, L + 1, V). */
 int dsk_accept_sample(const float* p_logits, const float* q_logits, int64_t V, int B, int L,
                       const int32_t* draft, float temperature, float top_p, int top_k,
                       int q_mul_inv_t, uint64_t seed, uint32_t offset, int32_t* n_out,
@@ -281,14 +296,16 @@ int dsk_accept_sample(const float* p_logits, const float* q_logits, int64_t V, i
  * with a per-round offset the host writes before each replay. */
 
 /* Row-wise sampling of truncate(softmax(logits / T)) (temperature > 0) or argmax
- * (temperature == 0): replaces _sample_arr / _pick (src/mlx_dspark/generate.py:135-146)
- * and the DFlash draft sampling (generate.py:541-557). logits f32 [R, V]; uniforms use
- * Philox counter row `row0 + r`. probs_out [R, V] f32 (the truncated distribution,
- * needed as q by dsk_accept_sample) may be NULL. */
+ * (temperature == 0, at most 1024 rows): replaces _sample_arr / _pick
+ * (src/mlx_dspark/generate.py:135-146) and the DFlash draft sampling (generate.py:541-557).
+ * logits f32 [R, V], V <= 2^19; the same canonical distribution as dsk_accept_sample; the draw
+ * of row r uses Philox counter {row0 + r, 0, 2, offset}. probs_out [R, V] f32 (the truncated
+ * distribution) may be NULL. workspace: dsk_sample_ws_bytes(R, V) bytes. */
+size_t dsk_sample_ws_bytes(int R, int64_t V);
 int dsk_sample_rows(const float* logits, int64_t V, int R, float temperature, float top_p,
                     int top_k, int mul_inv_t, uint64_t seed, uint32_t offset, int row0,
                     int32_t* token_out, float* probs_out, const uint32_t* offset_dev,
-                    dsk_stream_t stream);
+                    void* workspace, size_t ws_bytes, dsk_stream_t stream);
 
 /* Greedy pick per row, each row split over 64 workgroups: token_out[r] = argmax_v logits[r][v]
  * (lowest index on ties, 0 for a row of -inf / NaN). Replaces mx.argmax(head, axis=-1), the

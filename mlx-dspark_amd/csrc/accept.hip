@@ -1,15 +1,34 @@
 // Fused acceptance on gfx950: greedy argmax-compare and speculative-sampling acceptance
 // (min(1, p/q) with residual resampling) after temperature / top-k / top-p, plus the KV
 // rollback to the accepted length. One canonical arithmetic is shared with the CPU oracle
-// so decisions, sampled indices and rollback lengths are bit-identical:
+// (oracle/accept_oracle.c) so decisions, sampled indices and rollback lengths are identical:
 //   - exp: dsk_expf (Cody-Waite reduction by ln 2 with a two-word constant, Taylor
 //     polynomial to r^7 evaluated with explicit fmaf, inputs below -86 flush to zero);
-//   - probability sums: integers of fx(p) = floor(p * 2^44) (order-independent);
+//   - a row's distribution lives on the unnormalised exponentials e_j = dsk_expf(y_j - max y)
+//     with fixed-point masses w_j = fx(e_j) = floor(e_j * 2^44) (integer sums: order-free);
+//   - top-k keeps e_j >= the k-th largest e; top-p keeps e_j >= the largest value c whose
+//     mass at or above it reaches TP = ceil(top_p * Z); both keep e_j >= max of the two
+//     thresholds (the reference's top-k followed by top-p on the zeroed values); the final
+//     probability of a kept element is e_j / float(S * 2^-44), S the kept mass;
 //   - uniforms: Philox4x32-10 word 0, u = (w >> 8) * 2^-24;
-//   - categorical draws: inverse CDF over the fixed-point masses.
+//   - categorical draws: inverse CDF over fixed-point masses, in index order.
 // Floating-point contraction is off in this file: every fma is written out.
+//
+// The sampled paths split every row over many workgroups and run as a chain of kernels with
+// no fences or last-arriver counters (each kernel boundary is the only synchronisation):
+//   1 row max per slice;
+//   2 Z and a 512-bucket histogram of e's float key (count and mass per bucket), merged per
+//     row with integer atomics (exact in any order);
+//   3 (truncation only) the threshold buckets from the merged histogram, then every element
+//     of those buckets gathered as a candidate key;
+//   4 per row (a verify position: its target and draft rows): the exact thresholds by a radix
+//     select over the candidates, the kept mass S, and the accept test of the drafted token;
+//   5 per slice: the mass of the distribution each draw uses (residual at the first rejected
+//     position, or the bonus / row distribution);
+//   6 per draw: the slice holding the uniform's mass, then the element inside it.
 #pragma clang fp contract(off)
 
+#include <algorithm>
 #include <mutex>
 
 #include "common.h"
@@ -67,14 +86,28 @@ __device__ __forceinline__ uint32_t philox_word(uint64_t seed, uint32_t c0, uint
 
 __device__ __forceinline__ float u24_to_float(uint32_t w) { return (float)(w >> 8) * 0x1p-24f; }
 
-// ----------------------------------------------------------------------------- block helpers
-constexpr int kNT = 512;  // threads per row block
-constexpr int kNW = kNT / 64;
-
-__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
-  uint32_t lo = __shfl((uint32_t)v, src, 64), hi = __shfl((uint32_t)(v >> 32), src, 64);
-  return ((uint64_t)hi << 32) | lo;
+// TP = ceil(top_p * Z) exactly: top_p = M * 2^E with an integer M < 2^24, the product an integer
+// below 2^87, the ceiling a shift of a 128-bit sum. top_p <= 0 gives 0 (an empty nucleus).
+__device__ inline uint64_t top_p_target(float top_p, uint64_t Z) {
+  if (!(top_p > 0.0f)) return 0;
+  const uint32_t bits = f32_bits(top_p);
+  const uint32_t ex = (bits >> 23) & 0xFFu;
+  uint64_t M = bits & 0x7FFFFFu;
+  int E;
+  if (ex == 0) {
+    E = -149;
+  } else {
+    M |= 0x800000u;
+    E = (int)ex - 150;
+  }
+  const unsigned __int128 P = (unsigned __int128)M * Z;
+  if (E >= 0) return (uint64_t)(P << E);
+  const int sh = -E;
+  if (sh >= 128) return P ? 1 : 0;
+  return (uint64_t)((P + (((unsigned __int128)1 << sh) - 1)) >> sh);
 }
+
+// ----------------------------------------------------------------------------- wave helpers
 __device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int d) {
   uint32_t lo = __shfl_up((uint32_t)v, d, 64), hi = __shfl_up((uint32_t)(v >> 32), d, 64);
   return ((uint64_t)hi << 32) | lo;
@@ -96,263 +129,23 @@ __device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
   return v;
 }
 
-struct RowSmem {
-  uint64_t hist[2048];
-  uint64_t wsum[kNW];
-  float wmax[kNW];
-  uint64_t bc64[4];
-  uint32_t bc32[4];
-};
-
-__device__ uint64_t block_sum_u64(uint64_t v, RowSmem& sm) {
-  v = wave_sum_u64(v);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sm.wsum[w] = v;
-  __syncthreads();
-  uint64_t t = 0;
-#pragma unroll
-  for (int i = 0; i < kNW; ++i) t += sm.wsum[i];
-  return t;
-}
-
-__device__ float block_max(float v, RowSmem& sm) {
-  v = wave_max(v);
-  const int w = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) sm.wmax[w] = v;
-  __syncthreads();
-  float t = sm.wmax[0];
-#pragma unroll
-  for (int i = 1; i < kNW; ++i) t = fmaxf(t, sm.wmax[i]);
-  return t;
-}
-
-// Radix select over the keys of p (fp32 bits of non-negative values are ordered like the
-// values). Keys below `floor_key` count as key 0 with weight 0 (they were zeroed by an
-// earlier truncation). count_mode: weight 1 per element, else weight fx(p).
-// Returns the key K with weight(> K) < target <= weight(>= K); returns 0 when the total
-// weight stays below target.
-__device__ uint32_t radix_select(const float* __restrict__ p, int64_t V, uint32_t floor_key, int count_mode,
-                                 uint64_t target, RowSmem& sm) {
-  const int shifts[3] = {21, 10, 0};
-  const int widths[3] = {11, 11, 10};
-  uint32_t prefix = 0;
-  uint64_t above = 0;
-  for (int lv = 0; lv < 3; ++lv) {
-    const int sh = shifts[lv], wd = widths[lv];
-    const int nb = 1 << wd;
-    const int hi_sh = sh + wd;
-    __syncthreads();
-    for (int i = threadIdx.x; i < 2048; i += kNT) sm.hist[i] = 0;
-    __syncthreads();
-    for (int64_t j = threadIdx.x; j < V; j += kNT) {
-      float v = p[j];
-      uint32_t key = f32_bits(v);
-      uint64_t wgt;
-      if (key < floor_key) {
-        key = 0;
-        wgt = count_mode ? 1 : 0;
-      } else {
-        wgt = count_mode ? 1 : fx(v);
-      }
-      if (lv == 0 || (hi_sh >= 32 ? true : ((key >> hi_sh) == (prefix >> hi_sh)))) {
-        if (wgt) atomicAdd((unsigned long long*)&sm.hist[(key >> sh) & (nb - 1)], (unsigned long long)wgt);
-      }
-    }
-    __syncthreads();
-    // descending scan over the nb buckets: thread t owns buckets nb-1-4t .. nb-4-4t
-    const int per = 4;
-    const int nthr = nb / per;  // 512 or 256
-    uint64_t loc[4] = {0, 0, 0, 0};
-    uint64_t tsum = 0;
-    if ((int)threadIdx.x < nthr) {
-#pragma unroll
-      for (int q = 0; q < per; ++q) {
-        loc[q] = sm.hist[nb - 1 - (int)threadIdx.x * per - q];
-        tsum += loc[q];
-      }
-    }
-    // block exclusive scan of tsum in thread order
-    uint64_t incl = wave_incl_scan_u64(tsum);
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 63) sm.wsum[w] = incl;
-    if (threadIdx.x == 0) {
-      sm.bc32[0] = 0xFFFFFFFFu;
-      sm.bc64[0] = 0;
-    }
-    __syncthreads();
-    uint64_t wbefore = 0;
-    for (int i = 0; i < w; ++i) wbefore += sm.wsum[i];
-    uint64_t run = above + wbefore + incl - tsum;
-    if ((int)threadIdx.x < nthr) {
-#pragma unroll
-      for (int q = 0; q < per; ++q) {
-        const uint64_t nrun = run + loc[q];
-        if (run < target && nrun >= target) {
-          sm.bc32[0] = (uint32_t)(nb - 1 - (int)threadIdx.x * per - q);
-          sm.bc64[0] = run;  // weight above this bucket
-        }
-        run = nrun;
-      }
-    }
-    __syncthreads();
-    const uint32_t d = sm.bc32[0];
-    if (d == 0xFFFFFFFFu) return 0;  // never reached: everything qualifies
-    above = sm.bc64[0];
-    prefix |= d << sh;
-  }
-  return prefix;
-}
-
-// Softmax with temperature and truncation for one row. Leaves p = e / Z in `scratch` and
-// returns the cut key and the renormalisation denominator: the final probability of j is
-// trunc ? (key(p_j) >= cut ? p_j / den : 0) : p_j.
-struct RowProbs {
-  uint32_t cut;
-  int trunc;
-  float den;
-};
-
-__device__ __forceinline__ float final_prob(const RowProbs& rp, float pj) {
-  if (!rp.trunc) return pj;
-  return f32_bits(pj) >= rp.cut ? pj / rp.den : 0.0f;
-}
-
-__device__ RowProbs row_probs(const float* __restrict__ logits, int64_t V, float T, int mul_inv, float top_p,
-                              int top_k, float* __restrict__ scratch, RowSmem& sm) {
-  const float inv_t = 1.0f / T;
-  float m = -__builtin_inff();
-  for (int64_t j = threadIdx.x; j < V; j += kNT) {
-    float y = mul_inv ? logits[j] * inv_t : logits[j] / T;
-    m = fmaxf(m, y);
-  }
-  m = block_max(m, sm);
-  uint64_t z = 0;
-  for (int64_t j = threadIdx.x; j < V; j += kNT) {
-    float y = mul_inv ? logits[j] * inv_t : logits[j] / T;
-    float e = dsk_expf(y - m);
-    scratch[j] = e;
-    z += fx(e);
-  }
-  const uint64_t Z = block_sum_u64(z, sm);
-  const float Zf = fx_to_float(Z);
-  for (int64_t j = threadIdx.x; j < V; j += kNT) scratch[j] = scratch[j] / Zf;
-  __syncthreads();
-
-  RowProbs rp;
-  rp.trunc = 0;
-  rp.cut = 0;
-  rp.den = 1.0f;
-  const int do_k = (top_k > 0 && (int64_t)top_k < V);
-  const int do_p = (top_p < 1.0f);
-  if (!do_k && !do_p) return rp;
-  rp.trunc = 1;
-  uint32_t kk = 0;
-  if (do_k) kk = radix_select(scratch, V, 0, 1, (uint64_t)top_k, sm);
-  uint32_t cut = kk;
-  if (do_p) {
-    const uint64_t TP = (uint64_t)floor((double)top_p * 0x1p44);
-    if (TP == 0) {
-      cut = 0xFFFFFFFFu;  // empty nucleus: every probability becomes 0
-    } else {
-      uint32_t c = radix_select(scratch, V, kk, 0, TP, sm);
-      if (c > 0) cut = c;
-    }
-  }
-  rp.cut = cut;
-  uint64_t s = 0;
-  for (int64_t j = threadIdx.x; j < V; j += kNT) {
-    float pj = scratch[j];
-    if (f32_bits(pj) >= cut) s += fx(pj);
-  }
-  const uint64_t S = block_sum_u64(s, sm);
-  const float Sf = fx_to_float(S);
-  rp.den = Sf > 1e-12f ? Sf : 1e-12f;
-  return rp;
-}
-
-// Inverse-CDF draw; weight(j) is a device lambda giving the float weight of element j.
-// Each wave owns a contiguous slice of the index range so prefix order is index order.
-template <typename WF>
-__device__ int64_t block_categorical(int64_t V, uint32_t word, WF weight, RowSmem& sm) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t per_wave = ((V + kNW - 1) / kNW + 63) / 64 * 64;
-  const int64_t lo = (int64_t)w * per_wave, hi = min(V, lo + per_wave);
-  uint64_t tot = 0;
-  for (int64_t j = lo + lane; j < hi; j += 64) tot += fx(weight(j));
-  tot = wave_sum_u64(tot);
-  __syncthreads();
-  if (lane == 0) sm.wsum[w] = tot;
-  if (threadIdx.x == 0) sm.bc64[1] = (uint64_t)-1;
-  __syncthreads();
-  uint64_t W = 0, before = 0;
-#pragma unroll
-  for (int i = 0; i < kNW; ++i) {
-    if (i < w) before += sm.wsum[i];
-    W += sm.wsum[i];
-  }
-  const uint64_t u = word >> 8;
-  if (W == 0) return (int64_t)((u * (uint64_t)V) >> 24);
-  const uint64_t t = (W >> 24) * u + (((W & 0xFFFFFFull) * u) >> 24);
-  if (t >= before && t < before + sm.wsum[w]) {
-    uint64_t run = before;
-    for (int64_t j0 = lo; j0 < hi; j0 += 64) {
-      const int64_t j = j0 + lane;
-      uint64_t c = (j < hi) ? fx(weight(j)) : 0;
-      uint64_t incl = wave_incl_scan_u64(c) + run;
-      // first lane whose inclusive prefix exceeds t
-      unsigned long long hit = __ballot(j < hi && incl > t);
-      if (hit) {
-        int first = __ffsll(hit) - 1;
-        if (lane == first) sm.bc64[1] = (uint64_t)j;
-        break;
-      }
-      run = shfl_u64(incl, 63);
-    }
-  }
-  __syncthreads();
-  return (int64_t)sm.bc64[1];
-}
-
-// ----------------------------------------------------------------------------- workspace
-struct AcceptWs {
-  int* cnt;         // [B] arrival counters (zero between calls)
-  float* gval;      // [B*W*S] greedy slice maxima
-  int* gidx;        // [B*W*S]
-  int* acc;         // [B*(L+1)]
-  int* samp;        // [B*(L+1)]
-  float* scratch;   // [B*(L+1)][2][V]
-};
-
+// ----------------------------------------------------------------------------- greedy workspace
 constexpr int kGreedySlices = 64;  // slices per row: one per lane of the merging wave
-constexpr size_t kAcceptCounterBytes = 4096;
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-__host__ __device__ inline AcceptWs accept_ws(void* base, int B, int W, int64_t V) {
-  AcceptWs ws;
-  uint8_t* p = reinterpret_cast<uint8_t*>(base);
-  size_t off = 0;
-  ws.cnt = reinterpret_cast<int*>(p + off);
-  off += kAcceptCounterBytes;
-  const size_t rows = (size_t)B * W;
-  ws.gval = reinterpret_cast<float*>(p + off);
-  off += align256(rows * kGreedySlices * 4);
-  ws.gidx = reinterpret_cast<int*>(p + off);
-  off += align256(rows * kGreedySlices * 4);
-  ws.acc = reinterpret_cast<int*>(p + off);
-  off += align256(rows * 4);
-  ws.samp = reinterpret_cast<int*>(p + off);
-  off += align256(rows * 4);
-  ws.scratch = reinterpret_cast<float*>(p + off);
-  return ws;
-}
+struct GreedyWs {
+  float* gval;  // [rows * kGreedySlices] slice maxima
+  int* gidx;    // [rows * kGreedySlices] their indices
+};
 
-__host__ __device__ inline size_t accept_ws_total(int B, int W, int64_t V) {
-  const size_t rows = (size_t)B * W;
-  return kAcceptCounterBytes + 2 * align256(rows * kGreedySlices * 4) + 2 * align256(rows * 4) +
-         rows * 2 * (size_t)V * 4;
+__host__ inline size_t greedy_ws_bytes(size_t rows) { return 2 * align256(rows * kGreedySlices * 4); }
+
+__host__ inline GreedyWs greedy_ws(void* base, size_t rows) {
+  GreedyWs ws;
+  ws.gval = reinterpret_cast<float*>(base);
+  ws.gidx = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(base) + align256(rows * kGreedySlices * 4));
+  return ws;
 }
 
 // ----------------------------------------------------------------------------- greedy
@@ -467,7 +260,7 @@ __device__ inline int merge_row_argmax(const float* gval, const int* gidx, int r
 __global__ __launch_bounds__(256) void accept_greedy_finish_kernel(int W, int64_t V, const int32_t* __restrict__ draft,
                                                                    int32_t* __restrict__ tt, int32_t* __restrict__ n_out,
                                                                    int32_t* __restrict__ token_out,
-                                                                   int32_t* __restrict__ seq_lens, AcceptWs ws) {
+                                                                   int32_t* __restrict__ seq_lens, GreedyWs ws) {
   const int b = blockIdx.x;
   __shared__ int tts[256];
   for (int i = threadIdx.x >> 6; i < W; i += 4) {
@@ -494,158 +287,669 @@ __global__ __launch_bounds__(64) void argmax_merge_kernel(int64_t V, const float
   if (threadIdx.x == 0) token_out[blockIdx.x] = id;
 }
 
-// ----------------------------------------------------------------------------- sampled
-struct SampleArgs {
-  const float* p_logits;
-  const float* q_logits;
+// ============================================================================= sampled paths
+constexpr int kST = 512;              // threads per workgroup
+constexpr int kSW = kST / 64;
+constexpr int kMaxSlices = 32;        // workgroups per row
+constexpr int kEPT = 32;              // elements per thread in the gather pass: slice <= 16384
+constexpr int64_t kMaxSlice = (int64_t)kST * kEPT;
+constexpr int kL1 = 512;              // first-level buckets: key >> 21 (e <= 1 keeps it <= 508)
+constexpr int kL1Shift = 21;
+constexpr uint32_t kNone = 0xFFFFFFFFu;
+static_assert(kST == kL1, "the merged-histogram scan gives each thread one first-level bucket");
+
+struct RowInfo {        // the threshold buckets of one row (gather pass, slice 0)
+  uint32_t bk, bp;      // top-k bucket (by count), top-p bucket (by mass); kNone when inactive
+  uint32_t above_k;     // elements in buckets above bk
+  uint32_t pad;
+  uint64_t wabove_k;    // mass in buckets above bk
+  uint64_t wabove_p;    // mass in buckets above bp
+  uint64_t tp;          // ceil(top_p * Z)
+};
+
+struct RowParam {       // one row's final distribution: p'_j = key(e_j) >= thr ? e_j / sf : 0
+  float m;              // max of y over the row
+  uint32_t thr;         // 0 keeps every element, kNone keeps none
+  float sf;             // float(S * 2^-44), S the kept mass
+  uint32_t pad;
+};
+
+struct SampArgs {
+  // rows: p rows [0, Rp), then q rows [Rp, Rp + Rq), each V floats
+  const float* p;
+  const float* q;
   int64_t V;
-  int B, L;
-  const int32_t* draft;
+  int Rp, Rq;
+  int S;                // slices per row
+  int64_t slen;         // slice length (multiple of 4)
   float T, top_p;
-  int top_k, q_mul_inv_t;
+  int top_k, p_mul, q_mul;
+  int do_k, do_p;
+  // acceptance (mode 0): positions (b, i), i <= L; p row b*(L+1)+i, q row Rp + b*L + i
+  int mode;             // 0 acceptance, 1 row sampling
+  int B, L;
+  int all_pos;          // draw at every position (sample_out requested)
+  const int32_t* draft;
   uint64_t seed;
   uint32_t offset;
-  const uint32_t* offset_dev;  // when non-null, the Philox offset is read here (graph replays)
+  const uint32_t* offset_dev;
   int32_t* n_out;
   int32_t* token_out;
   int32_t* seq_lens;
   uint8_t* accept_out;
   int32_t* sample_out;
-  AcceptWs ws;
+  // row sampling (mode 1): row r draws with Philox row row0 + r
+  int row0;
+  int32_t* tok_rows;
+  float* probs_out;
+  // workspace
+  float* gmax;          // [rows][kMaxSlices]
+  uint64_t* zsum;       // [rows]
+  uint32_t* hcnt;       // [rows][kL1]
+  uint64_t* hwgt;       // [rows][kL1]
+  uint32_t* ccnt;       // [rows][2] candidate counts (top-k list from the front, top-p from the back)
+  RowInfo* info;        // [rows]
+  RowParam* prm;        // [rows]
+  int32_t* acc;         // [B][L] accept flags
+  uint64_t* wsum;       // [draws][kMaxSlices]
+  uint32_t* cand;       // [rows][V]
 };
 
-__global__ __launch_bounds__(kNT) void accept_sample_kernel(SampleArgs a) {
-  __shared__ RowSmem sm;
-  __shared__ int last;
-  const int R = a.L + 1;
-  const uint32_t off = a.offset_dev ? a.offset_dev[0] : a.offset;
-  const int b = blockIdx.x / R, i = blockIdx.x % R;
-  const int64_t V = a.V;
-  float* ps = a.ws.scratch + (size_t)blockIdx.x * 2 * V;
-  float* qs = ps + V;
-  const RowProbs pr =
-      row_probs(a.p_logits + ((int64_t)b * R + i) * V, V, a.T, 0, a.top_p, a.top_k, ps, sm);
-  int acc = 0;
-  int64_t samp;
-  if (i < a.L) {
-    const int32_t d = a.draft[(int64_t)b * a.L + i];
-    RowProbs qr;
-    qr.trunc = 0;
-    qr.cut = 0;
-    qr.den = 1.0f;
-    const bool onehot = (a.q_logits == nullptr);
-    if (!onehot) qr = row_probs(a.q_logits + ((int64_t)b * a.L + i) * V, V, a.T, a.q_mul_inv_t, a.top_p, a.top_k, qs, sm);
-    __syncthreads();
-    // a draft id outside [0, V) is rejected (probability 0 under p)
-    const bool dvalid = d >= 0 && (int64_t)d < V;
-    const float pd = dvalid ? final_prob(pr, ps[d]) : 0.0f;
-    const float qd = !dvalid ? 1.0f : (onehot ? 1.0f : final_prob(qr, qs[d]));
-    const float u = u24_to_float(philox_word(a.seed, (uint32_t)i, (uint32_t)b, 0u, off));
-    float ratio = pd / (qd > 1e-9f ? qd : 1e-9f);
-    if (ratio > 1.0f) ratio = 1.0f;
-    acc = u < ratio;
-    auto resid = [&](int64_t j) -> float {
-      float pj = final_prob(pr, ps[j]);
-      float qj = onehot ? (j == d ? 1.0f : 0.0f) : final_prob(qr, qs[j]);
-      float t = pj - qj;
-      return t > 0.0f ? t : 0.0f;
-    };
-    uint64_t r = 0;
-    for (int64_t j = threadIdx.x; j < V; j += kNT) r += fx(resid(j));
-    const uint64_t Rs = block_sum_u64(r, sm);
-    const float Rf = fx_to_float(Rs);
-    const float den = Rf > 1e-9f ? Rf : 1e-9f;
-    samp = block_categorical(V, philox_word(a.seed, (uint32_t)i, (uint32_t)b, 1u, off),
-                             [&](int64_t j) { return resid(j) / den; }, sm);
-  } else {
-    samp = block_categorical(V, philox_word(a.seed, (uint32_t)i, (uint32_t)b, 1u, off),
-                             [&](int64_t j) { return final_prob(pr, ps[j]); }, sm);
-  }
-  if (threadIdx.x == 0) {
-    a.ws.acc[blockIdx.x] = acc;
-    a.ws.samp[blockIdx.x] = (int)samp;
-    __threadfence();
-    int prev = atomicAdd(&a.ws.cnt[b], 1);
-    last = (prev == R - 1);
-  }
-  __syncthreads();
-  if (!last || threadIdx.x != 0) return;
-  __threadfence();
-  int n = 0, token = -1;
-  bool done = false;
-  for (int k = 0; k < R; ++k) {
-    const int ak = __builtin_nontemporal_load(&a.ws.acc[b * R + k]);
-    const int sk = __builtin_nontemporal_load(&a.ws.samp[b * R + k]);
-    if (a.accept_out && k < a.L) a.accept_out[(int64_t)b * a.L + k] = (uint8_t)ak;
-    if (a.sample_out) a.sample_out[(int64_t)b * R + k] = sk;
-    if (!done) {
-      if (k < a.L && ak) {
-        ++n;
-      } else {
-        done = true;
-        token = sk;
-      }
-    }
-  }
-  a.n_out[b] = n;
-  a.token_out[b] = token;
-  if (a.seq_lens) a.seq_lens[b] += n + 1;
-  a.ws.cnt[b] = 0;
+__device__ __forceinline__ const float* samp_row(const SampArgs& a, int r) {
+  return r < a.Rp ? a.p + (int64_t)r * a.V : a.q + (int64_t)(r - a.Rp) * a.V;
+}
+__device__ __forceinline__ int samp_mul(const SampArgs& a, int r) { return r < a.Rp ? a.p_mul : a.q_mul; }
+__device__ __forceinline__ float yval(float x, int mul, float T, float inv_t) { return mul ? x * inv_t : x / T; }
+__device__ __forceinline__ uint32_t samp_offset(const SampArgs& a) { return a.offset_dev ? a.offset_dev[0] : a.offset; }
+
+__device__ __forceinline__ float row_max(const SampArgs& a, int r) {
+  float m = a.gmax[r * kMaxSlices];
+  for (int s = 1; s < a.S; ++s) m = fmaxf(m, a.gmax[r * kMaxSlices + s]);
+  return m;
 }
 
-// ----------------------------------------------------------------------------- row sampling
-__global__ __launch_bounds__(kNT) void sample_rows_kernel(const float* __restrict__ logits, int64_t V, float T,
-                                                          float top_p, int top_k, int mul_inv, uint64_t seed,
-                                                          uint32_t offset, const uint32_t* __restrict__ offset_dev,
-                                                          int row0, int32_t* __restrict__ token_out,
-                                                          float* __restrict__ probs) {
-  __shared__ RowSmem sm;
-  const int r = blockIdx.x;
-  if (offset_dev) offset = offset_dev[0];
-  const float* l = logits + (int64_t)r * V;
-  if (T <= 0.0f) {
-    float best = -__builtin_inff();
-    int bi = 0x7fffffff;
-    for (int64_t j = threadIdx.x; j < V; j += kNT)
-      if (l[j] > best || (l[j] == best && j < bi)) {
-        best = l[j];
-        bi = (int)j;
-      }
-    for (int o = 32; o > 0; o >>= 1) {
-      float ov = __shfl_xor(best, o, 64);
-      int oi = __shfl_xor(bi, o, 64);
-      if (ov > best || (ov == best && oi < bi)) {
-        best = ov;
-        bi = oi;
+// final probability of element j of a row with parameters rp
+__device__ __forceinline__ float final_prob(const RowParam& rp, float x, int mul, float T, float inv_t) {
+  const float e = dsk_expf(yval(x, mul, T, inv_t) - rp.m);
+  return f32_bits(e) >= rp.thr && rp.thr != kNone ? e / rp.sf : 0.0f;
+}
+
+// Visits the slice [lo, hi) of row x: f(j, x_j) for this thread's elements, four 16-byte loads
+// in flight per thread when VEC (16-byte aligned rows, lo a multiple of 4).
+template <bool VEC, typename F>
+__device__ __forceinline__ void for_slice(const float* __restrict__ x, int64_t lo, int64_t hi, F f) {
+  if constexpr (VEC) {
+    constexpr int UN = 4;
+    const int64_t n4 = (hi - lo) / 4;
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(x + lo);
+    for (int64_t c0 = threadIdx.x; c0 < n4; c0 += kST * UN) {
+      f32x4 v[UN];
+#pragma unroll
+      for (int u = 0; u < UN; ++u)
+        if (c0 + u * kST < n4) v[u] = x4[c0 + u * kST];
+#pragma unroll
+      for (int u = 0; u < UN; ++u) {
+        const int64_t c = c0 + u * kST;
+        if (c < n4) {
+          const int64_t j = lo + 4 * c;
+          f(j, v[u][0]);
+          f(j + 1, v[u][1]);
+          f(j + 2, v[u][2]);
+          f(j + 3, v[u][3]);
+        }
       }
     }
-    __shared__ float sv[kNW];
-    __shared__ int si[kNW];
-    if ((threadIdx.x & 63) == 0) {
-      sv[threadIdx.x >> 6] = best;
-      si[threadIdx.x >> 6] = bi;
+    lo += 4 * n4;
+  }
+  for (int64_t j = lo + threadIdx.x; j < hi; j += kST) f(j, x[j]);
+}
+
+__device__ float block_max512(float v, float* sh) {
+  v = wave_max(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh[w] = v;
+  __syncthreads();
+  float t = sh[0];
+#pragma unroll
+  for (int i = 1; i < kSW; ++i) t = fmaxf(t, sh[i]);
+  return t;
+}
+
+__device__ uint64_t block_sum512(uint64_t v, uint64_t* sh) {
+  v = wave_sum_u64(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) sh[w] = v;
+  __syncthreads();
+  uint64_t t = 0;
+#pragma unroll
+  for (int i = 0; i < kSW; ++i) t += sh[i];
+  return t;
+}
+
+// inclusive block scan in thread order; total receives the block sum
+__device__ uint64_t block_scan512(uint64_t v, uint64_t* sh, uint64_t& total) {
+  const uint64_t incl = wave_incl_scan_u64(v);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 63) sh[w] = incl;
+  __syncthreads();
+  uint64_t before = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < kSW; ++i) {
+    if (i < w) before += sh[i];
+    tot += sh[i];
+  }
+  total = tot;
+  return before + incl;
+}
+
+// ---- pass 1: slice maxima of y; slice 0 clears the row's merged accumulators
+template <bool VEC>
+__global__ __launch_bounds__(kST) void samp_max_kernel(SampArgs a) {
+  __shared__ float sh[kSW];
+  const int r = blockIdx.x / a.S, s = blockIdx.x % a.S;
+  const float* x = samp_row(a, r);
+  const int mul = samp_mul(a, r);
+  const float T = a.T, inv_t = 1.0f / T;
+  const int64_t lo = min(a.V, (int64_t)s * a.slen), hi = min(a.V, lo + a.slen);
+  float m = -__builtin_inff();
+  for_slice<VEC>(x, lo, hi, [&](int64_t, float v) { m = fmaxf(m, yval(v, mul, T, inv_t)); });
+  m = block_max512(m, sh);
+  if (threadIdx.x == 0) a.gmax[r * kMaxSlices + s] = m;
+  if (s == 0) {
+    if (threadIdx.x == 0) a.zsum[r] = 0;
+    if (a.do_k || a.do_p) {
+      for (int b = threadIdx.x; b < kL1; b += kST) {
+        a.hcnt[r * kL1 + b] = 0;
+        a.hwgt[r * kL1 + b] = 0;
+      }
+      if (threadIdx.x < 2) a.ccnt[r * 2 + threadIdx.x] = 0;
+    }
+  }
+}
+
+// ---- pass 2: Z and the first-level histogram, merged per row by integer atomics
+template <bool VEC>
+__global__ __launch_bounds__(kST) void samp_stats_kernel(SampArgs a) {
+  __shared__ uint32_t hc[kL1];
+  __shared__ unsigned long long hw[kL1];
+  __shared__ uint64_t sh[kSW];
+  const int r = blockIdx.x / a.S, s = blockIdx.x % a.S;
+  const bool trunc = a.do_k || a.do_p;
+  const float* x = samp_row(a, r);
+  const int mul = samp_mul(a, r);
+  const float T = a.T, inv_t = 1.0f / T;
+  const float m = row_max(a, r);
+  if (trunc) {
+    for (int b = threadIdx.x; b < kL1; b += kST) {
+      hc[b] = 0;
+      hw[b] = 0;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-      for (int w = 1; w < kNW; ++w)
-        if (sv[w] > sv[0] || (sv[w] == sv[0] && si[w] < si[0])) {
-          sv[0] = sv[w];
-          si[0] = si[w];
-        }
-      token_out[r] = si[0] >= V ? 0 : si[0];
+  }
+  const int64_t lo = min(a.V, (int64_t)s * a.slen), hi = min(a.V, lo + a.slen);
+  uint64_t z = 0;
+  for_slice<VEC>(x, lo, hi, [&](int64_t, float v) {
+    const float e = dsk_expf(yval(v, mul, T, inv_t) - m);
+    const uint64_t w = fx(e);
+    z += w;
+    if (trunc) {
+      const uint32_t b = min(f32_bits(e) >> kL1Shift, (uint32_t)kL1 - 1);  // NaN stays in bounds
+      atomicAdd(&hc[b], 1u);
+      if (w) atomicAdd(&hw[b], (unsigned long long)w);
     }
+  });
+  z = block_sum512(z, sh);
+  if (threadIdx.x == 0) atomicAdd((unsigned long long*)&a.zsum[r], (unsigned long long)z);
+  if (trunc) {
+    __syncthreads();
+    for (int b = threadIdx.x; b < kL1; b += kST) {
+      if (hc[b]) atomicAdd(&a.hcnt[r * kL1 + b], hc[b]);
+      if (hw[b]) atomicAdd((unsigned long long*)&a.hwgt[r * kL1 + b], hw[b]);
+    }
+  }
+}
+
+// ---- pass 3 (truncation): threshold buckets, then the candidates in them
+__global__ __launch_bounds__(kST) void samp_gather_kernel(SampArgs a) {
+  __shared__ uint64_t sh[kSW];
+  __shared__ uint32_t sel[4];
+  __shared__ uint64_t selw[2];
+  __shared__ uint32_t base[2];
+  const int r = blockIdx.x / a.S, s = blockIdx.x % a.S;
+  const float* x = samp_row(a, r);
+  const int mul = samp_mul(a, r);
+  const float T = a.T, inv_t = 1.0f / T;
+  const uint64_t Z = a.zsum[r];
+  const uint64_t TP = a.do_p ? top_p_target(a.top_p, Z) : 0;
+  // merged histogram, buckets in descending order: thread t holds bucket kL1 - 1 - t
+  const int bb = kL1 - 1 - (int)threadIdx.x;
+  const uint64_t c = a.hcnt[r * kL1 + bb];
+  const uint64_t w = a.hwgt[r * kL1 + bb];
+  if (threadIdx.x == 0) {
+    sel[0] = kNone;
+    sel[1] = kNone;
+  }
+  uint64_t tot;
+  const uint64_t ic = block_scan512(c, sh, tot);
+  const uint64_t iw = block_scan512(w, sh, tot);
+  if (a.do_k && ic - c < (uint64_t)a.top_k && ic >= (uint64_t)a.top_k) {
+    sel[0] = (uint32_t)bb;
+    sel[2] = (uint32_t)(ic - c);
+    selw[0] = iw - w;
+  }
+  if (a.do_p && TP > 0 && iw - w < TP && iw >= TP) {
+    sel[1] = (uint32_t)bb;
+    selw[1] = iw - w;
+  }
+  __syncthreads();
+  const uint32_t bk = sel[0], bp = sel[1];
+  if (s == 0 && threadIdx.x == 0) {
+    RowInfo inf;
+    inf.bk = bk;
+    inf.bp = bp;
+    inf.above_k = bk == kNone ? 0 : sel[2];
+    inf.pad = 0;
+    inf.wabove_k = bk == kNone ? 0 : selw[0];
+    inf.wabove_p = bp == kNone ? 0 : selw[1];
+    inf.tp = TP;
+    a.info[r] = inf;
+  }
+  const uint32_t bq = (bp == bk) ? kNone : bp;  // one list when both thresholds share a bucket
+  if (bk == kNone && bq == kNone) return;
+  // this thread's elements, keys kept in registers
+  const float m = row_max(a, r);
+  const int64_t lo = min(a.V, (int64_t)s * a.slen), hi = min(a.V, lo + a.slen);
+  uint32_t keys[kEPT];
+  uint32_t nk = 0, np = 0;
+#pragma unroll
+  for (int i = 0; i < kEPT; ++i) {
+    const int64_t j = lo + (int64_t)i * kST + threadIdx.x;
+    uint32_t key = kNone;
+    if (j < hi) key = f32_bits(dsk_expf(yval(x[j], mul, T, inv_t) - m));
+    keys[i] = key;
+    const uint32_t b = key >> kL1Shift;
+    nk += (key != kNone && b == bk);
+    np += (key != kNone && b == bq);
+  }
+  uint64_t totk, totp;
+  const uint64_t offk = block_scan512(nk, sh, totk) - nk;
+  const uint64_t offp = block_scan512(np, sh, totp) - np;
+  if (threadIdx.x == 0) {
+    base[0] = totk ? atomicAdd(&a.ccnt[r * 2], (uint32_t)totk) : 0;
+    base[1] = totp ? atomicAdd(&a.ccnt[r * 2 + 1], (uint32_t)totp) : 0;
+  }
+  __syncthreads();
+  uint32_t* ck = a.cand + (int64_t)r * a.V;
+  uint32_t pk = base[0] + (uint32_t)offk, pp = base[1] + (uint32_t)offp;
+#pragma unroll
+  for (int i = 0; i < kEPT; ++i) {
+    const uint32_t key = keys[i];
+    if (key == kNone) continue;
+    const uint32_t b = key >> kL1Shift;
+    if (b == bk) ck[pk++] = key;
+    else if (b == bq) ck[a.V - 1 - (pp++)] = key;
+  }
+}
+
+// ---- pass 4: exact thresholds from the candidates, the kept mass, the accept test
+struct FinSmem {
+  unsigned long long hist[2048];
+  uint64_t sh[kSW];
+  uint32_t bc32;
+  uint64_t bc64;
+  RowParam rp[2];
+};
+
+// Key K among the n candidate keys (all in first-level bucket `bucket`) with
+// weight(> K) < target <= weight(>= K), weight 1 per key (count) or fx(value) (mass); two
+// radix levels over the key's low 21 bits (11 then 10 bits).
+__device__ uint32_t select_key(const uint32_t* __restrict__ cand, uint32_t n, bool mass, uint64_t target,
+                               uint32_t bucket, FinSmem& sm) {
+  uint32_t prefix = bucket << kL1Shift;
+  uint64_t above = 0;
+  const int shifts[2] = {10, 0};
+  const int widths[2] = {11, 10};
+  for (int lv = 0; lv < 2; ++lv) {
+    const int sh = shifts[lv], nb = 1 << widths[lv];
+    __syncthreads();
+    for (int i = threadIdx.x; i < nb; i += kST) sm.hist[i] = 0;
+    if (threadIdx.x == 0) sm.bc32 = kNone;
+    __syncthreads();
+    for (uint32_t c = threadIdx.x; c < n; c += kST) {
+      const uint32_t key = cand[c];
+      if (lv == 1 && (key >> 10) != (prefix >> 10)) continue;
+      const uint64_t w = mass ? fx(bits_f32(key)) : 1;
+      if (w) atomicAdd(&sm.hist[(key >> sh) & (nb - 1)], (unsigned long long)w);
+    }
+    __syncthreads();
+    // descending scan: thread t owns buckets nb-1-4t .. nb-4-4t
+    const int nthr = nb / 4;
+    uint64_t loc[4] = {0, 0, 0, 0}, tsum = 0;
+    if ((int)threadIdx.x < nthr) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        loc[q] = sm.hist[nb - 1 - (int)threadIdx.x * 4 - q];
+        tsum += loc[q];
+      }
+    }
+    uint64_t tot;
+    uint64_t run = above + block_scan512(tsum, sm.sh, tot) - tsum;
+    if ((int)threadIdx.x < nthr) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint64_t nrun = run + loc[q];
+        if (run < target && nrun >= target) {
+          sm.bc32 = (uint32_t)(nb - 1 - (int)threadIdx.x * 4 - q);
+          sm.bc64 = run;
+        }
+        run = nrun;
+      }
+    }
+    __syncthreads();
+    if (sm.bc32 == kNone) return prefix;  // unreachable: the bucket holds the target
+    above = sm.bc64;
+    prefix |= sm.bc32 << sh;
+  }
+  return prefix;
+}
+
+__device__ uint64_t mass_at_or_above(const uint32_t* __restrict__ cand, uint32_t n, uint32_t K, FinSmem& sm) {
+  uint64_t t = 0;
+  for (uint32_t c = threadIdx.x; c < n; c += kST) {
+    const uint32_t key = cand[c];
+    if (key >= K) t += fx(bits_f32(key));
+  }
+  return block_sum512(t, sm.sh);
+}
+
+__device__ RowParam finish_row(const SampArgs& a, int r, FinSmem& sm) {
+  RowParam rp;
+  rp.m = row_max(a, r);
+  rp.pad = 0;
+  const uint64_t Z = a.zsum[r];
+  if (!a.do_k && !a.do_p) {
+    rp.thr = 0;
+    rp.sf = fx_to_float(Z);
+    return rp;
+  }
+  const RowInfo inf = a.info[r];
+  if (a.do_p && inf.tp == 0) {  // empty nucleus
+    rp.thr = kNone;
+    rp.sf = 0.0f;
+    return rp;
+  }
+  const uint32_t* ck = a.cand + (int64_t)r * a.V;
+  const uint32_t nk = a.ccnt[r * 2];
+  const bool shared = inf.bp == inf.bk;
+  const uint32_t np = shared ? nk : a.ccnt[r * 2 + 1];
+  const uint32_t* cp = shared ? ck : ck + (a.V - np);
+  uint32_t kth = 0, cut = 0;
+  if (a.do_k && inf.bk != kNone) kth = select_key(ck, nk, false, (uint64_t)a.top_k - inf.above_k, inf.bk, sm);
+  if (a.do_p && inf.bp != kNone) cut = select_key(cp, np, true, inf.tp - inf.wabove_p, inf.bp, sm);
+  uint64_t S;
+  if (a.do_p && inf.bp != kNone && cut >= kth) {
+    rp.thr = cut;
+    S = inf.wabove_p + mass_at_or_above(cp, np, cut, sm);
+  } else if (a.do_k && inf.bk != kNone) {
+    rp.thr = kth;
+    S = inf.wabove_k + mass_at_or_above(ck, nk, kth, sm);
+  } else {  // unreachable: an active threshold always finds its bucket
+    rp.thr = 0;
+    S = Z;
+  }
+  rp.sf = fx_to_float(S);
+  return rp;
+}
+
+__global__ __launch_bounds__(kST) void samp_finish_kernel(SampArgs a) {
+  __shared__ FinSmem sm;
+  const int unit = blockIdx.x;
+  int rp_row, rq_row = -1, b = 0, i = 0;
+  if (a.mode == 0) {
+    b = unit / (a.L + 1);
+    i = unit % (a.L + 1);
+    rp_row = b * (a.L + 1) + i;
+    if (i < a.L && a.Rq) rq_row = a.Rp + b * a.L + i;
+  } else {
+    rp_row = unit;
+  }
+  const RowParam pp = finish_row(a, rp_row, sm);
+  if (threadIdx.x == 0) a.prm[rp_row] = pp;
+  RowParam qp = pp;
+  if (rq_row >= 0) {
+    __syncthreads();
+    qp = finish_row(a, rq_row, sm);
+    if (threadIdx.x == 0) a.prm[rq_row] = qp;
+  }
+  if (a.mode != 0 || i >= a.L || threadIdx.x != 0) return;
+  // accept test of the drafted token at position i; a draft id outside [0, V) is rejected
+  const float T = a.T, inv_t = 1.0f / T;
+  const int32_t d = a.draft[(int64_t)b * a.L + i];
+  const bool dvalid = d >= 0 && (int64_t)d < a.V;
+  const float pd = dvalid ? final_prob(pp, samp_row(a, rp_row)[d], a.p_mul, T, inv_t) : 0.0f;
+  const float qd = (!dvalid || rq_row < 0) ? 1.0f : final_prob(qp, samp_row(a, rq_row)[d], a.q_mul, T, inv_t);
+  const float u = u24_to_float(philox_word(a.seed, (uint32_t)i, (uint32_t)b, 0u, samp_offset(a)));
+  float ratio = pd / (qd > 1e-9f ? qd : 1e-9f);
+  if (ratio > 1.0f) ratio = 1.0f;
+  a.acc[(int64_t)b * a.L + i] = u < ratio;
+}
+
+// ---- the distribution one draw uses
+struct DrawSpec {
+  int prow, qrow;       // p row, q row of a residual draw (qrow -1: bonus / row draw)
+  int32_t d;            // drafted token of a residual draw with one-hot q (qrow -2)
+  RowParam pp, qp;
+  const float* px;
+  const float* qx;
+  int pmul, qmul;
+  int b, pos, n;        // acceptance: batch row, drawn position, accepted count
+  uint32_t word;
+};
+
+__device__ __forceinline__ uint64_t draw_weight(const DrawSpec& ds, int64_t j, float T, float inv_t) {
+  const float pj = final_prob(ds.pp, ds.px[j], ds.pmul, T, inv_t);
+  if (ds.qrow == -1) return fx(pj);
+  const float qj = ds.qrow == -2 ? (j == ds.d ? 1.0f : 0.0f) : final_prob(ds.qp, ds.qx[j], ds.qmul, T, inv_t);
+  const float t = pj - qj;
+  return fx(t > 0.0f ? t : 0.0f);
+}
+
+__device__ DrawSpec draw_spec(const SampArgs& a, int unit) {
+  DrawSpec ds;
+  ds.qrow = -1;
+  ds.d = -1;
+  ds.n = 0;
+  ds.b = 0;
+  ds.pos = 0;
+  const uint32_t off = samp_offset(a);
+  if (a.mode == 0) {
+    ds.b = a.all_pos ? unit / (a.L + 1) : unit;
+    int n = 0;
+    while (n < a.L && a.acc[(int64_t)ds.b * a.L + n]) ++n;
+    ds.n = n;
+    ds.pos = a.all_pos ? unit % (a.L + 1) : n;
+    ds.prow = ds.b * (a.L + 1) + ds.pos;
+    if (ds.pos < a.L) {
+      ds.d = a.draft[(int64_t)ds.b * a.L + ds.pos];
+      ds.qrow = a.Rq ? a.Rp + ds.b * a.L + ds.pos : -2;
+    }
+    ds.word = philox_word(a.seed, (uint32_t)ds.pos, (uint32_t)ds.b, 1u, off);
+  } else {
+    ds.prow = unit;
+    ds.word = philox_word(a.seed, (uint32_t)(a.row0 + unit), 0u, 2u, off);
+  }
+  ds.pp = a.prm[ds.prow];
+  ds.px = samp_row(a, ds.prow);
+  ds.pmul = samp_mul(a, ds.prow);
+  if (ds.qrow >= 0) {
+    ds.qp = a.prm[ds.qrow];
+    ds.qx = samp_row(a, ds.qrow);
+    ds.qmul = samp_mul(a, ds.qrow);
+  } else {
+    ds.qp = ds.pp;
+    ds.qx = ds.px;
+    ds.qmul = ds.pmul;
+  }
+  return ds;
+}
+
+// ---- pass 5: per-slice mass of each draw's distribution (row sampling also stores p')
+template <bool VEC>
+__global__ __launch_bounds__(kST) void samp_wsum_kernel(SampArgs a) {
+  __shared__ uint64_t sh[kSW];
+  const int unit = blockIdx.x / a.S, s = blockIdx.x % a.S;
+  const DrawSpec ds = draw_spec(a, unit);
+  const float T = a.T, inv_t = 1.0f / T;
+  const int64_t lo = min(a.V, (int64_t)s * a.slen), hi = min(a.V, lo + a.slen);
+  uint64_t t = 0;
+  if (a.mode == 1 && a.probs_out) {
+    float* po = a.probs_out + (int64_t)unit * a.V;
+    for_slice<VEC>(ds.px, lo, hi, [&](int64_t j, float v) {
+      const float pj = final_prob(ds.pp, v, ds.pmul, T, inv_t);
+      po[j] = pj;
+      t += fx(pj);
+    });
+  } else if (ds.qrow == -1) {
+    for_slice<VEC>(ds.px, lo, hi, [&](int64_t, float v) { t += fx(final_prob(ds.pp, v, ds.pmul, T, inv_t)); });
+  } else {
+    for (int64_t j = lo + threadIdx.x; j < hi; j += kST) t += draw_weight(ds, j, T, inv_t);
+  }
+  t = block_sum512(t, sh);
+  if (threadIdx.x == 0) a.wsum[(int64_t)unit * kMaxSlices + s] = t;
+}
+
+// ---- pass 6: the inverse-CDF draw, then the outputs
+__global__ __launch_bounds__(kST) void samp_draw_kernel(SampArgs a) {
+  __shared__ uint64_t sh[kSW];
+  __shared__ int64_t found;
+  __shared__ uint64_t sbase;
+  __shared__ int sslice;
+  const int unit = blockIdx.x;
+  const DrawSpec ds = draw_spec(a, unit);
+  const float T = a.T, inv_t = 1.0f / T;
+  const uint64_t* ws = a.wsum + (int64_t)unit * kMaxSlices;
+  const uint64_t u = ds.word >> 8;
+  if (threadIdx.x == 0) {
+    uint64_t W = 0;
+    for (int s = 0; s < a.S; ++s) W += ws[s];
+    found = -1;
+    sslice = -1;
+    if (W == 0) {
+      found = (int64_t)((u * (uint64_t)a.V) >> 24);
+    } else {
+      const uint64_t t = (W >> 24) * u + (((W & 0xFFFFFFull) * u) >> 24);
+      uint64_t run = 0;
+      for (int s = 0; s < a.S; ++s) {
+        if (t < run + ws[s]) {
+          sslice = s;
+          break;
+        }
+        run += ws[s];
+      }
+      sbase = t - run;  // the target inside the slice
+    }
+  }
+  __syncthreads();
+  if (found < 0 && sslice >= 0) {
+    const uint64_t tt = sbase;
+    const int64_t lo = min(a.V, (int64_t)sslice * a.slen), hi = min(a.V, lo + a.slen);
+    uint64_t run = 0;
+    for (int64_t c0 = lo; c0 < hi; c0 += 4 * kST) {
+      const int64_t j0 = c0 + 4 * (int64_t)threadIdx.x;
+      uint64_t w4[4], tsum = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        w4[e] = (j0 + e < hi) ? draw_weight(ds, j0 + e, T, inv_t) : 0;
+        tsum += w4[e];
+      }
+      uint64_t tot;
+      const uint64_t incl = block_scan512(tsum, sh, tot);
+      uint64_t r0 = run + incl - tsum;
+      if (r0 <= tt && tt < run + incl) {  // exactly one thread holds the crossing
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (tt < r0 + w4[e]) {
+            found = j0 + e;
+            break;
+          }
+          r0 += w4[e];
+        }
+      }
+      __syncthreads();
+      if (found >= 0) break;
+      run += tot;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  const int32_t tok = (int32_t)(found >= 0 ? found : 0);
+  if (a.mode == 1) {
+    a.tok_rows[unit] = tok;
     return;
   }
-  float* ps = probs + (int64_t)r * V;
-  const RowProbs pr = row_probs(l, V, T, mul_inv, top_p, top_k, ps, sm);
-  __syncthreads();
-  const int64_t tok = block_categorical(V, philox_word(seed, (uint32_t)(row0 + r), 0u, 2u, offset),
-                                        [&](int64_t j) { return final_prob(pr, ps[j]); }, sm);
-  __syncthreads();
-  if (pr.trunc)
-    for (int64_t j = threadIdx.x; j < V; j += kNT) ps[j] = final_prob(pr, ps[j]);
-  if (threadIdx.x == 0) token_out[r] = (int32_t)tok;
+  if (a.sample_out) a.sample_out[(int64_t)ds.b * (a.L + 1) + ds.pos] = tok;
+  if (ds.pos != ds.n) return;
+  a.n_out[ds.b] = ds.n;
+  a.token_out[ds.b] = tok;
+  if (a.seq_lens) a.seq_lens[ds.b] += ds.n + 1;
+  if (a.accept_out)
+    for (int k = 0; k < a.L; ++k) a.accept_out[(int64_t)ds.b * a.L + k] = (uint8_t)a.acc[(int64_t)ds.b * a.L + k];
 }
+
+// ---- workspace layout of the sampled paths
+struct SampLayout {
+  size_t gmax, zsum, hcnt, hwgt, ccnt, info, prm, acc, wsum, cand, total;
+};
+
+__host__ inline SampLayout samp_layout(size_t rows, size_t draws, size_t accs, int64_t V) {
+  SampLayout L;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off += align256(bytes);
+    return o;
+  };
+  L.gmax = take(rows * kMaxSlices * 4);
+  L.zsum = take(rows * 8);
+  L.hcnt = take(rows * kL1 * 4);
+  L.hwgt = take(rows * kL1 * 8);
+  L.ccnt = take(rows * 2 * 4);
+  L.info = take(rows * sizeof(RowInfo));
+  L.prm = take(rows * sizeof(RowParam));
+  L.acc = take(accs * 4);
+  L.wsum = take(draws * kMaxSlices * 8);
+  L.cand = take(rows * (size_t)V * 4);
+  L.total = off;
+  return L;
+}
+
+__host__ inline void samp_bind(SampArgs& a, void* base, const SampLayout& L) {
+  uint8_t* p = reinterpret_cast<uint8_t*>(base);
+  a.gmax = reinterpret_cast<float*>(p + L.gmax);
+  a.zsum = reinterpret_cast<uint64_t*>(p + L.zsum);
+  a.hcnt = reinterpret_cast<uint32_t*>(p + L.hcnt);
+  a.hwgt = reinterpret_cast<uint64_t*>(p + L.hwgt);
+  a.ccnt = reinterpret_cast<uint32_t*>(p + L.ccnt);
+  a.info = reinterpret_cast<RowInfo*>(p + L.info);
+  a.prm = reinterpret_cast<RowParam*>(p + L.prm);
+  a.acc = reinterpret_cast<int32_t*>(p + L.acc);
+  a.wsum = reinterpret_cast<uint64_t*>(p + L.wsum);
+  a.cand = reinterpret_cast<uint32_t*>(p + L.cand);
+}
+
+// slices per row: at least enough for the gather pass's registers, about 1024 workgroups in
+// all, at most kMaxSlices, never slices shorter than 512 elements
+__host__ inline int samp_slices(int rows, int64_t V) {
+  int64_t S = ceil_div(1024, rows);
+  S = std::min<int64_t>(S, std::max<int64_t>(1, V / 512));
+  S = std::max<int64_t>(S, ceil_div(V, kMaxSlice));
+  return (int)std::min<int64_t>(S, kMaxSlices);
+}
+
+__host__ inline int64_t samp_slice_len(int64_t V, int S) { return (ceil_div(V, S) + 3) & ~(int64_t)3; }
 
 }  // namespace dsk
 
@@ -653,7 +957,7 @@ using namespace dsk;
 
 // Pass 1 over `rows` rows of logits into ws.gval / ws.gidx; 16-byte chunk loads when every row
 // starts 16-byte aligned.
-static void launch_slice_argmax(const void* logits, int dtype, int64_t ldl, int64_t V, int rows, const AcceptWs& ws,
+static void launch_slice_argmax(const void* logits, int dtype, int64_t ldl, int64_t V, int rows, const GreedyWs& ws,
                                 hipStream_t st) {
   const int64_t esz = dtype == DSK_BF16 ? 2 : 4;
   const bool vec = ((uintptr_t)logits & 15) == 0 && (ldl * esz) % 16 == 0;
@@ -667,18 +971,53 @@ static void launch_slice_argmax(const void* logits, int dtype, int64_t ldl, int6
   }
 }
 
+// The sampled chain (passes 1-6) for the rows and draws a describes.
+static int launch_sampled(SampArgs& a, int draws, int finish_units, bool vec, hipStream_t st, const char* who) {
+  const int rows = a.Rp + a.Rq;
+  const dim3 blk(kST);
+  const dim3 grow((unsigned)(rows * a.S));
+  if (vec) {
+    hipLaunchKernelGGL(samp_max_kernel<true>, grow, blk, 0, st, a);
+    hipLaunchKernelGGL(samp_stats_kernel<true>, grow, blk, 0, st, a);
+  } else {
+    hipLaunchKernelGGL(samp_max_kernel<false>, grow, blk, 0, st, a);
+    hipLaunchKernelGGL(samp_stats_kernel<false>, grow, blk, 0, st, a);
+  }
+  if (a.do_k || a.do_p) hipLaunchKernelGGL(samp_gather_kernel, grow, blk, 0, st, a);
+  hipLaunchKernelGGL(samp_finish_kernel, dim3((unsigned)finish_units), blk, 0, st, a);
+  const dim3 gdraw((unsigned)(draws * a.S));
+  if (vec) hipLaunchKernelGGL(samp_wsum_kernel<true>, gdraw, blk, 0, st, a);
+  else hipLaunchKernelGGL(samp_wsum_kernel<false>, gdraw, blk, 0, st, a);
+  hipLaunchKernelGGL(samp_draw_kernel, dim3((unsigned)draws), blk, 0, st, a);
+  DSK_LAUNCH_CHECK(who);
+  return DSK_OK;
+}
+
+static void samp_common(SampArgs& a, int64_t V, int rows, float T, float top_p, int top_k) {
+  a.V = V;
+  a.T = T;
+  a.top_p = top_p;
+  a.top_k = top_k;
+  a.do_k = (top_k > 0 && (int64_t)top_k < V);
+  a.do_p = (top_p < 1.0f);
+  a.S = samp_slices(rows, V);
+  a.slen = samp_slice_len(V, a.S);
+}
+
+static size_t accept_sample_ws(int B, int L, int64_t V) {
+  const size_t rows = (size_t)B * (2 * L + 1);
+  return samp_layout(rows, (size_t)B * (L + 1), (size_t)B * std::max(L, 1), V).total;
+}
+
 extern "C" size_t dsk_accept_ws_bytes(int B, int W, int64_t V) {
   if (B <= 0 || W <= 0 || V <= 0) return 0;
-  return accept_ws_total(B, W, V);
+  return std::max(greedy_ws_bytes((size_t)B * W), accept_sample_ws(B, W - 1, V));
 }
 
 extern "C" int dsk_accept_ws_init(void* workspace, size_t ws_bytes, dsk_stream_t stream) {
-  DSK_REQUIRE(workspace && ws_bytes >= kAcceptCounterBytes, "dsk_accept_ws_init: workspace too small");
-  hipError_t e = hipMemsetAsync(workspace, 0, kAcceptCounterBytes, as_stream(stream));
-  if (e != hipSuccess) {
-    set_error("dsk_accept_ws_init: %s", hipGetErrorString(e));
-    return DSK_ELAUNCH;
-  }
+  // No kernel of this file keeps state in the workspace between calls: nothing to initialise.
+  (void)stream;
+  DSK_REQUIRE(workspace && ws_bytes > 0, "dsk_accept_ws_init: empty workspace");
   return DSK_OK;
 }
 
@@ -691,9 +1030,9 @@ extern "C" int dsk_accept_greedy(const void* logits, int dtype, int64_t ldl, int
               "dsk_accept_greedy: bad shape B=%d W=%d V=%lld", B, W, (long long)V);
   DSK_REQUIRE(ldl >= V, "dsk_accept_greedy: ldl < V");
   DSK_REQUIRE(dtype == DSK_F32 || dtype == DSK_BF16, "dsk_accept_greedy: dtype must be f32 or bf16");
-  DSK_REQUIRE(ws_bytes >= accept_ws_total(B, W, V) - (size_t)B * W * 2 * V * 4,
-              "dsk_accept_greedy: workspace too small");
-  AcceptWs ws = accept_ws(workspace, B, W, V);
+  DSK_REQUIRE(ws_bytes >= greedy_ws_bytes((size_t)B * W), "dsk_accept_greedy: workspace %zu < %zu", ws_bytes,
+              greedy_ws_bytes((size_t)B * W));
+  GreedyWs ws = greedy_ws(workspace, (size_t)B * W);
   const hipStream_t st = as_stream(stream);
   launch_slice_argmax(logits, dtype, ldl, V, B * W, ws, st);
   hipLaunchKernelGGL(accept_greedy_finish_kernel, dim3((unsigned)B), dim3(256), 0, st, W, V, draft, tt, n_out,
@@ -756,7 +1095,7 @@ extern "C" int dsk_accept_greedy_static(const void* logits, int dtype, int64_t l
   void* base = nullptr;
   const int rc = static_scratch(&base, "dsk_accept_greedy_static");
   if (rc != DSK_OK) return rc;
-  AcceptWs ws{};
+  GreedyWs ws;
   ws.gval = reinterpret_cast<float*>(base);
   ws.gidx = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(base) + kStaticSliceBytes);
   const hipStream_t st = as_stream(stream);
@@ -769,7 +1108,7 @@ extern "C" int dsk_accept_greedy_static(const void* logits, int dtype, int64_t l
 
 extern "C" size_t dsk_argmax_ws_bytes(int R) {
   if (R <= 0 || R > 1024) return 0;
-  return kAcceptCounterBytes + 2 * align256((size_t)R * kGreedySlices * 4);
+  return greedy_ws_bytes((size_t)R);
 }
 
 extern "C" int dsk_argmax_rows(const void* logits, int dtype, int64_t ldl, int64_t V, int R, int32_t* token_out,
@@ -781,7 +1120,7 @@ extern "C" int dsk_argmax_rows(const void* logits, int dtype, int64_t ldl, int64
   DSK_REQUIRE(dtype == DSK_F32 || dtype == DSK_BF16, "dsk_argmax_rows: dtype must be f32 or bf16");
   DSK_REQUIRE(ws_bytes >= dsk_argmax_ws_bytes(R), "dsk_argmax_rows: workspace %zu < %zu", ws_bytes,
               dsk_argmax_ws_bytes(R));
-  AcceptWs ws = accept_ws(workspace, R, 1, V);
+  GreedyWs ws = greedy_ws(workspace, (size_t)R);
   const hipStream_t st = as_stream(stream);
   launch_slice_argmax(logits, dtype, ldl, V, R, ws, st);
   hipLaunchKernelGGL(argmax_merge_kernel, dim3((unsigned)R), dim3(64), 0, st, V, ws.gval, ws.gidx, token_out);
@@ -796,22 +1135,24 @@ extern "C" int dsk_accept_sample(const float* p_logits, const float* q_logits, i
                                  size_t ws_bytes, const uint32_t* offset_dev, dsk_stream_t stream) {
   DSK_REQUIRE(p_logits && n_out && token_out && workspace, "dsk_accept_sample: null pointer");
   DSK_REQUIRE(L == 0 || draft, "dsk_accept_sample: draft is null");
-  DSK_REQUIRE(B > 0 && B <= 1024 && L >= 0 && L < 255 && V > 0 && V < (1ll << 31),
-              "dsk_accept_sample: bad shape B=%d L=%d V=%lld", B, L, (long long)V);
+  DSK_REQUIRE(B > 0 && B <= 1024 && L >= 0 && L < 255 && V > 0 && V <= (1ll << 19),
+              "dsk_accept_sample: bad shape B=%d L=%d V=%lld (V <= 2^19)", B, L, (long long)V);
   DSK_REQUIRE(temperature > 0.0f, "dsk_accept_sample: temperature must be > 0");
-  DSK_REQUIRE(ws_bytes >= accept_ws_total(B, L + 1, V), "dsk_accept_sample: workspace %zu < %zu", ws_bytes,
-              accept_ws_total(B, L + 1, V));
-  SampleArgs a;
-  a.p_logits = p_logits;
-  a.q_logits = q_logits;
-  a.V = V;
+  const size_t need = accept_sample_ws(B, L, V);
+  DSK_REQUIRE(ws_bytes >= need, "dsk_accept_sample: workspace %zu < %zu", ws_bytes, need);
+  SampArgs a{};
+  a.p = p_logits;
+  a.q = q_logits;
+  a.Rp = B * (L + 1);
+  a.Rq = q_logits ? B * L : 0;
+  samp_common(a, V, a.Rp + a.Rq, temperature, top_p, top_k);
+  a.p_mul = 0;
+  a.q_mul = q_mul_inv_t;
+  a.mode = 0;
   a.B = B;
   a.L = L;
+  a.all_pos = sample_out != nullptr;
   a.draft = draft;
-  a.T = temperature;
-  a.top_p = top_p;
-  a.top_k = top_k;
-  a.q_mul_inv_t = q_mul_inv_t;
   a.seed = seed;
   a.offset = offset;
   a.offset_dev = offset_dev;
@@ -820,20 +1161,51 @@ extern "C" int dsk_accept_sample(const float* p_logits, const float* q_logits, i
   a.seq_lens = seq_lens;
   a.accept_out = accept_out;
   a.sample_out = sample_out;
-  a.ws = accept_ws(workspace, B, L + 1, V);
-  hipLaunchKernelGGL(accept_sample_kernel, dim3((unsigned)(B * (L + 1))), dim3(kNT), 0, as_stream(stream), a);
-  DSK_LAUNCH_CHECK("dsk_accept_sample");
-  return DSK_OK;
+  samp_bind(a, workspace, samp_layout((size_t)B * (2 * L + 1), (size_t)B * (L + 1), (size_t)B * std::max(L, 1), V));
+  const bool vec = V % 4 == 0 && ((uintptr_t)p_logits & 15) == 0 && ((uintptr_t)q_logits & 15) == 0;
+  const int draws = a.all_pos ? B * (L + 1) : B;
+  return launch_sampled(a, draws, B * (L + 1), vec, as_stream(stream), "dsk_accept_sample");
+}
+
+extern "C" size_t dsk_sample_ws_bytes(int R, int64_t V) {
+  if (R <= 0 || V <= 0) return 0;
+  return std::max(R <= 1024 ? greedy_ws_bytes((size_t)R) : 0, samp_layout((size_t)R, (size_t)R, 1, V).total);
 }
 
 extern "C" int dsk_sample_rows(const float* logits, int64_t V, int R, float temperature, float top_p, int top_k,
                                int mul_inv_t, uint64_t seed, uint32_t offset, int row0, int32_t* token_out,
-                               float* probs_out, const uint32_t* offset_dev, dsk_stream_t stream) {
-  DSK_REQUIRE(logits && token_out, "dsk_sample_rows: null pointer");
-  DSK_REQUIRE(R > 0 && V > 0 && V < (1ll << 31), "dsk_sample_rows: bad shape");
-  DSK_REQUIRE(temperature <= 0.0f || probs_out, "dsk_sample_rows: probs_out is required when temperature > 0");
-  hipLaunchKernelGGL(sample_rows_kernel, dim3((unsigned)R), dim3(kNT), 0, as_stream(stream), logits, V, temperature,
-                     top_p, top_k, mul_inv_t, seed, offset, offset_dev, row0, token_out, probs_out);
-  DSK_LAUNCH_CHECK("dsk_sample_rows");
-  return DSK_OK;
+                               float* probs_out, const uint32_t* offset_dev, void* workspace, size_t ws_bytes,
+                               dsk_stream_t stream) {
+  DSK_REQUIRE(logits && token_out && workspace, "dsk_sample_rows: null pointer");
+  DSK_REQUIRE(R > 0 && V > 0 && V <= (1ll << 19), "dsk_sample_rows: bad shape R=%d V=%lld (V <= 2^19)", R,
+              (long long)V);
+  DSK_REQUIRE(ws_bytes >= dsk_sample_ws_bytes(R, V), "dsk_sample_rows: workspace %zu < %zu", ws_bytes,
+              dsk_sample_ws_bytes(R, V));
+  const hipStream_t st = as_stream(stream);
+  if (temperature <= 0.0f) {
+    DSK_REQUIRE(R <= 1024, "dsk_sample_rows: greedy picks take at most 1024 rows");
+    GreedyWs ws = greedy_ws(workspace, (size_t)R);
+    launch_slice_argmax(logits, DSK_F32, V, V, R, ws, st);
+    hipLaunchKernelGGL(argmax_merge_kernel, dim3((unsigned)R), dim3(64), 0, st, V, ws.gval, ws.gidx, token_out);
+    DSK_LAUNCH_CHECK("dsk_sample_rows");
+    return DSK_OK;
+  }
+  SampArgs a{};
+  a.p = logits;
+  a.q = nullptr;
+  a.Rp = R;
+  a.Rq = 0;
+  samp_common(a, V, R, temperature, top_p, top_k);
+  a.p_mul = mul_inv_t;
+  a.q_mul = 0;
+  a.mode = 1;
+  a.seed = seed;
+  a.offset = offset;
+  a.offset_dev = offset_dev;
+  a.row0 = row0;
+  a.tok_rows = token_out;
+  a.probs_out = probs_out;
+  samp_bind(a, workspace, samp_layout((size_t)R, (size_t)R, 1, V));
+  const bool vec = V % 4 == 0 && ((uintptr_t)logits & 15) == 0 && ((uintptr_t)probs_out & 15) == 0;
+  return launch_sampled(a, R, R, vec, st, "dsk_sample_rows");
 }

@@ -254,7 +254,7 @@ using namespace dsk;
 extern "C" size_t dsk_markov_ws_bytes(int B, int64_t V, int sampled) {
   if (B <= 0 || V <= 0) return 0;
   const size_t part = (size_t)2 * B * markov_nblk(V) * (sizeof(float) + sizeof(int32_t));
-  return ((part + 255) & ~(size_t)255) + (sampled ? (size_t)B * V * sizeof(float) : 0);
+  return ((part + 255) & ~(size_t)255) + (sampled ? dsk_sample_ws_bytes(1, V) : 0);
 }
 
 extern "C" int dsk_markov_block(const float* base, int64_t ldb, int B, int cap, int64_t V, int R,
@@ -290,8 +290,8 @@ extern "C" int dsk_markov_block(const float* base, int64_t ldb, int B, int cap, 
   const size_t part = (size_t)2 * B * a.nblk;
   a.pval = reinterpret_cast<float*>(workspace);
   a.pidx = reinterpret_cast<int32_t*>(a.pval + part);
-  float* probs = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) +
-                                          (((part * 8) + 255) & ~(size_t)255));
+  void* sample_ws = reinterpret_cast<uint8_t*>(workspace) + (((part * 8) + 255) & ~(size_t)255);
+  const size_t sample_ws_bytes = sampled ? dsk_sample_ws_bytes(1, V) : 0;
   hipStream_t st = as_stream(stream);
   for (int s = 0; s < cap; ++s) {
     a.step = s;
@@ -301,8 +301,8 @@ extern "C" int dsk_markov_block(const float* base, int64_t ldb, int B, int cap, 
       // q_i = truncate(softmax(logits_i * (1/T))), sampled; Philox rows b * cap + s
       for (int b = 0; b < B; ++b) {
         const int rc = dsk_sample_rows(q_logits_out + ((int64_t)b * cap + s) * V, V, 1, temperature, top_p, top_k, 1,
-                                       seed, offset, b * cap + s, tok_out + b * cap + s, probs + (int64_t)b * V,
-                                       nullptr, stream);
+                                       seed, offset, b * cap + s, tok_out + b * cap + s, nullptr, nullptr, sample_ws,
+                                       sample_ws_bytes, stream);
         if (rc != DSK_OK) return rc;
       }
     }

@@ -62,8 +62,9 @@ SIGNATURES: dict[str, tuple] = {
     "dsk_accept_sample": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_int, c_void_p, c_float, c_float, c_int,
                                   c_int, c_uint64, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_size_t, c_void_p, c_void_p]),
+    "dsk_sample_ws_bytes": (c_size_t, [c_int, c_int64]),
     "dsk_sample_rows": (c_int, [c_void_p, c_int64, c_int, c_float, c_float, c_int, c_int, c_uint64, c_uint32,
-                                c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+                                c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "dsk_argmax_ws_bytes": (c_size_t, [c_int]),
     "dsk_argmax_rows": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int, c_void_p, c_void_p, c_size_t, c_void_p]),
     "dsk_lens_add": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),

@@ -387,17 +387,17 @@ def accept_sample(p_logits: torch.Tensor, q_logits: torch.Tensor | None, draft: 
 def sample_rows(logits: torch.Tensor, temperature: float, top_p: float = 1.0, top_k: int = 0, *,
                 mul_inv_t: bool = False, seed: int = 0, offset: int = 0, row0: int = 0,
                 token_out=None, probs_out=None, offset_dev=None):
-    """logits [R, V] f32 -> tokens [R] (argmax at temperature 0) and the truncated probs."""
+    """logits [R, V] f32 -> tokens [R] (argmax at temperature 0) and, when probs_out [R, V] f32 is
+    given, the truncated distribution each row was drawn from."""
     R, V = logits.shape
     if temperature <= 0 and R <= 1024 and logits.dtype in (torch.float32, torch.bfloat16):
         return argmax_rows(logits, token_out=token_out), probs_out
     logits = logits.contiguous().float()
     token_out = torch.empty(R, dtype=torch.int32, device=logits.device) if token_out is None else token_out
-    if temperature > 0 and probs_out is None:
-        probs_out = torch.empty((R, V), dtype=torch.float32, device=logits.device)
+    buf = Workspace.get(logits.device).reserve("sample", _hip.lib.dsk_sample_ws_bytes(R, V))
     call("dsk_sample_rows", ptr(logits), V, R, float(temperature), float(top_p), int(top_k or 0),
          int(bool(mul_inv_t)), int(seed) & ((1 << 64) - 1), int(offset) & 0xFFFFFFFF, int(row0),
-         ptr(token_out), ptr(probs_out), ptr(offset_dev), stream_ptr())
+         ptr(token_out), ptr(probs_out), ptr(offset_dev), ptr(buf), buf.numel(), stream_ptr())
     return token_out, probs_out
 
 

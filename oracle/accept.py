@@ -12,6 +12,9 @@ Pinning:
   - oracle_expf against libm exp (ulp bound) over the softmax input range;
   - probs() against truncate_probs_ref() (float64 sort + cumsum, the reference's algorithm)
     on rows without near-ties at the nucleus boundary;
+  - the top-p target ceil(top_p * Z) against exact rational arithmetic, and the order-free
+    threshold rule the GPU uses (keep e >= max(k-th largest, nucleus cutoff of the untruncated
+    row)) against the sequential top-k-then-top-p of probs() on tie-heavy rows;
   - losslessness: the exact output distribution of one accept step (computed from the
     oracle's p and q) equals truncate(softmax(target / T)), and the statistical KAT of
     tests/test_generate_helpers.py:145-170 in the reference replays within 0.02;
@@ -40,6 +43,8 @@ def lib():
         L.oracle_expf.argtypes = [f32]
         L.oracle_expf.restype = f32
         L.oracle_probs.argtypes = [vp, i64, f32, i32, f32, i32, vp]
+        L.oracle_top_p_target.argtypes = [f32, u64]
+        L.oracle_top_p_target.restype = u64
         L.oracle_categorical.argtypes = [vp, i64, u32]
         L.oracle_categorical.restype = i64
         L.oracle_accept_sample.argtypes = [vp, vp, i64, i32, i32, vp, f32, f32, i32, i32, u64, u32,
@@ -70,6 +75,10 @@ def probs(logits: np.ndarray, T: float, top_p: float = 1.0, top_k: int = 0, mul_
     out = np.empty_like(logits)
     lib().oracle_probs(_p(logits), logits.size, T, int(mul_inv), top_p, int(top_k), _p(out))
     return out
+
+
+def top_p_target(top_p: float, Z: int) -> int:
+    return int(lib().oracle_top_p_target(float(top_p), int(Z)))
 
 
 def categorical(w: np.ndarray, word: int) -> int:

@@ -13,16 +13,22 @@
  *
  * The reference computes these with MLX float32 reductions and MLX's threefry RNG, neither
  * of which is available here. The engine fixes one canonical definition, implemented twice
- * (here, with sorting; on the GPU, with a radix select) and compared bit for bit:
+ * (here, with sorting and the reference's sequential truncation; on the GPU, with histograms
+ * and a candidate select) and compared bit for bit:
  *   - exp is dsk_expf below (Cody-Waite reduction by ln 2, Taylor polynomial to r^7,
  *     explicit fmaf, inputs below -86 flush to 0 so no subnormal is ever formed);
- *   - every probability sum is a fixed-point integer sum of fx(p) = floor(p * 2^44), so the
- *     result does not depend on summation order; a sum S converts back as
- *     (float)((double)S * 2^-44);
+ *   - a row's distribution is built on the unnormalised exponentials e_j = exp(y_j - max y)
+ *     with fixed-point masses w_j = fx(e_j) = floor(e_j * 2^44) and Z = sum w_j (integer
+ *     sums do not depend on summation order); softmax then truncation then renormalisation is
+ *     the same as truncating e and dividing by the kept mass, so the final probability of a
+ *     kept element is e_j / float(S * 2^-44) with S the kept mass;
+ *   - top-k keeps e_j >= the k-th largest e; top-p keeps an element while the mass strictly
+ *     before it (in descending order) is below TP = ceil(top_p * Z), an exact integer;
  *   - uniforms are Philox4x32-10 (Salmon et al., SC'11) words, u = (w >> 8) * 2^-24;
  *   - a categorical draw from weights w_j is the inverse CDF on the fixed-point masses:
  *     t = floor(u * sum fx(w)), pick the first j whose inclusive prefix exceeds t
- *     (uniform index floor(u * V) when every mass is zero).
+ *     (uniform index floor(u * V) when every mass is zero); the residual draw uses the
+ *     residual max(p - q, 0) itself (dividing it by its sum does not change the draw's law).
  * Compile with -ffp-contract=off: every fused multiply-add below is an explicit fmaf.
  */
 #include <math.h>
@@ -117,8 +123,32 @@ static int cmp_desc(const void* a, const void* b) {
   return (i < j) ? -1 : (i > j);
 }
 
-/* truncate(softmax(logits / T)) (or logits * (1/T) when mul_inv != 0) into out[V].
- * Returns nothing; out holds the final probabilities the accept test reads. */
+/* TP = ceil(top_p * Z) exactly: top_p = M * 2^E with an integer M < 2^24, so the product is
+ * an integer below 2^87 and the ceiling is a shift of a 128-bit sum. top_p <= 0 gives 0. */
+uint64_t oracle_top_p_target(float top_p, uint64_t Z) {
+  if (!(top_p > 0.0f)) return 0;
+  uint32_t bits;
+  memcpy(&bits, &top_p, 4);
+  const uint32_t ex = (bits >> 23) & 0xFFu;
+  uint64_t M = bits & 0x7FFFFFu;
+  int E;
+  if (ex == 0) {
+    E = -149;
+  } else {
+    M |= 0x800000u;
+    E = (int)ex - 150;
+  }
+  const unsigned __int128 P = (unsigned __int128)M * Z;
+  if (E >= 0) return (uint64_t)(P << E); /* top_p >= 2^23: never reached for top_p < 1 */
+  const int sh = -E;
+  if (sh >= 128) return P ? 1 : 0;
+  return (uint64_t)((P + (((unsigned __int128)1 << sh) - 1)) >> sh);
+}
+
+/* truncate(softmax(logits / T)) (or logits * (1/T) when mul_inv != 0) into out[V]: the final
+ * probabilities the accept test and the draws read. Follows sampling.py:18-44 step by step on
+ * the unnormalised exponentials: the k-th largest threshold, then the nucleus on the top-k
+ * zeroed (not renormalised) values, then the division by the kept mass. */
 void oracle_probs(const float* logits, int64_t V, float T, int mul_inv, float top_p, int top_k,
                   float* out) {
   const float inv_t = 1.0f / T;
@@ -134,47 +164,47 @@ void oracle_probs(const float* logits, int64_t V, float T, int mul_inv, float to
     out[j] = e;
     Z += fx(e);
   }
-  const float Zf = fx_to_float(Z);
-  for (int64_t j = 0; j < V; ++j) out[j] = out[j] / Zf;
-
   const int do_k = (top_k > 0 && (int64_t)top_k < V);
   const int do_p = (top_p < 1.0f);
-  if (!do_k && !do_p) return;
-
-  vi_t* s = (vi_t*)malloc(sizeof(vi_t) * (size_t)V);
-  if (do_k) {
-    for (int64_t j = 0; j < V; ++j) {
-      s[j].v = out[j];
-      s[j].i = j;
+  if (do_k || do_p) {
+    vi_t* s = (vi_t*)malloc(sizeof(vi_t) * (size_t)V);
+    if (do_k) {
+      for (int64_t j = 0; j < V; ++j) {
+        s[j].v = out[j];
+        s[j].i = j;
+      }
+      qsort(s, (size_t)V, sizeof(vi_t), cmp_desc);
+      float kth = s[top_k - 1].v;
+      for (int64_t j = 0; j < V; ++j)
+        if (!(out[j] >= kth)) out[j] = 0.0f;
     }
-    qsort(s, (size_t)V, sizeof(vi_t), cmp_desc);
-    float kth = s[top_k - 1].v;
-    for (int64_t j = 0; j < V; ++j)
-      if (!(out[j] >= kth)) out[j] = 0.0f;
+    if (do_p) {
+      const uint64_t TP = oracle_top_p_target(top_p, Z);
+      for (int64_t j = 0; j < V; ++j) {
+        s[j].v = out[j];
+        s[j].i = j;
+      }
+      qsort(s, (size_t)V, sizeof(vi_t), cmp_desc);
+      uint64_t before = 0;
+      float cutoff = INFINITY;
+      for (int64_t i = 0; i < V; ++i) {
+        if (before < TP) cutoff = s[i].v; /* in the nucleus: mass strictly before it < top_p */
+        else break;
+        before += fx(s[i].v);
+      }
+      for (int64_t j = 0; j < V; ++j)
+        if (!(out[j] >= cutoff)) out[j] = 0.0f;
+    }
+    free(s);
   }
-  if (do_p) {
-    for (int64_t j = 0; j < V; ++j) {
-      s[j].v = out[j];
-      s[j].i = j;
-    }
-    qsort(s, (size_t)V, sizeof(vi_t), cmp_desc);
-    const uint64_t TP = (uint64_t)floor((double)top_p * 0x1p44);
-    uint64_t before = 0;
-    float cutoff = INFINITY;
-    for (int64_t i = 0; i < V; ++i) {
-      if (before < TP) cutoff = s[i].v; /* in the nucleus: mass strictly before it < top_p */
-      else break;
-      before += fx(s[i].v);
-    }
-    for (int64_t j = 0; j < V; ++j)
-      if (!(out[j] >= cutoff)) out[j] = 0.0f;
-  }
-  free(s);
   uint64_t S = 0;
   for (int64_t j = 0; j < V; ++j) S += fx(out[j]);
-  float Sf = fx_to_float(S);
-  float den = Sf > 1e-12f ? Sf : 1e-12f;
-  for (int64_t j = 0; j < V; ++j) out[j] = out[j] / den;
+  if (S == 0) { /* an empty nucleus (top_p * Z rounds to 0): every probability is 0 */
+    for (int64_t j = 0; j < V; ++j) out[j] = 0.0f;
+    return;
+  }
+  const float Sf = fx_to_float(S);
+  for (int64_t j = 0; j < V; ++j) out[j] = out[j] / Sf;
 }
 
 /* inverse-CDF categorical draw on fixed-point masses of w[0..V) */
@@ -223,15 +253,10 @@ int oracle_accept_sample(const float* p_logits, const float* q_logits, int64_t V
         float ratio = pd / (qd > 1e-9f ? qd : 1e-9f);
         if (ratio > 1.0f) ratio = 1.0f;
         acc = u < ratio;
-        uint64_t R = 0;
         for (int64_t j = 0; j < V; ++j) {
           float t = p[j] - q[j];
           r[j] = t > 0.0f ? t : 0.0f;
-          R += fx(r[j]);
         }
-        float Rf = fx_to_float(R);
-        float den = Rf > 1e-9f ? Rf : 1e-9f;
-        for (int64_t j = 0; j < V; ++j) r[j] = r[j] / den;
         samp = (int)oracle_categorical(r, V, philox_word(seed, (uint32_t)i, (uint32_t)b, 1u, offset));
       } else {
         samp = (int)oracle_categorical(p, V, philox_word(seed, (uint32_t)i, (uint32_t)b, 1u, offset));

@@ -42,7 +42,10 @@ def test_size_queries_without_gpu():
     assert _hip.lib.dsk_w4_gemm_splits(65, 4096, 4096) == 0
     assert _hip.lib.dsk_argmax_ws_bytes(15) >= 4096 + 2 * 15 * 16 * 4
     assert _hip.lib.dsk_argmax_ws_bytes(0) == 0 and _hip.lib.dsk_argmax_ws_bytes(1025) == 0
-    assert _hip.lib.dsk_accept_ws_bytes(4, 17, 151936) > 4 * 17 * 2 * 151936 * 4
+    # sampled acceptance: one candidate key per vocabulary entry for each of the B * (2L + 1) rows
+    assert _hip.lib.dsk_accept_ws_bytes(4, 17, 151936) >= 4 * 33 * 151936 * 4
+    assert _hip.lib.dsk_sample_ws_bytes(15, 151936) >= 15 * 151936 * 4
+    assert _hip.lib.dsk_sample_ws_bytes(0, 151936) == 0
 
 
 def test_error_path_reports_message():

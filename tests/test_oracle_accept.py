@@ -1,8 +1,10 @@
 """CPU checks that pin the acceptance oracle (oracle/accept_oracle.c) to things other than
-itself: published Philox vectors, libm, the reference's float64 sort+cumsum truncation, the
-exact output distribution of speculative sampling, and brute force for greedy accept."""
+itself: published Philox vectors, libm, the reference's float64 sort+cumsum truncation, exact
+rational arithmetic for the top-p target, the exact output distribution of speculative
+sampling, and brute force for greedy accept and for the GPU's order-free threshold rule."""
 
 import math
+from fractions import Fraction
 
 import numpy as np
 import pytest
@@ -148,3 +150,55 @@ def test_accept_sample_all_accept_takes_bonus_from_last_row():
     res = A.accept_sample(p, p[:, :L], draft, 1.0, seed=9)
     assert res["n"][0] == L
     assert res["token"][0] == res["sample"][0, L]
+
+
+def test_top_p_target_is_the_exact_ceiling():
+    rng = np.random.default_rng(5)
+    for _ in range(3000):
+        top_p = np.float32(rng.uniform(0.0, 1.0))
+        Z = int(rng.integers(2**44, 2**62))
+        assert A.top_p_target(top_p, Z) == math.ceil(Fraction(float(top_p)) * Z)
+    assert A.top_p_target(0.0, 2**50) == 0 and A.top_p_target(-0.5, 2**50) == 0
+    assert A.top_p_target(1e-40, 2**44) == 1                       # subnormal top_p: keeps the top
+    assert A.top_p_target(0.5, 2**44 + 1) == 2**43 + 1              # ceiling, not floor
+    top = float(np.nextafter(np.float32(1.0), np.float32(0.0)))
+    Z = 2**61 + 12345
+    assert A.top_p_target(top, Z) == math.ceil(Fraction(top) * Z)
+
+
+def _fx(e):
+    return np.floor(np.asarray(e, np.float64) * 2.0**44).astype(np.int64)
+
+
+def _kept_by_max_rule(e, top_k, top_p):
+    """The GPU's rule: both thresholds from the untruncated row, keep e >= the larger one."""
+    V = e.size
+    w = _fx(e)
+    vals = np.sort(e)[::-1]
+    kth = float(vals[top_k - 1]) if 0 < top_k < V else 0.0
+    cut = 0.0
+    if top_p < 1.0:
+        TP = A.top_p_target(top_p, int(w.sum()))
+        if TP == 0:
+            return np.zeros(V, bool)
+        cands = [float(c) for c in np.unique(e)[::-1] if int(w[e >= c].sum()) >= TP]
+        cut = cands[0]
+    return e >= max(kth, cut)
+
+
+def test_order_free_threshold_rule_matches_sequential_truncation():
+    rng = np.random.default_rng(6)
+    checked = 0
+    for _ in range(3000):
+        V = int(rng.integers(2, 40))
+        logits = rng.integers(-4, 5, size=V).astype(np.float32) * np.float32(rng.choice([0.5, 1.0, 3.0]))
+        T = float(rng.choice([0.7, 1.0, 1.5]))
+        top_k = int(rng.integers(0, V + 2))
+        top_p = float(rng.choice([1.0, 0.0, rng.uniform(0.05, 1.0)]))
+        y = logits / np.float32(T)
+        e = np.array([A.expf(float(v - y.max())) for v in y], np.float32)
+        got = A.probs(logits, T, top_p, top_k) > 0
+        want = _kept_by_max_rule(e, top_k, top_p) & (e > 0)
+        assert np.array_equal(got, want), (logits, T, top_k, top_p)
+        checked += int(0 < top_k < V and top_p < 1.0)
+    assert checked > 500                    # both truncations together, many times
