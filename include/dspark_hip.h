@@ -269,7 +269,7 @@ int dsk_accept_greedy_static(const void* logits, int dtype, int64_t ldl, int B, 
  * p = truncate(softmax(p_logits / T)); q = truncate(softmax(q_logits / T)) or, when
  * q_mul_inv_t != 0, softmax(q_logits * (1/T)) (src/mlx_dspark/model.py:297, :304).
  * Canonical arithmetic (shared bit for bit with the CPU oracle): e_j = exp(y_j - max y) by
- * the library's own exp, masses floor(e_j * 2^44) summed as integers, top-k keeps e_j >= the
+ * the library's own exp, masses floor(e_j * 2^31) summed as integers, top-k keeps e_j >= the
  * k-th largest e, top-p keeps e_j >= the largest c whose mass at or above c reaches
  * ceil(top_p * Z), both keep e_j >= the larger threshold (the reference's top-k followed by
  * top-p on the zeroed values); a kept element's probability is e_j / (kept mass).

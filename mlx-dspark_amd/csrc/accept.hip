@@ -2,14 +2,14 @@
 // (min(1, p/q) with residual resampling) after temperature / top-k / top-p, plus the KV
 // rollback to the accepted length. One canonical arithmetic is shared with the CPU oracle
 // (oracle/accept_oracle.c) so decisions, sampled indices and rollback lengths are identical:
-//   - exp: dsk_expf (Cody-Waite reduction by ln 2 with a two-word constant, Taylor
+//   - exp: dsk_expf_le0 (Cody-Waite reduction by ln 2 with a two-word constant, Taylor
 //     polynomial to r^7 evaluated with explicit fmaf, inputs below -86 flush to zero);
-//   - a row's distribution lives on the unnormalised exponentials e_j = dsk_expf(y_j - max y)
-//     with fixed-point masses w_j = fx(e_j) = floor(e_j * 2^44) (integer sums: order-free);
+//   - a row's distribution lives on the unnormalised exponentials e_j = exp(y_j - max y)
+//     with fixed-point masses w_j = fx(e_j) = floor(e_j * 2^31) (integer sums: order-free);
 //   - top-k keeps e_j >= the k-th largest e; top-p keeps e_j >= the largest value c whose
 //     mass at or above it reaches TP = ceil(top_p * Z); both keep e_j >= max of the two
 //     thresholds (the reference's top-k followed by top-p on the zeroed values); the final
-//     probability of a kept element is e_j / float(S * 2^-44), S the kept mass;
+//     probability of a kept element is e_j / float(S * 2^-31), S the kept mass;
 //   - uniforms: Philox4x32-10 word 0, u = (w >> 8) * 2^-24;
 //   - categorical draws: inverse CDF over fixed-point masses, in index order.
 // Floating-point contraction is off in this file: every fma is written out.
@@ -36,13 +36,16 @@
 namespace dsk {
 
 // ----------------------------------------------------------------------------- math
-__device__ __forceinline__ float dsk_expf(float x) {
-  if (x < -86.0f) return 0.0f;
-  if (x != x) return x;
-  if (x > 88.7f) return __builtin_inff();
-  float t = x * 1.44269504f;
+// exp on x <= 0 (and NaN), the only arguments used here (x = y - max y), without branches:
+// Cody-Waite reduction by ln 2 with a two-word constant, Taylor polynomial to r^7 with explicit
+// fmaf, arguments below -86 flush to 0 (the polynomial runs on the clamped argument, so the
+// scale factor 2^k stays a normal number); the oracle's oracle_expf on the same inputs.
+__device__ __forceinline__ float dsk_expf_le0(float x) {
+  const bool under = x < -86.0f;
+  const float xc = under ? -86.0f : x;
+  float t = xc * 1.44269504f;
   float k = rintf(t);
-  float r = __builtin_fmaf(-k, 0.693145751953125f, x);
+  float r = __builtin_fmaf(-k, 0.693145751953125f, xc);
   r = __builtin_fmaf(-k, 1.428606765330187e-06f, r);
   float p = 1.98412698e-4f;
   p = __builtin_fmaf(p, r, 1.38888889e-3f);
@@ -52,16 +55,14 @@ __device__ __forceinline__ float dsk_expf(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  int ki = (int)k;
-  if (ki > 127) {
-    p = p * 0x1p127f;
-    ki -= 127;
-  }
-  return p * bits_f32((uint32_t)(ki + 127) << 23);
+  const float v = p * bits_f32((uint32_t)((int)k + 127) << 23);
+  return under ? 0.0f : v;
 }
 
-__device__ __forceinline__ uint64_t fx(float p) { return (uint64_t)(p * 0x1p44f); }
-__device__ __forceinline__ float fx_to_float(uint64_t s) { return (float)((double)s * 0x1p-44); }
+// p in [0, 1] (every mass here: e, p' and residuals are at most 1): p * 2^31 fits a u32 and the
+// conversion truncates, i.e. floors
+__device__ __forceinline__ uint64_t fx(float p) { return (uint64_t)(uint32_t)(p * 0x1p31f); }
+__device__ __forceinline__ float fx_to_float(uint64_t s) { return (float)((double)s * 0x1p-31); }
 
 __device__ __forceinline__ uint32_t philox_word(uint64_t seed, uint32_t c0, uint32_t c1, uint32_t c2,
                                                 uint32_t c3) {
@@ -290,27 +291,33 @@ __global__ __launch_bounds__(64) void argmax_merge_kernel(int64_t V, const float
 // ============================================================================= sampled paths
 constexpr int kST = 512;              // threads per workgroup
 constexpr int kSW = kST / 64;
-constexpr int kMaxSlices = 32;        // workgroups per row
+constexpr int kMaxSlices = 32;        // workgroups per row in the row passes
 constexpr int kEPT = 32;              // elements per thread in the gather pass: slice <= 16384
+constexpr int kMaxDrawSlices = 128;   // workgroups per draw in the draw passes (<= kST)
+constexpr int kDrawEPT = 8;           // elements per thread in the draw pass: draw slice <= 4096
+constexpr int kHistCopies = 8;        // lane-striped copies of the stats pass's LDS histogram
+constexpr int kFinCap = 10240;        // candidate keys the finishing pass stages in LDS
 constexpr int64_t kMaxSlice = (int64_t)kST * kEPT;
 constexpr int kL1 = 512;              // first-level buckets: key >> 21 (e <= 1 keeps it <= 508)
 constexpr int kL1Shift = 21;
 constexpr uint32_t kNone = 0xFFFFFFFFu;
 static_assert(kST == kL1, "the merged-histogram scan gives each thread one first-level bucket");
 
-struct RowInfo {        // the threshold buckets of one row (gather pass, slice 0)
+struct RowInfo {        // the threshold buckets of one row (selection pass)
   uint32_t bk, bp;      // top-k bucket (by count), top-p bucket (by mass); kNone when inactive
   uint32_t above_k;     // elements in buckets above bk
   uint32_t pad;
   uint64_t wabove_k;    // mass in buckets above bk
   uint64_t wabove_p;    // mass in buckets above bp
   uint64_t tp;          // ceil(top_p * Z)
+  float wlo, whi;       // window of x = y - m holding both buckets' elements
+  float vlo, vhi;       // the same window on raw values (used when T == 1)
 };
 
 struct RowParam {       // one row's final distribution: p'_j = key(e_j) >= thr ? e_j / sf : 0
   float m;              // max of y over the row
   uint32_t thr;         // 0 keeps every element, kNone keeps none
-  float sf;             // float(S * 2^-44), S the kept mass
+  float sf;             // float(S * 2^-31), S the kept mass
   uint32_t pad;
 };
 
@@ -320,11 +327,14 @@ struct SampArgs {
   const float* q;
   int64_t V;
   int Rp, Rq;
-  int S;                // slices per row
+  int S;                // slices per row (row passes)
   int64_t slen;         // slice length (multiple of 4)
+  int Sd;               // slices per draw (draw passes)
+  int64_t slen_d;       // draw slice length (multiple of 4, at most kST * kDrawEPT)
   float T, top_p;
   int top_k, p_mul, q_mul;
   int do_k, do_p;
+  int vec;              // rows 16-byte aligned, V % 4 == 0: float4 loads
   // acceptance (mode 0): positions (b, i), i <= L; p row b*(L+1)+i, q row Rp + b*L + i
   int mode;             // 0 acceptance, 1 row sampling
   int B, L;
@@ -351,7 +361,7 @@ struct SampArgs {
   RowInfo* info;        // [rows]
   RowParam* prm;        // [rows]
   int32_t* acc;         // [B][L] accept flags
-  uint64_t* wsum;       // [draws][kMaxSlices]
+  uint64_t* wsum;       // [draws][kMaxDrawSlices]
   uint32_t* cand;       // [rows][V]
 };
 
@@ -359,7 +369,16 @@ __device__ __forceinline__ const float* samp_row(const SampArgs& a, int r) {
   return r < a.Rp ? a.p + (int64_t)r * a.V : a.q + (int64_t)(r - a.Rp) * a.V;
 }
 __device__ __forceinline__ int samp_mul(const SampArgs& a, int r) { return r < a.Rp ? a.p_mul : a.q_mul; }
-__device__ __forceinline__ float yval(float x, int mul, float T, float inv_t) { return mul ? x * inv_t : x / T; }
+__device__ __forceinline__ float yval(float x, int mul, float T, float inv_t) {
+  if (T == 1.0f) return x;  // x / 1 == x * (1 / 1) == x exactly
+  return mul ? x * inv_t : x / T;
+}
+// the row passes are instantiated for T == 1 (TONE: y = x) and for any T
+template <bool TONE>
+__device__ __forceinline__ float yv(float x, int mul, float T, float inv_t) {
+  if constexpr (TONE) return x;
+  else return mul ? x * inv_t : x / T;
+}
 __device__ __forceinline__ uint32_t samp_offset(const SampArgs& a) { return a.offset_dev ? a.offset_dev[0] : a.offset; }
 
 __device__ __forceinline__ float row_max(const SampArgs& a, int r) {
@@ -370,39 +389,41 @@ __device__ __forceinline__ float row_max(const SampArgs& a, int r) {
 
 // final probability of element j of a row with parameters rp
 __device__ __forceinline__ float final_prob(const RowParam& rp, float x, int mul, float T, float inv_t) {
-  const float e = dsk_expf(yval(x, mul, T, inv_t) - rp.m);
+  const float e = dsk_expf_le0(yval(x, mul, T, inv_t) - rp.m);
   return f32_bits(e) >= rp.thr && rp.thr != kNone ? e / rp.sf : 0.0f;
 }
 
-// Visits the slice [lo, hi) of row x: f(j, x_j) for this thread's elements, four 16-byte loads
-// in flight per thread when VEC (16-byte aligned rows, lo a multiple of 4).
-template <bool VEC, typename F>
-__device__ __forceinline__ void for_slice(const float* __restrict__ x, int64_t lo, int64_t hi, F f) {
-  if constexpr (VEC) {
-    constexpr int UN = 4;
-    const int64_t n4 = (hi - lo) / 4;
-    const f32x4* x4 = reinterpret_cast<const f32x4*>(x + lo);
-    for (int64_t c0 = threadIdx.x; c0 < n4; c0 += kST * UN) {
-      f32x4 v[UN];
+// A thread's share of a row slice [lo, hi) (at most kST * kEPT elements), loaded into registers
+// with every load issued at once: VEC (16-byte aligned rows, lo and hi multiples of 4) as float4
+// c = tid + i * kST, else element j = lo + tid + i * kST.
+template <bool VEC>
+struct SliceRegs {
+  float v[kEPT];
+  __device__ __forceinline__ void load(const float* __restrict__ x, int64_t lo, int64_t hi) {
+    if constexpr (VEC) {
+      const f32x4* x4 = reinterpret_cast<const f32x4*>(x + lo);
 #pragma unroll
-      for (int u = 0; u < UN; ++u)
-        if (c0 + u * kST < n4) v[u] = x4[c0 + u * kST];
+      for (int i = 0; i < kEPT / 4; ++i) {
+        const int64_t c = (int64_t)i * kST + threadIdx.x;
+        f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (lo + 4 * c < hi) t = x4[c];
 #pragma unroll
-      for (int u = 0; u < UN; ++u) {
-        const int64_t c = c0 + u * kST;
-        if (c < n4) {
-          const int64_t j = lo + 4 * c;
-          f(j, v[u][0]);
-          f(j + 1, v[u][1]);
-          f(j + 2, v[u][2]);
-          f(j + 3, v[u][3]);
-        }
+        for (int e = 0; e < 4; ++e) v[4 * i + e] = t[e];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kEPT; ++i) {
+        const int64_t j = lo + (int64_t)i * kST + threadIdx.x;
+        v[i] = j < hi ? x[j] : 0.0f;
       }
     }
-    lo += 4 * n4;
   }
-  for (int64_t j = lo + threadIdx.x; j < hi; j += kST) f(j, x[j]);
-}
+  // element k of this thread lies in the slice (n = hi - lo; a float4 is whole or absent)
+  __device__ __forceinline__ static bool valid(int k, int n) {
+    if constexpr (VEC) return 4 * ((k / 4) * kST + (int)threadIdx.x) < n;
+    else return k * kST + (int)threadIdx.x < n;
+  }
+};
 
 __device__ float block_max512(float v, float* sh) {
   v = wave_max(v);
@@ -446,7 +467,7 @@ __device__ uint64_t block_scan512(uint64_t v, uint64_t* sh, uint64_t& total) {
 }
 
 // ---- pass 1: slice maxima of y; slice 0 clears the row's merged accumulators
-template <bool VEC>
+template <bool VEC, bool TONE>
 __global__ __launch_bounds__(kST) void samp_max_kernel(SampArgs a) {
   __shared__ float sh[kSW];
   const int r = blockIdx.x / a.S, s = blockIdx.x % a.S;
@@ -454,8 +475,13 @@ __global__ __launch_bounds__(kST) void samp_max_kernel(SampArgs a) {
   const int mul = samp_mul(a, r);
   const float T = a.T, inv_t = 1.0f / T;
   const int64_t lo = min(a.V, (int64_t)s * a.slen), hi = min(a.V, lo + a.slen);
+  SliceRegs<VEC> xr;
+  xr.load(x, lo, hi);
   float m = -__builtin_inff();
-  for_slice<VEC>(x, lo, hi, [&](int64_t, float v) { m = fmaxf(m, yval(v, mul, T, inv_t)); });
+  const int n = (int)(hi - lo);
+#pragma unroll
+  for (int k = 0; k < kEPT; ++k)
+    if (xr.valid(k, n)) m = fmaxf(m, yv<TONE>(xr.v[k], mul, T, inv_t));
   m = block_max512(m, sh);
   if (threadIdx.x == 0) a.gmax[r * kMaxSlices + s] = m;
   if (s == 0) {
@@ -470,61 +496,88 @@ __global__ __launch_bounds__(kST) void samp_max_kernel(SampArgs a) {
   }
 }
 
-// ---- pass 2: Z and the first-level histogram, merged per row by integer atomics
-template <bool VEC>
+// ---- pass 2: Z and the first-level histogram, merged per row by integer atomics. Lanes
+// spread their LDS atomics over kHistCopies copies (copy = lane % kHistCopies) so lanes of one
+// wave that hit the same bucket mostly hit different addresses.
+template <bool VEC, bool TONE>
 __global__ __launch_bounds__(kST) void samp_stats_kernel(SampArgs a) {
-  __shared__ uint32_t hc[kL1];
-  __shared__ unsigned long long hw[kL1];
+  __shared__ uint32_t hc[kHistCopies][kL1 + 1];  // +1: copies start in different LDS banks
+  __shared__ unsigned long long hw[kHistCopies][kL1 + 1];
   __shared__ uint64_t sh[kSW];
   const int r = blockIdx.x / a.S, s = blockIdx.x % a.S;
   const bool trunc = a.do_k || a.do_p;
   const float* x = samp_row(a, r);
   const int mul = samp_mul(a, r);
   const float T = a.T, inv_t = 1.0f / T;
+  const int64_t lo = min(a.V, (int64_t)s * a.slen), hi = min(a.V, lo + a.slen);
+  SliceRegs<VEC> xr;
+  xr.load(x, lo, hi);  // in flight while the row max is read and the histogram cleared
   const float m = row_max(a, r);
+  uint32_t* hcp = hc[threadIdx.x % kHistCopies];
+  unsigned long long* hwp = hw[threadIdx.x % kHistCopies];
   if (trunc) {
-    for (int b = threadIdx.x; b < kL1; b += kST) {
-      hc[b] = 0;
-      hw[b] = 0;
+    for (int b = threadIdx.x; b < kHistCopies * (kL1 + 1); b += kST) {
+      hc[b / (kL1 + 1)][b % (kL1 + 1)] = 0;
+      hw[b / (kL1 + 1)][b % (kL1 + 1)] = 0;
     }
     __syncthreads();
   }
-  const int64_t lo = min(a.V, (int64_t)s * a.slen), hi = min(a.V, lo + a.slen);
   uint64_t z = 0;
-  for_slice<VEC>(x, lo, hi, [&](int64_t, float v) {
-    const float e = dsk_expf(yval(v, mul, T, inv_t) - m);
+  const int n = (int)(hi - lo);
+#pragma unroll
+  for (int k = 0; k < kEPT; ++k) {
+    if (!xr.valid(k, n)) continue;
+    const float e = dsk_expf_le0(yv<TONE>(xr.v[k], mul, T, inv_t) - m);
     const uint64_t w = fx(e);
     z += w;
     if (trunc) {
       const uint32_t b = min(f32_bits(e) >> kL1Shift, (uint32_t)kL1 - 1);  // NaN stays in bounds
-      atomicAdd(&hc[b], 1u);
-      if (w) atomicAdd(&hw[b], (unsigned long long)w);
+      if (a.do_k) atomicAdd(hcp + b, 1u);
+      if (w) atomicAdd(hwp + b, (unsigned long long)w);
     }
-  });
+  }
   z = block_sum512(z, sh);
   if (threadIdx.x == 0) atomicAdd((unsigned long long*)&a.zsum[r], (unsigned long long)z);
   if (trunc) {
     __syncthreads();
     for (int b = threadIdx.x; b < kL1; b += kST) {
-      if (hc[b]) atomicAdd(&a.hcnt[r * kL1 + b], hc[b]);
-      if (hw[b]) atomicAdd((unsigned long long*)&a.hwgt[r * kL1 + b], hw[b]);
+      uint32_t c = 0;
+      unsigned long long w = 0;
+#pragma unroll
+      for (int k = 0; k < kHistCopies; ++k) {
+        c += hc[k][b];
+        w += hw[k][b];
+      }
+      if (c) atomicAdd(&a.hcnt[r * kL1 + b], c);
+      if (w) atomicAdd((unsigned long long*)&a.hwgt[r * kL1 + b], w);
     }
   }
 }
 
-// ---- pass 3 (truncation): threshold buckets, then the candidates in them
-__global__ __launch_bounds__(kST) void samp_gather_kernel(SampArgs a) {
+// A window of x = y - m that holds every element whose e lands in first-level bucket b (empty
+// for kNone): exp here is within 2 ulp of the true exp (a CPU test of the oracle's copy checks
+// this), so a 1e-3 margin on the logarithms of the bucket's bounds is far wider than needed.
+// The lowest buckets (e below 2^-122, where the flush to 0 lives) keep no upper bound.
+__device__ inline void bucket_window(uint32_t b, float& lo, float& hi) {
+  if (b == kNone) {
+    lo = __builtin_inff();
+    hi = -__builtin_inff();
+    return;
+  }
+  lo = b == 0 ? -__builtin_inff() : logf(bits_f32(b << kL1Shift)) - 1e-3f;
+  hi = b <= 8 ? __builtin_inff() : logf(bits_f32((b + 1) << kL1Shift)) + 1e-3f;
+}
+
+// ---- pass 3a (truncation), one workgroup per row: the threshold buckets from the merged
+// histogram (buckets scanned in descending order, thread t holding bucket kL1 - 1 - t), the
+// mass and count above them, and the window of x = y - m the gather stages.
+__global__ __launch_bounds__(kST) void samp_select_kernel(SampArgs a) {
   __shared__ uint64_t sh[kSW];
   __shared__ uint32_t sel[4];
   __shared__ uint64_t selw[2];
-  __shared__ uint32_t base[2];
-  const int r = blockIdx.x / a.S, s = blockIdx.x % a.S;
-  const float* x = samp_row(a, r);
-  const int mul = samp_mul(a, r);
-  const float T = a.T, inv_t = 1.0f / T;
+  const int r = blockIdx.x;
   const uint64_t Z = a.zsum[r];
   const uint64_t TP = a.do_p ? top_p_target(a.top_p, Z) : 0;
-  // merged histogram, buckets in descending order: thread t holds bucket kL1 - 1 - t
   const int bb = kL1 - 1 - (int)threadIdx.x;
   const uint64_t c = a.hcnt[r * kL1 + bb];
   const uint64_t w = a.hwgt[r * kL1 + bb];
@@ -545,34 +598,79 @@ __global__ __launch_bounds__(kST) void samp_gather_kernel(SampArgs a) {
     selw[1] = iw - w;
   }
   __syncthreads();
-  const uint32_t bk = sel[0], bp = sel[1];
-  if (s == 0 && threadIdx.x == 0) {
-    RowInfo inf;
-    inf.bk = bk;
-    inf.bp = bp;
-    inf.above_k = bk == kNone ? 0 : sel[2];
-    inf.pad = 0;
-    inf.wabove_k = bk == kNone ? 0 : selw[0];
-    inf.wabove_p = bp == kNone ? 0 : selw[1];
-    inf.tp = TP;
-    a.info[r] = inf;
-  }
-  const uint32_t bq = (bp == bk) ? kNone : bp;  // one list when both thresholds share a bucket
-  if (bk == kNone && bq == kNone) return;
-  // this thread's elements, keys kept in registers
+  if (threadIdx.x != 0) return;
+  RowInfo inf;
+  inf.bk = sel[0];
+  inf.bp = sel[1];
+  inf.above_k = inf.bk == kNone ? 0 : sel[2];
+  inf.pad = 0;
+  inf.wabove_k = inf.bk == kNone ? 0 : selw[0];
+  inf.wabove_p = inf.bp == kNone ? 0 : selw[1];
+  inf.tp = TP;
+  const uint32_t bq = (inf.bp == inf.bk) ? kNone : inf.bp;
+  float klo, khi, qlo, qhi;
+  bucket_window(inf.bk, klo, khi);
+  bucket_window(bq, qlo, qhi);
+  inf.wlo = fminf(klo, qlo);
+  inf.whi = fmaxf(khi, qhi);
+  // with T == 1 the window moves to the raw values (y = v): v - m in [wlo, whi] holds for every
+  // v in [m + wlo, m + whi] widened by one part in 2^20 of the bounds' magnitudes
   const float m = row_max(a, r);
+  inf.vlo = (m + inf.wlo) - fabsf(m + inf.wlo) * 0x1p-20f - 0x1p-100f;
+  inf.vhi = (m + inf.whi) + fabsf(m + inf.whi) * 0x1p-20f + 0x1p-100f;
+  a.info[r] = inf;
+}
+
+// ---- pass 3b (truncation): the candidates of the threshold buckets. A cheap window test
+// stages each wave's window elements in LDS by ballot; the exact keys of the staged elements are
+// then computed densely, so exp never runs divergently.
+template <bool VEC, bool TONE>
+__global__ __launch_bounds__(kST) void samp_gather_kernel(SampArgs a) {
+  __shared__ uint64_t sh[kSW];
+  __shared__ uint32_t base[2];
+  __shared__ uint32_t xs[kSW][64 * kEPT];  // per wave: staged x bits, then their keys
+  const int r = blockIdx.x / a.S, s = blockIdx.x % a.S;
+  const float* x = samp_row(a, r);
+  const int mul = samp_mul(a, r);
+  const float T = a.T, inv_t = 1.0f / T;
   const int64_t lo = min(a.V, (int64_t)s * a.slen), hi = min(a.V, lo + a.slen);
-  uint32_t keys[kEPT];
-  uint32_t nk = 0, np = 0;
+  const int n = (int)(hi - lo);
+  SliceRegs<VEC> xr;
+  xr.load(x, lo, hi);
+  const RowInfo inf = a.info[r];
+  const float m = row_max(a, r);
+  const uint32_t bk = inf.bk, bq = (inf.bp == inf.bk) ? kNone : inf.bp;
+  if (bk == kNone && bq == kNone) return;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  uint32_t* xw = xs[wv];
+  uint32_t cnt = 0;  // elements this wave staged (wave-uniform)
 #pragma unroll
-  for (int i = 0; i < kEPT; ++i) {
-    const int64_t j = lo + (int64_t)i * kST + threadIdx.x;
-    uint32_t key = kNone;
-    if (j < hi) key = f32_bits(dsk_expf(yval(x[j], mul, T, inv_t) - m));
-    keys[i] = key;
+  for (int k = 0; k < kEPT; ++k) {  // every lane of the wave takes part in each ballot
+    const float v = xr.v[k];
+    bool inw;
+    if constexpr (TONE) inw = v >= inf.vlo && v <= inf.vhi;
+    else {
+      const float xx = yv<TONE>(v, mul, T, inv_t) - m;
+      inw = xx >= inf.wlo && xx <= inf.whi;
+    }
+    inw = inw && xr.valid(k, n);
+    const uint64_t bal = __ballot(inw);
+    if (bal) {
+      if (inw) xw[cnt + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u))] =
+          f32_bits(yv<TONE>(v, mul, T, inv_t) - m);
+      cnt += (uint32_t)__popcll(bal);
+    }
+  }
+  // exact keys of the staged elements (a wave reads only its own staging area)
+  __syncthreads();
+  uint32_t nk = 0, np = 0;
+  for (uint32_t k = lane; k < cnt; k += 64) {
+    const uint32_t key = f32_bits(dsk_expf_le0(bits_f32(xw[k])));
     const uint32_t b = key >> kL1Shift;
-    nk += (key != kNone && b == bk);
-    np += (key != kNone && b == bq);
+    const uint32_t kept = (b == bk || b == bq) ? key : kNone;
+    xw[k] = kept;
+    nk += (kept != kNone && b == bk);
+    np += (kept != kNone && b == bq);
   }
   uint64_t totk, totp;
   const uint64_t offk = block_scan512(nk, sh, totk) - nk;
@@ -584,30 +682,28 @@ __global__ __launch_bounds__(kST) void samp_gather_kernel(SampArgs a) {
   __syncthreads();
   uint32_t* ck = a.cand + (int64_t)r * a.V;
   uint32_t pk = base[0] + (uint32_t)offk, pp = base[1] + (uint32_t)offp;
-#pragma unroll
-  for (int i = 0; i < kEPT; ++i) {
-    const uint32_t key = keys[i];
+  for (uint32_t k = lane; k < cnt; k += 64) {
+    const uint32_t key = xw[k];
     if (key == kNone) continue;
-    const uint32_t b = key >> kL1Shift;
-    if (b == bk) ck[pk++] = key;
-    else if (b == bq) ck[a.V - 1 - (pp++)] = key;
+    if ((key >> kL1Shift) == bk) ck[pk++] = key;
+    else ck[a.V - 1 - (pp++)] = key;
   }
 }
 
-// ---- pass 4: exact thresholds from the candidates, the kept mass, the accept test
+// ---- pass 4: per row, the exact thresholds from the candidates and the kept mass
 struct FinSmem {
   unsigned long long hist[2048];
+  uint32_t keys[kFinCap];
   uint64_t sh[kSW];
   uint32_t bc32;
   uint64_t bc64;
-  RowParam rp[2];
 };
 
 // Key K among the n candidate keys (all in first-level bucket `bucket`) with
 // weight(> K) < target <= weight(>= K), weight 1 per key (count) or fx(value) (mass); two
 // radix levels over the key's low 21 bits (11 then 10 bits).
-__device__ uint32_t select_key(const uint32_t* __restrict__ cand, uint32_t n, bool mass, uint64_t target,
-                               uint32_t bucket, FinSmem& sm) {
+__device__ uint32_t select_key(const uint32_t* cand, uint32_t n, bool mass, uint64_t target, uint32_t bucket,
+                               FinSmem& sm) {
   uint32_t prefix = bucket << kL1Shift;
   uint64_t above = 0;
   const int shifts[2] = {10, 0};
@@ -656,7 +752,7 @@ __device__ uint32_t select_key(const uint32_t* __restrict__ cand, uint32_t n, bo
   return prefix;
 }
 
-__device__ uint64_t mass_at_or_above(const uint32_t* __restrict__ cand, uint32_t n, uint32_t K, FinSmem& sm) {
+__device__ uint64_t mass_at_or_above(const uint32_t* cand, uint32_t n, uint32_t K, FinSmem& sm) {
   uint64_t t = 0;
   for (uint32_t c = threadIdx.x; c < n; c += kST) {
     const uint32_t key = cand[c];
@@ -665,7 +761,9 @@ __device__ uint64_t mass_at_or_above(const uint32_t* __restrict__ cand, uint32_t
   return block_sum512(t, sm.sh);
 }
 
-__device__ RowParam finish_row(const SampArgs& a, int r, FinSmem& sm) {
+__global__ __launch_bounds__(kST) void samp_finish_kernel(SampArgs a) {
+  __shared__ FinSmem sm;
+  const int r = blockIdx.x;
   RowParam rp;
   rp.m = row_max(a, r);
   rp.pad = 0;
@@ -673,68 +771,63 @@ __device__ RowParam finish_row(const SampArgs& a, int r, FinSmem& sm) {
   if (!a.do_k && !a.do_p) {
     rp.thr = 0;
     rp.sf = fx_to_float(Z);
-    return rp;
-  }
-  const RowInfo inf = a.info[r];
-  if (a.do_p && inf.tp == 0) {  // empty nucleus
+  } else if (a.do_p && a.info[r].tp == 0) {  // empty nucleus
     rp.thr = kNone;
     rp.sf = 0.0f;
-    return rp;
+  } else {
+    const RowInfo inf = a.info[r];
+    const uint32_t* gk = a.cand + (int64_t)r * a.V;
+    const uint32_t nk = a.ccnt[r * 2];
+    const bool shared = inf.bp == inf.bk;
+    const uint32_t np = shared ? nk : a.ccnt[r * 2 + 1];
+    const uint32_t* gp = shared ? gk : gk + (a.V - np);
+    // stage both lists in LDS when they fit (one read of the candidates), else read them in place
+    const uint32_t* ck = gk;
+    const uint32_t* cq = gp;
+    if ((uint64_t)nk + (shared ? 0 : np) <= (uint64_t)kFinCap) {
+      for (uint32_t c = threadIdx.x; c < nk; c += kST) sm.keys[c] = gk[c];
+      if (!shared)
+        for (uint32_t c = threadIdx.x; c < np; c += kST) sm.keys[nk + c] = gp[c];
+      __syncthreads();
+      ck = sm.keys;
+      cq = shared ? sm.keys : sm.keys + nk;
+    }
+    uint32_t kth = 0, cut = 0;
+    if (a.do_k && inf.bk != kNone) kth = select_key(ck, nk, false, (uint64_t)a.top_k - inf.above_k, inf.bk, sm);
+    if (a.do_p && inf.bp != kNone) cut = select_key(cq, np, true, inf.tp - inf.wabove_p, inf.bp, sm);
+    uint64_t S;
+    if (a.do_p && inf.bp != kNone && cut >= kth) {
+      rp.thr = cut;
+      S = inf.wabove_p + mass_at_or_above(cq, np, cut, sm);
+    } else if (a.do_k && inf.bk != kNone) {
+      rp.thr = kth;
+      S = inf.wabove_k + mass_at_or_above(ck, nk, kth, sm);
+    } else {  // unreachable: an active threshold always finds its bucket
+      rp.thr = 0;
+      S = Z;
+    }
+    rp.sf = fx_to_float(S);
   }
-  const uint32_t* ck = a.cand + (int64_t)r * a.V;
-  const uint32_t nk = a.ccnt[r * 2];
-  const bool shared = inf.bp == inf.bk;
-  const uint32_t np = shared ? nk : a.ccnt[r * 2 + 1];
-  const uint32_t* cp = shared ? ck : ck + (a.V - np);
-  uint32_t kth = 0, cut = 0;
-  if (a.do_k && inf.bk != kNone) kth = select_key(ck, nk, false, (uint64_t)a.top_k - inf.above_k, inf.bk, sm);
-  if (a.do_p && inf.bp != kNone) cut = select_key(cp, np, true, inf.tp - inf.wabove_p, inf.bp, sm);
-  uint64_t S;
-  if (a.do_p && inf.bp != kNone && cut >= kth) {
-    rp.thr = cut;
-    S = inf.wabove_p + mass_at_or_above(cp, np, cut, sm);
-  } else if (a.do_k && inf.bk != kNone) {
-    rp.thr = kth;
-    S = inf.wabove_k + mass_at_or_above(ck, nk, kth, sm);
-  } else {  // unreachable: an active threshold always finds its bucket
-    rp.thr = 0;
-    S = Z;
-  }
-  rp.sf = fx_to_float(S);
-  return rp;
+  if (threadIdx.x == 0) a.prm[r] = rp;
 }
 
-__global__ __launch_bounds__(kST) void samp_finish_kernel(SampArgs a) {
-  __shared__ FinSmem sm;
-  const int unit = blockIdx.x;
-  int rp_row, rq_row = -1, b = 0, i = 0;
-  if (a.mode == 0) {
-    b = unit / (a.L + 1);
-    i = unit % (a.L + 1);
-    rp_row = b * (a.L + 1) + i;
-    if (i < a.L && a.Rq) rq_row = a.Rp + b * a.L + i;
-  } else {
-    rp_row = unit;
-  }
-  const RowParam pp = finish_row(a, rp_row, sm);
-  if (threadIdx.x == 0) a.prm[rp_row] = pp;
-  RowParam qp = pp;
-  if (rq_row >= 0) {
-    __syncthreads();
-    qp = finish_row(a, rq_row, sm);
-    if (threadIdx.x == 0) a.prm[rq_row] = qp;
-  }
-  if (a.mode != 0 || i >= a.L || threadIdx.x != 0) return;
-  // accept test of the drafted token at position i; a draft id outside [0, V) is rejected
+// accept test of the drafted token at position i of batch row b (a draft id outside [0, V) is
+// rejected): u < min(1, p'(d) / max(q'(d), 1e-9)), q' = 1 for one-hot drafts
+__device__ int accept_test(const SampArgs& a, int b, int i, uint32_t off) {
   const float T = a.T, inv_t = 1.0f / T;
   const int32_t d = a.draft[(int64_t)b * a.L + i];
   const bool dvalid = d >= 0 && (int64_t)d < a.V;
-  const float pd = dvalid ? final_prob(pp, samp_row(a, rp_row)[d], a.p_mul, T, inv_t) : 0.0f;
-  const float qd = (!dvalid || rq_row < 0) ? 1.0f : final_prob(qp, samp_row(a, rq_row)[d], a.q_mul, T, inv_t);
-  const float u = u24_to_float(philox_word(a.seed, (uint32_t)i, (uint32_t)b, 0u, samp_offset(a)));
+  const int prow = b * (a.L + 1) + i;
+  const float pd = dvalid ? final_prob(a.prm[prow], samp_row(a, prow)[d], a.p_mul, T, inv_t) : 0.0f;
+  float qd = 1.0f;
+  if (dvalid && a.Rq) {
+    const int qrow = a.Rp + b * a.L + i;
+    qd = final_prob(a.prm[qrow], samp_row(a, qrow)[d], a.q_mul, T, inv_t);
+  }
+  const float u = u24_to_float(philox_word(a.seed, (uint32_t)i, (uint32_t)b, 0u, off));
   float ratio = pd / (qd > 1e-9f ? qd : 1e-9f);
   if (ratio > 1.0f) ratio = 1.0f;
-  a.acc[(int64_t)b * a.L + i] = u < ratio;
+  return u < ratio;
 }
 
 // ---- the distribution one draw uses
@@ -757,19 +850,18 @@ __device__ __forceinline__ uint64_t draw_weight(const DrawSpec& ds, int64_t j, f
   return fx(t > 0.0f ? t : 0.0f);
 }
 
-__device__ DrawSpec draw_spec(const SampArgs& a, int unit) {
+// The draw of `unit` (acceptance: batch row b, or (b, position) when every position draws; row
+// sampling: row r); n is batch row b's accepted count (acceptance).
+__device__ DrawSpec draw_spec(const SampArgs& a, int unit, int n) {
   DrawSpec ds;
   ds.qrow = -1;
   ds.d = -1;
-  ds.n = 0;
+  ds.n = n;
   ds.b = 0;
   ds.pos = 0;
   const uint32_t off = samp_offset(a);
   if (a.mode == 0) {
     ds.b = a.all_pos ? unit / (a.L + 1) : unit;
-    int n = 0;
-    while (n < a.L && a.acc[(int64_t)ds.b * a.L + n]) ++n;
-    ds.n = n;
     ds.pos = a.all_pos ? unit % (a.L + 1) : n;
     ds.prow = ds.b * (a.L + 1) + ds.pos;
     if (ds.pos < a.L) {
@@ -796,91 +888,124 @@ __device__ DrawSpec draw_spec(const SampArgs& a, int unit) {
   return ds;
 }
 
-// ---- pass 5: per-slice mass of each draw's distribution (row sampling also stores p')
-template <bool VEC>
+// ---- pass 5: the accept tests (every workgroup of a batch row repeats them; slice 0 stores
+// them), then the per-slice mass of each draw's distribution (row sampling also stores p')
 __global__ __launch_bounds__(kST) void samp_wsum_kernel(SampArgs a) {
   __shared__ uint64_t sh[kSW];
-  const int unit = blockIdx.x / a.S, s = blockIdx.x % a.S;
-  const DrawSpec ds = draw_spec(a, unit);
+  __shared__ int sacc[256];
+  __shared__ int sn;
+  const int unit = blockIdx.x / a.Sd, s = blockIdx.x % a.Sd;
+  int n = 0;
+  if (a.mode == 0) {
+    const int b = a.all_pos ? unit / (a.L + 1) : unit;
+    const uint32_t off = samp_offset(a);
+    if ((int)threadIdx.x < a.L) sacc[threadIdx.x] = accept_test(a, b, threadIdx.x, off);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int k = 0;
+      while (k < a.L && sacc[k]) ++k;
+      sn = k;
+    }
+    if (s == 0 && (!a.all_pos || unit % (a.L + 1) == 0) && (int)threadIdx.x < a.L)
+      a.acc[(int64_t)b * a.L + threadIdx.x] = sacc[threadIdx.x];
+    __syncthreads();
+    n = sn;
+  }
+  const DrawSpec ds = draw_spec(a, unit, n);
   const float T = a.T, inv_t = 1.0f / T;
-  const int64_t lo = min(a.V, (int64_t)s * a.slen), hi = min(a.V, lo + a.slen);
+  const int64_t lo = min(a.V, (int64_t)s * a.slen_d), hi = min(a.V, lo + a.slen_d);
+  // this thread's elements j = lo + tid + k * kST, loads first
+  float pv[kDrawEPT], qv[kDrawEPT];
+#pragma unroll
+  for (int k = 0; k < kDrawEPT; ++k) {
+    const int64_t j = lo + threadIdx.x + (int64_t)k * kST;
+    pv[k] = j < hi ? ds.px[j] : 0.0f;
+    qv[k] = (j < hi && ds.qrow >= 0) ? ds.qx[j] : 0.0f;
+  }
   uint64_t t = 0;
-  if (a.mode == 1 && a.probs_out) {
-    float* po = a.probs_out + (int64_t)unit * a.V;
-    for_slice<VEC>(ds.px, lo, hi, [&](int64_t j, float v) {
-      const float pj = final_prob(ds.pp, v, ds.pmul, T, inv_t);
-      po[j] = pj;
+  float* po = (a.mode == 1 && a.probs_out) ? a.probs_out + (int64_t)unit * a.V : nullptr;
+#pragma unroll
+  for (int k = 0; k < kDrawEPT; ++k) {
+    const int64_t j = lo + threadIdx.x + (int64_t)k * kST;
+    if (j >= hi) continue;
+    const float pj = final_prob(ds.pp, pv[k], ds.pmul, T, inv_t);
+    if (ds.qrow == -1) {
+      if (po) po[j] = pj;
       t += fx(pj);
-    });
-  } else if (ds.qrow == -1) {
-    for_slice<VEC>(ds.px, lo, hi, [&](int64_t, float v) { t += fx(final_prob(ds.pp, v, ds.pmul, T, inv_t)); });
-  } else {
-    for (int64_t j = lo + threadIdx.x; j < hi; j += kST) t += draw_weight(ds, j, T, inv_t);
+    } else {
+      const float qj = ds.qrow == -2 ? (j == ds.d ? 1.0f : 0.0f) : final_prob(ds.qp, qv[k], ds.qmul, T, inv_t);
+      const float r = pj - qj;
+      t += fx(r > 0.0f ? r : 0.0f);
+    }
   }
   t = block_sum512(t, sh);
-  if (threadIdx.x == 0) a.wsum[(int64_t)unit * kMaxSlices + s] = t;
+  if (threadIdx.x == 0) a.wsum[(int64_t)unit * kMaxDrawSlices + s] = t;
 }
 
-// ---- pass 6: the inverse-CDF draw, then the outputs
+// ---- pass 6: the inverse-CDF draw (the slice holding the uniform's mass, then the element:
+// each thread takes a contiguous run of the slice, one block scan finds the run), the outputs
 __global__ __launch_bounds__(kST) void samp_draw_kernel(SampArgs a) {
   __shared__ uint64_t sh[kSW];
   __shared__ int64_t found;
   __shared__ uint64_t sbase;
   __shared__ int sslice;
+  __shared__ int sn;
   const int unit = blockIdx.x;
-  const DrawSpec ds = draw_spec(a, unit);
-  const float T = a.T, inv_t = 1.0f / T;
-  const uint64_t* ws = a.wsum + (int64_t)unit * kMaxSlices;
-  const uint64_t u = ds.word >> 8;
   if (threadIdx.x == 0) {
-    uint64_t W = 0;
-    for (int s = 0; s < a.S; ++s) W += ws[s];
+    sn = a.L;
     found = -1;
     sslice = -1;
+  }
+  __syncthreads();
+  if (a.mode == 0 && (int)threadIdx.x < a.L) {  // n = the first rejected position (flags read in parallel)
+    const int b = a.all_pos ? unit / (a.L + 1) : unit;
+    if (!a.acc[(int64_t)b * a.L + threadIdx.x]) atomicMin(&sn, (int)threadIdx.x);
+  }
+  __syncthreads();
+  const int n = a.mode == 0 ? sn : 0;
+  const DrawSpec ds = draw_spec(a, unit, n);
+  const float T = a.T, inv_t = 1.0f / T;
+  const uint64_t* ws = a.wsum + (int64_t)unit * kMaxDrawSlices;
+  const uint64_t u = ds.word >> 8;
+  {  // the slice holding the target: slice sums scanned in thread order (Sd <= kST)
+    const uint64_t mine = (int)threadIdx.x < a.Sd ? ws[threadIdx.x] : 0;
+    uint64_t W;
+    const uint64_t incl = block_scan512(mine, sh, W);
     if (W == 0) {
-      found = (int64_t)((u * (uint64_t)a.V) >> 24);
+      if (threadIdx.x == 0) found = (int64_t)((u * (uint64_t)a.V) >> 24);
     } else {
       const uint64_t t = (W >> 24) * u + (((W & 0xFFFFFFull) * u) >> 24);
-      uint64_t run = 0;
-      for (int s = 0; s < a.S; ++s) {
-        if (t < run + ws[s]) {
-          sslice = s;
-          break;
-        }
-        run += ws[s];
+      if (incl - mine <= t && t < incl) {
+        sslice = (int)threadIdx.x;
+        sbase = t - (incl - mine);  // the target inside the slice
       }
-      sbase = t - run;  // the target inside the slice
     }
   }
   __syncthreads();
   if (found < 0 && sslice >= 0) {
     const uint64_t tt = sbase;
-    const int64_t lo = min(a.V, (int64_t)sslice * a.slen), hi = min(a.V, lo + a.slen);
-    uint64_t run = 0;
-    for (int64_t c0 = lo; c0 < hi; c0 += 4 * kST) {
-      const int64_t j0 = c0 + 4 * (int64_t)threadIdx.x;
-      uint64_t w4[4], tsum = 0;
+    const int64_t lo = min(a.V, (int64_t)sslice * a.slen_d), hi = min(a.V, lo + a.slen_d);
+    const int64_t per = ceil_div(hi - lo, kST);  // <= kDrawEPT
+    const int64_t j0 = lo + (int64_t)threadIdx.x * per;
+    uint64_t w[kDrawEPT], tsum = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        w4[e] = (j0 + e < hi) ? draw_weight(ds, j0 + e, T, inv_t) : 0;
-        tsum += w4[e];
-      }
-      uint64_t tot;
-      const uint64_t incl = block_scan512(tsum, sh, tot);
-      uint64_t r0 = run + incl - tsum;
-      if (r0 <= tt && tt < run + incl) {  // exactly one thread holds the crossing
+    for (int e = 0; e < kDrawEPT; ++e) {
+      const int64_t j = j0 + e;
+      w[e] = (e < per && j < hi) ? draw_weight(ds, j, T, inv_t) : 0;
+      tsum += w[e];
+    }
+    uint64_t tot;
+    const uint64_t incl = block_scan512(tsum, sh, tot);
+    uint64_t r0 = incl - tsum;
+    if (r0 <= tt && tt < incl) {  // exactly one thread holds the crossing
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (tt < r0 + w4[e]) {
-            found = j0 + e;
-            break;
-          }
-          r0 += w4[e];
+      for (int e = 0; e < kDrawEPT; ++e) {
+        if (tt < r0 + w[e]) {
+          found = j0 + e;
+          break;
         }
+        r0 += w[e];
       }
-      __syncthreads();
-      if (found >= 0) break;
-      run += tot;
     }
   }
   __syncthreads();
@@ -920,7 +1045,7 @@ __host__ inline SampLayout samp_layout(size_t rows, size_t draws, size_t accs, i
   L.info = take(rows * sizeof(RowInfo));
   L.prm = take(rows * sizeof(RowParam));
   L.acc = take(accs * 4);
-  L.wsum = take(draws * kMaxSlices * 8);
+  L.wsum = take(draws * kMaxDrawSlices * 8);
   L.cand = take(rows * (size_t)V * 4);
   L.total = off;
   return L;
@@ -951,6 +1076,13 @@ __host__ inline int samp_slices(int rows, int64_t V) {
 
 __host__ inline int64_t samp_slice_len(int64_t V, int S) { return (ceil_div(V, S) + 3) & ~(int64_t)3; }
 
+// draw slices: about 1024 workgroups over the draws, slices of at most kST * kDrawEPT elements
+__host__ inline int samp_draw_slices(int draws, int64_t V) {
+  int64_t S = std::max<int64_t>(ceil_div(1024, draws), ceil_div(V, (int64_t)kST * kDrawEPT));
+  S = std::min<int64_t>(S, std::max<int64_t>(ceil_div(V, (int64_t)kST * kDrawEPT), ceil_div(V, 256)));
+  return (int)std::max<int64_t>(1, std::min<int64_t>(S, kMaxDrawSlices));
+}
+
 }  // namespace dsk
 
 using namespace dsk;
@@ -972,22 +1104,30 @@ static void launch_slice_argmax(const void* logits, int dtype, int64_t ldl, int6
 }
 
 // The sampled chain (passes 1-6) for the rows and draws a describes.
-static int launch_sampled(SampArgs& a, int draws, int finish_units, bool vec, hipStream_t st, const char* who) {
+static int launch_sampled(SampArgs& a, int draws, hipStream_t st, const char* who) {
   const int rows = a.Rp + a.Rq;
   const dim3 blk(kST);
   const dim3 grow((unsigned)(rows * a.S));
-  if (vec) {
-    hipLaunchKernelGGL(samp_max_kernel<true>, grow, blk, 0, st, a);
-    hipLaunchKernelGGL(samp_stats_kernel<true>, grow, blk, 0, st, a);
-  } else {
-    hipLaunchKernelGGL(samp_max_kernel<false>, grow, blk, 0, st, a);
-    hipLaunchKernelGGL(samp_stats_kernel<false>, grow, blk, 0, st, a);
+  const bool one = a.T == 1.0f;
+#define DSK_ROW_PASSES(VEC_, ONE_)                                                 \
+  hipLaunchKernelGGL((samp_max_kernel<VEC_, ONE_>), grow, blk, 0, st, a);          \
+  hipLaunchKernelGGL((samp_stats_kernel<VEC_, ONE_>), grow, blk, 0, st, a);        \
+  if (a.do_k || a.do_p) {                                                          \
+    hipLaunchKernelGGL(samp_select_kernel, dim3((unsigned)rows), blk, 0, st, a);   \
+    hipLaunchKernelGGL((samp_gather_kernel<VEC_, ONE_>), grow, blk, 0, st, a);     \
   }
-  if (a.do_k || a.do_p) hipLaunchKernelGGL(samp_gather_kernel, grow, blk, 0, st, a);
-  hipLaunchKernelGGL(samp_finish_kernel, dim3((unsigned)finish_units), blk, 0, st, a);
-  const dim3 gdraw((unsigned)(draws * a.S));
-  if (vec) hipLaunchKernelGGL(samp_wsum_kernel<true>, gdraw, blk, 0, st, a);
-  else hipLaunchKernelGGL(samp_wsum_kernel<false>, gdraw, blk, 0, st, a);
+  if (a.vec && one) {
+    DSK_ROW_PASSES(true, true)
+  } else if (a.vec) {
+    DSK_ROW_PASSES(true, false)
+  } else if (one) {
+    DSK_ROW_PASSES(false, true)
+  } else {
+    DSK_ROW_PASSES(false, false)
+  }
+#undef DSK_ROW_PASSES
+  hipLaunchKernelGGL(samp_finish_kernel, dim3((unsigned)rows), blk, 0, st, a);
+  hipLaunchKernelGGL(samp_wsum_kernel, dim3((unsigned)(draws * a.Sd)), blk, 0, st, a);
   hipLaunchKernelGGL(samp_draw_kernel, dim3((unsigned)draws), blk, 0, st, a);
   DSK_LAUNCH_CHECK(who);
   return DSK_OK;
@@ -1002,6 +1142,11 @@ static void samp_common(SampArgs& a, int64_t V, int rows, float T, float top_p, 
   a.do_p = (top_p < 1.0f);
   a.S = samp_slices(rows, V);
   a.slen = samp_slice_len(V, a.S);
+}
+
+static void samp_draws(SampArgs& a, int draws) {
+  a.Sd = samp_draw_slices(draws, a.V);
+  a.slen_d = samp_slice_len(a.V, a.Sd);
 }
 
 static size_t accept_sample_ws(int B, int L, int64_t V) {
@@ -1162,9 +1307,10 @@ extern "C" int dsk_accept_sample(const float* p_logits, const float* q_logits, i
   a.accept_out = accept_out;
   a.sample_out = sample_out;
   samp_bind(a, workspace, samp_layout((size_t)B * (2 * L + 1), (size_t)B * (L + 1), (size_t)B * std::max(L, 1), V));
-  const bool vec = V % 4 == 0 && ((uintptr_t)p_logits & 15) == 0 && ((uintptr_t)q_logits & 15) == 0;
+  a.vec = V % 4 == 0 && ((uintptr_t)p_logits & 15) == 0 && ((uintptr_t)q_logits & 15) == 0;
   const int draws = a.all_pos ? B * (L + 1) : B;
-  return launch_sampled(a, draws, B * (L + 1), vec, as_stream(stream), "dsk_accept_sample");
+  samp_draws(a, draws);
+  return launch_sampled(a, draws, as_stream(stream), "dsk_accept_sample");
 }
 
 extern "C" size_t dsk_sample_ws_bytes(int R, int64_t V) {
@@ -1206,6 +1352,7 @@ extern "C" int dsk_sample_rows(const float* logits, int64_t V, int R, float temp
   a.tok_rows = token_out;
   a.probs_out = probs_out;
   samp_bind(a, workspace, samp_layout((size_t)R, (size_t)R, 1, V));
-  const bool vec = V % 4 == 0 && ((uintptr_t)logits & 15) == 0 && ((uintptr_t)probs_out & 15) == 0;
-  return launch_sampled(a, R, R, vec, st, "dsk_sample_rows");
+  a.vec = V % 4 == 0 && ((uintptr_t)logits & 15) == 0;
+  samp_draws(a, R);
+  return launch_sampled(a, R, st, "dsk_sample_rows");
 }

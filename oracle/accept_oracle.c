@@ -18,10 +18,10 @@
  *   - exp is dsk_expf below (Cody-Waite reduction by ln 2, Taylor polynomial to r^7,
  *     explicit fmaf, inputs below -86 flush to 0 so no subnormal is ever formed);
  *   - a row's distribution is built on the unnormalised exponentials e_j = exp(y_j - max y)
- *     with fixed-point masses w_j = fx(e_j) = floor(e_j * 2^44) and Z = sum w_j (integer
+ *     with fixed-point masses w_j = fx(e_j) = floor(e_j * 2^31) and Z = sum w_j (integer
  *     sums do not depend on summation order); softmax then truncation then renormalisation is
  *     the same as truncating e and dividing by the kept mass, so the final probability of a
- *     kept element is e_j / float(S * 2^-44) with S the kept mass;
+ *     kept element is e_j / float(S * 2^-31) with S the kept mass;
  *   - top-k keeps e_j >= the k-th largest e; top-p keeps an element while the mass strictly
  *     before it (in descending order) is below TP = ceil(top_p * Z), an exact integer;
  *   - uniforms are Philox4x32-10 (Salmon et al., SC'11) words, u = (w >> 8) * 2^-24;
@@ -106,8 +106,9 @@ float oracle_expf(float x) {
   return p * sc;
 }
 
-static uint64_t fx(float p) { return (uint64_t)(p * 0x1p44f); }
-static float fx_to_float(uint64_t s) { return (float)((double)s * 0x1p-44); }
+/* every mass is in [0, 1] (e, final probabilities, residuals): p * 2^31 is exact and fits */
+static uint64_t fx(float p) { return (uint64_t)(p * 0x1p31f); }
+static float fx_to_float(uint64_t s) { return (float)((double)s * 0x1p-31); }
 
 /* ------------------------------------------------------------------------ softmax + truncation */
 typedef struct {

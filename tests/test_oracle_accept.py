@@ -156,18 +156,18 @@ def test_top_p_target_is_the_exact_ceiling():
     rng = np.random.default_rng(5)
     for _ in range(3000):
         top_p = np.float32(rng.uniform(0.0, 1.0))
-        Z = int(rng.integers(2**44, 2**62))
+        Z = int(rng.integers(2**31, 2**50))
         assert A.top_p_target(top_p, Z) == math.ceil(Fraction(float(top_p)) * Z)
     assert A.top_p_target(0.0, 2**50) == 0 and A.top_p_target(-0.5, 2**50) == 0
-    assert A.top_p_target(1e-40, 2**44) == 1                       # subnormal top_p: keeps the top
-    assert A.top_p_target(0.5, 2**44 + 1) == 2**43 + 1              # ceiling, not floor
+    assert A.top_p_target(1e-40, 2**31) == 1                       # subnormal top_p: keeps the top
+    assert A.top_p_target(0.5, 2**31 + 1) == 2**30 + 1              # ceiling, not floor
     top = float(np.nextafter(np.float32(1.0), np.float32(0.0)))
-    Z = 2**61 + 12345
+    Z = 2**50 + 12345
     assert A.top_p_target(top, Z) == math.ceil(Fraction(top) * Z)
 
 
 def _fx(e):
-    return np.floor(np.asarray(e, np.float64) * 2.0**44).astype(np.int64)
+    return np.floor(np.asarray(e, np.float64) * 2.0**31).astype(np.int64)
 
 
 def _kept_by_max_rule(e, top_k, top_p):
