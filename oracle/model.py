@@ -21,11 +21,21 @@ does); ``double_round=True`` rounds the projection output first, as an unfused b
 would. On a 256-wide 4-layer random model the two conventions alone differ by 0.022 in the
 normalised-logit metric, which is the noise floor this oracle works at.
 
-Pinning: attention equals an explicit loop over heads with the GQA map h -> h // (nq/nkv)
-(tests/test_model.py:25-60 in the reference); the causal mask reproduces the reference's
-exact grids; RMSNorm / RoPE / SiLU are checked against float64 closed forms in
-tests/test_oracle_model.py. The mlx_lm op order and rounding points themselves are external
-to the reference: parity unpinned beyond the logits tolerance.
+Pinning: with the bf16 rounding points switched off, every composition equals an independent
+implementation of the public architecture on identical weights (tests/test_oracle_compose.py):
+OracleTarget equals transformers' Qwen3ForCausalLM (GQA, q/k norms, RoPE base, tied and untied
+heads, KV-cached continuation, hidden-state taps) and Gemma3ForCausalLM for the Gemma-style
+layout (sandwich norms, GeGLU, sliding-window layers with their own RoPE base, query scale,
+soft-cap, embedding scale); OracleDFlash and the qwen3 OracleDSpark equal stacks of
+Qwen3DecoderLayer run without a mask over [context; block] rows (the context rows' input norm
+made the identity), and the gemma4 OracleDSpark a stack of Gemma4TextDecoderLayer (k_eq_v,
+v_norm, proportional RoPE, scale 1, layer_scalar); to 1e-5 in the normalised-logit metric, and
+each comparison catches a planted mistake. Attention also equals an explicit loop over heads
+with the GQA map h -> h // (nq/nkv) (tests/test_model.py:25-60 in the reference); the causal
+mask reproduces the reference's exact grids; RMSNorm / RoPE / SiLU are checked against float64
+closed forms in tests/test_oracle_model.py. What stays unpinned is the rounding: where a bf16
+MLX graph rounds inside mlx_lm / mlx_vlm is external to the reference, so the rounding points
+here are this build's choice, covered by the logits tolerance.
 """
 
 from __future__ import annotations
