@@ -130,6 +130,27 @@ def build_target(name_or_args, seed: int = 0, device="cuda", keep_mlx: bool = Fa
     return Qwen3W8(args, layers, embed, lm_head, ones(H, device))
 
 
+def randomize_norms(model, seed: int, spread: float = 0.25) -> None:
+    """Scale every RMSNorm gain of a built model (target or drafter: layer norms, q/k norms,
+    sandwich norms, final and hidden norms) by 1 + spread * N(0, 1), in place, seeded: models
+    whose gains are not all equal, so a norm applied to the wrong tensor or left out changes the
+    output."""
+    g = torch.Generator().manual_seed(seed)
+    tensors = []
+    for L in getattr(model, "layers", []):
+        for name in ("in_norm", "post_norm", "q_norm", "k_norm", "attn_out_norm", "ff_out_norm"):
+            t = getattr(L, name, None)
+            if t is not None:
+                tensors.append(t)
+    for name in ("norm", "hidden_norm"):
+        t = getattr(model, name, None)
+        if torch.is_tensor(t):
+            tensors.append(t)
+    for t in tensors:
+        f = 1.0 + spread * torch.randn(t.shape, generator=g)
+        t.copy_((t.float().cpu() * f).to(t.dtype))
+
+
 def evenly_spaced_layers(n_target_layers: int, n: int) -> list[int]:
     """n distinct tap layers spread over the target: from layer 1 to layer L-3 (the DFlash
     convention) when the target is deep enough, else over all layers."""

@@ -77,8 +77,11 @@ def rope(x, pos, theta, inv=None):
     return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1)
 
 
-def sdpa(q, K, V, scale, mask=None):
-    """q [W, nq, hd], K/V [L, nkv, hd] -> [W, nq, hd]; GQA by head index // (nq/nkv)."""
+def sdpa(q, K, V, scale, mask=None, p_bf16=False):
+    """q [W, nq, hd], K/V [L, nkv, hd] -> [W, nq, hd]; GQA by head index // (nq/nkv).
+    p_bf16: the unnormalised probabilities exp(s - max) are rounded to bf16 before they weight
+    V and before they are summed for the normaliser (where a bf16 attention kernel rounds them);
+    otherwise the softmax stays float32."""
     W, nq, hd = q.shape
     nkv = K.shape[1]
     G = nq // nkv
@@ -87,7 +90,11 @@ def sdpa(q, K, V, scale, mask=None):
         s = (q[:, h] @ K[:, h // G].T) * scale
         if mask is not None:
             s = s.masked_fill(~mask, float("-inf"))
-        out[:, h] = torch.softmax(s, dim=-1) @ V[:, h // G]
+        if p_bf16:
+            p = bf(torch.exp(s - s.max(dim=-1, keepdim=True).values))
+            out[:, h] = (p @ V[:, h // G]) / p.sum(dim=-1, keepdim=True)
+        else:
+            out[:, h] = torch.softmax(s, dim=-1) @ V[:, h // G]
     return out
 
 
@@ -149,11 +156,12 @@ class OracleLayer:
 class OracleTarget:
     """Dense-KV CPU model built from a GPU model created with keep_mlx=True."""
 
-    def __init__(self, model, kv_bits=None, double_round: bool = False):
+    def __init__(self, model, kv_bits=None, double_round: bool = False, p_bf16: bool = False):
         a = model.args
         self.a = a
         self.kv_bits = kv_bits
         self.rr = bf if double_round else (lambda x: x)
+        self.p_bf16 = p_bf16
         self.layers = [OracleLayer(L, a.num_attention_heads, a.num_key_value_heads, a.head_dim) for L in model.layers]
         self.embed = deq_table(model.embed)
         self.lm_head = deq(model.lm_head)
@@ -191,7 +199,7 @@ class OracleTarget:
                 k, v = kv_quant_roundtrip(k), kv_quant_roundtrip(v)
             self.K[l] = torch.cat([self.K[l], k])
             self.V[l] = torch.cat([self.V[l], v])
-            o = bf(sdpa(q, self.K[l], self.V[l], a.attn_scale, causal_mask(self.offset, W, win)))
+            o = bf(sdpa(q, self.K[l], self.V[l], a.attn_scale, causal_mask(self.offset, W, win), self.p_bf16))
             if L.attn_out_norm is not None:     # sandwich: norm the projection output, then add
                 h = bf(h + bf(rmsnorm(bf(o.reshape(W, -1) @ L.wo.T), L.attn_out_norm, eps)))
             else:
@@ -219,9 +227,10 @@ class OracleTarget:
 class OracleDFlash:
     """CPU DFlash drafter (src/mlx_dspark/dflash_model.py:100-208) bound to an OracleTarget."""
 
-    def __init__(self, drafter, target: OracleTarget):
+    def __init__(self, drafter, target: OracleTarget, p_bf16: bool = False):
         c = drafter.config
         self.c = c
+        self.p_bf16 = p_bf16
         self.fc = deq(drafter.fc)
         self.hidden_norm = drafter.hidden_norm.float().cpu()
         self.norm = drafter.norm.float().cpu()
@@ -263,7 +272,7 @@ class OracleDFlash:
             self.V[l] = torch.cat([self.V[l], vc])
             K = torch.cat([self.K[l], kb])
             Vv = torch.cat([self.V[l], vb])
-            o = bf(sdpa(q, K, Vv, hd ** -0.5))
+            o = bf(sdpa(q, K, Vv, hd ** -0.5, None, self.p_bf16))
             h = bf(h + o.reshape(L, -1) @ Lw.wo.T)
             x = bf(rmsnorm(h, Lw.post_norm, eps))
             gu = bf(x @ Lw.wgu.T)
@@ -281,6 +290,14 @@ def normalized_maxdiff(a: torch.Tensor, b: torch.Tensor) -> float:
     an = a / a.pow(2).mean(-1, keepdim=True).sqrt()
     bn = b / b.pow(2).mean(-1, keepdim=True).sqrt()
     return float((an - bn).abs().max())
+
+
+def logit_diff(a: torch.Tensor, b: torch.Tensor):
+    """(max-abs, rms) of the difference of RMS-normalised logit rows."""
+    a = a.detach().float().cpu().reshape(-1, a.shape[-1])
+    b = b.detach().float().cpu().reshape(-1, b.shape[-1])
+    d = a / a.pow(2).mean(-1, keepdim=True).sqrt() - b / b.pow(2).mean(-1, keepdim=True).sqrt()
+    return float(d.abs().max()), float(d.pow(2).mean().sqrt())
 
 
 def greedy_decode(target: OracleTarget, prompt, n_new: int):
@@ -314,9 +331,10 @@ class OracleDSpark:
     (:270-281) with bf16 rounding points (logits, bias and their sum are bf16, as in a bf16
     graph), confidence logits (:311-320)."""
 
-    def __init__(self, drafter):
+    def __init__(self, drafter, p_bf16: bool = False):
         c = drafter.config
         self.c = c
+        self.p_bf16 = p_bf16
         self.gemma = c.family == "gemma4"
         self.nq, self.nkv, self.hd = c.num_attention_heads, c.n_kv_heads, c.attn_head_dim
         frac = c.partial_rotary_factor if c.rope_type == "proportional" else 1.0
@@ -381,7 +399,7 @@ class OracleDSpark:
             q = bf(x @ L.wq[: nq * hd].T).view(k, nq, hd)
             q = bf(rope(bf(rmsnorm(q, L.q_norm, eps)).transpose(0, 1), pos, c.rope_theta, self.inv).transpose(0, 1))
             kb, vb = self._kv(L, x, k, pos)
-            o = bf(sdpa(q, torch.cat([self.K[l], kb]), torch.cat([self.V[l], vb]), c.scaling))
+            o = bf(sdpa(q, torch.cat([self.K[l], kb]), torch.cat([self.V[l], vb]), c.scaling, None, self.p_bf16))
             if self.gemma:     # sandwich norms, tanh-GeLU, layer_scalar (model.py:172-184)
                 h = bf(h + bf(rmsnorm(bf(o.reshape(k, -1) @ L.wo.T), L.attn_out_norm, eps)))
                 x = bf(rmsnorm(h, L.post_norm, eps))

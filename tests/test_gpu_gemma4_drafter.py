@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 import torch
 
+from _parity import check_logits
 from oracle import model as OM
 
 pytestmark = pytest.mark.gpu
@@ -124,8 +125,9 @@ def test_gemma4_drafter_matches_oracle(dev, gemma4_pair):
     _, fused = model.prefill(prompt, cache, list(cfg.target_layer_ids))
     dcache = d.make_ctx_cache(max_ctx=256)
     d.update_context(fused[0], 0, dcache)
-    od = OM.OracleDSpark(d)
+    od, oa = OM.OracleDSpark(d, p_bf16=True), OM.OracleDSpark(d)
     od.update_context(fused[0].float().cpu())
+    oa.update_context(fused[0].float().cpu())
     # context K/V in the drafter cache against the oracle's
     k_pool, v_pool, _, _ = dcache.layer_args(0)
     bt = dcache.block_table[0].cpu()
@@ -139,9 +141,7 @@ def test_gemma4_drafter_matches_oracle(dev, gemma4_pair):
                          device=dev)
     got = d.block_logits(block, dcache, 5)[0]
     want = od.base_logits(block.cpu()[0], 5)
-    err = OM.normalized_maxdiff(got, want)
-    print(f"gemma4 drafter block logits: normalised max-abs {err:.4f}", flush=True)
-    assert err < 5e-2
+    check_logits(got, want, oa.base_logits(block.cpu()[0], 5), "gemma4 drafter block logits")
     assert float(got.abs().max()) <= 30.0
 
 
