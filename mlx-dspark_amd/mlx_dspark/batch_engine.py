@@ -27,7 +27,7 @@ import time
 import torch
 
 from . import blockdraft, ops
-from .generate import GenResult, _Streamer, _seed64, eos_token_ids
+from .generate import GenResult, _final_text, _seed64, _Streamer, eos_token_ids
 from .kv import PagedKVCache
 
 # --------------------------------------------------------------------------- capability
@@ -42,64 +42,56 @@ def batchable(target) -> bool:
     return getattr(target, "family", "qwen3") in ("qwen3", "gemma4")
 
 
-def _as_list(x, B):
+def _per_row(x, B):
+    """A per-row setting given once for all rows or as one value per row."""
     return list(x) if isinstance(x, (list, tuple)) else [x] * B
 
 
-class _RowTracker:
-    """Per-row streaming, stop strings, eos and max_new_tokens, and GenResult assembly
-    (behaviour of the reference's _RowTracker, batch_engine.py:233-303)."""
+class _Row:
+    """The output of one batched request. It ends the way a single request ends: at an eos
+    id, at ``limit`` tokens, or at a stop string (the streamer of the single-request loops).
+    A round's tokens are committed whole, up to the first eos, so a row may pass its limit
+    within its last round (the reference's batched rows do the same,
+    src/mlx_dspark/batch_engine.py:281-291)."""
 
-    def __init__(self, tokenizer, first_tokens, *, max_new_tokens, on_texts=None, stops=None):
-        self.tok = tokenizer
-        self.eos = eos_token_ids(tokenizer)
-        B = len(first_tokens)
-        self.B = B
-        self.mnt = _as_list(max_new_tokens, B)
-        ot = on_texts or [None] * B
-        sp = stops or [None] * B
-        self.streamers = [_Streamer(tokenizer, self.eos, ot[b], sp[b]) for b in range(B)]
-        self.out_ids = [[int(first_tokens[b])] for b in range(B)]
-        self.accept_lengths: list = [[] for _ in range(B)]
-        self.finished = [False] * B
-        for b in range(B):
-            self.streamers[b].update(self.out_ids[b])
-            self._check(b)
+    __slots__ = ("ids", "limit", "eos", "streamer", "accepts", "done", "t0")
 
-    def _check(self, b):
-        ids = self.out_ids[b]
-        if ids[-1] in self.eos or len(ids) >= self.mnt[b] or self.streamers[b].stopped:
-            self.finished[b] = True
+    def __init__(self, tokenizer, eos: set, first: int, limit: int, on_text=None, stop=None):
+        self.ids = [int(first)]
+        self.limit = int(limit)
+        self.eos = eos
+        self.streamer = _Streamer(tokenizer, eos, on_text, stop)
+        self.accepts: list = []
+        self.t0 = time.time()
+        self.done = False
+        self._settle()
 
-    def commit(self, b, tokens, accept_len=None):
-        if self.finished[b]:
+    def _settle(self) -> None:
+        self.streamer.update(self.ids)
+        self.done = self.ids[-1] in self.eos or len(self.ids) >= self.limit or self.streamer.stopped
+
+    def extend(self, tokens, accept_len: int | None = None) -> None:
+        if self.done:
             return
         if accept_len is not None:
-            self.accept_lengths[b].append(accept_len)
-        for tok in tokens:
-            self.out_ids[b].append(int(tok))
-            if tok in self.eos:
+            self.accepts.append(int(accept_len))
+        for t in tokens:
+            self.ids.append(int(t))
+            if self.ids[-1] in self.eos:
                 break
-        self.streamers[b].update(self.out_ids[b])
-        self._check(b)
+        self._settle()
 
-    def all_done(self):
-        return all(self.finished)
-
-    def results(self, secs):
-        out = []
-        for b in range(self.B):
-            self.streamers[b].flush()
-            ids = self.out_ids[b]
-            stopped = self.streamers[b].stopped
-            reason = "stop" if (ids[-1] in self.eos or stopped) else "length"
-            text = self.streamers[b].text if stopped else self.tok.decode([t for t in ids if t not in self.eos])
-            spec = bool(self.accept_lengths[b])
-            al = self.accept_lengths[b] if spec else [1] * len(ids)
-            out.append(GenResult(text=text, token_ids=ids, num_tokens=len(ids), num_rounds=len(al),
-                                 accept_lengths=al, target_forwards=(len(al) + 1) if spec else len(ids),
-                                 seconds=secs, finish_reason=reason))
-        return out
+    def result(self, tokenizer, seconds: float) -> GenResult:
+        st = self.streamer
+        st.flush()
+        ids = list(self.ids)
+        spec = bool(self.accepts)
+        rounds = list(self.accepts) if spec else [1] * len(ids)
+        reason = "stop" if (st.stopped or ids[-1] in self.eos) else "length"
+        return GenResult(text=_final_text(tokenizer, st, ids, self.eos), token_ids=ids, num_tokens=len(ids),
+                         num_rounds=len(rounds), accept_lengths=rounds,
+                         target_forwards=len(rounds) + 1 if spec else len(ids), seconds=seconds,
+                         finish_reason=reason)
 
 
 # --------------------------------------------------------------------------- baseline
@@ -116,7 +108,7 @@ def batch_generate_baseline(target, tokenizer, prompts_ids, *, max_new_tokens=12
         return []
     model = target.model
     dev = model.device
-    mnt = _as_list(max_new_tokens, B)
+    mnt = _per_row(max_new_tokens, B)
     need = max(len(p) for p in prompts_ids) + max(mnt) + 8
     cache = target.make_cache(B=B, max_ctx=max(max_ctx or 0, need))
     s64 = _seed64(seed)
@@ -126,19 +118,20 @@ def batch_generate_baseline(target, tokenizer, prompts_ids, *, max_new_tokens=12
         lg, _ = model.prefill(list(ids), cache.row(b))
         last[b].copy_(lg[0, -1])
     tok, _ = ops.sample_rows(last, temperature, top_p, top_k, seed=s64, offset=0)
-    first = [int(x) for x in tok.tolist()]
-    trk = _RowTracker(tokenizer, first, max_new_tokens=mnt, on_texts=on_texts, stops=stops)
+    eos = eos_token_ids(tokenizer)
+    ot, sp = _per_row(on_texts, B), _per_row(stops, B)
+    rows = [_Row(tokenizer, eos, t, mnt[b], ot[b], sp[b]) for b, t in enumerate(tok.tolist())]
     cur = tok.view(B, 1).to(torch.int32)
     step = 1
-    while not trk.all_done():
+    while not all(r.done for r in rows):
         lg, _ = model.forward(cur, cache, None)
         tok, _ = ops.sample_rows(lg[:, -1].contiguous(), temperature, top_p, top_k, seed=s64, offset=step)
         step += 1
-        toks = tok.tolist()
-        for b in range(B):
-            trk.commit(b, [int(toks[b])])
+        for r, t in zip(rows, tok.tolist()):
+            r.extend([t])
         cur = tok.view(B, 1).to(torch.int32)
-    return trk.results(time.time() - t0)
+    secs = time.time() - t0
+    return [r.result(tokenizer, secs) for r in rows]
 
 
 # --------------------------------------------------------------------------- spec slots
@@ -190,9 +183,9 @@ class SpecSlots:
         self.n_active = 0
         C = self.capacity
         self.pending = [0] * C
-        self.trk = [None] * C
+        self.rows: list = [None] * C
         self.meta = [None] * C
-        self.t0 = [0.0] * C
+        self.eos = eos_token_ids(tokenizer)
         # own page range of each slot (moves with the slot's block-table row on compaction)
         self.range_t = [self.cache.row_pages(b) for b in range(C)]
         self.range_d = [self.ctx.row_pages(b) for b in range(C)]
@@ -271,23 +264,21 @@ class SpecSlots:
                                  seed=self.s64, offset=0xFFFFFFFF)
         first = int(tok.item())
         self.pending[b] = first
-        self.trk[b] = _RowTracker(self.tokenizer, [first], max_new_tokens=[max_new_tokens], on_texts=[on_text],
-                                  stops=[stop])
+        self.rows[b] = _Row(self.tokenizer, self.eos, first, max_new_tokens, on_text, stop)
         self.meta[b] = meta
-        self.t0[b] = time.time()
         self.n_active += 1
 
     def _retire(self, b: int):
-        meta, res = self.meta[b], self.trk[b].results(time.time() - self.t0[b])[0]
+        meta, res = self.meta[b], self.rows[b].result(self.tokenizer, time.time() - self.rows[b].t0)
         last = self.n_active - 1
         if b != last:
             self.cache.swap_rows(b, last)
             self.ctx.swap_rows(b, last)
-            for st in (self.pending, self.trk, self.meta, self.t0, self.range_t, self.range_d):
+            for st in (self.pending, self.rows, self.meta, self.range_t, self.range_d):
                 st[b], st[last] = st[last], st[b]
         self.cache.set_row_length(last, 0)
         self.ctx.set_row_length(last, 0)
-        self.trk[last], self.meta[last], self.pending[last] = None, None, 0
+        self.rows[last], self.meta[last], self.pending[last] = None, None, 0
         self.n_active = last
         return meta, res
 
@@ -295,7 +286,7 @@ class SpecSlots:
         out = []
         b = 0
         while b < self.n_active:
-            if self.trk[b].finished[0]:
+            if self.rows[b].done:
                 out.append(self._retire(b))
             else:
                 b += 1
@@ -353,8 +344,8 @@ class SpecSlots:
             committed = [int(x) for x in dr[b][:n]] + [int(tok_list[b])]
             self.cache.lengths[b] += n + 1
             self.ctx.lengths[b] += n + 1
-            self.trk[b].commit(0, committed, accept_len=len(committed))
-            self.pending[b] = self.trk[b].out_ids[0][-1]
+            self.rows[b].extend(committed, accept_len=len(committed))
+            self.pending[b] = self.rows[b].ids[-1]
             if self.ctrl is not None:
                 self.ctrl.update(n, cap)
         return finished + self._sweep_finished()
@@ -368,9 +359,8 @@ def batch_spec_generate(target, tokenizer, drafter, prompts_ids, *, max_new_toke
     B = len(prompts_ids)
     if B == 0:
         return []
-    mnt = _as_list(max_new_tokens, B)
-    ot = on_texts or [None] * B
-    sp = stops or [None] * B
+    mnt = _per_row(max_new_tokens, B)
+    ot, sp = _per_row(on_texts, B), _per_row(stops, B)
     k = int(drafter.config.block_size)
     need = max(len(p) for p in prompts_ids) + max(mnt) + 2 * k + 8
     slots = SpecSlots(target, tokenizer, drafter, capacity=B, max_draft_tokens=max_draft_tokens,

@@ -71,10 +71,13 @@ class LayerView:
 
 
 class PagedKVCache(list):
-    """KV pools for ``n_layers`` layers and ``B`` rows, up to ``max_ctx`` tokens per row."""
+    """KV pools for ``n_layers`` layers and ``B`` rows, up to ``max_ctx`` tokens per row.
+    ``spare_rows`` rows' worth of pages (and ``spare_pages`` more) sit in the pools beyond the
+    rows' own pages, for block tables that point at shared or stored pages."""
 
     def __init__(self, n_layers: int, B: int, n_kv: int, head_dim: int, max_ctx: int, *,
-                 page: int = 64, kv_bits: int | None = None, device="cuda", spare_pages: int = 0):
+                 page: int = 64, kv_bits: int | None = None, device="cuda", spare_pages: int = 0,
+                 spare_rows: int = 0):
         super().__init__(LayerView(self, l) for l in range(n_layers))
         self.n_layers, self.B, self.n_kv, self.head_dim = n_layers, B, n_kv, head_dim
         self.page = page
@@ -83,7 +86,7 @@ class PagedKVCache(list):
         self.kv_dtype = DSK_KV_U8 if kv_bits == 8 else DSK_KV_BF16
         if kv_bits not in (None, 8):
             raise ValueError(f"kv_bits={kv_bits}: only 8-bit (or None = bf16) KV is supported")
-        self.n_pages = B * self.max_pages + spare_pages
+        self.n_pages = (B + spare_rows) * self.max_pages + spare_pages
         dev = torch.device(device)
         shape = (self.n_pages, n_kv, page, head_dim)
         dt = torch.uint8 if self.kv_dtype == DSK_KV_U8 else torch.bfloat16

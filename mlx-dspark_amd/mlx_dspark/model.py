@@ -105,11 +105,11 @@ class DSparkDrafter:
         out = ops.w8_embed(ids.reshape(-1), self.embed_tokens, self.embed_scale)
         return out.view(*shape, -1)
 
-    def make_ctx_cache(self, max_ctx: int = 16384, B: int = 1) -> PagedKVCache:
+    def make_ctx_cache(self, max_ctx: int = 16384, B: int = 1, spare_rows: int = 0) -> PagedKVCache:
         """Per-layer context K/V (the reference's [CtxCache] * n_layers, model.py:48-80, 250-251)."""
         c = self.config
         return PagedKVCache(c.num_hidden_layers, B, c.n_kv_heads, c.attn_head_dim, max_ctx + c.block_size,
-                            device=self.device)
+                            device=self.device, spare_rows=spare_rows)
 
     def update_context(self, target_hidden_cat: torch.Tensor, ctx_offset: int, ctx_caches: PagedKVCache,
                        n_valid=None) -> None:

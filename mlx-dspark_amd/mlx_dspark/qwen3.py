@@ -116,11 +116,11 @@ class Qwen3W8:
 
     # ------------------------------------------------------------------ cache
     def make_cache(self, B: int = 1, max_ctx: int | None = None, kv_bits: int | None = None,
-                   page: int = 64) -> PagedKVCache:
+                   page: int = 64, spare_rows: int = 0) -> PagedKVCache:
         a = self.args
         max_ctx = max_ctx or min(a.max_position_embeddings, 16384)
         return PagedKVCache(a.num_hidden_layers, B, a.num_key_value_heads, a.head_dim, max_ctx,
-                            page=page, kv_bits=kv_bits, device=self.device)
+                            page=page, kv_bits=kv_bits, device=self.device, spare_rows=spare_rows)
 
     @property
     def weight_bytes(self) -> int:

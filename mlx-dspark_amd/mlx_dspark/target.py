@@ -38,8 +38,8 @@ class Target:
         self._tied = bool(model.args.tie_word_embeddings)
 
     # -- cache --
-    def make_cache(self, B: int = 1, max_ctx: int | None = None):
-        return self.model.make_cache(B, max_ctx or self.max_ctx, self.kv_bits)
+    def make_cache(self, B: int = 1, max_ctx: int | None = None, spare_rows: int = 0):
+        return self.model.make_cache(B, max_ctx or self.max_ctx, self.kv_bits, spare_rows=spare_rows)
 
     # -- forward with hidden-state tap --
     def run(self, ids, cache, tap):

@@ -27,3 +27,30 @@ def check_logits(got, want, want_alt, what=""):
           f"bound {bmax:.4f} / {brms:.5f})", flush=True)
     assert mx <= bmax and rms <= brms, (what, mx, rms, fmax, frms)
     return bmax
+
+
+STREAM_TOL = 2e-2       # top-2 margin (RMS-normalised logits) below which bf16 may flip a pick
+
+
+def check_greedy_stream(model, prompt, got, min_match: int, tol: float = STREAM_TOL, oracle=None):
+    """Teacher-forced greedy parity. The oracle runs ``prompt + got[:-1]`` in one forward; at
+    every position the engine's token must be the oracle's argmax, or within ``tol`` of the
+    oracle's best RMS-normalised logit (a near-tie that bf16 rounding may flip). Every token is
+    checked, also after such a flip, and at least ``min_match`` of them (or all) must be the
+    oracle's exact argmax, so a stream of near-ties cannot pass. Returns the exact count."""
+    got = [int(t) for t in got]
+    if not got:
+        return 0
+    ot = oracle or OM.OracleTarget(model)
+    logits, _ = ot.forward(list(prompt) + got[:-1])
+    rows = logits[len(prompt) - 1:]
+    exact = 0
+    for i, t in enumerate(got):
+        rn = rows[i] / rows[i].pow(2).mean().sqrt()
+        best = int(rn.argmax())
+        gap = float(rn[best] - rn[t])
+        assert gap <= tol, f"token {i}: {t} is {gap:.4f} below the oracle's pick {best}"
+        exact += int(t == best)
+    print(f"greedy stream: {exact}/{len(got)} tokens are the oracle's argmax, the rest within {tol}", flush=True)
+    assert exact >= min(min_match, len(got)), f"only {exact} of {len(got)} tokens are the oracle's argmax"
+    return exact

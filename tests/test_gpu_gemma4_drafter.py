@@ -8,10 +8,11 @@ import numpy as np
 import pytest
 import torch
 
-from _parity import check_logits
+from _parity import check_logits, check_greedy_stream
 from oracle import model as OM
 
 pytestmark = pytest.mark.gpu
+MIN_MATCH = 8      # leading greedy tokens that must equal the oracle's
 TOL = 2e-2
 
 
@@ -154,9 +155,5 @@ def test_speculative_generate_gemma4_drafter(dev, gemma4_pair, graph):
     print(f"spec gemma4 drafter graph={graph}", flush=True)
     res = speculative_generate(target, tok, d, prompt_ids=prompt, max_new_tokens=16, max_draft_tokens=4,
                                lookup_drafts=False, use_graph=graph)
-    ref, margins = OM.greedy_decode(OM.OracleTarget(target.model), prompt, len(res.token_ids))
-    for i, (a, b) in enumerate(zip(res.token_ids, ref)):
-        if a != b:
-            assert margins[i] <= 6e-2, (i, a, b, margins[i])
-            break
+    check_greedy_stream(target.model, prompt, res.token_ids, MIN_MATCH, tol=6e-2)
     assert res.num_tokens >= 16 and sum(res.accept_lengths) + 1 == res.num_tokens
