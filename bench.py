@@ -18,8 +18,15 @@ replay each. Printed (one JSON line):
   roofline     the dominant kernel, the W8 GEMM at the gate_up shape (24576 x 4096, SwiGLU
                epilogue): algorithmic bytes per launch over its in-graph average launch time
                (36 launches, one per layer's weights, HIP events on the launch stream)
-  cpu_baseline the CPU oracle (torch, float32) on a bounded sample: one decoder layer and the
-               vocabulary head of the verify step, scaled to a whole round
+  sampled_round_extra_us  the same rounds at temperature 0.6 / top-p 0.95 / top-k 20 (draft
+               rows drawn, speculative-sampling acceptance), minus the greedy round time
+  acc_us       the standalone acceptance workload [4, 17, 151936] fp32 (T = 1, top-p 0.95),
+               graph-replayed, with its HBM roofline fraction
+  q06          the Qwen3-0.6B-shaped workload end to end (DSpark block 8, 256 new tokens)
+  cpu_baseline the CPU oracle (torch, float32 with bf16 rounding points) on the host cores:
+               value = accepted tok/s of 5 whole DFlash rounds on the same weights (random
+               4096-position context); q06 = the Q06 workload end to end on the same prompt;
+               acc = the acceptance workload, outputs compared with the GPU's
 """
 
 from __future__ import annotations
@@ -147,9 +154,12 @@ def acc_timing(reps: int = 50):
     torch.cuda.synchronize()
     us = s_ev.elapsed_time(e_ev) * 1e3 / reps
     nbytes = (p.numel() + q.numel()) * 4
+    word.zero_()                                  # offset 0: the outputs the CPU leg reproduces
+    run()
     return {"us": round(us, 2), "bytes": int(nbytes), "GBs": round(nbytes / us / 1e3, 1),
             "roofline_frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4),
-            "config": "B=4, 16 drafts + bonus, V=151936 fp32, T=1, top_p=0.95, top_k=0"}
+            "config": "B=4, 16 drafts + bonus, V=151936 fp32, T=1, top_p=0.95, top_k=0",
+            "n": n.tolist(), "token": tok.tolist()}
 
 
 def copy_calibration(nbytes: int = 256 << 20) -> None:
@@ -164,67 +174,147 @@ def copy_calibration(nbytes: int = 256 << 20) -> None:
     torch.cuda.synchronize()
 
 
-def cpu_baseline(tgt_args, dev_model_seed: int, ctx: int, W: int, mean_accept: float, budget_s: float = 12.0):
-    """The oracle (torch on the host CPU, float32 with bf16 rounding points) on one decoder
-    layer + the vocabulary head of one verify step at the same shapes; a round is scaled as
-    (target layers + drafter layers) * t_layer + 2 * t_head (target verify head + drafter head)."""
-    import types
+def _cores() -> int:
+    return len(os.sched_getaffinity(0))
 
-    import numpy as np
+
+def cpu_q8_rounds(model, drafter, dcfg, ctx: int, cap: int, kv_bits, rounds: int = 5):
+    """The oracle (torch on the host CPU, float32 with bf16 rounding points) running whole
+    greedy DFlash rounds on the bench's own target and drafter weights: drafter block over its
+    context, a 16-row verify of all 36 layers over a ctx-position 8-bit KV context, acceptance
+    and rollback. Both the target's KV and the drafter's context hold seeded random rows (an
+    oracle prefill of the 4096-token prompt would take hours on the CPU); one warm-up round,
+    then ``rounds`` timed rounds."""
     import torch
 
-    from mlx_dspark import synthetic
     from oracle import model as OM
+    from oracle import spec as SP
 
-    ncores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(ncores)
-    a = tgt_args
-    H, I = a.hidden_size, a.intermediate_size
-    nq, nkv, hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
-
-    def mlx(N, K, name):
-        w = synthetic.randn((N, K), dev_model_seed, name, "cuda")
-        from mlx_dspark.ops import W8Weight
-        q, s, b = W8Weight.quantize_mlx(w)
-        o = types.SimpleNamespace(mlx=(q.cpu(), s.cpu(), b.cpu()))
-        return o
-
-    ones = lambda n: torch.ones(n, dtype=torch.bfloat16)
-    qk = lambda: torch.full((hd,), hd ** -0.25).to(torch.bfloat16)
-    layer = types.SimpleNamespace(qkv=mlx(a.n_qkv, H, "layers.0.qkv"), o=mlx(H, nq * hd, "layers.0.o"),
-                                  gate_up=mlx(2 * I, H, "layers.0.gate_up"), down=mlx(H, I, "layers.0.down"),
-                                  in_norm=ones(H), post_norm=ones(H), q_norm=qk(), k_norm=qk())
-    emb = mlx(a.vocab_size, H, "embed_tokens").mlx
-    head = mlx(a.vocab_size, H, "lm_head")
-    m = types.SimpleNamespace(args=a, layers=[layer], embed=types.SimpleNamespace(q=emb[0], s=emb[1], b=emb[2]),
-                              lm_head=head, norm=ones(H))
-    ref = OM.OracleTarget(m)
-    g = torch.Generator().manual_seed(0)
-    t_all, t_head = [], []
-    ids = torch.randint(0, a.vocab_size, (W,), generator=g)
-    t_start = time.perf_counter()
-    while len(t_all) < 3 or time.perf_counter() - t_start < budget_s:
-        ref.K = [OM.bf(torch.randn(ctx, nkv, hd, generator=g))]
-        ref.V = [OM.bf(torch.randn(ctx, nkv, hd, generator=g))]
-        ref.offset = ctx
+    torch.set_num_threads(_cores())
+    t0 = time.perf_counter()
+    tgt = OM.OracleTarget(model, kv_bits=kv_bits)
+    od = OM.OracleDFlash(drafter, tgt)
+    build_s = time.perf_counter() - t0
+    a = model.args
+    g = torch.Generator().manual_seed(5)
+    for l in range(len(tgt.layers)):
+        tgt.K[l] = OM.bf(torch.randn(ctx, a.num_key_value_heads, a.head_dim, generator=g))
+        tgt.V[l] = OM.bf(torch.randn(ctx, a.num_key_value_heads, a.head_dim, generator=g))
+    tgt.offset = ctx
+    c = dcfg
+    for l in range(len(od.layers)):
+        od.K[l] = OM.bf(torch.randn(ctx, c.num_key_value_heads, c.head_dim, generator=g))
+        od.V[l] = OM.bf(torch.randn(ctx, c.num_key_value_heads, c.head_dim, generator=g))
+    tap = list(c.target_layer_ids)
+    new_ctx = OM.bf(torch.randn(1, len(tap) * a.hidden_size, generator=g))
+    pending = 1
+    times, accepted = [], []
+    for r in range(rounds + 1):
         t0 = time.perf_counter()
-        ref.forward(ids)
-        t_all.append(time.perf_counter() - t0)
-        x = torch.randn(W, H, generator=g)
+        n, token, drafts, new_ctx = SP.dflash_round(tgt, od, pending, new_ctx, cap, tap, int(c.mask_token_id),
+                                                     int(c.block_size))
+        dt = time.perf_counter() - t0
+        pending = token
+        if r:
+            times.append(dt)
+            accepted.append(n + 1)
+    # the verify forward alone, three times (rolled back each time)
+    vt = []
+    for _ in range(3):
+        ids = torch.randint(0, a.vocab_size, (cap + 1,), generator=g).tolist()
         t0 = time.perf_counter()
-        _ = OM.bf(x) @ ref.lm_head.T
-        t_head.append(time.perf_counter() - t0)
-    ta, th = statistics.median(t_all), statistics.median(t_head)
-    t_layer = max(ta - th, 1e-6)
-    n_layers_round = a.num_hidden_layers + 2
-    t_round = n_layers_round * t_layer + 2 * th
-    sample_s = sum(t_all) + sum(t_head)
-    return {"value": round(mean_accept / t_round, 4), "unit": "accepted tok/s", "cores": ncores, "kind": "port",
-            "sample": (f"oracle (torch fp32, bf16 rounding points) timed on 1 of {a.num_hidden_layers} decoder "
-                       f"layers + the {a.vocab_size}-row head for one {W}-row verify at {ctx} context "
-                       f"(median of {len(t_all)}, {sample_s:.1f} s of CPU work); round = "
-                       f"{n_layers_round} layers x {t_layer * 1e3:.1f} ms + 2 heads x {th * 1e3:.1f} ms = "
-                       f"{t_round * 1e3:.0f} ms, x mean accept length {mean_accept:.2f}")}
+        tgt.forward(ids, tap)
+        vt.append(time.perf_counter() - t0)
+        tgt.trim(cap + 1)
+    secs = sum(times)
+    return {"value": round(sum(accepted) / secs, 4), "unit": "accepted tok/s", "cores": _cores(), "kind": "port",
+            "sample": (f"oracle (torch fp32, bf16 rounding points): {rounds} whole greedy DFlash rounds after one "
+                       f"warm-up on the bench's weights (36-layer target verify of {cap + 1} rows over a "
+                       f"{ctx}-position {'8-bit' if kv_bits else 'bf16'} KV context of seeded random rows, "
+                       f"2-layer drafter block, 151936-row heads), {secs:.1f} s of CPU work; median round "
+                       f"{statistics.median(times) * 1e3:.0f} ms, mean accept length "
+                       f"{sum(accepted) / len(accepted):.2f}; build (dequantize to fp32) {build_s:.0f} s"),
+            "round_ms": round(statistics.median(times) * 1e3, 1),
+            "verify_ms": round(statistics.median(vt) * 1e3, 1)}
+
+
+def q06_models(seed: int = 6):
+    """The Qwen3-0.6B-shaped W8 target and its 1-layer DSpark drafter (taps 1, 14, 27,
+    block 8), kept with their MLX-layout codes for the oracle."""
+    from mlx_dspark import synthetic
+    from mlx_dspark.target import Target
+    from mlx_dspark.tokenizer import SyntheticTokenizer
+
+    model = synthetic.build_target("qwen3-0.6b", seed=seed, keep_mlx=True)
+    d, cfg = synthetic.build_dspark(model.args, seed=seed + 1, keep_mlx=True, num_hidden_layers=1, block_size=8,
+                                    taps=[1, 14, 27])
+    tok = SyntheticTokenizer(model.args.vocab_size)
+    return Target(model, tok), tok, d, cfg
+
+
+Q06_PROMPT, Q06_NEW = 512, 256
+
+
+def q06_gpu(target, tok, d) -> dict:
+    """Q06 end to end on the GPU: greedy DSpark decoding, block 8 (8 drafts verified per round,
+    W = 9), lookup drafts off, 256 new tokens after a 512-token prompt; one untimed run first
+    (graph capture), then one timed run."""
+    import numpy as np
+
+    from mlx_dspark.generate import speculative_generate
+    prompt = np.random.default_rng(512).integers(0, target.model.args.vocab_size, Q06_PROMPT).tolist()
+    kw = dict(prompt_ids=prompt, max_new_tokens=Q06_NEW, max_draft_tokens=8, lookup_drafts=False)
+    speculative_generate(target, tok, d, **kw)
+    res = speculative_generate(target, tok, d, **kw)
+    return {"tok_s": round(res.num_tokens / res.seconds, 1), "accept_len": round(res.mean_accept_len, 3),
+            "tokens": res.token_ids, "seconds": round(res.seconds, 4), "prompt": prompt}
+
+
+def cpu_q06(target, d, cfg, prompt) -> dict:
+    """Q06 end to end on the oracle: the same prompt, drafter and settings as ``q06_gpu``."""
+    import torch
+
+    from oracle import model as OM
+    from oracle import spec as SP
+
+    torch.set_num_threads(_cores())
+    tgt, od = OM.OracleTarget(target.model), OM.OracleDSpark(d)
+    t0 = time.perf_counter()
+    toks, accepts = SP.dspark_generate(tgt, od, prompt, Q06_NEW, 8, list(cfg.target_layer_ids),
+                                       int(cfg.mask_token_id), int(cfg.block_size))
+    secs = time.perf_counter() - t0
+    return {"tok_s": round(len(toks) / secs, 2), "accept_len": round(len(toks) / max(1, len(accepts)), 3),
+            "seconds": round(secs, 1), "tokens": toks}
+
+
+def q06_teacher_forced(target, prompt, tokens) -> dict:
+    """The oracle's verdict on the GPU's Q06 stream: one oracle forward over prompt + stream
+    (teacher forcing); how many GPU tokens are the oracle's argmax, and the largest gap between
+    the oracle's best RMS-normalised logit and the GPU token's."""
+    from oracle import model as OM
+    logits, _ = OM.OracleTarget(target.model).forward(list(prompt) + list(tokens[:-1]))
+    rows = logits[len(prompt) - 1:]
+    rn = rows / rows.pow(2).mean(-1, keepdim=True).sqrt()
+    import torch
+    t = torch.tensor(tokens)
+    gap = (rn.max(-1).values - rn.gather(1, t[:, None])[:, 0])
+    return {"oracle_argmax": int((gap == 0).sum()), "of": len(tokens), "max_gap": round(float(gap.max()), 4)}
+
+
+def cpu_acc(gpu_out=None, reps: int = 3) -> dict:
+    """The acceptance oracle (C, one thread) on the standalone acceptance workload: median of
+    ``reps`` runs; outputs compared with the GPU's on the same inputs and Philox (seed, offset)."""
+    from oracle import accept as A
+    p, q, draft = (t.numpy() for t in acc_inputs())
+    times, res = [], None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        res = A.accept_sample(p, q, draft, 1.0, 0.95, 0, seed=7, offset=0)
+        times.append(time.perf_counter() - t0)
+    out = {"ms": round(statistics.median(times) * 1e3, 1), "cores": 1}
+    if gpu_out is not None:
+        out["bit_exact_vs_gpu"] = bool(list(res["n"]) == gpu_out["n"] and list(res["token"]) == gpu_out["token"])
+    return out
 
 
 def main(argv=None) -> int:
@@ -242,6 +332,9 @@ def main(argv=None) -> int:
                     help="build the target, time the W8 GEMM shapes and a 256 MiB copy only (counter runs)")
     ap.add_argument("--acc-only", action="store_true",
                     help="time the standalone acceptance workload [4, 17, 151936] only")
+    ap.add_argument("--verify-eager", type=int, default=0, metavar="N",
+                    help="build the target, prefill the context, run N eager verify forwards and exit "
+                         "(one kernel launch per op: for counter collection)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this engine has no multi-GPU path (run with --gpus 1)",
@@ -262,8 +355,9 @@ def main(argv=None) -> int:
         print(json.dumps({"acc": acc_timing()}), flush=True)
         return 0
     t_build = time.time()
-    model = synthetic.build_target(args.target, seed=0)
-    drafter, dcfg = synthetic.build_dflash(model.args, seed=1, block_size=args.block, n_taps=5, bits=4)
+    keep = not args.no_cpu_baseline            # the oracle reads the MLX-layout codes
+    model = synthetic.build_target(args.target, seed=0, keep_mlx=keep)
+    drafter, dcfg = synthetic.build_dflash(model.args, seed=1, block_size=args.block, n_taps=5, bits=4, keep_mlx=keep)
     drafter.bind(model)
     log(f"built {args.target} W8 target ({model.weight_bytes / 1e9:.2f} GB) + DFlash drafter in "
         f"{time.time() - t_build:.1f} s")
@@ -276,13 +370,31 @@ def main(argv=None) -> int:
     target = Target(model, tok, kv_bits=kv_bits)
     cap = args.block - 1
     W = cap + 1
-    rounds_total = args.steps + args.warmup + 2
+    rounds_total = 2 * (args.steps + args.warmup) + 2          # greedy rounds, then sampled rounds
     max_ctx = args.ctx + W * (rounds_total + 2) + 64
     cache = target.make_cache(max_ctx=max_ctx)
     dcache = drafter.make_cache(max_ctx=max_ctx)
     prompt = np.random.default_rng(1234).integers(0, model.args.vocab_size, args.ctx).tolist()
     t0 = time.time()
     tap = list(dcfg.target_layer_ids)
+    if args.verify_eager:
+        # seeded random context written straight into the KV pools (no prefill), then eager
+        # verify forwards: every op is its own launch
+        g = torch.Generator(device=model.device).manual_seed(4)
+        for l in range(model.args.num_hidden_layers):
+            for pool, sb in ((cache.k[l], cache.k_sb[l]), (cache.v[l], cache.v_sb[l])):
+                if sb is None:
+                    pool.copy_(torch.randn(pool.shape, generator=g, device=model.device).to(pool.dtype))
+                else:
+                    pool.copy_(torch.randint(0, 256, pool.shape, generator=g, device=model.device).to(pool.dtype))
+                    sb.fill_(0x3C23 | (0xBF80 << 16) - (1 << 32))     # scale bf16(0.01), bias bf16(-1)
+        cache.set_lengths([args.ctx])
+        vids = torch.randint(0, model.args.vocab_size, (1, W), dtype=torch.int32, device=model.device)
+        for _ in range(args.verify_eager):
+            model.forward(vids, cache, tap, advance=False)
+        torch.cuda.synchronize()
+        print(json.dumps({"verify_eager": args.verify_eager, "rows": W, "context": cache.lengths[0]}), flush=True)
+        return 0
     logits, fused = model.prefill(prompt, cache, tap)
     drafter.ingest(fused, dcache)
     pending = _pick(logits[0, -1], 0.0)
@@ -305,6 +417,20 @@ def main(argv=None) -> int:
     tok_s = sum(accepted) / secs
     mean_accept = sum(accepted) / len(accepted)
     log(f"{args.steps} rounds: {ms_per_step:.3f} ms/round, {tok_s:.1f} accepted tok/s, accept {mean_accept:.2f}")
+
+    # ---- the same rounds sampled (T 0.6, top-p 0.95, top-k 20: draft rows drawn, speculative
+    # sampling acceptance), graph-replayed: the extra time per round over greedy
+    srnd = _DFlashRound(target, drafter, cache, dcache, cap, 0.6, 0.95, 20, 5)
+    srnd.pending.fill_(token)
+    for r in range(args.warmup):
+        srnd.run(r, use_graph=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for r in range(args.steps):
+        srnd.run(args.warmup + r, use_graph=True)
+    torch.cuda.synchronize()
+    sampled_ms = (time.perf_counter() - t0) / args.steps * 1e3
+    log(f"sampled rounds: {sampled_ms:.3f} ms/round (+{(sampled_ms - ms_per_step) * 1e3:.0f} us over greedy)")
 
     # ---- verify step alone: one graph of the 16-row target forward (no advance: idempotent)
     L_now = cache.lengths[0]
@@ -337,11 +463,31 @@ def main(argv=None) -> int:
     achieved = dom["bytes"] / dom["us"] / 1e3
     log(f"W8 GEMM per shape: {json.dumps(shapes)}")
 
+    # ---- standalone acceptance workload and the Q06 end-to-end workload on the GPU
+    acc = acc_timing()
+    log(f"acceptance [4, 17, 151936]: {acc['us']} us ({acc['roofline_frac'] * 100:.1f}% of HBM roofline)")
+    q_target, q_tok, q_d, q_cfg = q06_models()
+    q06 = q06_gpu(q_target, q_tok, q_d)
+    log(f"qwen3-0.6b DSpark k=8 end to end: {q06['tok_s']} tok/s, accept {q06['accept_len']}")
+
     cpu = None
     if not args.no_cpu_baseline:
         t0 = time.time()
-        cpu = cpu_baseline(model.args, 0, args.ctx, W, mean_accept)
-        log(f"cpu baseline in {time.time() - t0:.1f} s: {cpu}")
+        cpu = cpu_q8_rounds(model, drafter, dcfg, args.ctx, cap, kv_bits)
+        log(f"cpu baseline, Q8 rounds in {time.time() - t0:.1f} s: {cpu['value']} tok/s")
+        t0 = time.time()
+        cq = cpu_q06(q_target, q_d, q_cfg, q06["prompt"])
+        same = 0
+        while same < min(len(cq["tokens"]), len(q06["tokens"])) and cq["tokens"][same] == q06["tokens"][same]:
+            same += 1
+        tf = q06_teacher_forced(q_target, q06["prompt"], q06["tokens"])
+        cpu["q06"] = {"tok_s": cq["tok_s"], "accept_len": cq["accept_len"], "seconds": cq["seconds"],
+                      "tokens_equal_to_gpu": same, "gpu_stream_teacher_forced": tf}
+        log(f"cpu baseline, Q06 end to end in {time.time() - t0:.1f} s: {cq['tok_s']} tok/s, "
+            f"{same} leading tokens equal to the GPU's; GPU stream under the oracle: {tf}")
+        t0 = time.time()
+        cpu["acc"] = cpu_acc({"n": acc["n"], "token": acc["token"]})
+        log(f"cpu baseline, acceptance in {time.time() - t0:.1f} s: {cpu['acc']}")
 
     line = {
         "metric": "accepted tok/s (B=1, Qwen3-8B-shape W8, k=16); verify-step us; % HBM roofline",
@@ -356,6 +502,8 @@ def main(argv=None) -> int:
                    "weights": "target W8 affine group 64 (bf16 scale/bias); DFlash drafter linears 4-bit "
                               "group 64 (the reference's drafter default)"},
         "accept_len": round(mean_accept, 3),
+        "sampled_round_ms": round(sampled_ms, 4),
+        "sampled_round_extra_us": round((sampled_ms - ms_per_step) * 1e3, 1),
         "verify_us": round(verify_us, 1),
         "verify_alg_bytes": int(alg_bytes),
         "verify_roofline_frac": round(verify_frac, 4),
@@ -363,6 +511,12 @@ def main(argv=None) -> int:
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_GATE_UP,
                      "bytes_per_launch": dom["bytes"], "us_per_launch": dom["us"], "per_shape": shapes},
+        "acc_us": acc["us"],
+        "acc_roofline_frac": acc["roofline_frac"],
+        "acc": {k: v for k, v in acc.items() if k not in ("n", "token")},
+        "q06": {"tok_s": q06["tok_s"], "accept_len": q06["accept_len"],
+                "config": "qwen3-0.6b-shape W8 + 1-layer DSpark (taps 1, 14, 27), prompt 512, block 8, greedy, "
+                          "256 new tokens, bf16 KV"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -114,19 +114,22 @@ def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
     return 0.5 * x * (1.0 + torch.tanh(0.7978845608028654 * (x + 0.044715 * x * x * x)))
 
 
+def deq_codes(q: torch.Tensor, s: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """float32 w = s * q + b per group of 64 columns (q uint8 [N, K], s / b bf16 [N, K/64]), on
+    the CPU. s * q is exact in float32 (a bf16 times an integer below 256), so the one rounding
+    of the sum gives the float32 value of oracle/w8.py's float64 dequantize, bit for bit."""
+    q, s, b = q.cpu(), s.cpu(), b.cpu()
+    N, K = q.shape
+    w = q.view(N, K // 64, 64).float() * s.float().unsqueeze(-1) + b.float().unsqueeze(-1)
+    return w.view(N, K)
+
+
 def deq(wobj) -> torch.Tensor:
-    q, s, b = wobj.mlx
-    qn = q.cpu().numpy()
-    sn = s.view(torch.int16).cpu().numpy().view(np.uint16)
-    bn = b.view(torch.int16).cpu().numpy().view(np.uint16)
-    return torch.from_numpy(W8.dequantize(qn, sn, bn).astype(np.float32))
+    return deq_codes(*wobj.mlx)
 
 
 def deq_table(t) -> torch.Tensor:
-    qn = t.q.cpu().numpy()
-    sn = t.s.view(torch.int16).cpu().numpy().view(np.uint16)
-    bn = t.b.view(torch.int16).cpu().numpy().view(np.uint16)
-    return torch.from_numpy(W8.dequantize(qn, sn, bn).astype(np.float32))
+    return deq_codes(t.q, t.s, t.b)
 
 
 def kv_quant_roundtrip(x: torch.Tensor) -> torch.Tensor:
@@ -225,7 +228,14 @@ class OracleTarget:
 
 
 class OracleDFlash:
-    """CPU DFlash drafter (src/mlx_dspark/dflash_model.py:100-208) bound to an OracleTarget."""
+    """CPU DFlash drafter (src/mlx_dspark/dflash_model.py:100-208) bound to an OracleTarget.
+
+    Full-attention layers attend over every stored context row and the whole block without a
+    mask. Sliding layers (layer_types[l] == "sliding_attention", :90-92) attend causally with
+    a window of ``sliding_window`` positions: the block query at absolute position P sees the
+    keys at positions P - window + 1 .. P (:103-109 keep the last window - 1 context rows, and
+    :128-132 mask the block causally within the window). Context K is roped at its absolute
+    position and the block after the stored context (:118-122)."""
 
     def __init__(self, drafter, target: OracleTarget, p_bf16: bool = False):
         c = drafter.config
@@ -243,6 +253,10 @@ class OracleDFlash:
     @property
     def offset(self) -> int:
         return self.K[0].shape[0]
+
+    def _sliding(self, l: int) -> bool:
+        lt = getattr(self.c, "layer_types", None) or ()
+        return l < len(lt) and lt[l] == "sliding_attention"
 
     def __call__(self, block_ids, target_hidden, logits_start=1):
         c = self.c
@@ -272,7 +286,10 @@ class OracleDFlash:
             self.V[l] = torch.cat([self.V[l], vc])
             K = torch.cat([self.K[l], kb])
             Vv = torch.cat([self.V[l], vb])
-            o = bf(sdpa(q, K, Vv, hd ** -0.5, None, self.p_bf16))
+            mask = None
+            if self._sliding(l):
+                mask = causal_mask(off + S, L, int(c.sliding_window))
+            o = bf(sdpa(q, K, Vv, hd ** -0.5, mask, self.p_bf16))
             h = bf(h + o.reshape(L, -1) @ Lw.wo.T)
             x = bf(rmsnorm(h, Lw.post_norm, eps))
             gu = bf(x @ Lw.wgu.T)
@@ -424,7 +441,9 @@ class OracleDSpark:
 
     def step_logits(self, base_row, prev):
         """bf16(bf16(base) + bf16(w2 . bf16(w1[prev])))"""
-        bias = bf(self.w2.double() @ bf(self.w1[int(prev)]).double())
+        if getattr(self, "_w2_src", None) is not self.w2:        # float64 copy, made once per table
+            self._w2d, self._w2_src = self.w2.double(), self.w2
+        bias = bf(self._w2d @ bf(self.w1[int(prev)]).double())
         return bf(bf(torch.as_tensor(base_row).float()) + bias.float())
 
     def sample_block(self, base, first_prev):

@@ -30,7 +30,8 @@ import pytest
 import torch
 
 from oracle import model as OM
-from oracle import w8 as W8
+from oracle import w8 as W8  # noqa: F401
+from _oracle_models import _dspark, _layer, _norm_w, _target, _unit, _wobj  # noqa: F401
 
 transformers = pytest.importorskip("transformers")
 from transformers import Gemma3ForCausalLM, Gemma3TextConfig, Qwen3Config, Qwen3ForCausalLM  # noqa: E402
@@ -43,50 +44,6 @@ TOL = 1e-5   # normalized max-abs difference allowed between two float32 evaluat
 def no_rounding(monkeypatch):
     """The oracle with every bf16 rounding point switched off (float32 throughout)."""
     monkeypatch.setattr(OM, "bf", lambda x: x)
-
-
-def _wobj(w):
-    q, s, b = W8.quantize(w.numpy())
-    t = lambda x: torch.from_numpy(x.view(np.int16).copy()).view(torch.bfloat16)
-    return types.SimpleNamespace(mlx=(torch.from_numpy(q), t(s), t(b)))
-
-
-def _table(w):
-    o = _wobj(w)
-    return types.SimpleNamespace(q=o.mlx[0], s=o.mlx[1], b=o.mlx[2], mlx=o.mlx)
-
-
-def _norm_w(n, g):
-    return (1.0 + 0.3 * torch.randn(n, generator=g)).to(torch.bfloat16)
-
-
-def _unit(n):
-    return torch.ones(n, dtype=torch.bfloat16)
-
-
-def _layer(g, H, I, nq, nkv, hd, *, sandwich=False, unit_in=False, k_eq_v=False):
-    if k_eq_v:
-        wk = 0.05 * torch.randn(nkv * hd, H, generator=g)
-        qkv = _wobj(torch.cat([0.05 * torch.randn(nq * hd, H, generator=g), wk, wk]))
-    else:
-        qkv = _wobj(0.05 * torch.randn((nq + 2 * nkv) * hd, H, generator=g))
-    return types.SimpleNamespace(
-        qkv=qkv, o=_wobj(0.05 * torch.randn(H, nq * hd, generator=g)),
-        gate_up=_wobj(0.05 * torch.randn(2 * I, H, generator=g)), down=_wobj(0.05 * torch.randn(H, I, generator=g)),
-        in_norm=_unit(H) if unit_in else _norm_w(H, g), post_norm=_norm_w(H, g), q_norm=_norm_w(hd, g),
-        k_norm=_norm_w(hd, g), attn_out_norm=_norm_w(H, g) if sandwich else None,
-        ff_out_norm=_norm_w(H, g) if sandwich else None)
-
-
-def _target(a, g):
-    from mlx_dspark.qwen3 import TargetArgs  # noqa: F401  (the host-side config type)
-    H, I = a.hidden_size, a.intermediate_size
-    layers = [_layer(g, H, I, a.num_attention_heads, a.num_key_value_heads, a.head_dim, sandwich=a.sandwich_norms)
-              for _ in range(a.num_hidden_layers)]
-    emb = _table(0.5 * torch.randn(a.vocab_size, H, generator=g))
-    head = types.SimpleNamespace(mlx=emb.mlx) if a.tie_word_embeddings else _wobj(
-        0.05 * torch.randn(a.vocab_size, H, generator=g))
-    return types.SimpleNamespace(args=a, layers=layers, embed=emb, lm_head=head, norm=_norm_w(H, g))
 
 
 def _attn_sd(L, nq, nkv, hd, shift=0.0):
@@ -211,34 +168,43 @@ def _qwen3_stack(layers, H, I, nq, nkv, hd, eps, theta):
     return cfg, out
 
 
-def _run_qwen3_stack(cfg, stack, ctx, h, shift=0):
-    """Each layer over [ctx; h] without a mask at positions 0.. (the block rows' positions
-    moved by `shift`); the block rows carry on, the context rows restart every layer."""
+def _run_qwen3_stack(cfg, stack, ctx, h, shift=0, windows=None):
+    """Each layer over [ctx; h] at positions 0.. (the block rows' positions moved by `shift`):
+    without a mask, or, where windows[l] > 0, causal with that window (an additive mask); the
+    block rows carry on, the context rows restart every layer."""
     rot = Qwen3RotaryEmbedding(cfg)
     S = ctx.shape[0]
-    for d in stack:
+    for l, d in enumerate(stack):
         x = torch.cat([ctx, h])[None]
         pos = torch.arange(x.shape[1])
         pos[S:] += shift
+        mask = None
+        if windows and windows[l]:
+            r, c = pos[:, None], pos[None, :]
+            ok = (c <= r) & (r - c < windows[l])
+            mask = torch.zeros(ok.shape).masked_fill(~ok, float("-inf"))[None, None]
         pos = pos[None]
-        y = d(x, attention_mask=None, position_ids=pos, position_embeddings=rot(x, pos))
+        y = d(x, attention_mask=mask, position_ids=pos, position_embeddings=rot(x, pos))
         y = y[0] if isinstance(y, tuple) else y
         h = y[0, S:]
     return h
 
 
-@pytest.mark.parametrize("with_ctx", [False, True])
-def test_dflash_equals_qwen3_layer_stack(with_ctx):
+@pytest.mark.parametrize("with_ctx,window", [(False, 0), (True, 0), (True, 4)])
+def test_dflash_equals_qwen3_layer_stack(with_ctx, window):
+    """window > 0: layer 0 is a sliding layer (dflash_model.py:103-109, :128-132), layer 1 full."""
     from mlx_dspark.qwen3 import TargetArgs
-    g = torch.Generator().manual_seed(10 + with_ctx)
+    g = torch.Generator().manual_seed(10 + with_ctx + window)
     a = TargetArgs(model_type="qwen3", hidden_size=256, num_hidden_layers=2, intermediate_size=384,
                    num_attention_heads=4, num_key_value_heads=2, head_dim=64, vocab_size=500)
     tgt = OM.OracleTarget(_target(a, g))
     H, I, nq, nkv, hd = 256, 384, 4, 2, 64
     eps = 0.0 if with_ctx else 1e-6
     layers = [_layer(g, H, I, nq, nkv, hd, unit_in=with_ctx) for _ in range(2)]
+    lt = ("sliding_attention", "full_attention") if window else ()
     c = types.SimpleNamespace(num_attention_heads=nq, num_key_value_heads=nkv, head_dim=hd, rms_norm_eps=eps,
-                              rope_theta=1e6)
+                              rope_theta=1e6, layer_types=lt, sliding_window=window or None)
+    wins = [window, 0] if window else None
     drafter = types.SimpleNamespace(config=c, fc=_wobj(0.05 * torch.randn(H, 2 * H, generator=g)),
                                     hidden_norm=_unit(H) if with_ctx else _norm_w(H, g), norm=_norm_w(H, g),
                                     layers=layers)
@@ -252,35 +218,17 @@ def test_dflash_equals_qwen3_layer_stack(with_ctx):
         with torch.no_grad():
             got = od(ids, th, logits_start=1)
             ctx = torch.cat([ctx, OM.rmsnorm(th @ fc.T, hn, eps)])
-            want = OM.rmsnorm(_run_qwen3_stack(cfg, stack, ctx, tgt.embed[ids])[1:], nw, eps) @ tgt.lm_head.T
+            want = OM.rmsnorm(_run_qwen3_stack(cfg, stack, ctx, tgt.embed[ids], windows=wins)[1:], nw, eps) \
+                @ tgt.lm_head.T
             assert OM.normalized_maxdiff(got, want) < TOL
-    if with_ctx:   # planted mistake: the block roped at the context's offset instead of after it
-        with torch.no_grad():
-            bad = OM.rmsnorm(_run_qwen3_stack(cfg, stack, ctx, tgt.embed[ids], shift=-3)[1:], nw, eps) @ tgt.lm_head.T
-        assert OM.normalized_maxdiff(got, bad) > 1e-3
-
-
-def _dspark(g, family, H, I, V, eps, unit):
-    from mlx_dspark.config import DSparkConfig
-    gemma = family == "gemma4"
-    if gemma:
-        c = DSparkConfig(family="gemma4", hidden_size=H, vocab_size=V, num_hidden_layers=2, intermediate_size=I,
-                         rms_norm_eps=eps, num_attention_heads=4, num_key_value_heads=2, num_global_key_value_heads=1,
-                         head_dim=64, global_head_dim=512, attention_k_eq_v=True, rope_theta=1e6,
-                         partial_rotary_factor=0.25, rope_type="proportional", final_logit_softcapping=30.0,
-                         use_v_norm=True)
-    else:
-        c = DSparkConfig(family="qwen3", hidden_size=H, vocab_size=V, num_hidden_layers=2, intermediate_size=I,
-                         rms_norm_eps=eps, num_attention_heads=4, num_key_value_heads=2, head_dim=64,
-                         attention_k_eq_v=False, rope_theta=1e6, rope_type="default", final_logit_softcapping=None,
-                         use_v_norm=False, norm_style="qwen", mlp_activation="silu")
-    nq, nkv, hd = c.num_attention_heads, c.n_kv_heads, c.attn_head_dim
-    layers = [_layer(g, H, I, nq, nkv, hd, sandwich=gemma, unit_in=unit, k_eq_v=gemma) for _ in range(2)]
-    return types.SimpleNamespace(
-        config=c, layer_scalars=[0.75, 1.25] if gemma else None,
-        embed_tokens=_table(0.5 * torch.randn(V, H, generator=g)), fc=_wobj(0.05 * torch.randn(H, 2 * H, generator=g)),
-        hidden_norm=_unit(H) if unit else _norm_w(H, g), norm=_norm_w(H, g),
-        lm_head=_wobj(0.05 * torch.randn(V, H, generator=g)), layers=layers, markov_head=None, confidence_head=None)
+    if with_ctx:   # planted mistakes: the block roped at the context's offset instead of after it;
+        with torch.no_grad():   # a window one position longer; no window at all
+            bad = [_run_qwen3_stack(cfg, stack, ctx, tgt.embed[ids], shift=-3, windows=wins)]
+            if window:
+                bad += [_run_qwen3_stack(cfg, stack, ctx, tgt.embed[ids], windows=[window + 1, 0]),
+                        _run_qwen3_stack(cfg, stack, ctx, tgt.embed[ids])]
+        for hb in bad:
+            assert OM.normalized_maxdiff(got, OM.rmsnorm(hb[1:], nw, eps) @ tgt.lm_head.T) > 1e-3
 
 
 def _gemma4_stack(d):

@@ -51,3 +51,23 @@ def test_gemm_matches_bruteforce_dot():
         for n in range(8):
             ref = sum(float(x[m, k]) * (sf[n, k // 64] * int(q[n, k]) + bf[n, k // 64]) for k in range(128))
             assert abs(y[m, n] - ref) < 1e-9 * max(1.0, abs(ref))
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_torch_dequant_equals_float64_dequant(bits):
+    """The oracle models dequantize with float32 torch ops; that equals the float64 restatement
+    rounded to float32, bit for bit (s * q is exact in float32)."""
+    import torch
+
+    from oracle.model import deq_codes
+    rng = np.random.default_rng(bits)
+    N, K = 96, 512
+    q = rng.integers(0, 1 << bits, (N, K)).astype(np.uint8)
+    scale = (rng.standard_normal((N, K // 64)) * 10.0 ** rng.integers(-6, 1, (N, K // 64))).astype(np.float32)
+    bias = (rng.standard_normal((N, K // 64)) * 10.0 ** rng.integers(-6, 1, (N, K // 64))).astype(np.float32)
+    s16, b16 = w8.bf16_bits(np.abs(scale)), w8.bf16_bits(bias)
+    want = w8.dequantize(q, s16, b16).astype(np.float32)
+    st = torch.from_numpy(s16.view(np.int16)).view(torch.bfloat16)
+    bt = torch.from_numpy(b16.view(np.int16)).view(torch.bfloat16)
+    got = deq_codes(torch.from_numpy(q), st, bt).numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
