@@ -120,11 +120,42 @@ int dsk_act_pack_scaled(const float* part, int nsplit, const uint16_t* part_norm
  *   Gemma layers), ready as the next GEMM's x.
  * No workspace; no state is kept between calls.
  * ------------------------------------------------------------------------------------- */
-enum { DSK_EPI_STORE = 0, DSK_EPI_SWIGLU = 1, DSK_EPI_GEGLU = 2, DSK_EPI_PARTIAL = 3 };
+enum { DSK_EPI_STORE = 0, DSK_EPI_SWIGLU = 1, DSK_EPI_GEGLU = 2, DSK_EPI_PARTIAL = 3, DSK_EPI_RESIDUAL = 4 };
 int dsk_w8_gemm_splits(int M, int64_t N, int64_t K);
 int dsk_w8_gemm(const uint16_t* x, const uint8_t* wt, const uint32_t* sb, int M, int64_t N,
                 int64_t K, int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
                 int64_t ldr, float softcap, dsk_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Normed-later activations: the RMSNorm that precedes a projection applied after it.
+ * Replaces, for the Qwen3 layout, the chain residual add -> mx.fast.rms_norm -> quantized
+ * matmul of every decoder layer (input / post-attention norms inside mlx_lm, reached from the
+ * layer loop of src/mlx_dspark/target.py:66-67) and the final norm before the head
+ * (target.py:70-74). RMSNorm(h) . W^T = r * (bf16(h * w) . W^T) with r = rsqrt(mean(h^2) + eps)
+ * per row, so the producer of h writes x = bf16(h * w) packed plus per-16-column partial sums
+ * of h^2, ssq[m][k / 16] (fp32, [M][K / 16]), and the consuming GEMM multiplies each output of
+ * row m by r_m = rsqrt(sum_t ssq[m][t] / K + eps) before its epilogue (the partials summed
+ * in tile order t, t + 64, ... per lane, then across the wave: the same order in every
+ * kernel). Each 16-column partial is the balanced tree ((h0^2 + h1^2) + (h2^2 + h3^2)) + ...
+ *
+ * dsk_act_pack_rn: dsk_act_pack's residual add (part may be NULL: v = h), then copy[m][k] = v,
+ *   out = packed bf16(v * norm_w[k]) (norm_w NULL: v) and ssq_out[k / 16][m].
+ * dsk_w8_gemm_rn: dsk_w8_gemm (bits 8) or dsk_w4_gemm (bits 4) whose x is normed later when
+ *   x_ssq != NULL (x_tiles = K / 16 partials of x's rows, eps the norm's epsilon), plus
+ *   epi = DSK_EPI_RESIDUAL (o_proj / down_proj and the residual add after them): no K split;
+ *   h[m][n] = bf16(h[m][n] + y) in place (row stride ldh), copy[m][n] = h (row stride ldc,
+ *   or NULL: hidden-state tap, target.py:68-69), y = packed bf16(h * next_norm_w[n]) (the
+ *   next projection's x, normed later; next_norm_w NULL: h; y may be NULL) and ssq_out as
+ *   above. N % 64 == 0; the other limits are dsk_w8_gemm's.
+ * ------------------------------------------------------------------------------------- */
+int dsk_act_pack_rn(const float* part, int nsplit, uint16_t* h, int64_t ldh, uint16_t* copy,
+                    int64_t ldc, int M, int64_t K, const uint16_t* norm_w, uint16_t* out,
+                    float* ssq_out, dsk_stream_t stream);
+int dsk_w8_gemm_rn(const uint16_t* x, const uint8_t* wt, const uint32_t* sb, int bits, int M,
+                   int64_t N, int64_t K, int epi, void* y, int y_dtype, int64_t ldy, float softcap,
+                   const float* x_ssq, int x_tiles, float eps, uint16_t* h, int64_t ldh,
+                   uint16_t* copy, int64_t ldc, const uint16_t* next_norm_w, float* ssq_out,
+                   dsk_stream_t stream);
 
 /* 4-bit codes (MLX nn.quantize bits=4, group 64: the reference's drafter default,
  * src/mlx_dspark/load.py:155-215, :224-289 with bits=4; 4-bit target checkpoints).

@@ -181,6 +181,8 @@ struct PackArgs {
   uint16_t* out;       // packed, or null
   const uint16_t* res_norm_w;  // RMSNorm of the partial sum before the residual add, or null
   float out_scale;             // the residual-stream result is multiplied by this (rounded again)
+  float* ssq_out;              // normed later: out = bf16(v * norm_w), ssq_out[m][k / 16] = sum of
+                               // the 16 columns' v^2 (the consuming GEMM applies the row scale)
 };
 
 template <int NV, int MAXS>
@@ -268,7 +270,24 @@ __global__ __launch_bounds__(kPackThreads) void act_pack_kernel(PackArgs a) {
     v[i] = *reinterpret_cast<const u32x4*>(o);
   }
   float r = 1.0f;
-  if (a.norm_w) {
+  if (a.ssq_out) {
+    // per 16-column tile: this thread's 8 columns as ((v0 + v1) + (v2 + v3)) + ((v4 + v5) + ...),
+    // plus the neighbouring thread's 8 (the GEMM epilogue's 16-lane tree, in the same order)
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = tid + (int64_t)i * kPackThreads;
+      const uint16_t* hv2 = reinterpret_cast<const uint16_t*>(&v[i]);
+      float q[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = c < nchunk ? bf16_to_f32(hv2[e]) : 0.0f;
+        q[e] = f * f;
+      }
+      float t8 = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+      t8 += __shfl_xor(t8, 1, 64);
+      if (c < nchunk && (c & 1) == 0) a.ssq_out[(int64_t)m * (a.K / 16) + (c >> 1)] = t8;
+    }
+  } else if (a.norm_w) {
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -345,7 +364,31 @@ struct GemmArgs {
   int64_t ldr;
   float softcap;
   int bits;         // weight code width: 8 (dsk_w8_gemm) or 4 (dsk_w4_gemm)
+  // RMSNorm of x applied after the product (x = bf16(h * w) packed): every output of row m is
+  // multiplied by r_m = rsqrt(sum_{t < rs_tiles} rs_ssq[m * rs_tiles + t] / K + rs_eps) first
+  const float* rs_ssq;
+  int rs_tiles;
+  float rs_eps;
+  // DSK_EPI_RESIDUAL: h[m][n] = bf16(h[m][n] + y) in place (row stride ldh), copy[m][n] = h
+  // (tap, row stride ldc), y = packed bf16(h * g[n]) (or h when g is null; y may be null) and
+  // ssq_out[m][tile] = sum over the tile's 16 columns of h^2 (row stride N / 16)
+  uint16_t* h;
+  int64_t ldh;
+  uint16_t* copy;
+  int64_t ldc;
+  const uint16_t* g;
+  float* ssq_out;
 };
+
+// Sum of 16 values held by 16 consecutive lanes (the same balanced tree in every lane):
+// ((v0 + v1) + (v2 + v3)) + ... ; dsk_act_pack's normed-later path sums 8 + 8 the same way.
+__device__ __forceinline__ float sum16_lanes(float v) {
+  v += __shfl_xor(v, 1, 64);
+  v += __shfl_xor(v, 2, 64);
+  v += __shfl_xor(v, 4, 64);
+  v += __shfl_xor(v, 8, 64);
+  return v;
+}
 
 __device__ __forceinline__ void gemm_store(const GemmArgs& a, int m, int64_t n, float v) {
   if (a.res) v += bf16_to_f32(a.res[(int64_t)m * a.ldr + n]);
@@ -462,8 +505,12 @@ __device__ __forceinline__ void batch_compute(const Batch<MT, NT, U, BITS>& r, f
 // wave loads feeds NT tiles), then reduce through LDS in wave order.
 // EK: the epilogue family (0 store, 1 gated, 2 split-K partial) as a template parameter, so each
 // family is its own (smaller) kernel. PF: software-pipelined batch loads (two register sets).
-template <int MT, int NT, int U, int WAVES, int EK, bool PF, int BITS>
+// EKR = EK + 4 * RS: RS, the row scale of a normed-later x, is compiled into its own kernels
+// (its registers would otherwise weigh on every plan).
+template <int MT, int NT, int U, int WAVES, int EKR, bool PF, int BITS>
 __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
+  constexpr int EK = EKR & 3;
+  constexpr bool RS = EKR >= 4;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int slab = blockIdx.x / a.SK, ks = blockIdx.x % a.SK;
@@ -478,12 +525,61 @@ __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
 
+  // Row scales of x: wave w owns rows w, w + WAVES, ...; lane l sums the tile partials
+  // l, l + 64, l + 128, ... in that order, then the wave sums its lanes (the same order for
+  // every plan). The first 256 partials of each row go straight from memory into LDS before the
+  // main loop (global_load_lds: no registers held across it); the barrier before the epilogue
+  // waits for them.
+  constexpr int RPW = (MT * 16 + WAVES - 1) / WAVES;
+  constexpr int PRE = MT == 1 ? 4 : 0;  // 64-partial blocks per row staged in LDS (one row tile)
+  __shared__ float ssq_lds[RS && PRE ? MT * 16 * 64 * PRE : 1];
+  if constexpr (RS && PRE > 0) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int m = wave + WAVES * i;
+      if (m >= MT * 16) break;
+#pragma unroll
+      for (int j = 0; j < PRE; ++j) {
+        const int t = lane + 64 * j;
+        // lanes past the row count or the tile count load a valid word that is never summed
+        const float* src = (m < a.M && t < a.rs_tiles) ? a.rs_ssq + (int64_t)m * a.rs_tiles + t : a.rs_ssq;
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(ssq_lds + (m * PRE + j) * 64),
+                                         4, 0, 0);
+      }
+    }
+  }
+
+  // residual epilogue: the residual h and the next norm's gain of each output this thread
+  // stores, loaded before the main loop (after it they would cost two more memory round trips)
+  constexpr int NOUT = MT * NT * 256;
+  constexpr int PL = EK == 3 ? (NOUT + WAVES * 64 - 1) / (WAVES * 64) : 1;
+  uint16_t hpre[PL], gpre[PL];
+  if constexpr (EK == 3) {
+#pragma unroll
+    for (int u = 0; u < PL; ++u) {
+      const int o = threadIdx.x + u * WAVES * 64;
+      const int i = (o >> 8) / NT, j = (o >> 8) % NT;
+      const int m = i * 16 + ((o & 63) >> 4) * 4 + ((o >> 6) & 3);
+      const int64_t n = (t0 + j) * 16 + (o & 15);
+      const bool live = o < NOUT && m < a.M;
+      hpre[u] = live ? a.h[(int64_t)m * a.ldh + n] : 0;
+      gpre[u] = (live && a.g) ? a.g[n] : 0;
+    }
+  }
+
   if constexpr (PF) {
     // software pipeline over the wave's batches (bt = wave, wave + WAVES, ...): the next
     // batch's loads are issued before the current one is computed, alternating two register sets
     if (wave < nbatch) {
       Batch<MT, NT, U, BITS> ra, rb;
       batch_load<MT, NT, U, BITS>(a, t0, g_lo + (int64_t)wave * U, lane, ra);
+      // vmcnt(0) retires the staged row-scale partials with ra: the compiler cannot count
+      // LDS-direct loads and would otherwise wait for every load in flight at each batch
+      if constexpr (RS && PRE > 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       for (int bt = wave;;) {
         if (bt + WAVES < nbatch) batch_load<MT, NT, U, BITS>(a, t0, g_lo + (int64_t)(bt + WAVES) * U, lane, rb);
         batch_compute<MT, NT, U, BITS>(ra, acc);
@@ -499,22 +595,74 @@ __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
     for (int bt = wave; bt < nbatch; bt += WAVES) {
       Batch<MT, NT, U, BITS> r;
       batch_load<MT, NT, U, BITS>(a, t0, g_lo + (int64_t)bt * U, lane, r);
+      // the batch is waited for in full anyway; an explicit vmcnt(0) also retires the staged
+      // partials, so the compiler keeps exact load counts (it cannot count LDS-direct loads)
+      if constexpr (RS && PRE > 0) {
+        __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before the wait
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       batch_compute<MT, NT, U, BITS>(r, acc);
     }
   }
 
-  constexpr int NOUT = MT * NT * 256;
   __shared__ float red[WAVES][NOUT];
+  __shared__ float rsc[RS ? MT * 16 : 1];
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
     for (int j = 0; j < NT; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) red[wave][((i * NT + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+  constexpr bool rowscale = RS;
+  if constexpr (RS) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int m = wave + WAVES * i;
+      if (m >= MT * 16) break;
+      float s = 0.0f;
+#pragma unroll
+      for (int j = 0; j < PRE; ++j)
+        if (lane + 64 * j < a.rs_tiles) s += ssq_lds[(m * PRE + j) * 64 + lane];
+      for (int t = lane + 64 * PRE; t < a.rs_tiles; t += 64)
+        if (m < a.M) s += a.rs_ssq[(int64_t)m * a.rs_tiles + t];
+      s = wave_sum(s);
+      if (lane == 0) rsc[m] = m < a.M ? rsqrtf(s / (float)a.K + a.rs_eps) : 1.0f;
+    }
+  }
   __syncthreads();
 
   // output element o: lane ln = o % 64, r = (o / 64) % 4, tile (i, j) = o / 256
   constexpr bool gated = EK == 1;
+  if constexpr (EK == 3) {
+    // every lane of a wave runs the same iterations (NOUT and the stride are multiples of 64),
+    // so the 16-lane column sums below see whole row segments
+#pragma unroll
+    for (int u = 0; u < PL; ++u) {
+      const int o = threadIdx.x + u * WAVES * 64;
+      if (o >= NOUT) break;
+      const int i = (o >> 8) / NT, j = (o >> 8) % NT;
+      const int m = i * 16 + ((o & 63) >> 4) * 4 + ((o >> 6) & 3);
+      const bool live = m < a.M;
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) v += red[w][o];
+      const int64_t n = (t0 + j) * 16 + (o & 15);
+      float hn = 0.0f;
+      if (live) {
+        const uint16_t hb = f32_to_bf16(bf16_to_f32(hpre[u]) + v);
+        a.h[(int64_t)m * a.ldh + n] = hb;
+        hn = bf16_to_f32(hb);
+        if (a.copy) a.copy[(int64_t)m * a.ldc + n] = hb;
+        if (a.y)
+          reinterpret_cast<uint16_t*>(a.y)[apack_index(m, n, a.N / 64)] =
+              a.g ? f32_to_bf16(hn * bf16_to_f32(gpre[u])) : hb;
+      }
+      const float sq = sum16_lanes(hn * hn);
+      if (live && a.ssq_out && (o & 15) == 0) a.ssq_out[(int64_t)m * (a.N / 16) + t0 + j] = sq;
+    }
+    return;
+  }
   for (int o = threadIdx.x; o < NOUT; o += WAVES * 64) {
     const int i = (o >> 8) / NT, j = (o >> 8) % NT;
     const int m = i * 16 + ((o & 63) >> 4) * 4 + ((o >> 6) & 3);
@@ -522,6 +670,7 @@ __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
     float v = 0.0f;
 #pragma unroll
     for (int w = 0; w < WAVES; ++w) v += red[w][o];
+    if constexpr (rowscale) v *= rsc[m];
     const int64_t n = (t0 + j) * 16 + (o & 15);
     if constexpr (EK == 2) {
       reinterpret_cast<float*>(a.y)[((int64_t)ks * a.M + m) * a.N + n] = v;
@@ -531,6 +680,7 @@ __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
       float u = 0.0f;
 #pragma unroll
       for (int w = 0; w < WAVES; ++w) u += red[w][o + 256];
+      if constexpr (rowscale) u *= rsc[m];
       gemm_store_gated(a, m, ((t0 + j) >> 1) * 16 + (o & 15), v, u);
     }
   }
@@ -577,6 +727,19 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi, int bits = 8) {
   const int MT = (M + 15) / 16;
   const bool partial = epi == DSK_EPI_PARTIAL, gated = epi == DSK_EPI_SWIGLU || epi == DSK_EPI_GEGLU;
   GemmPlan p;
+  if (epi == DSK_EPI_RESIDUAL) {
+    // the residual-add epilogue needs whole rows of the product in one workgroup: no K split;
+    // one tile per workgroup and up to 16 waves splitting K (reduced through LDS)
+    p.nt = 1;
+    p.sk = 1;
+    p.u = (MT == 1 && G / 4 >= 16 && G % 4 == 0) ? 4 : 2;
+    p.gpb = G;
+    const int64_t nb = G / p.u;
+    p.waves = nb >= 16 ? 16 : (nb >= 8 ? 8 : 4);
+    while ((size_t)p.waves * MT * 1024 > 65536) p.waves /= 2;
+    p.pf = false;  // pipelined loads measured slower here (down 4096x12288: 18.5 -> 23.2 us)
+    return p;
+  }
   p.u = 2;
   if (partial) p.nt = G >= 128 ? 4 : 2;
   else p.nt = 4;
@@ -619,12 +782,20 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi, int bits = 8) {
 template <int MT, int NT, int U, int WAVES, bool PF, int BITS>
 static bool launch_gemm_t(const GemmArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)(a.n_slabs * a.SK)), blk(WAVES * 64);
+  const bool rs = a.rs_ssq != nullptr;
   if (a.epi == DSK_EPI_PARTIAL) {
-    hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 2, PF, BITS>), grid, blk, 0, st, a);
+    if (rs) hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 6, PF, BITS>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 2, PF, BITS>), grid, blk, 0, st, a);
+  } else if (a.epi == DSK_EPI_RESIDUAL) {
+    if constexpr (NT != 1) return false;
+    else if (rs) return false;  // the residual products' x (attention output, gated MLP) is never normed later
+    else hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 3, PF, BITS>), grid, blk, 0, st, a);
   } else if (a.epi == DSK_EPI_STORE) {
-    hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 0, PF, BITS>), grid, blk, 0, st, a);
+    if (rs) hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 4, PF, BITS>), grid, blk, 0, st, a);
+    else hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 0, PF, BITS>), grid, blk, 0, st, a);
   } else {
     if constexpr (NT % 2 != 0) return false;  // gated tiles come in gate|up pairs
+    else if (rs) hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 5, PF, BITS>), grid, blk, 0, st, a);
     else hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 1, PF, BITS>), grid, blk, 0, st, a);
   }
   return true;
@@ -689,6 +860,15 @@ static void gemm_prepare(GemmArgs& a, const GemmPlan& p, const void* xp, const u
   a.ldr = ldr;
   a.softcap = softcap;
   a.bits = 8;
+  a.rs_ssq = nullptr;
+  a.rs_tiles = 0;
+  a.rs_eps = 0.0f;
+  a.h = nullptr;
+  a.ldh = 0;
+  a.copy = nullptr;
+  a.ldc = 0;
+  a.g = nullptr;
+  a.ssq_out = nullptr;
 }
 
 // chunks per thread (NV) x split slices kept in registers (MAXS): NV * MAXS <= 16
@@ -793,10 +973,31 @@ extern "C" int dsk_act_pack_scaled(const float* part, int nsplit, const uint16_t
                 (uintptr_t)part_norm_w) & 15) == 0,
               "dsk_act_pack: pointers must be 16-byte aligned");
   DSK_REQUIRE(!part_norm_w || part, "dsk_act_pack: part_norm_w needs partial sums");
-  PackArgs a{part, nsplit, h, ldh, copy, ldc, M, K, norm_w, eps, out, part_norm_w, out_scale};
+  PackArgs a{part, nsplit, h, ldh, copy, ldc, M, K, norm_w, eps, out, part_norm_w, out_scale, nullptr};
   DSK_REQUIRE(pack_launch(a, as_stream(stream)), "dsk_act_pack: no kernel for K=%lld with %d slices", (long long)K,
               nsplit);
   DSK_LAUNCH_CHECK("dsk_act_pack");
+  return DSK_OK;
+}
+
+extern "C" int dsk_act_pack_rn(const float* part, int nsplit, uint16_t* h, int64_t ldh, uint16_t* copy, int64_t ldc,
+                               int M, int64_t K, const uint16_t* norm_w, uint16_t* out, float* ssq_out,
+                               dsk_stream_t stream) {
+  DSK_REQUIRE(h && out && ssq_out, "dsk_act_pack_rn: needs h, out and ssq_out");
+  DSK_REQUIRE(!part || (nsplit > 0 && nsplit <= kPackMaxSplits), "dsk_act_pack_rn: nsplit=%d outside [1, %d]", nsplit,
+              kPackMaxSplits);
+  DSK_REQUIRE(!part || (int64_t)(nsplit <= 4 ? 4 : (nsplit <= 8 ? 8 : 16)) * ceil_div(K / 8, kPackThreads) <= 16,
+              "dsk_act_pack_rn: %d partial slices of K=%lld exceed the kernel's registers", nsplit, (long long)K);
+  DSK_REQUIRE(M > 0 && M <= 64, "dsk_act_pack_rn: M=%d outside [1, 64]", M);
+  DSK_REQUIRE(K > 0 && K % 64 == 0 && K <= 6 * 8 * kPackThreads,
+              "dsk_act_pack_rn: K=%lld must be a multiple of 64 <= %d", (long long)K, 6 * 8 * kPackThreads);
+  DSK_REQUIRE(ldh >= K && ldh % 8 == 0 && (!copy || (ldc >= K && ldc % 8 == 0)), "dsk_act_pack_rn: bad row stride");
+  DSK_REQUIRE((((uintptr_t)part | (uintptr_t)h | (uintptr_t)copy | (uintptr_t)norm_w | (uintptr_t)out) & 15) == 0,
+              "dsk_act_pack_rn: pointers must be 16-byte aligned");
+  PackArgs a{part, nsplit, h, ldh, copy, ldc, M, K, norm_w, 0.0f, out, nullptr, 1.0f, ssq_out};
+  DSK_REQUIRE(pack_launch(a, as_stream(stream)), "dsk_act_pack_rn: no kernel for K=%lld with %d slices", (long long)K,
+              nsplit);
+  DSK_LAUNCH_CHECK("dsk_act_pack_rn");
   return DSK_OK;
 }
 
@@ -816,9 +1017,21 @@ extern "C" int dsk_w4_gemm_splits(int M, int64_t N, int64_t K) {
   return plan_gemm(M, N, K, DSK_EPI_PARTIAL, 4).sk;
 }
 
+struct NormIO {
+  const float* x_ssq;  // row scale of x (normed later), or null
+  int x_tiles;
+  float eps;
+  uint16_t* h;         // DSK_EPI_RESIDUAL
+  int64_t ldh;
+  uint16_t* copy;
+  int64_t ldc;
+  const uint16_t* next_w;
+  float* ssq_out;
+};
+
 static int gemm_entry(const char* who, int bits, const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int M,
                       int64_t N, int64_t K, int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
-                      int64_t ldr, float softcap, hipStream_t st);
+                      int64_t ldr, float softcap, hipStream_t st, const NormIO* nio = nullptr);
 
 extern "C" int dsk_w8_gemm(const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int M, int64_t N, int64_t K,
                            int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual, int64_t ldr,
@@ -834,17 +1047,38 @@ extern "C" int dsk_w4_gemm(const uint16_t* xp, const uint8_t* wt, const uint32_t
                     as_stream(stream));
 }
 
+extern "C" int dsk_w8_gemm_rn(const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int bits, int M, int64_t N,
+                              int64_t K, int epi, void* y, int y_dtype, int64_t ldy, float softcap, const float* x_ssq,
+                              int x_tiles, float eps, uint16_t* h, int64_t ldh, uint16_t* copy, int64_t ldc,
+                              const uint16_t* next_norm_w, float* ssq_out, dsk_stream_t stream) {
+  DSK_REQUIRE(bits == 8 || bits == 4, "dsk_w8_gemm_rn: bits=%d (8 or 4)", bits);
+  DSK_REQUIRE(!x_ssq || (x_tiles == K / 16 && eps >= 0.0f),
+              "dsk_w8_gemm_rn: the row scale of x needs K / 16 = %lld tile partials (got %d)", (long long)(K / 16),
+              x_tiles);
+  NormIO nio{x_ssq, x_ssq ? x_tiles : 0, eps, h, ldh, copy, ldc, next_norm_w, ssq_out};
+  return gemm_entry("dsk_w8_gemm_rn", bits, xp, wt, sb, M, N, K, epi, y, y_dtype, ldy, nullptr, 0, softcap,
+                    as_stream(stream), &nio);
+}
+
 static int gemm_entry(const char* who, int bits, const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int M,
                       int64_t N, int64_t K, int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
-                      int64_t ldr, float softcap, hipStream_t st) {
-  DSK_REQUIRE(xp && wt && sb && y, "dsk_w8_gemm: null pointer");
+                      int64_t ldr, float softcap, hipStream_t st, const NormIO* nio) {
+  DSK_REQUIRE(xp && wt && sb && (y || epi == DSK_EPI_RESIDUAL), "dsk_w8_gemm: null pointer");
   DSK_REQUIRE(M > 0 && M <= 64, "dsk_w8_gemm: M=%d outside [1, 64]", M);
   DSK_REQUIRE(N > 0 && N % 16 == 0 && K > 0 && K % 256 == 0,
               "dsk_w8_gemm: need N %% 16 == 0, K %% 256 == 0 (N=%lld K=%lld)", (long long)N, (long long)K);
   DSK_REQUIRE(((uintptr_t)xp & 15) == 0 && ((uintptr_t)wt & 15) == 0, "dsk_w8_gemm: x and W must be 16-byte aligned");
-  DSK_REQUIRE(epi >= DSK_EPI_STORE && epi <= DSK_EPI_PARTIAL, "dsk_w8_gemm: bad epilogue %d", epi);
+  DSK_REQUIRE(epi >= DSK_EPI_STORE && epi <= (nio ? DSK_EPI_RESIDUAL : DSK_EPI_PARTIAL), "%s: bad epilogue %d", who,
+              epi);
   const bool gated = epi == DSK_EPI_SWIGLU || epi == DSK_EPI_GEGLU;
-  if (epi == DSK_EPI_STORE) {
+  if (epi == DSK_EPI_RESIDUAL) {
+    DSK_REQUIRE(nio->h && nio->ldh >= N && (!nio->copy || nio->ldc >= N), "%s: the residual epilogue needs h [M, N]"
+                " (and copy) with row strides >= N", who);
+    DSK_REQUIRE(N % 64 == 0, "%s: the residual epilogue needs N %% 64 == 0 (N=%lld)", who, (long long)N);
+    DSK_REQUIRE(!y || y_dtype == DSK_BF16, "%s: the residual epilogue's packed output is bf16", who);
+    DSK_REQUIRE(!nio->next_w || nio->ssq_out, "%s: a later-normed output needs ssq_out", who);
+    DSK_REQUIRE(softcap == 0.0f, "%s: no soft-cap in the residual epilogue", who);
+  } else if (epi == DSK_EPI_STORE) {
     DSK_REQUIRE(y_dtype == DSK_F32 || y_dtype == DSK_BF16, "dsk_w8_gemm: y dtype must be f32 or bf16");
     DSK_REQUIRE(ldy >= N, "dsk_w8_gemm: ldy=%lld < N", (long long)ldy);
     DSK_REQUIRE(!residual || ldr >= N, "dsk_w8_gemm: ldr=%lld < N", (long long)ldr);
@@ -860,6 +1094,19 @@ static int gemm_entry(const char* who, int bits, const uint16_t* xp, const uint8
   GemmArgs a;
   gemm_prepare(a, p, xp, wt, sb, M, N, K, epi, y, y_dtype, ldy, residual, ldr, softcap);
   a.bits = bits;
+  if (nio) {
+    a.rs_ssq = nio->x_ssq;
+    a.rs_tiles = nio->x_tiles;
+    a.rs_eps = nio->eps;
+    if (epi == DSK_EPI_RESIDUAL) {
+      a.h = nio->h;
+      a.ldh = nio->ldh;
+      a.copy = nio->copy;
+      a.ldc = nio->ldc;
+      a.g = nio->next_w;
+      a.ssq_out = nio->ssq_out;
+    }
+  }
   if (!launch_gemm(a, (M + 15) / 16, p, st)) {
     set_error("%s: no kernel for M=%d NT=%d U=%d waves=%d", who, M, p.nt, p.u, p.waves);
     return DSK_EINVAL;

@@ -37,6 +37,11 @@ SIGNATURES: dict[str, tuple] = {
     "dsk_w4_gemm_splits": (c_int, [c_int, c_int64, c_int64]),
     "dsk_w8_gemm": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_int, c_void_p, c_int, c_int64,
                             c_void_p, c_int64, c_float, c_void_p]),
+    "dsk_act_pack_rn": (c_int, [c_void_p, c_int, c_void_p, c_int64, c_void_p, c_int64, c_int, c_int64, c_void_p,
+                                c_void_p, c_void_p, c_void_p]),
+    "dsk_w8_gemm_rn": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int64, c_int64, c_int, c_void_p, c_int,
+                               c_int64, c_float, c_void_p, c_int, c_float, c_void_p, c_int64, c_void_p, c_int64,
+                               c_void_p, c_void_p, c_void_p]),
     "dsk_w8_embed": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float,
                              c_void_p, c_int64, c_void_p]),
     "dsk_qkv_rope_append": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float,
@@ -79,7 +84,7 @@ SIGNATURES: dict[str, tuple] = {
 
 DSK_F32, DSK_BF16 = 0, 1
 DSK_KV_BF16, DSK_KV_U8 = 0, 1
-DSK_EPI_STORE, DSK_EPI_SWIGLU, DSK_EPI_GEGLU, DSK_EPI_PARTIAL = 0, 1, 2, 3
+DSK_EPI_STORE, DSK_EPI_SWIGLU, DSK_EPI_GEGLU, DSK_EPI_PARTIAL, DSK_EPI_RESIDUAL = 0, 1, 2, 3, 4
 
 
 def _load():

@@ -13,11 +13,11 @@ from dataclasses import dataclass
 import torch
 
 from . import _hip
-from ._hip import (DSK_BF16, DSK_EPI_GEGLU, DSK_EPI_PARTIAL, DSK_EPI_STORE, DSK_EPI_SWIGLU, DSK_F32, DSK_KV_BF16,
-                   DSK_KV_U8, call, ptr, stream_ptr)
+from ._hip import (DSK_BF16, DSK_EPI_GEGLU, DSK_EPI_PARTIAL, DSK_EPI_RESIDUAL, DSK_EPI_STORE, DSK_EPI_SWIGLU, DSK_F32,
+                   DSK_KV_BF16, DSK_KV_U8, call, ptr, stream_ptr)
 
 __all__ = [
-    "W8Weight", "W8Table", "Workspace", "Packed", "act_pack", "pack", "w8_gemm", "w8_embed",
+    "W8Weight", "W8Table", "Workspace", "Packed", "act_pack", "pack", "pack_rn", "w8_gemm", "w8_residual", "w8_embed",
     "qkv_rope_append", "attention", "qkv_attention", "row_logprobs", "accept_greedy", "accept_sample", "sample_rows",
     "argmax_rows", "lens_add",
     "rope_inv_freq", "DSK_EPI_STORE", "DSK_EPI_SWIGLU", "DSK_EPI_GEGLU", "DSK_EPI_PARTIAL", "DSK_KV_BF16",
@@ -160,18 +160,31 @@ class W8Table:
 # ----------------------------------------------------------------------------- GEMM path
 @dataclass
 class Packed:
-    """An [M, K] bf16 activation in the GEMM's packed operand layout (see w8.hip)."""
+    """An [M, K] bf16 activation in the GEMM's packed operand layout (see w8.hip).
+
+    Normed later (``ssq`` set): the packed values are bf16(h * w) of an RMSNorm whose row scale
+    rsqrt(mean(h^2) + eps) the consuming GEMM applies to its outputs; ``ssq`` f32 [M, K/16]
+    holds the per-16-column partial sums of h^2 it is computed from."""
 
     data: torch.Tensor   # bf16, dsk_act_pack_bytes(M, K) / 2 elements
     M: int
     K: int
+    ssq: torch.Tensor | None = None
+    eps: float = 0.0
 
     @staticmethod
-    def empty(M: int, K: int, device) -> "Packed":
+    def empty(M: int, K: int, device, normed_later: bool = False, eps: float = 0.0) -> "Packed":
         n = _hip.lib.dsk_act_pack_bytes(M, K)
         if n == 0:
             raise ValueError(f"cannot pack [{M}, {K}] (K must be a multiple of 64)")
-        return Packed(torch.empty(n // 2, dtype=torch.bfloat16, device=device), M, K)
+        ssq = torch.empty((M, K // 16), dtype=torch.float32, device=device) if normed_later else None
+        return Packed(torch.empty(n // 2, dtype=torch.bfloat16, device=device), M, K, ssq, float(eps))
+
+    def row_scale(self) -> torch.Tensor | None:
+        """[M] f32 rsqrt(mean(h^2) + eps) of a normed-later activation (for checks)."""
+        if self.ssq is None:
+            return None
+        return torch.rsqrt(self.ssq.sum(1) / self.K + self.eps)
 
     def unpack(self) -> torch.Tensor:
         """[M, K] bf16 copy (for checks; the engine never unpacks)."""
@@ -208,6 +221,40 @@ def act_pack(*, M: int, K: int, part: torch.Tensor | None = None, h: torch.Tenso
          ptr(copy), 0 if copy is None else copy.stride(0), M, K, ptr(norm_w), float(eps), float(scale),
          ptr(None if out is None else out.data), stream_ptr())
     return out
+
+
+def pack_rn(*, M: int, K: int, h: torch.Tensor, norm_w: torch.Tensor | None, eps: float,
+            part: torch.Tensor | None = None, copy: torch.Tensor | None = None,
+            out: Packed | None = None) -> Packed:
+    """act_pack's residual add of split-K partials (or h alone), with the RMSNorm left to the
+    consuming GEMM: returns the normed-later Packed bf16(h * norm_w) (dsk_act_pack_rn)."""
+    if not _rows_ok(h) or (copy is not None and not _rows_ok(copy)):
+        raise ValueError("pack_rn: h / copy need unit column stride, 16-byte aligned rows")
+    if part is not None and (part.dtype != torch.float32 or not part.is_contiguous() or part.shape[1:] != (M, K)):
+        raise ValueError(f"pack_rn: partials must be contiguous f32 [S, {M}, {K}]")
+    if out is None:
+        out = Packed.empty(M, K, h.device, normed_later=True, eps=eps)
+    call("dsk_act_pack_rn", ptr(part), 0 if part is None else part.shape[0], ptr(h), h.stride(0), ptr(copy),
+         0 if copy is None else copy.stride(0), M, K, ptr(norm_w), ptr(out.data), ptr(out.ssq), stream_ptr())
+    return out
+
+
+def w8_residual(x: Packed, w: W8Weight, h: torch.Tensor, *, next_norm: torch.Tensor | None, eps: float,
+                copy: torch.Tensor | None = None, out: bool = True) -> Packed | None:
+    """h += x . deq(W)^T in place (bf16, the residual add after o_proj / down_proj) in the
+    GEMM's epilogue, copy = h (a hidden-state tap), and the next projection's input normed
+    later: Packed bf16(h * next_norm) with its per-tile sums of h^2 (None when out is False)."""
+    if x.K != w.K:
+        raise ValueError(f"w8_residual: x has K={x.K}, W has K={w.K}")
+    M = x.M
+    if tuple(h.shape) != (M, w.N) or not _rows_ok(h) or (copy is not None and not _rows_ok(copy)):
+        raise ValueError(f"w8_residual: h must be bf16 [{M}, {w.N}] with aligned unit-stride rows")
+    y = Packed.empty(M, w.N, h.device, normed_later=True, eps=eps) if out else None
+    call("dsk_w8_gemm_rn", ptr(x.data), ptr(w.wt), ptr(w.sb), w.bits, M, w.N, w.K, DSK_EPI_RESIDUAL,
+         ptr(None if y is None else y.data), DSK_BF16, 0, 0.0, ptr(x.ssq), 0 if x.ssq is None else w.K // 16,
+         float(x.eps), ptr(h), h.stride(0), ptr(copy), 0 if copy is None else copy.stride(0),
+         ptr(next_norm if y is not None else None), ptr(None if y is None else y.ssq), stream_ptr())
+    return y
 
 
 def pack(x: torch.Tensor, norm_w: torch.Tensor | None = None, eps: float = 1e-6) -> Packed:
@@ -251,6 +298,12 @@ def w8_gemm(x: Packed, w: W8Weight, *, epi: int = DSK_EPI_STORE, out=None, out_d
         if out is None:
             out = Packed.empty(M, w.N // 2, dev)
         ydata = out.data
+    if x.ssq is not None:
+        if residual is not None:
+            raise ValueError("w8_gemm: a normed-later x takes no residual (use w8_residual)")
+        call("dsk_w8_gemm_rn", ptr(x.data), ptr(w.wt), ptr(w.sb), w.bits, M, w.N, w.K, int(epi), ptr(ydata), yd, ldy,
+             float(softcap), ptr(x.ssq), w.K // 16, float(x.eps), None, 0, None, 0, None, None, stream_ptr())
+        return out
     call("dsk_w8_gemm" if w.bits == 8 else "dsk_w4_gemm", ptr(x.data), ptr(w.wt), ptr(w.sb), M, w.N, w.K, int(epi),
          ptr(ydata), yd, ldy, ptr(residual), residual.stride(0) if residual is not None else 0, float(softcap),
          stream_ptr())

@@ -136,11 +136,11 @@ class Qwen3W8:
     def layer(self, l: int, x: ops.Packed, h: torch.Tensor, B: int, W: int, cache: PagedKVCache, *,
               causal: bool = True, next_norm: torch.Tensor | None = None, copy: torch.Tensor | None = None,
               want_next: bool = True) -> ops.Packed | None:
-        """One decoder layer. x: this layer's input, RMSNorm(h) packed; h [B*W, H] bf16 residual
-        stream (updated in place). Returns the next projection's packed input,
-        RMSNorm(h_out) with next_norm (the next layer's input norm or the final norm), or the
-        plain packed h_out when next_norm is None; None when want_next is False. copy, when
-        given, receives h_out (hidden-state tap)."""
+        """One decoder layer. x: this layer's input, RMSNorm(h) packed (normed later in the
+        Qwen3 layout); h [B*W, H] bf16 residual stream (updated in place). Returns the next
+        projection's packed input, RMSNorm(h_out) with next_norm (the next layer's input norm or
+        the final norm), or the plain packed h_out when next_norm is None; None when want_next is
+        False. copy, when given, receives h_out (hidden-state tap)."""
         a = self.args
         L = self.layers[l]
         nq, nkv, hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
@@ -155,6 +155,12 @@ class Qwen3W8:
         o = ops.attention(q, B, W, nq, nkv, hd, a.attn_scale, cache.seq_lens, cache.max_ctx,
                           cache.block_table, cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb,
                           causal=causal, window=a.window(l), packed=True)
+        if not a.sandwich_norms:
+            # the residual adds run in the o / down epilogues, each next RMSNorm in the GEMM that
+            # consumes it (normed later)
+            x = ops.w8_residual(o, L.o, h, next_norm=L.post_norm, eps=eps)
+            act = ops.w8_gemm(x, L.gate_up, epi=self.act_epi)
+            return ops.w8_residual(act, L.down, h, next_norm=next_norm, eps=eps, copy=copy, out=want_next)
         op = ops.w8_gemm(o, L.o, epi=ops.DSK_EPI_PARTIAL)
         x = ops.act_pack(M=M, K=H, part=op, h=h, norm_w=L.post_norm, eps=eps, part_norm_w=L.attn_out_norm)
         act = ops.w8_gemm(x, L.gate_up, epi=self.act_epi)
@@ -188,7 +194,10 @@ class Qwen3W8:
             fused = fused_out if fused_out is not None else torch.empty(
                 (M, len(tap) * H), dtype=torch.bfloat16, device=self.device)
         nl = a.num_hidden_layers
-        x = ops.pack(h, self.layers[0].in_norm, eps)
+        if a.sandwich_norms:
+            x = ops.pack(h, self.layers[0].in_norm, eps)
+        else:
+            x = ops.pack_rn(M=M, K=H, h=h, norm_w=self.layers[0].in_norm, eps=eps)
         for l in range(nl):
             last = l == nl - 1
             s = slots.get(l, ())

@@ -54,6 +54,14 @@ def rmsnorm(x, w, eps):
     return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) * w
 
 
+def norm_later(x, w, eps):
+    """The RMSNorm in front of a projection applied after it, where the engine's Qwen3 layout
+    applies it (the consuming GEMM scales its output rows): returns (bf16(x * w), r) with
+    r = rsqrt(mean(x^2) + eps) per row, so r * (bf16(x * w) @ W^T) is rmsnorm(x, w) @ W^T up
+    to where the product is rounded."""
+    return bf(x * w), torch.rsqrt((x * x).mean(-1, keepdim=True) + eps)
+
+
 def inv_freq(hd: int, theta: float, rotary_fraction: float = 1.0) -> torch.Tensor:
     """Rotate-half RoPE frequencies theta^(-2i/hd), i < hd/2 (float64, stored f32). A
     rotary_fraction below 1 is proportional RoPE (the gemma4 drafter's "proportional" rope
@@ -187,12 +195,18 @@ class OracleTarget:
         h = bf(bf(self.embed[ids]) * a.embed_scale)   # bf16 embedding rows, then the bf16 scale
         pos = torch.arange(self.offset, self.offset + W)
         gelu = getattr(a, "hidden_act", "silu") != "silu"
+        # the Qwen3 layout's norms are applied after their projections (norm_later); the
+        # Gemma-style layout normalises before them
+        sandwich = bool(getattr(a, "sandwich_norms", False))
         captured = []
         for l, L in enumerate(self.layers):
             win = a.window(l)
             theta = (a.rope_local_base_freq or a.rope_theta) if a.is_sliding(l) else a.rope_theta
-            x = bf(rmsnorm(h, L.in_norm, eps))
-            qkv = bf(x @ L.wq.T)
+            if sandwich:
+                qkv = bf(bf(rmsnorm(h, L.in_norm, eps)) @ L.wq.T)
+            else:
+                xg, r = norm_later(h, L.in_norm, eps)
+                qkv = bf(r * (xg @ L.wq.T))
             q = qkv[:, : nq * hd].view(W, nq, hd)
             k = qkv[:, nq * hd:(nq + nkv) * hd].view(W, nkv, hd)
             v = qkv[:, (nq + nkv) * hd:].view(W, nkv, hd)
@@ -207,8 +221,11 @@ class OracleTarget:
                 h = bf(h + bf(rmsnorm(bf(o.reshape(W, -1) @ L.wo.T), L.attn_out_norm, eps)))
             else:
                 h = bf(h + self.rr(o.reshape(W, -1) @ L.wo.T))
-            x = bf(rmsnorm(h, L.post_norm, eps))
-            gu = bf(x @ L.wgu.T)
+            if sandwich:
+                gu = bf(bf(rmsnorm(h, L.post_norm, eps)) @ L.wgu.T)
+            else:
+                xg, r = norm_later(h, L.post_norm, eps)
+                gu = bf(r * (xg @ L.wgu.T))
             I = gu.shape[1] // 2
             g, u = gu[:, :I], gu[:, I:]
             act = bf(bf(gelu_tanh(g) if gelu else g * torch.sigmoid(g)) * u)
@@ -219,7 +236,11 @@ class OracleTarget:
             if l in tap:
                 captured.append(h)
         self.offset += W
-        logits = bf(rmsnorm(h, self.norm, eps)) @ self.lm_head.T
+        if sandwich:
+            logits = bf(rmsnorm(h, self.norm, eps)) @ self.lm_head.T
+        else:
+            xg, r = norm_later(h, self.norm, eps)
+            logits = r * (xg @ self.lm_head.T)
         cap = getattr(a, "final_logit_softcapping", None)
         if cap:
             logits = torch.tanh(logits / cap) * cap
