@@ -243,6 +243,17 @@ int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, int hd, floa
                   const uint32_t* k_sb, const uint32_t* v_sb, uint16_t* out, int out_packed,
                   void* workspace, size_t ws_bytes, dsk_stream_t stream);
 
+/* dsk_qkv_rope_append (pos_offset 0) for a projection whose input was normed later
+ * (dsk_w8_gemm_rn): the summed split-K partials of row m are multiplied by
+ * r_m = rsqrt(sum_t x_ssq[m][t] / (16 x_tiles) + x_eps) before they are rounded to bf16, q/k
+ * normed and roped (the input RMSNorm of the Qwen3 layer, applied after q/k/v_proj). */
+int dsk_qkv_rope_append_rn(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
+                           const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                           const float* inv_freq, const int32_t* seq_lens, const int32_t* block_table,
+                           int max_pages, int page, int kv_dtype, void* k_pool, void* v_pool,
+                           uint32_t* k_sb, uint32_t* v_sb, uint16_t* q_out, const float* x_ssq,
+                           int x_tiles, float x_eps, dsk_stream_t stream);
+
 /* dsk_qkv_rope_append followed by dsk_attention in one kernel (plus the split combine):
  * from the qkv projection (bf16 or fp32 split-K slices, as for dsk_qkv_rope_append, with
  * pos_offset 0) each workgroup forms its queries (q RMSNorm, RoPE at seq_lens[b] + i); the

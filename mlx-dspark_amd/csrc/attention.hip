@@ -39,10 +39,11 @@ __device__ __forceinline__ void rope_sincos(int pos, float inv_freq, float& sn, 
 
 // One head row of HD dims spread over L consecutive lanes (L = 64: a wave; L = 16: a quarter
 // wave), PER = HD / L consecutive dims per lane starting at dim PER * (lane % L).
-// Sum of the projection's split-K slices in slice order, rounded to bf16.
+// Sum of the projection's split-K slices in slice order, times `scale` (the row scale of a
+// normed-later input; 1 otherwise), rounded to bf16.
 template <int PER>
 __device__ __forceinline__ void load_proj_row(const void* qkv, int splits, int64_t slice, int64_t off, int sub,
-                                              float (&v)[PER]) {
+                                              float (&v)[PER], float scale = 1.0f) {
   if (splits == 0) {
     const uint16_t* src = reinterpret_cast<const uint16_t*>(qkv) + off + (int64_t)sub * PER;
 #pragma unroll
@@ -66,7 +67,7 @@ __device__ __forceinline__ void load_proj_row(const void* qkv, int splits, int64
         if (sp + u < splits) v[e] += t[u][e];
   }
 #pragma unroll
-  for (int e = 0; e < PER; ++e) v[e] = round_bf16(v[e]);
+  for (int e = 0; e < PER; ++e) v[e] = round_bf16(v[e] * scale);
 }
 
 // sum over the L lanes of a row (L a power of two, rows aligned to L lanes)
@@ -156,14 +157,14 @@ __device__ __forceinline__ int64_t pool_token(const int32_t* block_table, int ma
 
 // ----------------------------------------------------------------------------- append
 // One wave per (token row, head): lane holds dims [PER*lane, PER*lane + PER) (PER = HD/64).
-template <int HD>
+template <int HD, bool RS>
 __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
     const void* __restrict__ qkv, int qkv_splits, int B, int W, int nq, int nkv, const uint16_t* __restrict__ q_norm,
     const uint16_t* __restrict__ k_norm, const uint16_t* __restrict__ v_norm, float eps,
     const float* __restrict__ inv_freq, const int32_t* __restrict__ seq_lens, int pos_offset,
     const int32_t* __restrict__ block_table, int max_pages, int page, int kv_dtype, void* __restrict__ k_pool,
     void* __restrict__ v_pool, uint32_t* __restrict__ k_sb, uint32_t* __restrict__ v_sb,
-    uint16_t* __restrict__ q_out) {
+    uint16_t* __restrict__ q_out, const float* __restrict__ x_ssq, int x_tiles, float x_k, float x_eps) {
   constexpr int PER = HD / 64;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int nheads = nq + 2 * nkv;
@@ -172,8 +173,23 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
   if (row >= B * W) return;
   const int b = row / W, i = row % W;
   const int pos = seq_lens[b] + i + pos_offset;
+  // row scale of a normed-later projection input: the tile partials of the row summed l, l + 64,
+  // ... per lane, then across the wave (the GEMM's own order)
   float v[PER];
-  load_proj_row<PER>(qkv, qkv_splits, (int64_t)B * W * nheads * HD, ((int64_t)row * nheads + head) * HD, lane, v);
+  if constexpr (RS) {
+    // the partials' loads and these are independent: one memory round trip for both
+    float xs[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      xs[j] = lane + 64 * j < x_tiles ? x_ssq[(int64_t)row * x_tiles + lane + 64 * j] : 0.0f;
+    float t = ((xs[0] + xs[1]) + xs[2]) + xs[3];
+    for (int j = lane + 256; j < x_tiles; j += 64) t += x_ssq[(int64_t)row * x_tiles + j];
+    const float rs = rsqrtf(wave_sum(t) / x_k + x_eps);
+    load_proj_row<PER>(qkv, qkv_splits, (int64_t)B * W * nheads * HD, ((int64_t)row * nheads + head) * HD, lane, v,
+                       rs);
+  } else {
+    load_proj_row<PER>(qkv, qkv_splits, (int64_t)B * W * nheads * HD, ((int64_t)row * nheads + head) * HD, lane, v);
+  }
   const bool is_q = head < nq, is_k = !is_q && head < nq + nkv;
   norm_rope_row<HD, 64>(v, lane, is_q ? q_norm : (is_k ? k_norm : v_norm), eps, is_q || is_k, inv_freq, pos);
   if (is_q) {
@@ -943,12 +959,42 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
 
 using namespace dsk;
 
+static int qkv_append_entry(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
+                            const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* v_norm, float eps,
+                            const float* inv_freq, const int32_t* seq_lens, int pos_offset, const int32_t* block_table,
+                            int max_pages, int page, int kv_dtype, void* k_pool, void* v_pool, uint32_t* k_sb,
+                            uint32_t* v_sb, uint16_t* q_out, const float* x_ssq, int x_tiles, float x_eps,
+                            dsk_stream_t stream);
+
 extern "C" int dsk_qkv_norm_rope_append(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
                                         const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* v_norm,
                                         float eps, const float* inv_freq, const int32_t* seq_lens, int pos_offset,
                                         const int32_t* block_table, int max_pages, int page, int kv_dtype,
                                         void* k_pool, void* v_pool, uint32_t* k_sb, uint32_t* v_sb, uint16_t* q_out,
                                         dsk_stream_t stream) {
+  return qkv_append_entry(qkv, qkv_splits, B, W, nq, nkv, hd, q_norm, k_norm, v_norm, eps, inv_freq, seq_lens,
+                          pos_offset, block_table, max_pages, page, kv_dtype, k_pool, v_pool, k_sb, v_sb, q_out,
+                          nullptr, 0, 0.0f, stream);
+}
+
+extern "C" int dsk_qkv_rope_append_rn(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
+                                      const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                      const float* inv_freq, const int32_t* seq_lens, const int32_t* block_table,
+                                      int max_pages, int page, int kv_dtype, void* k_pool, void* v_pool,
+                                      uint32_t* k_sb, uint32_t* v_sb, uint16_t* q_out, const float* x_ssq,
+                                      int x_tiles, float x_eps, dsk_stream_t stream) {
+  DSK_REQUIRE(x_ssq && x_tiles > 0 && x_eps >= 0.0f, "dsk_qkv_rope_append_rn: needs the input's row-scale partials");
+  return qkv_append_entry(qkv, qkv_splits, B, W, nq, nkv, hd, q_norm, k_norm, nullptr, eps, inv_freq, seq_lens, 0,
+                          block_table, max_pages, page, kv_dtype, k_pool, v_pool, k_sb, v_sb, q_out, x_ssq, x_tiles,
+                          x_eps, stream);
+}
+
+static int qkv_append_entry(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
+                            const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* v_norm, float eps,
+                            const float* inv_freq, const int32_t* seq_lens, int pos_offset, const int32_t* block_table,
+                            int max_pages, int page, int kv_dtype, void* k_pool, void* v_pool, uint32_t* k_sb,
+                            uint32_t* v_sb, uint16_t* q_out, const float* x_ssq, int x_tiles, float x_eps,
+                            dsk_stream_t stream) {
   DSK_REQUIRE(qkv && inv_freq && seq_lens && block_table && k_pool && v_pool && (q_out || nq == 0),
               "dsk_qkv_rope_append: null pointer");
   DSK_REQUIRE(hd == 128 || hd == 256 || hd == 512, "dsk_qkv_rope_append: head_dim %d not supported (128, 256, 512)",
@@ -961,12 +1007,22 @@ extern "C" int dsk_qkv_norm_rope_append(const void* qkv, int qkv_splits, int B, 
   const int tasks = B * W * (nq + 2 * nkv);
   dim3 grid((unsigned)ceil_div(tasks, 4));
 #define DSK_APPEND(HDV)                                                                                             \
-  hipLaunchKernelGGL(qkv_rope_append_kernel<HDV>, grid, dim3(256), 0, as_stream(stream), qkv, qkv_splits, B, W, nq, \
-                     nkv, q_norm, k_norm, v_norm, eps, inv_freq, seq_lens, pos_offset, block_table, max_pages, page, \
-                     kv_dtype, k_pool, v_pool, k_sb, v_sb, q_out)
-  if (hd == 128) DSK_APPEND(128);
-  else if (hd == 256) DSK_APPEND(256);
-  else DSK_APPEND(512);
+  if (x_ssq)                                                                                                        \
+    hipLaunchKernelGGL((qkv_rope_append_kernel<HDV, true>), grid, dim3(256), 0, as_stream(stream), qkv, qkv_splits, \
+                       B, W, nq, nkv, q_norm, k_norm, v_norm, eps, inv_freq, seq_lens, pos_offset, block_table,     \
+                       max_pages, page, kv_dtype, k_pool, v_pool, k_sb, v_sb, q_out, x_ssq, x_tiles,                \
+                       (float)(x_tiles * 16), x_eps);                                                               \
+  else                                                                                                              \
+    hipLaunchKernelGGL((qkv_rope_append_kernel<HDV, false>), grid, dim3(256), 0, as_stream(stream), qkv, qkv_splits,\
+                       B, W, nq, nkv, q_norm, k_norm, v_norm, eps, inv_freq, seq_lens, pos_offset, block_table,     \
+                       max_pages, page, kv_dtype, k_pool, v_pool, k_sb, v_sb, q_out, nullptr, 0, 0.0f, 0.0f)
+  if (hd == 128) {
+    DSK_APPEND(128);
+  } else if (hd == 256) {
+    DSK_APPEND(256);
+  } else {
+    DSK_APPEND(512);
+  }
 #undef DSK_APPEND
   DSK_LAUNCH_CHECK("dsk_qkv_rope_append");
   return DSK_OK;

@@ -50,6 +50,9 @@ SIGNATURES: dict[str, tuple] = {
     "dsk_qkv_norm_rope_append": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p,
                                          c_void_p, c_float, c_void_p, c_void_p, c_int, c_void_p, c_int, c_int, c_int,
                                          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "dsk_qkv_rope_append_rn": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float,
+                                       c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p,
+                                       c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_float, c_void_p]),
     "dsk_attn_ws_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "dsk_attention": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_int, c_int, c_float,
                               c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p,

@@ -180,6 +180,10 @@ class Packed:
         ssq = torch.empty((M, K // 16), dtype=torch.float32, device=device) if normed_later else None
         return Packed(torch.empty(n // 2, dtype=torch.bfloat16, device=device), M, K, ssq, float(eps))
 
+    def plain(self) -> "Packed":
+        """The packed values alone (a GEMM over them leaves the row scale to its consumer)."""
+        return Packed(self.data, self.M, self.K)
+
     def row_scale(self) -> torch.Tensor | None:
         """[M] f32 rsqrt(mean(h^2) + eps) of a normed-later activation (for checks)."""
         if self.ssq is None:
@@ -337,9 +341,11 @@ def rope_inv_freq(head_dim: int, theta: float, device, *, rotary_fraction: float
 
 
 def qkv_rope_append(qkv, B, W, nq, nkv, hd, q_norm, k_norm, eps, inv_freq, seq_lens, block_table,
-                    page, kv_dtype, k_pool, v_pool, k_sb=None, v_sb=None, q_out=None, pos_offset=0, v_norm=None):
+                    page, kv_dtype, k_pool, v_pool, k_sb=None, v_sb=None, q_out=None, pos_offset=0, v_norm=None,
+                    x: Packed | None = None):
     """qkv: bf16 [B*W, (nq+2nkv)*hd] or f32 split-K partials [S, B*W, (nq+2nkv)*hd]. v_norm
-    (bf16 [hd]) RMSNorms V too."""
+    (bf16 [hd]) RMSNorms V too. x: the projection's normed-later input, whose row scale the
+    summed partials take here (the projection then ran without it)."""
     splits = qkv.shape[0] if qkv.dim() == 3 else 0
     if splits and (qkv.dtype != torch.float32 or not qkv.is_contiguous()):
         raise ValueError("qkv partials must be contiguous f32")
@@ -347,6 +353,13 @@ def qkv_rope_append(qkv, B, W, nq, nkv, hd, q_norm, k_norm, eps, inv_freq, seq_l
         qkv = qkv.contiguous().to(torch.bfloat16)
     if q_out is None and nq:
         q_out = torch.empty((B * W, nq * hd), dtype=torch.bfloat16, device=qkv.device)
+    if x is not None and x.ssq is not None:
+        if pos_offset or v_norm is not None:
+            raise ValueError("qkv_rope_append: a normed-later input takes no pos_offset / v_norm")
+        call("dsk_qkv_rope_append_rn", ptr(qkv), splits, B, W, nq, nkv, hd, ptr(q_norm), ptr(k_norm), float(eps),
+             ptr(inv_freq), ptr(seq_lens), ptr(block_table), block_table.shape[1], page, kv_dtype, ptr(k_pool),
+             ptr(v_pool), ptr(k_sb), ptr(v_sb), ptr(q_out), ptr(x.ssq), x.K // 16, float(x.eps), stream_ptr())
+        return q_out
     call("dsk_qkv_norm_rope_append", ptr(qkv), splits, B, W, nq, nkv, hd, ptr(q_norm), ptr(k_norm), ptr(v_norm),
          float(eps), ptr(inv_freq), ptr(seq_lens), int(pos_offset), ptr(block_table), block_table.shape[1], page,
          kv_dtype, ptr(k_pool), ptr(v_pool), ptr(k_sb), ptr(v_sb), ptr(q_out), stream_ptr())

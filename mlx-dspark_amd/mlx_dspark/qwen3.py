@@ -146,12 +146,13 @@ class Qwen3W8:
         nq, nkv, hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
         M, H = B * W, a.hidden_size
         eps = a.rms_norm_eps
-        qkv = ops.w8_gemm(x, L.qkv, epi=ops.DSK_EPI_PARTIAL)
+        # a normed-later x: the split-K partials take its row scale where they are summed
+        qkv = ops.w8_gemm(x.plain(), L.qkv, epi=ops.DSK_EPI_PARTIAL)
         k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
         inv_freq = self.inv_freq_local if a.is_sliding(l) else self.inv_freq
         q = ops.qkv_rope_append(qkv, B, W, nq, nkv, hd, L.q_norm, L.k_norm, eps, inv_freq,
                                 cache.seq_lens, cache.block_table, cache.page, cache.kv_dtype,
-                                k_pool, v_pool, k_sb, v_sb)
+                                k_pool, v_pool, k_sb, v_sb, x=x)
         o = ops.attention(q, B, W, nq, nkv, hd, a.attn_scale, cache.seq_lens, cache.max_ctx,
                           cache.block_table, cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb,
                           causal=causal, window=a.window(l), packed=True)
@@ -211,7 +212,11 @@ class Qwen3W8:
         out = None
         if logits != "none":
             if logits != "all":
-                x = ops.pack(h.view(B, W, H)[:, -1], self.norm, eps)
+                hl = h.view(B, W, H)[:, -1]
+                if a.sandwich_norms:
+                    x = ops.pack(hl, self.norm, eps)
+                else:   # normed later, as the all-rows head is: both round the same way
+                    x = ops.pack_rn(M=B, K=H, h=hl, norm_w=self.norm, eps=eps)
             Mr = x.M
             out = logits_out if logits_out is not None else torch.empty(
                 (Mr, a.vocab_size), dtype=torch.float32, device=self.device)

@@ -158,22 +158,30 @@ def test_q8_dflash_graph_eager_and_greedy(dev, q8):
     s = a.token_ids[:48]
     # every token against the engine's other forward path, teacher-forced: the prompt's
     # chunked prefill, then one 47-row forward over the stream
-    cache = target.make_cache(max_ctx=4096 + 64)
-    first = target.model.prefill(prompt, cache)[0][0, -1:]
-    rest = target.model.forward(torch.tensor([s[:-1]], dtype=torch.int32, device=dev), cache, None)[0][0]
-    rows = torch.cat([first, rest]).float()
-    rn = rows / rows.pow(2).mean(-1, keepdim=True).sqrt()
-    t = torch.tensor(s, device=rows.device)
+    def teacher_forced(chunk):
+        cache = target.make_cache(max_ctx=4096 + 64)
+        first = target.model.prefill(prompt, cache)[0][0, -1:]
+        ids = torch.tensor([s[:-1]], dtype=torch.int32, device=dev)
+        rest = [target.model.forward(ids[:, c:c + chunk], cache, None)[0][0] for c in range(0, 47, chunk)]
+        rows = torch.cat([first] + rest).float()
+        return rows / rows.pow(2).mean(-1, keepdim=True).sqrt()
+    rn = teacher_forced(47)
+    # the same stream through 16-row forwards (the verify's GEMM plans): how far two valid bf16
+    # evaluations of the 36-layer model drift apart, the floor for a flipped near-tie here
+    drift = float((rn - teacher_forced(16)).abs().max())
+    bound = max(FULLWIDTH_FLIP, 1.5 * drift)
+    t = torch.tensor(s, device=rn.device)
     gap = rn.max(-1).values - rn.gather(1, t[:, None])[:, 0]
     exact = int((gap == 0).sum())
-    print(f"teacher-forced: {exact}/48 DFlash tokens are the other path's argmax, largest gap {float(gap.max()):.4f}",
-          flush=True)
-    assert float(gap.max()) <= FULLWIDTH_FLIP and exact >= 40
+    print(f"teacher-forced: {exact}/48 DFlash tokens are the other path's argmax, largest gap {float(gap.max()):.4f}"
+          f" (47- vs 16-row forwards differ by up to {drift:.4f}; bound {bound:.4f})", flush=True)
+    assert float(gap.max()) <= bound and exact >= 40
+    rows = rn
     base = greedy_generate(target, tok, prompt_ids=prompt, max_new_tokens=48)
     n = _common(s, base.token_ids)
     print(f"DFlash rounds and the one-token decode agree on {n} of 48 tokens", flush=True)
     if n < 48:       # the first difference is a near-tie of the engine's own logits
-        assert _margin(rows[n]) <= FULLWIDTH_FLIP, (n, _margin(rows[n]))
+        assert _margin(rows[n]) <= bound, (n, _margin(rows[n]))
 
 
 def test_g12_sampled_dspark_rounds_bit_exact(dev, monkeypatch):

@@ -50,7 +50,8 @@ def _fill_context(cache, l, K, V):
     return held
 
 
-@pytest.mark.parametrize("shape,ctx,W,kv_bits", [("qwen3-8b", 4096, 16, 8), ("qwen3-0.6b", 768, 9, None)])
+@pytest.mark.parametrize("shape,ctx,W,kv_bits", [("qwen3-8b", 4096, 16, 8), ("qwen3-0.6b", 768, 9, None),
+                                                  ("qwen3-8b", 4096, 47, 8), ("qwen3-8b", 4096, 64, 8)])
 def test_verify_logits_full_width(dev, shape, ctx, W, kv_bits):
     from mlx_dspark import synthetic
     print(f"full-width verify {shape} ctx={ctx} W={W} kv_bits={kv_bits}", flush=True)
