@@ -110,10 +110,14 @@ def load_target(repo_or_path: str = DEFAULT_TARGET, *, require_tap: bool = False
 
 def load_dflash(repo_or_path: str, *, quantize: bool = True, bits: int = 4, group_size: int = 64,
                 target_args: TargetArgs | None = None, seed: int = 1, keep_mlx: bool = False):
-    """(drafter, config) for a synthetic DFlash drafter (load.py:224-289); its linear layers
-    4-bit by default, as the reference quantizes them (8 also runs)."""
+    """(drafter, config) for a DFlash drafter (load.py:224-289): a local z-lab-format checkpoint
+    directory (exact key match; drafter_ckpt.py) or a synthetic name; its linear layers 4-bit by
+    default, as the reference quantizes them (8 also runs)."""
     if bits not in (4, 8) or group_size != 64 or not quantize:
         raise ValueError("this engine runs 4- or 8-bit (group 64) drafters")
+    from . import checkpoint, drafter_ckpt
+    if checkpoint.is_checkpoint_dir(repo_or_path):
+        return drafter_ckpt.load_dflash(repo_or_path, bits=bits, keep_mlx=keep_mlx)
     key = _synthetic_key(repo_or_path)
     if not key.startswith("dflash-"):
         raise ValueError(f"{repo_or_path!r} is not a DFlash drafter name")
@@ -128,12 +132,19 @@ def load_dflash(repo_or_path: str, *, quantize: bool = True, bits: int = 4, grou
 def load_drafter(repo_or_path: str = DEFAULT_DRAFTER, *, quantize: bool = True, bits: int = 4,
                  group_size: int = 64, strict: bool = True, target_args: TargetArgs | None = None, seed: int = 2,
                  keep_mlx: bool = False, **shape):
-    """(drafter, config) for a synthetic DSpark drafter (load.py:155-215); linear layers 4-bit by
-    default, as the reference quantizes them (8 also runs; the embedding and Markov head 8-bit).
-    ``shape`` overrides the builder's drafter knobs (num_hidden_layers, block_size, taps,
-    markov_rank, confidence, family: gemma4 by default for Gemma-style targets)."""
+    """(drafter, config) for a DSpark drafter (load.py:155-215): a local DeepSpec-format
+    checkpoint directory (key names checked, strict by default; drafter_ckpt.py) or a synthetic
+    name. Every linear and embedding table is quantized to ``bits`` (4 by default, as the
+    reference quantizes them; 8 also runs). ``shape`` overrides the synthetic builder's drafter
+    knobs (num_hidden_layers, block_size, taps, markov_rank, confidence, family: gemma4 by default
+    for Gemma-style targets)."""
     if bits not in (4, 8) or group_size != 64 or not quantize:
         raise ValueError("this engine runs 4- or 8-bit (group 64) drafters")
+    from . import checkpoint, drafter_ckpt
+    if checkpoint.is_checkpoint_dir(repo_or_path):
+        if shape:
+            raise ValueError(f"drafter shape overrides {sorted(shape)} apply to synthetic drafters only")
+        return drafter_ckpt.load_dspark(repo_or_path, bits=bits, strict=strict, keep_mlx=keep_mlx)
     key = _synthetic_key(repo_or_path)
     if not key.startswith("dspark-"):
         raise ValueError(f"{repo_or_path!r} is not a DSpark drafter name")

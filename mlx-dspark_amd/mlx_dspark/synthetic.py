@@ -186,8 +186,9 @@ def build_dspark(target_args: TargetArgs, seed: int = 2, device="cuda", keep_mlx
     family "gemma4": the target's q heads over one global kv head of ``global_head_dim``
     (k_eq_v, v_norm, proportional RoPE over a quarter of the dims), sandwich norms with
     layer_scalar 1, tanh-GeLU MLP, soft-cap 30, embedding scale sqrt(hidden).
-    bits: the linear layers' code width (4, the reference's drafter default, or 8); the
-    embedding and the Markov head stay 8-bit."""
+    bits: the code width of every linear and embedding table (4, the reference's drafter default,
+    or 8). Tables are gathered row by row and hold one code per byte; the Markov w2 projection
+    keeps 4-bit code values in the 8-bit tile layout its kernel streams."""
     from .config import DSparkConfig
     from .model import ConfidenceHead, DSparkDrafter, MarkovHead
 
@@ -232,8 +233,11 @@ def build_dspark(target_args: TargetArgs, seed: int = 2, device="cuda", keep_mlx
             attn_out_norm=ones(H, device) if gemma else None, ff_out_norm=ones(H, device) if gemma else None))
     markov = None
     if markov_rank > 0:
-        w1 = w8_table(a.vocab_size, markov_rank, seed, "dspark.markov_w1", device)
-        w2 = w8(a.vocab_size, markov_rank, seed, "dspark.markov_w2", device, keep_mlx)
+        w1 = w8_table(a.vocab_size, markov_rank, seed, "dspark.markov_w1", device, bits=bits)
+        q2, s2, b2 = W8Weight.quantize_mlx(randn((a.vocab_size, markov_rank), seed, "dspark.markov_w2", device), bits)
+        w2 = W8Weight.from_mlx(q2, s2, b2, bits=8)
+        if keep_mlx:
+            w2.mlx = (q2, s2, b2)
         markov = MarkovHead(w1, w2)
     conf = None
     if confidence:
@@ -245,7 +249,7 @@ def build_dspark(target_args: TargetArgs, seed: int = 2, device="cuda", keep_mlx
         if keep_mlx:
             cw.mlx = (q, s_, b_)
         conf = ConfidenceHead(cw, 0.5)
-    d = DSparkDrafter(cfg, embed=w8_table(a.vocab_size, H, seed, "dspark.embed_tokens", device),
+    d = DSparkDrafter(cfg, embed=w8_table(a.vocab_size, H, seed, "dspark.embed_tokens", device, bits=bits),
                       fc=w8(H, len(taps) * H, seed, "dspark.fc", device, keep_mlx, bits=bits),
                       hidden_norm=ones(H, device),
                       layers=layers, norm=ones(H, device),
