@@ -61,33 +61,43 @@ def kv_bytes_per_token(args, kv_bits) -> int:
 
 def gemm_roofline(model, M: int, reps: int = 10):
     """In-graph average launch duration of the W8 GEMM at every verify-step shape, with the
-    epilogue the forward uses (split-K partials for qkv / o / down, fused SwiGLU for gate_up,
-    f32 logits for the head). One CUDA graph per shape holds one launch per layer, each on
-    that layer's weights (so every launch streams its weights from HBM), replayed `reps` times
-    between two HIP events recorded on the launch stream; the average includes the ~1.5 us
-    dispatch gap between back-to-back graph kernels, which a kernel trace does not count."""
+    epilogue and input the forward uses: split-K partials for qkv, the residual-add epilogue for
+    o and down, the fused SwiGLU of a normed-later x for gate_up, f32 logits of a normed-later x
+    for the head. One CUDA graph per shape holds one launch per layer, each on that layer's
+    weights (so every launch streams its weights from HBM), replayed `reps` times between two
+    HIP events recorded on the launch stream; the average includes the dispatch gap between
+    back-to-back graph kernels, which a kernel trace does not count."""
     import torch
     from mlx_dspark import ops
 
     dev = model.device
-    P, SW = ops.DSK_EPI_PARTIAL, ops.DSK_EPI_SWIGLU
-    shapes = {"qkv": ([L.qkv for L in model.layers], P), "o": ([L.o for L in model.layers], P),
-              "gate_up": ([L.gate_up for L in model.layers], SW), "down": ([L.down for L in model.layers], P),
+    P, SW, R = ops.DSK_EPI_PARTIAL, ops.DSK_EPI_SWIGLU, ops.DSK_EPI_RESIDUAL
+    shapes = {"qkv": ([L.qkv for L in model.layers], P), "o": ([L.o for L in model.layers], R),
+              "gate_up": ([L.gate_up for L in model.layers], SW), "down": ([L.down for L in model.layers], R),
               "lm_head": ([model.lm_head], ops.DSK_EPI_STORE)}
     res = {}
     stream = torch.cuda.current_stream()
+    eps = model.args.rms_norm_eps
     for name, (ws, epi) in shapes.items():
-        K = ws[0].K
-        x = ops.pack(torch.randn(M, K, device=dev).to(torch.bfloat16))
-        out = None
-        if epi == ops.DSK_EPI_STORE:
-            out = torch.empty(M, ws[0].N, device=dev, dtype=torch.float32)
-        y = ops.w8_gemm(x, ws[0], epi=epi, out=out)
+        K, N = ws[0].K, ws[0].N
+        xr = torch.randn(M, K, device=dev).to(torch.bfloat16)
+        normed_later = name in ("gate_up", "lm_head")
+        x = ops.pack_rn(M=M, K=K, h=xr, norm_w=model.norm, eps=eps) if normed_later else ops.pack(xr)
+        h = torch.randn(M, N, device=dev).to(torch.bfloat16)
+
+        def launch(w, y=None):
+            if epi == R:
+                return ops.w8_residual(x, w, h, next_norm=model.norm, eps=eps)
+            out = y if y is not None else (torch.empty(M, N, device=dev, dtype=torch.float32)
+                                           if epi == ops.DSK_EPI_STORE else None)
+            return ops.w8_gemm(x, w, epi=epi, out=out)
+
+        y = launch(ws[0])
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for w in ws:
-                ops.w8_gemm(x, w, epi=epi, out=y)
+                launch(w, None if epi == R else y)
         for _ in range(2):
             g.replay()
         s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -98,8 +108,9 @@ def gemm_roofline(model, M: int, reps: int = 10):
         e_ev.record(stream)
         torch.cuda.synchronize()
         us = s_ev.elapsed_time(e_ev) * 1e3 / (reps * len(ws))
-        # algorithmic bytes: weights (q + scale/bias) + activation in + output out
-        out_b = {P: 4 * ops.gemm_splits(M, ws[0].N, K), SW: 1, ops.DSK_EPI_STORE: 4}[epi] * M * ws[0].N
+        # algorithmic bytes: weights (q + scale/bias) + activation in + output out (the residual
+        # epilogue reads and writes h and writes the packed next input)
+        out_b = {P: 4 * ops.gemm_splits(M, ws[0].N, K), SW: 1, ops.DSK_EPI_STORE: 4, R: 6}[epi] * M * ws[0].N
         by = ws[0].N * K * 1.0625 + M * K * 2 + out_b
         res[name] = {"us": round(us, 2), "bytes": int(by), "GBs": round(by / us / 1e3, 1), "launches": len(ws)}
         del g
@@ -395,11 +406,25 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         print(json.dumps({"verify_eager": args.verify_eager, "rows": W, "context": cache.lengths[0]}), flush=True)
         return 0
+    # the prompt's dense prefill (layer by layer over all rows), timed after a short warm-up
+    # prefill that settles the library GEMM's plans
+    wc = target.make_cache(max_ctx=1024)
+    model.prefill(prompt[:512], wc, tap)
+    del wc
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
     logits, fused = model.prefill(prompt, cache, tap)
+    torch.cuda.synchronize()
+    prefill_ms = (time.perf_counter() - t0) * 1e3
+    a_ = model.args
+    lin_params = sum(L.qkv.N * L.qkv.K + L.o.N * L.o.K + L.gate_up.N * L.gate_up.K + L.down.N * L.down.K
+                     for L in model.layers)
+    attn_flop = 4 * a_.num_attention_heads * a_.head_dim * a_.num_hidden_layers * args.ctx * (args.ctx + 1) / 2
+    prefill_flop = 2 * args.ctx * lin_params + attn_flop
+    log(f"prefill {args.ctx} tokens (dense): {prefill_ms:.1f} ms, {prefill_flop / prefill_ms / 1e9:.0f} TFLOP/s")
     drafter.ingest(fused, dcache)
     pending = _pick(logits[0, -1], 0.0)
     torch.cuda.synchronize()
-    log(f"prefill {args.ctx} tokens: {time.time() - t0:.1f} s")
 
     rnd = _DFlashRound(target, drafter, cache, dcache, cap, 0.0, 1.0, 0, 0)
     rnd.pending.fill_(pending)
@@ -507,7 +532,10 @@ def main(argv=None) -> int:
         "verify_us": round(verify_us, 1),
         "verify_alg_bytes": int(alg_bytes),
         "verify_roofline_frac": round(verify_frac, 4),
-        "roofline": {"kernel": "w8_gemm_kernel<1, 2, 2, 8, 1, true> (W8 GEMM, gate_up 24576x4096, M=16, SwiGLU)",
+        "prefill_ms": round(prefill_ms, 1),
+        "prefill_tflops": round(prefill_flop / prefill_ms / 1e9, 1),
+        "roofline": {"kernel": "w8_gemm_kernel<1, 2, 2, 8, 5, true, 8> (W8 GEMM, gate_up 24576x4096, M=16, "
+                               "SwiGLU of a normed-later x)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_GATE_UP,
                      "bytes_per_launch": dom["bytes"], "us_per_launch": dom["us"], "per_shape": shapes},

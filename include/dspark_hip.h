@@ -157,6 +157,25 @@ int dsk_w8_gemm_rn(const uint16_t* x, const uint8_t* wt, const uint32_t* sb, int
                    uint16_t* copy, int64_t ldc, const uint16_t* next_norm_w, float* ssq_out,
                    dsk_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Dense prefill (src/mlx_dspark/generate.py:613-656, _prefill_tapped: the prompt in chunks of
+ * PREFILL_CHUNK = 2048 rows through the target). A long prompt runs layer by layer over all of
+ * its rows: each layer's weights are expanded to bf16 once and multiplied by a library GEMM
+ * (hipBLASLt), with these kernels around it.
+ * dsk_w8_dequant_rows: a dsk_w8_repack (bits 8) / dsk_w4_repack (bits 4) weight -> bf16 [N, K]
+ *   rows out[n][k] = bf16(s * q + b) in source row order (paired: gate rows, then up rows).
+ * dsk_rows_rmsnorm: y[m] = bf16((x[m] * rsqrt(mean(x[m]^2) + eps)) * w) for M rows (the
+ *   RMSNorm formula of dsk_act_pack), row strides ldx / ldy.
+ * dsk_rows_gated: out[m][i] = bf16(bf16(act(gate)) * up) with gate = gu[m][i], up = gu[m][I + i],
+ *   act = DSK_EPI_SWIGLU (SiLU) or DSK_EPI_GEGLU (tanh GeLU), as dsk_w8_gemm's gated epilogue.
+ * ------------------------------------------------------------------------------------- */
+int dsk_w8_dequant_rows(const uint8_t* wt, const uint32_t* sb, int bits, int64_t N, int64_t K,
+                        int paired, uint16_t* out, dsk_stream_t stream);
+int dsk_rows_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* w, float eps, int64_t M,
+                     int64_t K, uint16_t* y, int64_t ldy, dsk_stream_t stream);
+int dsk_rows_gated(const uint16_t* gu, int64_t ldg, int64_t M, int64_t I, int act, uint16_t* out,
+                   int64_t ldo, dsk_stream_t stream);
+
 /* 4-bit codes (MLX nn.quantize bits=4, group 64: the reference's drafter default,
  * src/mlx_dspark/load.py:155-215, :224-289 with bits=4; 4-bit target checkpoints).
  * dsk_w4_quantize: as dsk_w8_quantize with codes 0..15 (s = (max - min) / 15), one per byte.
@@ -234,7 +253,10 @@ int dsk_qkv_norm_rope_append(const void* qkv, int qkv_splits, int B, int W, int 
  * fp32 (m, l); the splits are combined by a second kernel on the same stream; no state is
  * kept between calls). Every block_table entry of a row must name a valid page: a split
  * reads its whole key range through the table before it knows the row's length.
- * head_dim 128 or 256, or 512 (the gemma4 drafter's global head) without the fused entry. */
+ * head_dim 128 or 256, or 512 (the gemma4 drafter's global head) without the fused entry.
+ * W > 64 (a prefill's many queries): each workgroup takes one group of 4 query tiles over a split
+ * of 1024 keys, and a causal split past every query of a group is skipped (each row's combine
+ * reads the splits up to its own position). */
 size_t dsk_attn_ws_bytes(int B, int W, int nq, int hd, int max_ctx);
 int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, int hd, float scale,
                   int causal, int window, float softcap, const int32_t* seq_lens,

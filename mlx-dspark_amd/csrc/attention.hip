@@ -519,6 +519,12 @@ __global__ __launch_bounds__(256 * WPT) __attribute__((amdgpu_waves_per_eu(1, 2)
     j_beg = split * kps;
     const int kend = FUSED ? min(off, jmax) : Lk;  // the fused context splits stop at the cache
     if (j_beg >= kend) return;
+    // causal: a split past every query of this workgroup's tile group is never read (the
+    // combine counts each row's splits up to its own position)
+    if (causal && gridDim.y > 1) {
+      const int last_row = min(a.R, ((int)blockIdx.y * 4 + 4) * 16) - 1;
+      if (j_beg > off + last_row / a.G) return;
+    }
     j_end = min(kend, j_beg + kps);
   }
   const int nb = newsplit ? 1 : (j_end - j_beg + KEYS - 1) / KEYS;
@@ -727,7 +733,8 @@ __global__ __launch_bounds__(256 * WPT) __attribute__((amdgpu_waves_per_eu(1, 2)
     if constexpr (WPT == 2) {
       static_assert(4 * (DT * 4 + 2) * 64 * sizeof(float) <= KEYS * KROW * sizeof(uint16_t), "merge area");
       // the second key half's (m, l, o) through LDS (the K tile area) into the first half's waves
-      float* mb = reinterpret_cast<float*>(ks) + mytile * (DT * 4 + 2) * 64 + lane;
+      // indexed by the tile's place in this workgroup (0..3), not its global number
+      float* mb = reinterpret_cast<float*>(ks) + (wv & 3) * (DT * 4 + 2) * 64 + lane;
       __syncthreads();  // every wave is done with the last block
       if (half == 1 && mytile < ntiles) {
         mb[0] = m_run;
@@ -791,8 +798,11 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   // live splits: the first ns; with a.fused the context splits [0, ns - 1) and the new-token
   // split (the last one)
   const int jmax = a.max_pages * a.page;
+  // causal rows read the splits up to their own position (the attention kernel may skip later
+  // ones for whole query-tile groups); the fused form keeps its new-token split last
+  const int visible = a.causal && !a.fused ? a.seq_lens[b] + r / a.G + 1 : a.seq_lens[b] + a.W;
   const int ns = a.fused ? min((min(a.seq_lens[b], jmax) + a.kps - 1) / a.kps, a.nsplit - 1) + 1
-                         : min(a.nsplit, (min(a.seq_lens[b] + a.W, jmax) + a.kps - 1) / a.kps);
+                         : min(a.nsplit, (min(visible, jmax) + a.kps - 1) / a.kps);
   const int nlast = a.fused ? a.nsplit - 1 - (ns - 1) : 0;  // split index shift of the last live one
   const uint16_t* base_o = a.part_o + ((size_t)bk * a.nsplit * a.R + r) * HD + lane * PER;
   const float* base_ml = a.part_ml + ((size_t)bk * a.nsplit * a.R + r) * 2;
@@ -886,8 +896,12 @@ static int attn_split_keys(int hd, int) {
   return hd == 128 ? Split<128>::KEYS : (hd == 256 ? Split<256>::KEYS : Split<512>::KEYS);
 }
 static int attn_nsplit(int hd, int max_ctx) { return (int)ceil_div(max_ctx, attn_split_keys(hd, max_ctx)); }
-// blocks per split of the streamed path: about 24 splits per (row, kv head), at most 8 blocks
-static int attn_blocks(int hd, int max_ctx) {
+// blocks per split of the streamed path: about 24 splits per (row, kv head), at most 8 blocks;
+// a many-query pass (more than 64 new tokens: a prefill) takes 8 blocks per split, its query
+// tiles giving the parallelism
+constexpr int kAttnVerifyMaxW = 64;
+static int attn_blocks(int hd, int max_ctx, int W = 1) {
+  if (W > kAttnVerifyMaxW) return 8;
   const int64_t blocks = ceil_div(max_ctx, attn_split_keys(hd, max_ctx));
   return (int)std::min<int64_t>(8, std::max<int64_t>(1, ceil_div(blocks, 24)));
 }
@@ -913,15 +927,17 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
   a.G = a.nq / a.nkv;
   a.R = a.W * a.G;
   const int tiles = (a.R + 15) / 16;
-  // head_dim 512: one tile per wave, query-tile groups on the grid's y axis
-  const int QT = hd == 512 ? 1 : (tiles + 3) / 4;
-  const int tile_groups = hd == 512 ? (tiles + 3) / 4 : 1;
+  // head_dim 512 and many-query passes: one tile per wave, query-tile groups on the grid's y axis
+  const bool grouped = hd == 512 || a.W > kAttnVerifyMaxW;
+  const int QT = grouped ? 1 : (tiles + 3) / 4;
+  const int tile_groups = grouped ? (tiles + 3) / 4 : 1;
   DSK_REQUIRE(QT <= (hd == 128 ? 4 : 2), "%s: W*G=%d query rows per kv head exceeds %d", who, a.R,
               (hd == 128 ? 256 : 128));
+  DSK_REQUIRE(tile_groups <= 65535, "%s: %d query rows per kv head", who, a.R);
   DSK_REQUIRE(!fused || a.W <= 64, "%s: W=%d new tokens exceeds 64", who, a.W);
   DSK_REQUIRE(!a.out_packed || (a.B * a.W <= 64 && (a.nq * hd) % 64 == 0), "%s: packed output needs B*W <= 64", who);
   a.fused = fused ? 1 : 0;
-  int nblk = (fused || QT != 1) ? 1 : attn_blocks(hd, max_ctx);
+  int nblk = (fused || QT != 1) ? 1 : attn_blocks(hd, max_ctx, a.W);
   while (nblk > 1 && attn_split_keys(hd, max_ctx) * nblk / a.page + 1 > kAttnMaxSplitPages) --nblk;
   DSK_REQUIRE(attn_split_keys(hd, max_ctx) / a.page + 1 <= kAttnMaxSplitPages, "%s: page size %d too small", who,
               a.page);
@@ -1042,6 +1058,8 @@ extern "C" int dsk_qkv_rope_append(const void* qkv, int qkv_splits, int B, int W
 extern "C" size_t dsk_attn_ws_bytes(int B, int W, int nq, int hd, int max_ctx) {
   if (B <= 0 || W <= 0 || nq <= 0 || hd <= 0 || max_ctx <= 0) return 0;
   if (hd != 128 && hd != 256 && hd != 512) return 0;
+  if (W > kAttnVerifyMaxW)  // many-query passes: splits of 8 blocks
+    return attn_ws_need(B, W, nq, hd, (int)ceil_div(max_ctx, attn_split_keys(hd, max_ctx) * 8));
   return attn_ws_need(B, W, nq, hd, attn_nsplit(hd, max_ctx) + 1);  // + the fused new-token split
 }
 

@@ -18,6 +18,7 @@ from ._hip import (DSK_BF16, DSK_EPI_GEGLU, DSK_EPI_PARTIAL, DSK_EPI_RESIDUAL, D
 
 __all__ = [
     "W8Weight", "W8Table", "Workspace", "Packed", "act_pack", "pack", "pack_rn", "w8_gemm", "w8_residual", "w8_embed",
+    "w8_dequant", "rows_rmsnorm", "rows_gated",
     "qkv_rope_append", "attention", "qkv_attention", "row_logprobs", "accept_greedy", "accept_sample", "sample_rows",
     "argmax_rows", "lens_add",
     "rope_inv_freq", "DSK_EPI_STORE", "DSK_EPI_SWIGLU", "DSK_EPI_GEGLU", "DSK_EPI_PARTIAL", "DSK_KV_BF16",
@@ -311,6 +312,38 @@ def w8_gemm(x: Packed, w: W8Weight, *, epi: int = DSK_EPI_STORE, out=None, out_d
     call("dsk_w8_gemm" if w.bits == 8 else "dsk_w4_gemm", ptr(x.data), ptr(w.wt), ptr(w.sb), M, w.N, w.K, int(epi),
          ptr(ydata), yd, ldy, ptr(residual), residual.stride(0) if residual is not None else 0, float(softcap),
          stream_ptr())
+    return out
+
+
+def w8_dequant(w: W8Weight, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 [N, K] rows bf16(s * q + b) of a W8 / W4 weight in source row order (a paired
+    gate|up weight: the gate rows, then the up rows), for a library GEMM over many rows."""
+    n = w.N * w.K
+    if out is None:
+        out = torch.empty((w.N, w.K), dtype=torch.bfloat16, device=w.wt.device)
+    elif out.dtype != torch.bfloat16 or not out.is_contiguous() or out.numel() < n:
+        raise ValueError("w8_dequant: out must be a contiguous bf16 buffer of N*K elements")
+    out = out.view(-1)[:n].view(w.N, w.K)
+    call("dsk_w8_dequant_rows", ptr(w.wt), ptr(w.sb), w.bits, w.N, w.K, int(w.paired), ptr(out), stream_ptr())
+    return out
+
+
+def rows_rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16((x * rsqrt(mean(x^2) + eps)) * w) over the rows of x [M, K] bf16 (any M)."""
+    if x.dtype != torch.bfloat16 or not _rows_ok(x):
+        raise ValueError("rows_rmsnorm: x must be bf16 with unit column stride and aligned rows")
+    out = torch.empty_like(x) if out is None else out
+    call("dsk_rows_rmsnorm", ptr(x), x.stride(0), ptr(w), float(eps), x.shape[0], x.shape[1], ptr(out), out.stride(0),
+         stream_ptr())
+    return out
+
+
+def rows_gated(gu: torch.Tensor, act: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16(bf16(act(gate)) * up) for gu [M, 2I] bf16 = [gate | up] rows (act = DSK_EPI_SWIGLU
+    or DSK_EPI_GEGLU), as the GEMM's gated epilogue."""
+    M, I2 = gu.shape
+    out = torch.empty((M, I2 // 2), dtype=torch.bfloat16, device=gu.device) if out is None else out
+    call("dsk_rows_gated", ptr(gu), gu.stride(0), M, I2 // 2, int(act), ptr(out), out.stride(0), stream_ptr())
     return out
 
 

@@ -30,6 +30,8 @@ from .kv import PagedKVCache
 from .ops import DSK_EPI_GEGLU, DSK_EPI_SWIGLU, W8Table, W8Weight
 
 MAX_ROWS = 64  # rows per kernel pass (M of the skinny GEMM)
+DENSE_MIN_ROWS = 256   # prompts from this length prefill layer by layer through the library GEMM
+PREFILL_CHUNK = 2048   # prompt rows handed to a drafter per on_chunk call (generate.py:613-656)
 
 
 @dataclass
@@ -239,15 +241,21 @@ class Qwen3W8:
         return out
 
     def prefill(self, ids: list[int] | torch.Tensor, cache: PagedKVCache, tap=None, *, chunk: int = MAX_ROWS,
-                on_chunk=None):
-        """Chunked single-row prefill. Returns (last-position logits [1, 1, V], fused of the
-        whole prompt [1, L, n_tap*H] or None). on_chunk(fused_chunk, pos) lets a drafter
-        ingest each chunk's hidden states as it is produced."""
+                on_chunk=None, dense: bool | None = None):
+        """Single-row prefill. Returns (last-position logits [1, 1, V], fused of the whole prompt
+        [1, L, n_tap*H] or None). on_chunk(fused_chunk, pos) lets a drafter ingest the hidden
+        states chunk by chunk. A Qwen3-layout prompt of DENSE_MIN_ROWS rows or more runs layer
+        by layer over all its rows (prefill_dense); shorter ones (or dense=False) in forward
+        passes of ``chunk`` rows."""
         if not torch.is_tensor(ids):
             ids = torch.tensor(ids, dtype=torch.int32)
         ids = ids.reshape(1, -1).to(self.device, torch.int32)
         L = ids.shape[1]
         cache.check_room(L)
+        if dense is None:
+            dense = L >= DENSE_MIN_ROWS and not self.args.sandwich_norms
+        if dense:
+            return self.prefill_dense(ids, cache, tap, on_chunk=on_chunk)
         parts = []
         out = None
         pos = cache.lengths[0]
@@ -266,3 +274,59 @@ class Qwen3W8:
             fused_all = parts[0] if len(parts) == 1 else torch.cat(parts, dim=1)
         return out, fused_all
 
+
+    # ------------------------------------------------------------------ dense prefill
+    def prefill_dense(self, ids: torch.Tensor, cache: PagedKVCache, tap=None, *, on_chunk=None,
+                      chunk: int = PREFILL_CHUNK):
+        """Prefill of a long prompt, layer by layer over all L rows (the reference's chunked
+        _prefill_tapped, generate.py:613-656, computes the same causal result): each layer's W8
+        weights are expanded to bf16 once (dsk_w8_dequant_rows) and multiplied by the library
+        GEMM (hipBLASLt through torch.matmul / addmm, whose beta = 1 form is the fused residual
+        add), between the engine's RMSNorm, q/k-norm + RoPE + KV append, many-query attention and
+        SwiGLU kernels. The norms here normalise first. Returns what prefill() returns."""
+        a = self.args
+        if a.sandwich_norms:
+            raise ValueError("prefill_dense: the Qwen3 layout only")
+        ids = ids.reshape(1, -1)
+        L = ids.shape[1]
+        cache.check_room(L)
+        H, I, eps = a.hidden_size, a.intermediate_size, a.rms_norm_eps
+        nq, nkv, hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
+        dev = self.device
+        tap = list(tap or [])
+        h = self.embed_rows(ids.reshape(-1))
+        fused = torch.empty((L, len(tap) * H), dtype=torch.bfloat16, device=dev) if tap else None
+        nw = max(a.n_qkv * H, H * nq * hd, 2 * I * H, H * I)
+        wbuf = torch.empty(nw, dtype=torch.bfloat16, device=dev)
+        x = torch.empty((L, H), dtype=torch.bfloat16, device=dev)
+        qkv = torch.empty((L, a.n_qkv), dtype=torch.bfloat16, device=dev)
+        gu = torch.empty((L, 2 * I), dtype=torch.bfloat16, device=dev)
+        act = torch.empty((L, I), dtype=torch.bfloat16, device=dev)
+        for l, Lw in enumerate(self.layers):
+            ops.rows_rmsnorm(h, Lw.in_norm, eps, out=x)
+            torch.matmul(x, ops.w8_dequant(Lw.qkv, out=wbuf).t(), out=qkv)
+            k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
+            inv_freq = self.inv_freq_local if a.is_sliding(l) else self.inv_freq
+            q = ops.qkv_rope_append(qkv, 1, L, nq, nkv, hd, Lw.q_norm, Lw.k_norm, eps, inv_freq, cache.seq_lens,
+                                    cache.block_table, cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb)
+            o = ops.attention(q, 1, L, nq, nkv, hd, a.attn_scale, cache.seq_lens, cache.max_ctx, cache.block_table,
+                              cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb, causal=True, window=a.window(l))
+            h.addmm_(o, ops.w8_dequant(Lw.o, out=wbuf).t())
+            ops.rows_rmsnorm(h, Lw.post_norm, eps, out=x)
+            torch.matmul(x, ops.w8_dequant(Lw.gate_up, out=wbuf).t(), out=gu)
+            ops.rows_gated(gu, self.act_epi, out=act)
+            h.addmm_(act, ops.w8_dequant(Lw.down, out=wbuf).t())
+            for i, t in enumerate(tap):
+                if t == l:
+                    fused[:, i * H:(i + 1) * H].copy_(h)
+        pos = cache.lengths[0]
+        ops.lens_add(cache.seq_lens, None, L)
+        cache.note_lengths([pos + L])
+        x = ops.pack_rn(M=1, K=H, h=h[L - 1:L], norm_w=self.norm, eps=eps)
+        out = torch.empty((1, a.vocab_size), dtype=torch.float32, device=dev)
+        ops.w8_gemm(x, self.lm_head, out=out, softcap=a.final_logit_softcapping or 0.0)
+        if fused is not None and on_chunk is not None:
+            for c0 in range(0, L, chunk):
+                on_chunk(fused[c0:c0 + chunk].view(1, -1, len(tap) * H), pos + c0)
+            return out.view(1, 1, -1), None
+        return out.view(1, 1, -1), (fused.view(1, L, -1) if fused is not None else None)

@@ -180,6 +180,20 @@ class OracleTarget:
         self.K = [torch.zeros(0, a.num_key_value_heads, a.head_dim) for _ in self.layers]
         self.V = [torch.zeros(0, a.num_key_value_heads, a.head_dim) for _ in self.layers]
         self.offset = 0
+        # dense=True: the rounding of the engine's dense prefill (the norms normalise first and the
+        # projections multiply weights rounded to bf16, as a bf16 library GEMM over expanded
+        # weights does); the final norm and head keep the engine's normed-later form
+        self.dense = False
+        self._bf_w: dict = {}
+
+    def _w(self, l: int, name: str) -> torch.Tensor:
+        w = getattr(self.layers[l], name)
+        if not self.dense:
+            return w
+        key = (l, name)
+        if key not in self._bf_w:
+            self._bf_w[key] = bf(w)
+        return self._bf_w[key]
 
     def trim(self, n: int) -> None:
         """Roll back n tokens (metadata in the engine; a truncation here)."""
@@ -202,8 +216,8 @@ class OracleTarget:
         for l, L in enumerate(self.layers):
             win = a.window(l)
             theta = (a.rope_local_base_freq or a.rope_theta) if a.is_sliding(l) else a.rope_theta
-            if sandwich:
-                qkv = bf(bf(rmsnorm(h, L.in_norm, eps)) @ L.wq.T)
+            if sandwich or self.dense:
+                qkv = bf(bf(rmsnorm(h, L.in_norm, eps)) @ self._w(l, "wq").T)
             else:
                 xg, r = norm_later(h, L.in_norm, eps)
                 qkv = bf(r * (xg @ L.wq.T))
@@ -220,9 +234,9 @@ class OracleTarget:
             if L.attn_out_norm is not None:     # sandwich: norm the projection output, then add
                 h = bf(h + bf(rmsnorm(bf(o.reshape(W, -1) @ L.wo.T), L.attn_out_norm, eps)))
             else:
-                h = bf(h + self.rr(o.reshape(W, -1) @ L.wo.T))
-            if sandwich:
-                gu = bf(bf(rmsnorm(h, L.post_norm, eps)) @ L.wgu.T)
+                h = bf(h + self.rr(o.reshape(W, -1) @ self._w(l, "wo").T))
+            if sandwich or self.dense:
+                gu = bf(bf(rmsnorm(h, L.post_norm, eps)) @ self._w(l, "wgu").T)
             else:
                 xg, r = norm_later(h, L.post_norm, eps)
                 gu = bf(r * (xg @ L.wgu.T))
@@ -232,7 +246,7 @@ class OracleTarget:
             if L.ff_out_norm is not None:
                 h = bf(h + bf(rmsnorm(bf(act @ L.wd.T), L.ff_out_norm, eps)))
             else:
-                h = bf(h + self.rr(act @ L.wd.T))
+                h = bf(h + self.rr(act @ self._w(l, "wd").T))
             if l in tap:
                 captured.append(h)
         self.offset += W

@@ -1,0 +1,140 @@
+"""GPU: the dense prefill (src/mlx_dspark/generate.py:613-656 prefills the prompt in 2048-row
+chunks; here a long prompt runs layer by layer over all of its rows). Its kernels against closed
+forms: bf16 rows of a W8 / W4 weight bit for bit, the row RMSNorm and gated activation, and the
+many-query causal attention (W > 64: query-tile groups, long key splits, per-row split counts)
+against a float32 softmax over the stored K/V; then the whole prefill against the oracle: the
+last position's logits, the tapped hidden states, and a verify block decoded from the cache it
+filled."""
+
+import numpy as np
+import pytest
+import torch
+
+from _parity import check_logits
+from oracle import model as OM
+from oracle import w8 as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _mlx_np(q, s, b):
+    return (q.cpu().numpy(), s.view(torch.int16).cpu().numpy().view(np.uint16),
+            b.view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+@pytest.mark.parametrize("N,K,bits,paired", [(64, 256, 8, False), (256, 1024, 8, True), (96, 512, 4, False),
+                                             (128, 2048, 4, True)])
+def test_dequant_rows_bit_exact(dev, N, K, bits, paired):
+    from mlx_dspark.ops import W8Weight, w8_dequant
+    g = torch.Generator().manual_seed(N + K + bits)
+    q, s, b = W8Weight.quantize_mlx((torch.randn(N, K, generator=g) * 0.05).to(dev), bits)
+    W = W8Weight.from_mlx(q, s, b, paired, bits)
+    got = w8_dequant(W).float().cpu().numpy()
+    ref = O.bf16_round(O.dequantize(*_mlx_np(q, s, b)).astype(np.float32))
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("M,K", [(1, 64), (300, 1024), (2049, 4096)])
+def test_rows_rmsnorm(dev, M, K):
+    from mlx_dspark.ops import rows_rmsnorm
+    g = torch.Generator().manual_seed(M + K)
+    x = (torch.randn(M, K, generator=g) * 3).to(torch.bfloat16)
+    w = (1 + 0.3 * torch.randn(K, generator=g)).to(torch.bfloat16)
+    y = rows_rmsnorm(x.to(dev), w.to(dev), 1e-6).float().cpu().numpy()
+    xf = x.float().numpy().astype(np.float64)
+    ref = xf / np.sqrt((xf ** 2).mean(1, keepdims=True) + 1e-6) * w.float().numpy()
+    assert np.all(np.abs(y - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-6)
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+def test_rows_gated(dev, act):
+    from mlx_dspark.ops import DSK_EPI_GEGLU, DSK_EPI_SWIGLU, rows_gated
+    M, I = 333, 512
+    g = torch.Generator().manual_seed(5)
+    gu = (torch.randn(M, 2 * I, generator=g) * 2).to(torch.bfloat16)
+    out = rows_gated(gu.to(dev), DSK_EPI_SWIGLU if act == "silu" else DSK_EPI_GEGLU).float().cpu()
+    gt, ut = gu[:, :I].float(), gu[:, I:].float()
+    a = gt * torch.sigmoid(gt) if act == "silu" else 0.5 * gt * (1 + torch.tanh(0.7978845608028654 * (gt + 0.044715 * gt ** 3)))
+    ref = (a.to(torch.bfloat16).float() * ut).to(torch.bfloat16).float()
+    assert (out - ref).abs().max() <= 2 ** -6 * ref.abs().max()
+
+
+def _pool_rows(cache, l, n, which):
+    """[n, nkv, hd] float values the cache holds for tokens 0..n-1 of row 0 (dequantized)."""
+    page = cache.page
+    pool = cache.k[l] if which == "k" else cache.v[l]
+    sb = cache.k_sb[l] if which == "k" else cache.v_sb[l]
+    bt = cache.block_table[0].cpu().numpy()
+    rows = []
+    for j in range(n):
+        p = int(bt[j // page])
+        if sb is None:
+            rows.append(pool[p, :, j % page].float().cpu())
+        else:
+            q = pool[p, :, j % page].cpu().numpy().astype(np.float64)
+            w = sb[p, :, j % page].cpu().numpy().view(np.uint32)
+            s = O.bits_to_f32((w & 0xFFFF).astype(np.uint16)).astype(np.float64)
+            bb = O.bits_to_f32((w >> 16).astype(np.uint16)).astype(np.float64)
+            v = q.reshape(q.shape[0], -1, 64) * s[..., None] + bb[..., None]
+            rows.append(torch.from_numpy(O.bf16_round(v.reshape(q.shape).astype(np.float32))))
+    return torch.stack(rows)
+
+
+@pytest.mark.parametrize("kv_bits,L0,W", [(None, 0, 300), (8, 100, 300), (8, 500, 777), (None, 64, 129)])
+def test_many_query_attention(dev, kv_bits, L0, W):
+    """Causal attention of W > 64 new rows over the cache: float32 softmax over the stored K/V."""
+    from mlx_dspark import ops
+    from mlx_dspark.kv import PagedKVCache
+    print(f"many-query attention kv_bits={kv_bits} L0={L0} W={W}", flush=True)
+    nq, nkv, hd = 8, 2, 128
+    cache = PagedKVCache(1, 1, nkv, hd, L0 + W + 64, kv_bits=kv_bits)
+    g = torch.Generator().manual_seed(L0 + W)
+    qkv = (torch.randn(L0 + W, (nq + 2 * nkv) * hd, generator=g)).to(torch.bfloat16).to(dev)
+    inv = ops.rope_inv_freq(hd, 1e6, dev)
+    for r0, r1 in ((0, L0), (L0, L0 + W)):
+        if r1 > r0:
+            q = ops.qkv_rope_append(qkv[r0:r1].contiguous(), 1, r1 - r0, nq, nkv, hd, None, None, 1e-6, inv,
+                                    cache.seq_lens, cache.block_table, cache.page, cache.kv_dtype, *cache.layer_args(0))
+            if r0 == L0:
+                out = ops.attention(q, 1, W, nq, nkv, hd, hd ** -0.5, cache.seq_lens, cache.max_ctx,
+                                    cache.block_table, cache.page, cache.kv_dtype, *cache.layer_args(0))
+            ops.lens_add(cache.seq_lens, None, r1 - r0)
+    torch.cuda.synchronize()
+    K, V = _pool_rows(cache, 0, L0 + W, "k"), _pool_rows(cache, 0, L0 + W, "v")
+    qf = q.float().cpu().view(W, nq, hd)
+    ref = OM.sdpa(qf, K, V, hd ** -0.5, OM.causal_mask(L0, W))
+    got = out.float().cpu().view(W, nq, hd)
+    err = (got - ref).abs().max() / ref.abs().max()
+    assert err < 2e-2, err
+
+
+def test_dense_prefill_matches_oracle(dev):
+    from mlx_dspark import synthetic
+    print("dense prefill vs oracle: tiny model, 700-token prompt, taps 1 and 3, then a 9-row verify", flush=True)
+    model = synthetic.build_target("tiny", seed=21, keep_mlx=True)
+    synthetic.randomize_norms(model, seed=22)
+    V = model.args.vocab_size
+    prompt = np.random.default_rng(3).integers(0, V, 700).tolist()
+    block = np.random.default_rng(4).integers(0, V, 9).tolist()
+    cache = model.make_cache(max_ctx=800)
+    logits, fused = model.prefill(prompt, cache, [1, 3])
+    assert cache.lengths[0] == 700 and int(cache.seq_lens[0]) == 700
+    vl, _ = model.forward(torch.tensor([block], dtype=torch.int32, device=dev), cache, None)
+    torch.cuda.synchronize()
+    refs = {pb: OM.OracleTarget(model, p_bf16=pb) for pb in (True, False)}
+    for r in refs.values():
+        r.dense = True                   # the prompt with the dense prefill's rounding
+    outs = {pb: r.forward(prompt, tap=(1, 3)) for pb, r in refs.items()}
+    for r in refs.values():
+        r.dense = False
+    check_logits(logits[0, -1].float().cpu(), outs[True][0][-1], outs[False][0][-1], "dense prefill, last position")
+    tap_err = float((fused[0].float().cpu() - outs[True][1]).abs().max() / outs[True][1].abs().max())
+    assert tap_err < 2e-2, tap_err
+    vouts = {pb: r.forward(block)[0] for pb, r in refs.items()}
+    check_logits(vl[0].float().cpu(), vouts[True], vouts[False], "verify rows over the dense-prefilled cache")
+    # the chunked forward passes (the verify's rounding) fill an equivalent cache
+    c2 = model.make_cache(max_ctx=800)
+    l2, _ = model.prefill(prompt, c2, None, dense=False)
+    torch.cuda.synchronize()
+    chunked = {pb: OM.OracleTarget(model, p_bf16=pb).forward(prompt)[0][-1] for pb in (True, False)}
+    check_logits(l2[0, -1].float().cpu(), chunked[True], chunked[False], "chunked prefill, last position")
