@@ -874,6 +874,330 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
     a.out[attn_out_index(a, HD, b, i, kvh * a.G + hl, lane * PER + e)] = f32_to_bf16(acc[e] * inv);
 }
 
+// ----------------------------------------------------------------------------- verify (head_dim 128)
+// A verify pass (at most 64 query rows per kv head, head_dim 128, keys already in the pool): one
+// workgroup of 8 waves per (row b, kv head, split of 256 keys). Wave w owns the split's 32-key
+// block w: it loads the block's K/V rows straight from the pool into registers, dequantises each
+// element once (K row-major for the score MFMA, V transposed for the P.V MFMA), then runs the kv
+// head's query tiles (staged once in LDS) over its 32 keys, two tiles at a time. Per tile pair the
+// eight waves' (m, l, o) meet in LDS and wave w merges d tile w of both tiles into the split's
+// partial (or the output when there is one split).
+//  - head_dim order: lane group a = lane / 16 holds dims [32 a, 32 a + 32) of its key row (one
+//    contiguous 32-byte (8-bit) or 64-byte (bf16) load, inside one quantization group), so k-step
+//    s of the score MFMA takes dims 32 a + 8 s .. + 7 from both K (A operand: lane = key) and Q
+//    (B operand: lane = query): S^T[key][q] summed over a permutation of head_dim.
+//  - V is transposed in registers: v_mfma_f32_16x16x16_bf16 of a 16-key x 16-dim tile (lane =
+//    key, dims 32 a + 4 dt .. + 3) with the identity gives lane (a, c) the keys 4 a .. 4 a + 3 at
+//    physical dim 32 (c / 4) + 4 dt + c % 4 (exact: bf16 in, f32 out). Two key tiles give the 8
+//    keys {4 a + r, 16 + 4 a + r} the lane also holds scores for, so P^T goes from the score
+//    registers straight into the P.V MFMA.
+//  - O^T[dim index][q]: lane (a, q) ends with physical dims 32 a + 4 dt + r.
+// Masks, the softmax (probabilities rounded to bf16) and the partial layout are the attention
+// kernel's, so attention_combine_kernel merges the splits.
+constexpr int kVerifyBlock = 32;   // keys per page-aligned block (the page size is a multiple)
+constexpr int kVerifyWaves = 4;
+constexpr int kVerifyKeys = 256;   // keys per split: 64 per wave
+constexpr int kVerifyMaxR = 64;    // query rows per kv head
+
+template <int KVT>
+__device__ __forceinline__ void verify_load_rows(const void* pool, const uint32_t* sbp, int64_t tok, int grp,
+                                                 u32x4 (&c)[2], u32x4 (&c2)[2], uint32_t& sb) {
+  if (KVT == DSK_KV_BF16) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(pool) + tok * 128 + grp * 32);
+    c[0] = p[0];
+    c[1] = p[1];
+    c2[0] = p[2];
+    c2[1] = p[3];
+  } else {
+    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(pool) + tok * 128 + grp * 32);
+    c[0] = p[0];
+    c[1] = p[1];
+    sb = sbp[tok * 2 + (grp >> 1)];
+  }
+}
+
+// 8 values of a lane's 32-dim row slice, elements e0 .. e0 + 7 (dequantised for 8-bit KV)
+template <int KVT>
+__device__ __forceinline__ bf16x8 verify_elems8(const u32x4 (&c)[2], const u32x4 (&c2)[2], uint32_t sb, int e0) {
+  if (KVT == DSK_KV_BF16) {
+    const int w = e0 / 8;
+    return __builtin_bit_cast(bf16x8, w < 2 ? c[w] : c2[w - 2]);
+  } else {
+    const float s = bf16_to_f32((uint16_t)(sb & 0xffffu)), b = bf16_to_f32((uint16_t)(sb >> 16));
+    const u32x4 v = c[e0 / 16];
+    const uint32_t w0 = v[(e0 % 16) / 4], w1 = v[(e0 % 16) / 4 + 1];
+    uint32_t o[4];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t w = h ? w1 : w0;
+      o[2 * h] = pack_bf16x2(fmaf(s, (float)(w & 0xffu), b), fmaf(s, (float)((w >> 8) & 0xffu), b));
+      o[2 * h + 1] = pack_bf16x2(fmaf(s, (float)((w >> 16) & 0xffu), b), fmaf(s, (float)(w >> 24), b));
+    }
+    return __builtin_bit_cast(bf16x8, (u32x4{o[0], o[1], o[2], o[3]}));
+  }
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+
+template <int KVT, bool SOFTCAP, int QT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attention_verify_kernel(AttnArgs a) {
+  constexpr int HD = 128, QROW = HD + 8;
+  constexpr int NW = kVerifyWaves, KB = kVerifyKeys / NW / 16;  // waves, 16-key tiles per wave
+  __shared__ f32x4 mo[QT][NW][8][64];                // every tile's (o) per [tile][wave][d tile][lane]
+  __shared__ float2 mml[QT][NW][64];                 // and (m, l) per lane
+  __shared__ __attribute__((aligned(16))) uint16_t qs[QT * 16 * QROW];  // the kv head's query rows
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int grp = lane >> 4, row16 = lane & 15;
+  const int split = blockIdx.x % a.nsplit;
+  const int bk = blockIdx.x / a.nsplit;
+  const int b = bk / a.nkv, kvh = bk % a.nkv;
+  const int jmax = a.max_pages * a.page;
+  const int j_beg = split * kVerifyKeys;
+  const int j0 = j_beg + 16 * KB * wv;  // the wave's first key
+  // independent loads first: the wave's page ids (in the block table for any key) and the row length
+  int pg[KB / 2];
+#pragma unroll
+  for (int i = 0; i < KB / 2; ++i)
+    pg[i] = a.block_table[(int64_t)b * a.max_pages + min(j0 + 32 * i, jmax - 1) / a.page];
+  const int off = a.seq_lens[b];
+  const int j_lim = min(off + a.W, jmax);
+  if (j_beg >= j_lim) return;  // the whole workgroup: past every row's keys (the combine skips it)
+  const int j_end = min(j_lim, j_beg + kVerifyKeys);
+  const int ntiles = (a.R + 15) >> 4;
+  const bool live = j0 < j_end;  // the wave has keys (uniform)
+
+  // ---- loads: the wave's K/V rows (16-key tiles t: keys j0 + 16 t + row16), then the query rows
+  u32x4 kc[KB][2], kc2[KB][2], vc[KB][2], vc2[KB][2];
+  uint32_t ksb[KB], vsb[KB];
+  if (live) {
+#pragma unroll
+    for (int t = 0; t < KB; ++t) {
+      const int j = j0 + 16 * t;
+      const int64_t tok = ((int64_t)pg[t / 2] * a.nkv + kvh) * a.page + (j % a.page) + row16;
+      verify_load_rows<KVT>(a.k_pool, a.k_sb, tok, grp, kc[t], kc2[t], ksb[t]);
+      verify_load_rows<KVT>(a.v_pool, a.v_sb, tok, grp, vc[t], vc2[t], vsb[t]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < QT * 16 * 16 / 256; ++u) {
+    const int c = threadIdx.x + 256 * u;  // rows x 16 chunks of 8 dims
+    const int r = c >> 4, ch = c & 15;
+    u32x4 qv = u32x4{0, 0, 0, 0};
+    if (r < a.R)
+      qv = *reinterpret_cast<const u32x4*>(a.q + ((int64_t)(b * a.W + r / a.G) * a.nq + kvh * a.G + r % a.G) * HD +
+                                           ch * 8);
+    *reinterpret_cast<u32x4*>(qs + r * QROW + ch * 8) = qv;
+  }
+
+  // ---- K dequantised once (the A operand of every score MFMA), V transposed once
+  bf16x8 kel[KB][4], vt[KB / 2][8];
+  if (live) {
+#pragma unroll
+    for (int t = 0; t < KB; ++t)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kel[t][s] = verify_elems8<KVT>(kc[t], kc2[t], ksb[t], 8 * s);
+    // identity B operand of the transpose MFMA: B[k][n] = (k == n), lane holds k = 4 grp + e, n = row16
+    s16x4 ident;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ident[e] = (4 * grp + e == row16) ? (short)0x3f80 : (short)0;
+#pragma unroll
+    for (int cp = 0; cp < KB / 2; ++cp) {
+#pragma unroll
+      for (int dp = 0; dp < 4; ++dp) {
+        s16x8 v8[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int t = 2 * cp + u;
+          // whole-vector bit casts (a bit cast of one element of a bf16 vector reads element 0);
+          // keys past the split's end are zeroed (masked, but finite)
+          v8[u] = __builtin_bit_cast(s16x8, verify_elems8<KVT>(vc[t], vc2[t], vsb[t], 8 * dp));
+          if (j0 + 16 * t + row16 >= j_end) v8[u] = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          uint32_t w[4];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const s16x4 v4 = h ? __builtin_shufflevector(v8[u], v8[u], 4, 5, 6, 7)
+                               : __builtin_shufflevector(v8[u], v8[u], 0, 1, 2, 3);
+            const f32x4 tr = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v4, ident, f32x4{0, 0, 0, 0}, 0, 0, 0);
+            w[2 * u] = pack_bf16x2(tr[0], tr[1]);
+            w[2 * u + 1] = pack_bf16x2(tr[2], tr[3]);
+          }
+          vt[cp][2 * dp + h] = __builtin_bit_cast(bf16x8, (u32x4{w[0], w[1], w[2], w[3]}));
+        }
+      }
+    }
+  }
+  // exp(scale * s - m) as exp2 of one fma: c = scale * log2(e) (softcap: the capped score, c = log2(e))
+  const float softcap = a.softcap;
+  const float c2 = (SOFTCAP ? 1.0f : a.scale) * 1.4426950408889634f;
+  const float mscale = SOFTCAP ? 1.0f : a.scale;  // the stored max is in natural-log units of scale * s
+  // a block needs masks when a key may be past the split's end or past some row's position (the
+  // rows of a kv head sit at off .. off + W - 1), or with a sliding window
+  const bool masked = j0 + 16 * KB > j_end || (a.causal && (j0 + 16 * KB - 1 > off || a.window > 0));
+  __syncthreads();  // the query rows
+
+  // ---- every query tile over the wave's keys, the tiles interleaved: scores, softmax, P.V; then
+  // (m, l, o) to the merge slots (the host launches QT = the kv head's tile count)
+  float m[QT], l[QT];
+  f32x4 o[QT][8];
+#pragma unroll
+  for (int tile = 0; tile < QT; ++tile) {
+    m[tile] = -__builtin_inff();
+    l[tile] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) o[tile][d] = f32x4{0, 0, 0, 0};
+  }
+  if (live) {
+    f32x4 st[QT][KB];
+#pragma unroll
+    for (int tile = 0; tile < QT; ++tile)
+#pragma unroll
+      for (int t = 0; t < KB; ++t) st[tile][t] = f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      bf16x8 qf[QT];
+#pragma unroll
+      for (int tile = 0; tile < QT; ++tile)
+        qf[tile] = *reinterpret_cast<const bf16x8*>(qs + (tile * 16 + row16) * QROW + grp * 32 + 8 * s);
+#pragma unroll
+      for (int t = 0; t < KB; ++t)
+#pragma unroll
+        for (int tile = 0; tile < QT; ++tile)
+          st[tile][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kel[t][s], qf[tile], st[tile][t], 0, 0, 0);
+    }
+    // ---- softmax (lane: query row16, keys j0 + 16 t + 4 grp + rr); rows past R are not masked
+    // (their columns of the MFMAs touch no other row, and are not stored)
+    if (SOFTCAP) {
+#pragma unroll
+      for (int tile = 0; tile < QT; ++tile)
+#pragma unroll
+        for (int t = 0; t < KB; ++t)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) st[tile][t][rr] = tanhf(st[tile][t][rr] * a.scale / softcap) * softcap;
+    }
+    if (masked) {
+#pragma unroll
+      for (int tile = 0; tile < QT; ++tile) {
+        const int rq = tile * 16 + row16;
+        const int qpos = off + (rq < a.R ? rq : 0) / a.G;
+        int k_first = 0, k_last = j_end - 1;
+        if (a.causal) {
+          k_last = min(k_last, qpos);
+          if (a.window > 0) k_first = qpos - a.window + 1;
+        }
+#pragma unroll
+        for (int t = 0; t < KB; ++t)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const int j = j0 + 16 * t + 4 * grp + rr;
+            if (j < k_first || j > k_last) st[tile][t][rr] = -__builtin_inff();
+          }
+      }
+    }
+    float mx[QT];
+#pragma unroll
+    for (int tile = 0; tile < QT; ++tile) {
+      mx[tile] = -__builtin_inff();
+#pragma unroll
+      for (int t = 0; t < KB; ++t)
+        mx[tile] = fmaxf(mx[tile], fmaxf(fmaxf(st[tile][t][0], st[tile][t][1]), fmaxf(st[tile][t][2], st[tile][t][3])));
+    }
+#pragma unroll
+    for (int tile = 0; tile < QT; ++tile) mx[tile] = fmaxf(mx[tile], __shfl_xor(mx[tile], 16, 64));
+#pragma unroll
+    for (int tile = 0; tile < QT; ++tile) mx[tile] = fmaxf(mx[tile], __shfl_xor(mx[tile], 32, 64));
+    bf16x8 pb[QT][KB / 2];
+#pragma unroll
+    for (int tile = 0; tile < QT; ++tile) {
+      // masked keys: exp2(-inf) = 0; a row with no visible key keeps m = -inf, l = 0
+      const float mb = mx[tile] == -__builtin_inff() ? 0.0f : mx[tile] * c2;
+#pragma unroll
+      for (int cp = 0; cp < KB / 2; ++cp) {
+        uint32_t w[4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const f32x4& sv = st[tile][2 * cp + u];
+            w[2 * u + h] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(sv[2 * h], c2, -mb)),
+                                       __builtin_amdgcn_exp2f(fmaf(sv[2 * h + 1], c2, -mb)));
+            l[tile] += __uint_as_float(w[2 * u + h] << 16) + __uint_as_float(w[2 * u + h] & 0xffff0000u);
+          }
+        pb[tile][cp] = __builtin_bit_cast(bf16x8, (u32x4{w[0], w[1], w[2], w[3]}));
+      }
+      m[tile] = mx[tile] * mscale;
+    }
+#pragma unroll
+    for (int tile = 0; tile < QT; ++tile) l[tile] += __shfl_xor(l[tile], 16, 64);
+#pragma unroll
+    for (int tile = 0; tile < QT; ++tile) l[tile] += __shfl_xor(l[tile], 32, 64);
+    // ---- O^T = V^T . P^T over the wave's keys (32 per MFMA)
+#pragma unroll
+    for (int cp = 0; cp < KB / 2; ++cp)
+#pragma unroll
+      for (int d = 0; d < 8; ++d)
+#pragma unroll
+        for (int tile = 0; tile < QT; ++tile)
+          o[tile][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[cp][d], pb[tile][cp], o[tile][d], 0, 0, 0);
+  }
+#pragma unroll
+  for (int tile = 0; tile < QT; ++tile) {
+#pragma unroll
+    for (int d = 0; d < 8; ++d) mo[tile][wv][d][lane] = o[tile][d];
+    mml[tile][wv][lane] = float2{m[tile], l[tile]};
+  }
+  __syncthreads();
+  // ---- merge of the waves: wave w takes tiles w, w + NW, ... (lane: 32 dims of its row)
+  for (int tile = wv; tile < ntiles; tile += NW) {
+    const int rq = tile * 16 + row16;
+    if (rq >= a.R) continue;
+    float2 ml[NW];
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+      ml[q] = mml[tile][q][lane];
+      M = fmaxf(M, ml[q].x);
+    }
+    float L = 0.0f, wq[NW];
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+      wq[q] = ml[q].x == -__builtin_inff() ? 0.0f : __expf(ml[q].x - M);
+      L += ml[q].y * wq[q];
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    uint32_t w[16];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      f32x4 acc = f32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int q = 0; q < NW; ++q) acc += mo[tile][q][d][lane] * wq[q];
+      w[2 * d] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+      w[2 * d + 1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+    }
+    // dims 32 grp .. + 31 in two runs of 16 (contiguous in both output layouts)
+    u32x4* dst[2];
+    if (a.nsplit == 1) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        dst[h] = reinterpret_cast<u32x4*>(a.out + attn_out_index(a, HD, b, rq / a.G, kvh * a.G + rq % a.G,
+                                                                  grp * 32 + 16 * h));
+    } else {
+      const size_t prow = ((size_t)bk * a.nsplit + split) * a.R + rq;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) dst[h] = reinterpret_cast<u32x4*>(a.part_o + prow * HD + grp * 32 + 16 * h);
+      if (grp == 0) *reinterpret_cast<float2*>(a.part_ml + prow * 2) = float2{M, L};
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      dst[h][0] = u32x4{w[8 * h], w[8 * h + 1], w[8 * h + 2], w[8 * h + 3]};
+      dst[h][1] = u32x4{w[8 * h + 4], w[8 * h + 5], w[8 * h + 6], w[8 * h + 7]};
+    }
+  }
+}
+
 // ----------------------------------------------------------------------------- host helpers
 template <int HD, int QT, bool FUSED>
 static void launch_attention(const AttnArgs& a, int kv_dtype, bool softcap, dim3 grid, hipStream_t st) {
@@ -949,8 +1273,40 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
   a.part_ml = a.nsplit > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
                                                        attn_part_o_bytes(a.B, a.W, a.nq, hd, a.nsplit))
                            : nullptr;
-  dim3 grid((unsigned)(a.B * a.nkv * a.nsplit), (unsigned)tile_groups);
   const bool sc = softcap > 0.0f;
+  if (hd == 128 && !fused && a.R <= kVerifyMaxR && a.page % kVerifyBlock == 0) {
+    // verify passes: 4 waves per split of 256 keys, 64 keys each, every query tile
+    a.kps = kVerifyKeys;
+    a.nsplit = (int)ceil_div(max_ctx, a.kps);
+    const size_t need_v = attn_ws_need(a.B, a.W, a.nq, hd, a.nsplit);
+    DSK_REQUIRE(a.nsplit == 1 || (workspace && ws_bytes >= need_v), "%s: workspace %zu < %zu", who, ws_bytes, need_v);
+    a.part_o = reinterpret_cast<uint16_t*>(workspace);
+    a.part_ml = a.nsplit > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
+                                                        attn_part_o_bytes(a.B, a.W, a.nq, hd, a.nsplit))
+                             : nullptr;
+    const dim3 vgrid((unsigned)(a.B * a.nkv * a.nsplit));
+#define DSK_VERIFY_QT(kvt, scv)                                                                           \
+  switch (tiles) {                                                                                        \
+    case 1: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 1>), vgrid, dim3(256), 0, st, a); break; \
+    case 2: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 2>), vgrid, dim3(256), 0, st, a); break; \
+    case 3: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 3>), vgrid, dim3(256), 0, st, a); break; \
+    default: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 4>), vgrid, dim3(256), 0, st, a); break; \
+  }
+    if (a.kv_dtype == DSK_KV_U8) {
+      if (sc) { DSK_VERIFY_QT(DSK_KV_U8, true) } else { DSK_VERIFY_QT(DSK_KV_U8, false) }
+    } else {
+      if (sc) { DSK_VERIFY_QT(DSK_KV_BF16, true) } else { DSK_VERIFY_QT(DSK_KV_BF16, false) }
+    }
+#undef DSK_VERIFY_QT
+    DSK_LAUNCH_CHECK(who);
+    if (a.nsplit > 1) {
+      const dim3 cgrid((unsigned)ceil_div((int64_t)a.B * a.nkv * a.R, 4));
+      hipLaunchKernelGGL(attention_combine_kernel<128>, cgrid, dim3(256), 0, st, a);
+      DSK_LAUNCH_CHECK(who);
+    }
+    return DSK_OK;
+  }
+  dim3 grid((unsigned)(a.B * a.nkv * a.nsplit), (unsigned)tile_groups);
 #define DSK_ATTN_CASE(hdv, qt)                                      \
   if (hd == hdv && QT == qt) {                                      \
     if (fused) launch_attention<hdv, qt, true>(a, a.kv_dtype, sc, grid, st); \
@@ -1060,7 +1416,8 @@ extern "C" size_t dsk_attn_ws_bytes(int B, int W, int nq, int hd, int max_ctx) {
   if (hd != 128 && hd != 256 && hd != 512) return 0;
   if (W > kAttnVerifyMaxW)  // many-query passes: splits of 8 blocks
     return attn_ws_need(B, W, nq, hd, (int)ceil_div(max_ctx, attn_split_keys(hd, max_ctx) * 8));
-  return attn_ws_need(B, W, nq, hd, attn_nsplit(hd, max_ctx) + 1);  // + the fused new-token split
+  // + the fused new-token split (also covers the verify kernel's splits of 128 keys and more)
+  return attn_ws_need(B, W, nq, hd, attn_nsplit(hd, max_ctx) + 1);
 }
 
 extern "C" int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, int hd, float scale, int causal,

@@ -59,6 +59,13 @@ __host__ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 #endif
 }
 
+// two values in one v_cvt_pk_bf16_f32 (lo in bits 0..15): the same rounding as f32_to_bf16
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
+}
+
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
 __host__ __device__ __forceinline__ uint32_t f32_bits(float f) {
