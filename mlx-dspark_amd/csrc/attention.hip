@@ -962,7 +962,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     pg[i] = a.block_table[(int64_t)b * a.max_pages + min(j0 + 32 * i, jmax - 1) / a.page];
   const int off = a.seq_lens[b];
   const int j_lim = min(off + a.W, jmax);
-  if (j_beg >= j_lim) return;  // the whole workgroup: past every row's keys (the combine skips it)
+  if (j_beg >= j_lim) {
+    // past every row's keys: an empty partial (m = -inf) for the combine, which reads every split
+    if (a.nsplit > 1)
+      for (int r = threadIdx.x; r < a.R; r += 256)
+        *reinterpret_cast<float2*>(a.part_ml + (((size_t)bk * a.nsplit + split) * a.R + r) * 2) =
+            float2{-__builtin_inff(), 0.0f};
+    return;
+  }
   const int j_end = min(j_lim, j_beg + kVerifyKeys);
   const int ntiles = (a.R + 15) >> 4;
   const bool live = j0 < j_end;  // the wave has keys (uniform)
@@ -1198,6 +1205,63 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
 }
 
+// The verify kernel's splits merged: one thread per (row b, kv head, query row, 8 dims), every
+// split read (a split past the row length holds m = -inf and is skipped by value), the loads of
+// a batch of 24 splits issued together. Same merge as attention_combine_kernel: weights
+// exp(m_s - M) * l_s over the splits' normalised bf16 partial outputs.
+constexpr int kVerifyCombineThreads = 64;
+__global__ __launch_bounds__(kVerifyCombineThreads) void attention_verify_combine_kernel(AttnArgs a) {
+  constexpr int HD = 128, BATCH = 24;
+  const int64_t task = (int64_t)blockIdx.x * kVerifyCombineThreads + threadIdx.x;
+  if (task >= (int64_t)a.B * a.nkv * a.R * (HD / 8)) return;
+  const int ch = (int)(task & 15);
+  const int64_t rowt = task >> 4;
+  const int r = (int)(rowt % a.R);
+  const int bk = (int)(rowt / a.R);
+  const int b = bk / a.nkv, kvh = bk % a.nkv;
+  const size_t base = (size_t)bk * a.nsplit * a.R + r;  // partial row of split 0
+  float M = -__builtin_inff(), L = 0.0f, acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  for (int s0 = 0; s0 < a.nsplit; s0 += BATCH) {
+    float2 ml[BATCH];
+    u32x4 ov[BATCH];
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int sp = min(s0 + u, a.nsplit - 1);
+      const size_t prow = base + (size_t)sp * a.R;
+      ml[u] = *reinterpret_cast<const float2*>(a.part_ml + prow * 2);
+      ov[u] = *reinterpret_cast<const u32x4*>(a.part_o + prow * HD + ch * 8);
+      if (s0 + u >= a.nsplit) ml[u].x = -__builtin_inff();
+    }
+    float Mn = M;
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) Mn = fmaxf(Mn, ml[u].x);
+    if (Mn == -__builtin_inff()) continue;
+    const float rescale = M == -__builtin_inff() ? 0.0f : __expf(M - Mn);
+    L *= rescale;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] *= rescale;
+    M = Mn;
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      if (ml[u].x == -__builtin_inff()) continue;  // also skips a never-written partial output
+      const float wl = __expf(ml[u].x - M) * ml[u].y;
+      L += wl;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t x = ov[u][q];
+        acc[2 * q] += wl * __uint_as_float(x << 16);
+        acc[2 * q + 1] += wl * __uint_as_float(x & 0xffff0000u);
+      }
+    }
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  *reinterpret_cast<u32x4*>(a.out + attn_out_index(a, HD, b, r / a.G, kvh * a.G + r % a.G, ch * 8)) =
+      u32x4{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),
+            pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv)};
+}
+
 // ----------------------------------------------------------------------------- host helpers
 template <int HD, int QT, bool FUSED>
 static void launch_attention(const AttnArgs& a, int kv_dtype, bool softcap, dim3 grid, hipStream_t st) {
@@ -1300,8 +1364,8 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
 #undef DSK_VERIFY_QT
     DSK_LAUNCH_CHECK(who);
     if (a.nsplit > 1) {
-      const dim3 cgrid((unsigned)ceil_div((int64_t)a.B * a.nkv * a.R, 4));
-      hipLaunchKernelGGL(attention_combine_kernel<128>, cgrid, dim3(256), 0, st, a);
+      const dim3 cgrid((unsigned)ceil_div((int64_t)a.B * a.nkv * a.R * 16, kVerifyCombineThreads));
+      hipLaunchKernelGGL(attention_verify_combine_kernel, cgrid, dim3(kVerifyCombineThreads), 0, st, a);
       DSK_LAUNCH_CHECK(who);
     }
     return DSK_OK;
