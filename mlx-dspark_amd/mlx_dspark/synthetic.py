@@ -261,10 +261,13 @@ def build_dspark(target_args: TargetArgs, seed: int = 2, device="cuda", keep_mlx
 
 def build_dflash(target_args: TargetArgs, seed: int = 1, device="cuda", keep_mlx: bool = False,
                  num_hidden_layers: int = 2, block_size: int = 16, n_taps: int = 5,
-                 mask_token_id: int | None = None, bits: int = 4):
+                 mask_token_id: int | None = None, bits: int = 4, layer_types: tuple | None = None,
+                 sliding_window: int | None = None):
     """A DFlash drafter shaped like the target (same width, heads and MLP), conditioned on
     n_taps evenly spaced target layers, with a block of block_size positions; its linear
-    layers quantized to ``bits`` (4, the reference's default, or 8)."""
+    layers quantized to ``bits`` (4, the reference's default, or 8). ``layer_types`` /
+    ``sliding_window``: per-layer "sliding_attention" / "full_attention" as in the reference's
+    config (src/mlx_dspark/dflash_model.py:90-92); default all full."""
     from .dflash_model import DFlashConfig, DFlashDraftModel
 
     a = target_args
@@ -277,7 +280,8 @@ def build_dflash(target_args: TargetArgs, seed: int = 1, device="cuda", keep_mlx
         max_position_embeddings=a.max_position_embeddings, block_size=block_size,
         target_layer_ids=tuple(evenly_spaced_layers(a.num_hidden_layers, n_taps)),
         num_target_layers=a.num_hidden_layers,
-        mask_token_id=a.vocab_size - 1 if mask_token_id is None else mask_token_id)
+        mask_token_id=a.vocab_size - 1 if mask_token_id is None else mask_token_id,
+        layer_types=tuple(layer_types or ()), sliding_window=sliding_window)
     H, I = a.hidden_size, a.intermediate_size
     nq, nkv, hd = a.num_attention_heads, a.num_key_value_heads, a.head_dim
     layers = []

@@ -99,6 +99,39 @@ def test_dflash_drafter_matches_oracle(dev, tiny):
     check_logits(got2[0], want2, oa(block, more.float().cpu(), logits_start=1), "dflash round 2")
 
 
+def test_dflash_sliding_window_drafter_matches_oracle(dev, tiny):
+    """DFlash sliding-window layers (src/mlx_dspark/dflash_model.py:103-109, :128-132, :186-195):
+    layer 0 slides with a 6-position window (block queries see keys P - 5 .. P, the block causal
+    inside it), layer 1 attends to everything. Two rounds against the oracle; an oracle whose
+    window is longer differs from the GPU by more than the bound (the window is live)."""
+    import dataclasses
+    from mlx_dspark import synthetic
+    print("dflash sliding window 6", flush=True)
+    d, cfg = synthetic.build_dflash(tiny.args, seed=11, keep_mlx=True, num_hidden_layers=2, block_size=8, n_taps=2,
+                                    layer_types=("sliding_attention", "full_attention"), sliding_window=6)
+    d.bind(tiny)
+    rng = np.random.default_rng(3)
+    prompt = rng.integers(0, tiny.args.vocab_size, 40).tolist()
+    cache = tiny.make_cache(max_ctx=256)
+    _, fused = tiny.prefill(prompt, cache, list(cfg.target_layer_ids))
+    dcache = d.make_cache(max_ctx=256)
+    block = [int(prompt[-1])] + [cfg.mask_token_id] * (cfg.block_size - 1)
+    ref_t = OM.OracleTarget(tiny)
+    od, oa = OM.OracleDFlash(d, ref_t, p_bf16=True), OM.OracleDFlash(d, ref_t)
+    wide = OM.OracleDFlash(d, ref_t, p_bf16=True)
+    wide.c = dataclasses.replace(wide.c, sliding_window=12)
+    ctx = fused[0].float().cpu()
+    got = d(block, fused[0], dcache, logits_start=1)
+    bound = check_logits(got[0], od(block, ctx, logits_start=1), oa(block, ctx, logits_start=1), "sliding round 1")
+    mx, _ = OM.logit_diff(got[0], wide(block, ctx, logits_start=1))
+    print(f"oracle with a 12-position window: normalised max-abs {mx:.4f}", flush=True)
+    assert mx > bound
+    more = fused[0, :3]
+    got2 = d(block, more, dcache, logits_start=1)
+    check_logits(got2[0], od(block, more.float().cpu(), logits_start=1),
+                 oa(block, more.float().cpu(), logits_start=1), "sliding round 2")
+
+
 @pytest.mark.parametrize("use_graph", [False, True])
 def test_dflash_generate_reproduces_greedy_stream(dev, tiny, use_graph):
     from mlx_dspark import synthetic
