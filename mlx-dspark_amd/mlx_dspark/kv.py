@@ -132,6 +132,15 @@ class PagedKVCache(list):
         absolute position)."""
         self.set_lengths([min(int(length), l) for l in self.lengths])
 
+    def trim_rows(self, amounts) -> None:
+        """Roll row b back by amounts[b] positions, clamped at zero (the batch cache's per-row
+        trim, src/mlx_dspark/batch_engine.py:159-167): metadata only, so a row's next write lands
+        at its new length and overwrites what was there."""
+        amounts = [int(n) for n in amounts]
+        if len(amounts) != self.B or min(amounts) < 0:
+            raise ValueError(f"trim_rows needs {self.B} non-negative amounts, got {amounts}")
+        self.set_lengths([max(0, l - n) for l, n in zip(self.lengths, amounts)])
+
     def check_room(self, W: int) -> None:
         if max(self.lengths) + W > self.max_ctx:
             raise ValueError(f"KV cache full: {max(self.lengths)} + {W} > {self.max_ctx} tokens")
