@@ -396,7 +396,9 @@ int dsk_lens_add(int32_t* lens, const int32_t* n, int B, int add, dsk_stream_t s
  *   prev = first_prev[b]; for i < cap:
  *     l_i[v] = bf16(bf16(base[b][i][v]) + bf16(sum_r deq(w2)[v][r] * bf16(deq(w1)[prev][r])))
  *     greedy (temperature == 0): tok[b][i] = argmax_v l_i (lowest index on ties)
- *     sampled: tok[b][i] ~ truncate(softmax(l_i * (1/T))) (dsk_sample_rows, Philox row b*cap + i),
+ *     sampled: tok[b][i] ~ truncate(softmax(l_i * (1/T))) (dsk_sample_rows, Philox row
+ *              (row0 + b)*cap + i: a batch of more than 16 rows called in pieces of 16 with row0
+ *              = the piece's first row draws what one call over all rows would),
  *              q_logits_out[b][i] = l_i (the draft distribution's logits, for dsk_accept_sample
  *              with q_mul_inv_t = 1)
  *     prev = tok[b][i]
@@ -408,7 +410,7 @@ int dsk_markov_block(const float* base, int64_t ldb, int B, int cap, int64_t V, 
                      const int32_t* first_prev, const uint8_t* w1q, const uint16_t* w1s,
                      const uint16_t* w1b, const uint8_t* w2t, const uint32_t* w2sb,
                      float temperature, float top_p, int top_k, uint64_t seed, uint32_t offset,
-                     int32_t* tok_out, float* q_logits_out, void* workspace, size_t ws_bytes,
+                     int row0, int32_t* tok_out, float* q_logits_out, void* workspace, size_t ws_bytes,
                      dsk_stream_t stream);
 
 /* Presence / frequency penalties on verify logits: logits[r][ids[j]] -= vals[j] for

@@ -260,12 +260,13 @@ extern "C" size_t dsk_markov_ws_bytes(int B, int64_t V, int sampled) {
 extern "C" int dsk_markov_block(const float* base, int64_t ldb, int B, int cap, int64_t V, int R,
                                 const int32_t* first_prev, const uint8_t* w1q, const uint16_t* w1s,
                                 const uint16_t* w1b, const uint8_t* w2t, const uint32_t* w2sb, float temperature,
-                                float top_p, int top_k, uint64_t seed, uint32_t offset, int32_t* tok_out,
+                                float top_p, int top_k, uint64_t seed, uint32_t offset, int row0, int32_t* tok_out,
                                 float* q_logits_out, void* workspace, size_t ws_bytes, dsk_stream_t stream) {
   DSK_REQUIRE(base && first_prev && w1q && w1s && w1b && w2t && w2sb && tok_out && workspace,
               "dsk_markov_block: null pointer");
   DSK_REQUIRE(R == kMarkovR, "dsk_markov_block: markov rank %d not supported (%d)", R, kMarkovR);
   DSK_REQUIRE(B > 0 && B <= kMarkovMaxB && cap > 0 && cap <= 64, "dsk_markov_block: B=%d cap=%d", B, cap);
+  DSK_REQUIRE(row0 >= 0, "dsk_markov_block: row0=%d", row0);
   DSK_REQUIRE(V > 0 && V % 16 == 0 && V < (1ll << 31) && ldb >= V, "dsk_markov_block: bad V=%lld / ldb",
               (long long)V);
   const bool sampled = temperature > 0.0f;
@@ -298,10 +299,11 @@ extern "C" int dsk_markov_block(const float* base, int64_t ldb, int B, int cap, 
     hipLaunchKernelGGL(markov_step_kernel, dim3((unsigned)a.nblk), dim3(256), 0, st, a);
     DSK_LAUNCH_CHECK("dsk_markov_block (step)");
     if (sampled) {
-      // q_i = truncate(softmax(logits_i * (1/T))), sampled; Philox rows b * cap + s
+      // q_i = truncate(softmax(logits_i * (1/T))), sampled; Philox rows (row0 + b) * cap + s
       for (int b = 0; b < B; ++b) {
         const int rc = dsk_sample_rows(q_logits_out + ((int64_t)b * cap + s) * V, V, 1, temperature, top_p, top_k, 1,
-                                       seed, offset, b * cap + s, tok_out + b * cap + s, nullptr, nullptr, sample_ws,
+                                       seed, offset, (row0 + b) * cap + s, tok_out + b * cap + s, nullptr, nullptr,
+                                       sample_ws,
                                        sample_ws_bytes, stream);
         if (rc != DSK_OK) return rc;
       }

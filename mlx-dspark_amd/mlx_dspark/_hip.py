@@ -81,8 +81,8 @@ SIGNATURES: dict[str, tuple] = {
     "dsk_lens_add": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "dsk_markov_ws_bytes": (c_size_t, [c_int, c_int64, c_int]),
     "dsk_markov_block": (c_int, [c_void_p, c_int64, c_int, c_int, c_int64, c_int, c_void_p, c_void_p, c_void_p,
-                                 c_void_p, c_void_p, c_void_p, c_float, c_float, c_int, c_uint64, c_uint32, c_void_p,
-                                 c_void_p, c_void_p, c_size_t, c_void_p]),
+                                 c_void_p, c_void_p, c_void_p, c_float, c_float, c_int, c_uint64, c_uint32, c_int,
+                                 c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "dsk_row_logprobs": (c_int, [c_void_p, c_int64, c_int, c_int64, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
                                  c_void_p]),
     "dsk_logits_penalize": (c_int, [c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p, c_void_p]),

@@ -166,8 +166,9 @@ class SpecSlots:
         self.ctrl = cap_controller
         self.batched_drafter = batched_drafter
         self.capacity = int(capacity)
-        if self.capacity < 1 or self.capacity * max(self.k, self.cap + 1) > 64:
-            raise ValueError(f"capacity {capacity} x block {max(self.k, self.cap + 1)} exceeds 64 rows per forward")
+        # any capacity: batches of more than 64 rows run as groups of whole rows per kernel pass
+        if self.capacity < 1 or max(self.k, self.cap + 1) > 64:
+            raise ValueError(f"capacity {capacity} / block {max(self.k, self.cap + 1)}: a block is at most 64 rows")
         self.temperature, self.top_p, self.top_k = float(temperature), float(top_p), int(top_k)
         self.s64 = _seed64(seed)
         self.round = 0

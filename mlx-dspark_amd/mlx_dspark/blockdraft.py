@@ -62,8 +62,10 @@ def ingest_rows(d, fused: torch.Tensor, cache: PagedKVCache, n_valid: torch.Tens
     c, a = d.config, d.args
     v_norm = getattr(d, "v_norm", None)
     B, W = fused.shape[0], fused.shape[1]
-    if B * W > MAX_ROWS:
-        raise ValueError(f"batched context append of {B}x{W} rows > {MAX_ROWS}")
+    if B * W > MAX_ROWS:   # groups of whole batch rows, one kernel pass each
+        for b0, b1 in _groups(B, W):
+            ingest_rows(d, fused[b0:b1], cache.rows(b0, b1), n_valid[b0:b1])
+        return
     H = c.hidden_size
     th = fused.reshape(B * W, -1)
     hcp = ops.w8_gemm(ops.pack(th), d.fc, epi=ops.DSK_EPI_PARTIAL)
@@ -77,11 +79,28 @@ def ingest_rows(d, fused: torch.Tensor, cache: PagedKVCache, n_valid: torch.Tens
     ops.lens_add(cache.seq_lens[:B], n_valid, 1)
 
 
+def _groups(B: int, W: int):
+    """Groups of whole batch rows with at most 64 rows (B*W) each: one kernel pass per group."""
+    if W > MAX_ROWS:
+        raise ValueError(f"{W} rows per batch row > {MAX_ROWS}")
+    g = MAX_ROWS // W
+    return [(b0, min(B, b0 + g)) for b0 in range(0, B, g)]
+
+
 def block_layers(d, h: torch.Tensor, B: int, bs: int, cache: PagedKVCache, scale: float) -> torch.Tensor:
     """Run drafter ``d``'s decoder layers over the block rows h [B*bs, H] (bf16, updated in
     place) attending to context ++ block; returns h before the final norm. Llama 2-norm layers,
     or sandwich norms when the layers carry attn_out_norm / ff_out_norm (gemma4), with
-    d.layer_scalars multiplying each layer's output and d.v_norm normalising V."""
+    d.layer_scalars multiplying each layer's output and d.v_norm normalising V. More than 64
+    block rows run as groups of whole batch rows."""
+    if B * bs > MAX_ROWS:
+        for b0, b1 in _groups(B, bs):
+            _block_layers(d, h[b0 * bs:b1 * bs], b1 - b0, bs, cache.rows(b0, b1), scale)
+        return h
+    return _block_layers(d, h, B, bs, cache, scale)
+
+
+def _block_layers(d, h: torch.Tensor, B: int, bs: int, cache: PagedKVCache, scale: float) -> torch.Tensor:
     c, a = d.config, d.args
     M, H = B * bs, c.hidden_size
     eps = c.rms_norm_eps
@@ -113,8 +132,10 @@ def block_layers(d, h: torch.Tensor, B: int, bs: int, cache: PagedKVCache, scale
 def head_rows(d, h_rows: torch.Tensor, lm_head, out: torch.Tensor | None = None) -> torch.Tensor:
     """logits = lm_head(norm(h_rows)) (+ soft-cap) for h_rows [R, H] bf16 -> f32 [R, V]."""
     c = d.config
-    x = ops.pack(h_rows, d.norm, c.rms_norm_eps)
     out = out if out is not None else torch.empty((h_rows.shape[0], lm_head.N), dtype=torch.float32,
                                                   device=h_rows.device)
-    ops.w8_gemm(x, lm_head, out=out, softcap=c.final_logit_softcapping or 0.0)
+    for r0 in range(0, h_rows.shape[0], MAX_ROWS):
+        r1 = min(h_rows.shape[0], r0 + MAX_ROWS)
+        x = ops.pack(h_rows[r0:r1], d.norm, c.rms_norm_eps)
+        ops.w8_gemm(x, lm_head, out=out[r0:r1], softcap=c.final_logit_softcapping or 0.0)
     return out

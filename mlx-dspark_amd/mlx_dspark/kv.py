@@ -161,6 +161,11 @@ class PagedKVCache(list):
         length. Every single-row op (prefill, forward, drafter ingest) runs on it unchanged."""
         return RowCache(self, b)
 
+    def rows(self, b0: int, b1: int) -> "RowCache":
+        """Rows b0 .. b1-1 seen as a B = b1 - b0 cache (a group of a batch too wide for one
+        kernel pass)."""
+        return RowCache(self, b0, b1)
+
     def row_pages(self, b: int) -> list[int]:
         return [int(x) for x in self.block_table[b].tolist()]
 
@@ -188,25 +193,32 @@ class PagedKVCache(list):
 
 
 class RowCache(PagedKVCache):
-    """Row b of a PagedKVCache seen as a B = 1 cache (shares the parent's pools)."""
+    """Rows b .. b1-1 (default: row b alone) of a PagedKVCache seen as a cache of B = b1 - b
+    rows (shares the parent's pools, block-table rows and device lengths)."""
 
-    def __init__(self, parent: PagedKVCache, b: int):  # noqa: no super().__init__: nothing is allocated
+    def __init__(self, parent: PagedKVCache, b: int, b1: int | None = None):  # noqa: nothing is allocated
         list.__init__(self, (LayerView(self, l) for l in range(parent.n_layers)))
         self.parent, self.b = parent, int(b)
+        self.b1 = self.b + 1 if b1 is None else int(b1)
+        if not 0 <= self.b < self.b1 <= parent.B:
+            raise ValueError(f"rows {self.b} .. {self.b1 - 1} outside the cache's {parent.B} rows")
         for name in ("n_layers", "n_kv", "head_dim", "page", "max_pages", "max_ctx", "kv_dtype", "n_pages",
                      "k", "v", "k_sb", "v_sb"):
             setattr(self, name, getattr(parent, name))
-        self.B = 1
-        self.block_table = parent.block_table[self.b:self.b + 1]
-        self.seq_lens = parent.seq_lens[self.b:self.b + 1]
+        self.B = self.b1 - self.b
+        self.block_table = parent.block_table[self.b:self.b1]
+        self.seq_lens = parent.seq_lens[self.b:self.b1]
 
     @property
     def lengths(self):
-        return [self.parent.lengths[self.b]]
+        return self.parent.lengths[self.b:self.b1]
 
     @lengths.setter
     def lengths(self, v):
-        self.parent.lengths[self.b] = int(list(v)[0])
+        v = [int(x) for x in v]
+        if len(v) != self.B:
+            raise ValueError(f"{len(v)} lengths for {self.B} rows")
+        self.parent.lengths[self.b:self.b1] = v
 
     @property
     def layer_offsets(self):

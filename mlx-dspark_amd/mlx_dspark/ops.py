@@ -519,6 +519,9 @@ def lens_add(lens: torch.Tensor, n: torch.Tensor | None, add: int) -> None:
 
 
 # ----------------------------------------------------------------------------- DSpark Markov head
+MARKOV_MAX_B = 16  # batch rows of one dsk_markov_block call
+
+
 def markov_block(base_logits: torch.Tensor, first_prev: torch.Tensor, w1: W8Table, w2: W8Weight, *,
                  temperature: float = 0.0, top_p: float = 1.0, top_k: int = 0, seed: int = 0, offset: int = 0,
                  tok_out: torch.Tensor | None = None, q_logits_out: torch.Tensor | None = None):
@@ -543,11 +546,14 @@ def markov_block(base_logits: torch.Tensor, first_prev: torch.Tensor, w1: W8Tabl
         q_logits_out = torch.empty((B, cap, V), dtype=torch.float32, device=dev)
     R = w1.q.shape[1]
     ws = Workspace.get(dev)
-    buf = ws.reserve("markov", _hip.lib.dsk_markov_ws_bytes(B, V, int(sampled)))
-    call("dsk_markov_block", ptr(base_logits), V, B, cap, V, R, ptr(first_prev), ptr(w1.q), ptr(w1.s), ptr(w1.b),
-         ptr(w2.wt), ptr(w2.sb), float(temperature), float(top_p), int(top_k or 0), int(seed) & ((1 << 64) - 1),
-         int(offset) & 0xFFFFFFFF, ptr(tok_out), ptr(q_logits_out if sampled else None), ptr(buf), buf.numel(),
-         stream_ptr())
+    # pieces of MARKOV_MAX_B rows (the kernel's tile); row0 keeps every row's Philox stream
+    for b0 in range(0, B, MARKOV_MAX_B):
+        b1 = min(B, b0 + MARKOV_MAX_B)
+        buf = ws.reserve("markov", _hip.lib.dsk_markov_ws_bytes(b1 - b0, V, int(sampled)))
+        call("dsk_markov_block", ptr(base_logits[b0:b1]), V, b1 - b0, cap, V, R, ptr(first_prev[b0:b1]), ptr(w1.q),
+             ptr(w1.s), ptr(w1.b), ptr(w2.wt), ptr(w2.sb), float(temperature), float(top_p), int(top_k or 0),
+             int(seed) & ((1 << 64) - 1), int(offset) & 0xFFFFFFFF, b0, ptr(tok_out[b0:b1]),
+             ptr(q_logits_out[b0:b1] if sampled else None), ptr(buf), buf.numel(), stream_ptr())
     return (tok_out, q_logits_out) if sampled else tok_out
 
 

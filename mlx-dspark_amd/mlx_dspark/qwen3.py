@@ -174,16 +174,21 @@ class Qwen3W8:
     def forward(self, ids: torch.Tensor, cache: PagedKVCache, tap=None, *, advance: bool = True,
                 logits: str = "all", logits_out: torch.Tensor | None = None,
                 fused_out: torch.Tensor | None = None, h_out: torch.Tensor | None = None):
-        """ids [B, W] int32 on device (W rows per batch row, B*W <= 64).
+        """ids [B, W] int32 on device (W <= 64 rows per batch row).
 
         Positions come from cache.seq_lens (device). Returns (logits [B, W or 1, V] f32 or
         None, fused [B, W, n_tap*H] bf16 or None). advance=True moves seq_lens by W; the
-        speculative loops pass False and let the acceptance kernel apply n + 1."""
+        speculative loops pass False and let the acceptance kernel apply n + 1. A batch of
+        more than 64 rows runs as groups of whole batch rows, at most 64 rows each (the row
+        limit of one kernel pass), each group on a view of its rows of the cache."""
         a = self.args
         B, W = ids.shape
         M = B * W
+        if W > MAX_ROWS:
+            raise ValueError(f"forward pass of {W} rows per batch row > {MAX_ROWS}; chunk the prompt")
         if M > MAX_ROWS:
-            raise ValueError(f"forward pass of {M} rows > {MAX_ROWS}; chunk the prompt")
+            return self._forward_groups(ids, cache, tap, advance=advance, logits=logits, logits_out=logits_out,
+                                        fused_out=fused_out, h_out=h_out)
         H = a.hidden_size
         eps = a.rms_norm_eps
         tap = list(tap or [])
@@ -228,6 +233,33 @@ class Qwen3W8:
             ops.lens_add(cache.seq_lens, None, W)
             cache.note_lengths([l + W for l in cache.lengths])
         return out, (fused.view(B, W, -1) if fused is not None else None)
+
+    def _forward_groups(self, ids, cache, tap, *, advance, logits, logits_out, fused_out, h_out):
+        """forward over groups of floor(64 / W) batch rows; outputs land in row slices of one
+        buffer each, so the result is the same [B, ...] tensors a single pass returns."""
+        a = self.args
+        B, W = ids.shape
+        g = MAX_ROWS // W
+        per = W if logits == "all" else 1
+        out = None
+        if logits != "none":
+            out = logits_out if logits_out is not None else torch.empty(
+                (B * per, a.vocab_size), dtype=torch.float32, device=self.device)
+            out = out.view(B * per, a.vocab_size)
+        fused = None
+        if tap:
+            fused = fused_out if fused_out is not None else torch.empty(
+                (B * W, len(tap) * a.hidden_size), dtype=torch.bfloat16, device=self.device)
+            fused = fused.view(B * W, -1)
+        h_all = h_out.view(B * W, -1) if h_out is not None else None
+        for b0 in range(0, B, g):
+            b1 = min(B, b0 + g)
+            self.forward(ids[b0:b1], cache.rows(b0, b1), tap, advance=advance, logits=logits,
+                         logits_out=None if out is None else out[b0 * per:b1 * per],
+                         fused_out=None if fused is None else fused[b0 * W:b1 * W],
+                         h_out=None if h_all is None else h_all[b0 * W:b1 * W])
+        return (None if out is None else out.view(B, per, a.vocab_size),
+                None if fused is None else fused.view(B, W, -1))
 
     def head_logits(self, h: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         """lm_head(norm(h)) for h [M, H] bf16 (DFlash reuses the target head)."""

@@ -49,6 +49,21 @@ def test_batch_spec_generate_rows_follow_greedy(dev, pair, batched_drafter):
         _check_greedy(target.model, p, r.token_ids)
 
 
+def test_batch_wider_than_one_kernel_pass(dev, pair):
+    """20 rows at once: the verify forward (20 x 4 rows), the drafter's block (20 x 7 rows) and
+    context appends run as groups of whole rows of at most 64 rows, the Markov head in pieces of
+    16 rows; every row still follows its own prompt's greedy decoding."""
+    from mlx_dspark.batch_engine import batch_spec_generate
+    target, tok, d, cfg = pair
+    n = 20
+    prompts = _prompts(target.model.args.vocab_size, [9 + 3 * i for i in range(n)], 13)
+    print(f"batch_spec_generate over {n} rows", flush=True)
+    res = batch_spec_generate(target, tok, d, prompts, max_new_tokens=[8] * n, max_draft_tokens=3)
+    for p, r in zip(prompts, res):
+        assert r.num_tokens >= 8 and sum(r.accept_lengths) + 1 == r.num_tokens
+        _check_greedy(target.model, p, r.token_ids)
+
+
 def test_spec_slots_turnover(dev, pair):
     """Capacity 2, five requests admitted as slots free up: rows retire at different rounds,
     compaction moves block-table rows, and every result still follows its own prompt."""

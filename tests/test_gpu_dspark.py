@@ -32,7 +32,7 @@ def _table(V, R, seed, dev):
     return W8Table(q, s, b)
 
 
-@pytest.mark.parametrize("B,cap,V", [(1, 8, 4096), (3, 5, 151936 // 4), (1, 2, 1024)])
+@pytest.mark.parametrize("B,cap,V", [(1, 8, 4096), (3, 5, 151936 // 4), (1, 2, 1024), (20, 3, 4096)])
 def test_markov_greedy_matches_oracle(dev, B, cap, V):
     from mlx_dspark import ops
     print(f"markov greedy B={B} cap={cap} V={V}", flush=True)
@@ -55,14 +55,17 @@ def test_markov_greedy_matches_oracle(dev, B, cap, V):
             prev = t
 
 
-def test_markov_sampled_matches_oracle_sampling(dev):
+@pytest.mark.parametrize("B", [2, 20])
+def test_markov_sampled_matches_oracle_sampling(dev, B):
+    """B = 20 runs as pieces of 16 rows: every row still draws from its own Philox row."""
     from mlx_dspark import ops
-    B, cap, V = 2, 4, 8192
+    cap, V = 4, 8192
+    print(f"markov sampled B={B}", flush=True)
     w1 = _table(V, 256, 21, dev)
     w2 = _w8(V, 256, 22, dev)
     g = torch.Generator().manual_seed(5)
     base = torch.randn(B, cap, V, generator=g)
-    first = torch.tensor([3, 4000], dtype=torch.int32)
+    first = torch.tensor([3, 4000] + [(977 * b) % V for b in range(2, B)], dtype=torch.int32)
     tok, ql = ops.markov_block(base.to(dev), first.to(dev), w1, w2, temperature=0.8, top_p=0.9, top_k=0, seed=77,
                                offset=3)
     tok, ql = tok.cpu(), ql.cpu()
