@@ -46,8 +46,8 @@ sys.path.insert(0, str(REPO))
 PEAK_HBM_GBS = 8000.0
 # HBM bytes per gate_up launch from the FETCH_SIZE / WRITE_SIZE counter runs of
 # `bench.py --roofline-only` (profiles/w8_gemm_gate_up_24576x4096_m16_counters.md): fetches
-# 52778.54 KiB x 2.000 + writes 384 KiB x 1.000, the scales read on a 256 MiB copy
-TRAFFIC_GATE_UP = 108483666
+# 52855.72 KiB x 2.000 + writes 384 KiB x 1.000, the scales read on a 256 MiB copy
+TRAFFIC_GATE_UP = 108641739
 
 
 def log(*a):
