@@ -139,7 +139,7 @@ int dsk_w8_gemm(const uint16_t* x, const uint8_t* wt, const uint32_t* sb, int M,
  * kernel). Each 16-column partial is the balanced tree ((h0^2 + h1^2) + (h2^2 + h3^2)) + ...
  *
  * dsk_act_pack_rn: dsk_act_pack's residual add (part may be NULL: v = h), then copy[m][k] = v,
- *   out = packed bf16(v * norm_w[k]) (norm_w NULL: v) and ssq_out[k / 16][m].
+ *   out = packed bf16(v * norm_w[k]) (norm_w NULL: v) and ssq_out[m][k / 16].
  * dsk_w8_gemm_rn: dsk_w8_gemm (bits 8) or dsk_w4_gemm (bits 4) whose x is normed later when
  *   x_ssq != NULL (x_tiles = K / 16 partials of x's rows, eps the norm's epsilon), plus
  *   epi = DSK_EPI_RESIDUAL (o_proj / down_proj and the residual add after them): no K split;
