@@ -23,137 +23,9 @@
 #include <algorithm>
 
 #include "common.h"
+#include "kvrow.h"
 
 namespace dsk {
-
-// ----------------------------------------------------------------------------- row helpers
-// RoPE angle in fp32 as the reference computes it, reduced to [-1/2, 1/2) revolutions for
-// v_sin_f32 / v_cos_f32 (the reduction error is below the angle's own rounding).
-__device__ __forceinline__ void rope_sincos(int pos, float inv_freq, float& sn, float& cs) {
-  const float ang = (float)pos * inv_freq;
-  float rev = ang * 0.15915494309189535f;
-  rev -= rintf(rev);
-  sn = __builtin_amdgcn_sinf(rev);
-  cs = __builtin_amdgcn_cosf(rev);
-}
-
-// One head row of HD dims spread over L consecutive lanes (L = 64: a wave; L = 16: a quarter
-// wave), PER = HD / L consecutive dims per lane starting at dim PER * (lane % L).
-// Sum of the projection's split-K slices in slice order, times `scale` (the row scale of a
-// normed-later input; 1 otherwise), rounded to bf16.
-template <int PER>
-__device__ __forceinline__ void load_proj_row(const void* qkv, int splits, int64_t slice, int64_t off, int sub,
-                                              float (&v)[PER], float scale = 1.0f) {
-  if (splits == 0) {
-    const uint16_t* src = reinterpret_cast<const uint16_t*>(qkv) + off + (int64_t)sub * PER;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) v[e] = bf16_to_f32(src[e]);
-    return;
-  }
-  const float* src = reinterpret_cast<const float*>(qkv) + off + (int64_t)sub * PER;
-#pragma unroll
-  for (int e = 0; e < PER; ++e) v[e] = 0.0f;
-  // two slices' loads in flight at a time, summed in slice order
-  for (int sp = 0; sp < splits; sp += 2) {
-    float t[2][PER];
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int e = 0; e < PER; ++e) t[u][e] = sp + u < splits ? src[(sp + u) * slice + e] : 0.0f;
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int e = 0; e < PER; ++e)
-        if (sp + u < splits) v[e] += t[u][e];
-  }
-#pragma unroll
-  for (int e = 0; e < PER; ++e) v[e] = round_bf16(v[e] * scale);
-}
-
-// sum over the L lanes of a row (L a power of two, rows aligned to L lanes)
-template <int L>
-__device__ __forceinline__ float row_sum(float x) {
-#pragma unroll
-  for (int o = 1; o < L; o <<= 1) x += __shfl_xor(x, o, 64);
-  return x;
-}
-
-// per-head RMSNorm (nw != NULL) and rotate-half RoPE (rope) of one row held as above
-template <int HD, int L>
-__device__ __forceinline__ void norm_rope_row(float (&v)[HD / L], int sub, const uint16_t* nw, float eps, bool rope,
-                                              const float* inv_freq, int pos) {
-  constexpr int PER = HD / L;
-  if (nw) {
-    float ss = 0.0f;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) ss += v[e] * v[e];
-    ss = row_sum<L>(ss);
-    const float r = rsqrtf(ss / (float)HD + eps);
-#pragma unroll
-    for (int e = 0; e < PER; ++e) v[e] = round_bf16((v[e] * r) * bf16_to_f32(nw[sub * PER + e]));
-  }
-  if (rope) {
-    // dim d pairs with d + HD/2, which sits L/2 lanes away
-    const bool first_half = sub < L / 2;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      const float partner = __shfl_xor(v[e], L / 2, 64);
-      const int d = sub * PER + e;
-      float sn, cs;
-      rope_sincos(pos, inv_freq[first_half ? d : d - HD / 2], sn, cs);
-      const float x1 = first_half ? v[e] : partner, x2 = first_half ? partner : v[e];
-      v[e] = round_bf16(first_half ? x1 * cs - x2 * sn : x2 * cs + x1 * sn);
-    }
-  }
-}
-
-// Store one K or V row at pool token `tok` (bf16, or 8-bit affine group 64 with its scale and
-// bias) and leave in v the values attention reads back for it.
-template <int HD, int L>
-__device__ __forceinline__ void kv_store_row(float (&v)[HD / L], int sub, int kv_dtype, void* pool, uint32_t* sbp,
-                                             int64_t tok) {
-  constexpr int PER = HD / L;
-  if (kv_dtype == DSK_KV_BF16) {
-    uint16_t* dst = reinterpret_cast<uint16_t*>(pool) + tok * HD + sub * PER;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) dst[e] = f32_to_bf16(v[e]);
-    return;
-  }
-  constexpr int GL = 64 / PER;  // lanes per group of 64 dims
-  float lo = v[0], hi = v[0];
-#pragma unroll
-  for (int e = 1; e < PER; ++e) {
-    lo = fminf(lo, v[e]);
-    hi = fmaxf(hi, v[e]);
-  }
-#pragma unroll
-  for (int o = 1; o < GL; o <<= 1) {
-    lo = fminf(lo, __shfl_xor(lo, o, 64));
-    hi = fmaxf(hi, __shfl_xor(hi, o, 64));
-  }
-  uint16_t s16 = f32_to_bf16((hi - lo) / 255.0f);
-  float sf = bf16_to_f32(s16);
-  if (!(sf > 0.0f)) {
-    s16 = 0x3f80;
-    sf = 1.0f;
-  }
-  const uint16_t b16 = f32_to_bf16(lo);
-  const float bf = bf16_to_f32(b16);
-  uint8_t* qd = reinterpret_cast<uint8_t*>(pool) + tok * HD + sub * PER;
-#pragma unroll
-  for (int e = 0; e < PER; ++e) {
-    const float q = fminf(fmaxf(rintf((v[e] - bf) / sf), 0.0f), 255.0f);
-    qd[e] = (uint8_t)(int)q;
-    v[e] = round_bf16(fmaf(sf, q, bf));
-  }
-  if ((sub % GL) == 0) sbp[tok * (HD / 64) + (sub * PER) / 64] = (uint32_t)s16 | ((uint32_t)b16 << 16);
-}
-
-__device__ __forceinline__ int64_t pool_token(const int32_t* block_table, int max_pages, int page, int nkv, int b,
-                                              int kvh, int j) {
-  const int pg = block_table[(int64_t)b * max_pages + j / page];
-  return ((int64_t)pg * nkv + kvh) * page + (j % page);
-}
 
 // ----------------------------------------------------------------------------- append
 // One wave per (token row, head): lane holds dims [PER*lane, PER*lane + PER) (PER = HD/64).
@@ -177,14 +49,7 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
   // ... per lane, then across the wave (the GEMM's own order)
   float v[PER];
   if constexpr (RS) {
-    // the partials' loads and these are independent: one memory round trip for both
-    float xs[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      xs[j] = lane + 64 * j < x_tiles ? x_ssq[(int64_t)row * x_tiles + lane + 64 * j] : 0.0f;
-    float t = ((xs[0] + xs[1]) + xs[2]) + xs[3];
-    for (int j = lane + 256; j < x_tiles; j += 64) t += x_ssq[(int64_t)row * x_tiles + j];
-    const float rs = rsqrtf(wave_sum(t) / x_k + x_eps);
+    const float rs = proj_row_scale(x_ssq, x_tiles, row, lane, x_k, x_eps);
     load_proj_row<PER>(qkv, qkv_splits, (int64_t)B * W * nheads * HD, ((int64_t)row * nheads + head) * HD, lane, v,
                        rs);
   } else {
@@ -1262,6 +1127,254 @@ __global__ __launch_bounds__(kVerifyCombineThreads) void attention_verify_combin
             pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv)};
 }
 
+// ----------------------------------------------------------------------------- many-query pass
+// A prefill (head_dim 128, more than 64 new tokens per row): one workgroup per (row b, kv head,
+// block of 128 query rows), no key splits and so no combine. The row block's keys stream through
+// LDS in 64-key blocks (double-buffered: block n + 1 is dequantised into the other buffer while
+// block n is scored, block n + 2's loads are in flight meanwhile, one barrier per block). Each
+// wave owns two 16-query tiles, so every K and V fragment it reads from LDS feeds two tiles'
+// MFMAs. Scores S^T = K . Q^T and O^T = V^T . P^T as in the other attention kernels; masking
+// runs only on blocks that straddle a wave's causal diagonal, its window edge or the last key.
+// Row blocks with the most keys are launched first (the grid's y runs from the last block).
+constexpr int kPfKeys = 64;                   // keys per LDS block
+constexpr int kPfKRow = 128 + 8;              // K rows in LDS (bf16, padded: conflict-free reads)
+constexpr int kPfVRow = kPfKeys + 8;          // V^T rows in LDS (bf16, padded)
+constexpr int kPfTiles = 2;                   // 16-query tiles per wave
+constexpr int kPfRows = 4 * kPfTiles * 16;    // query rows per workgroup
+constexpr int kPfMaxPages = 1024;             // page ids of a row block's keys held in LDS
+
+template <int KVT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void attention_prefill_kernel(AttnArgs a) {
+  constexpr int HD = 128, KS = HD / 32, DT = HD / 16, NKT = kPfKeys / 16, TPW = kPfTiles;
+  constexpr int CK = kPfKeys * (HD / 8) / 256;        // 8-dim K chunks per thread
+  constexpr int CV = (kPfKeys / 2) * (HD / 8) / 256;  // (2 keys x 8 dims) V chunks per thread
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][kPfKeys * kPfKRow];
+  __shared__ __attribute__((aligned(16))) uint32_t vt[2][HD * kPfVRow / 2];
+  __shared__ int pgs[kPfMaxPages];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int bk = blockIdx.x, b = bk / a.nkv, kvh = bk % a.nkv;
+  const int nrb = (a.R + kPfRows - 1) / kPfRows;
+  const int rb = nrb - 1 - (int)blockIdx.y;
+  float scale = a.scale;
+  int causal = a.causal, window = a.window;
+  asm volatile("" : "+s"(scale), "+s"(causal), "+s"(window));
+  const int off = a.seq_lens[b];
+  const int jmax = a.max_pages * a.page;
+  const int Lk = min(off + a.W, jmax);
+  const int r0 = rb * kPfRows, r_last = min(a.R, r0 + kPfRows) - 1;
+  // the workgroup's keys [j_beg, j_end): up to its last row's position (causal), from its first
+  // row's window start, in whole blocks from there
+  int j_beg = 0, j_end = Lk;
+  if (causal) {
+    j_end = min(Lk, off + r_last / a.G + 1);
+    if (window > 0) j_beg = max(0, off + r0 / a.G - window + 1);
+  }
+  const int nb = j_end > j_beg ? (j_end - j_beg + kPfKeys - 1) / kPfKeys : 0;
+  const int pg0 = j_beg / a.page;
+  if (nb > 0) {
+    const int npg = (j_end - 1) / a.page - pg0 + 1;
+    for (int t = threadIdx.x; t < npg; t += 256) pgs[t] = a.block_table[(int64_t)b * a.max_pages + pg0 + t];
+  }
+  // this wave's query tiles (rows past R load row 0 and are never stored)
+  const int wr0 = r0 + wv * TPW * 16;
+  bf16x8 qf[TPW][KS];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    QTile<HD, false> qt;
+    qtile_load<HD, false>(a, b, kvh, wr0 / 16 + t, lane, qt);
+    qtile_finish<HD, false>(a, off, wr0 / 16 + t, lane, qt, qf[t]);
+  }
+  __syncthreads();  // the page ids
+
+  auto tok_of = [&](int j) -> int64_t {
+    j = min(j, j_end - 1);  // keys past the range load the last one and are zeroed in LDS
+    return ((int64_t)pgs[j / a.page - pg0] * a.nkv + kvh) * a.page + (j % a.page);
+  };
+  Chunk8 kc[CK], vc[CV][2];
+  auto issue = [&](int j0) {
+#pragma unroll
+    for (int ci = 0; ci < CK; ++ci) {
+      const int c = threadIdx.x + ci * 256;
+      load_chunk<KVT>(a.k_pool, a.k_sb, HD, tok_of(j0 + c / (HD / 8)), (c % (HD / 8)) * 8, kc[ci]);
+    }
+#pragma unroll
+    for (int ci = 0; ci < CV; ++ci) {
+      const int c = threadIdx.x + ci * 256;
+      const int kp = c % (kPfKeys / 2), d0 = (c / (kPfKeys / 2)) * 8;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) load_chunk<KVT>(a.v_pool, a.v_sb, HD, tok_of(j0 + 2 * kp + u), d0, vc[ci][u]);
+    }
+  };
+  // dequantise the loaded block [j_lo, j_hi) into LDS buffer buf (keys past j_hi zeroed)
+  auto to_lds = [&](int buf, int j_lo, int j_hi) {
+#pragma unroll
+    for (int ci = 0; ci < CK; ++ci) {
+      const int c = threadIdx.x + ci * 256;
+      const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
+      uint16_t h[8];
+      chunk_bf16<KVT>(kc[ci], h);
+      u32x4 w = *reinterpret_cast<const u32x4*>(h);
+      if (j_lo + key >= j_hi) w = u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&ks[buf][key * kPfKRow + d0]) = w;
+    }
+#pragma unroll
+    for (int ci = 0; ci < CV; ++ci) {
+      const int c = threadIdx.x + ci * 256;
+      const int kp = c % (kPfKeys / 2), d0 = (c / (kPfKeys / 2)) * 8;
+      const int j0 = j_lo + 2 * kp;
+      uint16_t h0[8], h1[8];
+      chunk_bf16<KVT>(vc[ci][0], h0);
+      chunk_bf16<KVT>(vc[ci][1], h1);
+      const bool z0 = j0 >= j_hi, z1 = j0 + 1 >= j_hi;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        vt[buf][((d0 + e) * kPfVRow) / 2 + kp] = (uint32_t)(z0 ? 0 : h0[e]) | ((uint32_t)(z1 ? 0 : h1[e]) << 16);
+    }
+  };
+
+  // running state per tile; l is each lane's partial over its keys (the four lanes of a query
+  // share its max, so their partials add up at the end)
+  float m_run[TPW], l_run[TPW];
+  f32x4 o[TPW][DT];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    m_run[t] = -__builtin_inff();
+    l_run[t] = 0.0f;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) o[t][d] = f32x4{0, 0, 0, 0};
+  }
+  const float c2 = scale * 1.4426950408889634f;
+  const bool wave_live = wr0 < a.R;
+  const bool wave_full = wr0 + TPW * 16 <= a.R;
+  const int wq_lo = off + min(wr0, a.R - 1) / a.G;                // smallest position of the wave's rows
+  const int wq_hi = off + min(wr0 + TPW * 16 - 1, a.R - 1) / a.G;  // largest
+
+  auto compute = [&](int buf, int j_lo, int j_hi) {
+    // ---- S^T[key][q]: k-step outer, every key tile's fragment feeding both query tiles
+    f32x4 st[TPW][NKT];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int h = 0; h < NKT; ++h) st[t][h] = f32x4{0, 0, 0, 0};
+    const uint16_t* kbase = &ks[buf][(lane & 15) * kPfKRow + (lane >> 4) * 8];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      bf16x8 kf[NKT];
+#pragma unroll
+      for (int h = 0; h < NKT; ++h) kf[h] = *reinterpret_cast<const bf16x8*>(kbase + h * 16 * kPfKRow + s * 32);
+#pragma unroll
+      for (int h = 0; h < NKT; ++h)
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) st[t][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[h], qf[t][s], st[t][h], 0, 0, 0);
+    }
+    // ---- mask (only a block that straddles a row's visible range), max, exp2, P
+    const bool masked = !wave_full || j_hi - j_lo < kPfKeys || (causal && j_lo + kPfKeys - 1 > wq_lo) ||
+                        (causal && window > 0 && j_lo < wq_hi - window + 1);
+    bf16x8 pb[TPW][NKT / 2];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      if (masked) {
+        const int rq = wr0 + t * 16 + (lane & 15);
+        const bool qvalid = rq < a.R;
+        const int qpos = off + (qvalid ? rq / a.G : 0);
+        int k_last = j_hi - 1, k_first = 0;
+        if (causal) {
+          k_last = min(k_last, qpos);
+          if (window > 0) k_first = qpos - window + 1;
+        }
+        if (!qvalid) k_last = -1;
+#pragma unroll
+        for (int h = 0; h < NKT; ++h)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int j = j_lo + h * 16 + (lane >> 4) * 4 + r;
+            if (j < k_first || j > k_last) st[t][h][r] = -__builtin_inff();
+          }
+      }
+      float mx = m_run[t];
+#pragma unroll
+      for (int h = 0; h < NKT; ++h) mx = fmaxf(mx, fmaxf(fmaxf(st[t][h][0], st[t][h][1]), fmaxf(st[t][h][2], st[t][h][3])));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // masked keys: exp2(-inf) = 0; a row with no visible key yet keeps m = -inf, l = 0, o = 0
+      const float mb = mx == -__builtin_inff() ? 0.0f : mx * c2;
+      const float alpha = m_run[t] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f((m_run[t] - mx) * c2);
+      float lsum = 0.0f;
+#pragma unroll
+      for (int cp = 0; cp < NKT / 2; ++cp) {
+        uint32_t w[4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const f32x4& sv = st[t][2 * cp + u];
+            w[2 * u + hh] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(sv[2 * hh], c2, -mb)),
+                                        __builtin_amdgcn_exp2f(fmaf(sv[2 * hh + 1], c2, -mb)));
+            lsum += __uint_as_float(w[2 * u + hh] << 16) + __uint_as_float(w[2 * u + hh] & 0xffff0000u);
+          }
+        pb[t][cp] = __builtin_bit_cast(bf16x8, (u32x4{w[0], w[1], w[2], w[3]}));
+      }
+      l_run[t] = l_run[t] * alpha + lsum;
+      m_run[t] = mx;
+      if (__any(alpha != 1.0f))
+#pragma unroll
+        for (int d = 0; d < DT; ++d) o[t][d] *= alpha;
+    }
+    // ---- O^T[d][q] += V^T . P^T: each V^T fragment feeds both query tiles
+    const uint16_t* vt16 = reinterpret_cast<const uint16_t*>(vt[buf]);
+#pragma unroll
+    for (int cp = 0; cp < NKT / 2; ++cp)
+#pragma unroll
+      for (int d = 0; d < DT; ++d) {
+        const uint16_t* vr = vt16 + (d * 16 + (lane & 15)) * kPfVRow + 32 * cp + (lane >> 4) * 4;
+        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, (u32x4{lo.x, lo.y, hi.x, hi.y}));
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) o[t][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[t][cp], o[t][d], 0, 0, 0);
+      }
+  };
+
+  if (nb > 0) {
+    issue(j_beg);
+    to_lds(0, j_beg, min(j_end, j_beg + kPfKeys));
+    if (nb > 1) issue(j_beg + kPfKeys);
+  }
+  __syncthreads();
+#pragma unroll 1
+  for (int n = 0; n < nb; ++n) {
+    const int j_lo = j_beg + n * kPfKeys, j_hi = min(j_end, j_lo + kPfKeys);
+    // a wave whose rows see none of the block skips it (causal: all its rows before the block;
+    // window: all its rows' windows past it)
+    const bool skip = !wave_live || (causal && j_lo > wq_hi) || (causal && window > 0 && j_hi - 1 < wq_lo - window + 1);
+    if (!skip) compute(n & 1, j_lo, j_hi);
+    if (n + 1 < nb) {
+      // the other buffer was last read in block n - 1, which every wave finished before the
+      // previous barrier
+      to_lds((n + 1) & 1, j_lo + kPfKeys, min(j_end, j_lo + 2 * kPfKeys));
+      if (n + 2 < nb) issue(j_lo + 2 * kPfKeys);
+    }
+    __syncthreads();
+  }
+
+  // ---- the output: o / l, 4 consecutive dims per lane and d tile
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    float l = l_run[t];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const int rq = wr0 + t * 16 + (lane & 15);
+    if (rq >= a.R) continue;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const int i = rq / a.G, hl = rq % a.G;
+    uint16_t* dst = a.out + attn_out_index(a, HD, b, i, kvh * a.G + hl, (lane >> 4) * 4);
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+      *reinterpret_cast<uint2*>(dst + d * 16) = uint2{pack_bf16x2(o[t][d][0] * inv, o[t][d][1] * inv),
+                                                      pack_bf16x2(o[t][d][2] * inv, o[t][d][3] * inv)};
+  }
+}
+
 // ----------------------------------------------------------------------------- host helpers
 template <int HD, int QT, bool FUSED>
 static void launch_attention(const AttnArgs& a, int kv_dtype, bool softcap, dim3 grid, hipStream_t st) {
@@ -1325,6 +1438,19 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
   DSK_REQUIRE(!fused || a.W <= 64, "%s: W=%d new tokens exceeds 64", who, a.W);
   DSK_REQUIRE(!a.out_packed || (a.B * a.W <= 64 && (a.nq * hd) % 64 == 0), "%s: packed output needs B*W <= 64", who);
   a.fused = fused ? 1 : 0;
+  const bool sc = softcap > 0.0f;
+  if (hd == 128 && !fused && !sc && !a.out_packed && a.W > kAttnVerifyMaxW && a.max_pages <= kPfMaxPages) {
+    // many-query passes (prefills): whole key ranges per query block, no splits, no combine
+    a.nsplit = 1;
+    a.kps = max_ctx;
+    a.part_o = nullptr;
+    a.part_ml = nullptr;
+    const dim3 pgrid((unsigned)(a.B * a.nkv), (unsigned)ceil_div(a.R, kPfRows));
+    if (a.kv_dtype == DSK_KV_U8) hipLaunchKernelGGL(attention_prefill_kernel<DSK_KV_U8>, pgrid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(attention_prefill_kernel<DSK_KV_BF16>, pgrid, dim3(256), 0, st, a);
+    DSK_LAUNCH_CHECK(who);
+    return DSK_OK;
+  }
   int nblk = (fused || QT != 1) ? 1 : attn_blocks(hd, max_ctx, a.W);
   while (nblk > 1 && attn_split_keys(hd, max_ctx) * nblk / a.page + 1 > kAttnMaxSplitPages) --nblk;
   DSK_REQUIRE(attn_split_keys(hd, max_ctx) / a.page + 1 <= kAttnMaxSplitPages, "%s: page size %d too small", who,
@@ -1337,7 +1463,6 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
   a.part_ml = a.nsplit > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
                                                        attn_part_o_bytes(a.B, a.W, a.nq, hd, a.nsplit))
                            : nullptr;
-  const bool sc = softcap > 0.0f;
   if (hd == 128 && !fused && a.R <= kVerifyMaxR && a.page % kVerifyBlock == 0) {
     // verify passes: 4 waves per split of 256 keys, 64 keys each, every query tile
     a.kps = kVerifyKeys;

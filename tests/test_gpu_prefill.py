@@ -1,8 +1,10 @@
 """GPU: the dense prefill (src/mlx_dspark/generate.py:613-656 prefills the prompt in 2048-row
 chunks; here a long prompt runs layer by layer over all of its rows). Its kernels against closed
 forms: bf16 rows of a W8 / W4 weight bit for bit, the row RMSNorm and gated activation, and the
-many-query causal attention (W > 64: query-tile groups, long key splits, per-row split counts)
-against a float32 softmax over the stored K/V; then the whole prefill against the oracle: the
+many-query attention (W > 64: one workgroup per 128-row query block streaming its whole key
+range in 64-key blocks; causal, bidirectional and sliding-window masks, ragged rows, GQA groups
+of 1 to 8) against a float32 softmax over the stored K/V; then the whole prefill against the
+oracle: the
 last position's logits, the tapped hidden states, and a verify block decoded from the cache it
 filled."""
 
@@ -106,6 +108,82 @@ def test_many_query_attention(dev, kv_bits, L0, W):
     got = out.float().cpu().view(W, nq, hd)
     err = (got - ref).abs().max() / ref.abs().max()
     assert err < 2e-2, err
+
+
+@pytest.mark.parametrize("kv_bits,lens,W,nq,nkv,causal,window", [
+    (8, [100, 1000], 300, 8, 2, True, 0),        # ragged rows, G = 4
+    (None, [0], 1100, 4, 2, True, 0),            # 18 key blocks through both LDS buffers, G = 2
+    (8, [50, 7], 130, 2, 2, False, 0),           # bidirectional, G = 1
+    (8, [400], 200, 8, 2, True, 128),            # sliding window
+    (None, [0, 64, 333], 65, 16, 2, True, 0),    # one row past the verify width, G = 8
+])
+def test_many_query_attention_masks_and_rows(dev, kv_bits, lens, W, nq, nkv, causal, window):
+    """Random K/V written straight into shuffled pages (8-bit codes with random scale / bias
+    words, or bf16), random queries; each row b's query i sits at position lens[b] + i."""
+    from mlx_dspark import ops
+    from mlx_dspark.kv import PagedKVCache
+    print(f"many-query attention kv_bits={kv_bits} lens={lens} W={W} nq={nq} nkv={nkv} causal={causal} "
+          f"window={window}", flush=True)
+    hd, B = 128, len(lens)
+    max_ctx = max(lens) + W + 64
+    cache = PagedKVCache(1, B, nkv, hd, max_ctx, kv_bits=kv_bits, spare_pages=5)
+    g = torch.Generator().manual_seed(sum(lens) + W + nq)
+    perm = torch.randperm(cache.n_pages, generator=g)[: B * cache.max_pages]
+    cache.block_table.copy_(perm.view(B, cache.max_pages).to(torch.int32))
+    if kv_bits is None:
+        for pool in (cache.k[0], cache.v[0]):
+            pool.copy_(torch.randn(pool.shape, generator=g).to(torch.bfloat16))
+    else:
+        for pool, sb in ((cache.k[0], cache.k_sb[0]), (cache.v[0], cache.v_sb[0])):
+            pool.copy_(torch.randint(0, 256, pool.shape, generator=g, dtype=torch.uint8))
+            sc = (0.01 + 0.02 * torch.rand(sb.shape, generator=g)).to(torch.bfloat16).view(torch.int16)
+            bi = (-2.0 + torch.rand(sb.shape, generator=g)).to(torch.bfloat16).view(torch.int16)
+            sb.copy_((sc.int() & 0xFFFF) | (bi.int() << 16))
+    cache.set_lengths(lens)
+    q = torch.randn(B * W, nq * hd, generator=g).to(torch.bfloat16).to(dev)
+    out = ops.attention(q, B, W, nq, nkv, hd, hd ** -0.5, cache.seq_lens, cache.max_ctx, cache.block_table,
+                        cache.page, cache.kv_dtype, *cache.layer_args(0), causal=causal, window=window)
+    torch.cuda.synchronize()
+    got = out.float().cpu().view(B, W, nq, hd)
+    G = nq // nkv
+    worst = 0.0
+    for b, L0 in enumerate(lens):
+        n = L0 + W
+        K, V = _row_pool_rows(cache, b, n, "k"), _row_pool_rows(cache, b, n, "v")   # [n, nkv, hd]
+        pos = torch.arange(L0, L0 + W)[:, None]
+        j = torch.arange(n)[None, :]
+        allowed = j <= pos if causal else torch.ones(W, n, dtype=torch.bool)
+        if window:
+            allowed = allowed & (j > pos - window)
+        qf = q.float().cpu().view(B, W, nq, hd)[b]
+        for h in range(nq):
+            sc = (qf[:, h] @ K[:, h // G].T) * hd ** -0.5
+            sc = sc.masked_fill(~allowed, float("-inf"))
+            ref = torch.softmax(sc, -1) @ V[:, h // G]
+            worst = max(worst, float((got[b, :, h] - ref).abs().max() / ref.abs().max()))
+    assert worst < 2e-2, worst
+
+
+def _row_pool_rows(cache, b, n, which):
+    """[n, nkv, hd] float values of row b's tokens 0..n-1 (dequantized as the kernels do)."""
+    page = cache.page
+    pool = (cache.k if which == "k" else cache.v)[0].cpu()
+    sb = (cache.k_sb if which == "k" else cache.v_sb)[0]
+    sb = None if sb is None else sb.cpu().numpy().view(np.uint32)
+    bt = cache.block_table[b].cpu().numpy()
+    rows = []
+    for j in range(n):
+        p = int(bt[j // page])
+        if sb is None:
+            rows.append(pool[p, :, j % page].float())
+        else:
+            qv = pool[p, :, j % page].numpy().astype(np.float32)
+            w = sb[p, :, j % page]
+            sc = O.bits_to_f32((w & 0xFFFF).astype(np.uint16))
+            bi = O.bits_to_f32((w >> 16).astype(np.uint16))
+            v = qv.reshape(qv.shape[0], -1, 64) * sc[..., None] + bi[..., None]
+            rows.append(torch.from_numpy(O.bf16_round(v.reshape(qv.shape).astype(np.float32))))
+    return torch.stack(rows)
 
 
 def test_dense_prefill_matches_oracle(dev):
