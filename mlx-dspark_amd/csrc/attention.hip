@@ -1132,24 +1132,32 @@ __global__ __launch_bounds__(kVerifyCombineThreads) void attention_verify_combin
 // block of 128 query rows), no key splits and so no combine. The row block's keys stream through
 // LDS in 64-key blocks (double-buffered: block n + 1 is dequantised into the other buffer while
 // block n is scored, block n + 2's loads are in flight meanwhile, one barrier per block). Each
-// wave owns two 16-query tiles, so every K and V fragment it reads from LDS feeds two tiles'
-// MFMAs. Scores S^T = K . Q^T and O^T = V^T . P^T as in the other attention kernels; masking
+// of the kPfWaves waves owns two 16-query tiles, so every K and V fragment it reads from LDS
+// feeds two tiles' MFMAs, and each block's dequantisation is shared by all the rows. The row
+// sums of P come out of the P.V MFMAs as one more V^T tile of ones. Scores S^T = K . Q^T and O^T = V^T . P^T as in the other attention kernels; masking
 // runs only on blocks that straddle a wave's causal diagonal, its window edge or the last key.
 // Row blocks with the most keys are launched first (the grid's y runs from the last block).
 constexpr int kPfKeys = 64;                   // keys per LDS block
 constexpr int kPfKRow = 128 + 8;              // K rows in LDS (bf16, padded: conflict-free reads)
 constexpr int kPfVRow = kPfKeys + 8;          // V^T rows in LDS (bf16, padded)
 constexpr int kPfTiles = 2;                   // 16-query tiles per wave
-constexpr int kPfRows = 4 * kPfTiles * 16;    // query rows per workgroup
+#ifndef DSK_PF_WAVES
+#define DSK_PF_WAVES 8
+#endif
+constexpr int kPfWaves = DSK_PF_WAVES;
+constexpr int kPfThreads = kPfWaves * 64;
+constexpr int kPfRows = kPfWaves * kPfTiles * 16;  // query rows per workgroup
 constexpr int kPfMaxPages = 1024;             // page ids of a row block's keys held in LDS
 
-// At most 256 VGPRs (two waves per SIMD): two workgroups share a CU, one's key staging running
-// under the other's MFMAs (measured 436 -> 299 us on the 4096-token Qwen3-8B layer).
+// At most 256 VGPRs (two waves per SIMD: one 8-wave workgroup per CU, whose waves' staging and
+// MFMAs interleave). On the 4096-token Qwen3-8B layer: 436 us with 4 waves and no bound, 299 us
+// with 4 waves and this bound, 239 us with 8 waves sharing each block's dequantisation.
 template <int KVT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_prefill_kernel(AttnArgs a) {
-  constexpr int HD = 128, KS = HD / 32, DT = HD / 16, NKT = kPfKeys / 16, TPW = kPfTiles;
-  constexpr int CK = kPfKeys * (HD / 8) / 256;        // 8-dim K chunks per thread
-  constexpr int CV = (kPfKeys / 2) * (HD / 8) / 256;  // (2 keys x 8 dims) V chunks per thread
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_prefill_kernel(AttnArgs a) {
+  constexpr int HD = 128, KS = HD / 32, DT = HD / 16, NKT = kPfKeys / 16, TPW = kPfTiles, NTHR = kPfThreads;
+  constexpr int CK = kPfKeys * (HD / 8) / NTHR;        // 8-dim K chunks per thread
+  constexpr int CV = (kPfKeys / 2) * (HD / 8) / NTHR;  // (2 keys x 8 dims) V chunks per thread
+  static_assert(CK * NTHR == kPfKeys * (HD / 8) && CV * NTHR == (kPfKeys / 2) * (HD / 8), "whole chunks per thread");
   __shared__ __attribute__((aligned(16))) uint16_t ks[2][kPfKeys * kPfKRow];
   __shared__ __attribute__((aligned(16))) uint32_t vt[2][HD * kPfVRow / 2];
   __shared__ int pgs[kPfMaxPages];
@@ -1175,7 +1183,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int pg0 = j_beg / a.page;
   if (nb > 0) {
     const int npg = (j_end - 1) / a.page - pg0 + 1;
-    for (int t = threadIdx.x; t < npg; t += 256) pgs[t] = a.block_table[(int64_t)b * a.max_pages + pg0 + t];
+    for (int t = threadIdx.x; t < npg; t += NTHR) pgs[t] = a.block_table[(int64_t)b * a.max_pages + pg0 + t];
   }
   // this wave's query tiles (rows past R load row 0 and are never stored)
   const int wr0 = r0 + wv * TPW * 16;
@@ -1200,12 +1208,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   auto issue = [&](int j0) {
 #pragma unroll
     for (int ci = 0; ci < CK; ++ci) {
-      const int c = threadIdx.x + ci * 256;
+      const int c = threadIdx.x + ci * NTHR;
       load_chunk<KVT>(a.k_pool, a.k_sb, HD, tok_of(j0 + c / (HD / 8)), (c % (HD / 8)) * 8, kc[ci]);
     }
 #pragma unroll
     for (int ci = 0; ci < CV; ++ci) {
-      const int c = threadIdx.x + ci * 256;
+      const int c = threadIdx.x + ci * NTHR;
       const int kp = c % (kPfKeys / 2), d0 = (c / (kPfKeys / 2)) * 8;
 #pragma unroll
       for (int u = 0; u < 2; ++u) load_chunk<KVT>(a.v_pool, a.v_sb, HD, tok_of(j0 + 2 * kp + u), d0, vc[ci][u]);
@@ -1228,7 +1236,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 #pragma unroll
     for (int ci = 0; ci < CK; ++ci) {
-      const int c = threadIdx.x + ci * 256;
+      const int c = threadIdx.x + ci * NTHR;
       const int key = c / (HD / 8), d0 = (c % (HD / 8)) * 8;
       uint16_t h[8];
       chunk_bf16<KVT>(kc[ci], h);
@@ -1238,7 +1246,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 #pragma unroll
     for (int ci = 0; ci < CV; ++ci) {
-      const int c = threadIdx.x + ci * 256;
+      const int c = threadIdx.x + ci * NTHR;
       const int kp = c % (kPfKeys / 2), d0 = (c / (kPfKeys / 2)) * 8;
       const int j0 = j_lo + 2 * kp;
       uint16_t h0[8], h1[8];
@@ -1251,17 +1259,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   };
 
-  // running state per tile; l is each lane's partial over its keys (the four lanes of a query
-  // share its max, so their partials add up at the end)
-  float m_run[TPW], l_run[TPW];
-  f32x4 o[TPW][DT];
+  // running state per tile: the max, O^T and the row sums of P (every element of lt[t] holds the
+  // lane's query's sum: a V^T tile of ones in the P.V product)
+  float m_run[TPW];
+  f32x4 o[TPW][DT], lt[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
     m_run[t] = -__builtin_inff();
-    l_run[t] = 0.0f;
+    lt[t] = f32x4{0, 0, 0, 0};
 #pragma unroll
     for (int d = 0; d < DT; ++d) o[t][d] = f32x4{0, 0, 0, 0};
   }
+  const u32x4 ones_u = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, ones_u);
   const float c2 = scale * 1.4426950408889634f;
   const bool wave_live = wr0 < a.R;
   const bool wave_full = wr0 + TPW * 16 <= a.R;
@@ -1318,7 +1328,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // masked keys: exp2(-inf) = 0; a row with no visible key yet keeps m = -inf, l = 0, o = 0
       const float mb = mx == -__builtin_inff() ? 0.0f : mx * c2;
       const float alpha = m_run[t] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f((m_run[t] - mx) * c2);
-      float lsum = 0.0f;
 #pragma unroll
       for (int cp = 0; cp < NKT / 2; ++cp) {
         uint32_t w[4];
@@ -1329,20 +1338,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const f32x4& sv = st[t][2 * cp + u];
             w[2 * u + hh] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(sv[2 * hh], c2, -mb)),
                                         __builtin_amdgcn_exp2f(fmaf(sv[2 * hh + 1], c2, -mb)));
-            lsum += __uint_as_float(w[2 * u + hh] << 16) + __uint_as_float(w[2 * u + hh] & 0xffff0000u);
           }
         pb[t][cp] = __builtin_bit_cast(bf16x8, (u32x4{w[0], w[1], w[2], w[3]}));
       }
-      l_run[t] = l_run[t] * alpha + lsum;
       m_run[t] = mx;
-      if (__any(alpha != 1.0f))
+      if (__any(alpha != 1.0f)) {
+        lt[t] *= alpha;
 #pragma unroll
         for (int d = 0; d < DT; ++d) o[t][d] *= alpha;
+      }
     }
     // ---- O^T[d][q] += V^T . P^T: each V^T fragment feeds both query tiles
     const uint16_t* vt16 = reinterpret_cast<const uint16_t*>(vt[buf]);
 #pragma unroll
-    for (int cp = 0; cp < NKT / 2; ++cp)
+    for (int cp = 0; cp < NKT / 2; ++cp) {
 #pragma unroll
       for (int d = 0; d < DT; ++d) {
         const uint16_t* vr = vt16 + (d * 16 + (lane & 15)) * kPfVRow + 32 * cp + (lane >> 4) * 4;
@@ -1352,6 +1361,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int t = 0; t < TPW; ++t) o[t][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[t][cp], o[t][d], 0, 0, 0);
       }
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) lt[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[t][cp], lt[t], 0, 0, 0);
+    }
   };
 
   if (nb > 0) {
@@ -1379,9 +1391,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // ---- the output: o / l, 4 consecutive dims per lane and d tile
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
-    float l = l_run[t];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    const float l = lt[t][0];
     const int rq = wr0 + t * 16 + (lane & 15);
     if (rq >= a.R) continue;
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
@@ -1465,8 +1475,8 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
     a.part_o = nullptr;
     a.part_ml = nullptr;
     const dim3 pgrid((unsigned)(a.B * a.nkv), (unsigned)ceil_div(a.R, kPfRows));
-    if (a.kv_dtype == DSK_KV_U8) hipLaunchKernelGGL(attention_prefill_kernel<DSK_KV_U8>, pgrid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(attention_prefill_kernel<DSK_KV_BF16>, pgrid, dim3(256), 0, st, a);
+    if (a.kv_dtype == DSK_KV_U8) hipLaunchKernelGGL(attention_prefill_kernel<DSK_KV_U8>, pgrid, dim3(kPfThreads), 0, st, a);
+    else hipLaunchKernelGGL(attention_prefill_kernel<DSK_KV_BF16>, pgrid, dim3(kPfThreads), 0, st, a);
     DSK_LAUNCH_CHECK(who);
     return DSK_OK;
   }
