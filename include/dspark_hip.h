@@ -254,9 +254,11 @@ int dsk_qkv_norm_rope_append(const void* qkv, int qkv_splits, int B, int W, int 
  * kept between calls). Every block_table entry of a row must name a valid page: a split
  * reads its whole key range through the table before it knows the row's length.
  * head_dim 128 or 256, or 512 (the gemma4 drafter's global head) without the fused entry.
- * W > 64 (a prefill's many queries): each workgroup takes one group of 4 query tiles over a split
- * of 1024 keys, and a causal split past every query of a group is skipped (each row's combine
- * reads the splits up to its own position). */
+ * W > 64 (a prefill's many queries), head_dim 128, no softcap, unpacked output and at most
+ * 1024 pages per row: one workgroup per 256 query rows of a (row, kv head) streams that block's
+ * whole key range, with no splits, no combine and no workspace use. Other many-query passes take
+ * groups of 4 query tiles over splits of 1024 keys, a causal split past every query of a group
+ * skipped (each row's combine reads the splits up to its own position). */
 size_t dsk_attn_ws_bytes(int B, int W, int nq, int hd, int max_ctx);
 int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, int hd, float scale,
                   int causal, int window, float softcap, const int32_t* seq_lens,
