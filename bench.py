@@ -23,6 +23,11 @@ replay each. Printed (one JSON line):
   acc_us       the standalone acceptance workload [4, 17, 151936] fp32 (T = 1, top-p 0.95),
                graph-replayed, with its HBM roofline fraction
   q06          the Qwen3-0.6B-shaped workload end to end (DSpark block 8, 256 new tokens)
+  config_verify  the verify step alone of the other configurations, each against its own
+               roofline: Q06 (0.6B shape, 9 rows, 768 context), G12 (Gemma-style 12B shape, 9
+               rows, 8192 context, sliding layers reading their 1024-token window) and CB (8B
+               shape, 4 rows of 9 over contexts 1024 / 3072 / 6144 / 12288); bf16 KV holding
+               seeded random values (timing only), one graph replayed 30 times
   cpu_baseline the CPU oracle (torch, float32 with bf16 rounding points) on the host cores:
                value = accepted tok/s of 5 whole DFlash rounds on the same weights (random
                4096-position context); q06 = the Q06 workload end to end on the same prompt;
@@ -312,6 +317,61 @@ def q06_teacher_forced(target, prompt, tokens) -> dict:
     return {"oracle_argmax": int((gap == 0).sum()), "of": len(tokens), "max_gap": round(float(gap.max()), 4)}
 
 
+# The other BASELINE configurations' verify steps, timed alone: (name, synthetic shape, context
+# per batch row, rows per batch row, the 70 %-of-roofline bound BASELINE states in us)
+CONFIG_LEGS = [
+    ("Q06", "qwen3-0.6b", [768], 9, 129.0),
+    ("G12", "gemma-12b", [8192], 9, 2388.0),
+    ("CB", "qwen3-8b", [1024, 3072, 6144, 12288], 9, 2029.0),
+]
+
+
+def verify_leg(shape: str, lens: list, W: int, reps: int = 30) -> dict:
+    """One graph-replayed verify forward of `shape` (B = len(lens) rows of W new tokens each over
+    contexts `lens`, bf16 KV holding seeded N(0, 1) values: a timing-only context, no prefill),
+    HIP events around `reps` replays. Algorithmic bytes: the W8 weights, each layer's visible K/V
+    of every row (a sliding layer at most its window), the new rows' K/V writes and the fp32
+    logits."""
+    import torch
+
+    from mlx_dspark import synthetic
+
+    model = synthetic.build_target(shape, seed=0)
+    a = model.args
+    B = len(lens)
+    cache = model.make_cache(B=B, max_ctx=max(lens) + W + 64)
+    g = torch.Generator(device=model.device).manual_seed(5)
+    for l in range(a.num_hidden_layers):
+        cache.k[l].normal_(generator=g)
+        cache.v[l].normal_(generator=g)
+    cache.set_lengths(lens)
+    ids = torch.randint(0, a.vocab_size, (B, W), dtype=torch.int32, device=model.device, generator=g)
+    model.forward(ids, cache, None, advance=False)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        model.forward(ids, cache, None, advance=False)
+    for _ in range(3):
+        graph.replay()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s_ev.record()
+    for _ in range(reps):
+        graph.replay()
+    e_ev.record()
+    torch.cuda.synchronize()
+    us = s_ev.elapsed_time(e_ev) * 1e3 / reps
+    per_tok = 2 * a.num_key_value_heads * a.head_dim * 2          # K and V, bf16, one layer
+    kv_read = sum(min(L + W, a.window(l) or (L + W)) * per_tok for l in range(a.num_hidden_layers) for L in lens)
+    kv_write = B * W * per_tok * a.num_hidden_layers
+    alg = model.weight_bytes + kv_read + kv_write + B * W * a.vocab_size * 4
+    out = {"verify_us": round(us, 1), "alg_bytes": int(alg),
+           "roofline_frac": round(alg / (us * 1e-6) / (PEAK_HBM_GBS * 1e9), 4),
+           "rows": B * W, "contexts": lens, "kv": "bf16 (seeded random values)"}
+    del graph, cache, model
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_acc(gpu_out=None, reps: int = 3) -> dict:
     """The acceptance oracle (C, one thread) on the standalone acceptance workload: median of
     ``reps`` runs; outputs compared with the GPU's on the same inputs and Philox (seed, offset)."""
@@ -338,6 +398,10 @@ def main(argv=None) -> int:
     ap.add_argument("--kv-bits", type=int, default=8, choices=[0, 8])
     ap.add_argument("--target", default="qwen3-8b")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-config-legs", action="store_true",
+                    help="skip the Q06 / G12 / CB verify-step timings")
+    ap.add_argument("--legs-only", action="store_true",
+                    help="only the Q06 / G12 / CB verify-step timings (one JSON line)")
     ap.add_argument("--verify-reps", type=int, default=50)
     ap.add_argument("--roofline-only", action="store_true",
                     help="build the target, time the W8 GEMM shapes and a 256 MiB copy only (counter runs)")
@@ -364,6 +428,14 @@ def main(argv=None) -> int:
     torch.cuda.init()
     if args.acc_only:
         print(json.dumps({"acc": acc_timing()}), flush=True)
+        return 0
+    if args.legs_only:
+        legs = {}
+        for name, shape, lens, w, bound in CONFIG_LEGS:
+            legs[name] = verify_leg(shape, lens, w)
+            legs[name]["baseline_bound_us"] = bound
+            log(f"{name} verify: {legs[name]['verify_us']} us, {legs[name]['roofline_frac'] * 100:.1f}% of roofline")
+        print(json.dumps({"config_verify": legs}), flush=True)
         return 0
     t_build = time.time()
     keep = not args.no_cpu_baseline            # the oracle reads the MLX-layout codes
@@ -514,6 +586,18 @@ def main(argv=None) -> int:
         cpu["acc"] = cpu_acc({"n": acc["n"], "token": acc["token"]})
         log(f"cpu baseline, acceptance in {time.time() - t0:.1f} s: {cpu['acc']}")
 
+    legs = {}
+    if not args.no_config_legs:
+        for name, shape, lens, w, bound in CONFIG_LEGS:
+            try:
+                legs[name] = verify_leg(shape, lens, w)
+                legs[name]["baseline_bound_us"] = bound
+                log(f"{name} verify ({shape}, rows {len(lens)}x{w}, contexts {lens}): {legs[name]['verify_us']} us, "
+                    f"{legs[name]['roofline_frac'] * 100:.1f}% of HBM roofline (BASELINE's 70% bound {bound} us)")
+            except Exception as e:                      # a leg never takes the headline line down
+                legs[name] = {"error": f"{type(e).__name__}: {e}"}
+                log(f"{name} verify leg failed: {legs[name]['error']}")
+
     line = {
         "metric": "accepted tok/s (B=1, Qwen3-8B-shape W8, k=16); verify-step us; % HBM roofline",
         "value": round(tok_s, 2), "unit": "accepted tok/s", "n_gpus": 1, "steps": args.steps,
@@ -545,6 +629,7 @@ def main(argv=None) -> int:
         "q06": {"tok_s": q06["tok_s"], "accept_len": q06["accept_len"],
                 "config": "qwen3-0.6b-shape W8 + 1-layer DSpark (taps 1, 14, 27), prompt 512, block 8, greedy, "
                           "256 new tokens, bf16 KV"},
+        "config_verify": legs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
