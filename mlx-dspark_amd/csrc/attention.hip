@@ -391,6 +391,13 @@ __global__ __launch_bounds__(256 * WPT) __attribute__((amdgpu_waves_per_eu(1, 2)
       if (j_beg > off + last_row / a.G) return;
     }
     j_end = min(kend, j_beg + kps);
+    // sliding window: a split wholly before the window of this workgroup's first row is never
+    // read (every later row's window starts later; the combine starts each row at the first
+    // split its window reaches)
+    if (causal && window > 0) {
+      const int first_row = gridDim.y > 1 ? (int)blockIdx.y * 4 * 16 : 0;
+      if (j_end <= off + first_row / a.G - window + 1) return;
+    }
   }
   const int nb = newsplit ? 1 : (j_end - j_beg + KEYS - 1) / KEYS;
   if (!newsplit) {
@@ -669,6 +676,9 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   const int ns = a.fused ? min((min(a.seq_lens[b], jmax) + a.kps - 1) / a.kps, a.nsplit - 1) + 1
                          : min(a.nsplit, (min(visible, jmax) + a.kps - 1) / a.kps);
   const int nlast = a.fused ? a.nsplit - 1 - (ns - 1) : 0;  // split index shift of the last live one
+  // a sliding-window row starts at the split holding its window's first key (the attention
+  // kernel skips the splits before every window of a workgroup)
+  const int s_beg = a.causal && !a.fused && a.window > 0 ? max(0, visible - a.window) / a.kps : 0;
   const uint16_t* base_o = a.part_o + ((size_t)bk * a.nsplit * a.R + r) * HD + lane * PER;
   const float* base_ml = a.part_ml + ((size_t)bk * a.nsplit * a.R + r) * 2;
   const size_t so = (size_t)a.R * HD, sml = (size_t)a.R * 2;
@@ -678,7 +688,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   float M = -__builtin_inff(), den = 0.0f;
   // rounds of RS splits: the (m, l) and partial-output loads of a round are issued together
   constexpr int RS = PER == 2 ? 64 : (PER == 4 ? 32 : 16);
-  for (int s0 = 0; s0 < ns; s0 += RS) {
+  for (int s0 = s_beg; s0 < ns; s0 += RS) {
     const int n = min(RS, ns - s0);
     float m = -__builtin_inff(), l = 0.0f;
     if (lane < n) {
@@ -741,12 +751,12 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
 
 // ----------------------------------------------------------------------------- verify (head_dim 128)
 // A verify pass (at most 64 query rows per kv head, head_dim 128, keys already in the pool): one
-// workgroup of 8 waves per (row b, kv head, split of 256 keys). Wave w owns the split's 32-key
-// block w: it loads the block's K/V rows straight from the pool into registers, dequantises each
-// element once (K row-major for the score MFMA, V transposed for the P.V MFMA), then runs the kv
-// head's query tiles (staged once in LDS) over its 32 keys, two tiles at a time. Per tile pair the
-// eight waves' (m, l, o) meet in LDS and wave w merges d tile w of both tiles into the split's
-// partial (or the output when there is one split).
+// workgroup of 4 waves per (row b, kv head, split of 256 keys). Wave w owns the split's keys
+// [64 w, 64 w + 64) (four 16-key tiles): it loads their K/V rows straight from the pool into
+// registers, dequantises each element once (K row-major for the score MFMA, V transposed for the
+// P.V MFMA), then runs every query tile of the kv head (staged once in LDS) over its 64 keys, the
+// tiles interleaved. The four waves' (o, m, l) meet in LDS and wave w merges query tile w into the
+// split's partial (or the output when there is one split).
 //  - head_dim order: lane group a = lane / 16 holds dims [32 a, 32 a + 32) of its key row (one
 //    contiguous 32-byte (8-bit) or 64-byte (bf16) load, inside one quantization group), so k-step
 //    s of the score MFMA takes dims 32 a + 8 s .. + 7 from both K (A operand: lane = key) and Q
@@ -758,7 +768,8 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
 //    registers straight into the P.V MFMA.
 //  - O^T[dim index][q]: lane (a, q) ends with physical dims 32 a + 4 dt + r.
 // Masks, the softmax (probabilities rounded to bf16) and the partial layout are the attention
-// kernel's, so attention_combine_kernel merges the splits.
+// kernel's; attention_verify_combine_kernel merges the splits (a split past a row's keys writes
+// m = -inf, which the merge skips).
 constexpr int kVerifyBlock = 32;   // keys per page-aligned block (the page size is a multiple)
 constexpr int kVerifyWaves = 4;
 constexpr int kVerifyKeys = 256;   // keys per split: 64 per wave

@@ -164,6 +164,53 @@ def test_many_query_attention_masks_and_rows(dev, kv_bits, lens, W, nq, nkv, cau
     assert worst < 2e-2, worst
 
 
+@pytest.mark.parametrize("kv_bits,lens,W,hd,window", [
+    (8, [3000], 9, 256, 1024),          # split kernel, head_dim 256: splits before the window skipped
+    (None, [2000, 300], 100, 256, 700), # its many-query form (query-tile groups on the grid)
+    (8, [3000, 40], 16, 128, 512),      # the verify kernel with a window
+])
+def test_sliding_window_attention_over_long_context(dev, kv_bits, lens, W, hd, window):
+    """Causal sliding-window attention where most of a row's context lies before its window:
+    the output against a float32 softmax over the window's keys."""
+    from mlx_dspark import ops
+    from mlx_dspark.kv import PagedKVCache
+    print(f"window attention kv_bits={kv_bits} lens={lens} W={W} hd={hd} window={window}", flush=True)
+    nq, nkv, B = 4, 2, len(lens)
+    cache = PagedKVCache(1, B, nkv, hd, max(lens) + W + 64, kv_bits=kv_bits, spare_pages=3)
+    g = torch.Generator().manual_seed(sum(lens) + hd + window)
+    perm = torch.randperm(cache.n_pages, generator=g)[: B * cache.max_pages]
+    cache.block_table.copy_(perm.view(B, cache.max_pages).to(torch.int32))
+    if kv_bits is None:
+        for pool in (cache.k[0], cache.v[0]):
+            pool.copy_(torch.randn(pool.shape, generator=g).to(torch.bfloat16))
+    else:
+        for pool, sb in ((cache.k[0], cache.k_sb[0]), (cache.v[0], cache.v_sb[0])):
+            pool.copy_(torch.randint(0, 256, pool.shape, generator=g, dtype=torch.uint8))
+            sc = (0.01 + 0.02 * torch.rand(sb.shape, generator=g)).to(torch.bfloat16).view(torch.int16)
+            bi = (-2.0 + torch.rand(sb.shape, generator=g)).to(torch.bfloat16).view(torch.int16)
+            sb.copy_((sc.int() & 0xFFFF) | (bi.int() << 16))
+    cache.set_lengths(lens)
+    q = torch.randn(B * W, nq * hd, generator=g).to(torch.bfloat16).to(dev)
+    out = ops.attention(q, B, W, nq, nkv, hd, hd ** -0.5, cache.seq_lens, cache.max_ctx, cache.block_table,
+                        cache.page, cache.kv_dtype, *cache.layer_args(0), causal=True, window=window)
+    torch.cuda.synchronize()
+    got = out.float().cpu().view(B, W, nq, hd)
+    G = nq // nkv
+    worst = 0.0
+    for b, L0 in enumerate(lens):
+        n = L0 + W
+        K, V = _row_pool_rows(cache, b, n, "k"), _row_pool_rows(cache, b, n, "v")
+        pos = torch.arange(L0, L0 + W)[:, None]
+        j = torch.arange(n)[None, :]
+        allowed = (j <= pos) & (j > pos - window)
+        qf = q.float().cpu().view(B, W, nq, hd)[b]
+        for h in range(nq):
+            sc = ((qf[:, h] @ K[:, h // G].T) * hd ** -0.5).masked_fill(~allowed, float("-inf"))
+            ref = torch.softmax(sc, -1) @ V[:, h // G]
+            worst = max(worst, float((got[b, :, h] - ref).abs().max() / ref.abs().max()))
+    assert worst < 2e-2, worst
+
+
 def _row_pool_rows(cache, b, n, which):
     """[n, nkv, hd] float values of row b's tokens 0..n-1 (dequantized as the kernels do)."""
     page = cache.page
