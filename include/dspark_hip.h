@@ -157,6 +157,20 @@ int dsk_w8_gemm_rn(const uint16_t* x, const uint8_t* wt, const uint32_t* sb, int
                    uint16_t* copy, int64_t ldc, const uint16_t* next_norm_w, float* ssq_out,
                    dsk_stream_t stream);
 
+/* Tuning entry, with no counterpart in the reference: dsk_w8_gemm_rn with an explicit plan instead
+ * of the library's own, for plan sweeps (the planner's rules were fitted from such sweeps):
+ * slab_tiles 16-row weight tiles per workgroup (dividing N / 16; even for the gated epilogues),
+ * batch_groups 2 or 4 groups of 64 along K per load batch, waves 4 / 8 / 16, k_splits K splits
+ * (DSK_EPI_PARTIAL only: y then holds k_splits slices [M][N]), pipelined loads (1) or not (0).
+ * A plan with no compiled kernel, or whose cross-wave reduction exceeds 64 KB of LDS, is
+ * rejected with DSK_EINVAL. */
+int dsk_w8_gemm_rn_planned(const uint16_t* x, const uint8_t* wt, const uint32_t* sb, int bits, int M,
+                           int64_t N, int64_t K, int epi, void* y, int y_dtype, int64_t ldy,
+                           float softcap, const float* x_ssq, int x_tiles, float eps, uint16_t* h,
+                           int64_t ldh, uint16_t* copy, int64_t ldc, const uint16_t* next_norm_w,
+                           float* ssq_out, int slab_tiles, int batch_groups, int waves, int k_splits,
+                           int pipelined, dsk_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------
  * Dense prefill (src/mlx_dspark/generate.py:613-656, _prefill_tapped: the prompt in chunks of
  * PREFILL_CHUNK = 2048 rows through the target). A long prompt runs layer by layer over all of

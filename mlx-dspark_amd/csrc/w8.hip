@@ -732,10 +732,13 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi, int bits = 8) {
     // one tile per workgroup and up to 16 waves splitting K (reduced through LDS)
     p.nt = 1;
     p.sk = 1;
-    p.u = (MT == 1 && G / 4 >= 16 && G % 4 == 0) ? 4 : 2;
+    p.u = ((MT == 1 || MT == 3) && G / 4 >= 16 && G % 4 == 0) ? 4 : 2;
     p.gpb = G;
     const int64_t nb = G / p.u;
     p.waves = nb >= 16 ? 16 : (nb >= 8 ? 8 : 4);
+    // more than one row tile (a sweep at M = 24, 36, 64 over o 4096x4096 and down 4096x12288):
+    // 8 waves of 2-group batches at two and four tiles, 16 waves of 4-group batches at three
+    if ((MT == 2 || MT == 4) && p.waves > 8) p.waves = 8;
     while ((size_t)p.waves * MT * 1024 > 65536) p.waves /= 2;
     p.pf = false;  // pipelined loads measured slower here (down 4096x12288: 18.5 -> 23.2 us)
     return p;
@@ -769,6 +772,28 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi, int bits = 8) {
     p.waves = 8;
     p.pf = true;
   }
+  // more than one row tile, from a sweep at M = 24, 36 and 64 over the Qwen3-8B verify shapes
+  // (the 16-row rules above stay as fitted): the activation rows read per weight byte grow with
+  // M, and the plans that won keep whole K ranges and wide slabs. Partial sums: pairs of tiles,
+  // no K split, 16 waves at two tiles, 8 above (qkv 6144x4096 at M = 36: 27.2 -> 17.6 us); gated:
+  // 8 waves at four tiles (gate_up 24576x4096 at M = 64: 72.1 -> 63.6 us); plain stores (the
+  // logits): slabs of 4 tiles at two and three (head 151936x4096 at M = 36: 223.5 -> 192.4 us).
+  if (MT >= 2 && bits == 8) {
+    if (partial) {
+      p.nt = tiles % 2 == 0 ? 2 : 1;
+      p.sk = 1;
+      p.u = 2;
+      p.gpb = G;
+      p.waves = MT == 2 ? 16 : 8;
+    } else if (gated) {
+      p.waves = MT >= 4 ? 8 : p.waves;
+    } else if (MT <= 3 && tiles % 4 == 0) {
+      p.nt = 4;
+      p.u = 2;
+      p.gpb = G;
+      p.waves = 4;
+    }
+  }
   while ((size_t)p.waves * MT * p.nt * 1024 > 65536) p.waves /= 2;  // LDS of the reduction
   // 4-bit codes: a wave's load of one tile-group is 512 B, half the 8-bit one. Where the waves
   // of the plan above each run several unpipelined batches (4 waves: down, the head), batches
@@ -790,7 +815,7 @@ static bool launch_gemm_t(const GemmArgs& a, hipStream_t st) {
     if (rs) hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 6, PF, BITS>), grid, blk, 0, st, a);
     else hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 2, PF, BITS>), grid, blk, 0, st, a);
   } else if (a.epi == DSK_EPI_RESIDUAL) {
-    if constexpr (NT != 1) return false;
+    if constexpr (NT > 2) return false;
     else if (rs) return false;  // the residual products' x (attention output, gated MLP) is never normed later
     else hipLaunchKernelGGL((w8_gemm_kernel<MT, NT, U, WAVES, 3, PF, BITS>), grid, blk, 0, st, a);
   } else if (a.epi == DSK_EPI_STORE) {
@@ -831,7 +856,7 @@ static bool launch_gemm_bits(const GemmArgs& a, int MT, const GemmPlan& p, hipSt
   DSK_GEMM_CASE(1, 3, 2) DSK_GEMM_CASE(1, 6, 2)
   DSK_GEMM_CASE(1, 1, 4) DSK_GEMM_CASE(1, 2, 4) DSK_GEMM_CASE(1, 4, 4)
   DSK_GEMM_CASE(2, 1, 2) DSK_GEMM_CASE(2, 2, 2) DSK_GEMM_CASE(2, 4, 2)
-  DSK_GEMM_CASE(3, 1, 2) DSK_GEMM_CASE(3, 2, 2)
+  DSK_GEMM_CASE(3, 1, 2) DSK_GEMM_CASE(3, 2, 2) DSK_GEMM_CASE(3, 4, 2) DSK_GEMM_CASE(3, 1, 4)
   DSK_GEMM_CASE(4, 1, 2) DSK_GEMM_CASE(4, 2, 2)
 #undef DSK_GEMM_CASE
   return false;
@@ -1034,7 +1059,8 @@ struct NormIO {
 
 static int gemm_entry(const char* who, int bits, const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int M,
                       int64_t N, int64_t K, int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
-                      int64_t ldr, float softcap, hipStream_t st, const NormIO* nio = nullptr);
+                      int64_t ldr, float softcap, hipStream_t st, const NormIO* nio = nullptr,
+                      const GemmPlan* forced = nullptr);
 
 extern "C" int dsk_w8_gemm(const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int M, int64_t N, int64_t K,
                            int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual, int64_t ldr,
@@ -1063,9 +1089,42 @@ extern "C" int dsk_w8_gemm_rn(const uint16_t* xp, const uint8_t* wt, const uint3
                     as_stream(stream), &nio);
 }
 
+extern "C" int dsk_w8_gemm_rn_planned(const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int bits, int M,
+                                      int64_t N, int64_t K, int epi, void* y, int y_dtype, int64_t ldy, float softcap,
+                                      const float* x_ssq, int x_tiles, float eps, uint16_t* h, int64_t ldh,
+                                      uint16_t* copy, int64_t ldc, const uint16_t* next_norm_w, float* ssq_out,
+                                      int slab_tiles, int batch_groups, int waves, int k_splits, int pipelined,
+                                      dsk_stream_t stream) {
+  const char* who = "dsk_w8_gemm_rn_planned";
+  DSK_REQUIRE(bits == 8 || bits == 4, "%s: bits=%d (8 or 4)", who, bits);
+  DSK_REQUIRE(!x_ssq || (x_tiles == K / 16 && eps >= 0.0f), "%s: the row scale of x needs K / 16 tile partials",
+              who);
+  const int64_t G = K / 64, tiles = N / 16;
+  const int MT = (M + 15) / 16;
+  DSK_REQUIRE(slab_tiles >= 1 && slab_tiles <= 8 && N % 16 == 0 && tiles % slab_tiles == 0,
+              "%s: %d tiles per slab do not divide N / 16 = %lld", who, slab_tiles, (long long)tiles);
+  DSK_REQUIRE((batch_groups == 2 || batch_groups == 4) && K % 64 == 0 && G % batch_groups == 0,
+              "%s: batches of %d groups", who, batch_groups);
+  DSK_REQUIRE(waves == 4 || waves == 8 || waves == 16, "%s: %d waves", who, waves);
+  DSK_REQUIRE(k_splits >= 1 && (k_splits == 1 || epi == DSK_EPI_PARTIAL) && k_splits <= G / batch_groups,
+              "%s: %d K splits (partial sums only, at most one batch each)", who, k_splits);
+  DSK_REQUIRE((size_t)waves * MT * slab_tiles * 1024 <= 65536, "%s: the cross-wave reduction exceeds 64 KB of LDS",
+              who);
+  GemmPlan p;
+  p.nt = slab_tiles;
+  p.u = batch_groups;
+  p.waves = waves;
+  p.sk = k_splits;
+  p.gpb = ((G / batch_groups + k_splits - 1) / k_splits) * batch_groups;
+  p.pf = pipelined != 0;
+  NormIO nio{x_ssq, x_ssq ? x_tiles : 0, eps, h, ldh, copy, ldc, next_norm_w, ssq_out};
+  return gemm_entry(who, bits, xp, wt, sb, M, N, K, epi, y, y_dtype, ldy, nullptr, 0, softcap, as_stream(stream),
+                    &nio, &p);
+}
+
 static int gemm_entry(const char* who, int bits, const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int M,
                       int64_t N, int64_t K, int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
-                      int64_t ldr, float softcap, hipStream_t st, const NormIO* nio) {
+                      int64_t ldr, float softcap, hipStream_t st, const NormIO* nio, const GemmPlan* forced) {
   DSK_REQUIRE(xp && wt && sb && (y || epi == DSK_EPI_RESIDUAL), "dsk_w8_gemm: null pointer");
   DSK_REQUIRE(M > 0 && M <= 64, "dsk_w8_gemm: M=%d outside [1, 64]", M);
   DSK_REQUIRE(N > 0 && N % 16 == 0 && K > 0 && K % 256 == 0,
@@ -1093,7 +1152,8 @@ static int gemm_entry(const char* who, int bits, const uint16_t* xp, const uint8
                 "dsk_w8_gemm: gated epilogue needs N %% 256 == 0 and a bf16 (packed) output");
     DSK_REQUIRE(gated || y_dtype == DSK_F32, "dsk_w8_gemm: partial sums are f32");
   }
-  const GemmPlan p = plan_gemm(M, N, K, epi, bits);
+  const GemmPlan p = forced ? *forced : plan_gemm(M, N, K, epi, bits);
+  DSK_REQUIRE(!(gated && p.nt % 2), "%s: gated tiles come in gate|up pairs (slab of %d tiles)", who, p.nt);
   GemmArgs a;
   gemm_prepare(a, p, xp, wt, sb, M, N, K, epi, y, y_dtype, ldy, residual, ldr, softcap);
   a.bits = bits;
