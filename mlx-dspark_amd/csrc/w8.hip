@@ -764,7 +764,9 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi, int bits = 8) {
   p.waves = (bps >= 8 && bps < 12) ? 8 : 4;
   if (!partial && slabs < 128) p.waves = bps >= 32 ? 16 : (bps >= 8 ? 8 : 4);
   p.pf = false;
-  // wide gated projections (>= 1024 tiles): pairs of tiles, 8 waves, pipelined loads
+  // wide gated projections (>= 1024 tiles): pairs of tiles, 8 waves, pipelined loads (4-group
+  // batches won a standalone sweep at M = 16 but not the verify forward, and slowed the Gemma-style
+  // GeGLU projection)
   if (gated && MT == 1 && tiles >= 1024 && tiles % 2 == 0) {
     p.nt = 2;
     p.sk = 1;
@@ -772,6 +774,18 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi, int bits = 8) {
     p.waves = 8;
     p.pf = true;
   }
+  // one row tile, a sweep at M = 16 over the Qwen3-8B verify shapes: wide partial sums with a long K (qkv 6144x4096) run whole K
+  // ranges in pairs of tiles, 16 waves, pipelined loads (8.7 us against 10.5 for 4 K splits of
+  // 8 waves); wide plain stores (the logits, 151936x4096) 8 waves (110.4 against 117.9 us)
+  if (MT == 1 && bits == 8 && partial && G >= 64 && tiles >= 384 && tiles % 2 == 0) {
+    p.nt = 2;
+    p.sk = 1;
+    p.u = 2;
+    p.gpb = G;
+    p.waves = 16;
+    p.pf = true;
+  }
+  if (MT == 1 && bits == 8 && epi == DSK_EPI_STORE && tiles >= 4096 && G >= 64 && p.nt == 4) p.waves = 8;
   // more than one row tile, from a sweep at M = 24, 36 and 64 over the Qwen3-8B verify shapes
   // (the 16-row rules above stay as fitted): the activation rows read per weight byte grow with
   // M, and the plans that won keep whole K ranges and wide slabs. Partial sums: pairs of tiles,
