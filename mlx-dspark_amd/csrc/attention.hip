@@ -817,7 +817,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 
 template <int KVT, bool SOFTCAP, int QT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void attention_verify_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void attention_verify_kernel(AttnArgs a) {
   constexpr int HD = 128, QROW = HD + 8;
   constexpr int NW = kVerifyWaves, KB = kVerifyKeys / NW / 16;  // waves, 16-key tiles per wave
   __shared__ f32x4 mo[QT][NW][8][64];                // every tile's (o) per [tile][wave][d tile][lane]
@@ -841,7 +841,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   if (j_beg >= j_lim) {
     // past every row's keys: an empty partial (m = -inf) for the combine, which reads every split
     if (a.nsplit > 1)
-      for (int r = threadIdx.x; r < a.R; r += 256)
+      for (int r = threadIdx.x; r < a.R; r += NW * 64)
         *reinterpret_cast<float2*>(a.part_ml + (((size_t)bk * a.nsplit + split) * a.R + r) * 2) =
             float2{-__builtin_inff(), 0.0f};
     return;
@@ -863,8 +863,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
   }
 #pragma unroll
-  for (int u = 0; u < QT * 16 * 16 / 256; ++u) {
-    const int c = threadIdx.x + 256 * u;  // rows x 16 chunks of 8 dims
+  for (int u = 0; u < QT * 16 * 16 / (NW * 64); ++u) {
+    const int c = threadIdx.x + NW * 64 * u;  // rows x 16 chunks of 8 dims
     const int r = c >> 4, ch = c & 15;
     u32x4 qv = u32x4{0, 0, 0, 0};
     if (r < a.R)
@@ -1516,10 +1516,10 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
     const dim3 vgrid((unsigned)(a.B * a.nkv * a.nsplit));
 #define DSK_VERIFY_QT(kvt, scv)                                                                           \
   switch (tiles) {                                                                                        \
-    case 1: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 1>), vgrid, dim3(256), 0, st, a); break; \
-    case 2: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 2>), vgrid, dim3(256), 0, st, a); break; \
-    case 3: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 3>), vgrid, dim3(256), 0, st, a); break; \
-    default: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 4>), vgrid, dim3(256), 0, st, a); break; \
+    case 1: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 1>), vgrid, dim3(kVerifyWaves * 64), 0, st, a); break; \
+    case 2: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 2>), vgrid, dim3(kVerifyWaves * 64), 0, st, a); break; \
+    case 3: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 3>), vgrid, dim3(kVerifyWaves * 64), 0, st, a); break; \
+    default: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 4>), vgrid, dim3(kVerifyWaves * 64), 0, st, a); break; \
   }
     if (a.kv_dtype == DSK_KV_U8) {
       if (sc) { DSK_VERIFY_QT(DSK_KV_U8, true) } else { DSK_VERIFY_QT(DSK_KV_U8, false) }
