@@ -284,7 +284,8 @@ int dsk_attention(const uint16_t* q, int B, int W, int nq, int nkv, int hd, floa
 /* dsk_qkv_rope_append (pos_offset 0) for a projection whose input was normed later
  * (dsk_w8_gemm_rn): the summed split-K partials of row m are multiplied by
  * r_m = rsqrt(sum_t x_ssq[m][t] / (16 x_tiles) + x_eps) before they are rounded to bf16, q/k
- * normed and roped (the input RMSNorm of the Qwen3 layer, applied after q/k/v_proj). */
+ * normed and roped (the input RMSNorm of the Qwen3 layer, applied after q/k/v_proj);
+ * qkv_splits >= 1 (f32 slices). */
 int dsk_qkv_rope_append_rn(const void* qkv, int qkv_splits, int B, int W, int nq, int nkv, int hd,
                            const uint16_t* q_norm, const uint16_t* k_norm, float eps,
                            const float* inv_freq, const int32_t* seq_lens, const int32_t* block_table,

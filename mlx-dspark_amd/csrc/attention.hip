@@ -29,7 +29,14 @@ namespace dsk {
 
 // ----------------------------------------------------------------------------- append
 // One wave per (token row, head): lane holds dims [PER*lane, PER*lane + PER) (PER = HD/64).
-template <int HD, bool RS>
+// F32: the projection arrives as qkv_splits f32 split-K slices (else one bf16 row); RS: their sum
+// takes the row scale of a normed-later projection input. Every independent load is issued
+// first, with no branch between them (a value that is not needed reads a valid address and is
+// discarded): the first two slices, the first 256 tile partials of the input's x^2, the norm gains
+// and RoPE frequencies, and, once the row length is in, a K/V row's page id. The slices are summed
+// as load_proj_row sums them; the row scale is the W8 GEMM's (rsqrt(sum / 16 x_tiles + x_eps),
+// the partials summed in the same order).
+template <int HD, bool RS, bool F32>
 __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
     const void* __restrict__ qkv, int qkv_splits, int B, int W, int nq, int nkv, const uint16_t* __restrict__ q_norm,
     const uint16_t* __restrict__ k_norm, const uint16_t* __restrict__ v_norm, float eps,
@@ -37,6 +44,7 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
     const int32_t* __restrict__ block_table, int max_pages, int page, int kv_dtype, void* __restrict__ k_pool,
     void* __restrict__ v_pool, uint32_t* __restrict__ k_sb, uint32_t* __restrict__ v_sb,
     uint16_t* __restrict__ q_out, const float* __restrict__ x_ssq, int x_tiles, float x_k, float x_eps) {
+  static_assert(F32 || !RS, "the row scale applies to split-K slices");
   constexpr int PER = HD / 64;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int nheads = nq + 2 * nkv;
@@ -44,28 +52,93 @@ __global__ __launch_bounds__(256) void qkv_rope_append_kernel(
   const int row = task / nheads, head = task % nheads;
   if (row >= B * W) return;
   const int b = row / W, i = row % W;
-  const int pos = seq_lens[b] + i + pos_offset;
-  // row scale of a normed-later projection input: the tile partials of the row summed l, l + 64,
-  // ... per lane, then across the wave (the GEMM's own order)
-  float v[PER];
-  if constexpr (RS) {
-    const float rs = proj_row_scale(x_ssq, x_tiles, row, lane, x_k, x_eps);
-    load_proj_row<PER>(qkv, qkv_splits, (int64_t)B * W * nheads * HD, ((int64_t)row * nheads + head) * HD, lane, v,
-                       rs);
-  } else {
-    load_proj_row<PER>(qkv, qkv_splits, (int64_t)B * W * nheads * HD, ((int64_t)row * nheads + head) * HD, lane, v);
-  }
   const bool is_q = head < nq, is_k = !is_q && head < nq + nkv;
-  norm_rope_row<HD, 64>(v, lane, is_q ? q_norm : (is_k ? k_norm : v_norm), eps, is_q || is_k, inv_freq, pos);
+  const uint16_t* nw = is_q ? q_norm : (is_k ? k_norm : v_norm);
+  const bool rope = is_q || is_k;
+  const int pos = seq_lens[b] + i + pos_offset;  // first: the page id load waits for it alone
+
+  const int64_t slice = (int64_t)B * W * nheads * HD, off = ((int64_t)row * nheads + head) * HD + lane * PER;
+  float t[2][PER];
+  if constexpr (F32) {
+    const float* src = reinterpret_cast<const float*>(qkv) + off;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int e = 0; e < PER; ++e) t[u][e] = src[(int64_t)min(u, qkv_splits - 1) * slice + e];
+  } else {
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(qkv) + off;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) t[0][e] = bf16_to_f32(src[e]);
+  }
+  float xs[4];
+  if constexpr (RS) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xs[j] = x_ssq[(int64_t)row * x_tiles + min(lane + 64 * j, x_tiles - 1)];
+  }
+  RowConsts<HD, 64> rc;
+  const uint16_t* wsrc = nw ? nw : reinterpret_cast<const uint16_t*>(inv_freq);  // HD / 2 floats: HD halves
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int d = lane * PER + e;
+    rc.w[e] = bf16_to_f32(wsrc[d]);
+    rc.inv[e] = inv_freq[lane < 32 ? d : d - HD / 2];
+  }
+  const int h = is_k ? head - nq : head - nq - nkv;
+  const bool stored = !is_q && pos >= 0 && pos < max_pages * page;  // beyond the row's block table: dropped
+  const int pg = block_table[stored ? (int64_t)b * max_pages + pos / page : 0];
+
+  float v[PER];
+  if constexpr (F32) {
+    // the slices summed in slice order (two loads in flight at a time past the first two), times
+    // the row scale, rounded to bf16
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      v[e] = 0.0f;
+      v[e] += t[0][e];
+      if (qkv_splits > 1) v[e] += t[1][e];
+    }
+    const float* src = reinterpret_cast<const float*>(qkv) + off;
+    for (int sp = 2; sp < qkv_splits; sp += 2) {
+      float n[2][PER];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < PER; ++e) n[u][e] = sp + u < qkv_splits ? src[(sp + u) * slice + e] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < PER; ++e)
+          if (sp + u < qkv_splits) v[e] += n[u][e];
+    }
+    float scale = 1.0f;
+    if constexpr (RS) {
+      // lane l sums the partials l, l + 64, ... in that order, then the wave sums its lanes
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xs[j] = lane + 64 * j < x_tiles ? xs[j] : 0.0f;
+      float ss = ((xs[0] + xs[1]) + xs[2]) + xs[3];
+      for (int j = lane + 256; j < x_tiles; j += 64) ss += x_ssq[(int64_t)row * x_tiles + j];
+      scale = rsqrtf(wave_sum(ss) / x_k + x_eps);
+    }
+#pragma unroll
+    for (int e = 0; e < PER; ++e) v[e] = round_bf16(v[e] * scale);
+  } else {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) v[e] = t[0][e];
+  }
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    if (!nw) rc.w[e] = 1.0f;
+    if (!rope) rc.inv[e] = 0.0f;
+  }
+  norm_rope_row<HD, 64>(v, lane, rc, nw != nullptr, eps, rope, pos);
   if (is_q) {
     uint16_t* dst = q_out + (int64_t)row * nq * HD + (int64_t)head * HD;
 #pragma unroll
     for (int e = 0; e < PER; ++e) dst[lane * PER + e] = f32_to_bf16(v[e]);
     return;
   }
-  const int h = is_k ? head - nq : head - nq - nkv;
-  if (pos < 0 || pos >= max_pages * page) return;  // beyond the row's block table: dropped
-  const int64_t tok = pool_token(block_table, max_pages, page, nkv, b, h, pos);
+  if (!stored) return;
+  const int64_t tok = ((int64_t)pg * nkv + h) * page + pos % page;
   kv_store_row<HD, 64>(v, lane, kv_dtype, is_k ? k_pool : v_pool, is_k ? k_sb : v_sb, tok);
 }
 
@@ -1603,20 +1676,27 @@ static int qkv_append_entry(const void* qkv, int qkv_splits, int B, int W, int n
   DSK_REQUIRE(B > 0 && W > 0 && nq >= 0 && nkv > 0 && nq % nkv == 0, "dsk_qkv_rope_append: bad shape");
   DSK_REQUIRE(page > 0 && max_pages > 0, "dsk_qkv_rope_append: bad page geometry");
   DSK_REQUIRE(qkv_splits >= 0, "dsk_qkv_rope_append: qkv_splits=%d", qkv_splits);
+  DSK_REQUIRE(!x_ssq || qkv_splits > 0, "dsk_qkv_rope_append_rn: the row scale applies to f32 split-K slices");
   DSK_REQUIRE(kv_dtype == DSK_KV_BF16 || (kv_dtype == DSK_KV_U8 && k_sb && v_sb),
               "dsk_qkv_rope_append: u8 KV needs scale/bias buffers");
   const int tasks = B * W * (nq + 2 * nkv);
   dim3 grid((unsigned)ceil_div(tasks, 4));
-#define DSK_APPEND(HDV)                                                                                             \
-  if (x_ssq)                                                                                                        \
-    hipLaunchKernelGGL((qkv_rope_append_kernel<HDV, true>), grid, dim3(256), 0, as_stream(stream), qkv, qkv_splits, \
-                       B, W, nq, nkv, q_norm, k_norm, v_norm, eps, inv_freq, seq_lens, pos_offset, block_table,     \
-                       max_pages, page, kv_dtype, k_pool, v_pool, k_sb, v_sb, q_out, x_ssq, x_tiles,                \
-                       (float)(x_tiles * 16), x_eps);                                                               \
-  else                                                                                                              \
-    hipLaunchKernelGGL((qkv_rope_append_kernel<HDV, false>), grid, dim3(256), 0, as_stream(stream), qkv, qkv_splits,\
-                       B, W, nq, nkv, q_norm, k_norm, v_norm, eps, inv_freq, seq_lens, pos_offset, block_table,     \
-                       max_pages, page, kv_dtype, k_pool, v_pool, k_sb, v_sb, q_out, nullptr, 0, 0.0f, 0.0f)
+#define DSK_APPEND(HDV)                                                                                         \
+  if (x_ssq)                                                                                                    \
+    hipLaunchKernelGGL((qkv_rope_append_kernel<HDV, true, true>), grid, dim3(256), 0, as_stream(stream), qkv,   \
+                       qkv_splits, B, W, nq, nkv, q_norm, k_norm, v_norm, eps, inv_freq, seq_lens, pos_offset,  \
+                       block_table, max_pages, page, kv_dtype, k_pool, v_pool, k_sb, v_sb, q_out, x_ssq,       \
+                       x_tiles, (float)(x_tiles * 16), x_eps);                                                  \
+  else if (qkv_splits > 0)                                                                                      \
+    hipLaunchKernelGGL((qkv_rope_append_kernel<HDV, false, true>), grid, dim3(256), 0, as_stream(stream), qkv,  \
+                       qkv_splits, B, W, nq, nkv, q_norm, k_norm, v_norm, eps, inv_freq, seq_lens, pos_offset,  \
+                       block_table, max_pages, page, kv_dtype, k_pool, v_pool, k_sb, v_sb, q_out, nullptr, 0,  \
+                       0.0f, 0.0f);                                                                             \
+  else                                                                                                          \
+    hipLaunchKernelGGL((qkv_rope_append_kernel<HDV, false, false>), grid, dim3(256), 0, as_stream(stream), qkv, \
+                       qkv_splits, B, W, nq, nkv, q_norm, k_norm, v_norm, eps, inv_freq, seq_lens, pos_offset,  \
+                       block_table, max_pages, page, kv_dtype, k_pool, v_pool, k_sb, v_sb, q_out, nullptr, 0,  \
+                       0.0f, 0.0f)
   if (hd == 128) {
     DSK_APPEND(128);
   } else if (hd == 256) {

@@ -19,19 +19,6 @@ __device__ __forceinline__ void rope_sincos(int pos, float inv_freq, float& sn, 
   cs = __builtin_amdgcn_cosf(rev);
 }
 
-// Row scale of a normed-later projection input, over the 64 lanes of a wave: the row's x_tiles
-// tile partials summed l, l + 64, l + 128, l + 192 per lane (then the rest), then across the wave
-// (the order the GEMM's own row scale uses); rsqrt(sum / x_k + x_eps).
-__device__ __forceinline__ float proj_row_scale(const float* x_ssq, int x_tiles, int64_t row, int lane, float x_k,
-                                                float x_eps) {
-  float xs[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) xs[j] = lane + 64 * j < x_tiles ? x_ssq[row * x_tiles + lane + 64 * j] : 0.0f;
-  float t = ((xs[0] + xs[1]) + xs[2]) + xs[3];
-  for (int j = lane + 256; j < x_tiles; j += 64) t += x_ssq[row * x_tiles + j];
-  return rsqrtf(wave_sum(t) / x_k + x_eps);
-}
-
 // One head row of HD dims spread over L consecutive lanes (L = 64: a wave; L = 16: a quarter
 // wave), PER = HD / L consecutive dims per lane starting at dim PER * (lane % L).
 // Sum of the projection's split-K slices in slice order, times `scale` (the row scale of a
