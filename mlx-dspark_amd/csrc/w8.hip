@@ -592,13 +592,20 @@ __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
       }
     }
   } else {
+    // registers per thread: 512 / (waves per SIMD); the batch, the accumulators and ~48 more
+    constexpr bool kWholeBatch =
+        sizeof(Batch<MT, NT, U, BITS>) / 4 + MT * NT * 4 + 48 <= 2048 / WAVES;
     for (int bt = wave; bt < nbatch; bt += WAVES) {
       Batch<MT, NT, U, BITS> r;
       batch_load<MT, NT, U, BITS>(a, t0, g_lo + (int64_t)bt * U, lane, r);
-      // the batch is waited for in full anyway; an explicit vmcnt(0) also retires the staged
-      // partials, so the compiler keeps exact load counts (it cannot count LDS-direct loads)
-      if constexpr (RS && PRE > 0) {
-        __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before the wait
+      // every load of the batch is issued before one wait for all of them (the batch is waited
+      // for in full anyway): left to itself the scheduler interleaves the loads with partial
+      // waits and MFMAs, so a batch took several memory round trips. Held to where the whole
+      // batch fits the plan's registers (1024-thread plans with wide batches would spill). The
+      // vmcnt(0) also retires staged row-scale partials, so the compiler keeps exact load counts
+      // (it cannot count LDS-direct loads).
+      if constexpr (kWholeBatch || (RS && PRE > 0)) {
+        __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(0x0f70);
         __builtin_amdgcn_sched_barrier(0);
       }
