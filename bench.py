@@ -420,7 +420,7 @@ def main(argv=None) -> int:
     import torch
 
     from mlx_dspark import ops, synthetic
-    from mlx_dspark.generate import _DFlashRound, _pick
+    from mlx_dspark.generate import _DFlashPipe, _pick
     from mlx_dspark.target import Target
     from mlx_dspark.tokenizer import SyntheticTokenizer
 
@@ -453,7 +453,7 @@ def main(argv=None) -> int:
     target = Target(model, tok, kv_bits=kv_bits)
     cap = args.block - 1
     W = cap + 1
-    rounds_total = 2 * (args.steps + args.warmup) + 2          # greedy rounds, then sampled rounds
+    rounds_total = 2 * (args.steps + max(args.warmup, 4)) + 2  # greedy rounds, then sampled rounds
     max_ctx = args.ctx + W * (rounds_total + 2) + 64
     cache = target.make_cache(max_ctx=max_ctx)
     dcache = drafter.make_cache(max_ctx=max_ctx)
@@ -498,15 +498,21 @@ def main(argv=None) -> int:
     pending = _pick(logits[0, -1], 0.0)
     torch.cuda.synchronize()
 
-    rnd = _DFlashRound(target, drafter, cache, dcache, cap, 0.0, 1.0, 0, 0)
-    rnd.pending.fill_(pending)
-    for r in range(args.warmup):
-        rnd.run(r, use_graph=True)
+    # rounds as dflash_generate runs them: each enqueued before the host reads the previous
+    # round's ids (two alternating graph-replayed round objects)
+    pipe = _DFlashPipe(target, drafter, cache, dcache, cap, 0.0, 1.0, 0, 0)
+    pipe.start(pending)
+    for r in range(max(args.warmup, 4)):       # both round objects captured before the timing
+        pipe.enqueue()
+        pipe.collect()
     torch.cuda.synchronize()
     accepted = []
     t0 = time.perf_counter()
+    pipe.enqueue()
     for r in range(args.steps):
-        n, token, _ = rnd.run(args.warmup + r, use_graph=True)
+        if r + 1 < args.steps:
+            pipe.enqueue()
+        n, token, _ = pipe.collect()
         accepted.append(n + 1)
     torch.cuda.synchronize()
     secs = time.perf_counter() - t0
@@ -517,14 +523,18 @@ def main(argv=None) -> int:
 
     # ---- the same rounds sampled (T 0.6, top-p 0.95, top-k 20: draft rows drawn, speculative
     # sampling acceptance), graph-replayed: the extra time per round over greedy
-    srnd = _DFlashRound(target, drafter, cache, dcache, cap, 0.6, 0.95, 20, 5)
-    srnd.pending.fill_(token)
-    for r in range(args.warmup):
-        srnd.run(r, use_graph=True)
+    spipe = _DFlashPipe(target, drafter, cache, dcache, cap, 0.6, 0.95, 20, 5)
+    spipe.start(token)
+    for r in range(max(args.warmup, 4)):
+        spipe.enqueue()
+        spipe.collect()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    spipe.enqueue()
     for r in range(args.steps):
-        srnd.run(args.warmup + r, use_graph=True)
+        if r + 1 < args.steps:
+            spipe.enqueue()
+        spipe.collect()
     torch.cuda.synchronize()
     sampled_ms = (time.perf_counter() - t0) / args.steps * 1e3
     log(f"sampled rounds: {sampled_ms:.3f} ms/round (+{(sampled_ms - ms_per_step) * 1e3:.0f} us over greedy)")

@@ -15,6 +15,7 @@ kernels eagerly, with Philox uniforms keyed by ``seed`` and the round number.
 
 from __future__ import annotations
 
+import collections
 import time
 from dataclasses import dataclass
 
@@ -283,8 +284,15 @@ class _DFlashRound:
         self.rng_off = torch.zeros(1, dtype=torch.int32, device=dev)
         self.graph = None
         self.calls = 0
+        # src: a partner round's pending slot this round copies its own from on the device
+        # (_DFlashPipe); the round's ids land in pinned host memory, ready at `ready`
+        self.src = None
+        self.host_out = torch.zeros(2 + cap, dtype=torch.int32, pin_memory=True)
+        self.ready = torch.cuda.Event()
 
     def body(self) -> None:
+        if self.src is not None:
+            self.pending.copy_(self.src)
         self.block[0, 0:1].copy_(self.pending)
         self.drafter.block_logits(self.block, self.dcache, 1, self.cap, out=self.head)
         if self.T > 0:
@@ -304,9 +312,9 @@ class _DFlashRound:
                               seq_lens=self.cache.seq_lens, tt=self.tt, n_out=self.n, token_out=self.token)
         self.drafter.ingest(self.v_fused, self.dcache, n_valid=self.n)     # commit [anchor, accepted]
 
-    def run(self, round_idx: int, use_graph: bool):
-        # the first round of this width runs eagerly (it sizes the workspaces), later ones
-        # replay one captured graph
+    def launch(self, round_idx: int, use_graph: bool) -> None:
+        """Enqueue the round: the first of this width runs eagerly (it sizes the workspaces),
+        later ones replay one captured graph; then the ids' copy to host memory."""
         self.rng_off.fill_(round_idx & 0x7FFFFFFF)
         if use_graph:
             if self.graph is None and self.calls >= 1:
@@ -320,11 +328,71 @@ class _DFlashRound:
         else:
             self.body()
         self.calls += 1
-        o = self.out.tolist()                                         # the round's one host sync
+        self.host_out.copy_(self.out, non_blocking=True)
+        self.ready.record()
+
+    def result(self):
+        """(n, token, draft) of the last launch: waits for it alone, then records the lengths
+        the device already advanced."""
+        self.ready.synchronize()
+        o = self.host_out.tolist()
         n, token, draft = o[0], o[1], o[2:]
         self.cache.note_lengths([self.cache.lengths[0] + n + 1])
         self.dcache.note_lengths([self.dcache.lengths[0] + n + 1])
         return n, token, draft
+
+    def run(self, round_idx: int, use_graph: bool):
+        self.launch(round_idx, use_graph)
+        return self.result()                                          # the round's one host sync
+
+
+class _DFlashPipe:
+    """Rounds of one width enqueued one ahead of the host: two _DFlashRound objects alternate,
+    each reading its pending token from the other's output on the device, so the next round is
+    on the GPU while the host reads this one's ids, checks the stop conditions and streams text
+    (one round at a time, the GPU sat idle meanwhile). The rounds and their inputs are the
+    sequential loop's; a round enqueued past the end of a generation is undone by restoring the
+    caches' lengths (its KV writes lie past them)."""
+
+    def __init__(self, target, drafter, cache, dcache, cap: int, temperature: float, top_p: float, top_k: int,
+                 seed: int, use_graph: bool = True):
+        self.rounds = [_DFlashRound(target, drafter, cache, dcache, cap, temperature, top_p, top_k, seed)
+                       for _ in range(2)]
+        self.rounds[0].src = self.rounds[1].pending
+        self.rounds[1].src = self.rounds[0].pending
+        self.cache, self.dcache, self.W = cache, dcache, cap + 1
+        self.use_graph = use_graph
+        self.queue: collections.deque = collections.deque()
+        self.turn = 0
+        self.next_idx = 0
+
+    def start(self, pending: int, round_idx: int = 0) -> None:
+        """The first round's pending token (its source slot) and Philox round index."""
+        self.rounds[1 - self.turn].pending.fill_(pending)
+        self.next_idx = round_idx
+
+    def room(self, rounds: int) -> bool:
+        """Whether `rounds` more rounds fit both caches (host lengths: rounds collected so far)."""
+        return (self.cache.lengths[0] + rounds * self.W <= self.cache.max_ctx
+                and self.dcache.lengths[0] + rounds * self.W <= self.dcache.max_ctx)
+
+    def enqueue(self) -> None:
+        rnd = self.rounds[self.turn]
+        self.turn ^= 1
+        rnd.launch(self.next_idx, self.use_graph)
+        self.next_idx += 1
+        self.queue.append(rnd)
+
+    def collect(self):
+        """(n, token, draft) of the oldest enqueued round."""
+        return self.queue.popleft().result()
+
+    def cancel(self) -> None:
+        """Undo the rounds still enqueued: the caches go back to the collected lengths."""
+        if self.queue:
+            self.queue.clear()
+            self.cache.set_lengths(self.cache.lengths)
+            self.dcache.set_lengths(self.dcache.lengths)
 
 
 def dflash_generate(target_model, tokenizer, drafter, prompt: str = "", *, prompt_ids=None, max_new_tokens: int = 128,
@@ -359,7 +427,33 @@ def dflash_generate(target_model, tokenizer, drafter, prompt: str = "", *, promp
     rounds: dict = {}
     st.update(out_ids)
     r = 0
-    while len(out_ids) < max_new_tokens and pending not in eos_ids and not st.stopped:
+    if use_graph and cap_controller is None:
+        # a fixed width: each round enqueued before the host reads the previous one
+        pipe = _DFlashPipe(target_model, drafter, cache, dcache, cap, temperature, top_p, top_k, s64)
+        pipe.start(pending)
+        going = len(out_ids) < max_new_tokens and pending not in eos_ids and not st.stopped
+        if going and pipe.room(1):
+            pipe.enqueue()
+        while pipe.queue:
+            if len(pipe.queue) == 1 and pipe.room(2):
+                pipe.enqueue()
+            n, token, draft = pipe.collect()
+            committed = draft[:n] + [token]
+            target_forwards += 1
+            accept_lengths.append(len(committed))
+            for tok in committed:
+                out_ids.append(tok)
+                if tok in eos_ids:
+                    break
+            pending = out_ids[-1]
+            st.update(out_ids)
+            if not (len(out_ids) < max_new_tokens and pending not in eos_ids and not st.stopped):
+                pipe.cancel()
+                break
+            if not pipe.queue and pipe.room(1):
+                pipe.enqueue()
+    while (not use_graph or cap_controller is not None) and len(out_ids) < max_new_tokens \
+            and pending not in eos_ids and not st.stopped:
         c = cap if cap_controller is None else max(1, min(int(cap_controller.cap), cap))
         if cache.lengths[0] + c + 1 > cache.max_ctx:
             break

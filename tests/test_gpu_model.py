@@ -207,3 +207,48 @@ def test_dflash_generate_sampled_is_seeded(dev, tiny):
     # draw exactly what the eager rounds draw
     e = dflash_generate(target, tok, d, use_graph=False, **kw)
     assert a.token_ids == e.token_ids and a.num_rounds >= 3
+
+
+@pytest.mark.parametrize("temperature", [0.0, 0.8])
+def test_dflash_pipelined_rounds_match_sequential(dev, tiny, temperature):
+    """Rounds enqueued one ahead of the host (two alternating round objects chained on the
+    device) return the sequential rounds' ids, and cancelling the round enqueued past the last
+    one leaves both caches (host and device lengths) where the sequential rounds leave them."""
+    from mlx_dspark import synthetic
+    from mlx_dspark.generate import _DFlashPipe, _DFlashRound, _pick
+    from mlx_dspark.target import Target
+    from mlx_dspark.tokenizer import SyntheticTokenizer
+    print(f"pipelined DFlash rounds T={temperature}", flush=True)
+    d, cfg = synthetic.build_dflash(tiny.args, seed=9, num_hidden_layers=2, block_size=8, n_taps=2)
+    d.bind(tiny)
+    target = Target(tiny, SyntheticTokenizer(tiny.args.vocab_size))
+    prompt = np.random.default_rng(5).integers(0, tiny.args.vocab_size, 37).tolist()
+    tap, cap, n_rounds = list(cfg.target_layer_ids), 7, 6
+
+    def fresh():
+        cache, dcache = target.make_cache(max_ctx=256), d.make_cache(max_ctx=256)
+        logits, fused = tiny.prefill(prompt, cache, tap)
+        d.ingest(fused, dcache)
+        return cache, dcache, _pick(logits[0, -1], 0.0)
+
+    cache, dcache, pending = fresh()
+    rnd = _DFlashRound(target, d, cache, dcache, cap, temperature, 0.9, 0, 77)
+    rnd.pending.fill_(pending)
+    seq = [rnd.run(r, True) for r in range(n_rounds)]
+    seq_lens = (list(cache.lengths), list(dcache.lengths))
+
+    cache2, dcache2, pending2 = fresh()
+    assert pending2 == pending
+    pipe = _DFlashPipe(target, d, cache2, dcache2, cap, temperature, 0.9, 0, 77)
+    pipe.start(pending2)
+    pipe.enqueue()
+    got = []
+    for r in range(n_rounds):
+        pipe.enqueue()                                   # the last one is past the end
+        got.append(pipe.collect())
+    pipe.cancel()
+    torch.cuda.synchronize()
+    assert got == seq
+    assert (list(cache2.lengths), list(dcache2.lengths)) == seq_lens
+    assert cache2.seq_lens.tolist() == cache.seq_lens.tolist() == seq_lens[0]
+    assert dcache2.seq_lens.tolist() == dcache.seq_lens.tolist() == seq_lens[1]
