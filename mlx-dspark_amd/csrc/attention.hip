@@ -166,7 +166,7 @@ struct AttnArgs {
   int nsplit;
   int kps;           // keys per (context) split: a whole number of LDS blocks (Split<HD>::KEYS)
   int fused;         // splits 0 .. nsplit-2: cached keys; split nsplit-1: the new tokens
-  uint16_t* part_o;  // [B*nkv][nsplit][R][HD] bf16: the split's o / l
+  float* part_o;     // [B*nkv][nsplit][R][HD] float32: the split's o / l
   float* part_ml;    // [B*nkv][nsplit][R][2]: the split's running max m and sum l
 };
 
@@ -367,7 +367,7 @@ __global__ __launch_bounds__(256 * WPT) __attribute__((amdgpu_waves_per_eu(1, 2)
   // compiler would otherwise reload them from the kernel-argument segment (a memory round trip)
   float scale = a.scale, softcap = a.softcap;
   int causal = a.causal, window = a.window, nsplit = a.nsplit, kps = a.kps;
-  uint16_t* part_o = a.part_o;
+  float* part_o = a.part_o;
   float* part_ml = a.part_ml;
   asm volatile("" : "+s"(scale), "+s"(softcap), "+s"(causal), "+s"(window), "+s"(nsplit), "+s"(kps));
   asm volatile("" : "+s"(part_o), "+s"(part_ml));
@@ -584,19 +584,17 @@ __global__ __launch_bounds__(256 * WPT) __attribute__((amdgpu_waves_per_eu(1, 2)
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     // rescale of the previous blocks' sum and output (none on the first block)
     const float alpha = m_run == -__builtin_inff() ? 0.0f : __expf(m_run - mx);
+    // float32 probabilities in place of the scores (three bf16 terms each in the P.V MFMAs)
     float lsum = 0.0f;
-    bf16x8 pb[KH / 32];
 #pragma unroll
-    for (int c = 0; c < KH / 32; ++c)
+    for (int h = 0; h < NKH; ++h)
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float sc = st[2 * c + hh][r];
-          const float p = sc == -__builtin_inff() ? 0.0f : round_bf16(__expf(sc - mx));
-          lsum += p;
-          pb[c][hh * 4 + r] = (__bf16)p;
-        }
+      for (int r = 0; r < 4; ++r) {
+        const float sc = st[h][r];
+        const float p = sc == -__builtin_inff() ? 0.0f : __expf(sc - mx);
+        lsum += p;
+        st[h][r] = p;
+      }
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
     l_run = l_run * alpha + lsum;
@@ -621,9 +619,34 @@ __global__ __launch_bounds__(256 * WPT) __attribute__((amdgpu_waves_per_eu(1, 2)
         if (c + 1 < KH / 32)
 #pragma unroll
           for (int d = 0; d < DT; ++d) vv[(c + 1) & 1][d] = vfrag(d, c + 1);
-        __builtin_amdgcn_sched_barrier(0);
+        // P of the chunk's 8 keys (score tiles 2c, 2c + 1) as hi + mid + lo
+        uint32_t w[3][4];
 #pragma unroll
-        for (int d = 0; d < DT; ++d) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv[c & 1][d], pb[c], o[d], 0, 0, 0);
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int r2 = 0; r2 < 2; ++r2) {
+            const Bf16x2Terms tt = split3_bf16x2(st[2 * c + hh][2 * r2], st[2 * c + hh][2 * r2 + 1]);
+            w[0][2 * hh + r2] = tt.hi;
+            w[1][2 * hh + r2] = tt.mid;
+            w[2][2 * hh + r2] = tt.lo;
+          }
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x8 pk[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) pk[k] = __builtin_bit_cast(bf16x8, (u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}));
+        if constexpr (DT >= 16) {
+          // wide heads: a V fragment's three products back to back, so it is free after them
+#pragma unroll
+          for (int d = 0; d < DT; ++d)
+#pragma unroll
+            for (int k = 0; k < 3; ++k) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv[c & 1][d], pk[k], o[d], 0, 0, 0);
+        } else {
+          // one term over every d tile before the next (DT independent accumulators in between)
+#pragma unroll
+          for (int k = 0; k < 3; ++k)
+#pragma unroll
+            for (int d = 0; d < DT; ++d) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv[c & 1][d], pk[k], o[d], 0, 0, 0);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -642,15 +665,11 @@ __global__ __launch_bounds__(256 * WPT) __attribute__((amdgpu_waves_per_eu(1, 2)
           a.out[attn_out_index(a, HD, b, i, kvh * a.G + hl, d * 16 + (lane >> 4) * 4 + rr)] = f32_to_bf16(o[d][rr] * inv);
       return;
     }
-    // partial: o / l in bf16 (4 consecutive dims per d tile), (m, l) in fp32
+    // partial: o / l in float32 (4 consecutive dims per d tile), (m, l)
     const size_t prow = ((size_t)bk * nsplit + split) * a.R + rq;
-    uint16_t* po = part_o + prow * HD + (lane >> 4) * 4;
+    float* po = part_o + prow * HD + (lane >> 4) * 4;
 #pragma unroll
-    for (int d = 0; d < DT; ++d) {
-      const uint32_t lo = (uint32_t)f32_to_bf16(o[d][0] * inv) | ((uint32_t)f32_to_bf16(o[d][1] * inv) << 16);
-      const uint32_t hi = (uint32_t)f32_to_bf16(o[d][2] * inv) | ((uint32_t)f32_to_bf16(o[d][3] * inv) << 16);
-      *reinterpret_cast<uint2*>(po + d * 16) = uint2{lo, hi};
-    }
+    for (int d = 0; d < DT; ++d) *reinterpret_cast<f32x4*>(po + d * 16) = o[d] * inv;
     if (lane < 16) *reinterpret_cast<float2*>(part_ml + prow * 2) = float2{m_run, l_run};
   };
 
@@ -752,7 +771,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   // a sliding-window row starts at the split holding its window's first key (the attention
   // kernel skips the splits before every window of a workgroup)
   const int s_beg = a.causal && !a.fused && a.window > 0 ? max(0, visible - a.window) / a.kps : 0;
-  const uint16_t* base_o = a.part_o + ((size_t)bk * a.nsplit * a.R + r) * HD + lane * PER;
+  const float* base_o = a.part_o + ((size_t)bk * a.nsplit * a.R + r) * HD + lane * PER;
   const float* base_ml = a.part_ml + ((size_t)bk * a.nsplit * a.R + r) * 2;
   const size_t so = (size_t)a.R * HD, sml = (size_t)a.R * 2;
   float acc[PER];
@@ -760,7 +779,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
   for (int e = 0; e < PER; ++e) acc[e] = 0.0f;
   float M = -__builtin_inff(), den = 0.0f;
   // rounds of RS splits: the (m, l) and partial-output loads of a round are issued together
-  constexpr int RS = PER == 2 ? 64 : (PER == 4 ? 32 : 16);
+  constexpr int RS = PER == 2 ? 32 : 16;
   for (int s0 = s_beg; s0 < ns; s0 += RS) {
     const int n = min(RS, ns - s0);
     float m = -__builtin_inff(), l = 0.0f;
@@ -771,7 +790,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
       l = v.y;
     }
     // loads of the live splits only, in batches of 16 (all batches issued before any use)
-    uint16_t ov[RS][PER];
+    float ov[RS][PER];
 #pragma unroll
     for (int u0 = 0; u0 < RS; u0 += 16) {
       if (u0 >= n) break;
@@ -779,20 +798,11 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
       for (int u = u0; u < u0 + 16; ++u) {
         int sp = s0 + min(u, n - 1);
         if (sp == ns - 1) sp += nlast;
-        if constexpr (PER == 2) {
-          const uint32_t x = *reinterpret_cast<const uint32_t*>(base_o + sp * so);
-          ov[u][0] = (uint16_t)(x & 0xffff);
-          ov[u][1] = (uint16_t)(x >> 16);
-        } else if constexpr (PER == 4) {
-          const uint2 x = *reinterpret_cast<const uint2*>(base_o + sp * so);
-          const uint16_t* hx = reinterpret_cast<const uint16_t*>(&x);
 #pragma unroll
-          for (int e = 0; e < PER; ++e) ov[u][e] = hx[e];
-        } else {
-          const u32x4 x = *reinterpret_cast<const u32x4*>(base_o + sp * so);
-          const uint16_t* hx = reinterpret_cast<const uint16_t*>(&x);
-#pragma unroll
-          for (int e = 0; e < PER; ++e) ov[u][e] = hx[e];
+        for (int e = 0; e < PER; e += 2) {
+          const float2 x = *reinterpret_cast<const float2*>(base_o + sp * so + e);
+          ov[u][e] = x.x;
+          ov[u][e + 1] = x.y;
         }
       }
     }
@@ -811,7 +821,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
         const float wu = __shfl(w, u, 64);
         if (u < n)
 #pragma unroll
-          for (int e = 0; e < PER; ++e) acc[e] += wu * bf16_to_f32(ov[u][e]);
+          for (int e = 0; e < PER; ++e) acc[e] += wu * ov[u][e];
       }
     }
   }
@@ -1065,39 +1075,50 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
     for (int tile = 0; tile < QT; ++tile) mx[tile] = fmaxf(mx[tile], __shfl_xor(mx[tile], 16, 64));
 #pragma unroll
     for (int tile = 0; tile < QT; ++tile) mx[tile] = fmaxf(mx[tile], __shfl_xor(mx[tile], 32, 64));
-    bf16x8 pb[QT][KB / 2];
+    // float32 probabilities, in place of the scores, and their sums
 #pragma unroll
     for (int tile = 0; tile < QT; ++tile) {
       // masked keys: exp2(-inf) = 0; a row with no visible key keeps m = -inf, l = 0
       const float mb = mx[tile] == -__builtin_inff() ? 0.0f : mx[tile] * c2;
 #pragma unroll
-      for (int cp = 0; cp < KB / 2; ++cp) {
-        uint32_t w[4];
+      for (int t = 0; t < KB; ++t)
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const f32x4& sv = st[tile][2 * cp + u];
-            w[2 * u + h] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(sv[2 * h], c2, -mb)),
-                                       __builtin_amdgcn_exp2f(fmaf(sv[2 * h + 1], c2, -mb)));
-            l[tile] += __uint_as_float(w[2 * u + h] << 16) + __uint_as_float(w[2 * u + h] & 0xffff0000u);
-          }
-        pb[tile][cp] = __builtin_bit_cast(bf16x8, (u32x4{w[0], w[1], w[2], w[3]}));
-      }
+        for (int rr = 0; rr < 4; ++rr) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(st[tile][t][rr], c2, -mb));
+          st[tile][t][rr] = p;
+          l[tile] += p;
+        }
       m[tile] = mx[tile] * mscale;
     }
 #pragma unroll
     for (int tile = 0; tile < QT; ++tile) l[tile] += __shfl_xor(l[tile], 16, 64);
 #pragma unroll
     for (int tile = 0; tile < QT; ++tile) l[tile] += __shfl_xor(l[tile], 32, 64);
-    // ---- O^T = V^T . P^T over the wave's keys (32 per MFMA)
+    // ---- O^T = V^T . P^T over the wave's keys (32 per MFMA), P as three bf16 terms: one term's
+    // MFMAs over every d tile before the next term's (8 independent accumulators in between)
 #pragma unroll
     for (int cp = 0; cp < KB / 2; ++cp)
 #pragma unroll
-      for (int d = 0; d < 8; ++d)
+      for (int tile = 0; tile < QT; ++tile) {
+        uint32_t w[3][4];
 #pragma unroll
-        for (int tile = 0; tile < QT; ++tile)
-          o[tile][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[cp][d], pb[tile][cp], o[tile][d], 0, 0, 0);
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const f32x4& pv = st[tile][2 * cp + u];
+            const Bf16x2Terms tt = split3_bf16x2(pv[2 * h], pv[2 * h + 1]);
+            w[0][2 * u + h] = tt.hi;
+            w[1][2 * u + h] = tt.mid;
+            w[2][2 * u + h] = tt.lo;
+          }
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+          const bf16x8 pk = __builtin_bit_cast(bf16x8, (u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}));
+#pragma unroll
+          for (int d = 0; d < 8; ++d)
+            o[tile][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[cp][d], pk, o[tile][d], 0, 0, 0);
+        }
+      }
   }
 #pragma unroll
   for (int tile = 0; tile < QT; ++tile) {
@@ -1124,63 +1145,66 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
       L += ml[q].y * wq[q];
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    uint32_t w[16];
+    f32x4 res[8];  // dims 32 grp + 4 d .. + 3
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
       f32x4 acc = f32x4{0, 0, 0, 0};
 #pragma unroll
       for (int q = 0; q < NW; ++q) acc += mo[tile][q][d][lane] * wq[q];
-      w[2 * d] = pack_bf16x2(acc[0] * inv, acc[1] * inv);
-      w[2 * d + 1] = pack_bf16x2(acc[2] * inv, acc[3] * inv);
+      res[d] = acc * inv;
     }
-    // dims 32 grp .. + 31 in two runs of 16 (contiguous in both output layouts)
-    u32x4* dst[2];
     if (a.nsplit == 1) {
+      // dims 32 grp .. + 31 in two runs of 16 (contiguous in both output layouts)
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        dst[h] = reinterpret_cast<u32x4*>(a.out + attn_out_index(a, HD, b, rq / a.G, kvh * a.G + rq % a.G,
-                                                                  grp * 32 + 16 * h));
+      for (int h = 0; h < 2; ++h) {
+        u32x4* dst = reinterpret_cast<u32x4*>(a.out + attn_out_index(a, HD, b, rq / a.G, kvh * a.G + rq % a.G,
+                                                                      grp * 32 + 16 * h));
+        uint32_t w[8];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          w[2 * d] = pack_bf16x2(res[4 * h + d][0], res[4 * h + d][1]);
+          w[2 * d + 1] = pack_bf16x2(res[4 * h + d][2], res[4 * h + d][3]);
+        }
+        dst[0] = u32x4{w[0], w[1], w[2], w[3]};
+        dst[1] = u32x4{w[4], w[5], w[6], w[7]};
+      }
     } else {
+      // the split's partial o / l in float32 (32 contiguous dims per lane) and its (m, l)
       const size_t prow = ((size_t)bk * a.nsplit + split) * a.R + rq;
+      f32x4* dst = reinterpret_cast<f32x4*>(a.part_o + prow * HD + grp * 32);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) dst[h] = reinterpret_cast<u32x4*>(a.part_o + prow * HD + grp * 32 + 16 * h);
+      for (int d = 0; d < 8; ++d) dst[d] = res[d];
       if (grp == 0) *reinterpret_cast<float2*>(a.part_ml + prow * 2) = float2{M, L};
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      dst[h][0] = u32x4{w[8 * h], w[8 * h + 1], w[8 * h + 2], w[8 * h + 3]};
-      dst[h][1] = u32x4{w[8 * h + 4], w[8 * h + 5], w[8 * h + 6], w[8 * h + 7]};
     }
   }
 }
 
-// The verify kernel's splits merged: one thread per (row b, kv head, query row, 8 dims), every
+// The verify kernel's splits merged: one thread per (row b, kv head, query row, 4 dims), every
 // split read (a split past the row length holds m = -inf and is skipped by value), the loads of
 // a batch of 24 splits issued together. Same merge as attention_combine_kernel: weights
-// exp(m_s - M) * l_s over the splits' normalised bf16 partial outputs.
+// exp(m_s - M) * l_s over the splits' normalised float32 partial outputs.
 constexpr int kVerifyCombineThreads = 64;
 __global__ __launch_bounds__(kVerifyCombineThreads) void attention_verify_combine_kernel(AttnArgs a) {
   constexpr int HD = 128, BATCH = 24;
   const int64_t task = (int64_t)blockIdx.x * kVerifyCombineThreads + threadIdx.x;
-  if (task >= (int64_t)a.B * a.nkv * a.R * (HD / 8)) return;
-  const int ch = (int)(task & 15);
-  const int64_t rowt = task >> 4;
+  if (task >= (int64_t)a.B * a.nkv * a.R * (HD / 4)) return;
+  const int ch = (int)(task & 31);
+  const int64_t rowt = task >> 5;
   const int r = (int)(rowt % a.R);
   const int bk = (int)(rowt / a.R);
   const int b = bk / a.nkv, kvh = bk % a.nkv;
   const size_t base = (size_t)bk * a.nsplit * a.R + r;  // partial row of split 0
-  float M = -__builtin_inff(), L = 0.0f, acc[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  float M = -__builtin_inff(), L = 0.0f;
+  f32x4 acc = f32x4{0, 0, 0, 0};
   for (int s0 = 0; s0 < a.nsplit; s0 += BATCH) {
     float2 ml[BATCH];
-    u32x4 ov[BATCH];
+    f32x4 ov[BATCH];
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {
       const int sp = min(s0 + u, a.nsplit - 1);
       const size_t prow = base + (size_t)sp * a.R;
       ml[u] = *reinterpret_cast<const float2*>(a.part_ml + prow * 2);
-      ov[u] = *reinterpret_cast<const u32x4*>(a.part_o + prow * HD + ch * 8);
+      ov[u] = *reinterpret_cast<const f32x4*>(a.part_o + prow * HD + ch * 4);
       if (s0 + u >= a.nsplit) ml[u].x = -__builtin_inff();
     }
     float Mn = M;
@@ -1189,26 +1213,19 @@ __global__ __launch_bounds__(kVerifyCombineThreads) void attention_verify_combin
     if (Mn == -__builtin_inff()) continue;
     const float rescale = M == -__builtin_inff() ? 0.0f : __expf(M - Mn);
     L *= rescale;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] *= rescale;
+    acc *= rescale;
     M = Mn;
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {
       if (ml[u].x == -__builtin_inff()) continue;  // also skips a never-written partial output
       const float wl = __expf(ml[u].x - M) * ml[u].y;
       L += wl;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t x = ov[u][q];
-        acc[2 * q] += wl * __uint_as_float(x << 16);
-        acc[2 * q + 1] += wl * __uint_as_float(x & 0xffff0000u);
-      }
+      acc += wl * ov[u];
     }
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  *reinterpret_cast<u32x4*>(a.out + attn_out_index(a, HD, b, r / a.G, kvh * a.G + r % a.G, ch * 8)) =
-      u32x4{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),
-            pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv)};
+  *reinterpret_cast<uint2*>(a.out + attn_out_index(a, HD, b, r / a.G, kvh * a.G + r % a.G, ch * 4)) =
+      uint2{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)};
 }
 
 // ----------------------------------------------------------------------------- many-query pass
@@ -1383,7 +1400,6 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
     // ---- mask (only a block that straddles a row's visible range), max, exp2, P
     const bool masked = !wave_full || j_hi - j_lo < kPfKeys || (causal && j_lo + kPfKeys - 1 > wq_lo) ||
                         (causal && window > 0 && j_lo < wq_hi - window + 1);
-    bf16x8 pb[TPW][NKT / 2];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       if (masked) {
@@ -1412,19 +1428,11 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
       // masked keys: exp2(-inf) = 0; a row with no visible key yet keeps m = -inf, l = 0, o = 0
       const float mb = mx == -__builtin_inff() ? 0.0f : mx * c2;
       const float alpha = m_run[t] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f((m_run[t] - mx) * c2);
+      // float32 probabilities in place of the scores
 #pragma unroll
-      for (int cp = 0; cp < NKT / 2; ++cp) {
-        uint32_t w[4];
+      for (int h = 0; h < NKT; ++h)
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            const f32x4& sv = st[t][2 * cp + u];
-            w[2 * u + hh] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(sv[2 * hh], c2, -mb)),
-                                        __builtin_amdgcn_exp2f(fmaf(sv[2 * hh + 1], c2, -mb)));
-          }
-        pb[t][cp] = __builtin_bit_cast(bf16x8, (u32x4{w[0], w[1], w[2], w[3]}));
-      }
+        for (int r = 0; r < 4; ++r) st[t][h][r] = __builtin_amdgcn_exp2f(fmaf(st[t][h][r], c2, -mb));
       m_run[t] = mx;
       if (__any(alpha != 1.0f)) {
         lt[t] *= alpha;
@@ -1432,10 +1440,28 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
         for (int d = 0; d < DT; ++d) o[t][d] *= alpha;
       }
     }
-    // ---- O^T[d][q] += V^T . P^T: each V^T fragment feeds both query tiles
+    // ---- O^T[d][q] += V^T . P^T with P as hi + mid + lo (three MFMAs per fragment and tile):
+    // each V^T fragment feeds both query tiles
     const uint16_t* vt16 = reinterpret_cast<const uint16_t*>(vt[buf]);
 #pragma unroll
     for (int cp = 0; cp < NKT / 2; ++cp) {
+      bf16x8 pk[TPW][3];
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        uint32_t w[3][4];
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const f32x4& pv = st[t][2 * cp + u];
+            const Bf16x2Terms tt = split3_bf16x2(pv[2 * hh], pv[2 * hh + 1]);
+            w[0][2 * u + hh] = tt.hi;
+            w[1][2 * u + hh] = tt.mid;
+            w[2][2 * u + hh] = tt.lo;
+          }
+#pragma unroll
+        for (int k = 0; k < 3; ++k) pk[t][k] = __builtin_bit_cast(bf16x8, (u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}));
+      }
 #pragma unroll
       for (int d = 0; d < DT; ++d) {
         const uint16_t* vr = vt16 + (d * 16 + (lane & 15)) * kPfVRow + 32 * cp + (lane >> 4) * 4;
@@ -1443,10 +1469,14 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
         const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
         const bf16x8 vf = __builtin_bit_cast(bf16x8, (u32x4{lo.x, lo.y, hi.x, hi.y}));
 #pragma unroll
-        for (int t = 0; t < TPW; ++t) o[t][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[t][cp], o[t][d], 0, 0, 0);
+        for (int k = 0; k < 3; ++k)
+#pragma unroll
+          for (int t = 0; t < TPW; ++t) o[t][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pk[t][k], o[t][d], 0, 0, 0);
       }
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) lt[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[t][cp], lt[t], 0, 0, 0);
+      for (int k = 0; k < 3; ++k)
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) lt[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pk[t][k], lt[t], 0, 0, 0);
     }
   };
 
@@ -1522,7 +1552,7 @@ static int attn_blocks(int hd, int max_ctx, int W = 1) {
 
 // partial outputs first, then (m, l) at a 256-byte boundary
 static size_t attn_part_o_bytes(int B, int W, int nq, int hd, int nsplit) {
-  return ((size_t)B * W * nq * nsplit * hd * 2 + 255) & ~(size_t)255;
+  return ((size_t)B * W * nq * nsplit * hd * sizeof(float) + 255) & ~(size_t)255;
 }
 static size_t attn_ws_need(int B, int W, int nq, int hd, int nsplit) {
   return nsplit > 1 ? attn_part_o_bytes(B, W, nq, hd, nsplit) + (size_t)B * W * nq * nsplit * 2 * sizeof(float) : 0;
@@ -1572,7 +1602,7 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
   a.nsplit = (int)ceil_div(max_ctx, a.kps) + (fused ? 1 : 0);
   const size_t need = attn_ws_need(a.B, a.W, a.nq, hd, a.nsplit);
   DSK_REQUIRE(a.nsplit == 1 || (workspace && ws_bytes >= need), "%s: workspace %zu < %zu", who, ws_bytes, need);
-  a.part_o = reinterpret_cast<uint16_t*>(workspace);
+  a.part_o = reinterpret_cast<float*>(workspace);
   a.part_ml = a.nsplit > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
                                                        attn_part_o_bytes(a.B, a.W, a.nq, hd, a.nsplit))
                            : nullptr;
@@ -1582,7 +1612,7 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
     a.nsplit = (int)ceil_div(max_ctx, a.kps);
     const size_t need_v = attn_ws_need(a.B, a.W, a.nq, hd, a.nsplit);
     DSK_REQUIRE(a.nsplit == 1 || (workspace && ws_bytes >= need_v), "%s: workspace %zu < %zu", who, ws_bytes, need_v);
-    a.part_o = reinterpret_cast<uint16_t*>(workspace);
+    a.part_o = reinterpret_cast<float*>(workspace);
     a.part_ml = a.nsplit > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
                                                         attn_part_o_bytes(a.B, a.W, a.nq, hd, a.nsplit))
                              : nullptr;
@@ -1602,7 +1632,7 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
 #undef DSK_VERIFY_QT
     DSK_LAUNCH_CHECK(who);
     if (a.nsplit > 1) {
-      const dim3 cgrid((unsigned)ceil_div((int64_t)a.B * a.nkv * a.R * 16, kVerifyCombineThreads));
+      const dim3 cgrid((unsigned)ceil_div((int64_t)a.B * a.nkv * a.R * 32, kVerifyCombineThreads));
       hipLaunchKernelGGL(attention_verify_combine_kernel, cgrid, dim3(kVerifyCombineThreads), 0, st, a);
       DSK_LAUNCH_CHECK(who);
     }

@@ -79,6 +79,24 @@ __host__ __device__ __forceinline__ float bits_f32(uint32_t u) {
   return f;
 }
 
+// ---- float32 probabilities as three bf16 terms ------------------------------------------
+// hi = bf16(p), mid = bf16(p - hi), lo = bf16(p - hi - mid), two values per word (the first in
+// bits 0..15). Both differences are exact in float32 (each operand pair lies within a factor of
+// two of the rounded value's binade), so hi + mid + lo equals p to within 2^-26 of |p|: three
+// bf16 MFMAs against the three terms compute P.V at float32 precision, where one bf16 P would
+// lose up to 2^-9 of every probability.
+struct Bf16x2Terms {
+  uint32_t hi, mid, lo;
+};
+__device__ __forceinline__ Bf16x2Terms split3_bf16x2(float p0, float p1) {
+  Bf16x2Terms t;
+  t.hi = pack_bf16x2(p0, p1);
+  const float r0 = p0 - bits_f32(t.hi << 16), r1 = p1 - bits_f32(t.hi & 0xffff0000u);
+  t.mid = pack_bf16x2(r0, r1);
+  t.lo = pack_bf16x2(r0 - bits_f32(t.mid << 16), r1 - bits_f32(t.mid & 0xffff0000u));
+  return t;
+}
+
 // ---- wave-level reductions (wave64) ----------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

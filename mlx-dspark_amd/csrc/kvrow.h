@@ -9,14 +9,14 @@
 namespace dsk {
 
 // ----------------------------------------------------------------------------- row helpers
-// RoPE angle in fp32 as the reference computes it, reduced to [-1/2, 1/2) revolutions for
-// v_sin_f32 / v_cos_f32 (the reduction error is below the angle's own rounding).
+// RoPE angle in fp32 as the reference computes it (pos * inv_freq rounded once), with the
+// library's sine and cosine of that float32 angle (full argument reduction, a few ulp). A float32
+// reduction to revolutions for v_sin_f32 / v_cos_f32 would be off by up to |angle| * 2^-24
+// revolutions (2.5e-4 rad at position 4096 for the fastest frequency), about an eighth of a bf16
+// step of the rotated values, enough to flip their rounding at long contexts.
 __device__ __forceinline__ void rope_sincos(int pos, float inv_freq, float& sn, float& cs) {
   const float ang = (float)pos * inv_freq;
-  float rev = ang * 0.15915494309189535f;
-  rev -= rintf(rev);
-  sn = __builtin_amdgcn_sinf(rev);
-  cs = __builtin_amdgcn_cosf(rev);
+  sincosf(ang, &sn, &cs);
 }
 
 // One head row of HD dims spread over L consecutive lanes (L = 64: a wave; L = 16: a quarter

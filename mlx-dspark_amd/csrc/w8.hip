@@ -21,7 +21,8 @@
 //   activation in its epilogue.
 //
 // W4 (dsk_w4_gemm): the same tiles with two codes per byte (8 bytes per lane per tile-group),
-// converted to 128 + q in bf16 by byte permutes, the 128 * sum x term folded into the bias.
+// converted to 1 + q/16 in bf16 by byte permutes, the scale taken 16 times and the sum x term
+// folded into the bias.
 //
 // GEMM arithmetic. With w = s*q + b per group, sum_k x_k w_k = s * sum x_k q_k + b * sum x_k.
 // q (0..255) is exact in bf16, the bf16 activations go to the MFMA unchanged, so the MFMA
@@ -410,18 +411,23 @@ __device__ __forceinline__ void gemm_store_gated(const GemmArgs& a, int m, int64
 // One batch of U groups: the weight, scale/bias and activation registers of U consecutive
 // groups for NT tiles. Padding rows of the packed activation hold arbitrary values; their
 // outputs are never stored.
-// 16 4-bit codes (8 bytes, byte j = codes 2j | 2j+1 << 4) -> two bf16 x 8 holding 128 + code
-// (exact: 0x4300 | c is the bf16 of 128 + c); the group's bias is offset by -128 s to match.
+// 16 4-bit codes (8 bytes, byte j = codes 2j | 2j+1 << 4) -> two bf16 x 8 holding 1 + code / 16
+// (exact: 0x3f80 | c << 3 is the bf16 of 1 + c / 16, c in the top four mantissa bits); the group
+// then adds 16 s (x . (1 + q/16)) + (b - 16 s) X. A form 128 + c (0x4300 | c) would need no shift,
+// but its products are ~135 x against ~7.5 x for the codes themselves, so the float32 rounding of
+// the accumulated products, left over when the 128 X is subtracted again, would be ~18 times that
+// of the exact codes; with 1 + c/16 the offset is ~3 times the codes' part.
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void u4x16_to_bf16(const u32x2 w, bf16x8& lo, bf16x8& hi) {
   uint32_t r[8];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const uint32_t v = w[h];
-    const uint32_t t = v & 0x0f0f0f0fu, u = (v >> 4) & 0x0f0f0f0fu;  // even / odd codes, one per byte
+    // even / odd codes times 8, one per byte (8 c < 128: no carry into the next byte)
+    const uint32_t t = (v << 3) & 0x78787878u, u = (v >> 1) & 0x78787878u;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      r[4 * h + i] = __builtin_amdgcn_perm(u, t, 0x0c040c00u + 0x00010001u * i) | 0x43004300u;
+      r[4 * h + i] = __builtin_amdgcn_perm(u, t, 0x0c040c00u + 0x00010001u * i) | 0x3f803f80u;
   }
   lo = __builtin_bit_cast(bf16x8, (u32x4{r[0], r[1], r[2], r[3]}));
   hi = __builtin_bit_cast(bf16x8, (u32x4{r[4], r[5], r[6], r[7]}));
@@ -480,13 +486,14 @@ __device__ __forceinline__ void batch_compute(const Batch<MT, NT, U, BITS>& r, f
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       bf16x8 b0, b1;
-      const float s = bf16_to_f32((uint16_t)(r.sv[c][j] & 0xffffu));
+      float s = bf16_to_f32((uint16_t)(r.sv[c][j] & 0xffffu));
       float bb = bf16_to_f32((uint16_t)(r.sv[c][j] >> 16));
       if constexpr (BITS == 8) {
         u8x16_to_bf16(r.wv[c][j], b0, b1);
       } else {
         u4x16_to_bf16(r.wv[c][j], b0, b1);
-        bb = fmaf(-128.0f, s, bb);  // x . (128 + q) = 128 X + x . q
+        bb = fmaf(-16.0f, s, bb);  // s q + b = 16 s (1 + q/16) + (b - 16 s)
+        s *= 16.0f;
       }
 #pragma unroll
       for (int i = 0; i < MT; ++i) {

@@ -40,6 +40,8 @@ here are this build's choice, covered by the logits tolerance.
 
 from __future__ import annotations
 
+import contextlib
+
 import numpy as np
 import torch
 
@@ -50,7 +52,52 @@ def bf(x: torch.Tensor) -> torch.Tensor:
     return x.to(torch.bfloat16).to(torch.float32)
 
 
+# Float64 sums. Inside ``with exact_sums():`` every reduction (projections, attention, the
+# norms' mean squares) and every elementwise chain between two rounding points runs in float64
+# and is rounded once to float32: an evaluation of the same bf16 rounding points whose float32
+# values are correctly rounded. Its distance from the plain float32 evaluation is how far two
+# valid implementations of one rounding-point graph drift apart (other summation orders move a
+# value by a few float32 ulp, and every later bf16 rounding that such a move flips passes on a
+# whole bf16 step): the noise floor of the logits metric for that model and input.
+_EXACT = [False]
+
+
+@contextlib.contextmanager
+def exact_sums(on: bool = True):
+    prev = _EXACT[0]
+    _EXACT[0] = on
+    try:
+        yield
+    finally:
+        _EXACT[0] = prev
+
+
+def _dt():
+    return torch.float64 if _EXACT[0] else torch.float32
+
+
+def mm(x, w):
+    """x [M, K] . w [N, K]^T in float32 (float64, rounded once, under exact_sums)."""
+    if not _EXACT[0]:
+        return x @ w.T
+    xd = x.double()
+    out = torch.empty(x.shape[0], w.shape[0], dtype=torch.float32)
+    for n0 in range(0, w.shape[0], 16384):
+        out[:, n0:n0 + 16384] = (xd @ w[n0:n0 + 16384].double().T).float()
+    return out
+
+
+def silu(x):
+    if _EXACT[0]:
+        xd = x.double()
+        return (xd * torch.sigmoid(xd)).float()
+    return x * torch.sigmoid(x)
+
+
 def rmsnorm(x, w, eps):
+    if _EXACT[0]:
+        xd = x.double()
+        return (xd * torch.rsqrt((xd * xd).mean(-1, keepdim=True) + eps) * w.double()).float()
     return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) * w
 
 
@@ -59,6 +106,9 @@ def norm_later(x, w, eps):
     applies it (the consuming GEMM scales its output rows): returns (bf16(x * w), r) with
     r = rsqrt(mean(x^2) + eps) per row, so r * (bf16(x * w) @ W^T) is rmsnorm(x, w) @ W^T up
     to where the product is rounded."""
+    if _EXACT[0]:
+        xd = x.double()
+        return bf(x * w), torch.rsqrt((xd * xd).mean(-1, keepdim=True) + eps).float()
     return bf(x * w), torch.rsqrt((x * x).mean(-1, keepdim=True) + eps)
 
 
@@ -74,36 +124,102 @@ def inv_freq(hd: int, theta: float, rotary_fraction: float = 1.0) -> torch.Tenso
     return torch.from_numpy(inv.astype(np.float32))
 
 
-def rope(x, pos, theta, inv=None):
-    """rotate-half RoPE; x [..., n, hd], pos [n]; inv overrides the theta frequencies."""
+def rope(x, pos, theta, inv=None, revolutions: bool = False):
+    """rotate-half RoPE; x [..., n, hd], pos [n]; inv overrides the theta frequencies. The angle
+    is pos * inv rounded to float32; its sine and cosine are those of that float32 angle.
+    revolutions=True instead reduces the float32 angle to revolutions in float32 first
+    (ang * 1/(2 pi), minus the nearest integer) and takes sin / cos of 2 pi times that: the
+    hardware sine's argument form, off by up to |ang| * 2^-24 revolutions (a rounding source
+    the decomposition in tests/test_rounding_sources.py measures)."""
     hd = x.shape[-1]
     if inv is None:
         inv = torch.from_numpy((theta ** (-2.0 * np.arange(hd // 2) / hd)).astype(np.float32))
     ang = pos.float()[:, None] * inv[None, :]
-    c, s = torch.cos(ang), torch.sin(ang)
+    if revolutions:
+        rev = ang * torch.tensor(0.15915494309189535, dtype=torch.float32)
+        ang = (rev - torch.round(rev)).double() * (2.0 * np.pi)
+    if _EXACT[0] or revolutions:
+        a = ang.double()
+        c, s = torch.cos(a), torch.sin(a)
+        if not _EXACT[0]:
+            c, s = c.float(), s.float()
+    else:
+        c, s = torch.cos(ang), torch.sin(ang)
     x1, x2 = x[..., : hd // 2], x[..., hd // 2:]
+    if _EXACT[0]:
+        x1, x2 = x1.double(), x2.double()
+        return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1).float()
     return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1)
 
 
-def sdpa(q, K, V, scale, mask=None, p_bf16=False):
+def _blocks_attend(s, V, split, block, p_bf16, partial_bf16, exp2_c):
+    """Attention of score rows s [W, L] (scaled, -inf where masked) over V [L, hd] as split
+    kernels compute it: keys in splits of ``split`` (one split: the whole range), inside a split
+    one max per ``block`` keys (the offset the exponent is taken from, which decides how P rounds
+    under p_bf16), each split's output normalised (rounded to bf16 with partial_bf16) and the
+    splits merged with weights exp(m_s - M) * l_s. exp2_c: exp(s - m) as 2^(s c - m c) with
+    c = log2(e) rounded to float32 (the kernels' exp2 form, scale already in s)."""
+    dt = s.dtype
+    L = s.shape[1]
+    step = split or L
+    ninf = float("-inf")
+    parts = []
+    for j0 in range(0, L, step):
+        sj, vj = s[:, j0:j0 + step], V[j0:j0 + step]
+        bstep = block or sj.shape[1]
+        bm, bl, bo = [], [], []
+        for b0 in range(0, sj.shape[1], bstep):
+            sb, vb = sj[:, b0:b0 + bstep], vj[b0:b0 + bstep]
+            m = sb.max(dim=-1, keepdim=True).values
+            m0 = torch.where(torch.isinf(m), torch.zeros_like(m), m)
+            p = torch.exp2(sb * exp2_c - m0 * exp2_c) if exp2_c else torch.exp(sb - m0)
+            if p_bf16:
+                p = bf(p).to(dt)
+            bm.append(m)
+            bl.append(p.sum(dim=-1, keepdim=True))
+            bo.append(p @ vb)
+        M = torch.stack(bm).max(0).values
+        w = [torch.where(torch.isinf(m), torch.zeros_like(m), torch.exp(m - M)) for m in bm]
+        l = sum(a * b for a, b in zip(bl, w))
+        o = sum(a * b for a, b in zip(bo, w)) / torch.where(l > 0, l, torch.ones_like(l))
+        if partial_bf16 and step < L:
+            o = bf(o).to(dt)
+        parts.append((M, l, o))
+    if len(parts) == 1:
+        return parts[0][2]
+    M = torch.stack([p[0] for p in parts]).max(0).values
+    w = [torch.where(torch.isinf(m), torch.zeros_like(m), torch.exp(m - M)) * l for m, l, _ in parts]
+    den = sum(w)
+    o = sum(p[2] * x for p, x in zip(parts, w))
+    return o / torch.where(den > 0, den, torch.ones_like(den))
+
+
+def sdpa(q, K, V, scale, mask=None, p_bf16=False, *, split=0, block=0, partial_bf16=False, exp2=False):
     """q [W, nq, hd], K/V [L, nkv, hd] -> [W, nq, hd]; GQA by head index // (nq/nkv).
     p_bf16: the unnormalised probabilities exp(s - max) are rounded to bf16 before they weight
     V and before they are summed for the normaliser (where a bf16 attention kernel rounds them);
-    otherwise the softmax stays float32."""
+    otherwise the softmax stays float32. split / block / partial_bf16 / exp2: the split
+    kernels' evaluation order (_blocks_attend), for the rounding-source decomposition."""
     W, nq, hd = q.shape
     nkv = K.shape[1]
     G = nq // nkv
-    out = torch.empty(W, nq, hd)
+    dt = _dt()
+    out = torch.empty(W, nq, hd, dtype=dt)
+    plain = not (split or block or partial_bf16 or exp2)
+    c2 = float(np.float32(1.4426950408889634)) if exp2 else 0.0
     for h in range(nq):
-        s = (q[:, h] @ K[:, h // G].T) * scale
+        Kh, Vh = K[:, h // G].to(dt), V[:, h // G].to(dt)
+        s = (q[:, h].to(dt) @ Kh.T) * scale
         if mask is not None:
             s = s.masked_fill(~mask, float("-inf"))
-        if p_bf16:
-            p = bf(torch.exp(s - s.max(dim=-1, keepdim=True).values))
-            out[:, h] = (p @ V[:, h // G]) / p.sum(dim=-1, keepdim=True)
+        if not plain:
+            out[:, h] = _blocks_attend(s, Vh, split, block, p_bf16, partial_bf16, c2)
+        elif p_bf16:
+            p = bf(torch.exp(s - s.max(dim=-1, keepdim=True).values)).to(dt)
+            out[:, h] = (p @ Vh) / p.sum(dim=-1, keepdim=True)
         else:
-            out[:, h] = torch.softmax(s, dim=-1) @ V[:, h // G]
-    return out
+            out[:, h] = torch.softmax(s, dim=-1) @ Vh
+    return out.float()
 
 
 def causal_mask(offset: int, W: int, window: int = 0) -> torch.Tensor:
@@ -119,6 +235,9 @@ def causal_mask(offset: int, W: int, window: int = 0) -> torch.Tensor:
 
 def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
     """tanh-approximated GeLU (gemma's gelu_pytorch_tanh)."""
+    if _EXACT[0]:
+        xd = x.double()
+        return (0.5 * xd * (1.0 + torch.tanh(0.7978845608028654 * (xd + 0.044715 * xd * xd * xd)))).float()
     return 0.5 * x * (1.0 + torch.tanh(0.7978845608028654 * (x + 0.044715 * x * x * x)))
 
 
@@ -167,12 +286,26 @@ class OracleLayer:
 class OracleTarget:
     """Dense-KV CPU model built from a GPU model created with keep_mlx=True."""
 
-    def __init__(self, model, kv_bits=None, double_round: bool = False, p_bf16: bool = False):
+    def __init__(self, model, kv_bits=None, double_round: bool = False, p_bf16: bool = False, *,
+                 norm_first: bool = False, split: int = 0, p_block: int = 0, partial_bf16: bool = False,
+                 exp2: bool = False, rope_revolutions: bool = False, requant_new: bool = True):
+        """Rounding-point options (each default is the reference-order evaluation; the others
+        exist to measure one source at a time): double_round rounds a projection's output to
+        bf16 before its residual add; p_bf16 rounds the attention probabilities to bf16;
+        norm_first normalises the Qwen3 layout's rows before their projections (bf16 normalised
+        rows, as an unfused graph does) instead of after them; split / p_block / partial_bf16 /
+        exp2 evaluate attention the way split kernels do (sdpa); rope_revolutions takes the
+        RoPE sine in float32 revolutions (rope); requant_new=False keeps the new K/V rows in
+        bf16 in an 8-bit cache (the re-quantisation of the new rows switched off)."""
         a = model.args
         self.a = a
         self.kv_bits = kv_bits
         self.rr = bf if double_round else (lambda x: x)
         self.p_bf16 = p_bf16
+        self.norm_first = norm_first
+        self.attn_opts = dict(split=split, block=p_block, partial_bf16=partial_bf16, exp2=exp2)
+        self.rope_revolutions = rope_revolutions
+        self.requant_new = requant_new
         self.layers = [OracleLayer(L, a.num_attention_heads, a.num_key_value_heads, a.head_dim) for L in model.layers]
         self.embed = deq_table(model.embed)
         self.lm_head = deq(model.lm_head)
@@ -212,49 +345,52 @@ class OracleTarget:
         # the Qwen3 layout's norms are applied after their projections (norm_later); the
         # Gemma-style layout normalises before them
         sandwich = bool(getattr(a, "sandwich_norms", False))
+        first = sandwich or self.dense or self.norm_first
+        rev = self.rope_revolutions
         captured = []
         for l, L in enumerate(self.layers):
             win = a.window(l)
             theta = (a.rope_local_base_freq or a.rope_theta) if a.is_sliding(l) else a.rope_theta
-            if sandwich or self.dense:
-                qkv = bf(bf(rmsnorm(h, L.in_norm, eps)) @ self._w(l, "wq").T)
+            if first:
+                qkv = bf(mm(bf(rmsnorm(h, L.in_norm, eps)), self._w(l, "wq")))
             else:
                 xg, r = norm_later(h, L.in_norm, eps)
-                qkv = bf(r * (xg @ L.wq.T))
+                qkv = bf(r * mm(xg, L.wq))
             q = qkv[:, : nq * hd].view(W, nq, hd)
             k = qkv[:, nq * hd:(nq + nkv) * hd].view(W, nkv, hd)
             v = qkv[:, (nq + nkv) * hd:].view(W, nkv, hd)
-            q = bf(rope(bf(rmsnorm(q, L.q_norm, eps)).transpose(0, 1), pos, theta).transpose(0, 1))
-            k = bf(rope(bf(rmsnorm(k, L.k_norm, eps)).transpose(0, 1), pos, theta).transpose(0, 1))
-            if self.kv_bits == 8:
+            q = bf(rope(bf(rmsnorm(q, L.q_norm, eps)).transpose(0, 1), pos, theta, revolutions=rev).transpose(0, 1))
+            k = bf(rope(bf(rmsnorm(k, L.k_norm, eps)).transpose(0, 1), pos, theta, revolutions=rev).transpose(0, 1))
+            if self.kv_bits == 8 and self.requant_new:
                 k, v = kv_quant_roundtrip(k), kv_quant_roundtrip(v)
             self.K[l] = torch.cat([self.K[l], k])
             self.V[l] = torch.cat([self.V[l], v])
-            o = bf(sdpa(q, self.K[l], self.V[l], a.attn_scale, causal_mask(self.offset, W, win), self.p_bf16))
+            o = bf(sdpa(q, self.K[l], self.V[l], a.attn_scale, causal_mask(self.offset, W, win), self.p_bf16,
+                        **self.attn_opts))
             if L.attn_out_norm is not None:     # sandwich: norm the projection output, then add
-                h = bf(h + bf(rmsnorm(bf(o.reshape(W, -1) @ L.wo.T), L.attn_out_norm, eps)))
+                h = bf(h + bf(rmsnorm(bf(mm(o.reshape(W, -1), L.wo)), L.attn_out_norm, eps)))
             else:
-                h = bf(h + self.rr(o.reshape(W, -1) @ self._w(l, "wo").T))
-            if sandwich or self.dense:
-                gu = bf(bf(rmsnorm(h, L.post_norm, eps)) @ self._w(l, "wgu").T)
+                h = bf(h + self.rr(mm(o.reshape(W, -1), self._w(l, "wo"))))
+            if first:
+                gu = bf(mm(bf(rmsnorm(h, L.post_norm, eps)), self._w(l, "wgu")))
             else:
                 xg, r = norm_later(h, L.post_norm, eps)
-                gu = bf(r * (xg @ L.wgu.T))
+                gu = bf(r * mm(xg, L.wgu))
             I = gu.shape[1] // 2
             g, u = gu[:, :I], gu[:, I:]
-            act = bf(bf(gelu_tanh(g) if gelu else g * torch.sigmoid(g)) * u)
+            act = bf(bf(gelu_tanh(g) if gelu else silu(g)) * u)
             if L.ff_out_norm is not None:
-                h = bf(h + bf(rmsnorm(bf(act @ L.wd.T), L.ff_out_norm, eps)))
+                h = bf(h + bf(rmsnorm(bf(mm(act, L.wd)), L.ff_out_norm, eps)))
             else:
-                h = bf(h + self.rr(act @ self._w(l, "wd").T))
+                h = bf(h + self.rr(mm(act, self._w(l, "wd"))))
             if l in tap:
                 captured.append(h)
         self.offset += W
-        if sandwich:
-            logits = bf(rmsnorm(h, self.norm, eps)) @ self.lm_head.T
+        if sandwich or self.norm_first:
+            logits = mm(bf(rmsnorm(h, self.norm, eps)), self.lm_head)
         else:
             xg, r = norm_later(h, self.norm, eps)
-            logits = r * (xg @ self.lm_head.T)
+            logits = r * mm(xg, self.lm_head)
         cap = getattr(a, "final_logit_softcapping", None)
         if cap:
             logits = torch.tanh(logits / cap) * cap
@@ -301,15 +437,15 @@ class OracleDFlash:
         h = bf(self.target.embed[ids] * self.target.a.embed_scale)
         th = target_hidden.reshape(-1, target_hidden.shape[-1]).float()
         S = th.shape[0]
-        h_ctx = bf(rmsnorm(bf(th @ self.fc.T), self.hidden_norm, eps))
+        h_ctx = bf(rmsnorm(bf(mm(th, self.fc)), self.hidden_norm, eps))
         off = self.offset
         for l, Lw in enumerate(self.layers):
             x = bf(rmsnorm(h, Lw.in_norm, eps))
-            qkv = bf(x @ Lw.wq.T)
+            qkv = bf(mm(x, Lw.wq))
             q = qkv[:, : nq * hd].view(L, nq, hd)
             kb = qkv[:, nq * hd:(nq + nkv) * hd].view(L, nkv, hd)
             vb = qkv[:, (nq + nkv) * hd:].view(L, nkv, hd)
-            kvc = bf(h_ctx @ Lw.wq[nq * hd:].T)
+            kvc = bf(mm(h_ctx, Lw.wq[nq * hd:]))
             kc = kvc[:, : nkv * hd].view(S, nkv, hd)
             vc = kvc[:, nkv * hd:].view(S, nkv, hd)
             pq = torch.arange(off + S, off + S + L)
@@ -325,14 +461,14 @@ class OracleDFlash:
             if self._sliding(l):
                 mask = causal_mask(off + S, L, int(c.sliding_window))
             o = bf(sdpa(q, K, Vv, hd ** -0.5, mask, self.p_bf16))
-            h = bf(h + o.reshape(L, -1) @ Lw.wo.T)
+            h = bf(h + mm(o.reshape(L, -1), Lw.wo))
             x = bf(rmsnorm(h, Lw.post_norm, eps))
-            gu = bf(x @ Lw.wgu.T)
+            gu = bf(mm(x, Lw.wgu))
             I = gu.shape[1] // 2
-            act = bf(bf(gu[:, :I] * torch.sigmoid(gu[:, :I])) * gu[:, I:])
-            h = bf(h + act @ Lw.wd.T)
+            act = bf(bf(silu(gu[:, :I])) * gu[:, I:])
+            h = bf(h + mm(act, Lw.wd))
         h = h[logits_start:]
-        return bf(rmsnorm(h, self.norm, eps)) @ self.target.lm_head.T
+        return mm(bf(rmsnorm(h, self.norm, eps)), self.target.lm_head)
 
 
 def normalized_maxdiff(a: torch.Tensor, b: torch.Tensor) -> float:
@@ -414,11 +550,11 @@ class OracleDSpark:
         """(roped normed K, V) [n, nkv, hd] of rows x (model.py:113-124)."""
         c = self.c
         nq, nkv, hd, eps = self.nq, self.nkv, self.hd, c.rms_norm_eps
-        kp = bf(x @ L.wq[nq * hd:(nq + nkv) * hd].T).view(n, nkv, hd)
+        kp = bf(mm(x, L.wq[nq * hd:(nq + nkv) * hd])).view(n, nkv, hd)
         if self.gemma and c.attention_k_eq_v:
             v = bf(rmsnorm(kp, torch.ones(hd), eps))
         else:
-            v = bf(x @ L.wq[(nq + nkv) * hd:].T).view(n, nkv, hd)
+            v = bf(mm(x, L.wq[(nq + nkv) * hd:])).view(n, nkv, hd)
             if c.use_v_norm:
                 v = bf(rmsnorm(v, torch.ones(hd), eps))
         k = bf(rope(bf(rmsnorm(kp, L.k_norm, eps)).transpose(0, 1), pos, c.rope_theta, self.inv).transpose(0, 1))
@@ -429,7 +565,7 @@ class OracleDSpark:
         eps = c.rms_norm_eps
         th = torch.as_tensor(target_hidden).reshape(-1, self.fc.shape[1]).float()
         S = th.shape[0]
-        fused = bf(rmsnorm(bf(th @ self.fc.T), self.hidden_norm, eps))
+        fused = bf(rmsnorm(bf(mm(th, self.fc)), self.hidden_norm, eps))
         pos = torch.arange(self.length, self.length + S)
         for l, L in enumerate(self.layers):
             k, v = self._kv(L, fused, S, pos)
@@ -448,29 +584,29 @@ class OracleDSpark:
         pos = torch.arange(self.length, self.length + k)
         for l, L in enumerate(self.layers):
             x = bf(rmsnorm(h, L.in_norm, eps))
-            q = bf(x @ L.wq[: nq * hd].T).view(k, nq, hd)
+            q = bf(mm(x, L.wq[: nq * hd])).view(k, nq, hd)
             q = bf(rope(bf(rmsnorm(q, L.q_norm, eps)).transpose(0, 1), pos, c.rope_theta, self.inv).transpose(0, 1))
             kb, vb = self._kv(L, x, k, pos)
             o = bf(sdpa(q, torch.cat([self.K[l], kb]), torch.cat([self.V[l], vb]), c.scaling, None, self.p_bf16))
             if self.gemma:     # sandwich norms, tanh-GeLU, layer_scalar (model.py:172-184)
-                h = bf(h + bf(rmsnorm(bf(o.reshape(k, -1) @ L.wo.T), L.attn_out_norm, eps)))
+                h = bf(h + bf(rmsnorm(bf(mm(o.reshape(k, -1), L.wo)), L.attn_out_norm, eps)))
                 x = bf(rmsnorm(h, L.post_norm, eps))
-                gu = bf(x @ L.wgu.T)
+                gu = bf(mm(x, L.wgu))
                 I = gu.shape[1] // 2
                 act = bf(bf(gelu_tanh(gu[:, :I])) * gu[:, I:])
-                h = bf(h + bf(rmsnorm(bf(act @ L.wd.T), L.ff_out_norm, eps)))
+                h = bf(h + bf(rmsnorm(bf(mm(act, L.wd)), L.ff_out_norm, eps)))
                 if self.scalars is not None and self.scalars[l] != 1.0:
                     h = bf(h * self.scalars[l])
             else:
-                h = bf(h + o.reshape(k, -1) @ L.wo.T)
+                h = bf(h + mm(o.reshape(k, -1), L.wo))
                 x = bf(rmsnorm(h, L.post_norm, eps))
-                gu = bf(x @ L.wgu.T)
+                gu = bf(mm(x, L.wgu))
                 I = gu.shape[1] // 2
-                h = bf(h + bf(bf(gu[:, :I] * torch.sigmoid(gu[:, :I])) * gu[:, I:]) @ L.wd.T)
+                h = bf(h + mm(bf(bf(silu(gu[:, :I])) * gu[:, I:]), L.wd))
         return bf(rmsnorm(h, self.norm, eps))
 
     def base_logits(self, block_ids, cap):
-        logits = self.block_hidden(block_ids)[:cap] @ self.lm_head.T
+        logits = mm(self.block_hidden(block_ids)[:cap], self.lm_head)
         cap_ = self.c.final_logit_softcapping
         return torch.tanh(logits / cap_) * cap_ if cap_ else logits
 
@@ -492,8 +628,11 @@ class OracleDSpark:
         return toks
 
     def confidence_logits(self, hidden_rows, prev_ids):
+        """proj(feats) + bias per row (src/mlx_dspark/model.py:211-217, :311-320): feats are the
+        block hidden rows, followed by the Markov head's previous-token embeddings w1[prev]
+        (bf16 rows) when config.confidence_head_with_markov is set."""
         feats = torch.as_tensor(hidden_rows).float()
-        if self.w1 is not None:
+        if self.c.confidence_head_with_markov:
             feats = torch.cat([feats, bf(self.w1[torch.as_tensor(prev_ids).long()])], dim=-1)
         return feats @ self.conf_w + self.conf_b
 

@@ -1,31 +1,85 @@
-"""Logit agreement for the GPU parity tests, bounded by the bf16 noise floor of the metric.
+"""Logit agreement for the GPU parity tests.
 
-Two oracles that differ only in whether the attention probabilities are rounded to bf16 (as the
-attention kernel rounds them) or kept float32 are both valid bf16 evaluations of the same
-forward. How far apart they are in the RMS-normalised logit metric is the metric's noise floor for
-that model, input and width: 0.046-0.050 max-abs / 0.009 rms at the Qwen3-8B and Qwen3-0.6B
-widths over the full 151936-entry vocabulary (tests/test_gpu_fullwidth.py prints it), 0.02-0.04
-max-abs on the narrow test models. The kernels have several such rounding choices (the RoPE
-angle reduction, the exp of the softmax, bf16 split partials, the 8-bit KV quantizer on slightly
-different inputs) where the floor measures one, so the GPU logits must agree with the
-kernel-matching oracle within 1.5x the floor; the floor replaces the nominal 2e-2 max-abs /
-3e-3 rms only where it is larger."""
+The tolerance is the north star's: max-abs <= 2e-2 between RMS-normalised logit rows of the GPU
+and of the reference-order oracle (float32 softmax), unless the measured noise floor of the case
+is larger. The floor is the distance between two valid evaluations of the oracle's own
+rounding-point graph: the float32 oracle and its twin with float64 sums (oracle.model.exact_sums,
+each value between two rounding points correctly rounded). Every bf16 rounding that a few float32
+ulp of difference flips passes on a whole bf16 step, so any implementation with other summation
+orders (the GPU's MFMA tiles, split-K slices, attention splits) lands about that far from the
+oracle: at the benchmark widths with random weights the floor is 0.02-0.04, above 2e-2
+(tests/test_rounding_sources.py measures it on a 2-layer Qwen3-8B-width model, with the
+contribution of each rounding source alone).
+
+The GPU is then a third valid evaluation, and its distance to the oracle scatters around the
+floor: over the 31 logits checks of the GPU suite the ratio of the GPU's distance to the floor
+measured 0.62-1.27 in max-abs and 0.68-1.09 in rms. The rms is a stable statistic and is held to
+FLOOR_SCATTER_RMS times the floor's rms; the max-abs is the largest of a few thousand to a few
+million entries with a heavy tail (an 8-bit K/V code flip moves a whole group of 64 values), and
+is held to FLOOR_SCATTER times the floor's max-abs. Where 2e-2 is larger it is the bound, and the
+rms then stays below the rms of noise whose largest entry over the N compared entries would be
+2e-2 (2e-2 / sqrt(2 ln N)), so a systematic offset below the max-abs bound still fails."""
+
+import math
+
+import torch
 
 from oracle import model as OM
 
-HEADROOM = 1.5
-NOMINAL_MAX, NOMINAL_RMS = 2e-2, 3e-3
+NOMINAL_MAX = 2e-2
+FLOOR_SCATTER = 1.5
+FLOOR_SCATTER_RMS = 1.25
 
 
-def check_logits(got, want, want_alt, what=""):
-    """got: GPU logits; want: the oracle with bf16 attention probabilities; want_alt: the same
-    oracle with float32 probabilities (the floor's second evaluation)."""
-    fmax, frms = OM.logit_diff(want, want_alt)
+class Twin:
+    """An oracle and its float64-sums twin, driven by the same calls: a method call returns
+    the pair (float32 result, float64-sums result). Attribute writes go to both."""
+
+    def __init__(self, make):
+        object.__setattr__(self, "_pair", (make(), make()))
+
+    def _both(self, fa, fb):
+        def call(*args, **kw):
+            ra = fa(*args, **kw)
+            with OM.exact_sums():
+                rb = fb(*args, **kw)
+            return ra, rb
+        return call
+
+    def __getattr__(self, name):
+        fa, fb = (getattr(o, name) for o in self._pair)
+        return self._both(fa, fb) if callable(fa) else fa
+
+    def __setattr__(self, name, value):
+        for o in self._pair:
+            setattr(o, name, value)
+
+    def __call__(self, *args, **kw):
+        return self._both(*self._pair)(*args, **kw)
+
+    @property
+    def f32(self):
+        return self._pair[0]
+
+
+def logit_floor(want, exact):
+    """(max-abs, rms) between the float32 and the float64-sums oracle."""
+    return OM.logit_diff(want, exact)
+
+
+def check_logits(got, want, what="", exact=None, floor=None):
+    """got: GPU logits; want: the reference-order oracle's logits (float32 softmax); exact: the
+    same oracle's float64-sums logits (or floor: their (max-abs, rms) measured by the caller)."""
+    if exact is not None:
+        floor = logit_floor(want, exact)
     mx, rms = OM.logit_diff(got, want)
-    bmax, brms = HEADROOM * max(fmax, NOMINAL_MAX), HEADROOM * max(frms, NOMINAL_RMS)
-    print(f"{what}: normalised max-abs {mx:.4f} rms {rms:.5f} (floor {fmax:.4f} / {frms:.5f}; "
-          f"bound {bmax:.4f} / {brms:.5f})", flush=True)
-    assert mx <= bmax and rms <= brms, (what, mx, rms, fmax, frms)
+    n = max(2, torch.as_tensor(want).numel())
+    bmax, brms = NOMINAL_MAX, NOMINAL_MAX / math.sqrt(2.0 * math.log(n))
+    if floor is not None:
+        bmax, brms = max(bmax, FLOOR_SCATTER * floor[0]), max(brms, FLOOR_SCATTER_RMS * floor[1])
+    fl = "" if floor is None else f"; floor {floor[0]:.4f} / {floor[1]:.5f}"
+    print(f"{what}: normalised max-abs {mx:.4f} rms {rms:.5f} (bound {bmax:.4f} / {brms:.5f}{fl})", flush=True)
+    assert mx <= bmax and rms <= brms, (what, mx, rms, bmax, brms)
     return bmax
 
 
@@ -44,6 +98,15 @@ def check_greedy_stream(model, prompt, got, min_match: int, tol: float = STREAM_
     ot = oracle or OM.OracleTarget(model)
     logits, _ = ot.forward(list(prompt) + got[:-1])
     rows = logits[len(prompt) - 1:]
+    if oracle is None:
+        # the rows' noise floor: the same forward with float64 sums
+        with OM.exact_sums():
+            erows = OM.OracleTarget(model).forward(list(prompt) + got[:-1])[0][len(prompt) - 1:]
+        floor = OM.logit_diff(rows, erows)[0]
+        if FLOOR_SCATTER * floor > tol:
+            print(f"greedy stream: margin tolerance {FLOOR_SCATTER * floor:.4f} ({FLOOR_SCATTER} x the rows' "
+                  f"floor {floor:.4f}) in place of {tol}", flush=True)
+            tol = FLOOR_SCATTER * floor
     exact = 0
     for i, t in enumerate(got):
         rn = rows[i] / rows[i].pow(2).mean().sqrt()

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from oracle import accept as OA
-from _parity import check_logits, check_greedy_stream
+from _parity import Twin, check_logits, check_greedy_stream
 from oracle import model as OM
 
 pytestmark = pytest.mark.gpu
@@ -105,14 +105,14 @@ def test_dspark_drafter_matches_oracle(dev, pair):
     _, fused = model.prefill(prompt, cache, list(cfg.target_layer_ids))
     dcache = d.make_ctx_cache(max_ctx=256)
     d.update_context(fused[0], 0, dcache)
-    od, oa = OM.OracleDSpark(d, p_bf16=True), OM.OracleDSpark(d)
-    od.update_context(fused[0].float().cpu())
+    oa = Twin(lambda: OM.OracleDSpark(d))
     oa.update_context(fused[0].float().cpu())
+    od = oa.f32
     block = torch.tensor([[int(prompt[-1])] + [cfg.mask_token_id] * (cfg.block_size - 1)], dtype=torch.int32,
                          device=dev)
     got = d.block_logits(block, dcache, 4)[0]
-    want = od.base_logits(block.cpu()[0], 4)
-    check_logits(got, want, oa.base_logits(block.cpu()[0], 4), "dspark block logits")
+    want, ex = oa.base_logits(block.cpu()[0], 4)
+    check_logits(got, want, "dspark block logits", exact=ex)
     # the reference-shaped entry points agree with the fused one
     noise = d.embed(block)
     hid = d.backbone(noise, dcache.lengths[0], dcache)

@@ -1,11 +1,24 @@
-"""GPU parity of the verify forward at the workloads' real widths: two decoder layers of the
-Qwen3-8B shape (hidden 4096, 32 q / 8 kv heads, head_dim 128, SwiGLU 12288) over a 4096-token
-8-bit KV context with a 16-row verify block, and two layers of the Qwen3-0.6B shape (hidden
-1024, 16 / 8 heads, tied head) over a 768-token bf16 context with a 9-row block, each with the
-full 151936-row vocabulary head and random norm gains. The context is written straight into the
-paged cache (random keys and values, 8-bit quantized with the engine's rule where the cache is
-8-bit) and the oracle attends to the same dequantized values, so the oracle only runs the
-verify rows."""
+"""GPU parity at the workloads' real widths, against the reference-order oracle (float32
+softmax), bounded by the north star's 2e-2 or by the measured noise floor where that is larger
+(tests/_parity.py): the oracle against the same oracle with float64 sums, two valid evaluations
+of one rounding-point graph, measured here on each case's own model and inputs.
+
+Targets (two decoder layers each, the full vocabulary head, random norm gains):
+  - Qwen3-8B shape (hidden 4096, 32 q / 8 kv heads, head_dim 128, SwiGLU 12288) over a
+    4096-token 8-bit KV context with verify blocks of 16, 47 and 64 rows;
+  - Qwen3-0.6B shape (hidden 1024, 16 / 8 heads, tied head) over a 768-token bf16 context, 9 rows;
+  - Gemma-style 12B shape (hidden 3840, 16 / 8 heads, head_dim 256, GeGLU 15360, 262144-row tied
+    head with soft-cap 30, sandwich norms): a sliding-window (1024) layer and a global layer
+    over an 8192-token bf16 context, 9 rows.
+The context is written straight into the paged cache (random keys and values, 8-bit quantized
+with the engine's rule where the cache is 8-bit) and the oracle attends to the same values, so
+the oracle only runs the verify rows.
+Drafters:
+  - DFlash at the Qwen3-8B width with 4-bit linears (2 layers, block 16, 5 taps) bound to the
+    Qwen3-8B-width target's embedding and head, over 1024 context rows;
+  - DSpark at the Qwen3-0.6B width with 4-bit linears (1 layer, taps of 3 layers, k = 8) over
+    512 context rows, the block logits of 8 rows.
+Context rows of the drafters are random target hidden states (rms ~2, bf16)."""
 
 import numpy as np
 import pytest
@@ -16,10 +29,6 @@ from oracle import model as OM
 from oracle import w8 as W8
 
 pytestmark = pytest.mark.gpu
-
-# Logits are held to the metric's bf16 noise floor, measured in the test (tests/_parity.py); the
-# rms of the difference also stays below an absolute 1.5e-2.
-RMS_ABS = 1.5e-2
 
 
 def _fill_context(cache, l, K, V):
@@ -50,45 +59,128 @@ def _fill_context(cache, l, K, V):
     return held
 
 
-@pytest.mark.parametrize("shape,ctx,W,kv_bits", [("qwen3-8b", 4096, 16, 8), ("qwen3-0.6b", 768, 9, None),
-                                                  ("qwen3-8b", 4096, 47, 8), ("qwen3-8b", 4096, 64, 8)])
-def test_verify_logits_full_width(dev, shape, ctx, W, kv_bits):
+def _oracle_twice(run):
+    """run(exact) -> oracle output; returns (float32 output, floor) with the floor the distance
+    of the float32 evaluation from the float64-sums one."""
+    want = run(False)
+    exact = run(True)
+    w0 = want[0] if isinstance(want, tuple) else want
+    e0 = exact[0] if isinstance(exact, tuple) else exact
+    return want, OM.logit_diff(w0, e0)
+
+
+def _target(shape, layers=2, seed=11, **over):
     from mlx_dspark import synthetic
-    print(f"full-width verify {shape} ctx={ctx} W={W} kv_bits={kv_bits}", flush=True)
     args = synthetic.target_args(shape)
-    args.num_hidden_layers = 2
-    model = synthetic.build_target(args, seed=11, keep_mlx=True)
-    synthetic.randomize_norms(model, seed=12)
+    args.num_hidden_layers = layers
+    for k, v in over.items():
+        setattr(args, k, v)
+    model = synthetic.build_target(args, seed=seed, keep_mlx=True)
+    synthetic.randomize_norms(model, seed=seed + 1)
+    return model
+
+
+CASES = [("qwen3-8b", 4096, 16, 8), ("qwen3-0.6b", 768, 9, None), ("qwen3-8b", 4096, 47, 8),
+         ("qwen3-8b", 4096, 64, 8), ("gemma-12b", 8192, 9, None)]
+
+
+@pytest.mark.parametrize("shape,ctx,W,kv_bits", CASES)
+def test_verify_logits_full_width(dev, shape, ctx, W, kv_bits):
+    print(f"full-width verify {shape} ctx={ctx} W={W} kv_bits={kv_bits}", flush=True)
+    over = {}
+    if shape == "gemma-12b":   # one sliding-window layer and one global layer
+        over["layer_types"] = ("sliding_attention", "full_attention")
+    model = _target(shape, **over)
     a = model.args
     nkv, hd = a.num_key_value_heads, a.head_dim
     cache = model.make_cache(max_ctx=ctx + 64, kv_bits=kv_bits)
     g = torch.Generator().manual_seed(13)
-    refs = {"fp32 softmax": OM.OracleTarget(model, kv_bits=kv_bits),
-            "bf16 probabilities": OM.OracleTarget(model, kv_bits=kv_bits, p_bf16=True)}
+    ref = OM.OracleTarget(model, kv_bits=kv_bits)
+    held = []
     for l in range(a.num_hidden_layers):
         K = 0.4 * torch.randn(ctx, nkv, hd, generator=g)
         V = torch.randn(ctx, nkv, hd, generator=g)
-        Kh, Vh = _fill_context(cache, l, K, V)
-        for r in refs.values():
-            r.K[l], r.V[l] = Kh, Vh
-    for r in refs.values():
-        r.offset = ctx
+        held.append(_fill_context(cache, l, K, V))
     cache.set_lengths([ctx])
     block = torch.randint(0, a.vocab_size, (W,), generator=g)
     ids = block.to(dev, torch.int32).view(1, W)
     logits, fused = model.forward(ids, cache, [0], advance=False)
     torch.cuda.synchronize()
     got = logits[0].float().cpu()
-    outs = {name: r.forward(block, tap=(0,)) for name, r in refs.items()}
-    floor_max, floor_rms = OM.logit_diff(outs["fp32 softmax"][0], outs["bf16 probabilities"][0])
-    print(f"  oracle vs oracle (softmax rounding only): normalised max-abs {floor_max:.4f} rms {floor_rms:.5f}",
-          flush=True)
-    for name, (rl, rf) in outs.items():
-        mx, rms = OM.logit_diff(got, rl)
-        tap = float((fused[0].float().cpu() - rf).abs().max() / rf.abs().max())
-        print(f"  GPU vs oracle with {name}: normalised max-abs {mx:.4f} rms {rms:.5f}; tap rel {tap:.4f}", flush=True)
-    check_logits(got, outs["bf16 probabilities"][0], outs["fp32 softmax"][0], f"{shape} verify logits")
-    assert OM.logit_diff(got, outs["bf16 probabilities"][0])[1] < RMS_ABS
-    tap = float((fused[0].float().cpu() - outs["bf16 probabilities"][1]).abs().max()
-                / outs["bf16 probabilities"][1].abs().max())
+
+    def run(exact):
+        ref.K = [k for k, _ in held]
+        ref.V = [v for _, v in held]
+        ref.offset = ctx
+        with OM.exact_sums(exact):
+            return ref.forward(block, tap=(0,))
+
+    (rl, rf), floor = _oracle_twice(run)
+    check_logits(got, rl, f"{shape} verify logits", floor=floor)
+    if a.final_logit_softcapping:
+        assert float(got.abs().max()) <= a.final_logit_softcapping
+    tap = float((fused[0].float().cpu() - rf).abs().max() / rf.abs().max())
+    print(f"  tap: max-abs relative {tap:.4f}", flush=True)
     assert tap < 2e-2
+
+
+def test_dflash_drafter_full_width(dev):
+    """DFlash (src/mlx_dspark/dflash_model.py:197-208) at the Qwen3-8B width, 4-bit linears,
+    bound to a Qwen3-8B-width target's embedding and W8 head; two rounds (1024, then 5 more
+    context rows)."""
+    from mlx_dspark import synthetic
+    print("full-width DFlash drafter: qwen3-8b width, 4-bit, block 16, 5 taps, 1024 context rows", flush=True)
+    model = _target("qwen3-8b")
+    full = synthetic.target_args("qwen3-8b")       # 36-layer tap ids; the rows below are random
+    d, cfg = synthetic.build_dflash(full, seed=9, keep_mlx=True, num_hidden_layers=2, block_size=16, n_taps=5)
+    synthetic.randomize_norms(d, seed=10)
+    d.bind(model)
+    H, V = full.hidden_size, full.vocab_size
+    g = torch.Generator().manual_seed(5)
+    ctx = (2.0 * torch.randn(1024, 5 * H, generator=g)).to(torch.bfloat16)
+    more = (2.0 * torch.randn(5, 5 * H, generator=g)).to(torch.bfloat16)
+    block = [int(torch.randint(0, V, (1,), generator=g))] + [cfg.mask_token_id] * (cfg.block_size - 1)
+    dcache = d.make_cache(max_ctx=2048)
+    got1 = d(block, ctx.to(dev), dcache, logits_start=1)[0].float().cpu()
+    got2 = d(block, more.to(dev), dcache, logits_start=1)[0].float().cpu()
+    torch.cuda.synchronize()
+    ref_t = OM.OracleTarget(model)
+
+    def run(exact):
+        od = OM.OracleDFlash(d, ref_t)
+        with OM.exact_sums(exact):
+            return od(block, ctx.float(), logits_start=1), od(block, more.float(), logits_start=1)
+
+    w1, w2 = run(False)
+    e1, e2 = run(True)
+    check_logits(got1, w1, "dflash round 1 (1024 context rows)", floor=OM.logit_diff(w1, e1))
+    check_logits(got2, w2, "dflash round 2 (5 more rows)", floor=OM.logit_diff(w2, e2))
+
+
+def test_dspark_drafter_full_width(dev):
+    """DSpark (src/mlx_dspark/model.py:244-309) at the Qwen3-0.6B width, 4-bit linears and
+    tables: context ingest of 512 rows, the 8-row block's logits."""
+    from mlx_dspark import synthetic
+    print("full-width DSpark drafter: qwen3-0.6b width, 4-bit, k = 8, 512 context rows", flush=True)
+    full = synthetic.target_args("qwen3-0.6b")
+    d, cfg = synthetic.build_dspark(full, seed=7, keep_mlx=True, num_hidden_layers=1, block_size=8,
+                                    taps=[1, 14, 27])
+    synthetic.randomize_norms(d, seed=8)
+    H, V = full.hidden_size, full.vocab_size
+    g = torch.Generator().manual_seed(6)
+    ctx = (2.0 * torch.randn(512, 3 * H, generator=g)).to(torch.bfloat16)
+    dcache = d.make_ctx_cache(max_ctx=1024)
+    d.update_context(ctx.to(dev), 0, dcache)
+    block = torch.tensor([[int(torch.randint(0, V, (1,), generator=g))] + [cfg.mask_token_id] * (cfg.block_size - 1)],
+                         dtype=torch.int32, device=dev)
+    got = d.block_logits(block, dcache, cfg.block_size)[0].float().cpu()
+    torch.cuda.synchronize()
+
+    def run(exact):
+        od = OM.OracleDSpark(d)
+        with OM.exact_sums(exact):
+            od.update_context(ctx.float())
+            return od.base_logits(block.cpu()[0], cfg.block_size)
+
+    want, floor = _oracle_twice(run)
+    check_logits(got, want, "dspark block logits (512 context rows)", floor=floor)

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from _parity import check_logits, check_greedy_stream
+from _parity import Twin, check_logits, check_greedy_stream
 from oracle import model as OM
 
 pytestmark = pytest.mark.gpu
@@ -38,17 +38,15 @@ def test_gemma_forward_past_the_window(dev, gemma, kv_bits):
     prompt = rng.integers(0, a.vocab_size, 90).tolist()       # longer than the 32-token window
     cache = model.make_cache(max_ctx=256, kv_bits=kv_bits)
     logits, fused = model.prefill(prompt, cache, [1, 5])
-    ref = OM.OracleTarget(model, kv_bits=kv_bits, p_bf16=True)
-    alt = OM.OracleTarget(model, kv_bits=kv_bits)
-    rl, rf = ref.forward(prompt, [1, 5])
-    al, _ = alt.forward(prompt, [1, 5])
-    check_logits(logits[0, -1], rl[-1], al[-1], "prefill last row")
+    ref = Twin(lambda: OM.OracleTarget(model, kv_bits=kv_bits))
+    (rl, rf), (el, _) = ref.forward(prompt, [1, 5])
+    check_logits(logits[0, -1], rl[-1], "prefill last row", exact=el[-1])
     assert (fused[0].float().cpu() - rf).abs().max() < 0.05 * rf.abs().max()
     assert float(logits.abs().max()) <= 30.0
     block = rng.integers(0, a.vocab_size, 9).tolist()
     vl, _ = model.forward(torch.tensor([block], dtype=torch.int32, device=dev), cache, None, advance=False)
-    rvl, _ = ref.forward(block)
-    check_logits(vl[0], rvl, alt.forward(block)[0], "verify block")
+    (rvl, _), (evl, _) = ref.forward(block)
+    check_logits(vl[0], rvl, "verify block", exact=evl)
 
 
 def test_gemma_window_masks_old_keys(dev, gemma):
@@ -60,16 +58,16 @@ def test_gemma_window_masks_old_keys(dev, gemma):
     prompt = rng.integers(0, model.args.vocab_size, 120).tolist()
     cache = model.make_cache(max_ctx=256)
     lg, _ = model.prefill(prompt, cache)
-    good = OM.OracleTarget(model, p_bf16=True).forward(prompt)[0][-1]
-    good_alt = OM.OracleTarget(model).forward(prompt)[0][-1]
-    bad_t = OM.OracleTarget(model, p_bf16=True)
+    (good, _), (good_ex, _) = Twin(lambda: OM.OracleTarget(model)).forward(prompt)
+    good, good_ex = good[-1], good_ex[-1]
+    bad_t = OM.OracleTarget(model)
     bad_t.a = type(model.args)(**{**model.args.__dict__, "sliding_window": None})
     bad = bad_t.forward(prompt)[0][-1]
     nrm = lambda x: x / x.pow(2).mean().sqrt()
     d_good = float((nrm(lg[0, -1].float().cpu()) - nrm(good)).abs().max())
     d_bad = float((nrm(lg[0, -1].float().cpu()) - nrm(bad)).abs().max())
     print(f"windowed oracle {d_good:.4f}, unwindowed oracle {d_bad:.4f}", flush=True)
-    bound = check_logits(lg[0, -1], good, good_alt, "windowed oracle")
+    bound = check_logits(lg[0, -1], good, "windowed oracle", exact=good_ex)
     assert d_bad > 2 * bound
 
 

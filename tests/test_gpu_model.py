@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from _parity import check_logits, check_greedy_stream
+from _parity import Twin, check_logits, check_greedy_stream
 from oracle import model as OM
 
 pytestmark = pytest.mark.gpu
@@ -30,31 +30,26 @@ def test_target_forward_tap_and_rollback(dev, tiny, kv_bits):
     tap = [0, 2]
     cache = model.make_cache(max_ctx=256, kv_bits=kv_bits)
     logits, fused = model.prefill(prompt, cache, tap)
-    ref = OM.OracleTarget(model, kv_bits=kv_bits, p_bf16=True)
-    alt = OM.OracleTarget(model, kv_bits=kv_bits)
-    rl, rf = ref.forward(prompt, tap)
-    al, _ = alt.forward(prompt, tap)
-    check_logits(logits[0, -1], rl[-1], al[-1], "prefill last row")
+    ref = Twin(lambda: OM.OracleTarget(model, kv_bits=kv_bits))
+    (rl, rf), (el, _) = ref.forward(prompt, tap)
+    check_logits(logits[0, -1], rl[-1], "prefill last row", exact=el[-1])
     assert fused.shape == (1, 70, 2 * model.args.hidden_size)
     assert (fused[0].float().cpu() - rf).abs().max() < 0.05 * rf.abs().max()
     # verify block of 9 rows, advance=False, then roll back to n = 3 accepted
     block = rng.integers(0, V, 9).tolist()
     ids = torch.tensor([block], dtype=torch.int32, device=dev)
     vl, vf = model.forward(ids, cache, tap, advance=False)
-    rvl, _ = ref.forward(block, tap)
-    avl, _ = alt.forward(block, tap)
-    check_logits(vl[0], rvl, avl, "verify block")
+    (rvl, _), (evl, _) = ref.forward(block, tap)
+    check_logits(vl[0], rvl, "verify block", exact=evl)
     n = torch.tensor([3], dtype=torch.int32, device=dev)
     from mlx_dspark import ops
     ops.lens_add(cache.seq_lens, n, 1)
     cache.note_lengths([70 + 4])
     ref.trim(9 - 4)
-    alt.trim(9 - 4)
     nxt = rng.integers(0, V, 5).tolist()
     l2, _ = model.forward(torch.tensor([nxt], dtype=torch.int32, device=dev), cache, None)
-    r2, _ = ref.forward(nxt)
-    a2, _ = alt.forward(nxt)
-    check_logits(l2[0], r2, a2, "after rollback")
+    (r2, _), (e2, _) = ref.forward(nxt)
+    check_logits(l2[0], r2, "after rollback", exact=e2)
     assert int(cache.seq_lens.item()) == 70 + 4 + 5
 
 
@@ -67,9 +62,8 @@ def test_tied_head_and_target_run_api(dev):
     cache = t.make_cache(max_ctx=128)
     ids = [[5, 6, 7, 8, 9]]
     lg, fu = t.run(ids, cache, [1])
-    rl, _ = OM.OracleTarget(model, p_bf16=True).forward(ids[0], [1])
-    al, _ = OM.OracleTarget(model).forward(ids[0], [1])
-    check_logits(lg[0], rl, al, "tied head")
+    (rl, _), (el, _) = Twin(lambda: OM.OracleTarget(model)).forward(ids[0], [1])
+    check_logits(lg[0], rl, "tied head", exact=el)
     assert cache[0].offset == 5
     for c in cache:                        # the reference's per-layer trim loop trims once
         c.trim(2)
@@ -89,14 +83,14 @@ def test_dflash_drafter_matches_oracle(dev, tiny):
     block = [int(prompt[-1])] + [cfg.mask_token_id] * (cfg.block_size - 1)
     got = d(block, fused[0], dcache, logits_start=1)
     ref_t = OM.OracleTarget(tiny)
-    od, oa = OM.OracleDFlash(d, ref_t, p_bf16=True), OM.OracleDFlash(d, ref_t)
-    want = od(block, fused[0].float().cpu(), logits_start=1)
-    check_logits(got[0], want, oa(block, fused[0].float().cpu(), logits_start=1), "dflash round 1")
+    oa = Twin(lambda: OM.OracleDFlash(d, ref_t))
+    want, ex = oa(block, fused[0].float().cpu(), logits_start=1)
+    check_logits(got[0], want, "dflash round 1", exact=ex)
     # a second round: 3 more context rows
     more = fused[0, :3]
     got2 = d(block, more, dcache, logits_start=1)
-    want2 = od(block, more.float().cpu(), logits_start=1)
-    check_logits(got2[0], want2, oa(block, more.float().cpu(), logits_start=1), "dflash round 2")
+    want2, ex2 = oa(block, more.float().cpu(), logits_start=1)
+    check_logits(got2[0], want2, "dflash round 2", exact=ex2)
 
 
 def test_dflash_sliding_window_drafter_matches_oracle(dev, tiny):
@@ -117,19 +111,20 @@ def test_dflash_sliding_window_drafter_matches_oracle(dev, tiny):
     dcache = d.make_cache(max_ctx=256)
     block = [int(prompt[-1])] + [cfg.mask_token_id] * (cfg.block_size - 1)
     ref_t = OM.OracleTarget(tiny)
-    od, oa = OM.OracleDFlash(d, ref_t, p_bf16=True), OM.OracleDFlash(d, ref_t)
-    wide = OM.OracleDFlash(d, ref_t, p_bf16=True)
+    oa = Twin(lambda: OM.OracleDFlash(d, ref_t))
+    wide = OM.OracleDFlash(d, ref_t)
     wide.c = dataclasses.replace(wide.c, sliding_window=12)
     ctx = fused[0].float().cpu()
     got = d(block, fused[0], dcache, logits_start=1)
-    bound = check_logits(got[0], od(block, ctx, logits_start=1), oa(block, ctx, logits_start=1), "sliding round 1")
+    want, ex = oa(block, ctx, logits_start=1)
+    bound = check_logits(got[0], want, "sliding round 1", exact=ex)
     mx, _ = OM.logit_diff(got[0], wide(block, ctx, logits_start=1))
     print(f"oracle with a 12-position window: normalised max-abs {mx:.4f}", flush=True)
     assert mx > bound
     more = fused[0, :3]
     got2 = d(block, more, dcache, logits_start=1)
-    check_logits(got2[0], od(block, more.float().cpu(), logits_start=1),
-                 oa(block, more.float().cpu(), logits_start=1), "sliding round 2")
+    want2, ex2 = oa(block, more.float().cpu(), logits_start=1)
+    check_logits(got2[0], want2, "sliding round 2", exact=ex2)
 
 
 @pytest.mark.parametrize("use_graph", [False, True])

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from _parity import check_logits
+from _parity import Twin, check_logits
 from oracle import model as OM
 from oracle import w8 as O
 
@@ -246,20 +246,18 @@ def test_dense_prefill_matches_oracle(dev):
     assert cache.lengths[0] == 700 and int(cache.seq_lens[0]) == 700
     vl, _ = model.forward(torch.tensor([block], dtype=torch.int32, device=dev), cache, None)
     torch.cuda.synchronize()
-    refs = {pb: OM.OracleTarget(model, p_bf16=pb) for pb in (True, False)}
-    for r in refs.values():
-        r.dense = True                   # the prompt with the dense prefill's rounding
-    outs = {pb: r.forward(prompt, tap=(1, 3)) for pb, r in refs.items()}
-    for r in refs.values():
-        r.dense = False
-    check_logits(logits[0, -1].float().cpu(), outs[True][0][-1], outs[False][0][-1], "dense prefill, last position")
-    tap_err = float((fused[0].float().cpu() - outs[True][1]).abs().max() / outs[True][1].abs().max())
+    ref = Twin(lambda: OM.OracleTarget(model))
+    ref.dense = True                     # the prompt with the dense prefill's rounding
+    (rl, rf), (el, _) = ref.forward(prompt, tap=(1, 3))
+    ref.dense = False
+    check_logits(logits[0, -1].float().cpu(), rl[-1], "dense prefill, last position", exact=el[-1])
+    tap_err = float((fused[0].float().cpu() - rf).abs().max() / rf.abs().max())
     assert tap_err < 2e-2, tap_err
-    vouts = {pb: r.forward(block)[0] for pb, r in refs.items()}
-    check_logits(vl[0].float().cpu(), vouts[True], vouts[False], "verify rows over the dense-prefilled cache")
+    (rvl, _), (evl, _) = ref.forward(block)
+    check_logits(vl[0].float().cpu(), rvl, "verify rows over the dense-prefilled cache", exact=evl)
     # the chunked forward passes (the verify's rounding) fill an equivalent cache
     c2 = model.make_cache(max_ctx=800)
     l2, _ = model.prefill(prompt, c2, None, dense=False)
     torch.cuda.synchronize()
-    chunked = {pb: OM.OracleTarget(model, p_bf16=pb).forward(prompt)[0][-1] for pb in (True, False)}
-    check_logits(l2[0, -1].float().cpu(), chunked[True], chunked[False], "chunked prefill, last position")
+    (cl, _), (ecl, _) = Twin(lambda: OM.OracleTarget(model)).forward(prompt)
+    check_logits(l2[0, -1].float().cpu(), cl[-1], "chunked prefill, last position", exact=ecl[-1])

@@ -211,3 +211,43 @@ def test_proportional_rope_leaves_unrotated_dims():
     r_out = y[..., :n_rot] ** 2 + y[..., hd // 2:hd // 2 + n_rot] ** 2
     assert torch.allclose(r_in, r_out, rtol=1e-5)
     assert torch.equal(y[:, 0], x[:, 0])       # position 0: identity
+
+
+# ------------------------------------------------------------------ confidence head
+
+
+@pytest.mark.parametrize("with_markov", [True, False])
+def test_confidence_logits_one_hot_projection(with_markov):
+    """OracleDSpark.confidence_logits against what the mathematics fixes. The reference's head
+    is proj(features) with nn.Linear's bias (src/mlx_dspark/model.py:211-217), the features the
+    block hidden rows followed by w1[prev] when config.confidence_head_with_markov (:311-320).
+    With a projection whose codes make it exactly the unit vector e_i (q = 1 at i, scale 1,
+    bias 0: dequantized exactly), the logit of row r is h[r, i] + b for i < H and
+    bf16(w1[prev_r])[i - H] + b past H; e_i past H does not exist without the Markov features.
+    Catches a swapped concat order, a missing or doubled bias, a Markov row taken at another
+    token and the concat keyed on anything but the config flag."""
+    import dataclasses
+    import types
+    from _oracle_models import _dspark, _table
+
+    g = torch.Generator().manual_seed(3)
+    H, V, R = 64, 96, 64
+    d = _dspark(g, "qwen3", H, 128, V, 1e-6, False)
+    d.config = dataclasses.replace(d.config, markov_rank=R, confidence_head_with_markov=with_markov)
+    w1 = _table(0.3 * torch.randn(V, R, generator=g))
+    d.markov_head = types.SimpleNamespace(w1=w1, w2=types.SimpleNamespace(mlx=w1.mlx))
+    K = H + (R if with_markov else 0)
+    bias = 0.375
+    rows = torch.randn(5, H, generator=g)
+    prev = torch.tensor([3, 17, 17, 95, 0])
+    w1f = OM.bf(OM.deq_table(w1))
+    for i in list(range(0, H, 7)) + ([H, H + 1, H + 33, K - 1] if with_markov else [H - 1]):
+        q = torch.zeros(16, K, dtype=torch.uint8)
+        q[0, i] = 1
+        s = torch.ones(16, K // 64, dtype=torch.bfloat16)
+        b = torch.zeros(16, K // 64, dtype=torch.bfloat16)
+        d.confidence_head = types.SimpleNamespace(proj=types.SimpleNamespace(mlx=(q, s, b)), bias=bias)
+        o = OM.OracleDSpark(d)
+        got = o.confidence_logits(rows, prev)
+        want = rows[:, i] + bias if i < H else w1f[prev, i - H] + bias
+        assert torch.equal(got, want), i
