@@ -263,8 +263,9 @@ int dsk_qkv_norm_rope_append(const void* qkv, int qkv_splits, int B, int W, int 
  * max_ctx bounds seq_lens[b] + W (sizes the split grid so the launch is graph-stable).
  * softcap > 0: scores = tanh(scores / softcap) * softcap before the mask.
  * out_packed != 0 writes the output in the packed activation layout (the o-projection's x).
- * Probabilities stay float32: every P.V product runs as three bf16 MFMAs over P's
- * hi + mid + lo terms (within 2^-26 of the float32 value), and the row sums add the float32 P.
+ * Probabilities stay float32: the P.V products run as three bf16 MFMAs over P's hi + mid + lo
+ * terms (within 2^-26 of the float32 value) and the row sums add the float32 P; the many-query
+ * form below (a prefill, MFMA-heavy) uses the first two terms (within 2^-17) for both.
  * workspace: dsk_attn_ws_bytes(...) bytes for the split partials (fp32 o / l per split and
  * fp32 (m, l); the splits are combined by a second kernel on the same stream; no state is
  * kept between calls). Every block_table entry of a row must name a valid page: a split

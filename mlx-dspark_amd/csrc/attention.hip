@@ -1075,7 +1075,10 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
     for (int tile = 0; tile < QT; ++tile) mx[tile] = fmaxf(mx[tile], __shfl_xor(mx[tile], 16, 64));
 #pragma unroll
     for (int tile = 0; tile < QT; ++tile) mx[tile] = fmaxf(mx[tile], __shfl_xor(mx[tile], 32, 64));
-    // float32 probabilities, in place of the scores, and their sums
+    // per tile: float32 probabilities (in place of the scores) and their sums, then
+    // O^T += V^T . P^T over the wave's keys (32 per MFMA) with P as three bf16 terms; a tile's
+    // MFMAs run while the next tile's exponentials are computed. One term's MFMAs go over every
+    // d tile before the next term's (8 independent accumulators in between).
 #pragma unroll
     for (int tile = 0; tile < QT; ++tile) {
       // masked keys: exp2(-inf) = 0; a row with no visible key keeps m = -inf, l = 0
@@ -1089,17 +1092,8 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
           l[tile] += p;
         }
       m[tile] = mx[tile] * mscale;
-    }
 #pragma unroll
-    for (int tile = 0; tile < QT; ++tile) l[tile] += __shfl_xor(l[tile], 16, 64);
-#pragma unroll
-    for (int tile = 0; tile < QT; ++tile) l[tile] += __shfl_xor(l[tile], 32, 64);
-    // ---- O^T = V^T . P^T over the wave's keys (32 per MFMA), P as three bf16 terms: one term's
-    // MFMAs over every d tile before the next term's (8 independent accumulators in between)
-#pragma unroll
-    for (int cp = 0; cp < KB / 2; ++cp)
-#pragma unroll
-      for (int tile = 0; tile < QT; ++tile) {
+      for (int cp = 0; cp < KB / 2; ++cp) {
         uint32_t w[3][4];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
@@ -1119,6 +1113,11 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
             o[tile][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[cp][d], pk, o[tile][d], 0, 0, 0);
         }
       }
+    }
+#pragma unroll
+    for (int tile = 0; tile < QT; ++tile) l[tile] += __shfl_xor(l[tile], 16, 64);
+#pragma unroll
+    for (int tile = 0; tile < QT; ++tile) l[tile] += __shfl_xor(l[tile], 32, 64);
   }
 #pragma unroll
   for (int tile = 0; tile < QT; ++tile) {
@@ -1440,27 +1439,25 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
         for (int d = 0; d < DT; ++d) o[t][d] *= alpha;
       }
     }
-    // ---- O^T[d][q] += V^T . P^T with P as hi + mid + lo (three MFMAs per fragment and tile):
+    // ---- O^T[d][q] += V^T . P^T with P as hi + lo (two MFMAs per fragment and tile; a prefill
+    // is MFMA-heavy, so the third term of the verify kernels is left out: P within 2^-17):
     // each V^T fragment feeds both query tiles
     const uint16_t* vt16 = reinterpret_cast<const uint16_t*>(vt[buf]);
 #pragma unroll
     for (int cp = 0; cp < NKT / 2; ++cp) {
-      bf16x8 pk[TPW][3];
+      bf16x8 pk[TPW][2];
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
-        uint32_t w[3][4];
+        uint32_t w[2][4];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
             const f32x4& pv = st[t][2 * cp + u];
-            const Bf16x2Terms tt = split3_bf16x2(pv[2 * hh], pv[2 * hh + 1]);
-            w[0][2 * u + hh] = tt.hi;
-            w[1][2 * u + hh] = tt.mid;
-            w[2][2 * u + hh] = tt.lo;
+            split2_bf16x2(pv[2 * hh], pv[2 * hh + 1], w[0][2 * u + hh], w[1][2 * u + hh]);
           }
 #pragma unroll
-        for (int k = 0; k < 3; ++k) pk[t][k] = __builtin_bit_cast(bf16x8, (u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}));
+        for (int k = 0; k < 2; ++k) pk[t][k] = __builtin_bit_cast(bf16x8, (u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}));
       }
 #pragma unroll
       for (int d = 0; d < DT; ++d) {
@@ -1469,12 +1466,12 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(2, 2
         const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
         const bf16x8 vf = __builtin_bit_cast(bf16x8, (u32x4{lo.x, lo.y, hi.x, hi.y}));
 #pragma unroll
-        for (int k = 0; k < 3; ++k)
+        for (int k = 0; k < 2; ++k)
 #pragma unroll
           for (int t = 0; t < TPW; ++t) o[t][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pk[t][k], o[t][d], 0, 0, 0);
       }
 #pragma unroll
-      for (int k = 0; k < 3; ++k)
+      for (int k = 0; k < 2; ++k)
 #pragma unroll
         for (int t = 0; t < TPW; ++t) lt[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pk[t][k], lt[t], 0, 0, 0);
     }

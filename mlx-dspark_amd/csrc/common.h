@@ -97,6 +97,12 @@ __device__ __forceinline__ Bf16x2Terms split3_bf16x2(float p0, float p1) {
   return t;
 }
 
+// The first two terms alone (hi + lo, lo = bf16(p - hi)): within 2^-17 of |p|.
+__device__ __forceinline__ void split2_bf16x2(float p0, float p1, uint32_t& hi, uint32_t& lo) {
+  hi = pack_bf16x2(p0, p1);
+  lo = pack_bf16x2(p0 - bits_f32(hi << 16), p1 - bits_f32(hi & 0xffff0000u));
+}
+
 // ---- wave-level reductions (wave64) ----------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -152,13 +152,14 @@ def rope(x, pos, theta, inv=None, revolutions: bool = False):
     return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1)
 
 
-def _blocks_attend(s, V, split, block, p_bf16, partial_bf16, exp2_c):
+def _blocks_attend(s, V, split, block, p_bf16, partial_bf16, exp2_c, terms=0):
     """Attention of score rows s [W, L] (scaled, -inf where masked) over V [L, hd] as split
     kernels compute it: keys in splits of ``split`` (one split: the whole range), inside a split
     one max per ``block`` keys (the offset the exponent is taken from, which decides how P rounds
     under p_bf16), each split's output normalised (rounded to bf16 with partial_bf16) and the
     splits merged with weights exp(m_s - M) * l_s. exp2_c: exp(s - m) as 2^(s c - m c) with
-    c = log2(e) rounded to float32 (the kernels' exp2 form, scale already in s)."""
+    c = log2(e) rounded to float32 (the kernels' exp2 form, scale already in s). terms=2: P
+    weights V and is summed as bf16(p) + bf16(p - bf16(p)) (the two-term form)."""
     dt = s.dtype
     L = s.shape[1]
     step = split or L
@@ -175,6 +176,9 @@ def _blocks_attend(s, V, split, block, p_bf16, partial_bf16, exp2_c):
             p = torch.exp2(sb * exp2_c - m0 * exp2_c) if exp2_c else torch.exp(sb - m0)
             if p_bf16:
                 p = bf(p).to(dt)
+            elif terms == 2:
+                hi = bf(p).to(dt)
+                p = hi + bf(p - hi).to(dt)
             bm.append(m)
             bl.append(p.sum(dim=-1, keepdim=True))
             bo.append(p @ vb)
@@ -194,18 +198,19 @@ def _blocks_attend(s, V, split, block, p_bf16, partial_bf16, exp2_c):
     return o / torch.where(den > 0, den, torch.ones_like(den))
 
 
-def sdpa(q, K, V, scale, mask=None, p_bf16=False, *, split=0, block=0, partial_bf16=False, exp2=False):
+def sdpa(q, K, V, scale, mask=None, p_bf16=False, *, split=0, block=0, partial_bf16=False, exp2=False,
+         terms=0):
     """q [W, nq, hd], K/V [L, nkv, hd] -> [W, nq, hd]; GQA by head index // (nq/nkv).
     p_bf16: the unnormalised probabilities exp(s - max) are rounded to bf16 before they weight
     V and before they are summed for the normaliser (where a bf16 attention kernel rounds them);
-    otherwise the softmax stays float32. split / block / partial_bf16 / exp2: the split
+    otherwise the softmax stays float32. split / block / partial_bf16 / exp2 / terms: the split
     kernels' evaluation order (_blocks_attend), for the rounding-source decomposition."""
     W, nq, hd = q.shape
     nkv = K.shape[1]
     G = nq // nkv
     dt = _dt()
     out = torch.empty(W, nq, hd, dtype=dt)
-    plain = not (split or block or partial_bf16 or exp2)
+    plain = not (split or block or partial_bf16 or exp2 or terms)
     c2 = float(np.float32(1.4426950408889634)) if exp2 else 0.0
     for h in range(nq):
         Kh, Vh = K[:, h // G].to(dt), V[:, h // G].to(dt)
@@ -213,7 +218,7 @@ def sdpa(q, K, V, scale, mask=None, p_bf16=False, *, split=0, block=0, partial_b
         if mask is not None:
             s = s.masked_fill(~mask, float("-inf"))
         if not plain:
-            out[:, h] = _blocks_attend(s, Vh, split, block, p_bf16, partial_bf16, c2)
+            out[:, h] = _blocks_attend(s, Vh, split, block, p_bf16, partial_bf16, c2, terms)
         elif p_bf16:
             p = bf(torch.exp(s - s.max(dim=-1, keepdim=True).values)).to(dt)
             out[:, h] = (p @ Vh) / p.sum(dim=-1, keepdim=True)
@@ -288,13 +293,13 @@ class OracleTarget:
 
     def __init__(self, model, kv_bits=None, double_round: bool = False, p_bf16: bool = False, *,
                  norm_first: bool = False, split: int = 0, p_block: int = 0, partial_bf16: bool = False,
-                 exp2: bool = False, rope_revolutions: bool = False, requant_new: bool = True):
+                 exp2: bool = False, p_terms: int = 0, rope_revolutions: bool = False, requant_new: bool = True):
         """Rounding-point options (each default is the reference-order evaluation; the others
         exist to measure one source at a time): double_round rounds a projection's output to
         bf16 before its residual add; p_bf16 rounds the attention probabilities to bf16;
         norm_first normalises the Qwen3 layout's rows before their projections (bf16 normalised
         rows, as an unfused graph does) instead of after them; split / p_block / partial_bf16 /
-        exp2 evaluate attention the way split kernels do (sdpa); rope_revolutions takes the
+        exp2 / p_terms evaluate attention the way split kernels do (sdpa); rope_revolutions takes the
         RoPE sine in float32 revolutions (rope); requant_new=False keeps the new K/V rows in
         bf16 in an 8-bit cache (the re-quantisation of the new rows switched off)."""
         a = model.args
@@ -303,7 +308,7 @@ class OracleTarget:
         self.rr = bf if double_round else (lambda x: x)
         self.p_bf16 = p_bf16
         self.norm_first = norm_first
-        self.attn_opts = dict(split=split, block=p_block, partial_bf16=partial_bf16, exp2=exp2)
+        self.attn_opts = dict(split=split, block=p_block, partial_bf16=partial_bf16, exp2=exp2, terms=p_terms)
         self.rope_revolutions = rope_revolutions
         self.requant_new = requant_new
         self.layers = [OracleLayer(L, a.num_attention_heads, a.num_key_value_heads, a.head_dim) for L in model.layers]

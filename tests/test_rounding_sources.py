@@ -71,12 +71,12 @@ def fullwidth():
 def _run(fw, *, exact=False, **knobs):
     ot, ctx, block = fw
     base = dict(p_bf16=False, norm_first=False, rope_revolutions=False, requant_new=True,
-                rr=lambda x: x, attn_opts=dict(split=0, block=0, partial_bf16=False, exp2=False))
+                rr=lambda x: x, attn_opts=dict(split=0, block=0, partial_bf16=False, exp2=False, terms=0))
     opts = dict(base)
     attn = dict(base["attn_opts"])
     for k, v in knobs.items():
-        if k in attn:
-            attn[k] = v
+        if k in attn or k == "p_terms":
+            attn["terms" if k == "p_terms" else k] = v
         elif k == "double_round":
             opts["rr"] = OM.bf if v else (lambda x: x)
         else:
@@ -102,6 +102,7 @@ def test_rounding_sources(fullwidth):
         "split-kernel order, float32 P and partials": dict(KERNEL_ORDER),
         "  + float64 sums": dict(KERNEL_ORDER, exact=True),
         "bf16 P (one max per row)": dict(p_bf16=True),
+        "two-term P (hi + lo, the many-query prefill kernel)": dict(KERNEL_ORDER, p_terms=2),
         "bf16 P, one max per 64 keys, bf16 256-key partials": dict(KERNEL_ORDER, p_bf16=True, partial_bf16=True),
         "bf16 256-key split partials (float32 P)": dict(KERNEL_ORDER, partial_bf16=True),
         "RoPE sine of float32 revolutions": dict(rope_revolutions=True),
