@@ -27,7 +27,8 @@ import time
 import torch
 
 from . import blockdraft, ops
-from .generate import GenResult, _final_text, _seed64, _Streamer, eos_token_ids
+from .generate import GenResult, _seed64
+from .textstream import TextStream, eos_token_ids
 from .kv import PagedKVCache
 
 # --------------------------------------------------------------------------- capability
@@ -60,15 +61,15 @@ class _Row:
         self.ids = [int(first)]
         self.limit = int(limit)
         self.eos = eos
-        self.streamer = _Streamer(tokenizer, eos, on_text, stop)
+        self.streamer = TextStream(tokenizer, eos, on_text, stop)
         self.accepts: list = []
         self.t0 = time.time()
         self.done = False
         self._settle()
 
     def _settle(self) -> None:
-        self.streamer.update(self.ids)
-        self.done = self.ids[-1] in self.eos or len(self.ids) >= self.limit or self.streamer.stopped
+        self.streamer.feed(self.ids)
+        self.done = self.ids[-1] in self.eos or len(self.ids) >= self.limit or self.streamer.closed
 
     def extend(self, tokens, accept_len: int | None = None) -> None:
         if self.done:
@@ -83,12 +84,12 @@ class _Row:
 
     def result(self, tokenizer, seconds: float) -> GenResult:
         st = self.streamer
-        st.flush()
+        st.close()
         ids = list(self.ids)
         spec = bool(self.accepts)
         rounds = list(self.accepts) if spec else [1] * len(ids)
-        reason = "stop" if (st.stopped or ids[-1] in self.eos) else "length"
-        return GenResult(text=_final_text(tokenizer, st, ids, self.eos), token_ids=ids, num_tokens=len(ids),
+        reason = st.finish_reason(ids, self.limit, ids[-1])
+        return GenResult(text=st.result_text(ids), token_ids=ids, num_tokens=len(ids),
                          num_rounds=len(rounds), accept_lengths=rounds,
                          target_forwards=len(rounds) + 1 if spec else len(ids), seconds=seconds,
                          finish_reason=reason)

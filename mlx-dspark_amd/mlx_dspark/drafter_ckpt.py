@@ -16,8 +16,12 @@ checkpoints load as they are:
     fc.weight, hidden_norm.weight, norm.weight and the same per-layer attention / MLP / two-norm keys.
 
 A checkpoint whose key set differs from the config's raises ValueError (strict, as the reference
-does); ``strict=False`` loads the intersection with the missing matrices zero and missing norms
-one (a DSpark drafter only, as in the reference). Weights in bf16/f16/f32 are quantized on load
+does); ``strict=False`` loads the intersection (a DSpark drafter only, as in the reference), and a
+missing parameter takes the value a fresh reference module gives it: norm weights one, a linear
+matrix uniform in +-sqrt(1/K) (nn.Linear's initialiser), an embedding table normal with scale
+sqrt(1/dims) (nn.Embedding's); a missing bias is zero (nn.Linear would draw it uniform too). Those draws are seeded by the key name, so a load is
+reproducible; MLX's own random stream is not, so a partially loaded drafter drafts like some
+fresh reference module, not like the one the reference would build. Weights in bf16/f16/f32 are quantized on load
 with the engine's affine group-64 quantizer: every linear and embedding table (the reference's
 nn.quantize over the DSpark drafter; the DFlash backbone linears only) at ``bits`` (4 by default,
 as the reference). An MLX-quantized matrix (uint32 ``.weight`` with ``.scales`` / ``.biases``) is
@@ -27,6 +31,8 @@ with 4-bit code values (the Markov kernel streams byte codes).
 """
 
 from __future__ import annotations
+
+import hashlib
 
 import json
 import warnings
@@ -88,6 +94,18 @@ def _ckpt_keys(t: _Tensors) -> set[str]:
     return keys
 
 
+def _fresh_init(key: str, N: int, K: int, embedding: bool, device) -> torch.Tensor:
+    """A fresh module's value for a parameter missing from a checkpoint: nn.Embedding's normal
+    draw (scale sqrt(1/K)) or nn.Linear's uniform one (+-sqrt(1/K)), seeded by the key name."""
+    g = torch.Generator().manual_seed(int.from_bytes(hashlib.sha256(key.encode()).digest()[:8], "little") >> 1)
+    scale = (1.0 / K) ** 0.5
+    if embedding:
+        w = torch.randn((N, K), generator=g) * scale
+    else:
+        w = (torch.rand((N, K), generator=g) * 2.0 - 1.0) * scale
+    return w.to(device)
+
+
 def _check_keys(where: str, want: list[str], t: _Tensors, strict: bool, what: str) -> set[str]:
     have = _ckpt_keys(t)
     missing = sorted(set(want) - have)
@@ -121,9 +139,10 @@ class _Loader:
             raise ValueError(f"{key}: expected shape {tuple(shape)}, got {tuple(w.shape)}")
         return w
 
-    def triplet(self, name: str, N: int, K: int, bits: int | None = None):
+    def triplet(self, name: str, N: int, K: int, bits: int | None = None, embedding: bool = False):
         """(codes u8 [N, K] one per byte, scales, biases bf16 [N, K/64]) of a matrix: its own codes
-        when MLX-quantized, else quantized here (zeros when missing, strict=False)."""
+        when MLX-quantized, else quantized here (a missing one, strict=False, a seeded draw of the
+        module's initialiser: ``embedding`` tables normal, linears uniform)."""
         bits = bits or self.bits
         key = name + ".weight"
         if key in self.present and self.t.has(name + ".scales"):
@@ -143,7 +162,7 @@ class _Loader:
             return q.contiguous(), s, b, qbits
         w = self._float(key, (N, K))
         if w is None:
-            w = torch.zeros((N, K), dtype=torch.float32, device=self.device)
+            w = _fresh_init(key, N, K, embedding, self.device)
         q, s, b = W8Weight.quantize_mlx(w.to(torch.bfloat16) if w.dtype != torch.float32 else w, bits)
         return q, s, b, bits
 
@@ -162,7 +181,7 @@ class _Loader:
         return W
 
     def table(self, name: str, N: int, K: int) -> W8Table:
-        q, s, b, _ = self.triplet(name, N, K)
+        q, s, b, _ = self.triplet(name, N, K, embedding=True)
         return W8Table(q, s, b)
 
     def vec(self, key: str, n: int, default: float = 1.0) -> torch.Tensor:

@@ -22,6 +22,7 @@ from dataclasses import dataclass
 import torch
 
 from . import blockdraft, ops
+from .textstream import StopStreaming, TextStream, encode_messages, encode_prompt, eos_token_ids  # noqa: F401
 
 # ============================================================================ results
 @dataclass
@@ -44,129 +45,6 @@ class GenResult:
     @property
     def tokens_per_sec(self) -> float:
         return self.num_tokens / max(self.seconds, 1e-9)
-
-
-class StopStreaming(Exception):
-    """Raised from an on_text callback to end generation at the next round boundary with a
-    normal (partial) GenResult and consistent caches (src/mlx_dspark/generate.py:231-235)."""
-
-
-# ============================================================================ tokenizer helpers
-def eos_token_ids(tokenizer) -> set:
-    """eos ids plus the usual turn-end markers the tokenizer knows (unknown id excluded)."""
-    out: set = set()
-    for attr in ("eos_token_ids", "eos_token_id"):
-        v = getattr(tokenizer, attr, None)
-        if isinstance(v, int):
-            out.add(v)
-        elif v:
-            out.update(int(x) for x in v)
-    unk = getattr(tokenizer, "unk_token_id", None)
-    conv = getattr(tokenizer, "convert_tokens_to_ids", None)
-    if conv is not None:
-        for t in ("<turn|>", "<end_of_turn>", "<|im_end|>", "<|endoftext|>", "<eos>"):
-            try:
-                i = conv(t)
-            except Exception:
-                continue
-            if isinstance(i, int) and i >= 0 and i != unk:
-                out.add(i)
-    return out
-
-
-def _flat_ids(r):
-    if isinstance(r, (list, tuple)):
-        return list(r[0]) if r and isinstance(r[0], (list, tuple)) else list(r)
-    ii = r["input_ids"] if hasattr(r, "__contains__") and "input_ids" in r else getattr(r, "input_ids", None)
-    if ii is not None:
-        ii = list(ii)
-        return list(ii[0]) if ii and isinstance(ii[0], (list, tuple)) else ii
-    return list(r.ids) if hasattr(r, "ids") else None
-
-
-def encode_messages(tokenizer, messages, add_generation_prompt=True, **template_kwargs) -> list:
-    if getattr(tokenizer, "chat_template", None):
-        try:
-            r = tokenizer.apply_chat_template(messages, add_generation_prompt=add_generation_prompt, **template_kwargs)
-        except (TypeError, ValueError):
-            r = tokenizer.apply_chat_template(messages, add_generation_prompt=add_generation_prompt)
-        ids = _flat_ids(r)
-        if ids is not None:
-            return ids
-    return list(tokenizer.encode("\n".join(str(m.get("content", "")) for m in messages)))
-
-
-def encode_prompt(tokenizer, prompt: str, use_chat: bool = True) -> list:
-    if use_chat and getattr(tokenizer, "chat_template", None):
-        return encode_messages(tokenizer, [{"role": "user", "content": prompt}])
-    return list(tokenizer.encode(prompt))
-
-
-class _Streamer:
-    """Round-granular text streaming with stop strings (behaviour of the reference's
-    _Streamer, src/mlx_dspark/generate.py:294-362): new tokens are decoded incrementally,
-    stop strings are searched from max_stop - 1 characters back so one that straddles two
-    rounds is found, and emission holds back the last max_stop - 1 characters until they
-    are known not to start a stop string. StopStreaming from on_text ends the loop cleanly."""
-
-    def __init__(self, tokenizer, eos_ids, on_text, stop):
-        self.tok = tokenizer
-        self.eos = eos_ids
-        self.on_text = on_text
-        self.stop = [s for s in (stop or []) if s]
-        self.max_stop = max((len(s) for s in self.stop), default=0)
-        self.active = on_text is not None or bool(self.stop)
-        self.ids: list = []
-        self.n_fed = 0
-        self.scan_from = 0
-        self.streamed = 0
-        self.text = ""
-        self.stopped = False
-
-    def update(self, out_ids) -> None:
-        if not self.active or self.stopped:
-            return
-        self.ids.extend(t for t in out_ids[self.n_fed:] if t not in self.eos)
-        self.n_fed = len(out_ids)
-        self._advance(final=False)
-
-    def flush(self) -> None:
-        if self.active and not self.stopped:
-            self._advance(final=True)
-
-    def _advance(self, final: bool) -> None:
-        text = self.tok.decode(self.ids)
-        if self.stop:
-            hits = [i for i in (text.find(s, self.scan_from) for s in self.stop) if i != -1]
-            if hits:
-                text = text[:min(hits)]
-                self.stopped = True
-            else:
-                self.scan_from = max(0, len(text) - (self.max_stop - 1))
-        self.text = text
-        if self.on_text is None:
-            return
-        end = len(text)
-        if not (self.stopped or final) and self.max_stop > 1:
-            end = max(self.streamed, len(text) - (self.max_stop - 1))
-        if end > self.streamed:
-            try:
-                self.on_text(text[self.streamed:end])
-            except StopStreaming:
-                self.on_text = None
-                self.stopped = True
-                return
-            self.streamed = end
-
-
-def _finish_reason(out_ids, max_new_tokens, last_tok, eos_ids, streamer) -> str:
-    if streamer.stopped or last_tok in eos_ids:
-        return "stop"
-    return "length" if len(out_ids) >= max_new_tokens else "stop"
-
-
-def _final_text(tokenizer, st: _Streamer, out_ids, eos_ids) -> str:
-    return st.text if st.stopped else tokenizer.decode([t for t in out_ids if t not in eos_ids])
 
 
 # ============================================================================ sampling helpers
@@ -217,7 +95,7 @@ def greedy_generate(target_model, tokenizer, prompt: str = "", *, prompt_ids=Non
     if cache is None:
         cache = target_model.make_cache()
         reuse_len = 0
-    st = _Streamer(tokenizer, eos_ids, on_text, stop)
+    st = TextStream(tokenizer, eos_ids, on_text, stop)
     s64 = _seed64(seed)
     pen = _Penalizer(presence_penalty, frequency_penalty)
     lp_list: list | None = [] if logprobs is not None else None
@@ -237,17 +115,17 @@ def greedy_generate(target_model, tokenizer, prompt: str = "", *, prompt_ids=Non
         pen.add([nxt])
         if lp_list is not None:
             lp_list.extend(_logprobs_for_block(row, [nxt], logprobs))
-        st.update(out_ids)
-        if len(out_ids) >= max_new_tokens or nxt in eos_ids or st.stopped:
+        st.feed(out_ids)
+        if len(out_ids) >= max_new_tokens or nxt in eos_ids or st.closed:
             break
         cur.fill_(nxt)
         lg, _ = model.forward(cur, cache, None)
         row = lg[0, -1:]
-    st.flush()
+    st.close()
     secs = time.time() - t0
-    return GenResult(text=_final_text(tokenizer, st, out_ids, eos_ids), token_ids=out_ids, num_tokens=len(out_ids),
+    return GenResult(text=st.result_text(out_ids), token_ids=out_ids, num_tokens=len(out_ids),
                      num_rounds=len(out_ids), accept_lengths=[1] * len(out_ids), target_forwards=len(out_ids),
-                     seconds=secs, finish_reason=_finish_reason(out_ids, max_new_tokens, nxt, eos_ids, st),
+                     seconds=secs, finish_reason=st.finish_reason(out_ids, max_new_tokens, nxt),
                      logprobs=lp_list)
 
 
@@ -412,7 +290,7 @@ def dflash_generate(target_model, tokenizer, drafter, prompt: str = "", *, promp
     max_ctx = max(max_ctx or 0, need)
     cache = target_model.make_cache(max_ctx=max_ctx)
     dcache = drafter.make_cache(max_ctx=max_ctx)
-    st = _Streamer(tokenizer, eos_ids, on_text, stop)
+    st = TextStream(tokenizer, eos_ids, on_text, stop)
     s64 = _seed64(seed)
     t0 = time.time()
 
@@ -425,13 +303,13 @@ def dflash_generate(target_model, tokenizer, drafter, prompt: str = "", *, promp
     # one round object (static buffers, captured graph) per verify width: a cap controller may
     # pick a different cap every round (generate.py:537-538)
     rounds: dict = {}
-    st.update(out_ids)
+    st.feed(out_ids)
     r = 0
     if use_graph and cap_controller is None:
         # a fixed width: each round enqueued before the host reads the previous one
         pipe = _DFlashPipe(target_model, drafter, cache, dcache, cap, temperature, top_p, top_k, s64)
         pipe.start(pending)
-        going = len(out_ids) < max_new_tokens and pending not in eos_ids and not st.stopped
+        going = len(out_ids) < max_new_tokens and pending not in eos_ids and not st.closed
         if going and pipe.room(1):
             pipe.enqueue()
         while pipe.queue:
@@ -446,14 +324,14 @@ def dflash_generate(target_model, tokenizer, drafter, prompt: str = "", *, promp
                 if tok in eos_ids:
                     break
             pending = out_ids[-1]
-            st.update(out_ids)
-            if not (len(out_ids) < max_new_tokens and pending not in eos_ids and not st.stopped):
+            st.feed(out_ids)
+            if not (len(out_ids) < max_new_tokens and pending not in eos_ids and not st.closed):
                 pipe.cancel()
                 break
             if not pipe.queue and pipe.room(1):
                 pipe.enqueue()
     while (not use_graph or cap_controller is not None) and len(out_ids) < max_new_tokens \
-            and pending not in eos_ids and not st.stopped:
+            and pending not in eos_ids and not st.closed:
         c = cap if cap_controller is None else max(1, min(int(cap_controller.cap), cap))
         if cache.lengths[0] + c + 1 > cache.max_ctx:
             break
@@ -473,12 +351,12 @@ def dflash_generate(target_model, tokenizer, drafter, prompt: str = "", *, promp
             if tok in eos_ids:
                 break
         pending = out_ids[-1]
-        st.update(out_ids)
-    st.flush()
+        st.feed(out_ids)
+    st.close()
     secs = time.time() - t0
-    return GenResult(text=_final_text(tokenizer, st, out_ids, eos_ids), token_ids=out_ids, num_tokens=len(out_ids),
+    return GenResult(text=st.result_text(out_ids), token_ids=out_ids, num_tokens=len(out_ids),
                      num_rounds=len(accept_lengths), accept_lengths=accept_lengths, target_forwards=target_forwards,
-                     seconds=secs, finish_reason=_finish_reason(out_ids, max_new_tokens, pending, eos_ids, st))
+                     seconds=secs, finish_reason=st.finish_reason(out_ids, max_new_tokens, pending))
 
 
 # ============================================================================ penalties
@@ -624,7 +502,7 @@ def speculative_generate(target_model, tokenizer, drafter, prompt: str = "", *, 
         reuse_len = 0
     elif ctx_caches is None:
         raise ValueError("a reused target cache needs its drafter ctx_caches")
-    st = _Streamer(tokenizer, eos_ids, on_text, stop)
+    st = TextStream(tokenizer, eos_ids, on_text, stop)
     s64 = _seed64(seed)
     t0 = time.time()
 
@@ -656,9 +534,9 @@ def speculative_generate(target_model, tokenizer, drafter, prompt: str = "", *, 
     rounds: dict = {}
     mask_id = int(cfg.mask_token_id)
     dev = model.device
-    st.update(out_ids)
+    st.feed(out_ids)
     r = 0
-    while len(out_ids) < max_new_tokens and pending not in eos_ids and not st.stopped:
+    while len(out_ids) < max_new_tokens and pending not in eos_ids and not st.closed:
         lk = index.propose() if index is not None else []
         cap = cap_ceiling if cap_controller is None else max(1, min(int(cap_controller.cap), cap_ceiling))
         width = 1 + (len(lk) if lk else cap)
@@ -735,13 +613,13 @@ def speculative_generate(target_model, tokenizer, drafter, prompt: str = "", *, 
         if index is not None:
             index.extend(appended)
         pending = out_ids[-1]
-        st.update(out_ids)
+        st.feed(out_ids)
         if verbose:
             print(f"  round {len(accept_lengths):3d}: {'lookup' if lk else 'drafter'} drafted {len(draft)}, "
                   f"accepted {n}, committed {len(committed)}")
-    st.flush()
+    st.close()
     secs = time.time() - t0
-    return GenResult(text=_final_text(tokenizer, st, out_ids, eos_ids), token_ids=out_ids, num_tokens=len(out_ids),
+    return GenResult(text=st.result_text(out_ids), token_ids=out_ids, num_tokens=len(out_ids),
                      num_rounds=len(accept_lengths), accept_lengths=accept_lengths, target_forwards=target_forwards,
-                     seconds=secs, finish_reason=_finish_reason(out_ids, max_new_tokens, pending, eos_ids, st),
+                     seconds=secs, finish_reason=st.finish_reason(out_ids, max_new_tokens, pending),
                      lookup_rounds=lookup_rounds, logprobs=lp_list)

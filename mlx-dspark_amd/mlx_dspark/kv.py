@@ -198,10 +198,13 @@ class RowCache(PagedKVCache):
 
     def __init__(self, parent: PagedKVCache, b: int, b1: int | None = None):  # noqa: nothing is allocated
         list.__init__(self, (LayerView(self, l) for l in range(parent.n_layers)))
-        self.parent, self.b = parent, int(b)
-        self.b1 = self.b + 1 if b1 is None else int(b1)
-        if not 0 <= self.b < self.b1 <= parent.B:
-            raise ValueError(f"rows {self.b} .. {self.b1 - 1} outside the cache's {parent.B} rows")
+        b = int(b)
+        b1 = b + 1 if b1 is None else int(b1)
+        if not 0 <= b < b1 <= parent.B:
+            raise ValueError(f"rows {b} .. {b1 - 1} outside the cache's {parent.B} rows")
+        if isinstance(parent, RowCache):        # rows of a view: the same rows of the root cache
+            b, b1, parent = parent.b + b, parent.b + b1, parent.parent
+        self.parent, self.b, self.b1 = parent, b, b1
         for name in ("n_layers", "n_kv", "head_dim", "page", "max_pages", "max_ctx", "kv_dtype", "n_pages",
                      "k", "v", "k_sb", "v_sb"):
             setattr(self, name, getattr(parent, name))
@@ -219,6 +222,17 @@ class RowCache(PagedKVCache):
         if len(v) != self.B:
             raise ValueError(f"{len(v)} lengths for {self.B} rows")
         self.parent.lengths[self.b:self.b1] = v
+
+    # row operations act on the root cache's rows (the host lengths live there)
+    def swap_rows(self, a: int, b: int) -> None:
+        if not (0 <= a < self.B and 0 <= b < self.B):
+            raise ValueError(f"rows {a}, {b} outside the view's {self.B} rows")
+        self.parent.swap_rows(self.b + a, self.b + b)
+
+    def set_row_length(self, b: int, n: int) -> None:
+        if not 0 <= b < self.B:
+            raise ValueError(f"row {b} outside the view's {self.B} rows")
+        self.parent.set_row_length(self.b + b, n)
 
     @property
     def layer_offsets(self):

@@ -59,8 +59,8 @@ def lookup_generate(target_model, tokenizer, prompt: str = "", *, prompt_ids=Non
     import torch
 
     from . import ops
-    from .generate import (GenResult, _final_text, _finish_reason, _pick, _seed64, _Streamer, encode_prompt,
-                           eos_token_ids)
+    from .generate import GenResult, _pick, _seed64
+    from .textstream import TextStream, encode_prompt, eos_token_ids
     eos_ids = eos_token_ids(tokenizer)
     ids = prompt_ids if prompt_ids is not None else encode_prompt(tokenizer, prompt, apply_chat_template)
     model = target_model.model
@@ -69,7 +69,7 @@ def lookup_generate(target_model, tokenizer, prompt: str = "", *, prompt_ids=Non
         reuse_len = 0
     elif reuse_len and cache.lengths[0] != reuse_len:
         raise ValueError(f"reused cache holds {cache.lengths[0]} tokens, reuse_len={reuse_len}")
-    st = _Streamer(tokenizer, eos_ids, on_text, stop)
+    st = TextStream(tokenizer, eos_ids, on_text, stop)
     s64 = _seed64(seed)
     index = NGramIndex(min_n=ngram_min, max_n=ngram_max, max_draft=max(1, max_draft_tokens))
     index.extend(ids)
@@ -86,8 +86,8 @@ def lookup_generate(target_model, tokenizer, prompt: str = "", *, prompt_ids=Non
     n_t = torch.zeros(1, dtype=torch.int32, device=dev)
     tok_t = torch.zeros(1, dtype=torch.int32, device=dev)
     r = lookup_rounds = 0
-    st.update(out_ids)
-    while len(out_ids) < max_new_tokens and pending not in eos_ids and not st.stopped:
+    st.feed(out_ids)
+    while len(out_ids) < max_new_tokens and pending not in eos_ids and not st.closed:
         draft = index.propose()
         if cache.lengths[0] + 1 + len(draft) > cache.max_ctx:
             break
@@ -120,10 +120,10 @@ def lookup_generate(target_model, tokenizer, prompt: str = "", *, prompt_ids=Non
                 break
         index.extend(appended)
         pending = out_ids[-1]
-        st.update(out_ids)
-    st.flush()
+        st.feed(out_ids)
+    st.close()
     secs = time.time() - t0
-    return GenResult(text=_final_text(tokenizer, st, out_ids, eos_ids), token_ids=out_ids, num_tokens=len(out_ids),
+    return GenResult(text=st.result_text(out_ids), token_ids=out_ids, num_tokens=len(out_ids),
                      num_rounds=len(accept_lengths), accept_lengths=accept_lengths, target_forwards=target_forwards,
-                     seconds=secs, finish_reason=_finish_reason(out_ids, max_new_tokens, pending, eos_ids, st),
+                     seconds=secs, finish_reason=st.finish_reason(out_ids, max_new_tokens, pending),
                      lookup_rounds=lookup_rounds)

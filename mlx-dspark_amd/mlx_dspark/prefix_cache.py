@@ -173,22 +173,29 @@ class PrefixCache:
         pinned = shared + ([cow] if cow is not None else [])
         for node in pinned:
             node.pins += 1
+        taken = []                          # (arena, page): row 0's private pages so far
         try:
             for node in pinned:
-                self._load(node)
+                self._load(node)            # a loaded node keeps its pages: they are stored ones
             self._tick(shared[-1] if shared else None)
             if cow is not None:
                 cow.tick = self._clock
             for ai, ar in enumerate(self.arenas):
                 c = ar.cache
                 own = self._alloc(ai, c.max_pages - n_shared)
+                taken += [(ar, p) for p in own]
                 if cow is not None:
                     ar.copy_page(cow.pages[ai], own[0])
                 c.set_row_pages(0, [n.pages[ai] for n in shared] + own)
                 c.set_lengths([reuse])
         except BaseException:
+            # give back what this call took and leave row 0 empty in every arena
             for node in pinned:
                 node.pins -= 1
+            for ar, p in taken:
+                ar.give(p)
+            for ar in self.arenas:
+                ar.cache.set_lengths([0])
             raise
         if cow is not None:
             cow.pins -= 1                  # its contents now live in a private page
@@ -375,14 +382,18 @@ class PrefixCache:
 
         data = load_file(node.disk)
         pages = []
-        for ai, ar in enumerate(self.arenas):
-            p = self._alloc(ai, 1)[0]
-            for name, t in ar.pools.items():
-                src = data[f"{ai}.{name}"]
-                if src.shape != t.shape[1:] or src.dtype != t.dtype:
-                    raise ValueError(f"spilled page {node.disk} does not match the arena layout ({name})")
-                t[p].copy_(src.to(t.device))
-            pages.append(p)
+        try:
+            for ai, ar in enumerate(self.arenas):
+                pages.append(self._alloc(ai, 1)[0])
+                for name, t in ar.pools.items():
+                    src = data[f"{ai}.{name}"]
+                    if src.shape != t.shape[1:] or src.dtype != t.dtype:
+                        raise ValueError(f"spilled page {node.disk} does not match the arena layout ({name})")
+                    t[pages[-1]].copy_(src.to(t.device))
+        except BaseException:
+            for ai, p in enumerate(pages):      # the node stays spilled; its pages go back
+                self.arenas[ai].give(p)
+            raise
         node.pages = tuple(pages)
         self._unlink_disk(node)
 

@@ -78,3 +78,26 @@ def test_row_view_narrows_to_its_row():
     assert c.lengths == [3, 2, 4]
     assert c.seq_lens.tolist() == [3, 2, 4]
     assert r.row_pages(0) == c.row_pages(1)
+
+
+def test_views_of_views_write_through_to_the_root_cache():
+    # a view of a view addresses the root cache's rows: lengths set, noted, swapped or set per row
+    # on it land in the root's host lengths and device seq_lens alike
+    c = _cache(6)
+    c.set_lengths([1, 2, 3, 4, 5, 6])
+    outer = c.rows(1, 5)                         # root rows 1..4
+    inner = outer.rows(1, 3)                     # root rows 2..3
+    assert inner.parent is c and (inner.b, inner.b1) == (2, 4)
+    assert inner.lengths == [3, 4]
+    inner.note_lengths([13, 14])
+    assert c.lengths == [1, 2, 13, 14, 5, 6]
+    inner.set_lengths([23, 24])
+    assert c.lengths == [1, 2, 23, 24, 5, 6] and c.seq_lens.tolist() == [1, 2, 23, 24, 5, 6]
+    pages = [c.row_pages(b) for b in range(6)]
+    inner.swap_rows(0, 1)
+    assert c.lengths == [1, 2, 24, 23, 5, 6] and c.seq_lens.tolist() == [1, 2, 24, 23, 5, 6]
+    assert c.row_pages(2) == pages[3] and c.row_pages(3) == pages[2]
+    outer.row(3).set_row_length(0, 9)            # root row 4
+    assert c.lengths == [1, 2, 24, 23, 9, 6] and int(c.seq_lens[4]) == 9
+    with pytest.raises(ValueError):
+        outer.rows(2, 5)                         # past the outer view's 4 rows

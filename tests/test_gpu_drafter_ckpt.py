@@ -143,16 +143,22 @@ def test_dspark_bf16_checkpoint_quantized_on_load(dev, tmp_path, family):
             assert d.layer_scalars[l] == pytest.approx(0.8, rel=1e-2)
         else:
             assert torch.equal(L.post_norm, on(p + "post_attention_layernorm.weight"))
-    # a partial checkpoint: strict refuses it, strict=False warns and loads (the missing matrix zero)
+    # a partial checkpoint: strict refuses it, strict=False warns and loads (the missing matrix a
+    # seeded draw of nn.Linear's initialiser: uniform in +-sqrt(1/K), not zero)
     del t["layers.1.mlp.up_proj.weight"]
     save_file(t, str(tmp_path / "model.safetensors"))
     with pytest.raises(ValueError, match="missing in checkpoint"):
         load_drafter(str(tmp_path))
     with warnings.catch_warnings(record=True) as w:
         warnings.simplefilter("always")
-        e, _ = load_drafter(str(tmp_path), strict=False)
+        e, _ = load_drafter(str(tmp_path), strict=False, keep_mlx=True)
     assert any("key mismatch" in str(x.message) for x in w)
     _same_w(e.layers[0].gate_up, d.layers[0].gate_up, "intact layer")
+    I, H = d.config.intermediate_size, d.config.hidden_size
+    from oracle import model as OM
+    up = OM.deq(e.layers[1].gate_up)[I:]
+    bound = (1.0 / H) ** 0.5
+    assert float(up.abs().max()) <= 1.01 * bound and float(up.std()) > 0.5 * bound / 3 ** 0.5
 
 
 def test_dflash_save_load_round_trip(dev, tmp_path):

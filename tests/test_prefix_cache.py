@@ -226,3 +226,48 @@ def test_spill_budget_keeps_the_newest_pages_resident(tmp_path):
 
 def test_paged_caches_are_always_reusable():
     assert target_cache_reusable(_mk()())
+
+
+def _free(pc):
+    return [len(a.free) for a in pc.arenas]
+
+
+def test_failed_acquire_returns_every_page_it_took():
+    # the second arena's allocation fails after the first arena's private pages were taken and
+    # set into row 0: they go back to the free list and row 0 is left empty in both arenas
+    pc = PrefixCache(_mk(), _mk(layers=1), min_reuse=4)
+    p = list(range(100, 140))
+    _serve(pc, p, [1, 2, 3])
+    before = _free(pc)
+    real = pc._alloc
+
+    def alloc(ai, n):
+        if ai == 1:
+            raise RuntimeError("planted: no pages in the second arena")
+        return real(ai, n)
+
+    pc._alloc = alloc
+    with pytest.raises(RuntimeError, match="planted"):
+        pc.acquire(p + [1, 2, 9])
+    assert _free(pc) == before and [a.cache.lengths for a in pc.arenas] == [[0], [0]]
+    assert pc._out is None
+    pc._alloc = real
+    assert _serve(pc, p + [1, 2, 9], [4]) == len(p) + 2          # the stored prefix is intact
+
+
+def test_failed_load_of_a_spilled_page_returns_its_pages(tmp_path):
+    # a spilled page whose file no longer matches the arena layout: the load fails after the
+    # first arena's page was allocated for it; that page goes back and the node stays spilled
+    pc = PrefixCache(_mk(), _mk(layers=1), min_reuse=4, l2_dir=str(tmp_path), max_ram_bytes=1, slots=2)
+    p = list(range(300, 340))
+    _serve(pc, p, list(range(6)))
+    assert pc.info()["pages"]["resident"] == 0
+    from safetensors.torch import load_file, save_file
+    for f in tmp_path.iterdir():
+        data = load_file(str(f))
+        data = {k: (v[..., :1].contiguous() if k.startswith("1.") else v) for k, v in data.items()}
+        save_file(data, str(f))
+    before = _free(pc)
+    with pytest.raises(ValueError, match="does not match the arena layout"):
+        pc.acquire(p + [5, 5])
+    assert _free(pc) == before and pc.info()["pages"]["resident"] == 0 and pc._out is None
