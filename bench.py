@@ -15,9 +15,12 @@ replay each. Printed (one JSON line):
                drafter almost never matches, so ~1 token per round: accept length is reported)
   verify_us    one verify forward (16 rows, 4096 context), graph-replayed, HIP events
   verify_roofline_frac  algorithmic bytes of that forward / verify_us / 8 TB/s
-  roofline     the dominant kernel, the W8 GEMM at the gate_up shape (24576 x 4096, SwiGLU
-               epilogue): algorithmic bytes per launch over its in-graph average launch time
-               (36 launches, one per layer's weights, HIP events on the launch stream)
+  verify17_us  the same at 17 rows (k = 16 drafts + the bonus row), with its roofline fraction
+  roofline     the dominant kernel: of the W8 GEMM instantiations the verify forward runs (named
+               as a kernel trace names them), the one with the most time per forward; its
+               average launch's algorithmic bytes over its average in-graph launch time (one
+               launch per layer's weights, HIP events on the launch stream); every instantiation
+               with its share is listed under roofline.kernels
   sampled_round_extra_us  the same rounds at temperature 0.6 / top-p 0.95 / top-k 20 (draft
                rows drawn, speculative-sampling acceptance), minus the greedy round time
   acc_us       the standalone acceptance workload [4, 17, 151936] fp32 (T = 1, top-p 0.95),
@@ -31,7 +34,10 @@ replay each. Printed (one JSON line):
   cpu_baseline the CPU oracle (torch, float32 with bf16 rounding points) on the host cores:
                value = accepted tok/s of 5 whole DFlash rounds on the same weights (random
                4096-position context); q06 = the Q06 workload end to end on the same prompt;
-               acc = the acceptance workload, outputs compared with the GPU's
+               acc = the acceptance workload on every host core, outputs compared with the GPU's
+Options for measurements outside the default line: --roofline-only (the GEMM shapes and a copy,
+for counter runs), --gemm-sweep M (every plan of the GEMM at the verify shapes), --legs-only,
+--acc-only, --verify-eager N.
 """
 
 from __future__ import annotations
@@ -49,10 +55,19 @@ sys.path.insert(0, str(REPO / "mlx-dspark_amd"))
 sys.path.insert(0, str(REPO))
 
 PEAK_HBM_GBS = 8000.0
-# HBM bytes per gate_up launch from the FETCH_SIZE / WRITE_SIZE counter runs of
-# `bench.py --roofline-only` (profiles/w8_gemm_gate_up_24576x4096_m16_counters.md): fetches
-# 52855.72 KiB x 2.000 + writes 384 KiB x 1.000, the scales read on a 256 MiB copy
-TRAFFIC_GATE_UP = 108641739
+# HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter runs of `bench.py --roofline-only`
+# (profiles/w8_gemm_*_counters.md), per kernel instantiation: the counters' KiB per dispatch
+# scaled by what they read for a 256 MiB copy
+TRAFFIC = {
+    # gate_up 24576x4096: fetches 52855.70 KiB x 2.000 + writes 384 KiB x 1.000
+    "w8_gemm_kernel<1, 2, 2, 8, 5, true, 8>": 108641693,
+    # o 4096x4096 and down 4096x12288 (one instantiation, mean over both): 18725.63 KiB x 2.000 + 384 KiB
+    "w8_gemm_kernel<1, 1, 4, 16, 3, false, 8>": 38743306,
+    # qkv 6144x4096, split-K partials: 13606.78 KiB x 2.000 + 384 KiB
+    "w8_gemm_kernel<1, 2, 2, 16, 2, true, 8>": 28259905,
+    # lm_head 151936x4096, f32 logits: 323496.43 KiB x 2.000 + 9496.25 KiB
+    "w8_gemm_kernel<1, 4, 2, 8, 4, false, 8>": 672244854,
+}
 
 
 def log(*a):
@@ -117,9 +132,112 @@ def gemm_roofline(model, M: int, reps: int = 10):
         # epilogue reads and writes h and writes the packed next input)
         out_b = {P: 4 * ops.gemm_splits(M, ws[0].N, K), SW: 1, ops.DSK_EPI_STORE: 4, R: 6}[epi] * M * ws[0].N
         by = ws[0].N * K * 1.0625 + M * K * 2 + out_b
-        res[name] = {"us": round(us, 2), "bytes": int(by), "GBs": round(by / us / 1e3, 1), "launches": len(ws)}
+        res[name] = {"us": round(us, 2), "bytes": int(by), "GBs": round(by / us / 1e3, 1), "launches": len(ws),
+                     "kernel": ops.gemm_kernel_name(M, ws[0].N, K, epi, normed_later)}
         del g
     return res
+
+
+def gemm_by_kernel(shapes: dict) -> list:
+    """The per-shape timings grouped by the kernel instantiation that runs them, with each
+    instantiation's time per verify forward (its shapes' in-graph launch times x launches) and
+    share of the GEMM time, largest first. A group's achieved rate is its algorithmic bytes over
+    its time per forward: the average launch's bytes over the average launch's duration."""
+    groups = {}
+    for name, r in shapes.items():
+        g = groups.setdefault(r["kernel"], {"kernel": r["kernel"], "shapes": [], "us_per_forward": 0.0,
+                                            "bytes_per_forward": 0, "launches_per_forward": 0})
+        g["shapes"].append(name)
+        g["us_per_forward"] += r["us"] * r["launches"]
+        g["bytes_per_forward"] += r["bytes"] * r["launches"]
+        g["launches_per_forward"] += r["launches"]
+    total = sum(g["us_per_forward"] for g in groups.values())
+    out = []
+    for g in sorted(groups.values(), key=lambda g: -g["us_per_forward"]):
+        achieved = g["bytes_per_forward"] / g["us_per_forward"] / 1e3
+        out.append({**g, "us_per_forward": round(g["us_per_forward"], 1), "share": round(g["us_per_forward"] / total, 4),
+                    "bytes_per_launch": int(g["bytes_per_forward"] / g["launches_per_forward"]),
+                    "us_per_launch": round(g["us_per_forward"] / g["launches_per_forward"], 2),
+                    "achieved": round(achieved, 1), "frac": round(achieved / PEAK_HBM_GBS, 4),
+                    "traffic": TRAFFIC.get(g["kernel"])})
+    return out
+
+
+def gemm_sweep(model, M: int, reps: int = 10) -> dict:
+    """Plan sweep of the W8 GEMM at the verify-step shapes through the explicit-plan tuning
+    entry (dsk_w8_gemm_rn_planned): every plan it accepts (slab tiles 1-8 dividing the tile
+    count, 2- or 4-group batches, 4 / 8 / 16 waves, 1-8 K splits for the partial sums, loads
+    pipelined or not), each timed as gemm_roofline times the planner's own (one launch per layer
+    on that layer's weights in one graph, HIP events); the planner's choice is marked. The
+    planner's rules (w8.hip, plan_gemm) were fitted to sweeps of this kind."""
+    import torch
+    from mlx_dspark import _hip, ops
+    from mlx_dspark._hip import ptr, stream_ptr
+
+    dev = model.device
+    P, SW, R, ST = ops.DSK_EPI_PARTIAL, ops.DSK_EPI_SWIGLU, ops.DSK_EPI_RESIDUAL, ops.DSK_EPI_STORE
+    eps = model.args.rms_norm_eps
+    shapes = {"qkv": ([L.qkv for L in model.layers], P, False), "o": ([L.o for L in model.layers], R, False),
+              "gate_up": ([L.gate_up for L in model.layers], SW, True),
+              "down": ([L.down for L in model.layers], R, False), "lm_head": ([model.lm_head], ST, True)}
+    stream = torch.cuda.current_stream()
+    out = {}
+    for name, (ws, epi, rs) in shapes.items():
+        N, K = ws[0].N, ws[0].K
+        xr = torch.randn(M, K, device=dev).to(torch.bfloat16)
+        x = ops.pack_rn(M=M, K=K, h=xr, norm_w=model.norm, eps=eps) if rs else ops.pack(xr)
+        h = torch.randn(M, N, device=dev).to(torch.bfloat16)
+        nxt = ops.Packed.empty(M, N, dev, normed_later=True, eps=eps) if epi == R else None
+        tiles, G = N // 16, K // 64
+        planner = ops.gemm_plan(M, N, K, epi)
+        rows = []
+        for nt in (1, 2, 3, 4, 6, 8):
+            if tiles % nt or (epi == SW and nt % 2):
+                continue
+            for u in (2, 4):
+                for waves in (4, 8, 16):
+                    for sk in ((1, 2, 3, 4, 5, 8) if epi == P else (1,)):
+                        for pf in (0, 1):
+                            plan = (nt, u, waves, sk, pf)
+                            if G % u or sk > G // u or waves * ((M + 15) // 16) * nt * 1024 > 65536:
+                                continue
+                            y = (torch.empty(sk, M, N, device=dev) if epi == P else
+                                 torch.empty(M, N, device=dev) if epi == ST else ops.Packed.empty(M, N // 2, dev).data)
+
+                            def launch(w, plan=plan, y=y):
+                                _hip.call("dsk_w8_gemm_rn_planned", ptr(x.data), ptr(w.wt), ptr(w.sb), w.bits, M, N, K,
+                                          epi, ptr(nxt.data if epi == R else y), ops.DSK_F32 if epi in (P, ST) else ops.DSK_BF16,
+                                          N if epi == ST else 0, 0.0, ptr(x.ssq), K // 16 if rs else 0, float(eps),
+                                          ptr(h if epi == R else None), N if epi == R else 0, None, 0,
+                                          ptr(model.norm if epi == R else None),
+                                          ptr(nxt.ssq if epi == R else None), *plan, stream_ptr())
+                            try:
+                                launch(ws[0])
+                                torch.cuda.synchronize()
+                            except RuntimeError:            # no compiled kernel for this plan
+                                continue
+                            g = torch.cuda.CUDAGraph()
+                            with torch.cuda.graph(g):
+                                for w in ws:
+                                    launch(w)
+                            g.replay()
+                            s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                            torch.cuda.synchronize()
+                            s_ev.record(stream)
+                            for _ in range(reps):
+                                g.replay()
+                            e_ev.record(stream)
+                            torch.cuda.synchronize()
+                            us = s_ev.elapsed_time(e_ev) * 1e3 / (reps * len(ws))
+                            rows.append({"plan": list(plan), "us": round(us, 2), "planner": plan == tuple(planner)})
+                            del g
+        rows.sort(key=lambda r: r["us"])
+        out[name] = {"N": N, "K": K, "planner_plan": list(planner),
+                     "planner_us": next((r["us"] for r in rows if r["planner"]), None),
+                     "best": rows[0] if rows else None, "plans": rows}
+        log(f"sweep {name} {N}x{K} at M={M}: {len(rows)} plans, best {rows[0] if rows else None}, "
+            f"planner {out[name]['planner_us']} us")
+    return out
 
 
 ACC_SHAPE = (4, 16, 151936)   # batch, drafts per row, vocabulary
@@ -373,8 +491,9 @@ def verify_leg(shape: str, lens: list, W: int, reps: int = 30) -> dict:
 
 
 def cpu_acc(gpu_out=None, reps: int = 3) -> dict:
-    """The acceptance oracle (C, one thread) on the standalone acceptance workload: median of
-    ``reps`` runs; outputs compared with the GPU's on the same inputs and Philox (seed, offset)."""
+    """The acceptance oracle (C; its (row, position) items spread over the host cores with OpenMP)
+    on the standalone acceptance workload: median of ``reps`` runs; outputs compared with the GPU's
+    on the same inputs and Philox (seed, offset)."""
     from oracle import accept as A
     p, q, draft = (t.numpy() for t in acc_inputs())
     times, res = [], None
@@ -382,7 +501,7 @@ def cpu_acc(gpu_out=None, reps: int = 3) -> dict:
         t0 = time.perf_counter()
         res = A.accept_sample(p, q, draft, 1.0, 0.95, 0, seed=7, offset=0)
         times.append(time.perf_counter() - t0)
-    out = {"ms": round(statistics.median(times) * 1e3, 1), "cores": 1}
+    out = {"ms": round(statistics.median(times) * 1e3, 1), "cores": A.threads()}
     if gpu_out is not None:
         out["bit_exact_vs_gpu"] = bool(list(res["n"]) == gpu_out["n"] and list(res["token"]) == gpu_out["token"])
     return out
@@ -407,6 +526,8 @@ def main(argv=None) -> int:
                     help="build the target, time the W8 GEMM shapes and a 256 MiB copy only (counter runs)")
     ap.add_argument("--acc-only", action="store_true",
                     help="time the standalone acceptance workload [4, 17, 151936] only")
+    ap.add_argument("--gemm-sweep", type=int, default=0, metavar="M",
+                    help="build the target and sweep the W8 GEMM plans at the verify shapes for M rows (one JSON line)")
     ap.add_argument("--verify-eager", type=int, default=0, metavar="N",
                     help="build the target, prefill the context, run N eager verify forwards and exit "
                          "(one kernel launch per op: for counter collection)")
@@ -448,6 +569,10 @@ def main(argv=None) -> int:
         shapes = gemm_roofline(model, args.block)
         copy_calibration()
         print(json.dumps({"roofline_only": shapes}), flush=True)
+        return 0
+    if args.gemm_sweep:
+        print(json.dumps({"gemm_sweep": {"M": args.gemm_sweep, "shapes": gemm_sweep(model, args.gemm_sweep)}}),
+              flush=True)
         return 0
     tok = SyntheticTokenizer(model.args.vocab_size)
     target = Target(model, tok, kv_bits=kv_bits)
@@ -564,11 +689,35 @@ def main(argv=None) -> int:
     log(f"verify step: {verify_us:.1f} us for {alg_bytes / 1e9:.3f} GB algorithmic "
         f"-> {alg_bytes / verify_us / 1e3:.0f} GB/s ({verify_frac * 100:.1f}% of HBM roofline)")
 
-    # ---- dominant kernel: the W8 GEMM, gate_up shape (the largest share of the verify step)
+    # ---- the same verify step at W = 17 (k = 16 drafts + the bonus row)
+    W17 = W + 1
+    vids17 = torch.randint(0, model.args.vocab_size, (1, W17), dtype=torch.int32, device=model.device)
+    model.forward(vids17, cache, tap, advance=False)
+    g17 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g17):
+        model.forward(vids17, cache, tap, advance=False)
+    for _ in range(3):
+        g17.replay()
+    torch.cuda.synchronize()
+    s_ev.record()
+    for _ in range(args.verify_reps):
+        g17.replay()
+    e_ev.record()
+    torch.cuda.synchronize()
+    verify17_us = s_ev.elapsed_time(e_ev) * 1e3 / args.verify_reps
+    alg17 = model.weight_bytes + kvpt * L_now + kvpt * W17 + W17 * model.args.vocab_size * 4
+    verify17_frac = alg17 / (verify17_us * 1e-6) / (PEAK_HBM_GBS * 1e9)
+    del g17
+    log(f"verify step at W = {W17}: {verify17_us:.1f} us ({verify17_frac * 100:.1f}% of HBM roofline)")
+
+    # ---- the dominant kernel: of the W8 GEMM instantiations the verify step runs, the one with
+    # the most time per forward (in-graph launch times x launches per forward)
     shapes = gemm_roofline(model, W)
-    dom = shapes["gate_up"]
-    achieved = dom["bytes"] / dom["us"] / 1e3
+    kernels = gemm_by_kernel(shapes)
+    dom = kernels[0]
+    achieved = dom["achieved"]
     log(f"W8 GEMM per shape: {json.dumps(shapes)}")
+    log(f"W8 GEMM per kernel: {json.dumps(kernels)}")
 
     # ---- standalone acceptance workload and the Q06 end-to-end workload on the GPU
     acc = acc_timing()
@@ -628,11 +777,15 @@ def main(argv=None) -> int:
         "verify_roofline_frac": round(verify_frac, 4),
         "prefill_ms": round(prefill_ms, 1),
         "prefill_tflops": round(prefill_flop / prefill_ms / 1e9, 1),
-        "roofline": {"kernel": "w8_gemm_kernel<1, 2, 2, 8, 5, true, 8> (W8 GEMM, gate_up 24576x4096, M=16, "
-                               "SwiGLU of a normed-later x)",
+        "verify17_us": round(verify17_us, 1),
+        "verify17_alg_bytes": int(alg17),
+        "verify17_roofline_frac": round(verify17_frac, 4),
+        "roofline": {"kernel": f"{dom['kernel']} (W8 GEMM: {' and '.join(dom['shapes'])} of the {W}-row verify, "
+                               f"{dom['share'] * 100:.1f}% of its GEMM time)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_GATE_UP,
-                     "bytes_per_launch": dom["bytes"], "us_per_launch": dom["us"], "per_shape": shapes},
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": TRAFFIC.get(dom["kernel"]),
+                     "bytes_per_launch": dom["bytes_per_launch"], "us_per_launch": dom["us_per_launch"],
+                     "kernels": kernels, "per_shape": shapes},
         "acc_us": acc["us"],
         "acc_roofline_frac": acc["roofline_frac"],
         "acc": {k: v for k, v in acc.items() if k not in ("n", "token")},

@@ -171,6 +171,12 @@ int dsk_w8_gemm_rn_planned(const uint16_t* x, const uint8_t* wt, const uint32_t*
                            float* ssq_out, int slab_tiles, int batch_groups, int waves, int k_splits,
                            int pipelined, dsk_stream_t stream);
 
+/* Introspection entry, with no counterpart in the reference: the plan dsk_w8_gemm / dsk_w8_gemm_rn
+ * run for this shape and epilogue, as plan[5] = {slab_tiles, batch_groups, waves, k_splits,
+ * pipelined} in the terms of dsk_w8_gemm_rn_planned (for plan sweeps and to name the kernel
+ * instantiation a measurement covers). */
+int dsk_w8_gemm_plan(int M, int64_t N, int64_t K, int epi, int bits, int* plan);
+
 /* ---------------------------------------------------------------------------------------
  * Dense prefill (src/mlx_dspark/generate.py:613-656, _prefill_tapped: the prompt in chunks of
  * PREFILL_CHUNK = 2048 rows through the target). A long prompt runs layer by layer over all of

@@ -68,7 +68,7 @@ def build_hip(jobs: int | None = None) -> Path:
 
 def build_oracle() -> Path:
     tmp = ORACLE_LIB.with_suffix(".so.tmp")
-    _run(["gcc", "-O2", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared",
+    _run(["gcc", "-O2", "-ffp-contract=off", "-fno-fast-math", "-fopenmp", "-fPIC", "-shared",
           str(ORACLE_SRC), "-o", str(tmp), "-lm"])
     os.replace(tmp, ORACLE_LIB)
     return ORACLE_LIB

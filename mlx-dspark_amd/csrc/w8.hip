@@ -1150,6 +1150,20 @@ extern "C" int dsk_w8_gemm_rn_planned(const uint16_t* xp, const uint8_t* wt, con
                     &nio, &p);
 }
 
+extern "C" int dsk_w8_gemm_plan(int M, int64_t N, int64_t K, int epi, int bits, int* plan) {
+  DSK_REQUIRE(plan, "dsk_w8_gemm_plan: null output");
+  DSK_REQUIRE(bits == 8 || bits == 4, "dsk_w8_gemm_plan: bits=%d (8 or 4)", bits);
+  DSK_REQUIRE(M > 0 && M <= 64 && N > 0 && N % 16 == 0 && K > 0 && K % 256 == 0,
+              "dsk_w8_gemm_plan: shape M=%d N=%lld K=%lld outside the GEMM's limits", M, (long long)N, (long long)K);
+  const GemmPlan p = plan_gemm(M, N, K, epi, bits);
+  plan[0] = p.nt;
+  plan[1] = p.u;
+  plan[2] = p.waves;
+  plan[3] = p.sk;
+  plan[4] = p.pf ? 1 : 0;
+  return DSK_OK;
+}
+
 static int gemm_entry(const char* who, int bits, const uint16_t* xp, const uint8_t* wt, const uint32_t* sb, int M,
                       int64_t N, int64_t K, int epi, void* y, int y_dtype, int64_t ldy, const uint16_t* residual,
                       int64_t ldr, float softcap, hipStream_t st, const NormIO* nio, const GemmPlan* forced) {

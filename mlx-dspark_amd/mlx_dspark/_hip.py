@@ -42,6 +42,7 @@ SIGNATURES: dict[str, tuple] = {
     "dsk_w8_gemm_rn": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int64, c_int64, c_int, c_void_p, c_int,
                                c_int64, c_float, c_void_p, c_int, c_float, c_void_p, c_int64, c_void_p, c_int64,
                                c_void_p, c_void_p, c_void_p]),
+    "dsk_w8_gemm_plan": (c_int, [c_int, c_int64, c_int64, c_int, c_int, c_void_p]),
     "dsk_w8_gemm_rn_planned": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int64, c_int64, c_int, c_void_p,
                                        c_int, c_int64, c_float, c_void_p, c_int, c_float, c_void_p, c_int64, c_void_p,
                                        c_int64, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),

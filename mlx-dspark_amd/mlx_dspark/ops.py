@@ -7,6 +7,8 @@ tensors must live on a HIP device.
 
 from __future__ import annotations
 
+import ctypes
+
 import math
 from dataclasses import dataclass
 
@@ -273,6 +275,26 @@ def pack(x: torch.Tensor, norm_w: torch.Tensor | None = None, eps: float = 1e-6)
 def gemm_splits(M: int, N: int, K: int, bits: int = 8) -> int:
     """K-split slices of a DSK_EPI_PARTIAL product (the 4-bit kernel plans its own)."""
     return (_hip.lib.dsk_w8_gemm_splits if bits == 8 else _hip.lib.dsk_w4_gemm_splits)(M, N, K)
+
+
+def gemm_plan(M: int, N: int, K: int, epi: int, bits: int = 8) -> tuple:
+    """The plan the library runs for this GEMM: (slab_tiles, batch_groups, waves, k_splits,
+    pipelined), in the terms of the explicit-plan tuning entry (dsk_w8_gemm_plan)."""
+    out = (ctypes.c_int * 5)()
+    call("dsk_w8_gemm_plan", int(M), int(N), int(K), int(epi), int(bits), ctypes.cast(out, ctypes.c_void_p))
+    return tuple(out)
+
+
+_EPILOGUE_KIND = {DSK_EPI_STORE: 0, DSK_EPI_SWIGLU: 1, DSK_EPI_GEGLU: 1, DSK_EPI_PARTIAL: 2, DSK_EPI_RESIDUAL: 3}
+
+
+def gemm_kernel_name(M: int, N: int, K: int, epi: int, row_scale: bool, bits: int = 8, plan=None) -> str:
+    """The kernel instantiation a GEMM launch runs (as a kernel trace names it):
+    w8_gemm_kernel<row tiles, slab tiles, batch groups, waves, epilogue (+4 with the row scale
+    of a normed-later x passed in), pipelined, bits>."""
+    nt, u, waves, _, pf = plan or gemm_plan(M, N, K, epi, bits)
+    ekr = _EPILOGUE_KIND[epi] + (4 if row_scale else 0)
+    return f"w8_gemm_kernel<{(M + 15) // 16}, {nt}, {u}, {waves}, {ekr}, {'true' if pf else 'false'}, {bits}>"
 
 
 def w8_gemm(x: Packed, w: W8Weight, *, epi: int = DSK_EPI_STORE, out=None, out_dtype: torch.dtype = torch.bfloat16,

@@ -51,12 +51,18 @@ def lib():
                                            vp, vp, vp, vp, vp]
         L.oracle_accept_greedy.argtypes = [vp, i32, i64, i32, i32, i64, vp, vp, vp, vp, vp]
         L.oracle_sample_rows.argtypes = [vp, i64, i32, f32, f32, i32, i32, u64, u32, i32, vp, vp]
+        L.oracle_threads.restype = i32
         _lib = L
     return _lib
 
 
 def _p(a):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def threads() -> int:
+    """Threads the sampled acceptance spreads its (row, position) items over (OpenMP)."""
+    return int(lib().oracle_threads())
 
 
 def philox(ctr, key):

@@ -34,6 +34,9 @@
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 #include <string.h>
 
 /* ------------------------------------------------------------------------ Philox4x32-10 */
@@ -224,52 +227,93 @@ int64_t oracle_categorical(const float* w, int64_t V, uint32_t word) {
 }
 
 /* ------------------------------------------------------------------------ accept (sampled) */
+/* Every (row b, position i) item is independent (its p, q, residual and uniforms are keyed by
+ * b and i), so the items run in parallel (OpenMP, each item in its own buffers); the accepted
+ * prefix of each row is then read off in order. Results do not depend on the thread count. */
+static void accept_item(const float* p_logits, const float* q_logits, int64_t V, int L, const int32_t* draft,
+                        float T, float top_p, int top_k, int q_mul_inv_t, uint64_t seed, uint32_t offset, int b,
+                        int i, float* p, float* q, float* r, uint8_t* acc_out, int32_t* samp_out) {
+  const float* pl = p_logits + ((int64_t)b * (L + 1) + i) * V;
+  oracle_probs(pl, V, T, 0, top_p, top_k, p);
+  int acc = 0, samp;
+  if (i < L) {
+    const int32_t d = draft[(int64_t)b * L + i];
+    const int dvalid = d >= 0 && (int64_t)d < V; /* an out-of-range id is rejected */
+    float qd;
+    if (q_logits) {
+      oracle_probs(q_logits + ((int64_t)b * L + i) * V, V, T, q_mul_inv_t, top_p, top_k, q);
+      qd = dvalid ? q[d] : 1.0f;
+    } else {
+      for (int64_t j = 0; j < V; ++j) q[j] = (j == d) ? 1.0f : 0.0f;
+      qd = 1.0f;
+    }
+    const float pd = dvalid ? p[d] : 0.0f;
+    const float u = u24_to_float(philox_word(seed, (uint32_t)i, (uint32_t)b, 0u, offset));
+    float ratio = pd / (qd > 1e-9f ? qd : 1e-9f);
+    if (ratio > 1.0f) ratio = 1.0f;
+    acc = u < ratio;
+    for (int64_t j = 0; j < V; ++j) {
+      float t = p[j] - q[j];
+      r[j] = t > 0.0f ? t : 0.0f;
+    }
+    samp = (int)oracle_categorical(r, V, philox_word(seed, (uint32_t)i, (uint32_t)b, 1u, offset));
+  } else {
+    samp = (int)oracle_categorical(p, V, philox_word(seed, (uint32_t)i, (uint32_t)b, 1u, offset));
+  }
+  *acc_out = (uint8_t)acc;
+  *samp_out = samp;
+}
+
+int oracle_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
 int oracle_accept_sample(const float* p_logits, const float* q_logits, int64_t V, int B, int L,
                          const int32_t* draft, float T, float top_p, int top_k, int q_mul_inv_t,
                          uint64_t seed, uint32_t offset, int32_t* n_out, int32_t* token_out,
                          int32_t* seq_lens, uint8_t* accept_out, int32_t* sample_out) {
-  float* p = (float*)malloc(sizeof(float) * (size_t)V);
-  float* q = (float*)malloc(sizeof(float) * (size_t)V);
-  float* r = (float*)malloc(sizeof(float) * (size_t)V);
-  if (!p || !q || !r) return -1;
+  const int items = B * (L + 1);
+  uint8_t* accv = (uint8_t*)malloc((size_t)items);
+  int32_t* sampv = (int32_t*)malloc(sizeof(int32_t) * (size_t)items);
+  if (!accv || !sampv) return -1;
+  int fail = 0;
+#pragma omp parallel for schedule(dynamic, 1)
+  for (int it = 0; it < items; ++it) {
+    float* p = (float*)malloc(sizeof(float) * (size_t)V);
+    float* q = (float*)malloc(sizeof(float) * (size_t)V);
+    float* r = (float*)malloc(sizeof(float) * (size_t)V);
+    if (p && q && r)
+      accept_item(p_logits, q_logits, V, L, draft, T, top_p, top_k, q_mul_inv_t, seed, offset, it / (L + 1),
+                  it % (L + 1), p, q, r, accv + it, sampv + it);
+    else {
+#pragma omp atomic write
+      fail = 1;
+    }
+    free(p);
+    free(q);
+    free(r);
+  }
+  if (fail) {
+    free(accv);
+    free(sampv);
+    return -1;
+  }
   for (int b = 0; b < B; ++b) {
     int n = 0, done = 0, token = -1;
     for (int i = 0; i <= L; ++i) {
-      const float* pl = p_logits + ((int64_t)b * (L + 1) + i) * V;
-      oracle_probs(pl, V, T, 0, top_p, top_k, p);
-      int acc = 0, samp;
-      if (i < L) {
-        const int32_t d = draft[(int64_t)b * L + i];
-        const int dvalid = d >= 0 && (int64_t)d < V; /* an out-of-range id is rejected */
-        float qd;
-        if (q_logits) {
-          oracle_probs(q_logits + ((int64_t)b * L + i) * V, V, T, q_mul_inv_t, top_p, top_k, q);
-          qd = dvalid ? q[d] : 1.0f;
-        } else {
-          for (int64_t j = 0; j < V; ++j) q[j] = (j == d) ? 1.0f : 0.0f;
-          qd = 1.0f;
-        }
-        const float pd = dvalid ? p[d] : 0.0f;
-        const float u = u24_to_float(philox_word(seed, (uint32_t)i, (uint32_t)b, 0u, offset));
-        float ratio = pd / (qd > 1e-9f ? qd : 1e-9f);
-        if (ratio > 1.0f) ratio = 1.0f;
-        acc = u < ratio;
-        for (int64_t j = 0; j < V; ++j) {
-          float t = p[j] - q[j];
-          r[j] = t > 0.0f ? t : 0.0f;
-        }
-        samp = (int)oracle_categorical(r, V, philox_word(seed, (uint32_t)i, (uint32_t)b, 1u, offset));
-      } else {
-        samp = (int)oracle_categorical(p, V, philox_word(seed, (uint32_t)i, (uint32_t)b, 1u, offset));
-      }
-      if (accept_out && i < L) accept_out[(int64_t)b * L + i] = (uint8_t)acc;
-      if (sample_out) sample_out[(int64_t)b * (L + 1) + i] = samp;
+      const int it = b * (L + 1) + i;
+      if (accept_out && i < L) accept_out[(int64_t)b * L + i] = accv[it];
+      if (sample_out) sample_out[(int64_t)b * (L + 1) + i] = sampv[it];
       if (!done) {
-        if (i < L && acc) {
+        if (i < L && accv[it]) {
           ++n;
         } else {
           done = 1;
-          token = samp;
+          token = sampv[it];
         }
       }
     }
@@ -277,9 +321,8 @@ int oracle_accept_sample(const float* p_logits, const float* q_logits, int64_t V
     token_out[b] = token;
     if (seq_lens) seq_lens[b] += n + 1;
   }
-  free(p);
-  free(q);
-  free(r);
+  free(accv);
+  free(sampv);
   return 0;
 }
 

@@ -53,3 +53,21 @@ def test_error_path_reports_message():
     rc = _hip.lib.dsk_w8_quantize(None, 0, 16, 64, None, None, None, None)
     assert rc == -1
     assert b"null pointer" in _hip.lib.dsk_last_error()
+
+
+def test_gemm_plan_query_names_the_traced_kernels():
+    # the verify step's GEMMs at 16 rows, named as the kernel trace of the Qwen3-8B verify forward
+    # names them (w8_gemm_kernel<row tiles, slab tiles, batch groups, waves, epilogue, pipelined, bits>)
+    from mlx_dspark import ops
+    P, R, SW, ST = ops.DSK_EPI_PARTIAL, ops.DSK_EPI_RESIDUAL, ops.DSK_EPI_SWIGLU, ops.DSK_EPI_STORE
+    want = {(6144, 4096, P, False): "w8_gemm_kernel<1, 2, 2, 16, 2, true, 8>",
+            (4096, 4096, R, False): "w8_gemm_kernel<1, 1, 4, 16, 3, false, 8>",
+            (24576, 4096, SW, True): "w8_gemm_kernel<1, 2, 2, 8, 5, true, 8>",
+            (4096, 12288, R, False): "w8_gemm_kernel<1, 1, 4, 16, 3, false, 8>",
+            (151936, 4096, ST, True): "w8_gemm_kernel<1, 4, 2, 8, 4, false, 8>"}
+    for (N, K, epi, rs), name in want.items():
+        assert ops.gemm_kernel_name(16, N, K, epi, rs) == name
+    assert ops.gemm_plan(16, 4096, 4096, R)[3] == 1            # the residual epilogue never splits K
+    import pytest
+    with pytest.raises(RuntimeError):
+        ops.gemm_plan(16, 4096, 4000, R)
