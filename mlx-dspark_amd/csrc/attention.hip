@@ -168,6 +168,9 @@ struct AttnArgs {
   int fused;         // splits 0 .. nsplit-2: cached keys; split nsplit-1: the new tokens
   float* part_o;     // [B*nkv][nsplit][R][HD] float32: the split's o / l
   float* part_ml;    // [B*nkv][nsplit][R][2]: the split's running max m and sum l
+  int tgroups;       // verify kernel: groups of QT query tiles per kv head, one workgroup each
+  int wrel;          // verify kernel, sliding window: split s of row b starts at split
+                     // max(0, seq_lens[b] - window + 1) / kps + s (nsplit covers one window)
 };
 
 // page ids one split may span (kps / page + 1), held in LDS
@@ -832,55 +835,57 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
     a.out[attn_out_index(a, HD, b, i, kvh * a.G + hl, lane * PER + e)] = f32_to_bf16(acc[e] * inv);
 }
 
-// ----------------------------------------------------------------------------- verify (head_dim 128)
-// A verify pass (at most 64 query rows per kv head, head_dim 128, keys already in the pool): one
-// workgroup of 4 waves per (row b, kv head, split of 256 keys). Wave w owns the split's keys
-// [64 w, 64 w + 64) (four 16-key tiles): it loads their K/V rows straight from the pool into
-// registers, dequantises each element once (K row-major for the score MFMA, V transposed for the
-// P.V MFMA), then runs every query tile of the kv head (staged once in LDS) over its 64 keys, the
-// tiles interleaved. The four waves' (o, m, l) meet in LDS and wave w merges query tile w into the
-// split's partial (or the output when there is one split).
-//  - head_dim order: lane group a = lane / 16 holds dims [32 a, 32 a + 32) of its key row (one
-//    contiguous 32-byte (8-bit) or 64-byte (bf16) load, inside one quantization group), so k-step
-//    s of the score MFMA takes dims 32 a + 8 s .. + 7 from both K (A operand: lane = key) and Q
+// ----------------------------------------------------------------------------- verify passes
+// A verify pass (at most 64 query rows per kv head at head_dim 128, 32 at 256; keys already in
+// the pool): one workgroup of 4 waves per (row b, kv head, split of 4 x 16 KB keys), KB 16-key
+// tiles per wave (4 at head_dim 128: 256-key splits; 2 at 256: 128-key splits). Wave w owns the
+// split's keys [16 KB w, 16 KB (w + 1)): it loads their K/V rows straight from the pool into
+// registers, dequantises each element once (K row-major for the score MFMA, V transposed for
+// the P.V MFMA), then runs every query tile of its group (staged once in LDS) over its keys, the
+// tiles interleaved. The four waves' (o, m, l) meet in LDS and wave w merges query tile w into
+// the split's partial (or the output when there is one split).
+//  - head_dim order: lane group a = lane / 16 holds dims [DPL a, DPL a + DPL) of its key row,
+//    DPL = HD / 4 (one contiguous load, inside one 64-dim quantization group), so k-step s of
+//    the score MFMA takes dims DPL a + 8 s .. + 7 from both K (A operand: lane = key) and Q
 //    (B operand: lane = query): S^T[key][q] summed over a permutation of head_dim.
 //  - V is transposed in registers: v_mfma_f32_16x16x16_bf16 of a 16-key x 16-dim tile (lane =
-//    key, dims 32 a + 4 dt .. + 3) with the identity gives lane (a, c) the keys 4 a .. 4 a + 3 at
-//    physical dim 32 (c / 4) + 4 dt + c % 4 (exact: bf16 in, f32 out). Two key tiles give the 8
-//    keys {4 a + r, 16 + 4 a + r} the lane also holds scores for, so P^T goes from the score
-//    registers straight into the P.V MFMA.
-//  - O^T[dim index][q]: lane (a, q) ends with physical dims 32 a + 4 dt + r.
-// Masks, the softmax (probabilities rounded to bf16) and the partial layout are the attention
-// kernel's; attention_verify_combine_kernel merges the splits (a split past a row's keys writes
-// m = -inf, which the merge skips).
+//    key, dims DPL a + 4 dt .. + 3) with the identity gives lane (a, c) the keys 4 a .. 4 a + 3
+//    at physical dim DPL (c / 4) + 4 dt + c % 4 (exact: bf16 in, f32 out). Two key tiles give
+//    the 8 keys {4 a + r, 16 + 4 a + r} the lane also holds scores for, so P^T goes from the
+//    score registers straight into the P.V MFMA.
+//  - O^T[dim index][q]: lane (a, q) ends with physical dims DPL a + 4 dt + r.
+// The probabilities stay float32 (three bf16 terms in the P.V MFMAs); masks and the partial
+// layout are the attention kernel's; attention_verify_combine_kernel merges the splits (a split
+// past a row's keys, or before every window of its rows, writes m = -inf, which the merge skips).
 constexpr int kVerifyBlock = 32;   // keys per page-aligned block (the page size is a multiple)
 constexpr int kVerifyWaves = 4;
-constexpr int kVerifyKeys = 256;   // keys per split: 64 per wave
-constexpr int kVerifyMaxR = 64;    // query rows per kv head
+template <int HD> struct VerifyShape {
+  static constexpr int KB = HD == 128 ? 4 : 2;          // 16-key tiles per wave
+  static constexpr int KEYS = kVerifyWaves * 16 * KB;   // keys per split
+  static constexpr int MAXR = HD == 128 ? 64 : 32;      // query rows per kv head (LDS of the merge)
+};
 
-template <int KVT>
+template <int HD, int KVT>
 __device__ __forceinline__ void verify_load_rows(const void* pool, const uint32_t* sbp, int64_t tok, int grp,
-                                                 u32x4 (&c)[2], u32x4 (&c2)[2], uint32_t& sb) {
+                                                 u32x4 (&c)[HD / 32], uint32_t& sb) {
+  constexpr int DPL = HD / 4;
   if (KVT == DSK_KV_BF16) {
-    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(pool) + tok * 128 + grp * 32);
-    c[0] = p[0];
-    c[1] = p[1];
-    c2[0] = p[2];
-    c2[1] = p[3];
+    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(pool) + tok * HD + grp * DPL);
+#pragma unroll
+    for (int i = 0; i < DPL / 8; ++i) c[i] = p[i];
   } else {
-    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(pool) + tok * 128 + grp * 32);
-    c[0] = p[0];
-    c[1] = p[1];
-    sb = sbp[tok * 2 + (grp >> 1)];
+    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(pool) + tok * HD + grp * DPL);
+#pragma unroll
+    for (int i = 0; i < DPL / 16; ++i) c[i] = p[i];
+    sb = sbp[tok * (HD / 64) + grp * DPL / 64];
   }
 }
 
-// 8 values of a lane's 32-dim row slice, elements e0 .. e0 + 7 (dequantised for 8-bit KV)
-template <int KVT>
-__device__ __forceinline__ bf16x8 verify_elems8(const u32x4 (&c)[2], const u32x4 (&c2)[2], uint32_t sb, int e0) {
+// 8 values of a lane's DPL-dim row slice, elements e0 .. e0 + 7 (dequantised for 8-bit KV)
+template <int HD, int KVT>
+__device__ __forceinline__ bf16x8 verify_elems8(const u32x4 (&c)[HD / 32], uint32_t sb, int e0) {
   if (KVT == DSK_KV_BF16) {
-    const int w = e0 / 8;
-    return __builtin_bit_cast(bf16x8, w < 2 ? c[w] : c2[w - 2]);
+    return __builtin_bit_cast(bf16x8, c[e0 / 8]);
   } else {
     const float s = bf16_to_f32((uint16_t)(sb & 0xffffu)), b = bf16_to_f32((uint16_t)(sb >> 16));
     const u32x4 v = c[e0 / 16];
@@ -899,70 +904,87 @@ __device__ __forceinline__ bf16x8 verify_elems8(const u32x4 (&c)[2], const u32x4
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 
-template <int KVT, bool SOFTCAP, int QT>
-__global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void attention_verify_kernel(AttnArgs a) {
-  constexpr int HD = 128, QROW = HD + 8;
-  constexpr int NW = kVerifyWaves, KB = kVerifyKeys / NW / 16;  // waves, 16-key tiles per wave
-  __shared__ f32x4 mo[QT][NW][8][64];                // every tile's (o) per [tile][wave][d tile][lane]
+// Workgroups: (row b, kv head, split) x tgroups query-tile groups of QT tiles. The groups of one
+// split are 8 workgroup ids apart, so they run on one XCD (workgroups go to the 8 XCDs round
+// robin) and the second reads the split's K/V from that XCD's L2; ids past the grid's
+// (b, kv head, split) count exit at once.
+template <int HD, int KVT, bool SOFTCAP, int QT>
+__global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_eu(QT <= 2 && HD == 128 ? 2 : 1,
+                                                                                   QT <= 2 && HD == 128 ? 2 : 1)))
+void attention_verify_kernel(AttnArgs a) {
+  constexpr int QROW = HD + 8, DPL = HD / 4, DT = HD / 16;    // LDS query row, dims per lane, d tiles
+  constexpr int NW = kVerifyWaves, KB = VerifyShape<HD>::KB, KEYS = VerifyShape<HD>::KEYS;
+  constexpr int NC = KVT == DSK_KV_BF16 ? DPL / 8 : DPL / 16;  // 16-byte loads per lane and key row
+  __shared__ f32x4 mo[QT][NW][DT][64];               // every tile's (o) per [tile][wave][d tile][lane]
   __shared__ float2 mml[QT][NW][64];                 // and (m, l) per lane
-  __shared__ __attribute__((aligned(16))) uint16_t qs[QT * 16 * QROW];  // the kv head's query rows
+  __shared__ __attribute__((aligned(16))) uint16_t qs[QT * 16 * QROW];  // the group's query rows
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int grp = lane >> 4, row16 = lane & 15;
-  const int split = blockIdx.x % a.nsplit;
-  const int bk = blockIdx.x / a.nsplit;
+  const int per = 8 * a.tgroups;
+  const int tg = (int)(blockIdx.x % per) / 8;
+  const int task = (int)(blockIdx.x / per) * 8 + (int)(blockIdx.x % 8);
+  if (task >= a.B * a.nkv * a.nsplit) return;
+  const int split = task % a.nsplit;
+  const int bk = task / a.nsplit;
+  const int r0 = tg * QT * 16;                       // the group's first query row
   const int b = bk / a.nkv, kvh = bk % a.nkv;
   const int jmax = a.max_pages * a.page;
-  const int j_beg = split * kVerifyKeys;
+  // splits relative to the window (wrel): the row length first, then the page ids
+  const int off_w = a.wrel ? a.seq_lens[b] : 0;
+  const int j_beg = (split + (a.wrel ? max(0, off_w - a.window + 1) / KEYS : 0)) * KEYS;
   const int j0 = j_beg + 16 * KB * wv;  // the wave's first key
   // independent loads first: the wave's page ids (in the block table for any key) and the row length
-  int pg[KB / 2];
+  int pg[(KB + 1) / 2];
 #pragma unroll
-  for (int i = 0; i < KB / 2; ++i)
+  for (int i = 0; i < (KB + 1) / 2; ++i)
     pg[i] = a.block_table[(int64_t)b * a.max_pages + min(j0 + 32 * i, jmax - 1) / a.page];
-  const int off = a.seq_lens[b];
+  const int off = a.wrel ? off_w : a.seq_lens[b];
   const int j_lim = min(off + a.W, jmax);
-  if (j_beg >= j_lim) {
-    // past every row's keys: an empty partial (m = -inf) for the combine, which reads every split
+  // past every row's keys, or (sliding window) before the window of the group's first row and
+  // so of every row after it: an empty partial (m = -inf) for the combine
+  const bool before_window = a.causal && a.window > 0 && j_beg + KEYS <= off + r0 / a.G - a.window + 1;
+  if (j_beg >= j_lim || before_window) {
     if (a.nsplit > 1)
-      for (int r = threadIdx.x; r < a.R; r += NW * 64)
+      for (int r = r0 + threadIdx.x; r < min(a.R, r0 + QT * 16); r += NW * 64)
         *reinterpret_cast<float2*>(a.part_ml + (((size_t)bk * a.nsplit + split) * a.R + r) * 2) =
             float2{-__builtin_inff(), 0.0f};
     return;
   }
-  const int j_end = min(j_lim, j_beg + kVerifyKeys);
-  const int ntiles = (a.R + 15) >> 4;
+  const int j_end = min(j_lim, j_beg + KEYS);
+  const int ntiles = min(QT, ((a.R + 15) >> 4) - tg * QT);  // the group's tiles
   const bool live = j0 < j_end;  // the wave has keys (uniform)
 
   // ---- loads: the wave's K/V rows (16-key tiles t: keys j0 + 16 t + row16), then the query rows
-  u32x4 kc[KB][2], kc2[KB][2], vc[KB][2], vc2[KB][2];
+  u32x4 kc[KB][HD / 32], vc[KB][HD / 32];
   uint32_t ksb[KB], vsb[KB];
   if (live) {
 #pragma unroll
     for (int t = 0; t < KB; ++t) {
       const int j = j0 + 16 * t;
       const int64_t tok = ((int64_t)pg[t / 2] * a.nkv + kvh) * a.page + (j % a.page) + row16;
-      verify_load_rows<KVT>(a.k_pool, a.k_sb, tok, grp, kc[t], kc2[t], ksb[t]);
-      verify_load_rows<KVT>(a.v_pool, a.v_sb, tok, grp, vc[t], vc2[t], vsb[t]);
+      verify_load_rows<HD, KVT>(a.k_pool, a.k_sb, tok, grp, kc[t], ksb[t]);
+      verify_load_rows<HD, KVT>(a.v_pool, a.v_sb, tok, grp, vc[t], vsb[t]);
     }
   }
+  static_assert(NC <= HD / 32, "row slice registers");
 #pragma unroll
-  for (int u = 0; u < QT * 16 * 16 / (NW * 64); ++u) {
-    const int c = threadIdx.x + NW * 64 * u;  // rows x 16 chunks of 8 dims
-    const int r = c >> 4, ch = c & 15;
+  for (int u = 0; u < QT * 16 * (HD / 8) / (NW * 64); ++u) {
+    const int c = threadIdx.x + NW * 64 * u;  // rows x HD / 8 chunks of 8 dims
+    const int r = c / (HD / 8), ch = c % (HD / 8), rq = r0 + r;
     u32x4 qv = u32x4{0, 0, 0, 0};
-    if (r < a.R)
-      qv = *reinterpret_cast<const u32x4*>(a.q + ((int64_t)(b * a.W + r / a.G) * a.nq + kvh * a.G + r % a.G) * HD +
+    if (rq < a.R)
+      qv = *reinterpret_cast<const u32x4*>(a.q + ((int64_t)(b * a.W + rq / a.G) * a.nq + kvh * a.G + rq % a.G) * HD +
                                            ch * 8);
     *reinterpret_cast<u32x4*>(qs + r * QROW + ch * 8) = qv;
   }
 
   // ---- K dequantised once (the A operand of every score MFMA), V transposed once
-  bf16x8 kel[KB][4], vt[KB / 2][8];
+  bf16x8 kel[KB][DPL / 8], vt[KB / 2][DT];
   if (live) {
 #pragma unroll
     for (int t = 0; t < KB; ++t)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) kel[t][s] = verify_elems8<KVT>(kc[t], kc2[t], ksb[t], 8 * s);
+      for (int s = 0; s < DPL / 8; ++s) kel[t][s] = verify_elems8<HD, KVT>(kc[t], ksb[t], 8 * s);
     // identity B operand of the transpose MFMA: B[k][n] = (k == n), lane holds k = 4 grp + e, n = row16
     s16x4 ident;
 #pragma unroll
@@ -970,14 +992,14 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
 #pragma unroll
     for (int cp = 0; cp < KB / 2; ++cp) {
 #pragma unroll
-      for (int dp = 0; dp < 4; ++dp) {
+      for (int dp = 0; dp < DPL / 8; ++dp) {
         s16x8 v8[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int t = 2 * cp + u;
           // whole-vector bit casts (a bit cast of one element of a bf16 vector reads element 0);
           // keys past the split's end are zeroed (masked, but finite)
-          v8[u] = __builtin_bit_cast(s16x8, verify_elems8<KVT>(vc[t], vc2[t], vsb[t], 8 * dp));
+          v8[u] = __builtin_bit_cast(s16x8, verify_elems8<HD, KVT>(vc[t], vsb[t], 8 * dp));
           if (j0 + 16 * t + row16 >= j_end) v8[u] = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
         }
 #pragma unroll
@@ -1001,20 +1023,20 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
   const float c2 = (SOFTCAP ? 1.0f : a.scale) * 1.4426950408889634f;
   const float mscale = SOFTCAP ? 1.0f : a.scale;  // the stored max is in natural-log units of scale * s
   // a block needs masks when a key may be past the split's end or past some row's position (the
-  // rows of a kv head sit at off .. off + W - 1), or with a sliding window
-  const bool masked = j0 + 16 * KB > j_end || (a.causal && (j0 + 16 * KB - 1 > off || a.window > 0));
+  // group's rows sit at off + r0 / G .. off + W - 1), or with a sliding window
+  const bool masked = j0 + 16 * KB > j_end || (a.causal && (j0 + 16 * KB - 1 > off + r0 / a.G || a.window > 0));
   __syncthreads();  // the query rows
 
   // ---- every query tile over the wave's keys, the tiles interleaved: scores, softmax, P.V; then
-  // (m, l, o) to the merge slots (the host launches QT = the kv head's tile count)
+  // (m, l, o) to the merge slots
   float m[QT], l[QT];
-  f32x4 o[QT][8];
+  f32x4 o[QT][DT];
 #pragma unroll
   for (int tile = 0; tile < QT; ++tile) {
     m[tile] = -__builtin_inff();
     l[tile] = 0.0f;
 #pragma unroll
-    for (int d = 0; d < 8; ++d) o[tile][d] = f32x4{0, 0, 0, 0};
+    for (int d = 0; d < DT; ++d) o[tile][d] = f32x4{0, 0, 0, 0};
   }
   if (live) {
     f32x4 st[QT][KB];
@@ -1023,11 +1045,11 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
 #pragma unroll
       for (int t = 0; t < KB; ++t) st[tile][t] = f32x4{0, 0, 0, 0};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < DPL / 8; ++s) {
       bf16x8 qf[QT];
 #pragma unroll
       for (int tile = 0; tile < QT; ++tile)
-        qf[tile] = *reinterpret_cast<const bf16x8*>(qs + (tile * 16 + row16) * QROW + grp * 32 + 8 * s);
+        qf[tile] = *reinterpret_cast<const bf16x8*>(qs + (tile * 16 + row16) * QROW + grp * DPL + 8 * s);
 #pragma unroll
       for (int t = 0; t < KB; ++t)
 #pragma unroll
@@ -1047,7 +1069,7 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
     if (masked) {
 #pragma unroll
       for (int tile = 0; tile < QT; ++tile) {
-        const int rq = tile * 16 + row16;
+        const int rq = r0 + tile * 16 + row16;
         const int qpos = off + (rq < a.R ? rq : 0) / a.G;
         int k_first = 0, k_last = j_end - 1;
         if (a.causal) {
@@ -1078,7 +1100,7 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
     // per tile: float32 probabilities (in place of the scores) and their sums, then
     // O^T += V^T . P^T over the wave's keys (32 per MFMA) with P as three bf16 terms; a tile's
     // MFMAs run while the next tile's exponentials are computed. One term's MFMAs go over every
-    // d tile before the next term's (8 independent accumulators in between).
+    // d tile before the next term's (independent accumulators in between).
 #pragma unroll
     for (int tile = 0; tile < QT; ++tile) {
       // masked keys: exp2(-inf) = 0; a row with no visible key keeps m = -inf, l = 0
@@ -1109,7 +1131,7 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
         for (int k = 0; k < 3; ++k) {
           const bf16x8 pk = __builtin_bit_cast(bf16x8, (u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}));
 #pragma unroll
-          for (int d = 0; d < 8; ++d)
+          for (int d = 0; d < DT; ++d)
             o[tile][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[cp][d], pk, o[tile][d], 0, 0, 0);
         }
       }
@@ -1122,13 +1144,13 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
 #pragma unroll
   for (int tile = 0; tile < QT; ++tile) {
 #pragma unroll
-    for (int d = 0; d < 8; ++d) mo[tile][wv][d][lane] = o[tile][d];
+    for (int d = 0; d < DT; ++d) mo[tile][wv][d][lane] = o[tile][d];
     mml[tile][wv][lane] = float2{m[tile], l[tile]};
   }
   __syncthreads();
-  // ---- merge of the waves: wave w takes tiles w, w + NW, ... (lane: 32 dims of its row)
+  // ---- merge of the waves: wave w takes tiles w, w + NW, ... (lane: DPL dims of its row)
   for (int tile = wv; tile < ntiles; tile += NW) {
-    const int rq = tile * 16 + row16;
+    const int rq = r0 + tile * 16 + row16;
     if (rq >= a.R) continue;
     float2 ml[NW];
     float M = -__builtin_inff();
@@ -1144,20 +1166,20 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
       L += ml[q].y * wq[q];
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    f32x4 res[8];  // dims 32 grp + 4 d .. + 3
+    f32x4 res[DT];  // dims DPL grp + 4 d .. + 3
 #pragma unroll
-    for (int d = 0; d < 8; ++d) {
+    for (int d = 0; d < DT; ++d) {
       f32x4 acc = f32x4{0, 0, 0, 0};
 #pragma unroll
       for (int q = 0; q < NW; ++q) acc += mo[tile][q][d][lane] * wq[q];
       res[d] = acc * inv;
     }
     if (a.nsplit == 1) {
-      // dims 32 grp .. + 31 in two runs of 16 (contiguous in both output layouts)
+      // dims DPL grp .. + DPL - 1 in runs of 16 (contiguous in both output layouts)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < DPL / 16; ++h) {
         u32x4* dst = reinterpret_cast<u32x4*>(a.out + attn_out_index(a, HD, b, rq / a.G, kvh * a.G + rq % a.G,
-                                                                      grp * 32 + 16 * h));
+                                                                      grp * DPL + 16 * h));
         uint32_t w[8];
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
@@ -1168,34 +1190,40 @@ __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_
         dst[1] = u32x4{w[4], w[5], w[6], w[7]};
       }
     } else {
-      // the split's partial o / l in float32 (32 contiguous dims per lane) and its (m, l)
+      // the split's partial o / l in float32 (DPL contiguous dims per lane) and its (m, l)
       const size_t prow = ((size_t)bk * a.nsplit + split) * a.R + rq;
-      f32x4* dst = reinterpret_cast<f32x4*>(a.part_o + prow * HD + grp * 32);
+      f32x4* dst = reinterpret_cast<f32x4*>(a.part_o + prow * HD + grp * DPL);
 #pragma unroll
-      for (int d = 0; d < 8; ++d) dst[d] = res[d];
+      for (int d = 0; d < DT; ++d) dst[d] = res[d];
       if (grp == 0) *reinterpret_cast<float2*>(a.part_ml + prow * 2) = float2{M, L};
     }
   }
 }
 
 // The verify kernel's splits merged: one thread per (row b, kv head, query row, 4 dims), every
-// split read (a split past the row length holds m = -inf and is skipped by value), the loads of
-// a batch of 24 splits issued together. Same merge as attention_combine_kernel: weights
-// exp(m_s - M) * l_s over the splits' normalised float32 partial outputs.
+// split from the first one the row's sliding window reaches (a split past the row length holds
+// m = -inf and is skipped by value), the loads of a batch of 24 splits issued together. Same
+// merge as attention_combine_kernel: weights exp(m_s - M) * l_s over the splits' normalised
+// float32 partial outputs.
 constexpr int kVerifyCombineThreads = 64;
+template <int HD>
 __global__ __launch_bounds__(kVerifyCombineThreads) void attention_verify_combine_kernel(AttnArgs a) {
-  constexpr int HD = 128, BATCH = 24;
+  constexpr int BATCH = 24, CH = HD / 4;
   const int64_t task = (int64_t)blockIdx.x * kVerifyCombineThreads + threadIdx.x;
-  if (task >= (int64_t)a.B * a.nkv * a.R * (HD / 4)) return;
-  const int ch = (int)(task & 31);
-  const int64_t rowt = task >> 5;
+  if (task >= (int64_t)a.B * a.nkv * a.R * CH) return;
+  const int ch = (int)(task % CH);
+  const int64_t rowt = task / CH;
   const int r = (int)(rowt % a.R);
   const int bk = (int)(rowt / a.R);
   const int b = bk / a.nkv, kvh = bk % a.nkv;
+  const int sl = a.seq_lens[b];
+  const int s_beg = a.causal && a.window > 0 ? max(0, sl + r / a.G + 1 - a.window) / a.kps -
+                                                   (a.wrel ? max(0, sl - a.window + 1) / a.kps : 0)
+                                             : 0;
   const size_t base = (size_t)bk * a.nsplit * a.R + r;  // partial row of split 0
   float M = -__builtin_inff(), L = 0.0f;
   f32x4 acc = f32x4{0, 0, 0, 0};
-  for (int s0 = 0; s0 < a.nsplit; s0 += BATCH) {
+  for (int s0 = s_beg; s0 < a.nsplit; s0 += BATCH) {
     float2 ml[BATCH];
     f32x4 ov[BATCH];
 #pragma unroll
@@ -1537,14 +1565,17 @@ static int attn_split_keys(int hd, int) {
   return hd == 128 ? Split<128>::KEYS : (hd == 256 ? Split<256>::KEYS : Split<512>::KEYS);
 }
 static int attn_nsplit(int hd, int max_ctx) { return (int)ceil_div(max_ctx, attn_split_keys(hd, max_ctx)); }
-// blocks per split of the streamed path: about 24 splits per (row, kv head), at most 8 blocks;
-// a many-query pass (more than 64 new tokens: a prefill) takes 8 blocks per split, its query
-// tiles giving the parallelism
+// blocks per split of the streamed path: about DSK_ATTN_SPLITS splits over the keys a row
+// reads (its sliding window, when it has one), at most 8 blocks; a many-query pass (more than
+// 64 new tokens: a prefill) takes 8 blocks per split, its query tiles giving the parallelism
+#ifndef DSK_ATTN_SPLITS
+#define DSK_ATTN_SPLITS 24
+#endif
 constexpr int kAttnVerifyMaxW = 64;
-static int attn_blocks(int hd, int max_ctx, int W = 1) {
+static int attn_blocks(int hd, int span, int W = 1) {
   if (W > kAttnVerifyMaxW) return 8;
-  const int64_t blocks = ceil_div(max_ctx, attn_split_keys(hd, max_ctx));
-  return (int)std::min<int64_t>(8, std::max<int64_t>(1, ceil_div(blocks, 24)));
+  const int64_t blocks = ceil_div(span, attn_split_keys(hd, span));
+  return (int)std::min<int64_t>(8, std::max<int64_t>(1, ceil_div(blocks, DSK_ATTN_SPLITS)));
 }
 
 // partial outputs first, then (m, l) at a 256-byte boundary
@@ -1591,7 +1622,10 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
     DSK_LAUNCH_CHECK(who);
     return DSK_OK;
   }
-  int nblk = (fused || QT != 1) ? 1 : attn_blocks(hd, max_ctx, a.W);
+  // a sliding-window pass reads at most window + W keys per row: its splits are sized for that
+  // span (the splits before a window exit at once), not for the whole cache
+  const int span = (a.causal && a.window > 0) ? std::min(max_ctx, a.window + a.W) : max_ctx;
+  int nblk = (fused || QT != 1) ? 1 : attn_blocks(hd, span, a.W);
   while (nblk > 1 && attn_split_keys(hd, max_ctx) * nblk / a.page + 1 > kAttnMaxSplitPages) --nblk;
   DSK_REQUIRE(attn_split_keys(hd, max_ctx) / a.page + 1 <= kAttnMaxSplitPages, "%s: page size %d too small", who,
               a.page);
@@ -1603,23 +1637,46 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
   a.part_ml = a.nsplit > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
                                                        attn_part_o_bytes(a.B, a.W, a.nq, hd, a.nsplit))
                            : nullptr;
-  if (hd == 128 && !fused && a.R <= kVerifyMaxR && a.page % kVerifyBlock == 0) {
-    // verify passes: 4 waves per split of 256 keys, 64 keys each, every query tile
-    a.kps = kVerifyKeys;
+  const int verify_keys = hd == 128 ? VerifyShape<128>::KEYS : VerifyShape<256>::KEYS;
+  const int verify_maxr = hd == 128 ? VerifyShape<128>::MAXR : VerifyShape<256>::MAXR;
+  if ((hd == 128 || hd == 256) && !fused && a.R <= verify_maxr && a.page % kVerifyBlock == 0) {
+    // verify passes: 4 waves per split (256 keys at head_dim 128, 128 at 256), every query tile
+    a.kps = verify_keys;
     a.nsplit = (int)ceil_div(max_ctx, a.kps);
+    // a sliding window spans at most (window + W - 2) / kps + 2 splits from the one holding the
+    // first row's window start: only those are launched
+    a.wrel = 0;
+    if (a.causal && a.window > 0) {
+      const int nw = (a.window + a.W - 2) / a.kps + 2;
+      if (nw < a.nsplit) {
+        a.nsplit = nw;
+        a.wrel = 1;
+      }
+    }
     const size_t need_v = attn_ws_need(a.B, a.W, a.nq, hd, a.nsplit);
     DSK_REQUIRE(a.nsplit == 1 || (workspace && ws_bytes >= need_v), "%s: workspace %zu < %zu", who, ws_bytes, need_v);
     a.part_o = reinterpret_cast<float*>(workspace);
     a.part_ml = a.nsplit > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
                                                         attn_part_o_bytes(a.B, a.W, a.nq, hd, a.nsplit))
                              : nullptr;
-    const dim3 vgrid((unsigned)(a.B * a.nkv * a.nsplit));
+    // two query-tile groups per split when the (b, kv head, split) workgroups leave most CUs
+    // free: each group dequantises the split's K/V again but runs half the softmax, P.V and
+    // merge, and twice the waves run at once
+    const int tasks = a.B * a.nkv * a.nsplit;
+    a.tgroups = ((tiles == 2 || tiles == 4) && tasks <= 128) ? 2 : 1;
+    const int qt = tiles / a.tgroups;
+    const dim3 vgrid((unsigned)(ceil_div(tasks, 8) * 8 * a.tgroups)), vblk(kVerifyWaves * 64);
 #define DSK_VERIFY_QT(kvt, scv)                                                                           \
-  switch (tiles) {                                                                                        \
-    case 1: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 1>), vgrid, dim3(kVerifyWaves * 64), 0, st, a); break; \
-    case 2: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 2>), vgrid, dim3(kVerifyWaves * 64), 0, st, a); break; \
-    case 3: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 3>), vgrid, dim3(kVerifyWaves * 64), 0, st, a); break; \
-    default: hipLaunchKernelGGL((attention_verify_kernel<kvt, scv, 4>), vgrid, dim3(kVerifyWaves * 64), 0, st, a); break; \
+  if (hd == 256) {                                                                                        \
+    if (qt == 1) hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 1>), vgrid, vblk, 0, st, a);  \
+    else hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 2>), vgrid, vblk, 0, st, a);          \
+  } else {                                                                                                \
+    switch (qt) {                                                                                         \
+      case 1: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 1>), vgrid, vblk, 0, st, a); break; \
+      case 2: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 2>), vgrid, vblk, 0, st, a); break; \
+      case 3: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 3>), vgrid, vblk, 0, st, a); break; \
+      default: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 4>), vgrid, vblk, 0, st, a); break; \
+    }                                                                                                     \
   }
     if (a.kv_dtype == DSK_KV_U8) {
       if (sc) { DSK_VERIFY_QT(DSK_KV_U8, true) } else { DSK_VERIFY_QT(DSK_KV_U8, false) }
@@ -1629,8 +1686,9 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
 #undef DSK_VERIFY_QT
     DSK_LAUNCH_CHECK(who);
     if (a.nsplit > 1) {
-      const dim3 cgrid((unsigned)ceil_div((int64_t)a.B * a.nkv * a.R * 32, kVerifyCombineThreads));
-      hipLaunchKernelGGL(attention_verify_combine_kernel, cgrid, dim3(kVerifyCombineThreads), 0, st, a);
+      const dim3 cgrid((unsigned)ceil_div((int64_t)a.B * a.nkv * a.R * (hd / 4), kVerifyCombineThreads));
+      if (hd == 256) hipLaunchKernelGGL(attention_verify_combine_kernel<256>, cgrid, dim3(kVerifyCombineThreads), 0, st, a);
+      else hipLaunchKernelGGL(attention_verify_combine_kernel<128>, cgrid, dim3(kVerifyCombineThreads), 0, st, a);
       DSK_LAUNCH_CHECK(who);
     }
     return DSK_OK;

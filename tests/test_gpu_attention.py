@@ -259,14 +259,15 @@ def _random_case(dev, kv_dtype, lens, W, max_ctx, nq=8, nkv=2, hd=128, page=64):
                 max_ctx=max_ctx, kv_dtype=kv_dtype, lens=lens)
 
 
-def _run_case(c, out=None):
+def _run_case(c, out=None, window=0):
     from mlx_dspark.ops import attention
     p = c["pool"]
     return attention(c["qd"], c["B"], c["W"], c["nq"], c["nkv"], c["hd"], c["hd"] ** -0.5, c["sl"], c["max_ctx"],
-                     p.block_table, c["page"], c["kv_dtype"], p.k, p.v, p.ksb, p.vsb, causal=True, out=out)
+                     p.block_table, c["page"], c["kv_dtype"], p.k, p.v, p.ksb, p.vsb, causal=True, window=window,
+                     out=out)
 
 
-def _check_case(c, out):
+def _check_case(c, out, window=0):
     B, W, nq, nkv, hd = c["B"], c["W"], c["nq"], c["nkv"], c["hd"]
     G = nq // nkv
     scale = hd ** -0.5
@@ -277,9 +278,12 @@ def _check_case(c, out):
         ref = torch.empty(W, nq, hd)
         j = torch.arange(L0 + W)[None, :]
         i = torch.arange(W)[:, None]
+        hidden = j > L0 + i
+        if window:
+            hidden = hidden | (j <= L0 + i - window)      # query at L0 + i sees keys > L0 + i - window
         for h in range(nq):
             s = (qb[:, h] @ K[:, h // G].T) * scale
-            s = s.masked_fill(j > L0 + i, float("-inf"))
+            s = s.masked_fill(hidden, float("-inf"))
             ref[:, h] = torch.softmax(s, -1) @ V[:, h // G]
         got = out.view(B, W, nq, hd)[b].float().cpu()
         err = (got - ref).abs().max().item()
@@ -320,3 +324,33 @@ def test_attention_interleaved_shapes_repeat(dev, kv_dtype):
                 first.append(out.clone())
             else:
                 assert torch.equal(out, first[k]), (rep, k)
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+@pytest.mark.parametrize("lens,W,max_ctx,window", [([8192], 9, 8208, 0), ([8192], 9, 8208, 1024),
+                                                   ([3000, 70], 16, 3100, 0), ([100, 1030], 9, 1200, 1024),
+                                                   ([0, 64], 4, 200, 0), ([500], 1, 640, 64), ([300], 9, 400, 0)])
+def test_attention_head_dim_256(dev, kv_dtype, lens, W, max_ctx, window):
+    """head_dim 256 verify passes (the Gemma-style shape: 16 query / 8 kv heads, 9 new tokens,
+    an 8192-key global layer and 1024-key sliding windows), ragged rows, rows shorter than a
+    window, single-token rows and a short context split into two query-tile groups; against a float32 softmax over the stored K/V with the
+    window's mask (a query at position p sees keys p - window + 1 .. p)."""
+    print(f"attn hd256 kv={kv_dtype} lens={lens} W={W} max_ctx={max_ctx} window={window}", flush=True)
+    c = _random_case(dev, kv_dtype, lens, W, max_ctx, nq=16, nkv=8, hd=256)
+    out = _run_case(c, window=window)
+    torch.cuda.synchronize()
+    _check_case(c, out, window=window)
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+@pytest.mark.parametrize("lens,W,max_ctx,window", [([3000, 200, 5000], 16, 5200, 1024), ([4100], 9, 4200, 300),
+                                                   ([700, 700], 4, 1024, 256)])
+def test_attention_sliding_window_head_dim_128(dev, kv_dtype, lens, W, max_ctx, window):
+    """head_dim 128 verify passes with a sliding window: only the splits of one window are
+    launched, each row's starting where its first row's window starts (ragged rows start at
+    different splits, windows that begin on and off a split boundary)."""
+    print(f"attn window hd128 kv={kv_dtype} lens={lens} W={W} max_ctx={max_ctx} window={window}", flush=True)
+    c = _random_case(dev, kv_dtype, lens, W, max_ctx)
+    out = _run_case(c, window=window)
+    torch.cuda.synchronize()
+    _check_case(c, out, window=window)
