@@ -175,11 +175,19 @@ def gemm_sweep(model, M: int, reps: int = 10) -> dict:
     from mlx_dspark._hip import ptr, stream_ptr
 
     dev = model.device
-    P, SW, R, ST = ops.DSK_EPI_PARTIAL, ops.DSK_EPI_SWIGLU, ops.DSK_EPI_RESIDUAL, ops.DSK_EPI_STORE
+    P, R, ST = ops.DSK_EPI_PARTIAL, ops.DSK_EPI_RESIDUAL, ops.DSK_EPI_STORE
+    SW = model.act_epi
     eps = model.args.rms_norm_eps
-    shapes = {"qkv": ([L.qkv for L in model.layers], P, False), "o": ([L.o for L in model.layers], R, False),
-              "gate_up": ([L.gate_up for L in model.layers], SW, True),
-              "down": ([L.down for L in model.layers], R, False), "lm_head": ([model.lm_head], ST, True)}
+    if model.args.sandwich_norms:
+        # sandwich norms (the Gemma-style layout): o and down leave split-K partials for the norm
+        # that follows them, every projection's x is normed in full
+        shapes = {"qkv": ([L.qkv for L in model.layers], P, False), "o": ([L.o for L in model.layers], P, False),
+                  "gate_up": ([L.gate_up for L in model.layers], SW, False),
+                  "down": ([L.down for L in model.layers], P, False), "lm_head": ([model.lm_head], ST, False)}
+    else:
+        shapes = {"qkv": ([L.qkv for L in model.layers], P, False), "o": ([L.o for L in model.layers], R, False),
+                  "gate_up": ([L.gate_up for L in model.layers], SW, True),
+                  "down": ([L.down for L in model.layers], R, False), "lm_head": ([model.lm_head], ST, True)}
     stream = torch.cuda.current_stream()
     out = {}
     for name, (ws, epi, rs) in shapes.items():
@@ -560,7 +568,12 @@ def main(argv=None) -> int:
         return 0
     t_build = time.time()
     keep = not args.no_cpu_baseline            # the oracle reads the MLX-layout codes
-    model = synthetic.build_target(args.target, seed=0, keep_mlx=keep)
+    model = synthetic.build_target(args.target, seed=0, keep_mlx=keep and not args.gemm_sweep)
+    if args.gemm_sweep:
+        log(f"built {args.target} W8 target ({model.weight_bytes / 1e9:.2f} GB) in {time.time() - t_build:.1f} s")
+        print(json.dumps({"gemm_sweep": {"target": args.target, "M": args.gemm_sweep,
+                                         "shapes": gemm_sweep(model, args.gemm_sweep)}}), flush=True)
+        return 0
     drafter, dcfg = synthetic.build_dflash(model.args, seed=1, block_size=args.block, n_taps=5, bits=4, keep_mlx=keep)
     drafter.bind(model)
     log(f"built {args.target} W8 target ({model.weight_bytes / 1e9:.2f} GB) + DFlash drafter in "
@@ -569,10 +582,6 @@ def main(argv=None) -> int:
         shapes = gemm_roofline(model, args.block)
         copy_calibration()
         print(json.dumps({"roofline_only": shapes}), flush=True)
-        return 0
-    if args.gemm_sweep:
-        print(json.dumps({"gemm_sweep": {"M": args.gemm_sweep, "shapes": gemm_sweep(model, args.gemm_sweep)}}),
-              flush=True)
         return 0
     tok = SyntheticTokenizer(model.args.vocab_size)
     target = Target(model, tok, kv_bits=kv_bits)
