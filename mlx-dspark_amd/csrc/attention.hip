@@ -858,6 +858,9 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
 // layout are the attention kernel's; attention_verify_combine_kernel merges the splits (a split
 // past a row's keys, or before every window of its rows, writes m = -inf, which the merge skips).
 constexpr int kVerifyBlock = 32;   // keys per page-aligned block (the page size is a multiple)
+#ifndef DSK_VERIFY_TG_MAX
+#define DSK_VERIFY_TG_MAX 128      // most (b, kv head, split) workgroups that get two query-tile groups
+#endif
 constexpr int kVerifyWaves = 4;
 template <int HD> struct VerifyShape {
   static constexpr int KB = HD == 128 ? 4 : 2;          // 16-key tiles per wave
@@ -909,14 +912,14 @@ typedef short s16x8 __attribute__((ext_vector_type(8)));
 // robin) and the second reads the split's K/V from that XCD's L2; ids past the grid's
 // (b, kv head, split) count exit at once.
 template <int HD, int KVT, bool SOFTCAP, int QT>
-__global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_eu(QT <= 2 && HD == 128 ? 2 : 1,
-                                                                                   QT <= 2 && HD == 128 ? 2 : 1)))
+__global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attention_verify_kernel(AttnArgs a) {
   constexpr int QROW = HD + 8, DPL = HD / 4, DT = HD / 16;    // LDS query row, dims per lane, d tiles
   constexpr int NW = kVerifyWaves, KB = VerifyShape<HD>::KB, KEYS = VerifyShape<HD>::KEYS;
   constexpr int NC = KVT == DSK_KV_BF16 ? DPL / 8 : DPL / 16;  // 16-byte loads per lane and key row
-  __shared__ f32x4 mo[QT][NW][DT][64];               // every tile's (o) per [tile][wave][d tile][lane]
-  __shared__ float2 mml[QT][NW][64];                 // and (m, l) per lane
+  constexpr int MC = 8;                              // d tiles per merge chunk
+  __shared__ f32x4 mo[NW][MC][64];                   // one chunk of a tile's (o) per [wave][d tile][lane]
+  __shared__ float2 mml[NW][64];                     // and the tile's (m, l) per lane
   __shared__ __attribute__((aligned(16))) uint16_t qs[QT * 16 * QROW];  // the group's query rows
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int grp = lane >> 4, row16 = lane & 15;
@@ -1027,48 +1030,34 @@ void attention_verify_kernel(AttnArgs a) {
   const bool masked = j0 + 16 * KB > j_end || (a.causal && (j0 + 16 * KB - 1 > off + r0 / a.G || a.window > 0));
   __syncthreads();  // the query rows
 
-  // ---- every query tile over the wave's keys, the tiles interleaved: scores, softmax, P.V; then
-  // (m, l, o) to the merge slots
-  float m[QT], l[QT];
-  f32x4 o[QT][DT];
+  // ---- one query tile at a time over the wave's keys: scores, softmax, P.V, then the four waves'
+  // (m, l, o) meet in LDS, a chunk of 8 d tiles at a time, and every wave merges two of its d tiles
+  // for all the tile's rows (only one tile's accumulators and one chunk of LDS are ever live)
 #pragma unroll
   for (int tile = 0; tile < QT; ++tile) {
-    m[tile] = -__builtin_inff();
-    l[tile] = 0.0f;
+    float m = -__builtin_inff(), l = 0.0f;
+    f32x4 o[DT];
 #pragma unroll
-    for (int d = 0; d < DT; ++d) o[tile][d] = f32x4{0, 0, 0, 0};
-  }
-  if (live) {
-    f32x4 st[QT][KB];
+    for (int d = 0; d < DT; ++d) o[d] = f32x4{0, 0, 0, 0};
+    if (live) {
+      f32x4 st[KB];
 #pragma unroll
-    for (int tile = 0; tile < QT; ++tile)
+      for (int t = 0; t < KB; ++t) st[t] = f32x4{0, 0, 0, 0};
 #pragma unroll
-      for (int t = 0; t < KB; ++t) st[tile][t] = f32x4{0, 0, 0, 0};
+      for (int s = 0; s < DPL / 8; ++s) {
+        const bf16x8 qf = *reinterpret_cast<const bf16x8*>(qs + (tile * 16 + row16) * QROW + grp * DPL + 8 * s);
 #pragma unroll
-    for (int s = 0; s < DPL / 8; ++s) {
-      bf16x8 qf[QT];
-#pragma unroll
-      for (int tile = 0; tile < QT; ++tile)
-        qf[tile] = *reinterpret_cast<const bf16x8*>(qs + (tile * 16 + row16) * QROW + grp * DPL + 8 * s);
-#pragma unroll
-      for (int t = 0; t < KB; ++t)
-#pragma unroll
-        for (int tile = 0; tile < QT; ++tile)
-          st[tile][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kel[t][s], qf[tile], st[tile][t], 0, 0, 0);
-    }
-    // ---- softmax (lane: query row16, keys j0 + 16 t + 4 grp + rr); rows past R are not masked
-    // (their columns of the MFMAs touch no other row, and are not stored)
-    if (SOFTCAP) {
-#pragma unroll
-      for (int tile = 0; tile < QT; ++tile)
+        for (int t = 0; t < KB; ++t) st[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kel[t][s], qf, st[t], 0, 0, 0);
+      }
+      // ---- softmax (lane: query row16, keys j0 + 16 t + 4 grp + rr); rows past R are not masked
+      // (their columns of the MFMAs touch no other row, and are not stored)
+      if (SOFTCAP) {
 #pragma unroll
         for (int t = 0; t < KB; ++t)
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) st[tile][t][rr] = tanhf(st[tile][t][rr] * a.scale / softcap) * softcap;
-    }
-    if (masked) {
-#pragma unroll
-      for (int tile = 0; tile < QT; ++tile) {
+          for (int rr = 0; rr < 4; ++rr) st[t][rr] = tanhf(st[t][rr] * a.scale / softcap) * softcap;
+      }
+      if (masked) {
         const int rq = r0 + tile * 16 + row16;
         const int qpos = off + (rq < a.R ? rq : 0) / a.G;
         int k_first = 0, k_last = j_end - 1;
@@ -1081,39 +1070,28 @@ void attention_verify_kernel(AttnArgs a) {
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) {
             const int j = j0 + 16 * t + 4 * grp + rr;
-            if (j < k_first || j > k_last) st[tile][t][rr] = -__builtin_inff();
+            if (j < k_first || j > k_last) st[t][rr] = -__builtin_inff();
           }
       }
-    }
-    float mx[QT];
+      float mx = -__builtin_inff();
 #pragma unroll
-    for (int tile = 0; tile < QT; ++tile) {
-      mx[tile] = -__builtin_inff();
-#pragma unroll
-      for (int t = 0; t < KB; ++t)
-        mx[tile] = fmaxf(mx[tile], fmaxf(fmaxf(st[tile][t][0], st[tile][t][1]), fmaxf(st[tile][t][2], st[tile][t][3])));
-    }
-#pragma unroll
-    for (int tile = 0; tile < QT; ++tile) mx[tile] = fmaxf(mx[tile], __shfl_xor(mx[tile], 16, 64));
-#pragma unroll
-    for (int tile = 0; tile < QT; ++tile) mx[tile] = fmaxf(mx[tile], __shfl_xor(mx[tile], 32, 64));
-    // per tile: float32 probabilities (in place of the scores) and their sums, then
-    // O^T += V^T . P^T over the wave's keys (32 per MFMA) with P as three bf16 terms; a tile's
-    // MFMAs run while the next tile's exponentials are computed. One term's MFMAs go over every
-    // d tile before the next term's (independent accumulators in between).
-#pragma unroll
-    for (int tile = 0; tile < QT; ++tile) {
-      // masked keys: exp2(-inf) = 0; a row with no visible key keeps m = -inf, l = 0
-      const float mb = mx[tile] == -__builtin_inff() ? 0.0f : mx[tile] * c2;
+      for (int t = 0; t < KB; ++t) mx = fmaxf(mx, fmaxf(fmaxf(st[t][0], st[t][1]), fmaxf(st[t][2], st[t][3])));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // float32 probabilities (in place of the scores) and their sums, then O^T += V^T . P^T over
+      // the wave's keys (32 per MFMA) with P as three bf16 terms; one term's MFMAs go over every d
+      // tile before the next term's. Masked keys: exp2(-inf) = 0; a row with no visible key keeps
+      // m = -inf, l = 0.
+      const float mb = mx == -__builtin_inff() ? 0.0f : mx * c2;
 #pragma unroll
       for (int t = 0; t < KB; ++t)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(st[tile][t][rr], c2, -mb));
-          st[tile][t][rr] = p;
-          l[tile] += p;
+          const float p = __builtin_amdgcn_exp2f(fmaf(st[t][rr], c2, -mb));
+          st[t][rr] = p;
+          l += p;
         }
-      m[tile] = mx[tile] * mscale;
+      m = mx * mscale;
 #pragma unroll
       for (int cp = 0; cp < KB / 2; ++cp) {
         uint32_t w[3][4];
@@ -1121,7 +1099,7 @@ void attention_verify_kernel(AttnArgs a) {
         for (int u = 0; u < 2; ++u)
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const f32x4& pv = st[tile][2 * cp + u];
+            const f32x4& pv = st[2 * cp + u];
             const Bf16x2Terms tt = split3_bf16x2(pv[2 * h], pv[2 * h + 1]);
             w[0][2 * u + h] = tt.hi;
             w[1][2 * u + h] = tt.mid;
@@ -1131,71 +1109,61 @@ void attention_verify_kernel(AttnArgs a) {
         for (int k = 0; k < 3; ++k) {
           const bf16x8 pk = __builtin_bit_cast(bf16x8, (u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}));
 #pragma unroll
-          for (int d = 0; d < DT; ++d)
-            o[tile][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[cp][d], pk, o[tile][d], 0, 0, 0);
+          for (int d = 0; d < DT; ++d) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[cp][d], pk, o[d], 0, 0, 0);
         }
       }
+      l += __shfl_xor(l, 16, 64);
+      l += __shfl_xor(l, 32, 64);
     }
-#pragma unroll
-    for (int tile = 0; tile < QT; ++tile) l[tile] += __shfl_xor(l[tile], 16, 64);
-#pragma unroll
-    for (int tile = 0; tile < QT; ++tile) l[tile] += __shfl_xor(l[tile], 32, 64);
-  }
-#pragma unroll
-  for (int tile = 0; tile < QT; ++tile) {
-#pragma unroll
-    for (int d = 0; d < DT; ++d) mo[tile][wv][d][lane] = o[tile][d];
-    mml[tile][wv][lane] = float2{m[tile], l[tile]};
-  }
-  __syncthreads();
-  // ---- merge of the waves: wave w takes tiles w, w + NW, ... (lane: DPL dims of its row)
-  for (int tile = wv; tile < ntiles; tile += NW) {
+    // ---- merge of the waves, chunk by chunk: wave w takes d tiles c0 + 2 w and c0 + 2 w + 1 of
+    // every row of the tile (lane: its row16 and its group's 8 dims DPL grp + 4 (c0 + 2 w) .. + 7)
     const int rq = r0 + tile * 16 + row16;
-    if (rq >= a.R) continue;
-    float2 ml[NW];
-    float M = -__builtin_inff();
+    const bool store = tile < ntiles && rq < a.R;
 #pragma unroll
-    for (int q = 0; q < NW; ++q) {
-      ml[q] = mml[tile][q][lane];
-      M = fmaxf(M, ml[q].x);
-    }
-    float L = 0.0f, wq[NW];
+    for (int c0 = 0; c0 < DT; c0 += MC) {
+      if (tile > 0 || c0 > 0) __syncthreads();   // the previous chunk's merge has read the slots
 #pragma unroll
-    for (int q = 0; q < NW; ++q) {
-      wq[q] = ml[q].x == -__builtin_inff() ? 0.0f : __expf(ml[q].x - M);
-      L += ml[q].y * wq[q];
-    }
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    f32x4 res[DT];  // dims DPL grp + 4 d .. + 3
+      for (int d = 0; d < MC; ++d) mo[wv][d][lane] = o[c0 + d];
+      if (c0 == 0) mml[wv][lane] = float2{m, l};
+      __syncthreads();
+      if (store) {
+        float2 ml[NW];
+        float M = -__builtin_inff();
 #pragma unroll
-    for (int d = 0; d < DT; ++d) {
-      f32x4 acc = f32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int q = 0; q < NW; ++q) acc += mo[tile][q][d][lane] * wq[q];
-      res[d] = acc * inv;
-    }
-    if (a.nsplit == 1) {
-      // dims DPL grp .. + DPL - 1 in runs of 16 (contiguous in both output layouts)
-#pragma unroll
-      for (int h = 0; h < DPL / 16; ++h) {
-        u32x4* dst = reinterpret_cast<u32x4*>(a.out + attn_out_index(a, HD, b, rq / a.G, kvh * a.G + rq % a.G,
-                                                                      grp * DPL + 16 * h));
-        uint32_t w[8];
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          w[2 * d] = pack_bf16x2(res[4 * h + d][0], res[4 * h + d][1]);
-          w[2 * d + 1] = pack_bf16x2(res[4 * h + d][2], res[4 * h + d][3]);
+        for (int q = 0; q < NW; ++q) {
+          ml[q] = mml[q][lane];
+          M = fmaxf(M, ml[q].x);
         }
-        dst[0] = u32x4{w[0], w[1], w[2], w[3]};
-        dst[1] = u32x4{w[4], w[5], w[6], w[7]};
-      }
-    } else {
-      // the split's partial o / l in float32 (DPL contiguous dims per lane) and its (m, l)
-      const size_t prow = ((size_t)bk * a.nsplit + split) * a.R + rq;
-      f32x4* dst = reinterpret_cast<f32x4*>(a.part_o + prow * HD + grp * DPL);
+        float L = 0.0f, wq[NW];
 #pragma unroll
-      for (int d = 0; d < DT; ++d) dst[d] = res[d];
-      if (grp == 0) *reinterpret_cast<float2*>(a.part_ml + prow * 2) = float2{M, L};
+        for (int q = 0; q < NW; ++q) {
+          wq[q] = ml[q].x == -__builtin_inff() ? 0.0f : __expf(ml[q].x - M);
+          L += ml[q].y * wq[q];
+        }
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        f32x4 res[2];
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd) {
+          f32x4 acc = f32x4{0, 0, 0, 0};
+#pragma unroll
+          for (int q = 0; q < NW; ++q) acc += mo[q][2 * wv + dd][lane] * wq[q];
+          res[dd] = acc * inv;
+        }
+        const int dim0 = grp * DPL + 4 * (c0 + 2 * wv);
+        if (a.nsplit == 1) {
+          // 8 contiguous dims (one run in both output layouts)
+          *reinterpret_cast<u32x4*>(a.out + attn_out_index(a, HD, b, rq / a.G, kvh * a.G + rq % a.G, dim0)) =
+              u32x4{pack_bf16x2(res[0][0], res[0][1]), pack_bf16x2(res[0][2], res[0][3]),
+                    pack_bf16x2(res[1][0], res[1][1]), pack_bf16x2(res[1][2], res[1][3])};
+        } else {
+          // the split's partial o / l in float32 and its (m, l)
+          const size_t prow = ((size_t)bk * a.nsplit + split) * a.R + rq;
+          f32x4* dst = reinterpret_cast<f32x4*>(a.part_o + prow * HD + dim0);
+          dst[0] = res[0];
+          dst[1] = res[1];
+          if (wv == 0 && grp == 0 && c0 == 0) *reinterpret_cast<float2*>(a.part_ml + prow * 2) = float2{M, L};
+        }
+      }
     }
   }
 }
@@ -1663,7 +1631,7 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
     // free: each group dequantises the split's K/V again but runs half the softmax, P.V and
     // merge, and twice the waves run at once
     const int tasks = a.B * a.nkv * a.nsplit;
-    a.tgroups = ((tiles == 2 || tiles == 4) && tasks <= 128) ? 2 : 1;
+    a.tgroups = ((tiles == 2 || tiles == 4) && tasks <= DSK_VERIFY_TG_MAX) ? 2 : 1;
     const int qt = tiles / a.tgroups;
     const dim3 vgrid((unsigned)(ceil_div(tasks, 8) * 8 * a.tgroups)), vblk(kVerifyWaves * 64);
 #define DSK_VERIFY_QT(kvt, scv)                                                                           \

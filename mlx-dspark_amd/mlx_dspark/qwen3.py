@@ -115,6 +115,7 @@ class Qwen3W8:
         self.inv_freq_local = (ops.rope_inv_freq(args.head_dim, args.rope_local_base_freq, self.device)
                                if args.rope_local_base_freq else self.inv_freq)
         self.act_epi = DSK_EPI_SWIGLU if args.hidden_act == "silu" else DSK_EPI_GEGLU
+        self._dense_w = None   # bf16 rows of every layer's weights, when keep_dense_weights holds them
 
     # ------------------------------------------------------------------ cache
     def make_cache(self, B: int = 1, max_ctx: int | None = None, kv_bits: int | None = None,
@@ -308,14 +309,29 @@ class Qwen3W8:
 
 
     # ------------------------------------------------------------------ dense prefill
+    def keep_dense_weights(self, keep: bool = True) -> int:
+        """Hold every layer's weights expanded to bf16 rows in HBM for the dense prefill (two
+        bytes per weight: 15.1 GB for the Qwen3-8B shape, against 8 GB of 8-bit codes), so a
+        prefill multiplies them directly instead of expanding each layer's four matrices first
+        (4 ms of a 4096-token prefill). The rows are the ones the per-layer expansion writes, bit
+        for bit. keep=False releases them. Returns the bytes held."""
+        if not keep:
+            self._dense_w = None
+            return 0
+        if self._dense_w is None:
+            self._dense_w = [{k: ops.w8_dequant(getattr(Lw, k)) for k in ("qkv", "o", "gate_up", "down")}
+                             for Lw in self.layers]
+        return sum(t.numel() * t.element_size() for d in self._dense_w for t in d.values())
+
     def prefill_dense(self, ids: torch.Tensor, cache: PagedKVCache, tap=None, *, on_chunk=None,
                       chunk: int = PREFILL_CHUNK):
         """Prefill of a long prompt, layer by layer over all L rows (the reference's chunked
         _prefill_tapped, generate.py:613-656, computes the same causal result): each layer's W8
-        weights are expanded to bf16 once (dsk_w8_dequant_rows) and multiplied by the library
-        GEMM (hipBLASLt through torch.matmul / addmm, whose beta = 1 form is the fused residual
-        add), between the engine's RMSNorm, q/k-norm + RoPE + KV append, many-query attention and
-        SwiGLU kernels. The norms here normalise first. Returns what prefill() returns."""
+        weights are expanded to bf16 once (dsk_w8_dequant_rows; or held expanded, see
+        keep_dense_weights) and multiplied by the library GEMM (hipBLASLt through torch.matmul /
+        addmm, whose beta = 1 form is the fused residual add), between the engine's RMSNorm,
+        q/k-norm + RoPE + KV append, many-query attention and SwiGLU kernels. The norms here
+        normalise first. Returns what prefill() returns."""
         a = self.args
         if a.sandwich_norms:
             raise ValueError("prefill_dense: the Qwen3 layout only")
@@ -328,26 +344,31 @@ class Qwen3W8:
         tap = list(tap or [])
         h = self.embed_rows(ids.reshape(-1))
         fused = torch.empty((L, len(tap) * H), dtype=torch.bfloat16, device=dev) if tap else None
-        nw = max(a.n_qkv * H, H * nq * hd, 2 * I * H, H * I)
-        wbuf = torch.empty(nw, dtype=torch.bfloat16, device=dev)
+        held = self._dense_w
+        wbuf = None
+        if held is None:
+            wbuf = torch.empty(max(a.n_qkv * H, H * nq * hd, 2 * I * H, H * I), dtype=torch.bfloat16, device=dev)
+
+        def rows(l, name):
+            return held[l][name] if held is not None else ops.w8_dequant(getattr(self.layers[l], name), out=wbuf)
         x = torch.empty((L, H), dtype=torch.bfloat16, device=dev)
         qkv = torch.empty((L, a.n_qkv), dtype=torch.bfloat16, device=dev)
         gu = torch.empty((L, 2 * I), dtype=torch.bfloat16, device=dev)
         act = torch.empty((L, I), dtype=torch.bfloat16, device=dev)
         for l, Lw in enumerate(self.layers):
             ops.rows_rmsnorm(h, Lw.in_norm, eps, out=x)
-            torch.matmul(x, ops.w8_dequant(Lw.qkv, out=wbuf).t(), out=qkv)
+            torch.matmul(x, rows(l, "qkv").t(), out=qkv)
             k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
             inv_freq = self.inv_freq_local if a.is_sliding(l) else self.inv_freq
             q = ops.qkv_rope_append(qkv, 1, L, nq, nkv, hd, Lw.q_norm, Lw.k_norm, eps, inv_freq, cache.seq_lens,
                                     cache.block_table, cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb)
             o = ops.attention(q, 1, L, nq, nkv, hd, a.attn_scale, cache.seq_lens, cache.max_ctx, cache.block_table,
                               cache.page, cache.kv_dtype, k_pool, v_pool, k_sb, v_sb, causal=True, window=a.window(l))
-            h.addmm_(o, ops.w8_dequant(Lw.o, out=wbuf).t())
+            h.addmm_(o, rows(l, "o").t())
             ops.rows_rmsnorm(h, Lw.post_norm, eps, out=x)
-            torch.matmul(x, ops.w8_dequant(Lw.gate_up, out=wbuf).t(), out=gu)
+            torch.matmul(x, rows(l, "gate_up").t(), out=gu)
             ops.rows_gated(gu, self.act_epi, out=act)
-            h.addmm_(act, ops.w8_dequant(Lw.down, out=wbuf).t())
+            h.addmm_(act, rows(l, "down").t())
             for i, t in enumerate(tap):
                 if t == l:
                     fused[:, i * H:(i + 1) * H].copy_(h)

@@ -261,3 +261,24 @@ def test_dense_prefill_matches_oracle(dev):
     torch.cuda.synchronize()
     (cl, _), (ecl, _) = Twin(lambda: OM.OracleTarget(model)).forward(prompt)
     check_logits(l2[0, -1].float().cpu(), cl[-1], "chunked prefill, last position", exact=ecl[-1])
+
+
+def test_dense_prefill_with_held_weights_is_bit_identical(dev):
+    """keep_dense_weights: the prefill over the held bf16 rows writes the same cache, taps and
+    logits, bit for bit, as the prefill that expands each layer's weights as it goes."""
+    from mlx_dspark import synthetic
+    print("dense prefill: held bf16 weight rows against per-layer expansion, tiny model, 600 tokens", flush=True)
+    model = synthetic.build_target("tiny", seed=31)
+    prompt = np.random.default_rng(5).integers(0, model.args.vocab_size, 600).tolist()
+    outs = []
+    for keep in (False, True):
+        held = model.keep_dense_weights(keep)
+        assert (held > 0) == keep
+        cache = model.make_cache(max_ctx=700)
+        logits, fused = model.prefill(prompt, cache, [0, 2])
+        torch.cuda.synchronize()
+        outs.append((logits.clone(), fused.clone(), [k.clone() for k in cache.k], [v.clone() for v in cache.v]))
+    model.keep_dense_weights(False)
+    (la, fa, ka, va), (lb, fb, kb, vb) = outs
+    assert torch.equal(la, lb) and torch.equal(fa, fb)
+    assert all(torch.equal(x, y) for x, y in zip(ka, kb)) and all(torch.equal(x, y) for x, y in zip(va, vb))
