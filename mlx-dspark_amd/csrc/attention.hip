@@ -836,14 +836,15 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
 }
 
 // ----------------------------------------------------------------------------- verify passes
-// A verify pass (at most 64 query rows per kv head at head_dim 128, 32 at 256; keys already in
+// A verify pass (at most 80 query rows per kv head at head_dim 128, 64 at 256; keys already in
 // the pool): one workgroup of 4 waves per (row b, kv head, split of 4 x 16 KB keys), KB 16-key
 // tiles per wave (4 at head_dim 128: 256-key splits; 2 at 256: 128-key splits). Wave w owns the
 // split's keys [16 KB w, 16 KB (w + 1)): it loads their K/V rows straight from the pool into
 // registers, dequantises each element once (K row-major for the score MFMA, V transposed for
-// the P.V MFMA), then runs every query tile of its group (staged once in LDS) over its keys, the
-// tiles interleaved. The four waves' (o, m, l) meet in LDS and wave w merges query tile w into
-// the split's partial (or the output when there is one split).
+// the P.V MFMA), then runs the query tiles of its group (staged once in LDS) one at a time over
+// its keys. After each tile the four waves' (o, m, l) meet in LDS, 8 d tiles at a time (32 KB),
+// and each wave merges two d tiles of every row into the split's partial (or the output when
+// there is one split). At most 256 registers and ~54 KB of LDS: two workgroups share a CU.
 //  - head_dim order: lane group a = lane / 16 holds dims [DPL a, DPL a + DPL) of its key row,
 //    DPL = HD / 4 (one contiguous load, inside one 64-dim quantization group), so k-step s of
 //    the score MFMA takes dims DPL a + 8 s .. + 7 from both K (A operand: lane = key) and Q
@@ -865,7 +866,7 @@ constexpr int kVerifyWaves = 4;
 template <int HD> struct VerifyShape {
   static constexpr int KB = HD == 128 ? 4 : 2;          // 16-key tiles per wave
   static constexpr int KEYS = kVerifyWaves * 16 * KB;   // keys per split
-  static constexpr int MAXR = HD == 128 ? 64 : 32;      // query rows per kv head (LDS of the merge)
+  static constexpr int MAXR = HD == 128 ? 80 : 64;      // query rows per kv head (5 or 4 tiles)
 };
 
 template <int HD, int KVT>
@@ -1636,14 +1637,19 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
     const dim3 vgrid((unsigned)(ceil_div(tasks, 8) * 8 * a.tgroups)), vblk(kVerifyWaves * 64);
 #define DSK_VERIFY_QT(kvt, scv)                                                                           \
   if (hd == 256) {                                                                                        \
-    if (qt == 1) hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 1>), vgrid, vblk, 0, st, a);  \
-    else hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 2>), vgrid, vblk, 0, st, a);          \
+    switch (qt) {                                                                                         \
+      case 1: hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 1>), vgrid, vblk, 0, st, a); break; \
+      case 2: hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 2>), vgrid, vblk, 0, st, a); break; \
+      case 3: hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 3>), vgrid, vblk, 0, st, a); break; \
+      default: hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 4>), vgrid, vblk, 0, st, a); break; \
+    }                                                                                                     \
   } else {                                                                                                \
     switch (qt) {                                                                                         \
       case 1: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 1>), vgrid, vblk, 0, st, a); break; \
       case 2: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 2>), vgrid, vblk, 0, st, a); break; \
       case 3: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 3>), vgrid, vblk, 0, st, a); break; \
-      default: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 4>), vgrid, vblk, 0, st, a); break; \
+      case 4: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 4>), vgrid, vblk, 0, st, a); break; \
+      default: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 5>), vgrid, vblk, 0, st, a); break; \
     }                                                                                                     \
   }
     if (a.kv_dtype == DSK_KV_U8) {

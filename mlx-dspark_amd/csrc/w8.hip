@@ -760,6 +760,9 @@ static const TunedPlan kTunedPlans[] = {
     {1, 30720, 3840, 1, 4, 2, 8, 1, false},
     {1, 3840, 15360, 2, 2, 2, 8, 2, false},
     {1, 262144, 3840, 0, 4, 2, 8, 1, false},
+    // Qwen3-8B, 17-row verify (16 drafts and the bonus row): qkv 9.52 (10.13), gate_up 30.4 (33.3)
+    {2, 6144, 4096, 2, 2, 2, 8, 4, false},
+    {2, 24576, 4096, 1, 2, 2, 8, 1, false},
     // Qwen3-8B, 36-row batch: qkv 11.85 (12.46)
     {3, 6144, 4096, 2, 2, 2, 4, 4, false},
 };

@@ -293,7 +293,8 @@ def _check_case(c, out, window=0):
 @pytest.mark.parametrize("kv_dtype", [0, 1])
 @pytest.mark.parametrize("lens,W,max_ctx", [([4096], 16, 5184), ([3000, 5000], 9, 5200), ([100], 16, 8000),
                                             ([6000, 1000], 16, 12288), ([0, 64, 127], 4, 3500),
-                                            ([0, 130], 16, 300), ([8100], 4, 8192)])
+                                            ([0, 130], 16, 300), ([8100], 4, 8192), ([4096], 17, 4200),
+                                            ([300, 2000], 20, 2100)])
 def test_attention_streamed_splits(dev, kv_dtype, lens, W, max_ctx):
     """Long contexts: each split streams several key blocks (the split size grows with max_ctx),
     with ragged rows, splits past a row's length, a causal edge inside a block and rows whose
@@ -329,7 +330,8 @@ def test_attention_interleaved_shapes_repeat(dev, kv_dtype):
 @pytest.mark.parametrize("kv_dtype", [0, 1])
 @pytest.mark.parametrize("lens,W,max_ctx,window", [([8192], 9, 8208, 0), ([8192], 9, 8208, 1024),
                                                    ([3000, 70], 16, 3100, 0), ([100, 1030], 9, 1200, 1024),
-                                                   ([0, 64], 4, 200, 0), ([500], 1, 640, 64), ([300], 9, 400, 0)])
+                                                   ([0, 64], 4, 200, 0), ([500], 1, 640, 64), ([300], 9, 400, 0),
+                                                   ([5000], 17, 5100, 0), ([2000, 40], 32, 2100, 1024)])
 def test_attention_head_dim_256(dev, kv_dtype, lens, W, max_ctx, window):
     """head_dim 256 verify passes (the Gemma-style shape: 16 query / 8 kv heads, 9 new tokens,
     an 8192-key global layer and 1024-key sliding windows), ragged rows, rows shorter than a
