@@ -55,18 +55,20 @@ sys.path.insert(0, str(REPO / "mlx-dspark_amd"))
 sys.path.insert(0, str(REPO))
 
 PEAK_HBM_GBS = 8000.0
-# HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter runs of `bench.py --roofline-only`
-# (profiles/w8_gemm_*_counters.md), per kernel instantiation: the counters' KiB per dispatch
-# scaled by what they read for a 256 MiB copy
+# HBM bytes per launch from the FETCH_SIZE / WRITE_SIZE counter runs of `bench.py --verify-eager 2`
+# (profiles/verify_kernels_*_counters.md), per kernel instantiation: the counters' KiB per dispatch
+# scaled by what they read for a 256 MiB copy (`bench.py --roofline-only` runs one)
 TRAFFIC = {
-    # gate_up 24576x4096: fetches 52855.70 KiB x 2.000 + writes 384 KiB x 1.000
-    "w8_gemm_kernel<1, 2, 2, 8, 5, true, 8>": 108641693,
-    # o 4096x4096 and down 4096x12288 (one instantiation, mean over both): 18725.63 KiB x 2.000 + 384 KiB
-    "w8_gemm_kernel<1, 1, 4, 16, 3, false, 8>": 38743306,
-    # qkv 6144x4096, split-K partials: 13606.78 KiB x 2.000 + 384 KiB
-    "w8_gemm_kernel<1, 2, 2, 16, 2, true, 8>": 28259905,
-    # lm_head 151936x4096, f32 logits: 323496.43 KiB x 2.000 + 9496.25 KiB
-    "w8_gemm_kernel<1, 4, 2, 8, 4, false, 8>": 672244854,
+    # qkv 6144x4096, split-K partials: 13342.68 KiB x 2.000 + 768 KiB
+    "w8_gemm_kernel<1, 3, 2, 16, 2, false, 8>": 28112249,
+    # o 4096x4096, residual epilogue: 9509.66 KiB x 2.000 + 384 KiB
+    "w8_gemm_kernel<1, 1, 4, 16, 3, false, 8>": 19869003,
+    # gate_up 24576x4096, SwiGLU: 52856.84 KiB x 2.000 + 384 KiB
+    "w8_gemm_kernel<1, 2, 2, 8, 5, true, 8>": 108644025,
+    # down 4096x12288, residual epilogue: 27939.95 KiB x 2.000 + 401.78 KiB
+    "w8_gemm_kernel<1, 1, 2, 8, 3, false, 8>": 57632436,
+    # lm_head 151936x4096, f32 logits: 323501.28 KiB x 2.000 + 9496.38 KiB
+    "w8_gemm_kernel<1, 4, 2, 8, 4, false, 8>": 672254912,
 }
 
 
@@ -574,6 +576,31 @@ def main(argv=None) -> int:
         print(json.dumps({"gemm_sweep": {"target": args.target, "M": args.gemm_sweep,
                                          "shapes": gemm_sweep(model, args.gemm_sweep)}}), flush=True)
         return 0
+    if args.verify_eager:
+        # seeded random context written straight into the KV pools (no prefill), then eager
+        # verify forwards of --block rows: every op is its own launch (for counter collection,
+        # any --target; the hidden-state taps a 5-tap drafter would read)
+        from mlx_dspark.synthetic import evenly_spaced_layers
+        W = args.block
+        target = Target(model, SyntheticTokenizer(model.args.vocab_size), kv_bits=kv_bits)
+        cache = target.make_cache(max_ctx=args.ctx + W + 64)
+        tap = list(evenly_spaced_layers(model.args.num_hidden_layers, 5))
+        g = torch.Generator(device=model.device).manual_seed(4)
+        for l in range(model.args.num_hidden_layers):
+            for pool, sb in ((cache.k[l], cache.k_sb[l]), (cache.v[l], cache.v_sb[l])):
+                if sb is None:
+                    pool.copy_(torch.randn(pool.shape, generator=g, device=model.device).to(pool.dtype))
+                else:
+                    pool.copy_(torch.randint(0, 256, pool.shape, generator=g, device=model.device).to(pool.dtype))
+                    sb.fill_(0x3C23 | (0xBF80 << 16) - (1 << 32))     # scale bf16(0.01), bias bf16(-1)
+        cache.set_lengths([args.ctx])
+        vids = torch.randint(0, model.args.vocab_size, (1, W), dtype=torch.int32, device=model.device)
+        for _ in range(args.verify_eager):
+            model.forward(vids, cache, tap, advance=False)
+        torch.cuda.synchronize()
+        print(json.dumps({"verify_eager": args.verify_eager, "target": args.target, "rows": W,
+                          "context": cache.lengths[0]}), flush=True)
+        return 0
     drafter, dcfg = synthetic.build_dflash(model.args, seed=1, block_size=args.block, n_taps=5, bits=4, keep_mlx=keep)
     drafter.bind(model)
     log(f"built {args.target} W8 target ({model.weight_bytes / 1e9:.2f} GB) + DFlash drafter in "
@@ -594,24 +621,6 @@ def main(argv=None) -> int:
     prompt = np.random.default_rng(1234).integers(0, model.args.vocab_size, args.ctx).tolist()
     t0 = time.time()
     tap = list(dcfg.target_layer_ids)
-    if args.verify_eager:
-        # seeded random context written straight into the KV pools (no prefill), then eager
-        # verify forwards: every op is its own launch
-        g = torch.Generator(device=model.device).manual_seed(4)
-        for l in range(model.args.num_hidden_layers):
-            for pool, sb in ((cache.k[l], cache.k_sb[l]), (cache.v[l], cache.v_sb[l])):
-                if sb is None:
-                    pool.copy_(torch.randn(pool.shape, generator=g, device=model.device).to(pool.dtype))
-                else:
-                    pool.copy_(torch.randint(0, 256, pool.shape, generator=g, device=model.device).to(pool.dtype))
-                    sb.fill_(0x3C23 | (0xBF80 << 16) - (1 << 32))     # scale bf16(0.01), bias bf16(-1)
-        cache.set_lengths([args.ctx])
-        vids = torch.randint(0, model.args.vocab_size, (1, W), dtype=torch.int32, device=model.device)
-        for _ in range(args.verify_eager):
-            model.forward(vids, cache, tap, advance=False)
-        torch.cuda.synchronize()
-        print(json.dumps({"verify_eager": args.verify_eager, "rows": W, "context": cache.lengths[0]}), flush=True)
-        return 0
     # the prompt's dense prefill (layer by layer over all rows), timed after a short warm-up
     # prefill that settles the library GEMM's plans; the weights' bf16 rows are held in HBM
     # (expanded once here, as a server does at load), so the prefill multiplies them directly

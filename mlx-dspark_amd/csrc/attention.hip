@@ -918,9 +918,12 @@ void attention_verify_kernel(AttnArgs a) {
   constexpr int QROW = HD + 8, DPL = HD / 4, DT = HD / 16;    // LDS query row, dims per lane, d tiles
   constexpr int NW = kVerifyWaves, KB = VerifyShape<HD>::KB, KEYS = VerifyShape<HD>::KEYS;
   constexpr int NC = KVT == DSK_KV_BF16 ? DPL / 8 : DPL / 16;  // 16-byte loads per lane and key row
-  constexpr int MC = 8;                              // d tiles per merge chunk
-  __shared__ f32x4 mo[NW][MC][64];                   // one chunk of a tile's (o) per [wave][d tile][lane]
-  __shared__ float2 mml[NW][64];                     // and the tile's (m, l) per lane
+  // TP query tiles per pass (interleaved: their MFMAs and exponentials overlap; pairs at head_dim
+  // 128, single tiles at 256 where a pair's accumulators exceed the registers), merged through
+  // LDS in chunks of MC d tiles: TP * MC = 8 d tiles of 4 waves' partials, 32 KB
+  constexpr int TP = HD == 128 && QT >= 2 && QT != 5 ? 2 : 1, MC = 8 / TP;  // (five tiles in pairs spill)
+  __shared__ f32x4 mo[NW][TP][MC][64];               // one chunk of a pass's (o) per [wave][tile][d tile][lane]
+  __shared__ float2 mml[NW][TP][64];                 // and the pass's (m, l) per lane
   __shared__ __attribute__((aligned(16))) uint16_t qs[QT * 16 * QROW];  // the group's query rows
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int grp = lane >> 4, row16 = lane & 15;
@@ -1031,108 +1034,138 @@ void attention_verify_kernel(AttnArgs a) {
   const bool masked = j0 + 16 * KB > j_end || (a.causal && (j0 + 16 * KB - 1 > off + r0 / a.G || a.window > 0));
   __syncthreads();  // the query rows
 
-  // ---- one query tile at a time over the wave's keys: scores, softmax, P.V, then the four waves'
-  // (m, l, o) meet in LDS, a chunk of 8 d tiles at a time, and every wave merges two of its d tiles
-  // for all the tile's rows (only one tile's accumulators and one chunk of LDS are ever live)
+  // ---- passes of TP query tiles over the wave's keys: scores, softmax, P.V, then the four waves'
+  // (m, l, o) meet in LDS, MC d tiles of each tile at a time, and every wave merges two d tiles
+  // (of one tile) for all that tile's rows. Only one pass's accumulators and one chunk of LDS are
+  // ever live.
 #pragma unroll
-  for (int tile = 0; tile < QT; ++tile) {
-    float m = -__builtin_inff(), l = 0.0f;
-    f32x4 o[DT];
+  for (int p0 = 0; p0 < QT; p0 += TP) {
+    float m[TP], l[TP];
+    f32x4 o[TP][DT];
 #pragma unroll
-    for (int d = 0; d < DT; ++d) o[d] = f32x4{0, 0, 0, 0};
+    for (int u = 0; u < TP; ++u) {
+      m[u] = -__builtin_inff();
+      l[u] = 0.0f;
+#pragma unroll
+      for (int d = 0; d < DT; ++d) o[u][d] = f32x4{0, 0, 0, 0};
+    }
     if (live) {
-      f32x4 st[KB];
+      f32x4 st[TP][KB];
 #pragma unroll
-      for (int t = 0; t < KB; ++t) st[t] = f32x4{0, 0, 0, 0};
+      for (int u = 0; u < TP; ++u)
+#pragma unroll
+        for (int t = 0; t < KB; ++t) st[u][t] = f32x4{0, 0, 0, 0};
 #pragma unroll
       for (int s = 0; s < DPL / 8; ++s) {
-        const bf16x8 qf = *reinterpret_cast<const bf16x8*>(qs + (tile * 16 + row16) * QROW + grp * DPL + 8 * s);
 #pragma unroll
-        for (int t = 0; t < KB; ++t) st[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kel[t][s], qf, st[t], 0, 0, 0);
+        for (int u = 0; u < TP; ++u) {
+          if (p0 + u >= QT) break;
+          const bf16x8 qf =
+              *reinterpret_cast<const bf16x8*>(qs + ((p0 + u) * 16 + row16) * QROW + grp * DPL + 8 * s);
+#pragma unroll
+          for (int t = 0; t < KB; ++t)
+            st[u][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kel[t][s], qf, st[u][t], 0, 0, 0);
+        }
       }
-      // ---- softmax (lane: query row16, keys j0 + 16 t + 4 grp + rr); rows past R are not masked
-      // (their columns of the MFMAs touch no other row, and are not stored)
-      if (SOFTCAP) {
+      // ---- softmax (lane: query row16, keys j0 + 16 t + 4 grp + rr); rows past R are not
+      // masked (their columns of the MFMAs touch no other row, and are not stored)
+      float mx[TP];
+#pragma unroll
+      for (int u = 0; u < TP; ++u) {
+        mx[u] = -__builtin_inff();
+        if (p0 + u >= QT) break;
+        if (SOFTCAP) {
+#pragma unroll
+          for (int t = 0; t < KB; ++t)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) st[u][t][rr] = tanhf(st[u][t][rr] * a.scale / softcap) * softcap;
+        }
+        if (masked) {
+          const int rq = r0 + (p0 + u) * 16 + row16;
+          const int qpos = off + (rq < a.R ? rq : 0) / a.G;
+          int k_first = 0, k_last = j_end - 1;
+          if (a.causal) {
+            k_last = min(k_last, qpos);
+            if (a.window > 0) k_first = qpos - a.window + 1;
+          }
+#pragma unroll
+          for (int t = 0; t < KB; ++t)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+              const int j = j0 + 16 * t + 4 * grp + rr;
+              if (j < k_first || j > k_last) st[u][t][rr] = -__builtin_inff();
+            }
+        }
 #pragma unroll
         for (int t = 0; t < KB; ++t)
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) st[t][rr] = tanhf(st[t][rr] * a.scale / softcap) * softcap;
+          mx[u] = fmaxf(mx[u], fmaxf(fmaxf(st[u][t][0], st[u][t][1]), fmaxf(st[u][t][2], st[u][t][3])));
+        mx[u] = fmaxf(mx[u], __shfl_xor(mx[u], 16, 64));
+        mx[u] = fmaxf(mx[u], __shfl_xor(mx[u], 32, 64));
       }
-      if (masked) {
-        const int rq = r0 + tile * 16 + row16;
-        const int qpos = off + (rq < a.R ? rq : 0) / a.G;
-        int k_first = 0, k_last = j_end - 1;
-        if (a.causal) {
-          k_last = min(k_last, qpos);
-          if (a.window > 0) k_first = qpos - a.window + 1;
-        }
+      // per tile: float32 probabilities (in place of the scores) and their sums, then O^T +=
+      // V^T . P^T over the wave's keys (32 per MFMA) with P as three bf16 terms; a tile's MFMAs
+      // run while the next tile's exponentials are computed. Masked keys: exp2(-inf) = 0; a row
+      // with no visible key keeps m = -inf, l = 0.
+#pragma unroll
+      for (int u = 0; u < TP; ++u) {
+        if (p0 + u >= QT) break;
+        const float mb = mx[u] == -__builtin_inff() ? 0.0f : mx[u] * c2;
 #pragma unroll
         for (int t = 0; t < KB; ++t)
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) {
-            const int j = j0 + 16 * t + 4 * grp + rr;
-            if (j < k_first || j > k_last) st[t][rr] = -__builtin_inff();
+            const float pr = __builtin_amdgcn_exp2f(fmaf(st[u][t][rr], c2, -mb));
+            st[u][t][rr] = pr;
+            l[u] += pr;
           }
-      }
-      float mx = -__builtin_inff();
+        m[u] = mx[u] * mscale;
 #pragma unroll
-      for (int t = 0; t < KB; ++t) mx = fmaxf(mx, fmaxf(fmaxf(st[t][0], st[t][1]), fmaxf(st[t][2], st[t][3])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      // float32 probabilities (in place of the scores) and their sums, then O^T += V^T . P^T over
-      // the wave's keys (32 per MFMA) with P as three bf16 terms; one term's MFMAs go over every d
-      // tile before the next term's. Masked keys: exp2(-inf) = 0; a row with no visible key keeps
-      // m = -inf, l = 0.
-      const float mb = mx == -__builtin_inff() ? 0.0f : mx * c2;
+        for (int cp = 0; cp < KB / 2; ++cp) {
+          uint32_t w[3][4];
 #pragma unroll
-      for (int t = 0; t < KB; ++t)
+          for (int v = 0; v < 2; ++v)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(st[t][rr], c2, -mb));
-          st[t][rr] = p;
-          l += p;
-        }
-      m = mx * mscale;
+            for (int h = 0; h < 2; ++h) {
+              const f32x4& pv = st[u][2 * cp + v];
+              const Bf16x2Terms tt = split3_bf16x2(pv[2 * h], pv[2 * h + 1]);
+              w[0][2 * v + h] = tt.hi;
+              w[1][2 * v + h] = tt.mid;
+              w[2][2 * v + h] = tt.lo;
+            }
 #pragma unroll
-      for (int cp = 0; cp < KB / 2; ++cp) {
-        uint32_t w[3][4];
+          for (int k = 0; k < 3; ++k) {
+            const bf16x8 pk = __builtin_bit_cast(bf16x8, (u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}));
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const f32x4& pv = st[2 * cp + u];
-            const Bf16x2Terms tt = split3_bf16x2(pv[2 * h], pv[2 * h + 1]);
-            w[0][2 * u + h] = tt.hi;
-            w[1][2 * u + h] = tt.mid;
-            w[2][2 * u + h] = tt.lo;
+            for (int d = 0; d < DT; ++d)
+              o[u][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[cp][d], pk, o[u][d], 0, 0, 0);
           }
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-          const bf16x8 pk = __builtin_bit_cast(bf16x8, (u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}));
-#pragma unroll
-          for (int d = 0; d < DT; ++d) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt[cp][d], pk, o[d], 0, 0, 0);
         }
+        l[u] += __shfl_xor(l[u], 16, 64);
+        l[u] += __shfl_xor(l[u], 32, 64);
       }
-      l += __shfl_xor(l, 16, 64);
-      l += __shfl_xor(l, 32, 64);
     }
-    // ---- merge of the waves, chunk by chunk: wave w takes d tiles c0 + 2 w and c0 + 2 w + 1 of
-    // every row of the tile (lane: its row16 and its group's 8 dims DPL grp + 4 (c0 + 2 w) .. + 7)
-    const int rq = r0 + tile * 16 + row16;
-    const bool store = tile < ntiles && rq < a.R;
+    // ---- merge of the waves, chunk by chunk: wave w takes tile p0 + (2 w) / MC, d tiles
+    // c0 + (2 w) % MC and the one after, of every row of that tile (lane: its row16 and its
+    // group's 8 dims DPL grp + 4 (c0 + (2 w) % MC) .. + 7)
+    const int mu = (2 * wv) / MC, md = (2 * wv) % MC;
+    const int rq = r0 + (p0 + mu) * 16 + row16;
+    const bool store = p0 + mu < QT && p0 + mu < ntiles && rq < a.R;
 #pragma unroll
     for (int c0 = 0; c0 < DT; c0 += MC) {
-      if (tile > 0 || c0 > 0) __syncthreads();   // the previous chunk's merge has read the slots
+      if (p0 > 0 || c0 > 0) __syncthreads();   // the previous chunk's merge has read the slots
 #pragma unroll
-      for (int d = 0; d < MC; ++d) mo[wv][d][lane] = o[c0 + d];
-      if (c0 == 0) mml[wv][lane] = float2{m, l};
+      for (int u = 0; u < TP; ++u) {
+#pragma unroll
+        for (int d = 0; d < MC; ++d) mo[wv][u][d][lane] = o[u][c0 + d];
+        if (c0 == 0) mml[wv][u][lane] = float2{m[u], l[u]};
+      }
       __syncthreads();
       if (store) {
         float2 ml[NW];
         float M = -__builtin_inff();
 #pragma unroll
         for (int q = 0; q < NW; ++q) {
-          ml[q] = mml[q][lane];
+          ml[q] = mml[q][mu][lane];
           M = fmaxf(M, ml[q].x);
         }
         float L = 0.0f, wq[NW];
@@ -1147,10 +1180,10 @@ void attention_verify_kernel(AttnArgs a) {
         for (int dd = 0; dd < 2; ++dd) {
           f32x4 acc = f32x4{0, 0, 0, 0};
 #pragma unroll
-          for (int q = 0; q < NW; ++q) acc += mo[q][2 * wv + dd][lane] * wq[q];
+          for (int q = 0; q < NW; ++q) acc += mo[q][mu][md + dd][lane] * wq[q];
           res[dd] = acc * inv;
         }
-        const int dim0 = grp * DPL + 4 * (c0 + 2 * wv);
+        const int dim0 = grp * DPL + 4 * (c0 + md);
         if (a.nsplit == 1) {
           // 8 contiguous dims (one run in both output layouts)
           *reinterpret_cast<u32x4*>(a.out + attn_out_index(a, HD, b, rq / a.G, kvh * a.G + rq % a.G, dim0)) =
@@ -1162,7 +1195,7 @@ void attention_verify_kernel(AttnArgs a) {
           f32x4* dst = reinterpret_cast<f32x4*>(a.part_o + prow * HD + dim0);
           dst[0] = res[0];
           dst[1] = res[1];
-          if (wv == 0 && grp == 0 && c0 == 0) *reinterpret_cast<float2*>(a.part_ml + prow * 2) = float2{M, L};
+          if (md == 0 && grp == 0 && c0 == 0) *reinterpret_cast<float2*>(a.part_ml + prow * 2) = float2{M, L};
         }
       }
     }
