@@ -356,3 +356,17 @@ def test_attention_sliding_window_head_dim_128(dev, kv_dtype, lens, W, max_ctx, 
     out = _run_case(c, window=window)
     torch.cuda.synchronize()
     _check_case(c, out, window=window)
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+@pytest.mark.parametrize("lens,W,max_ctx", [([4096], 16, 4200), ([8192, 3000], 16, 8300),
+                                            ([5000, 100, 2000, 7000], 9, 7100), ([4096], 17, 4200)])
+def test_attention_qwen3_8b_heads(dev, kv_dtype, lens, W, max_ctx):
+    """The Qwen3-8B head shape (32 query / 8 kv heads): grids that fit the CUs once run the wide
+    kernel (every query tile interleaved, one workgroup per CU), larger ones the compact kernel
+    (two workgroups per CU), 3- and 5-tile row groups included."""
+    print(f"attn 32/8 heads kv={kv_dtype} lens={lens} W={W} max_ctx={max_ctx}", flush=True)
+    c = _random_case(dev, kv_dtype, lens, W, max_ctx, nq=32, nkv=8)
+    out = _run_case(c)
+    torch.cuda.synchronize()
+    _check_case(c, out)
