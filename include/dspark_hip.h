@@ -277,6 +277,9 @@ int dsk_qkv_norm_rope_append(const void* qkv, int qkv_splits, int B, int W, int 
  * kept between calls). Every block_table entry of a row must name a valid page: a split
  * reads its whole key range through the table before it knows the row's length.
  * head_dim 128 or 256, or 512 (the gemma4 drafter's global head) without the fused entry.
+ * Verify passes (at most 80 query rows W * nq / nkv per kv head at head_dim 128, 64 at 256, page
+ * a multiple of 32) take splits of 256 (128) keys; with a sliding window only the splits of one
+ * window are launched, each row's placed from its seq_lens entry on the device.
  * W > 64 (a prefill's many queries), head_dim 128, no softcap, unpacked output and at most
  * 1024 pages per row: one workgroup per 256 query rows of a (row, kv head) streams that block's
  * whole key range, with no splits, no combine and no workspace use. Other many-query passes take
