@@ -173,6 +173,15 @@ struct AttnArgs {
                      // max(0, seq_lens[b] - window + 1) / kps + s (nsplit covers one window)
 };
 
+// bf16 terms that carry a float32 probability into the P.V MFMAs of the verify and split
+// kernels: hi + mid + lo is within 2^-26 of p. Two terms (within 2^-17) put the full-width
+// Qwen3-8B verify logits at 1.3x the noise floor's rms against the float32-softmax reference
+// (1.07x with three); one term (bf16 P) moves them further.
+#ifndef DSK_ATTN_P_TERMS
+#define DSK_ATTN_P_TERMS 3
+#endif
+constexpr int kPTerms = DSK_ATTN_P_TERMS;
+
 // page ids one split may span (kps / page + 1), held in LDS
 constexpr int kAttnMaxSplitPages = 256;
 
@@ -587,7 +596,7 @@ __global__ __launch_bounds__(256 * WPT) __attribute__((amdgpu_waves_per_eu(1, 2)
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     // rescale of the previous blocks' sum and output (none on the first block)
     const float alpha = m_run == -__builtin_inff() ? 0.0f : __expf(m_run - mx);
-    // float32 probabilities in place of the scores (three bf16 terms each in the P.V MFMAs)
+    // float32 probabilities in place of the scores (kPTerms bf16 terms each in the P.V MFMAs)
     float lsum = 0.0f;
 #pragma unroll
     for (int h = 0; h < NKH; ++h)
@@ -622,31 +631,31 @@ __global__ __launch_bounds__(256 * WPT) __attribute__((amdgpu_waves_per_eu(1, 2)
         if (c + 1 < KH / 32)
 #pragma unroll
           for (int d = 0; d < DT; ++d) vv[(c + 1) & 1][d] = vfrag(d, c + 1);
-        // P of the chunk's 8 keys (score tiles 2c, 2c + 1) as hi + mid + lo
-        uint32_t w[3][4];
+        // P of the chunk's 8 keys (score tiles 2c, 2c + 1) as kPTerms bf16 terms
+        uint32_t w[kPTerms][4];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
           for (int r2 = 0; r2 < 2; ++r2) {
-            const Bf16x2Terms tt = split3_bf16x2(st[2 * c + hh][2 * r2], st[2 * c + hh][2 * r2 + 1]);
-            w[0][2 * hh + r2] = tt.hi;
-            w[1][2 * hh + r2] = tt.mid;
-            w[2][2 * hh + r2] = tt.lo;
+            uint32_t tt[kPTerms];
+            split_terms_bf16x2<kPTerms>(st[2 * c + hh][2 * r2], st[2 * c + hh][2 * r2 + 1], tt);
+#pragma unroll
+            for (int k = 0; k < kPTerms; ++k) w[k][2 * hh + r2] = tt[k];
           }
         __builtin_amdgcn_sched_barrier(0);
-        bf16x8 pk[3];
+        bf16x8 pk[kPTerms];
 #pragma unroll
-        for (int k = 0; k < 3; ++k) pk[k] = __builtin_bit_cast(bf16x8, (u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}));
+        for (int k = 0; k < kPTerms; ++k) pk[k] = __builtin_bit_cast(bf16x8, (u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}));
         if constexpr (DT >= 16) {
-          // wide heads: a V fragment's three products back to back, so it is free after them
+          // wide heads: a V fragment's products back to back, so it is free after them
 #pragma unroll
           for (int d = 0; d < DT; ++d)
 #pragma unroll
-            for (int k = 0; k < 3; ++k) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv[c & 1][d], pk[k], o[d], 0, 0, 0);
+            for (int k = 0; k < kPTerms; ++k) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv[c & 1][d], pk[k], o[d], 0, 0, 0);
         } else {
           // one term over every d tile before the next (DT independent accumulators in between)
 #pragma unroll
-          for (int k = 0; k < 3; ++k)
+          for (int k = 0; k < kPTerms; ++k)
 #pragma unroll
             for (int d = 0; d < DT; ++d) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vv[c & 1][d], pk[k], o[d], 0, 0, 0);
         }
@@ -855,7 +864,7 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(AttnArgs a) {
 //    the 8 keys {4 a + r, 16 + 4 a + r} the lane also holds scores for, so P^T goes from the
 //    score registers straight into the P.V MFMA.
 //  - O^T[dim index][q]: lane (a, q) ends with physical dims DPL a + 4 dt + r.
-// The probabilities stay float32 (three bf16 terms in the P.V MFMAs); masks and the partial
+// The probabilities stay float32 (kPTerms bf16 terms in the P.V MFMAs); masks and the partial
 // layout are the attention kernel's; attention_verify_combine_kernel merges the splits (a split
 // past a row's keys, or before every window of its rows, writes m = -inf, which the merge skips).
 constexpr int kVerifyBlock = 32;   // keys per page-aligned block (the page size is a multiple)
@@ -1103,7 +1112,7 @@ void attention_verify_kernel(AttnArgs a) {
         mx[u] = fmaxf(mx[u], __shfl_xor(mx[u], 32, 64));
       }
       // per tile: float32 probabilities (in place of the scores) and their sums, then O^T +=
-      // V^T . P^T over the wave's keys (32 per MFMA) with P as three bf16 terms; a tile's MFMAs
+      // V^T . P^T over the wave's keys (32 per MFMA) with P as kPTerms bf16 terms; a tile's MFMAs
       // run while the next tile's exponentials are computed. Masked keys: exp2(-inf) = 0; a row
       // with no visible key keeps m = -inf, l = 0.
 #pragma unroll
@@ -1121,19 +1130,19 @@ void attention_verify_kernel(AttnArgs a) {
         m[u] = mx[u] * mscale;
 #pragma unroll
         for (int cp = 0; cp < KB / 2; ++cp) {
-          uint32_t w[3][4];
+          uint32_t w[kPTerms][4];
 #pragma unroll
           for (int v = 0; v < 2; ++v)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
               const f32x4& pv = st[u][2 * cp + v];
-              const Bf16x2Terms tt = split3_bf16x2(pv[2 * h], pv[2 * h + 1]);
-              w[0][2 * v + h] = tt.hi;
-              w[1][2 * v + h] = tt.mid;
-              w[2][2 * v + h] = tt.lo;
+              uint32_t tt[kPTerms];
+              split_terms_bf16x2<kPTerms>(pv[2 * h], pv[2 * h + 1], tt);
+#pragma unroll
+              for (int k = 0; k < kPTerms; ++k) w[k][2 * v + h] = tt[k];
             }
 #pragma unroll
-          for (int k = 0; k < 3; ++k) {
+          for (int k = 0; k < kPTerms; ++k) {
             const bf16x8 pk = __builtin_bit_cast(bf16x8, (u32x4{w[k][0], w[k][1], w[k][2], w[k][3]}));
 #pragma unroll
             for (int d = 0; d < DT; ++d)

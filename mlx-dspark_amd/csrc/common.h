@@ -103,6 +103,22 @@ __device__ __forceinline__ void split2_bf16x2(float p0, float p1, uint32_t& hi, 
   lo = pack_bf16x2(p0 - bits_f32(hi << 16), p1 - bits_f32(hi & 0xffff0000u));
 }
 
+// The first NT terms (1: bf16(p), 2: hi + lo, 3: hi + mid + lo) of two probabilities.
+template <int NT>
+__device__ __forceinline__ void split_terms_bf16x2(float p0, float p1, uint32_t (&t)[NT]) {
+  static_assert(NT >= 1 && NT <= 3, "1 to 3 terms");
+  if constexpr (NT == 3) {
+    const Bf16x2Terms x = split3_bf16x2(p0, p1);
+    t[0] = x.hi;
+    t[1] = x.mid;
+    t[2] = x.lo;
+  } else if constexpr (NT == 2) {
+    split2_bf16x2(p0, p1, t[0], t[1]);
+  } else {
+    t[0] = pack_bf16x2(p0, p1);
+  }
+}
+
 // ---- wave-level reductions (wave64) ----------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);

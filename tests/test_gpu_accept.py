@@ -147,25 +147,31 @@ def test_argmax_rows_first_index_on_ties(dev, R, V, ld, dtype):
         assert np.array_equal(tok2.cpu().numpy(), ref), rep
 
 
-@pytest.mark.parametrize("kind", ["equal", "ties", "spike"])
+@pytest.mark.parametrize("kind", ["equal", "ties", "spike", "tail"])
 def test_accept_sample_degenerate_rows(dev, kind):
     """Rows whose threshold bucket holds the whole vocabulary (all-equal logits), rows of heavy
-    exact ties, and rows where one logit carries almost all the mass: the candidate select
-    sees its largest and smallest inputs."""
+    exact ties, rows where one logit carries almost all the mass, and rows whose long flat tail
+    of tiny probabilities (e ~ e^-12 each) holds about half the mass: the candidate select sees
+    its largest and smallest inputs."""
     from mlx_dspark.ops import accept_sample
     B, L, V = 2, 3, 151936
-    rng = np.random.default_rng({"equal": 1, "ties": 2, "spike": 3}[kind])
+    rng = np.random.default_rng({"equal": 1, "ties": 2, "spike": 3, "tail": 4}[kind])
     if kind == "equal":
         q = np.zeros((B, L, V), np.float32)
         p = np.zeros((B, L + 1, V), np.float32)
     elif kind == "ties":
         q = rng.integers(-3, 4, size=(B, L, V)).astype(np.float32)
         p = rng.integers(-3, 4, size=(B, L + 1, V)).astype(np.float32)
-    else:
+    elif kind == "spike":
         q = (rng.standard_normal((B, L, V))).astype(np.float32)
         p = (rng.standard_normal((B, L + 1, V))).astype(np.float32)
         p[:, :, 17] = 40.0
         q[:, :, 17] = 38.0
+    else:   # one token at 12 over a tail near 0: each tail e ~ e^-12 < 2^-16, ~half the mass
+        q = (0.01 * rng.standard_normal((B, L, V))).astype(np.float32)
+        p = (0.01 * rng.standard_normal((B, L + 1, V))).astype(np.float32)
+        p[:, :, 17] = 12.0
+        q[:, :, 17] = 11.5
     draft = rng.integers(0, V, size=(B, L)).astype(np.int32)
     draft[:, 0] = 17
     for T, tp, tk in [(1.0, 0.95, 0), (1.0, 0.9, 1000), (0.6, 1.0, 7)]:
