@@ -731,6 +731,31 @@ def main(argv=None) -> int:
     del g17
     log(f"verify step at W = {W17}: {verify17_us:.1f} us ({verify17_frac * 100:.1f}% of HBM roofline)")
 
+    # ---- overlap experiment: the same 16-row verify with each layer's o and gate|up weights read
+    # on a side stream during its attention stage (Qwen3W8.prefetch_weights); same logits
+    model.prefetch_weights(True)
+    vlp = torch.empty_like(vl)
+    model.forward(vids, cache, tap, advance=False, logits_out=vlp, fused_out=vf)
+    gp = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gp):
+        model.forward(vids, cache, tap, advance=False, logits_out=vlp, fused_out=vf)
+    for _ in range(3):
+        gp.replay()
+    torch.cuda.synchronize()
+    s_ev.record()
+    for _ in range(args.verify_reps):
+        gp.replay()
+    e_ev.record()
+    torch.cuda.synchronize()
+    verify_prefetch_us = s_ev.elapsed_time(e_ev) * 1e3 / args.verify_reps
+    g.replay()
+    torch.cuda.synchronize()
+    prefetch_same = bool(torch.equal(vl, vlp))
+    del gp
+    model.prefetch_weights(False)
+    log(f"verify step with the o / gate_up weights prefetched on a side stream: {verify_prefetch_us:.1f} us "
+        f"(logits identical: {prefetch_same})")
+
     # ---- the dominant kernel: of the W8 GEMM instantiations the verify step runs, the one with
     # the most time per forward (in-graph launch times x launches per forward)
     shapes = gemm_roofline(model, W)
@@ -802,6 +827,9 @@ def main(argv=None) -> int:
         "verify17_us": round(verify17_us, 1),
         "verify17_alg_bytes": int(alg17),
         "verify17_roofline_frac": round(verify17_frac, 4),
+        "verify_prefetch_us": round(verify_prefetch_us, 1),
+        "verify_prefetch": "the 16-row verify with each layer's o and gate|up weights read on a side stream during "
+                           f"its attention stage (overlap experiment, off in the engine); logits identical: {prefetch_same}",
         "roofline": {"kernel": f"{dom['kernel']} (W8 GEMM: {' and '.join(dom['shapes'])} of the {W}-row verify, "
                                f"{dom['share'] * 100:.1f}% of its GEMM time)",
                      "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",

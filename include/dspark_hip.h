@@ -415,6 +415,12 @@ int dsk_argmax_rows(const void* logits, int dtype, int64_t ldl, int64_t V, int R
  * accepted rows, :935-937). */
 int dsk_lens_add(int32_t* lens, const int32_t* n, int B, int add, dsk_stream_t stream);
 
+/* Read-only touch of bytes [p, p + bytes) by `workgroups` workgroups, for overlap experiments: a
+ * side stream running it during the attention stage brings the next GEMMs' weights into the
+ * memory-side cache. No counterpart in the reference (MLX schedules its own kernels); the engine
+ * uses it only when asked (Qwen3W8.prefetch_weights). sink: 16 bytes the kernel may write. */
+int dsk_prefetch(const void* p, size_t bytes, int workgroups, void* sink, dsk_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------
  * DSpark drafter heads.
  * ------------------------------------------------------------------------------------- */

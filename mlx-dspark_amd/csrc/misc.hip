@@ -97,6 +97,23 @@ __global__ __launch_bounds__(kLpThreads) void row_logprobs_kernel(const float* _
   }
 }
 
+// Reads [p, p + n16 * 16) and keeps nothing: the bytes pass through the memory-side cache on
+// their way, so a kernel that reads them soon after finds them there. The xor of everything
+// read is stored only if it equals a value no real weight image produces in practice, and then
+// into the caller's 16-byte sink, so the loads cannot be dropped.
+__global__ __launch_bounds__(256) void prefetch_kernel(const uint4* __restrict__ p, int64_t n16,
+                                                       uint4* __restrict__ sink) {
+  uint4 acc = {0, 0, 0, 0};
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256) {
+    const uint4 v = p[i];
+    acc.x ^= v.x;
+    acc.y ^= v.y;
+    acc.z ^= v.z;
+    acc.w ^= v.w;
+  }
+  if (acc.x == 0x9e3779b9u && acc.y == 0x7f4a7c15u && acc.z == 0xf39cc060u && acc.w == 0x5ced1a3bu) *sink = acc;
+}
+
 }  // namespace dsk
 
 using namespace dsk;
@@ -118,6 +135,17 @@ extern "C" int dsk_logits_penalize(float* logits, int64_t ldl, int R, const int3
   hipLaunchKernelGGL(penalize_kernel, dim3((unsigned)R), dim3(64), 0, as_stream(stream), logits, ldl, row_ptr, ids,
                      vals);
   DSK_LAUNCH_CHECK("dsk_logits_penalize");
+  return DSK_OK;
+}
+
+extern "C" int dsk_prefetch(const void* p, size_t bytes, int workgroups, void* sink, dsk_stream_t stream) {
+  DSK_REQUIRE(p && sink && workgroups > 0, "dsk_prefetch: bad arguments");
+  DSK_REQUIRE(((uintptr_t)p & 15) == 0 && bytes % 16 == 0 && ((uintptr_t)sink & 15) == 0,
+              "dsk_prefetch: 16-byte aligned pointers and a multiple of 16 bytes");
+  if (bytes == 0) return DSK_OK;
+  hipLaunchKernelGGL(prefetch_kernel, dim3((unsigned)workgroups), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const uint4*>(p), (int64_t)(bytes / 16), reinterpret_cast<uint4*>(sink));
+  DSK_LAUNCH_CHECK("dsk_prefetch");
   return DSK_OK;
 }
 

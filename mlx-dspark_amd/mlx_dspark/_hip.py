@@ -83,6 +83,7 @@ SIGNATURES: dict[str, tuple] = {
     "dsk_argmax_ws_bytes": (c_size_t, [c_int]),
     "dsk_argmax_rows": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int, c_void_p, c_void_p, c_size_t, c_void_p]),
     "dsk_lens_add": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "dsk_prefetch": (c_int, [c_void_p, c_size_t, c_int, c_void_p, c_void_p]),
     "dsk_markov_ws_bytes": (c_size_t, [c_int, c_int64, c_int]),
     "dsk_markov_block": (c_int, [c_void_p, c_int64, c_int, c_int, c_int64, c_int, c_void_p, c_void_p, c_void_p,
                                  c_void_p, c_void_p, c_void_p, c_float, c_float, c_int, c_uint64, c_uint32, c_int,

@@ -536,6 +536,14 @@ def argmax_rows(logits: torch.Tensor, *, token_out=None) -> torch.Tensor:
     return token_out
 
 
+def prefetch(w: W8Weight, sink: torch.Tensor, workgroups: int = 512) -> None:
+    """Read a weight's codes and scale words on the current stream and keep nothing
+    (dsk_prefetch): run on a side stream, it brings them into the memory-side cache for the
+    GEMM that reads them next. sink: a 16-byte device buffer the kernel may write."""
+    for t in (w.wt, w.sb):
+        call("dsk_prefetch", ptr(t), t.numel() * t.element_size(), int(workgroups), ptr(sink), stream_ptr())
+
+
 def lens_add(lens: torch.Tensor, n: torch.Tensor | None, add: int) -> None:
     call("dsk_lens_add", ptr(lens), ptr(n), lens.numel(), int(add), stream_ptr())
 

@@ -116,6 +116,7 @@ class Qwen3W8:
                                if args.rope_local_base_freq else self.inv_freq)
         self.act_epi = DSK_EPI_SWIGLU if args.hidden_act == "silu" else DSK_EPI_GEGLU
         self._dense_w = None   # bf16 rows of every layer's weights, when keep_dense_weights holds them
+        self._prefetch = None  # (side stream, sink, workgroups) when prefetch_weights is on
 
     # ------------------------------------------------------------------ cache
     def make_cache(self, B: int = 1, max_ctx: int | None = None, kv_bits: int | None = None,
@@ -131,6 +132,17 @@ class Qwen3W8:
         for L in self.layers:
             t += L.qkv.nbytes + L.o.nbytes + L.gate_up.nbytes + L.down.nbytes
         return t
+
+    def prefetch_weights(self, on: bool = True, workgroups: int = 512) -> None:
+        """Overlap experiment (off by default): each Qwen3-layout layer forks a side stream after
+        its q/k/v projection that reads the layer's o and gate|up weights (dsk_prefetch) while the
+        RoPE/append, attention and combine run, so those GEMMs find their weights in the
+        memory-side cache; the forward joins the side stream before it returns."""
+        if not on:
+            self._prefetch = None
+            return
+        self._prefetch = (torch.cuda.Stream(device=self.device),
+                          torch.zeros(4, dtype=torch.int32, device=self.device), int(workgroups))
 
     # ------------------------------------------------------------------ forward
     def embed_rows(self, ids: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -151,6 +163,12 @@ class Qwen3W8:
         eps = a.rms_norm_eps
         # a normed-later x: the split-K partials take its row scale where they are summed
         qkv = ops.w8_gemm(x.plain(), L.qkv, epi=ops.DSK_EPI_PARTIAL)
+        if self._prefetch is not None and not a.sandwich_norms:
+            side, sink, wg = self._prefetch
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                ops.prefetch(L.o, sink, wg)
+                ops.prefetch(L.gate_up, sink, wg)
         k_pool, v_pool, k_sb, v_sb = cache.layer_args(l)
         inv_freq = self.inv_freq_local if a.is_sliding(l) else self.inv_freq
         q = ops.qkv_rope_append(qkv, B, W, nq, nkv, hd, L.q_norm, L.k_norm, eps, inv_freq,
@@ -233,6 +251,8 @@ class Qwen3W8:
         if advance:
             ops.lens_add(cache.seq_lens, None, W)
             cache.note_lengths([l + W for l in cache.lengths])
+        if self._prefetch is not None:
+            torch.cuda.current_stream().wait_stream(self._prefetch[0])   # join the side stream
         return out, (fused.view(B, W, -1) if fused is not None else None)
 
     def _forward_groups(self, ids, cache, tap, *, advance, logits, logits_out, fused_out, h_out):

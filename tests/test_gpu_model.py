@@ -247,3 +247,34 @@ def test_dflash_pipelined_rounds_match_sequential(dev, tiny, temperature):
     assert (list(cache2.lengths), list(dcache2.lengths)) == seq_lens
     assert cache2.seq_lens.tolist() == cache.seq_lens.tolist() == seq_lens[0]
     assert dcache2.seq_lens.tolist() == dcache.seq_lens.tolist() == seq_lens[1]
+
+
+def test_weight_prefetch_side_stream_leaves_the_forward_unchanged(dev, tiny):
+    """prefetch_weights: each layer's o and gate|up weights read on a side stream during its
+    attention stage; the logits and taps are bit-identical, eager and graph-replayed, and the
+    cache lengths advance as without it."""
+    print("weight prefetch on a side stream: tiny model, 8-bit KV, 64-token context, 16 rows", flush=True)
+    model = tiny
+    ctx = torch.randint(0, model.args.vocab_size, (1, 64), dtype=torch.int32, device=dev)
+    ids = torch.randint(0, model.args.vocab_size, (1, 16), dtype=torch.int32, device=dev)
+    outs = []
+    for on in (False, True):
+        model.prefetch_weights(on)
+        cache = model.make_cache(max_ctx=128, kv_bits=8)
+        model.forward(ctx, cache, None)
+        eager = model.forward(ids, cache, [0, 1], advance=False)
+        lo = torch.empty((16, model.args.vocab_size), dtype=torch.float32, device=dev)
+        model.forward(ids, cache, [0, 1], advance=False, logits_out=lo)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            model.forward(ids, cache, [0, 1], advance=False, logits_out=lo)
+        lo.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        outs.append((eager[0].clone(), eager[1].clone(), lo.clone(), cache.lengths[0], int(cache.seq_lens[0])))
+        del g
+    model.prefetch_weights(False)
+    (l0, f0, g0, n0, d0), (l1, f1, g1, n1, d1) = outs
+    assert torch.equal(l0, l1) and torch.equal(f0, f1) and torch.equal(g0, g1)
+    assert torch.equal(g0.view_as(l0), l0)
+    assert (n0, d0) == (n1, d1) == (64, 64)
