@@ -295,7 +295,8 @@ constexpr int kMaxSlices = 32;        // workgroups per row in the row passes
 constexpr int kEPT = 32;              // elements per thread in the gather pass: slice <= 16384
 constexpr int kMaxDrawSlices = 128;   // workgroups per draw in the draw passes (<= kST)
 constexpr int kDrawEPT = 8;           // elements per thread in the draw pass: draw slice <= 4096
-constexpr int kHistCopies = 8;        // lane-striped copies of the stats pass's LDS histogram
+constexpr int kHistCopies = 2;        // lane-striped copies of the stats pass's LDS histogram
+                                      // (2 measured 2.3 us faster over the whole ACC than 8)
 constexpr int kFinCap = 10240;        // candidate keys the finishing pass stages in LDS
 constexpr int64_t kMaxSlice = (int64_t)kST * kEPT;
 constexpr int kL1 = 512;              // first-level buckets: key >> 21 (e <= 1 keeps it <= 508)

@@ -872,9 +872,15 @@ constexpr int kVerifyBlock = 32;   // keys per page-aligned block (the page size
 #define DSK_VERIFY_TG_MAX 128      // most (b, kv head, split) workgroups that get two query-tile groups
 #endif
 constexpr int kVerifyWaves = 4;
+// 16-key tiles per wave (KB): 4 at head_dim 128 (256-key splits), 2 at 256 (128 keys), and 2 at
+// head_dim 128 for grids of at most DSK_VERIFY_KB2_MAX 256-key (b, kv head, split) workgroups
+// of at most 2 query tiles: twice the splits then fill more CUs. Measured on 9 rows of a
+// 16-query-head / 8-kv-head model over 768 keys: 2 us less per layer; on 16 rows of a 32 / 8
+// model over 4096 keys (136 workgroups) 3 us more, so larger grids keep 256-key splits.
+#ifndef DSK_VERIFY_KB2_MAX
+#define DSK_VERIFY_KB2_MAX 64
+#endif
 template <int HD> struct VerifyShape {
-  static constexpr int KB = HD == 128 ? 4 : 2;          // 16-key tiles per wave
-  static constexpr int KEYS = kVerifyWaves * 16 * KB;   // keys per split
   static constexpr int MAXR = HD == 128 ? 80 : 64;      // query rows per kv head (5 or 4 tiles)
 };
 
@@ -921,11 +927,12 @@ typedef short s16x8 __attribute__((ext_vector_type(8)));
 // split are 8 workgroup ids apart, so they run on one XCD (workgroups go to the 8 XCDs round
 // robin) and the second reads the split's K/V from that XCD's L2; ids past the grid's
 // (b, kv head, split) count exit at once.
-template <int HD, int KVT, bool SOFTCAP, int QT>
+template <int HD, int KVT, bool SOFTCAP, int QT, int KB>
 __global__ __launch_bounds__(kVerifyWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attention_verify_kernel(AttnArgs a) {
   constexpr int QROW = HD + 8, DPL = HD / 4, DT = HD / 16;    // LDS query row, dims per lane, d tiles
-  constexpr int NW = kVerifyWaves, KB = VerifyShape<HD>::KB, KEYS = VerifyShape<HD>::KEYS;
+  constexpr int NW = kVerifyWaves, KEYS = NW * 16 * KB;      // keys per split
+  static_assert(KB == 2 || KB == 4, "key tiles per wave");
   constexpr int NC = KVT == DSK_KV_BF16 ? DPL / 8 : DPL / 16;  // 16-byte loads per lane and key row
   // TP query tiles per pass (interleaved: their MFMAs and exponentials overlap; pairs at head_dim
   // 128, single tiles at 256 where a pair's accumulators exceed the registers), merged through
@@ -1648,11 +1655,12 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
   a.part_ml = a.nsplit > 1 ? reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) +
                                                        attn_part_o_bytes(a.B, a.W, a.nq, hd, a.nsplit))
                            : nullptr;
-  const int verify_keys = hd == 128 ? VerifyShape<128>::KEYS : VerifyShape<256>::KEYS;
   const int verify_maxr = hd == 128 ? VerifyShape<128>::MAXR : VerifyShape<256>::MAXR;
   if ((hd == 128 || hd == 256) && !fused && a.R <= verify_maxr && a.page % kVerifyBlock == 0) {
-    // verify passes: 4 waves per split (256 keys at head_dim 128, 128 at 256), every query tile
-    a.kps = verify_keys;
+    // verify passes: 4 waves per split (256 keys at head_dim 128, 128 at 256 and for small
+    // head_dim-128 grids), every query tile
+    const int kb = hd == 256 || (tiles <= 2 && (int64_t)a.B * a.nkv * ceil_div(span, 256) <= DSK_VERIFY_KB2_MAX) ? 2 : 4;
+    a.kps = kVerifyWaves * 16 * kb;
     a.nsplit = (int)ceil_div(max_ctx, a.kps);
     // a sliding window spans at most (window + W - 2) / kps + 2 splits from the one holding the
     // first row's window start: only those are launched
@@ -1677,22 +1685,25 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
     a.tgroups = ((tiles == 2 || tiles == 4) && tasks <= DSK_VERIFY_TG_MAX) ? 2 : 1;
     const int qt = tiles / a.tgroups;
     const dim3 vgrid((unsigned)(ceil_div(tasks, 8) * 8 * a.tgroups)), vblk(kVerifyWaves * 64);
-#define DSK_VERIFY_QT(kvt, scv)                                                                           \
-  if (hd == 256) {                                                                                        \
-    switch (qt) {                                                                                         \
-      case 1: hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 1>), vgrid, vblk, 0, st, a); break; \
-      case 2: hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 2>), vgrid, vblk, 0, st, a); break; \
-      case 3: hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 3>), vgrid, vblk, 0, st, a); break; \
-      default: hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 4>), vgrid, vblk, 0, st, a); break; \
-    }                                                                                                     \
-  } else {                                                                                                \
-    switch (qt) {                                                                                         \
-      case 1: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 1>), vgrid, vblk, 0, st, a); break; \
-      case 2: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 2>), vgrid, vblk, 0, st, a); break; \
-      case 3: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 3>), vgrid, vblk, 0, st, a); break; \
-      case 4: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 4>), vgrid, vblk, 0, st, a); break; \
-      default: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 5>), vgrid, vblk, 0, st, a); break; \
-    }                                                                                                     \
+#define DSK_VERIFY_QT(kvt, scv)                                                                              \
+  if (hd == 256) {                                                                                           \
+    switch (qt) {                                                                                            \
+      case 1: hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 1, 2>), vgrid, vblk, 0, st, a); break; \
+      case 2: hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 2, 2>), vgrid, vblk, 0, st, a); break; \
+      case 3: hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 3, 2>), vgrid, vblk, 0, st, a); break; \
+      default: hipLaunchKernelGGL((attention_verify_kernel<256, kvt, scv, 4, 2>), vgrid, vblk, 0, st, a); break; \
+    }                                                                                                        \
+  } else if (kb == 2) {                                                                                      \
+    if (qt == 1) hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 1, 2>), vgrid, vblk, 0, st, a);  \
+    else hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 2, 2>), vgrid, vblk, 0, st, a);          \
+  } else {                                                                                                   \
+    switch (qt) {                                                                                            \
+      case 1: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 1, 4>), vgrid, vblk, 0, st, a); break; \
+      case 2: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 2, 4>), vgrid, vblk, 0, st, a); break; \
+      case 3: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 3, 4>), vgrid, vblk, 0, st, a); break; \
+      case 4: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 4, 4>), vgrid, vblk, 0, st, a); break; \
+      default: hipLaunchKernelGGL((attention_verify_kernel<128, kvt, scv, 5, 4>), vgrid, vblk, 0, st, a); break; \
+    }                                                                                                        \
   }
     if (a.kv_dtype == DSK_KV_U8) {
       if (sc) { DSK_VERIFY_QT(DSK_KV_U8, true) } else { DSK_VERIFY_QT(DSK_KV_U8, false) }

@@ -362,11 +362,25 @@ def test_attention_sliding_window_head_dim_128(dev, kv_dtype, lens, W, max_ctx, 
 @pytest.mark.parametrize("lens,W,max_ctx", [([4096], 16, 4200), ([8192, 3000], 16, 8300),
                                             ([5000, 100, 2000, 7000], 9, 7100), ([4096], 17, 4200)])
 def test_attention_qwen3_8b_heads(dev, kv_dtype, lens, W, max_ctx):
-    """The Qwen3-8B head shape (32 query / 8 kv heads): grids that fit the CUs once run the wide
-    kernel (every query tile interleaved, one workgroup per CU), larger ones the compact kernel
-    (two workgroups per CU), 3- and 5-tile row groups included."""
+    """The Qwen3-8B head shape (32 query / 8 kv heads): four 16-row query tiles per kv head in
+    two passes of two (3- and 5-tile row groups included), ragged rows over long contexts."""
     print(f"attn 32/8 heads kv={kv_dtype} lens={lens} W={W} max_ctx={max_ctx}", flush=True)
     c = _random_case(dev, kv_dtype, lens, W, max_ctx, nq=32, nkv=8)
     out = _run_case(c)
     torch.cuda.synchronize()
     _check_case(c, out)
+
+
+@pytest.mark.parametrize("kv_dtype", [0, 1])
+@pytest.mark.parametrize("lens,W,max_ctx,window", [([768], 9, 841, 0), ([700, 40], 9, 800, 0), ([760], 9, 841, 256),
+                                                   ([500, 0], 1, 640, 0), ([1000], 9, 2100, 0)])
+def test_attention_qwen3_06b_heads(dev, kv_dtype, lens, W, max_ctx, window):
+    """The Qwen3-0.6B head shape (16 query / 8 kv heads, 9 new tokens: two query tiles per kv
+    head). Grids of at most 64 (row, kv head, 256-key split) workgroups run 128-key splits (the
+    first four cases, ragged rows, a sliding window and single-token rows included); the last
+    case's 72 run 256-key splits."""
+    print(f"attn 16/8 heads kv={kv_dtype} lens={lens} W={W} max_ctx={max_ctx} window={window}", flush=True)
+    c = _random_case(dev, kv_dtype, lens, W, max_ctx, nq=16, nkv=8)
+    out = _run_case(c, window=window)
+    torch.cuda.synchronize()
+    _check_case(c, out, window=window)
