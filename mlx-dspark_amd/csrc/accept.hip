@@ -55,7 +55,7 @@ __device__ __forceinline__ float dsk_expf_le0(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  const float v = p * bits_f32((uint32_t)((int)k + 127) << 23);
+  const float v = ldexpf(p, (int)k);  // k in [-124, 0]: p * 2^k exactly, as a multiply by 2^k
   return under ? 0.0f : v;
 }
 
@@ -163,8 +163,8 @@ __device__ inline void span_argmax(const void* __restrict__ row, int64_t lo, int
     for (int64_t c0 = threadIdx.x; c0 < nv; c0 += 256 * UN) {
       u32x4 v[UN];
 #pragma unroll
-      for (int u = 0; u < UN; ++u)
-        if (c0 + u * 256 < nv) v[u] = __builtin_nontemporal_load(p + c0 + u * 256);
+      for (int u = 0; u < UN; ++u)  // all in flight: a chunk past nv reads chunk c0 (skipped below)
+        v[u] = __builtin_nontemporal_load(p + (c0 + u * 256 < nv ? c0 + u * 256 : c0));
 #pragma unroll
       for (int u = 0; u < UN; ++u) {
         const int64_t c = c0 + u * 256;
@@ -400,22 +400,30 @@ __device__ __forceinline__ float final_prob(const RowParam& rp, float x, int mul
 template <bool VEC>
 struct SliceRegs {
   float v[kEPT];
+  // Every load is issued without a branch, so all of them are in flight together: an index
+  // past the slice reads the slice's first element instead, and every user masks such
+  // elements with valid().
   __device__ __forceinline__ void load(const float* __restrict__ x, int64_t lo, int64_t hi) {
+    const int n = (int)(hi - lo);
+    if (n <= 0) {
+#pragma unroll
+      for (int k = 0; k < kEPT; ++k) v[k] = 0.0f;
+      return;
+    }
     if constexpr (VEC) {
       const f32x4* x4 = reinterpret_cast<const f32x4*>(x + lo);
 #pragma unroll
       for (int i = 0; i < kEPT / 4; ++i) {
-        const int64_t c = (int64_t)i * kST + threadIdx.x;
-        f32x4 t = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (lo + 4 * c < hi) t = x4[c];
+        const int c = i * kST + (int)threadIdx.x;
+        const f32x4 t = x4[4 * c < n ? c : 0];
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[4 * i + e] = t[e];
       }
     } else {
 #pragma unroll
       for (int i = 0; i < kEPT; ++i) {
-        const int64_t j = lo + (int64_t)i * kST + threadIdx.x;
-        v[i] = j < hi ? x[j] : 0.0f;
+        const int j = i * kST + (int)threadIdx.x;
+        v[i] = x[lo + (j < n ? j : 0)];
       }
     }
   }
@@ -497,6 +505,29 @@ __global__ __launch_bounds__(kST) void samp_max_kernel(SampArgs a) {
   }
 }
 
+// A thread's elements of the stats pass: the sum of their masses, and (HW) each element's mass
+// and (HK) count added to its bucket in the thread's histogram copy. Straight-line code: an
+// element past the slice takes x = -inf, so e = 0 and no mass (its count lands in bucket 0, and
+// the caller takes the kST * kEPT - n such counts off again).
+template <bool VEC, bool TONE, bool HW, bool HK>
+__device__ __forceinline__ uint64_t stats_elems(const SliceRegs<VEC>& xr, int n, int mul, float T, float inv_t,
+                                                float m, uint32_t* hcp, unsigned long long* hwp) {
+  uint64_t z = 0;
+#pragma unroll
+  for (int k = 0; k < kEPT; ++k) {
+    const float xv = xr.valid(k, n) ? yv<TONE>(xr.v[k], mul, T, inv_t) - m : -__builtin_inff();
+    const float e = dsk_expf_le0(xv);
+    const uint64_t w = fx(e);
+    z += w;
+    if constexpr (HW) {
+      const uint32_t b = min(f32_bits(e) >> kL1Shift, (uint32_t)kL1 - 1);  // NaN stays in bounds
+      if constexpr (HK) atomicAdd(hcp + b, 1u);
+      atomicAdd(hwp + b, (unsigned long long)w);
+    }
+  }
+  return z;
+}
+
 // ---- pass 2: Z and the first-level histogram, merged per row by integer atomics. Lanes
 // spread their LDS atomics over kHistCopies copies (copy = lane % kHistCopies) so lanes of one
 // wave that hit the same bucket mostly hit different addresses.
@@ -523,20 +554,12 @@ __global__ __launch_bounds__(kST) void samp_stats_kernel(SampArgs a) {
     }
     __syncthreads();
   }
-  uint64_t z = 0;
   const int n = (int)(hi - lo);
-#pragma unroll
-  for (int k = 0; k < kEPT; ++k) {
-    if (!xr.valid(k, n)) continue;
-    const float e = dsk_expf_le0(yv<TONE>(xr.v[k], mul, T, inv_t) - m);
-    const uint64_t w = fx(e);
-    z += w;
-    if (trunc) {
-      const uint32_t b = min(f32_bits(e) >> kL1Shift, (uint32_t)kL1 - 1);  // NaN stays in bounds
-      if (a.do_k) atomicAdd(hcp + b, 1u);
-      if (w) atomicAdd(hwp + b, (unsigned long long)w);
-    }
-  }
+  uint64_t z;
+  if (!trunc) z = stats_elems<VEC, TONE, false, false>(xr, n, mul, T, inv_t, m, hcp, hwp);
+  else if (a.do_k) z = stats_elems<VEC, TONE, true, true>(xr, n, mul, T, inv_t, m, hcp, hwp);
+  else z = stats_elems<VEC, TONE, true, false>(xr, n, mul, T, inv_t, m, hcp, hwp);
+  if (trunc && a.do_k && threadIdx.x == 0) atomicSub(&hc[0][0], (uint32_t)(kST * kEPT - n));
   z = block_sum512(z, sh);
   if (threadIdx.x == 0) atomicAdd((unsigned long long*)&a.zsum[r], (unsigned long long)z);
   if (trunc) {
@@ -916,12 +939,21 @@ __global__ __launch_bounds__(kST) void samp_wsum_kernel(SampArgs a) {
   const float T = a.T, inv_t = 1.0f / T;
   const int64_t lo = min(a.V, (int64_t)s * a.slen_d), hi = min(a.V, lo + a.slen_d);
   // this thread's elements j = lo + tid + k * kST, loads first
-  float pv[kDrawEPT], qv[kDrawEPT];
+  // (without branches, as in SliceRegs::load: a j past the slice reads element lo; such j are
+  // skipped below)
+  float pv[kDrawEPT], qv[kDrawEPT] = {};
+  const int64_t jc = hi > lo ? lo : 0;
 #pragma unroll
   for (int k = 0; k < kDrawEPT; ++k) {
     const int64_t j = lo + threadIdx.x + (int64_t)k * kST;
-    pv[k] = j < hi ? ds.px[j] : 0.0f;
-    qv[k] = (j < hi && ds.qrow >= 0) ? ds.qx[j] : 0.0f;
+    pv[k] = ds.px[j < hi ? j : jc];
+  }
+  if (ds.qrow >= 0) {
+#pragma unroll
+    for (int k = 0; k < kDrawEPT; ++k) {
+      const int64_t j = lo + threadIdx.x + (int64_t)k * kST;
+      qv[k] = ds.qx[j < hi ? j : jc];
+    }
   }
   uint64_t t = 0;
   float* po = (a.mode == 1 && a.probs_out) ? a.probs_out + (int64_t)unit * a.V : nullptr;
