@@ -977,7 +977,19 @@ void attention_verify_kernel(AttnArgs a) {
   const int ntiles = min(QT, ((a.R + 15) >> 4) - tg * QT);  // the group's tiles
   const bool live = j0 < j_end;  // the wave has keys (uniform)
 
-  // ---- loads: the wave's K/V rows (16-key tiles t: keys j0 + 16 t + row16), then the query rows
+  // ---- loads: the group's query rows (issued before the K/V loads and stored to LDS after them,
+  // so that every load is in flight at once; a row past R reads row R - 1 and stores zeros),
+  // then the wave's K/V rows (16-key tiles t: keys j0 + 16 t + row16)
+  constexpr int NQ = QT * 16 * (HD / 8) / (NW * 64);  // 8-dim query chunks per thread
+  static_assert(NQ * NW * 64 == QT * 16 * (HD / 8), "whole query chunks per thread");
+  u32x4 qv[NQ];
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) {
+    const int c = threadIdx.x + NW * 64 * u;  // rows x HD / 8 chunks of 8 dims
+    const int rq = min(r0 + c / (HD / 8), a.R - 1), ch = c % (HD / 8);
+    qv[u] = *reinterpret_cast<const u32x4*>(a.q + ((int64_t)(b * a.W + rq / a.G) * a.nq + kvh * a.G + rq % a.G) * HD +
+                                            ch * 8);
+  }
   u32x4 kc[KB][HD / 32], vc[KB][HD / 32];
   uint32_t ksb[KB], vsb[KB];
   if (live) {
@@ -991,14 +1003,10 @@ void attention_verify_kernel(AttnArgs a) {
   }
   static_assert(NC <= HD / 32, "row slice registers");
 #pragma unroll
-  for (int u = 0; u < QT * 16 * (HD / 8) / (NW * 64); ++u) {
-    const int c = threadIdx.x + NW * 64 * u;  // rows x HD / 8 chunks of 8 dims
-    const int r = c / (HD / 8), ch = c % (HD / 8), rq = r0 + r;
-    u32x4 qv = u32x4{0, 0, 0, 0};
-    if (rq < a.R)
-      qv = *reinterpret_cast<const u32x4*>(a.q + ((int64_t)(b * a.W + rq / a.G) * a.nq + kvh * a.G + rq % a.G) * HD +
-                                           ch * 8);
-    *reinterpret_cast<u32x4*>(qs + r * QROW + ch * 8) = qv;
+  for (int u = 0; u < NQ; ++u) {
+    const int c = threadIdx.x + NW * 64 * u;
+    const int r = c / (HD / 8), ch = c % (HD / 8);
+    *reinterpret_cast<u32x4*>(qs + r * QROW + ch * 8) = r0 + r < a.R ? qv[u] : u32x4{0, 0, 0, 0};
   }
 
   // ---- K dequantised once (the A operand of every score MFMA), V transposed once
