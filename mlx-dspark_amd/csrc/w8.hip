@@ -193,14 +193,17 @@ __global__ __launch_bounds__(kPackThreads) void act_pack_kernel(PackArgs a) {
   const int64_t nchunk = a.K / 8;
   const int64_t G = a.K / 64;
   const int S = a.part ? a.nsplit : 0;
-  // ---- every load up front: norm weights, residual, and each split's 8 values per chunk
-  u32x4 v[NV], wv[NV], hv[NV];
+  // ---- every load up front, all in flight at once: norm weights, residual, each split's 8
+  // values per chunk (slices past S re-read slice S - 1 and are not added), the sandwich norm's
+  // weights
+  u32x4 v[NV], wv[NV], hv[NV], w1v[NV];
   f32x4 pl[NV][MAXS > 0 ? MAXS : 1], ph[NV][MAXS > 0 ? MAXS : 1];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int64_t c = min(tid + (int64_t)i * kPackThreads, nchunk - 1);
     if (a.norm_w) wv[i] = *reinterpret_cast<const u32x4*>(a.norm_w + c * 8);
     if (a.h) hv[i] = *reinterpret_cast<const u32x4*>(a.h + (int64_t)m * a.ldh + c * 8);
+    if (a.res_norm_w) w1v[i] = *reinterpret_cast<const u32x4*>(a.res_norm_w + c * 8);
 #pragma unroll
     for (int s = 0; s < MAXS; ++s) {
       const float* p = a.part + ((int64_t)min(s, S - 1) * a.M + m) * a.K + c * 8;
@@ -226,12 +229,12 @@ __global__ __launch_bounds__(kPackThreads) void act_pack_kernel(PackArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) fv[i][e] = 0.0f;
 #pragma unroll
-    for (int s = 0; s < MAXS; ++s) {
-      if (s >= S) break;
+    for (int s = 0; s < MAXS; ++s) {  // selects, not a branch: the loads stay ahead of any wait
+      const bool in = s < S;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        fv[i][e] += pl[i][s][e];
-        fv[i][4 + e] += ph[i][s][e];
+        fv[i][e] = in ? fv[i][e] + pl[i][s][e] : fv[i][e];
+        fv[i][4 + e] = in ? fv[i][4 + e] + ph[i][s][e] : fv[i][4 + e];
       }
     }
   }
@@ -251,9 +254,7 @@ __global__ __launch_bounds__(kPackThreads) void act_pack_kernel(PackArgs a) {
     const float r1 = rsqrtf(block_sum(ss) / (float)a.K + a.eps);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-      const int64_t c = min(tid + (int64_t)i * kPackThreads, nchunk - 1);
-      const u32x4 w1 = *reinterpret_cast<const u32x4*>(a.res_norm_w + c * 8);
-      const uint16_t* g = reinterpret_cast<const uint16_t*>(&w1);
+      const uint16_t* g = reinterpret_cast<const uint16_t*>(&w1v[i]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) fv[i][e] = round_bf16((fv[i][e] * r1) * bf16_to_f32(g[e]));
     }
@@ -568,9 +569,19 @@ __global__ __launch_bounds__(WAVES * 64) void w8_gemm_kernel(GemmArgs a) {
       const int i = (o >> 8) / NT, j = (o >> 8) % NT;
       const int m = i * 16 + ((o & 63) >> 4) * 4 + ((o >> 6) & 3);
       const int64_t n = (t0 + j) * 16 + (o & 15);
-      const bool live = o < NOUT && m < a.M;
-      hpre[u] = live ? a.h[(int64_t)m * a.ldh + n] : 0;
-      gpre[u] = (live && a.g) ? a.g[n] : 0;
+      if constexpr (WAVES <= 8) {
+        // without branches, so both loads stay in flight through the main loop (guarded, each
+        // took its own round trip first): a dead output (o past NOUT or m past M: n is still a
+        // column of the slab) reads row M - 1 of its column, and gpre is used only when a.g is
+        // set. Measured slower with 16 waves (most of them then hold dead outputs only), which
+        // keep the guarded loads.
+        hpre[u] = a.h[(int64_t)min(m, a.M - 1) * a.ldh + n];
+        gpre[u] = (a.g ? a.g : a.h)[n];
+      } else {
+        const bool live = o < NOUT && m < a.M;
+        hpre[u] = live ? a.h[(int64_t)m * a.ldh + n] : 0;
+        gpre[u] = (live && a.g) ? a.g[n] : 0;
+      }
     }
   }
 
