@@ -1228,13 +1228,14 @@ void attention_verify_kernel(AttnArgs a) {
 
 // The verify kernel's splits merged: one thread per (row b, kv head, query row, 4 dims), every
 // split from the first one the row's sliding window reaches (a split past the row length holds
-// m = -inf and is skipped by value), the loads of a batch of 24 splits issued together. Same
-// merge as attention_combine_kernel: weights exp(m_s - M) * l_s over the splits' normalised
-// float32 partial outputs.
+// m = -inf and is skipped by value), the loads of a batch of BATCH splits issued together (the
+// split count rounded up to 4, at most 24: past the last split a load re-reads it and is not
+// merged). Same merge as attention_combine_kernel: weights exp(m_s - M) * l_s over the splits'
+// normalised float32 partial outputs.
 constexpr int kVerifyCombineThreads = 64;
-template <int HD>
+template <int HD, int BATCH>
 __global__ __launch_bounds__(kVerifyCombineThreads) void attention_verify_combine_kernel(AttnArgs a) {
-  constexpr int BATCH = 24, CH = HD / 4;
+  constexpr int CH = HD / 4;
   const int64_t task = (int64_t)blockIdx.x * kVerifyCombineThreads + threadIdx.x;
   if (task >= (int64_t)a.B * a.nkv * a.R * CH) return;
   const int ch = (int)(task % CH);
@@ -1242,10 +1243,11 @@ __global__ __launch_bounds__(kVerifyCombineThreads) void attention_verify_combin
   const int r = (int)(rowt % a.R);
   const int bk = (int)(rowt / a.R);
   const int b = bk / a.nkv, kvh = bk % a.nkv;
-  const int sl = a.seq_lens[b];
-  const int s_beg = a.causal && a.window > 0 ? max(0, sl + r / a.G + 1 - a.window) / a.kps -
-                                                   (a.wrel ? max(0, sl - a.window + 1) / a.kps : 0)
-                                             : 0;
+  int s_beg = 0;
+  if (a.causal && a.window > 0) {  // only a sliding window needs the row length (one round trip)
+    const int sl = a.seq_lens[b];
+    s_beg = max(0, sl + r / a.G + 1 - a.window) / a.kps - (a.wrel ? max(0, sl - a.window + 1) / a.kps : 0);
+  }
   const size_t base = (size_t)bk * a.nsplit * a.R + r;  // partial row of split 0
   float M = -__builtin_inff(), L = 0.0f;
   f32x4 acc = f32x4{0, 0, 0, 0};
@@ -1722,8 +1724,22 @@ static int attention_run(AttnArgs& a, int hd, int max_ctx, float softcap, void* 
     DSK_LAUNCH_CHECK(who);
     if (a.nsplit > 1) {
       const dim3 cgrid((unsigned)ceil_div((int64_t)a.B * a.nkv * a.R * (hd / 4), kVerifyCombineThreads));
-      if (hd == 256) hipLaunchKernelGGL(attention_verify_combine_kernel<256>, cgrid, dim3(kVerifyCombineThreads), 0, st, a);
-      else hipLaunchKernelGGL(attention_verify_combine_kernel<128>, cgrid, dim3(kVerifyCombineThreads), 0, st, a);
+      // splits per batch of loads: the split count rounded up to 4, at most 24
+      const int batch = std::min(24, (a.nsplit + 3) / 4 * 4);
+#define DSK_COMBINE(HDV, BV) \
+  hipLaunchKernelGGL((attention_verify_combine_kernel<HDV, BV>), cgrid, dim3(kVerifyCombineThreads), 0, st, a)
+#define DSK_COMBINE_B(HDV)                                                                          \
+  switch (batch) {                                                                                  \
+    case 4: DSK_COMBINE(HDV, 4); break;                                                             \
+    case 8: DSK_COMBINE(HDV, 8); break;                                                             \
+    case 12: DSK_COMBINE(HDV, 12); break;                                                           \
+    case 16: DSK_COMBINE(HDV, 16); break;                                                           \
+    case 20: DSK_COMBINE(HDV, 20); break;                                                           \
+    default: DSK_COMBINE(HDV, 24); break;                                                           \
+  }
+      if (hd == 256) { DSK_COMBINE_B(256) } else { DSK_COMBINE_B(128) }
+#undef DSK_COMBINE_B
+#undef DSK_COMBINE
       DSK_LAUNCH_CHECK(who);
     }
     return DSK_OK;
