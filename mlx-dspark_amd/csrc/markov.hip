@@ -18,7 +18,7 @@
 namespace dsk {
 
 constexpr int kMarkovR = 256;          // rank supported (the DSpark checkpoints use 256)
-constexpr int kMarkovTilesPerBlock = 16;
+constexpr int kMarkovTilesPerBlock = 20;  // 5 per wave: one round of 2 waves per SIMD holds every tile of V = 151936
 constexpr int kMarkovMaxB = 16;
 
 struct MarkovArgs {
@@ -60,11 +60,17 @@ __device__ __forceinline__ void reduce_partials(const float* pv, const int32_t* 
     float v[8];
     int id[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < 8; ++u) {  // without branches: every load in flight at once
       const int k = k0 + u * 64 + lane;
-      v[u] = k < n ? pv[k] : -__builtin_inff();
-      id[u] = k < n ? pi[k] : 0x7fffffff;
+      v[u] = pv[min(k, n - 1)];
+      id[u] = pi[min(k, n - 1)];
     }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (k0 + u * 64 + lane >= n) {
+        v[u] = -__builtin_inff();
+        id[u] = 0x7fffffff;
+      }
 #pragma unroll
     for (int u = 0; u < 8; ++u)
       if (better(v[u], id[u], bv, bi)) {
@@ -75,7 +81,7 @@ __device__ __forceinline__ void reduce_partials(const float* pv, const int32_t* 
   wave_argmax(bv, bi);
 }
 
-__global__ __launch_bounds__(256) void markov_step_kernel(MarkovArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void markov_step_kernel(MarkovArgs a) {
   constexpr int R = kMarkovR, G = R / 64;
   __shared__ int prev_s[kMarkovMaxB];
   __shared__ __attribute__((aligned(16))) uint16_t e_lds[16 * R];  // [row][R]
@@ -83,6 +89,32 @@ __global__ __launch_bounds__(256) void markov_step_kernel(MarkovArgs a) {
   __shared__ int red_i[4][kMarkovMaxB];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const bool greedy = a.logits_out == nullptr;
+
+  // ---- 0. the wave's w2 tiles, their scales and the base logits, issued first: they do not
+  // depend on the previous token, so they stream in while it and its w1 row are found (a tile
+  // index past the block's tiles re-reads its last tile, a row past B row B - 1: not used)
+  constexpr int TPW = kMarkovTilesPerBlock / 4;  // tiles per wave
+  const int64_t ntiles = a.V / 16;
+  const int64_t t_lo = (int64_t)blockIdx.x * kMarkovTilesPerBlock;
+  const int64_t t_hi = min(ntiles, t_lo + kMarkovTilesPerBlock);
+  u32x4 wq[TPW][G];
+  uint32_t sv[TPW][G];
+  float bs[TPW][4];
+#pragma unroll
+  for (int i = 0; i < TPW; ++i) {
+    const int64_t t = min(t_lo + wv + 4 * i, t_hi - 1);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      wq[i][g] = __builtin_nontemporal_load(&a.w2t[(t * G + g) * 64 + lane]);
+      sv[i][g] = a.w2sb[(t * G + g) * 16 + (lane & 15)];
+    }
+    const int64_t v = t * 16 + (lane & 15);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int b = min((lane >> 4) * 4 + r, a.B - 1);
+      bs[i][r] = a.base[((int64_t)b * a.cap + a.step) * a.ldb + v];
+    }
+  }
 
   // ---- 1. previous token of every batch row
   if (a.step == 0) {
@@ -134,10 +166,7 @@ __global__ __launch_bounds__(256) void markov_step_kernel(MarkovArgs a) {
     X[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ea[g][1], ones, X[g], 0, 0, 0);
   }
 
-  // ---- 3. this block's tiles, round-robin over the waves
-  const int64_t ntiles = a.V / 16;
-  const int64_t t_lo = (int64_t)blockIdx.x * kMarkovTilesPerBlock;
-  const int64_t t_hi = min(ntiles, t_lo + kMarkovTilesPerBlock);
+  // ---- 3. this block's tiles, round-robin over the waves (loaded in step 0)
   float bestv[4];
   int besti[4];
 #pragma unroll
@@ -145,21 +174,11 @@ __global__ __launch_bounds__(256) void markov_step_kernel(MarkovArgs a) {
     bestv[r] = -__builtin_inff();
     besti[r] = 0x7fffffff;
   }
-  for (int64_t t = t_lo + wv; t < t_hi; t += 4) {
-    u32x4 wq[G];
-    uint32_t sv[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      wq[g] = __builtin_nontemporal_load(&a.w2t[(t * G + g) * 64 + lane]);
-      sv[g] = a.w2sb[(t * G + g) * 16 + (lane & 15)];
-    }
+  for (int it = 0; it < TPW; ++it) {
+    const int64_t t = t_lo + wv + 4 * it;
+    if (t >= t_hi) break;
     const int64_t v = t * 16 + (lane & 15);
-    float bs[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int b = (lane >> 4) * 4 + r;
-      bs[r] = b < a.B ? a.base[((int64_t)b * a.cap + a.step) * a.ldb + v] : 0.0f;
-    }
     f32x4 acc = {0, 0, 0, 0};
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -168,7 +187,7 @@ __global__ __launch_bounds__(256) void markov_step_kernel(MarkovArgs a) {
         uint32_t rr[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const uint32_t q = wq[g][i];
+          const uint32_t q = wq[it][g][i];
           rr[2 * i] = __builtin_amdgcn_perm(f32_bits((float)((q >> 8) & 0xffu)), f32_bits((float)(q & 0xffu)),
                                             0x07060302u);
           rr[2 * i + 1] = __builtin_amdgcn_perm(f32_bits((float)(q >> 24)), f32_bits((float)((q >> 16) & 0xffu)),
@@ -179,7 +198,7 @@ __global__ __launch_bounds__(256) void markov_step_kernel(MarkovArgs a) {
       }
       f32x4 tq = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ea[g][0], b0, f32x4{0, 0, 0, 0}, 0, 0, 0);
       tq = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ea[g][1], b1, tq, 0, 0, 0);
-      const float s = bf16_to_f32((uint16_t)(sv[g] & 0xffffu)), bb = bf16_to_f32((uint16_t)(sv[g] >> 16));
+      const float s = bf16_to_f32((uint16_t)(sv[it][g] & 0xffffu)), bb = bf16_to_f32((uint16_t)(sv[it][g] >> 16));
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[r] = fmaf(s, tq[r], fmaf(bb, X[g][r], acc[r]));
     }
@@ -188,7 +207,7 @@ __global__ __launch_bounds__(256) void markov_step_kernel(MarkovArgs a) {
     for (int r = 0; r < 4; ++r) {
       const int b = (lane >> 4) * 4 + r;
       if (b >= a.B) continue;
-      const float lg = round_bf16(round_bf16(bs[r]) + round_bf16(acc[r]));
+      const float lg = round_bf16(round_bf16(bs[it][r]) + round_bf16(acc[r]));
       if (a.logits_out) a.logits_out[((int64_t)b * a.cap + a.step) * a.V + v] = lg;
       if (better(lg, (int)v, bestv[r], besti[r])) {
         bestv[r] = lg;
