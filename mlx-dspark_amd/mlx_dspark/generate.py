@@ -193,7 +193,8 @@ class _DFlashRound:
     def launch(self, round_idx: int, use_graph: bool) -> None:
         """Enqueue the round: the first of this width runs eagerly (it sizes the workspaces),
         later ones replay one captured graph; then the ids' copy to host memory."""
-        self.rng_off.fill_(round_idx & 0x7FFFFFFF)
+        if self.T > 0:                                               # greedy rounds draw nothing
+            self.rng_off.fill_(round_idx & 0x7FFFFFFF)
         if use_graph:
             if self.graph is None and self.calls >= 1:
                 self.graph = torch.cuda.CUDAGraph()
