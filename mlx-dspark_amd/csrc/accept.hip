@@ -295,8 +295,9 @@ constexpr int kMaxSlices = 32;        // workgroups per row in the row passes
 constexpr int kEPT = 32;              // elements per thread in the gather pass: slice <= 16384
 constexpr int kMaxDrawSlices = 128;   // workgroups per draw in the draw passes (<= kST)
 constexpr int kDrawEPT = 8;           // elements per thread in the draw pass: draw slice <= 4096
-constexpr int kHistCopies = 2;        // lane-striped copies of the stats pass's LDS histogram
-                                      // (2 measured 2.3 us faster over the whole ACC than 8)
+constexpr int kHistCopies = 8;        // lane-striped copies of the stats pass's LDS histogram
+                                      // (rows whose probabilities fill few buckets: 2 copies took
+                                      // the T = 0.6, top-k 20 stats pass from 15.8 to 39.0 us)
 constexpr int kFinCap = 10240;        // candidate keys the finishing pass stages in LDS
 constexpr int64_t kMaxSlice = (int64_t)kST * kEPT;
 constexpr int kL1 = 512;              // first-level buckets: key >> 21 (e <= 1 keeps it <= 508)
@@ -505,29 +506,6 @@ __global__ __launch_bounds__(kST) void samp_max_kernel(SampArgs a) {
   }
 }
 
-// A thread's elements of the stats pass: the sum of their masses, and (HW) each element's mass
-// and (HK) count added to its bucket in the thread's histogram copy. Straight-line code: an
-// element past the slice takes x = -inf, so e = 0 and no mass (its count lands in bucket 0, and
-// the caller takes the kST * kEPT - n such counts off again).
-template <bool VEC, bool TONE, bool HW, bool HK>
-__device__ __forceinline__ uint64_t stats_elems(const SliceRegs<VEC>& xr, int n, int mul, float T, float inv_t,
-                                                float m, uint32_t* hcp, unsigned long long* hwp) {
-  uint64_t z = 0;
-#pragma unroll
-  for (int k = 0; k < kEPT; ++k) {
-    const float xv = xr.valid(k, n) ? yv<TONE>(xr.v[k], mul, T, inv_t) - m : -__builtin_inff();
-    const float e = dsk_expf_le0(xv);
-    const uint64_t w = fx(e);
-    z += w;
-    if constexpr (HW) {
-      const uint32_t b = min(f32_bits(e) >> kL1Shift, (uint32_t)kL1 - 1);  // NaN stays in bounds
-      if constexpr (HK) atomicAdd(hcp + b, 1u);
-      atomicAdd(hwp + b, (unsigned long long)w);
-    }
-  }
-  return z;
-}
-
 // ---- pass 2: Z and the first-level histogram, merged per row by integer atomics. Lanes
 // spread their LDS atomics over kHistCopies copies (copy = lane % kHistCopies) so lanes of one
 // wave that hit the same bucket mostly hit different addresses.
@@ -554,12 +532,22 @@ __global__ __launch_bounds__(kST) void samp_stats_kernel(SampArgs a) {
     }
     __syncthreads();
   }
+  uint64_t z = 0;
   const int n = (int)(hi - lo);
-  uint64_t z;
-  if (!trunc) z = stats_elems<VEC, TONE, false, false>(xr, n, mul, T, inv_t, m, hcp, hwp);
-  else if (a.do_k) z = stats_elems<VEC, TONE, true, true>(xr, n, mul, T, inv_t, m, hcp, hwp);
-  else z = stats_elems<VEC, TONE, true, false>(xr, n, mul, T, inv_t, m, hcp, hwp);
-  if (trunc && a.do_k && threadIdx.x == 0) atomicSub(&hc[0][0], (uint32_t)(kST * kEPT - n));
+  // element by element (uniform branches on the histogram flags keep few registers live: three
+  // workgroups per CU, which the histogram copies' LDS allows)
+#pragma unroll
+  for (int k = 0; k < kEPT; ++k) {
+    if (!xr.valid(k, n)) continue;
+    const float e = dsk_expf_le0(yv<TONE>(xr.v[k], mul, T, inv_t) - m);
+    const uint64_t w = fx(e);
+    z += w;
+    if (trunc) {
+      const uint32_t b = min(f32_bits(e) >> kL1Shift, (uint32_t)kL1 - 1);  // NaN stays in bounds
+      if (a.do_k) atomicAdd(hcp + b, 1u);
+      if (w) atomicAdd(hwp + b, (unsigned long long)w);  // zero masses pile up in the low buckets
+    }
+  }
   z = block_sum512(z, sh);
   if (threadIdx.x == 0) atomicAdd((unsigned long long*)&a.zsum[r], (unsigned long long)z);
   if (trunc) {
