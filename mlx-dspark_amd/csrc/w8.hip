@@ -756,26 +756,34 @@ struct TunedPlan {
   int fam;
   int nt, u, waves, sk;
   bool pf;
+  int bits;
 };
 static const TunedPlan kTunedPlans[] = {
     // Qwen3-8B, 16-row verify: qkv 7.35 us (rules 8.38), down 14.37 (14.97)
-    {1, 6144, 4096, 2, 3, 2, 16, 2, false},
-    {1, 4096, 12288, 3, 1, 2, 8, 1, false},
+    {1, 6144, 4096, 2, 3, 2, 16, 2, false, 8},
+    {1, 4096, 12288, 3, 1, 2, 8, 1, false, 8},
     // Qwen3-0.6B, 9-row verify: qkv 3.32 (3.60), gate_up 4.88 (6.37), head 38.8 (40.7)
-    {1, 4096, 1024, 2, 1, 4, 4, 1, true},
-    {1, 6144, 1024, 1, 2, 2, 16, 1, true},
-    {1, 151936, 1024, 0, 4, 2, 4, 1, false},
+    {1, 4096, 1024, 2, 1, 4, 4, 1, true, 8},
+    {1, 6144, 1024, 1, 2, 2, 16, 1, true, 8},
+    {1, 151936, 1024, 0, 4, 2, 4, 1, false, 8},
     // Gemma-style 12B (sandwich norms), 9-row verify: o 5.41 (5.81), gate_up 24.2 (25.7),
     // down 13.0 (14.3), head 176.4 (179.6)
-    {1, 3840, 4096, 2, 2, 2, 8, 2, false},
-    {1, 30720, 3840, 1, 4, 2, 8, 1, false},
-    {1, 3840, 15360, 2, 2, 2, 8, 2, false},
-    {1, 262144, 3840, 0, 4, 2, 8, 1, false},
+    {1, 3840, 4096, 2, 2, 2, 8, 2, false, 8},
+    {1, 30720, 3840, 1, 4, 2, 8, 1, false, 8},
+    {1, 3840, 15360, 2, 2, 2, 8, 2, false, 8},
+    {1, 262144, 3840, 0, 4, 2, 8, 1, false, 8},
     // Qwen3-8B, 17-row verify (16 drafts and the bonus row): qkv 9.52 (10.13), gate_up 30.4 (33.3)
-    {2, 6144, 4096, 2, 2, 2, 8, 4, false},
-    {2, 24576, 4096, 1, 2, 2, 8, 1, false},
+    {2, 6144, 4096, 2, 2, 2, 8, 4, false, 8},
+    {2, 24576, 4096, 1, 2, 2, 8, 1, false, 8},
     // Qwen3-8B, 36-row batch: qkv 11.85 (12.46)
-    {3, 6144, 4096, 2, 2, 2, 4, 4, false},
+    {3, 6144, 4096, 2, 2, 2, 4, 4, false, 8},
+    // 4-bit DFlash drafter of the Qwen3-8B shape: 16 block rows o 7.22 (7.76), gate_up 16.82
+    // (19.09), down 10.67 (12.61); 17 context rows fc 20.76 (22.14), k|v 7.33 (8.10)
+    {1, 4096, 4096, 2, 4, 2, 4, 8, true, 4},
+    {1, 24576, 4096, 1, 6, 2, 8, 1, false, 4},
+    {1, 4096, 12288, 2, 4, 4, 8, 4, false, 4},
+    {2, 4096, 20480, 2, 4, 2, 8, 4, false, 4},
+    {2, 2048, 4096, 2, 2, 2, 8, 8, false, 4},
 };
 
 static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi, int bits = 8) {
@@ -785,17 +793,16 @@ static GemmPlan plan_gemm(int M, int64_t N, int64_t K, int epi, int bits = 8) {
   const bool partial = epi == DSK_EPI_PARTIAL, gated = epi == DSK_EPI_SWIGLU || epi == DSK_EPI_GEGLU;
   GemmPlan p;
   const int fam = partial ? 2 : (gated ? 1 : (epi == DSK_EPI_RESIDUAL ? 3 : 0));
-  if (bits == 8)
-    for (const TunedPlan& t : kTunedPlans)
-      if (t.mt == MT && t.n == N && t.k == K && t.fam == fam) {
-        p.nt = t.nt;
-        p.u = t.u;
-        p.waves = t.waves;
-        p.sk = t.sk;
-        p.gpb = ((G / t.u + t.sk - 1) / t.sk) * t.u;
-        p.pf = t.pf;
-        return p;
-      }
+  for (const TunedPlan& t : kTunedPlans)
+    if (t.bits == bits && t.mt == MT && t.n == N && t.k == K && t.fam == fam) {
+      p.nt = t.nt;
+      p.u = t.u;
+      p.waves = t.waves;
+      p.sk = t.sk;
+      p.gpb = ((G / t.u + t.sk - 1) / t.sk) * t.u;
+      p.pf = t.pf;
+      return p;
+    }
   if (epi == DSK_EPI_RESIDUAL) {
     // the residual-add epilogue needs whole rows of the product in one workgroup: no K split;
     // one tile per workgroup and up to 16 waves splitting K (reduced through LDS)
