@@ -250,6 +250,58 @@ def gemm_sweep(model, M: int, reps: int = 10) -> dict:
     return out
 
 
+def mall_probe(model, M: int, reps: int = 10) -> dict:
+    """The verify GEMMs with their weights in HBM against weights resident in the 256 MB
+    memory-side cache: per shape, the in-graph average of 36 launches with the epilogue the
+    forward uses, on the 36 layers' weights (`cold`), on one layer's weights 36 times (`same`:
+    every launch after the first finds them in the cache) and on two layers' weights in turn
+    (`pair`). The gap bounds what prefetching a layer's weights ahead of its GEMM can gain."""
+    import torch
+    from mlx_dspark import ops
+
+    P, SW, R = ops.DSK_EPI_PARTIAL, ops.DSK_EPI_SWIGLU, ops.DSK_EPI_RESIDUAL
+    eps = model.args.rms_norm_eps
+    stream = torch.cuda.current_stream()
+    shapes = {"qkv": (lambda L: L.qkv, P), "o": (lambda L: L.o, R), "gate_up": (lambda L: L.gate_up, SW),
+              "down": (lambda L: L.down, R)}
+    out = {}
+    for name, (get, epi) in shapes.items():
+        ws_all = [get(L) for L in model.layers]
+        K, N = ws_all[0].K, ws_all[0].N
+        xr = torch.randn(M, K, device=model.device).to(torch.bfloat16)
+        x = (ops.pack_rn(M=M, K=K, h=xr, norm_w=model.norm, eps=eps) if name == "gate_up" else ops.pack(xr))
+        h = torch.randn(M, N, device=model.device).to(torch.bfloat16)
+
+        def launch(w):
+            if epi == R:
+                return ops.w8_residual(x, w, h, next_norm=model.norm, eps=eps)
+            return ops.w8_gemm(x, w, epi=epi)
+
+        n = len(ws_all)
+        row = {"N": N, "K": K}
+        for mode, ws in (("cold", ws_all), ("same", [ws_all[0]] * n), ("pair", [ws_all[i % 2] for i in range(n)])):
+            launch(ws[0])
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for w in ws:
+                    launch(w)
+            for _ in range(2):
+                g.replay()
+            s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            s_ev.record(stream)
+            for _ in range(reps):
+                g.replay()
+            e_ev.record(stream)
+            torch.cuda.synchronize()
+            row[f"{mode}_us"] = round(s_ev.elapsed_time(e_ev) * 1e3 / (reps * n), 2)
+            del g
+        out[name] = row
+        log(f"memory-side cache probe {name} {N}x{K}: {row}")
+    return out
+
+
 ACC_SHAPE = (4, 16, 151936)   # batch, drafts per row, vocabulary
 
 
@@ -536,6 +588,9 @@ def main(argv=None) -> int:
                     help="build the target, time the W8 GEMM shapes and a 256 MiB copy only (counter runs)")
     ap.add_argument("--acc-only", action="store_true",
                     help="time the standalone acceptance workload [4, 17, 151936] only")
+    ap.add_argument("--mall-probe", action="store_true",
+                    help="build the target and time the verify GEMMs with their weights in HBM and "
+                         "resident in the memory-side cache (one JSON line)")
     ap.add_argument("--gemm-sweep", type=int, default=0, metavar="M",
                     help="build the target and sweep the W8 GEMM plans at the verify shapes for M rows (one JSON line)")
     ap.add_argument("--verify-eager", type=int, default=0, metavar="N",
@@ -571,6 +626,10 @@ def main(argv=None) -> int:
     t_build = time.time()
     keep = not args.no_cpu_baseline            # the oracle reads the MLX-layout codes
     model = synthetic.build_target(args.target, seed=0, keep_mlx=keep and not args.gemm_sweep)
+    if args.mall_probe:
+        print(json.dumps({"mall_probe": {"target": args.target, "M": args.block,
+                                         "shapes": mall_probe(model, args.block)}}), flush=True)
+        return 0
     if args.gemm_sweep:
         log(f"built {args.target} W8 target ({model.weight_bytes / 1e9:.2f} GB) in {time.time() - t_build:.1f} s")
         print(json.dumps({"gemm_sweep": {"target": args.target, "M": args.gemm_sweep,
