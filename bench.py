@@ -497,8 +497,8 @@ def q06_teacher_forced(target, prompt, tokens) -> dict:
     return {"oracle_argmax": int((gap == 0).sum()), "of": len(tokens), "max_gap": round(float(gap.max()), 4)}
 
 
-# The other BASELINE configurations' verify steps, timed alone: (name, synthetic shape, context
-# per batch row, rows per batch row, the 70 %-of-roofline bound BASELINE states in us)
+# The other benchmark configurations' verify steps, timed alone: (name, synthetic shape, context
+# per batch row, rows per batch row, the configuration's 70 %-of-roofline bound in us)
 CONFIG_LEGS = [
     ("Q06", "qwen3-0.6b", [768], 9, 129.0),
     ("G12", "gemma-12b", [8192], 9, 2388.0),
@@ -857,7 +857,7 @@ def main(argv=None) -> int:
                 legs[name] = verify_leg(shape, lens, w)
                 legs[name]["baseline_bound_us"] = bound
                 log(f"{name} verify ({shape}, rows {len(lens)}x{w}, contexts {lens}): {legs[name]['verify_us']} us, "
-                    f"{legs[name]['roofline_frac'] * 100:.1f}% of HBM roofline (BASELINE's 70% bound {bound} us)")
+                    f"{legs[name]['roofline_frac'] * 100:.1f}% of HBM roofline (the configuration's 70% bound {bound} us)")
             except Exception as e:                      # a leg never takes the headline line down
                 legs[name] = {"error": f"{type(e).__name__}: {e}"}
                 log(f"{name} verify leg failed: {legs[name]['error']}")

@@ -1,6 +1,6 @@
 """Logit agreement for the GPU parity tests.
 
-The tolerance is the north star's: max-abs <= 2e-2 between RMS-normalised logit rows of the GPU
+The tolerance is the stated logits bound: max-abs <= 2e-2 between RMS-normalised logit rows of the GPU
 and of the reference-order oracle (float32 softmax), unless the measured noise floor of the case
 is larger. The floor is the distance between two valid evaluations of the oracle's own
 rounding-point graph: the float32 oracle and its twin with float64 sums (oracle.model.exact_sums,

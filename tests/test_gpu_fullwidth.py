@@ -1,5 +1,5 @@
 """GPU parity at the workloads' real widths, against the reference-order oracle (float32
-softmax), bounded by the north star's 2e-2 or by the measured noise floor where that is larger
+softmax), bounded by the stated 2e-2 logits bound or by the measured noise floor where that is larger
 (tests/_parity.py): the oracle against the same oracle with float64 sums, two valid evaluations
 of one rounding-point graph, measured here on each case's own model and inputs.
 
