@@ -53,6 +53,7 @@ CASES = [
     (2, 3, 151936, 1.0, 0.95, 50, False, False), # both truncations at the vocabulary width
     (1, 0, 4096, 1.0, 0.9, 0, False, False),     # no drafts: only the bonus draw
     (2, 4, 3001, 0.8, 1e-6, 1, False, True),     # a one-element nucleus, top-1
+    (2, 4, 151936, 0.6, 0.95, 20, True, False),  # a sampled round's settings at the vocabulary width
 ]
 
 
