@@ -255,9 +255,11 @@ def mall_probe(model, M: int, reps: int = 10) -> dict:
     memory-side cache: per shape, the in-graph average of 36 launches with the epilogue the
     forward uses, on the 36 layers' weights (`cold`), on one layer's weights 36 times (`same`:
     every launch after the first finds them in the cache) and on two layers' weights in turn
-    (`pair`). The gap bounds what prefetching a layer's weights ahead of its GEMM can gain."""
+    (`pair`). The gap bounds what prefetching a layer's weights ahead of its GEMM can gain.
+    `read` is a plain read of the 36 layers' codes (dsk_prefetch: no arithmetic, no output)."""
     import torch
-    from mlx_dspark import ops
+    from mlx_dspark import _hip, ops
+    from mlx_dspark._hip import ptr, stream_ptr
 
     P, SW, R = ops.DSK_EPI_PARTIAL, ops.DSK_EPI_SWIGLU, ops.DSK_EPI_RESIDUAL
     eps = model.args.rms_norm_eps
@@ -297,6 +299,29 @@ def mall_probe(model, M: int, reps: int = 10) -> dict:
             torch.cuda.synchronize()
             row[f"{mode}_us"] = round(s_ev.elapsed_time(e_ev) * 1e3 / (reps * n), 2)
             del g
+        # a plain read of the same 36 layers' codes (dsk_prefetch, 512 workgroups, one launch per
+        # layer, no arithmetic): the codes are 94 % of a weight's bytes
+        sink = torch.zeros(64, dtype=torch.uint8, device=model.device)
+
+        def read(w):
+            _hip.call("dsk_prefetch", ptr(w.wt), w.wt.numel() * w.wt.element_size(), 512, ptr(sink), stream_ptr())
+
+        read(ws_all[0])
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for w in ws_all:
+                read(w)
+        g.replay()
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        s_ev.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e_ev.record(stream)
+        torch.cuda.synchronize()
+        row["read_us"] = round(s_ev.elapsed_time(e_ev) * 1e3 / (reps * n), 2)
+        del g
         out[name] = row
         log(f"memory-side cache probe {name} {N}x{K}: {row}")
     return out
