@@ -256,7 +256,8 @@ def mall_probe(model, M: int, reps: int = 10) -> dict:
     forward uses, on the 36 layers' weights (`cold`), on one layer's weights 36 times (`same`:
     every launch after the first finds them in the cache) and on two layers' weights in turn
     (`pair`). The gap bounds what prefetching a layer's weights ahead of its GEMM can gain.
-    `read` is a plain read of the 36 layers' codes (dsk_prefetch: no arithmetic, no output)."""
+    `read` is a plain read of the 36 layers' codes (dsk_prefetch: no arithmetic, no output), the
+    fastest of four grid sizes."""
     import torch
     from mlx_dspark import _hip, ops
     from mlx_dspark._hip import ptr, stream_ptr
@@ -299,31 +300,58 @@ def mall_probe(model, M: int, reps: int = 10) -> dict:
             torch.cuda.synchronize()
             row[f"{mode}_us"] = round(s_ev.elapsed_time(e_ev) * 1e3 / (reps * n), 2)
             del g
-        # a plain read of the same 36 layers' codes (dsk_prefetch, 512 workgroups, one launch per
-        # layer, no arithmetic): the codes are 94 % of a weight's bytes
+        # a plain read of the same 36 layers' codes (dsk_prefetch: one launch per layer, no
+        # arithmetic, 32 KB in flight per workgroup) at several grid sizes, the fastest kept: the
+        # codes are 94 % of a weight's bytes
         sink = torch.zeros(64, dtype=torch.uint8, device=model.device)
+        best = None
+        for wg in (256, 512, 1024, 2048):
+            def read(w, wg=wg):
+                _hip.call("dsk_prefetch", ptr(w.wt), w.wt.numel() * w.wt.element_size(), wg, ptr(sink),
+                          stream_ptr())
 
-        def read(w):
-            _hip.call("dsk_prefetch", ptr(w.wt), w.wt.numel() * w.wt.element_size(), 512, ptr(sink), stream_ptr())
-
-        read(ws_all[0])
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for w in ws_all:
-                read(w)
-        g.replay()
-        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        s_ev.record(stream)
-        for _ in range(reps):
+            read(ws_all[0])
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for w in ws_all:
+                    read(w)
             g.replay()
-        e_ev.record(stream)
-        torch.cuda.synchronize()
-        row["read_us"] = round(s_ev.elapsed_time(e_ev) * 1e3 / (reps * n), 2)
-        del g
+            s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            s_ev.record(stream)
+            for _ in range(reps):
+                g.replay()
+            e_ev.record(stream)
+            torch.cuda.synchronize()
+            us = round(s_ev.elapsed_time(e_ev) * 1e3 / (reps * n), 2)
+            del g
+            if best is None or us < best[0]:
+                best = (us, wg)
+        row["read_us"], row["read_workgroups"] = best
+        row["read_TBs"] = round(ws_all[0].wt.numel() * ws_all[0].wt.element_size() / best[0] / 1e6, 2)
         out[name] = row
         log(f"memory-side cache probe {name} {N}x{K}: {row}")
+    # the same read over the logits head's codes, one launch: the streaming rate without the
+    # per-launch ramp and tail weighing on it
+    w = model.lm_head
+    nbytes = w.wt.numel() * w.wt.element_size()
+    best = None
+    for wg in (512, 1024, 2048, 4096):
+        _hip.call("dsk_prefetch", ptr(w.wt), nbytes, wg, ptr(sink), stream_ptr())
+        torch.cuda.synchronize()
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_ev.record(stream)
+        for _ in range(reps):
+            _hip.call("dsk_prefetch", ptr(w.wt), nbytes, wg, ptr(sink), stream_ptr())
+        e_ev.record(stream)
+        torch.cuda.synchronize()
+        us = round(s_ev.elapsed_time(e_ev) * 1e3 / reps, 2)
+        if best is None or us < best[0]:
+            best = (us, wg)
+    out["head_read"] = {"bytes": nbytes, "us": best[0], "workgroups": best[1],
+                        "TBs": round(nbytes / best[0] / 1e6, 2)}
+    log(f"memory-side cache probe: plain read of the head's codes {out['head_read']}")
     return out
 
 

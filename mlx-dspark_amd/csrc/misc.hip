@@ -98,18 +98,28 @@ __global__ __launch_bounds__(kLpThreads) void row_logprobs_kernel(const float* _
 }
 
 // Reads [p, p + n16 * 16) and keeps nothing: the bytes pass through the memory-side cache on
-// their way, so a kernel that reads them soon after finds them there. The xor of everything
-// read is stored only if it equals a value no real weight image produces in practice, and then
-// into the caller's 16-byte sink, so the loads cannot be dropped.
+// their way, so a kernel that reads them soon after finds them there. Each thread issues
+// kPrefetchLoads 16-byte loads before it uses any (a lane past the end re-reads the last chunk),
+// so a workgroup keeps 32 KB in flight. The xor of everything read is stored only if it equals a
+// value no real weight image produces in practice, and then into the caller's 16-byte sink, so
+// the loads cannot be dropped.
+constexpr int kPrefetchLoads = 8;
+
 __global__ __launch_bounds__(256) void prefetch_kernel(const uint4* __restrict__ p, int64_t n16,
                                                        uint4* __restrict__ sink) {
   uint4 acc = {0, 0, 0, 0};
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (int64_t)gridDim.x * 256) {
-    const uint4 v = p[i];
-    acc.x ^= v.x;
-    acc.y ^= v.y;
-    acc.z ^= v.z;
-    acc.w ^= v.w;
+  const int64_t step = (int64_t)gridDim.x * 256 * kPrefetchLoads;
+  for (int64_t base = (int64_t)blockIdx.x * 256 * kPrefetchLoads + threadIdx.x; base < n16; base += step) {
+    uint4 v[kPrefetchLoads];
+#pragma unroll
+    for (int u = 0; u < kPrefetchLoads; ++u) v[u] = p[min(base + u * 256, n16 - 1)];
+#pragma unroll
+    for (int u = 0; u < kPrefetchLoads; ++u) {
+      acc.x ^= v[u].x;
+      acc.y ^= v[u].y;
+      acc.z ^= v[u].z;
+      acc.w ^= v[u].w;
+    }
   }
   if (acc.x == 0x9e3779b9u && acc.y == 0x7f4a7c15u && acc.z == 0xf39cc060u && acc.w == 0x5ced1a3bu) *sink = acc;
 }
