@@ -278,3 +278,19 @@ def test_weight_prefetch_side_stream_leaves_the_forward_unchanged(dev, tiny):
     assert torch.equal(l0, l1) and torch.equal(f0, f1) and torch.equal(g0, g1)
     assert torch.equal(g0.view_as(l0), l0)
     assert (n0, d0) == (n1, d1) == (64, 64)
+
+
+@pytest.mark.parametrize("nbytes", [16, 4080, 32768 + 16, (1 << 20) + 48])
+def test_plain_read_kernel_ragged_sizes(dev, nbytes):
+    """dsk_prefetch over sizes that end mid-chunk, from one workgroup to more workgroups than
+    chunks: every load stays inside [p, p + bytes) (the lanes past the end re-read the last
+    16 bytes), and the 16-byte sink is untouched for a buffer whose xor is not the sentinel."""
+    from mlx_dspark import _hip
+    from mlx_dspark._hip import ptr, stream_ptr
+    print(f"plain read: {nbytes} bytes", flush=True)
+    buf = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(16, dtype=torch.uint8, device=dev)
+    for wg in (1, 3, 512, 4096):
+        _hip.call("dsk_prefetch", ptr(buf), nbytes, wg, ptr(sink), stream_ptr())
+    torch.cuda.synchronize()
+    assert int(sink.sum()) == 0
