@@ -61,8 +61,8 @@ PEAK_HBM_GBS = 8000.0
 TRAFFIC = {
     # qkv 6144x4096, split-K partials: 13342.68 KiB x 2.000 + 768 KiB
     "w8_gemm_kernel<1, 3, 2, 16, 2, false, 8>": 28112249,
-    # o 4096x4096, residual epilogue: 9509.66 KiB x 2.000 + 384 KiB
-    "w8_gemm_kernel<1, 1, 4, 16, 3, false, 8>": 19869003,
+    # o 4096x4096, residual epilogue: 9522.66 KiB x 2.000 + 384 KiB
+    "w8_gemm_kernel<1, 1, 2, 16, 3, true, 8>": 19895624,
     # gate_up 24576x4096, SwiGLU: 52856.84 KiB x 2.000 + 384 KiB
     "w8_gemm_kernel<1, 2, 2, 8, 5, true, 8>": 108644025,
     # down 4096x12288, residual epilogue: 27939.95 KiB x 2.000 + 401.78 KiB
