@@ -352,6 +352,26 @@ def mall_probe(model, M: int, reps: int = 10) -> dict:
     out["head_read"] = {"bytes": nbytes, "us": best[0], "workgroups": best[1],
                         "TBs": round(nbytes / best[0] / 1e6, 2)}
     log(f"memory-side cache probe: plain read of the head's codes {out['head_read']}")
+    # the cost of a launch itself: 100 launches of a one-workgroup kernel with one load and one
+    # store (dsk_lens_add on one length) in one graph
+    lens = torch.zeros(1, dtype=torch.int32, device=model.device)
+    ops.lens_add(lens, None, 1)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(100):
+            ops.lens_add(lens, None, 1)
+    g.replay()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s_ev.record(stream)
+    for _ in range(reps):
+        g.replay()
+    e_ev.record(stream)
+    torch.cuda.synchronize()
+    out["launch_us"] = round(s_ev.elapsed_time(e_ev) * 1e3 / (reps * 100), 2)
+    del g
+    log(f"memory-side cache probe: one tiny kernel in a graph {out['launch_us']} us per launch")
     return out
 
 
