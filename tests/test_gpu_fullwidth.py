@@ -10,7 +10,8 @@ Targets (two decoder layers each, the full vocabulary head, random norm gains):
   - Gemma-style 12B shape (hidden 3840, 16 / 8 heads, head_dim 256, GeGLU 15360, 262144-row tied
     head with soft-cap 30, sandwich norms): a sliding-window (1024) layer and a global layer
     over an 8192-token bf16 context, 9 rows.
-At full depth: the whole 36-layer Qwen3-8B shape, 16 rows over a 1024-token 8-bit KV context.
+At full depth: the whole 36-layer Qwen3-8B shape, 16 rows over a 1024-token 8-bit KV context, and
+the whole 48-layer Gemma-style shape, 9 rows over a 2048-token bf16 context.
 The context is written straight into the paged cache (random keys and values, 8-bit quantized
 with the engine's rule where the cache is 8-bit) and the oracle attends to the same values, so
 the oracle only runs the verify rows.
@@ -222,6 +223,49 @@ def test_verify_logits_full_depth_qwen3_8b(dev):
     check_logits(got, rl, "qwen3-8b 36-layer verify logits", floor=floor)
     # the greedy picks the verify decides: the GPU's argmax is the oracle's, or within the
     # bound of the oracle's best normalised logit
+    rn = rl / rl.pow(2).mean(-1, keepdim=True).sqrt()
+    pick = got.argmax(-1)
+    gap = rn.max(-1).values - rn.gather(1, pick[:, None])[:, 0]
+    print(f"  greedy picks: {int((gap == 0).sum())}/{W} are the oracle's argmax, largest gap "
+          f"{float(gap.max()):.4f}", flush=True)
+    assert float(gap.max()) <= max(2e-2, 1.5 * floor[0])
+
+
+def test_verify_logits_full_depth_gemma_12b(dev):
+    """The whole 48-layer Gemma-style 12B target (40 sliding-window layers of 1024 keys, 8 global
+    ones, sandwich norms, soft-capped 262144-row head; random norm gains), a 9-row verify over a
+    2048-token bf16 context in every layer, against the oracle at full depth with the same
+    floor rule."""
+    print("full-depth verify gemma-12b: 48 layers, ctx=2048, W=9, bf16 KV", flush=True)
+    model = _target("gemma-12b", layers=48, seed=31)
+    a = model.args
+    nkv, hd, ctx, W = a.num_key_value_heads, a.head_dim, 2048, 9
+    assert sum(a.is_sliding(l) for l in range(a.num_hidden_layers)) == 40
+    cache = model.make_cache(max_ctx=ctx + 64, kv_bits=None)
+    g = torch.Generator().manual_seed(33)
+    held = []
+    for l in range(a.num_hidden_layers):
+        K = 0.4 * torch.randn(ctx, nkv, hd, generator=g)
+        V = torch.randn(ctx, nkv, hd, generator=g)
+        held.append(_fill_context(cache, l, K, V))
+    cache.set_lengths([ctx])
+    block = torch.randint(0, a.vocab_size, (W,), generator=g)
+    ids = block.to(dev, torch.int32).view(1, W)
+    logits, _ = model.forward(ids, cache, None, advance=False)
+    torch.cuda.synchronize()
+    got = logits[0].float().cpu()
+    assert float(got.abs().max()) <= a.final_logit_softcapping
+    ref = OM.OracleTarget(model, kv_bits=None)
+
+    def run(exact):
+        ref.K = [k for k, _ in held]
+        ref.V = [v for _, v in held]
+        ref.offset = ctx
+        with OM.exact_sums(exact):
+            return ref.forward(block)[0]
+
+    rl, floor = _oracle_twice(run)
+    check_logits(got, rl, "gemma-12b 48-layer verify logits", floor=floor)
     rn = rl / rl.pow(2).mean(-1, keepdim=True).sqrt()
     pick = got.argmax(-1)
     gap = rn.max(-1).values - rn.gather(1, pick[:, None])[:, 0]
