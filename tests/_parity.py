@@ -86,22 +86,24 @@ def check_logits(got, want, what="", exact=None, floor=None):
 STREAM_TOL = 2e-2       # top-2 margin (RMS-normalised logits) below which bf16 may flip a pick
 
 
-def check_greedy_stream(model, prompt, got, min_match: int, tol: float = STREAM_TOL, oracle=None):
+def check_greedy_stream(model, prompt, got, min_match: int, tol: float = STREAM_TOL, oracle=None,
+                        kv_bits=None):
     """Teacher-forced greedy parity. The oracle runs ``prompt + got[:-1]`` in one forward; at
     every position the engine's token must be the oracle's argmax, or within ``tol`` of the
     oracle's best RMS-normalised logit (a near-tie that bf16 rounding may flip). Every token is
     checked, also after such a flip, and at least ``min_match`` of them (or all) must be the
-    oracle's exact argmax, so a stream of near-ties cannot pass. Returns the exact count."""
+    oracle's exact argmax, so a stream of near-ties cannot pass. kv_bits: the engine's KV
+    cache format, which the oracle's cache then follows. Returns the exact count."""
     got = [int(t) for t in got]
     if not got:
         return 0
-    ot = oracle or OM.OracleTarget(model)
+    ot = oracle or OM.OracleTarget(model, kv_bits=kv_bits)
     logits, _ = ot.forward(list(prompt) + got[:-1])
     rows = logits[len(prompt) - 1:]
     if oracle is None:
         # the rows' noise floor: the same forward with float64 sums
         with OM.exact_sums():
-            erows = OM.OracleTarget(model).forward(list(prompt) + got[:-1])[0][len(prompt) - 1:]
+            erows = OM.OracleTarget(model, kv_bits=kv_bits).forward(list(prompt) + got[:-1])[0][len(prompt) - 1:]
         floor = OM.logit_diff(rows, erows)[0]
         if FLOOR_SCATTER * floor > tol:
             print(f"greedy stream: margin tolerance {FLOOR_SCATTER * floor:.4f} ({FLOOR_SCATTER} x the rows' "

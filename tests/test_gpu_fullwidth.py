@@ -11,7 +11,8 @@ Targets (two decoder layers each, the full vocabulary head, random norm gains):
     head with soft-cap 30, sandwich norms): a sliding-window (1024) layer and a global layer
     over an 8192-token bf16 context, 9 rows.
 At full depth: the whole 36-layer Qwen3-8B shape, 16 rows over a 1024-token 8-bit KV context, and
-the whole 48-layer Gemma-style shape, 9 rows over a 2048-token bf16 context.
+the whole 48-layer Gemma-style shape, 9 rows over a 2048-token bf16 context; and the Q8 pair end to
+end (36-layer target, 2-layer DFlash drafter), its greedy stream teacher-forced under the oracle.
 The context is written straight into the paged cache (random keys and values, 8-bit quantized
 with the engine's rule where the cache is 8-bit) and the oracle attends to the same values, so
 the oracle only runs the verify rows.
@@ -26,7 +27,7 @@ import numpy as np
 import pytest
 import torch
 
-from _parity import check_logits
+from _parity import check_greedy_stream, check_logits
 from oracle import model as OM
 from oracle import w8 as W8
 
@@ -272,3 +273,25 @@ def test_verify_logits_full_depth_gemma_12b(dev):
     print(f"  greedy picks: {int((gap == 0).sum())}/{W} are the oracle's argmax, largest gap "
           f"{float(gap.max()):.4f}", flush=True)
     assert float(gap.max()) <= max(2e-2, 1.5 * floor[0])
+
+
+def test_q8_dflash_stream_full_depth(dev):
+    """The Q8 pair end to end at full depth: the 36-layer Qwen3-8B-shaped W8 target with 8-bit KV
+    and the 2-layer 4-bit DFlash drafter (block 16) decode 32 tokens after a 64-token prompt in
+    graph-replayed rounds; the stream, teacher-forced under the oracle's 36-layer target with the
+    same 8-bit cache, is the oracle's greedy decoding under the margin rule."""
+    from mlx_dspark import synthetic
+    from mlx_dspark.generate import dflash_generate
+    from mlx_dspark.target import Target
+    from mlx_dspark.tokenizer import SyntheticTokenizer
+    print("Q8 pair at full depth: 36-layer W8 target, 8-bit KV, 2-layer 4-bit DFlash, 32 tokens", flush=True)
+    model = synthetic.build_target("qwen3-8b", seed=41, keep_mlx=True)
+    tok = SyntheticTokenizer(model.args.vocab_size)
+    target = Target(model, tok, kv_bits=8)
+    d, _ = synthetic.build_dflash(model.args, seed=42, block_size=16, n_taps=5, bits=4)
+    d.bind(model)
+    prompt = np.random.default_rng(43).integers(0, model.args.vocab_size, 64).tolist()
+    r = dflash_generate(target, tok, d, prompt_ids=prompt, max_new_tokens=32, use_graph=True)
+    s = r.token_ids[:32]
+    assert len(s) == 32 and r.num_rounds >= 8
+    check_greedy_stream(model, prompt, s, 24, kv_bits=8)
