@@ -12,7 +12,8 @@ Targets (two decoder layers each, the full vocabulary head, random norm gains):
     over an 8192-token bf16 context, 9 rows.
 At full depth: the whole 36-layer Qwen3-8B shape, 16 rows over a 1024-token 8-bit KV context, and
 the whole 48-layer Gemma-style shape, 9 rows over a 2048-token bf16 context; and the Q8 pair end to
-end (36-layer target, 2-layer DFlash drafter), its greedy stream teacher-forced under the oracle.
+end (36-layer target, 2-layer DFlash drafter) and the G12 pair (48-layer target, gemma4 DSpark
+drafter), their greedy streams teacher-forced under the oracle.
 The context is written straight into the paged cache (random keys and values, 8-bit quantized
 with the engine's rule where the cache is 8-bit) and the oracle attends to the same values, so
 the oracle only runs the verify rows.
@@ -295,3 +296,26 @@ def test_q8_dflash_stream_full_depth(dev):
     s = r.token_ids[:32]
     assert len(s) == 32 and r.num_rounds >= 8
     check_greedy_stream(model, prompt, s, 24, kv_bits=8)
+
+
+def test_g12_dspark_stream_full_depth(dev):
+    """The G12 pair end to end at full depth: the 48-layer Gemma-style W8 target (40 sliding
+    layers) with 8-bit KV and the 1-layer gemma4 DSpark drafter decode 24 greedy tokens (block 8,
+    lookup drafts off) after a 64-token prompt; the stream, teacher-forced under the oracle's
+    48-layer target with the same 8-bit cache, is the oracle's greedy decoding under the margin
+    rule."""
+    from mlx_dspark import synthetic
+    from mlx_dspark.generate import speculative_generate
+    from mlx_dspark.target import Target
+    from mlx_dspark.tokenizer import SyntheticTokenizer
+    print("G12 pair at full depth: 48-layer W8 target, 8-bit KV, gemma4 DSpark, 24 tokens", flush=True)
+    model = synthetic.build_target("gemma-12b", seed=51, keep_mlx=True)
+    d, _ = synthetic.build_dspark(model.args, seed=52, num_hidden_layers=1, block_size=8, family="gemma4")
+    tok = SyntheticTokenizer(model.args.vocab_size)
+    target = Target(model, tok, kv_bits=8)
+    prompt = np.random.default_rng(53).integers(0, model.args.vocab_size, 64).tolist()
+    r = speculative_generate(target, tok, d, prompt_ids=prompt, max_new_tokens=24, max_draft_tokens=8,
+                             lookup_drafts=False)
+    s = r.token_ids[:24]
+    assert len(s) == 24
+    check_greedy_stream(model, prompt, s, 18, kv_bits=8)
