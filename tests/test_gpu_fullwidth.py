@@ -13,7 +13,8 @@ Targets (two decoder layers each, the full vocabulary head, random norm gains):
 At full depth: the whole 36-layer Qwen3-8B shape, 16 rows over a 1024-token 8-bit KV context, and
 the whole 48-layer Gemma-style shape, 9 rows over a 2048-token bf16 context; and the Q8 pair end to
 end (36-layer target, 2-layer DFlash drafter) and the G12 pair (48-layer target, gemma4 DSpark
-drafter), their greedy streams teacher-forced under the oracle.
+drafter), and the CB engine (SpecSlots, three ragged rows over the 36-layer target), their greedy
+streams teacher-forced under the oracle.
 The context is written straight into the paged cache (random keys and values, 8-bit quantized
 with the engine's rule where the cache is 8-bit) and the oracle attends to the same values, so
 the oracle only runs the verify rows.
@@ -319,3 +320,34 @@ def test_g12_dspark_stream_full_depth(dev):
     s = r.token_ids[:24]
     assert len(s) == 24
     check_greedy_stream(model, prompt, s, 18, kv_bits=8)
+
+
+def test_cb_slots_greedy_full_depth(dev):
+    """The CB engine at full depth: SpecSlots over the 36-layer Qwen3-8B-shaped W8 target with
+    8-bit KV and a 1-layer DSpark drafter (8 drafts, W = 9), three rows with ragged prompts
+    decoding greedily together; each row's stream, teacher-forced under the oracle's 36-layer
+    target with the same 8-bit cache, is the oracle's greedy decoding under the margin rule."""
+    from mlx_dspark import synthetic
+    from mlx_dspark.batch_engine import SpecSlots
+    from mlx_dspark.target import Target
+    from mlx_dspark.tokenizer import SyntheticTokenizer
+    print("CB engine at full depth: 36-layer W8 target, 8-bit KV, DSpark k = 8, 3 ragged rows", flush=True)
+    model = synthetic.build_target("qwen3-8b", seed=61, keep_mlx=True)
+    tok = SyntheticTokenizer(model.args.vocab_size)
+    target = Target(model, tok, kv_bits=8)
+    d, _ = synthetic.build_dspark(model.args, seed=62, num_hidden_layers=1, block_size=8)
+    rng = np.random.default_rng(63)
+    prompts = [rng.integers(0, model.args.vocab_size, n).tolist() for n in (40, 72, 24)]
+    slots = SpecSlots(target, tok, d, capacity=3, max_draft_tokens=8, max_ctx=256)
+    for i, p in enumerate(prompts):
+        slots.admit(p, max_new_tokens=16, meta=i)
+    done, rounds = {}, 0
+    while slots.n_active:
+        for meta, r in slots.step():
+            done[meta] = r
+        rounds += 1
+        assert rounds < 100
+    for i, p in enumerate(prompts):
+        s = done[i].token_ids[:16]
+        assert len(s) == 16
+        check_greedy_stream(model, p, s, 12, kv_bits=8)
