@@ -62,7 +62,7 @@ def test_gemm_plan_query_names_the_traced_kernels():
     P, R, SW, ST = ops.DSK_EPI_PARTIAL, ops.DSK_EPI_RESIDUAL, ops.DSK_EPI_SWIGLU, ops.DSK_EPI_STORE
     want = {(6144, 4096, P, False): "w8_gemm_kernel<1, 3, 2, 16, 2, false, 8>",
             (4096, 4096, R, False): "w8_gemm_kernel<1, 1, 2, 16, 3, true, 8>",
-            (24576, 4096, SW, True): "w8_gemm_kernel<1, 2, 2, 8, 5, true, 8>",
+            (24576, 4096, SW, True): "w8_gemm_kernel<1, 2, 2, 8, 5, false, 8>",
             (4096, 12288, R, False): "w8_gemm_kernel<1, 1, 2, 8, 3, false, 8>",
             (151936, 4096, ST, True): "w8_gemm_kernel<1, 4, 2, 8, 4, false, 8>"}
     for (N, K, epi, rs), name in want.items():
